@@ -1,0 +1,532 @@
+// Keyframe poses, skeleton transforms, and the per-tick application of an animation frame to the
+// nodes of a humanoid with GRF's smoothing. Semantics: include/cuju/animation/keyframes.h:16-194,
+// include/cuju/animation/skeleton.h:98-222, include/cuju/animation/apply.h:16-367,
+// include/cuju/simulation/humanoid.h:178-296 (spatial state).
+#pragma once
+
+#include "world.h"
+
+namespace eng {
+
+// The pose of node `n` at `frame`, interpolated from its keys (also run on the host to fill the
+// interpolation table, so table reads equal this computation bit for bit).
+HDN void ComputeInterpolated(const Anim &a, const KeyFrame *keys, int keyCount, int frame, Quat &ori, Vec3 &pos) {
+    struct Weighed {
+        const KeyFrame *key = nullptr;
+        float influence = 0.0f;
+        int frame = 0;
+    } wk[2];
+    int n = 0;
+    pos = Vec3(0);
+    ori = Quat::Identity();
+    if (frame > 0 && frame < a.frameCount) {
+        for (int k = 0; k < keyCount; k++) {
+            if (keys[k].frame < frame) n = 0;
+            wk[n].key = &keys[k];
+            wk[n++].frame = keys[k].frame;
+            if (keys[k].frame >= frame) break;
+        }
+        float bias = 0;
+        if (n == 1) {
+            wk[0].influence = 1;
+        } else if (n == 2) {
+            int distance = wk[1].frame - wk[0].frame;
+            float d1 = frame - wk[0].frame, d2 = wk[1].frame - frame;
+            wk[0].influence = (float)(1 - d1 / (distance * 1.0));
+            wk[1].influence = (float)(1 - d2 / (distance * 1.0));
+            int rel = frame - wk[0].frame;
+            bias = (float)((rel * 1.0) / (distance * 1.0));
+        }
+        if (n > 1) {
+            ori = wk[0].key->orientation.Slerp(bias, wk[1].key->orientation);
+            pos = wk[0].key->position * wk[0].influence + wk[1].key->position * wk[1].influence;
+        } else {
+            ori = wk[0].key->orientation;
+            pos = wk[0].key->position * wk[0].influence;
+        }
+    } else if (frame >= a.frameCount) {
+        for (int k = keyCount; k-- > 0;) {
+            wk[n].key = &keys[k];
+            wk[n++].frame = keys[k].frame;
+            if (n == 2) break;
+        }
+        if (n == 0) return;
+        if (n == 1) {
+            ori = wk[0].key->orientation;
+            pos = wk[0].key->position;
+            return;
+        }
+        float spacing = wk[0].frame - wk[1].frame;
+        float past = frame - wk[0].frame;
+        float bias = 1 + ((1 / spacing) * past);
+        ori = wk[1].key->orientation.Slerp(bias, wk[0].key->orientation);
+        pos = wk[1].key->position * (1 - bias) + wk[0].key->position * bias;
+    } else {
+        ori = keys[0].orientation;
+        pos = keys[0].position;
+    }
+}
+
+HD void Interpolated(const Ctx &c, const Anim &a, const NodeAnim &n, int frame, Quat &ori, Vec3 &pos) {
+    if (frame < n.interpFrames) {
+        const InterpEntry &e = c.t->interp[n.interpFirst + (frame < 0 ? 0 : frame)];
+        ori = e.orientation;
+        pos = e.position;
+        return;
+    }
+    ComputeInterpolated(a, c.t->keys + n.keyFirst, n.keyCount, frame, ori, pos);
+}
+
+HD void BlendFrames(Quat at, const Vec3 &pAt, const Quat &next, const Vec3 &pNext, float bias, Quat &ori, Vec3 &pos) {
+    at.MakeSameNeighborhood(next);
+    ori = at.Lerp(bias, next).Normalized();
+    pos = pAt * (1.0f - bias) + pNext * bias;
+}
+
+HD void InterpolatedZ(const Ctx &c, const Anim &a, const NodeAnim &n, int frame, Quat &ori, Vec3 &pos, float &z) {
+    if (frame < n.interpFrames) {
+        const InterpEntry &e = c.t->interp[n.interpFirst + (frame < 0 ? 0 : frame)];
+        ori = e.orientation;
+        pos = e.position;
+        z = e.angleZ;
+        return;
+    }
+    ComputeInterpolated(a, c.t->keys + n.keyFirst, n.keyCount, frame, ori, pos);
+    float x, y;
+    ori.Angles(x, y, z);
+}
+
+HD void GetKeyFrameZ(const Ctx &c, const Anim &a, int bodyPart, int frame, Quat &ori, Vec3 &pos, float &z) {
+    for (int i = 0; i < a.nodeCount; i++) {
+        const NodeAnim &n = c.t->nodes[a.nodeFirst + i];
+        if (n.bodyPart == bodyPart) {
+            InterpolatedZ(c, a, n, frame, ori, pos, z);
+            return;
+        }
+    }
+    float x, y;
+    ori.Angles(x, y, z);
+}
+
+HD bool GetKeyFrame(const Ctx &c, const Anim &a, int bodyPart, int frame, Quat &ori, Vec3 &pos) {
+    for (int i = 0; i < a.nodeCount; i++) {
+        const NodeAnim &n = c.t->nodes[a.nodeFirst + i];
+        if (n.bodyPart == bodyPart) {
+            Interpolated(c, a, n, frame, ori, pos);
+            for (int k = 0; k < n.keyCount; k++)
+                if (c.t->keys[n.keyFirst + k].frame == frame) return true;
+            return false;
+        }
+    }
+    return false;
+}
+
+// ---- skeleton transforms -------------------------------------------------------------------------
+struct Derived {
+    Vec3 position, scale;
+    Quat rotation;
+};
+HDN Derived DeriveChild(const Derived *parent, int localMode, const Vec3 &pos, const Quat &rot, const Vec3 &scale) {
+    Derived d;
+    if (localMode == kLocalRelative && parent) {
+        d.rotation = (parent->rotation * rot).Normalized();
+        d.scale = parent->scale * scale;
+        d.position = parent->rotation * (parent->scale * pos);
+        d.position += parent->position;
+    } else {
+        d.rotation = rot;
+        d.scale = scale;
+        d.position = pos;
+    }
+    return d;
+}
+HD void DeriveNodes(const Skeleton &sk, const NodeState *nodes, Derived *out) {
+    for (int n = 0; n < sk.nodeCount; n++) {
+        const Derived *parent = sk.nodes[n].parent >= 0 ? &out[sk.nodes[n].parent] : nullptr;
+        out[n] = DeriveChild(parent, nodes[n].localMode, nodes[n].position, nodes[n].rotation, nodes[n].scale);
+    }
+}
+
+struct Aabb {
+    Vec3 lo, hi;
+    // GRF: the maximum starts at FLT_MIN / 100, just above zero, which collisions depend on.
+    HD void Reset() {
+        const float smallest = 1.17549435e-38f / 100, largest = 3.40282347e+38f / 100;
+        lo = Vec3(largest, largest, largest);
+        hi = Vec3(smallest, smallest, smallest);
+    }
+    HDN Aabb Rotated(const Quat &r) const {
+        Vec3 corners[8] = {Vec3(lo.v[0], lo.v[1], lo.v[2]), Vec3(hi.v[0], lo.v[1], lo.v[2]),
+                           Vec3(lo.v[0], hi.v[1], lo.v[2]), Vec3(hi.v[0], hi.v[1], lo.v[2]),
+                           Vec3(lo.v[0], lo.v[1], hi.v[2]), Vec3(hi.v[0], lo.v[1], hi.v[2]),
+                           Vec3(lo.v[0], hi.v[1], hi.v[2]), Vec3(hi.v[0], hi.v[1], hi.v[2])};
+        Aabb b;
+        b.Reset();
+        for (Vec3 &cn : corners) {
+            cn = r * cn;
+            for (int k = 0; k < 3; k++) {
+                if (cn.v[k] < b.lo.v[k]) b.lo.v[k] = cn.v[k];
+                if (cn.v[k] > b.hi.v[k]) b.hi.v[k] = cn.v[k];
+            }
+        }
+        return b;
+    }
+    HD Aabb Translated(const Vec3 &o) const {
+        Aabb b = *this;
+        b.lo += o;
+        b.hi += o;
+        return b;
+    }
+    HDN bool Intersects(const Vec3 &center, float radius) const {
+        float d2 = 0;
+        for (int k = 0; k < 3; k++) {
+            if (center.v[k] < lo.v[k]) {
+                float d = center.v[k] - lo.v[k];
+                d2 += d * d;
+            } else if (center.v[k] > hi.v[k]) {
+                float d = center.v[k] - hi.v[k];
+                d2 += d * d;
+            }
+        }
+        return d2 <= radius * radius;
+    }
+    // Each coordinate divides by 2 in double and rounds to float.
+    HD Vec3 Center() const {
+        float x = (lo.v[0] + hi.v[0]) / 2.0, y = (lo.v[1] + hi.v[1]) / 2.0, z = (lo.v[2] + hi.v[2]) / 2.0;
+        return Vec3(x, y, z);
+    }
+    // Squares and roots in double (std::pow(float, int)), rounded to float twice.
+    HD float Radius() const {
+        float x = hi.v[0] - lo.v[0], y = hi.v[1] - lo.v[1], z = hi.v[2] - lo.v[2];
+        float l = (float)sqrt((double)x * x + (double)y * y);
+        return (float)(sqrt((double)l * l + (double)z * z) / 2.0);
+    }
+};
+struct WorldGeometry {
+    Aabb box;
+    Vec3 position;
+};
+// GRF: the mesh box rotated and moved by the world transform; the scale does not enter.
+HD WorldGeometry GeometryWorld(const SkelGeometry &g, const Derived &node) {
+    Derived d = DeriveChild(&node, g.localMode, g.position, g.rotation, g.scale);
+    Aabb local{g.boxMin, g.boxMax};
+    return WorldGeometry{local.Rotated(d.rotation).Translated(d.position), d.position};
+}
+
+// ---- applying a frame ------------------------------------------------------------------------------
+HD float SmoothBeginBias(int frame) {
+    int f = frame < 0 ? 0 : frame > 8 ? 8 : frame;
+    return libm::PowfPos(Curve(1.0f - NormalizedClamp((float)f, 0, 8), 1.0f), 0.5f);
+}
+HD int JointSpeedClass(int bp) {
+    if (bp == kBpLeftElbow || bp == kBpRightElbow || bp == kBpLeftKnee || bp == kBpRightKnee) return 1;
+    if (bp == kBpLeftAnkle || bp == kBpRightAnkle) return 2;
+    return 0;
+}
+HD float JointSpeedLimit(int cls, float beginBias) {
+    float m = 7.5f * PI;
+    if (cls == 1) m *= 1.2f;
+    else if (cls == 2) m *= 1.6f;
+    return (0.3f + 0.7f * (1.0f - beginBias)) * m;
+}
+HD float JointSpeed(float dot, int dtMs) {
+    return 2.0f * libm::acosf(Clamp(dot, -1.0f, 1.0f)) / ((float)dtMs * 0.001f);
+}
+
+struct ApplyPlan {
+    int16_t entry[kBodyParts];
+    bool isNew[kBodyParts];
+    float beginBias;
+};
+
+// Each node takes the last history entry of its body part or appends one, in node order.
+HD void ApplyPrepare(const Ctx &c, const Anim &a, Humanoid &h, bool smooth, int frame, ApplyPlan &plan) {
+    plan.beginBias = smooth ? SmoothBeginBias(frame) : 0.0f;
+    if (a.nodeCount > kBodyParts) Fatal("an animation moves more body parts than a humanoid has");
+    if (!smooth) return;
+    auto &hist = h.movementHistory;
+    int16_t last[kBodyParts];
+    for (int b = 0; b < kBodyParts; b++) last[b] = -1;
+    for (int i = 0; i < hist.count; i++) {
+        int32_t b = hist[i].nodeName;
+        if (b >= 0 && b < kBodyParts) last[b] = (int16_t)i;
+    }
+    for (int n = 0; n < a.nodeCount; n++) {
+        int bp = c.t->nodes[a.nodeFirst + n].bodyPart;
+        int found = last[bp];
+        plan.isNew[n] = found < 0;
+        if (found < 0) {
+            MovementHistoryEntry e;
+            memset(&e, 0, sizeof(e));
+            e.nodeName = bp;
+            e.timeDifferenceMs = 10;
+            hist.push_back(e);
+            found = hist.count - 1;
+        }
+        plan.entry[n] = (int16_t)found;
+    }
+}
+
+HDN void ApplyNode(const Ctx &c, const Anim &a, const Skeleton &sk, Humanoid &h, int ni, int frame, bool smooth,
+                   float smoothFactor, const Vec3 &basePos, float baseRot, BiasedOffset *offsets, int dtMs, bool noPos,
+                   const ApplyPlan &plan) {
+    const NodeAnim &na = c.t->nodes[a.nodeFirst + ni];
+    const int bp = na.bodyPart;
+    NodeState &node = h.nodes[sk.nodeMap[bp]];
+    Quat ori;
+    Vec3 pos;
+    // The table's halfway pose while `ori` still equals it, else null.
+    const MiddleEntry *middle = nullptr;
+    if (frame >= 0 && frame + 1 < na.interpFrames) {
+        middle = &c.t->middle[na.interpFirst + frame];
+        ori = middle->orientation;
+        pos = middle->position;
+    } else {
+        Quat oa, ob;
+        Vec3 pa, pb;
+        Interpolated(c, a, na, frame, oa, pa);
+        Interpolated(c, a, na, frame + 1, ob, pb);
+        BlendFrames(oa, pa, ob, pb, 0.5f, ori, pos);
+    }
+    if (bp == kBpPlayer) {
+        if (noPos) {
+            pos.v[0] = 0;
+            pos.v[1] = 0;
+        } else {
+            pos.Rotate2D(baseRot);
+        }
+    }
+    if (bp == kBpBody) {
+        Quat rz;
+        rz.SetAngleAxis(baseRot, Vec3(0, 0, 1));
+        ori = rz * ori;
+        ori.Normalize();
+        middle = nullptr;
+    }
+    {
+        BiasedOffset &off = offsets[bp];
+        if (off.bias != 0.0) {
+            off.orientation.MakeSameNeighborhood(ori);
+            ori = ori.Lerp(off.bias, off.orientation).Normalized();
+            middle = nullptr;
+        }
+    }
+    if (smooth) {
+        MovementHistoryEntry *e = &h.movementHistory[plan.entry[ni]];
+        if (plan.isNew[ni]) {
+            e->position = pos;
+            e->orientation = ori;
+        }
+        const float beginBias = plan.beginBias;
+        float curBias = 0.0f + beginBias * smoothFactor * 0.5f;
+        if (bp != kBpPlayer) {
+            const Quat prevOri = e->orientation;
+            Quat curOri = node.rotation;
+            curOri.MakeSameNeighborhood(prevOri);
+            if (dtMs > 0) {
+                bool steady = false;
+                // The zero-bias slerp of the normalized halfway pose: each nonzero element is kept
+                // and each zero takes the sign of a sum of two zeros, which normalizing preserves.
+                if (middle && middle->normalizedKeepsZeros && curBias == 0.0f) {
+                    const Quat &from = middle->orientation;
+                    Quat target = curOri;
+                    float ch = from.q[3] * target.q[3] + from.q[0] * target.q[0] + from.q[1] * target.q[1] +
+                               from.q[2] * target.q[2];
+                    if (ch < 0) {
+                        target = -target;
+                        ch = -ch;
+                    }
+                    if (fabsf(ch) >= 1.0f) {
+                        ori = middle->normalized;
+                        steady = true;
+                    } else if (fabsf(ch) < 1.0f) {
+                        for (int k = 0; k < 4; k++) {
+                            const float own = middle->normalized.q[k];
+                            ori.q[k] = own != 0.0f ? own
+                                       : (signbit(own) && signbit(target.q[k]) != signbit(curBias)) ? -0.0f
+                                                                                                     : 0.0f;
+                        }
+                        steady = true;
+                    }
+                }
+                if (!steady) ori = ori.Slerp(curBias, curOri).Normalized();
+                float dot = ori.MakeSameNeighborhood(curOri);
+                const int cls = JointSpeedClass(bp);
+                const float maxAngle = JointSpeedLimit(cls, beginBias);
+                float aps = JointSpeed(dot, dtMs);
+                if (aps > maxAngle) {
+                    float allowed = maxAngle / aps;
+                    Quat desired = curOri.RotationTo(ori).Normalized();
+                    ori = (desired.RotationMultipliedBy(allowed) * curOri).Normalized();
+                }
+            }
+            e->orientation = curOri;
+            e->timeDifferenceMs = dtMs;
+        } else {
+            const Vec3 curPos = node.position;
+            if (dtMs > 0 && beginBias > 0.01f) {
+                pos.v[2] = pos.v[2] * (1.0f - curBias) + curPos.v[2] * curBias;
+                float maxMps = 2.8f;
+                if (a.outgoingSpecialState != kStrEmpty) maxMps = 6.0f;
+                float allowed = maxMps * ((float)dtMs * 0.001f);
+                float newZ = pos.v[2] + basePos.v[2];
+                float desired = fabsf(newZ - curPos.v[2]);
+                float hb = 1.0f;
+                if (desired > allowed) hb = allowed / desired;
+                newZ = (newZ * hb + curPos.v[2] * (1.0f - hb)) * beginBias + newZ * (1.0f - beginBias);
+                pos = pos.Get2D() + Vec3(0, 0, newZ);
+            }
+            e->position = curPos;
+            e->timeDifferenceMs = dtMs;
+        }
+    }
+    if (bp != kBpPlayer) {
+        Quat cur = node.rotation;
+        ori.MakeSameNeighborhood(cur);
+        node.rotation = ori;
+    } else {
+        node.position = pos + basePos;
+    }
+}
+
+// Applies every humanoid's buffered frame; humanoids are independent.
+HDN void FetchPutBuffers(const Ctx &c, const Skeleton *const *skels, Humanoid *const *hums, int count) {
+    for (int k = 0; k < count; k++) {
+        Humanoid &h = *hums[k];
+        AnimApplyBuffer &buf = h.applyBuf;
+        const Anim &a = c.A(buf.anim);
+        ApplyPlan plan;
+        ApplyPrepare(c, a, h, buf.smooth, buf.frameNum, plan);
+        for (int n = 0; n < a.nodeCount; n++)
+            ApplyNode(c, a, *skels[k], h, n, buf.frameNum, buf.smooth, buf.smoothFactor, buf.position,
+                      buf.orientation.value(), buf.offsets, 10, buf.noPos, plan);
+    }
+}
+
+// ---- spatial state --------------------------------------------------------------------------------
+// The body directions allowed relative to movement, and the zero vector last.
+HD Vec3 AllowedBodyDir(int i) {
+    const float s = 0x1.6a09e6p-1f;
+    switch (i) {
+        case 0:
+            return Vec3(0, -1, 0);
+        case 1:
+            return Vec3(-s, -s, 0);
+        case 2:
+            return Vec3(s, -s, 0);
+        case 3:
+            return Vec3(-s, s, 0);
+        case 4:
+            return Vec3(s, s, 0);
+    }
+    return Vec3(0, 0, 0);
+}
+// Angle2D(Vec3(0,-1,0)) of each allowed direction: the first is -0, the last +0.
+HD float AllowedBodyDirAngle(int i) {
+    switch (i) {
+        case 0:
+            return -0.0f;
+        case 1:
+            return -0x1.921fb6p-1f;
+        case 2:
+            return 0x1.921fb6p-1f;
+        case 3:
+            return -0x1.2d97c8p+1f;
+        case 4:
+            return 0x1.2d97c8p+1f;
+    }
+    return 0.0f;
+}
+constexpr int kNoAllowedBodyDirection = 5;
+HDN int ForceIntoAllowedBodyDirectionIndex(const Vec3 &src) {
+    float best = -1.0f;
+    int bi = kNoAllowedBodyDirection;
+    for (int i = 0; i < 5; i++) {
+        float d = AllowedBodyDir(i).Dot(src);
+        if (d > best) {
+            best = d;
+            bi = i;
+        }
+    }
+    return bi;
+}
+HD Vec3 ForceIntoAllowedBodyDirectionVector(const Vec3 &src) { return AllowedBodyDir(ForceIntoAllowedBodyDirectionIndex(src)); }
+
+// Ground-plane movement in m/s at `frame` of a position list of two frames or more.
+HDN Vec3 MovementAtFrame(const Vec3 *pos, int count, uint32_t frame, uint32_t smooth) {
+    if (frame == (uint32_t)(count - 1)) return (pos[count - 1] - pos[count - 2]).Get2D() * 100.0f;
+    if (frame == 0) return (pos[1] - pos[0]).Get2D() * 100.0f;
+    Vec3 total;
+    uint32_t n = 0;
+    for (int f = (int)(frame - smooth); f <= (int)(frame + smooth); f++) {
+        if (f > 0 && f < count) {
+            total += (pos[f] - pos[f - 1]).Get2D() * 100.0f;
+            n++;
+        }
+    }
+    if (n > 0) total /= Vec3((float)n);
+    return total;
+}
+
+HDN void CalculateSpatialState(const Ctx &c, Humanoid &h) {
+    AnimationState &cur = h.anim;
+    const Anim &a = c.A(cur.anim);
+    SpatialState &s = h.spatial;
+    Vec3 position;
+    if ((uint32_t)cur.positions.count > (uint32_t)cur.frameNum) {
+        position = h.startPos + cur.positions[cur.frameNum] + cur.actionSmuggleOffset + cur.actionSmuggleSustainOffset +
+                   cur.movementSmuggleOffset;
+    } else {
+        Quat o;
+        GetKeyFrame(c, a, kBpPlayer, cur.frameNum, o, position);
+        position.v[2] = 0.0f;
+        position = h.startPos + position.Rotated2D(h.startAngle.value()) + cur.actionSmuggleOffset +
+                   cur.actionSmuggleSustainOffset + cur.movementSmuggleOffset;
+    }
+    if (cur.frameNum > 12) s.foot = a.outgoingFoot;
+    s.actualMovement = (position - h.prevPosition2D) * 100.0f;
+    s.physicsMovement = s.actualMovement - (s.actionSmuggleMovement) - (s.movementSmuggleMovement) -
+                        (s.positionOffsetMovement * 0.5f);
+    s.animationMovement = s.physicsMovement;
+    if (cur.positions.count > 0)
+        s.animationMovement =
+            MovementAtFrame(c.t->positions + a.posFirst, a.posCount, cur.frameNum, 1).Rotated2D(h.startAngle.value());
+    s.movement = s.physicsMovement;
+    Vec3 bodyPos;
+    Quat bodyOri;
+    float z;
+    GetKeyFrameZ(c, a, kBpBody, cur.frameNum, bodyOri, bodyPos, z);
+    Vec3 bodyDir = Vec3(0, -1, 0).Rotated2D(z + h.startAngle.value() + cur.rotationSmuggleOffset.value());
+    s.floatVelocity = s.movement.Length();
+    s.velocityCat = VelocityCat(s.floatVelocity);
+    if (s.velocityCat != kVelIdle) s.directionVec = s.movement.Normalized();
+    else s.directionVec = bodyDir;
+    s.position = position;
+    s.angle.set(ModulateIntoRange(-PI, PI, FixAngle(s.directionVec.Angle2D())));
+    int bd = 0;
+    float nonQuantized = AllowedBodyDirAngle(0);
+    if (s.velocityCat != kVelIdle) {
+        Vec3 adapted = bodyDir.Rotated2D(-s.angle.value());
+        float rel = adapted.Angle2D(Vec3(0, -1, 0));
+        nonQuantized = rel;
+        if (s.velocityCat == kVelSprint && fabsf(rel) >= 0.125f * PI) {
+            adapted = Vec3(0, -1, 0).Rotated2D(0.12f * PI * SignSide(rel));
+            nonQuantized = adapted.Angle2D(Vec3(0, -1, 0));
+        } else if (s.velocityCat == kVelWalk && fabsf(rel) >= 0.5f * PI) {
+            adapted = Vec3(0, -1, 0).Rotated2D(0.495f * PI * SignSide(rel));
+            nonQuantized = adapted.Angle2D(Vec3(0, -1, 0));
+        }
+        s.relBodyDirectionVecNonQuantized = adapted;
+        bd = ForceIntoAllowedBodyDirectionIndex(adapted);
+    } else {
+        s.relBodyDirectionVecNonQuantized = Vec3(0, -1, 0);
+    }
+    s.relBodyDirectionVec = AllowedBodyDir(bd);
+    s.relBodyAngle.set(AllowedBodyDirAngle(bd));
+    s.relBodyAngleNonQuantized.set(nonQuantized);
+    s.bodyDirectionVec = s.relBodyDirectionVec.Rotated2D(s.angle.value());
+    s.bodyAngle.set(s.bodyDirectionVec.Angle2D(Vec3(0, -1, 0)));
+    h.prevPosition2D = position;
+}
+
+}  // namespace eng

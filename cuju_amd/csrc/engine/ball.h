@@ -1,0 +1,452 @@
+// Ball flight, the earliest reach times of players, and player possession.
+// Semantics: include/cuju/ball.h:23-348 (prediction), include/cuju/ai_time.h:97-239 (time needed,
+// the device form), include/cuju/possession.h:35-123 (scan),
+// include/cuju/simulation/player_possession.h:15-126, include/cuju/simulation/ball_touch.h:17-143.
+#pragma once
+
+#include "world.h"
+
+namespace eng {
+
+struct BallSpatial {
+    Vec3 momentum;
+    Quat rotationPerMs;
+};
+
+// Entry k of `predictions` is the position after 10k ms. When the first step lands where the last
+// tick predicted, the predictions shift down one entry instead, at most `validPredictions` times.
+HDN BallSpatial BallCalculatePrediction(Ball &ball, bool ballIsInGoal) {
+    const float bounce = 0.62f, linearBounce = 0.06f, drag = 0.015f, friction = 0.04f,
+                linearFriction = 1.6f, gravity = -9.81f, grassHeight = 0.025f, dt = 0.01f;
+    BallSpatial out;
+    Vec3 nextPos = ball.positionBuffer;
+    Quat nextOri = ball.orientationBuffer;
+    Vec3 mom = ball.momentum;
+    Quat rot = ball.rotationPerMs;
+    ball.predictions[0] = nextPos;
+    bool firstTime = true, useCache = false;
+    Vec3 angles;
+    bool anglesValid = false;
+    auto curAngles = [&]() {
+        if (!anglesValid) {
+            rot.Angles(angles.v[0], angles.v[1], angles.v[2]);
+            anglesValid = true;
+        }
+        return angles;
+    };
+    ball.touchesNet = false;
+    for (uint32_t t = 10; t < kBallPredictionSpanMs + kCachedPredictions * 10; t += 10) {
+        if (useCache) {
+            // GRF: the last shift reads predictions[400], which no tick writes.
+            ball.predictions[t / 10] = ball.predictions[t / 10 + 1];
+            continue;
+        }
+        float frictionFactor = 0.0f;
+        mom.v[2] = mom.v[2] + gravity * dt;
+        float vel = mom.Length();
+        float velDragged = vel - drag * (vel * vel) * dt;
+        mom = mom.Normalized(0) * velDragged;
+        float bottom = nextPos.v[2] - 0.11f;
+        float grass = Clamp(1.0f - (bottom / grassHeight), 0.0f, 1.0f);
+        grass = libm::PowfPos(grass, 0.7f);
+        if (nextPos.v[2] < 0.11f) {
+            if (mom.v[2] < 0.0f) {
+                frictionFactor = NormalizedClamp(-mom.v[2] - 0.5f, 0.0f, 12.0f);
+                mom.v[2] = -mom.v[2] * bounce;
+                float bv = mom.v[2] - linearBounce;
+                mom.v[2] = bv > 0.0f ? bv : 0.0f;
+            }
+            nextPos.v[2] = 0.11f;
+        }
+        if (nextPos.v[2] < 0.11f + grassHeight) {
+            float af = (friction * grass);
+            Vec3 hm = mom.Get2D();
+            float hv = hm.Length();
+            float nv = hv - af * (hv * hv) * dt;
+            nv = Clamp(nv - (linearFriction * grass * dt), 0.0f, 100000.0f);
+            hm.Normalize(Vec3(0));
+            hm *= nv;
+            mom.v[0] = hm.v[0];
+            mom.v[1] = hm.v[1];
+        }
+        const float netExponent = 2.6f, powerFactor = 1.8f, postAbsorb = 0.8f, ballR = 0.11f,
+                    postR = 0.07f, netAbsorb = 0.95f;
+        // GRF: the posts and the crossbar act on the first step only.
+        if (firstTime) {
+            if (nextPos.v[2] < kGoalHeight + ballR + postR &&
+                (nextPos.Get2D().Absolute() - Vec3(kPitchHalfLength, kGoalHalfWidth, 0)).Length() < ballR + postR) {
+                float sx = nextPos.v[0] < 0 ? -kPitchHalfLength : kPitchHalfLength;
+                float sy = nextPos.v[1] < 0 ? -kGoalHalfWidth : kGoalHalfWidth;
+                Vec3 fallback = nextPos.v[0] < 0 ? Vec3(1, 0, 0) : Vec3(-1, 0, 0);
+                Vec3 post(sx, sy, 0);
+                Vec3 normal = (nextPos.Get2D() - post).Normalized(fallback);
+                float z = nextPos.v[2];
+                nextPos = post + normal * (postR + ballR);
+                nextPos.v[2] = z;
+                mom = (mom.Get2D().Normalized(normal) + (normal * 1.1f)).Normalized() * mom.Get2D().Length() * postAbsorb +
+                      (Vec3(0, 0, 1) * mom.v[2]);
+            }
+            Vec3 xz = nextPos * Vec3(1, 0, 1);
+            if ((xz.Absolute() - Vec3(kPitchHalfLength, 0, kGoalHeight)).Length() < ballR + postR &&
+                fabsf(nextPos.v[1]) < kGoalHalfWidth + ballR + postR) {
+                Vec3 bar = nextPos.v[0] < 0 ? Vec3(-kPitchHalfLength, 0, kGoalHeight) : Vec3(kPitchHalfLength, 0, kGoalHeight);
+                Vec3 fallback = nextPos.v[0] < 0 ? Vec3(0, 0, 1) : Vec3(0, 0, -1);
+                Vec3 normal = (xz - bar).Normalized(fallback);
+                float y = nextPos.v[1];
+                nextPos = bar + normal * (postR + ballR);
+                nextPos.v[1] = y;
+                Vec3 mxz = mom * Vec3(1, 0, 1);
+                mom = (mxz.Normalized(normal) + (normal * 1.1f)).Normalized() * mxz.Length() * postAbsorb +
+                      (Vec3(0, 1, 0) * mom.v[1]);
+            }
+        }
+        // GRF: the netting too acts on the first step only.
+        if (t <= 10) {
+            int inGoal = ballIsInGoal ? 1 : -1;
+            bool behind = fabsf(nextPos.v[0]) > kPitchHalfLength + 0.11f;
+            bool beforeBack = fabsf(nextPos.v[0]) < kPitchHalfLength + kGoalDepth - 0.11f;
+            bool below = nextPos.v[2] < kGoalHeight + 0.11f;
+            bool between = fabsf(nextPos.v[1]) < kGoalHalfWidth - 0.11f;
+            if (ballIsInGoal && !between && behind) {
+                float nd = Clamp(fabsf(fabsf(nextPos.v[1]) - kGoalHalfWidth), 0, 1);
+                float power = libm::powf(nd, netExponent) * -SignSide(nextPos.v[1]) * inGoal;
+                float tension = Clamp((fabsf(mom.v[0]) - kPitchHalfLength) * 2.0f, 0.0f, 1.0f);
+                float apf = powerFactor + (1.0f - tension) * 3.0f;
+                mom.v[1] = mom.v[1] * netAbsorb + power * apf * (100 * dt);
+                if (t == 10) ball.touchesNet = true;
+            }
+            if (ballIsInGoal && !beforeBack && behind) {
+                float nd = Clamp(fabsf(fabsf(nextPos.v[0]) - (kPitchHalfLength + kGoalDepth)), 0, 1);
+                float power = libm::powf(nd, netExponent) * -SignSide(nextPos.v[0]) * inGoal;
+                mom.v[0] = mom.v[0] * netAbsorb + power * powerFactor * (100 * dt);
+                if (t == 10) ball.touchesNet = true;
+            }
+            if (ballIsInGoal && !below && behind) {
+                float nd = Clamp(fabsf(fabsf(nextPos.v[2]) - kGoalHeight), 0, 1);
+                float power = libm::powf(nd, netExponent) * -inGoal;
+                float tension = Clamp((fabsf(mom.v[0]) - kPitchHalfLength) * 2.0f, 0.0f, 1.0f);
+                float apf = powerFactor + (1.0f - tension) * 3.0f;
+                mom.v[2] = mom.v[2] * netAbsorb + power * apf * (100 * dt);
+                if (t == 10) ball.touchesNet = true;
+            }
+        }
+        if (nextPos.v[2] < 0.11f + grassHeight) {
+            const float radius = 0.11f;
+            float avx = mom.v[1] / radius, avy = mom.v[0] / radius;
+            Quat rx, ry;
+            rx.SetAngleAxis(Clamp(avx * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(-1, 0, 0));
+            ry.SetAngleAxis(Clamp(avy * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(0, 1, 0));
+            Quat ground = rx * ry;
+            Quat o2n = rot.RotationTo(ground).Normalized();
+            float change = fabsf(o2n.RotationAngle(Quat::Identity())) * 1000.0f;
+            float maxChange = 1.0f * PI * grass;
+            if (frictionFactor > 0.0f) maxChange += 4.0f * PI;
+            float factor = 1.0f;
+            if (change > maxChange) factor = maxChange / change;
+            if (factor < 1.0f) o2n = o2n.RotationMultipliedBy(factor);
+            Quat newRot = o2n * rot;
+            const Vec3 a = curAngles();
+            float x = -a.v[0], y = a.v[1];
+            Vec3 rm;
+            rm.v[0] = y * radius * 1000.0f;
+            rm.v[1] = x * radius * 1000.0f;
+            float rb = 0.01f;
+            rb *= grass;
+            if (frictionFactor > 0.0f) rb += 0.5f * frictionFactor;
+            rb = Clamp(rb, 0.0f, 1.0f);
+            mom.v[0] = mom.v[0] * (1.0f - rb) + rm.v[0] * rb;
+            mom.v[1] = mom.v[1] * (1.0f - rb) + rm.v[1] * rb;
+            rot = newRot;
+            anglesValid = false;
+        }
+        {
+            Vec3 spin = curAngles();
+            spin *= 10.0f;
+            float swerve = NormalizedClamp(mom.Length(), 0.0f, 70.0f);
+            swerve = libm::PowfPos(libm::sinf(swerve * PI * 0.94f), 2.6f);
+            Vec3 adapted = mom.Normalized(0) * swerve * 30.0f;
+            Vec3 sw = adapted.Cross(-spin) * 1.0f;
+            mom += sw * dt;
+        }
+        nextPos += mom * dt;
+        if (t == 10) {
+            Vec3 rv = curAngles();
+            rv *= dt / 0.001f;
+            Quat step;
+            step.SetAngles(rv.v[0], rv.v[1], rv.v[2]);
+            nextOri = step * nextOri;
+            out.momentum = mom;
+            out.rotationPerMs = rot;
+            ball.orientationPrediction = nextOri;
+            if (ball.validPredictions > 0 && ball.predictions[2] == nextPos) {
+                ball.validPredictions--;
+                useCache = true;
+            } else {
+                ball.validPredictions = kCachedPredictions;
+            }
+        }
+        ball.predictions[t / 10] = nextPos;
+        firstTime = false;
+    }
+    return out;
+}
+
+HD void BallRecalculatePrediction(World &w) {
+    BallMaterialize(w.match.ball);
+    BallCalculatePrediction(w.match.ball, w.match.ballIsInGoal);
+}
+
+HDN void BallProcess(Ball &b, bool inGoal) {
+    BallMaterialize(b);
+    BallSpatial s = BallCalculatePrediction(b, inGoal);
+    b.momentum = s.momentum;
+    b.rotationPerMs = s.rotationPerMs;
+    b.positionBuffer = BallPredictRaw(b.predictions, 10);
+    b.orientationBuffer = b.orientationPrediction;
+    auto &h = b.positionHistory;
+    if (h.count < (int)kBallHistorySize) {
+        h.push_back(b.positionBuffer);
+    } else {
+        for (int i = 1; i < h.count; i++) h[i - 1] = h[i];
+        h[h.count - 1] = b.positionBuffer;
+    }
+}
+
+// `clamp((float)(10 k) / (float)700, 0, 1)`, computed in float once per step index.
+HD float TimeNeededBias(uint32_t step) { return Clamp((float)(step * 10) / (float)700, 0, 1); }
+
+struct TimeNeeded {
+    uint32_t usual = 0, optimistic = 0;
+};
+
+HD uint32_t DirectTimeMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &target, float maxVel) {
+    return (uint32_t)TruncToInt32(roundf((target - (pos + mov * 0.2f)).Length() / (maxVel * 0.75f) * 1000));
+}
+
+// Velocities in m/s; `maxTime` is UINT32_MAX for no limit.
+HDN TimeNeeded GetTimeNeededMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &target, float maxVel,
+                               bool precise, uint32_t maxTime) {
+    TimeNeeded r;
+    if ((pos - target).Length() > (precise ? 48.0f : 16.0f)) {
+        r.usual = DirectTimeMs(pos, mov, target, maxVel);
+        r.optimistic = r.usual - 200;
+        return r;
+    }
+    Vec3 cur = pos, cm = mov;
+    if (cm.Length() > kIdleDribbleSwitch) {
+        cur += cm.Normalized() * 0.1f;
+        cur += cm * 0.01f;
+    } else {
+        cur += (target - pos).Normalized(0) * 0.1f;
+    }
+    uint32_t time = 0;
+    const uint32_t step = 10;
+    float usualR = 0.28f, optR = 0.9f, resultingUsualR = usualR;
+    bool foundOpt = false;
+    float amv = maxVel * 0.94f;
+    while (true) {
+        float bias = TimeNeededBias(time / step);
+        if (bias >= 1.0f) {
+            float rem = Clamp((target - cur).Length() - usualR, 0.0f, 100000.0f);
+            r.usual = TruncToUint32((float)time + (rem / amv) * 1000);
+            resultingUsualR = usualR + rem;
+            if (!foundOpt) {
+                float ro = Clamp((target - cur).Length() - optR, 0.0f, 100000.0f);
+                r.optimistic = TruncToUint32((float)time + (ro / amv) * 1000);
+            }
+            break;
+        }
+        cm.v[0] = mov.v[0] * (1.0f - bias);
+        cm.v[1] = mov.v[1] * (1.0f - bias);
+        cur.v[0] += cm.v[0] * step * 0.001f;
+        cur.v[1] += cm.v[1] * step * 0.001f;
+        usualR += amv * bias * step * 0.001f;
+        optR += amv * bias * step * 0.001f;
+        float d2 = (target - cur).SquaredLength();
+        if ((d2 < optR * optR || (maxTime != (uint32_t)-1 && time > maxTime)) && !foundOpt) {
+            r.optimistic = time;
+            foundOpt = true;
+        }
+        if (d2 < usualR * usualR || (maxTime != (uint32_t)-1 && time > maxTime)) {
+            resultingUsualR = usualR;
+            r.usual = time;
+            break;
+        }
+        time += step;
+    }
+    if (maxTime != (uint32_t)-1 && time > maxTime) {
+        uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
+        r.usual = def > ext ? def : ext;
+        if (!foundOpt) r.optimistic = r.usual;
+        return r;
+    }
+    if (r.usual == 0) {
+        r.usual = (uint32_t)TruncToInt32(roundf(Clamp((target - pos).Length() / resultingUsualR, 0.0f, 1.0f) * 10));
+        r.optimistic = r.usual;
+    }
+    return r;
+}
+
+struct ScanResult {
+    uint32_t timeToBall, timeToBallOptimistic;
+};
+
+HD Vec3 PredFlip(const Vec3 *pred, bool flip, int ms) {
+    Vec3 v = BallPredictRaw(pred, ms);
+    if (flip) v.Mirror();
+    return v;
+}
+
+HDN ScanResult PossessionScan(const Vec3 *pred, bool flip, const Vec3 &pos, const Vec3 &mov, float maxVel,
+                              bool precise, uint32_t start) {
+    ScanResult s;
+    {
+        uint32_t latest = kBallPredictionSpanMs;
+        uint32_t direct = TruncToUint32(roundf(
+            (PredFlip(pred, flip, kBallPredictionSpanMs - 10).Get2D() - (pos + mov * 0.2f)).Length() /
+            (maxVel * 0.75f) * 1000));
+        s.timeToBall = latest > direct ? latest : direct;
+    }
+    s.timeToBallOptimistic = s.timeToBall;
+    bool refine = false;
+    uint32_t stepMs = 10, prev = 0;
+    for (uint32_t ms = start; ms < kBallPredictionSpanMs; ms += stepMs) {
+        if (PredFlip(pred, flip, ms).v[2] < 1.5f) {
+            const Vec3 target = PredFlip(pred, flip, ms).Get2D();
+            TimeNeeded r = GetTimeNeededMs(pos, mov, target, maxVel, precise, ms);
+            if (r.optimistic <= ms && ms < s.timeToBallOptimistic) s.timeToBallOptimistic = ms;
+            if (r.usual <= ms) {
+                if (!refine) {
+                    ms = prev;
+                    stepMs = 10;
+                    refine = true;
+                } else {
+                    s.timeToBall = ms;
+                    break;
+                }
+            }
+        }
+        if (!refine) {
+            float dist = (pos - PredFlip(pred, flip, ms).Get2D()).Length() + 0.2f;
+            uint32_t toGo = (uint32_t)TruncToInt32(roundf((dist / 50.0f) * 1000.0f));
+            stepMs = TruncToUint32(Clamp((float)toGo, 10, 500));
+            stepMs = (stepMs / 10) * 10;
+        } else {
+            stepMs = 10;
+        }
+        prev = ms;
+    }
+    return s;
+}
+
+HDN bool HasPossession(const World &w, int p) {
+    const Ball &b = w.match.ball;
+    const SpatialState &s = Sp(w, p);
+    if ((double)(s.position - BallPredict(b, 0)).Length() > 5.0) return false;
+    if ((double)fabsf(BallPredict(b, 0).v[2]) > 0.5) return false;
+    bool distOk = true;
+    Vec3 center = s.position + s.movement * 0.05f + s.directionVec * 0.1f;
+    if ((BallPredict(b, 0).Get2D() - center).Length() > 1.0f) distOk = false;
+    bool movOk = true;
+    Vec3 bm = (BallPredict(b, 10) - BallPredict(b, 0)) * 100.0f;
+    if ((bm - s.movement).Length() > 6.0f) movOk = false;
+    return distOk && movOk;
+}
+
+HD bool IsPassOrShot(int f) { return f == kFnShortPass || f == kFnLongPass || f == kFnHighPass || f == kFnShot; }
+
+HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p) {
+    Player &ps = w.match.players[p];
+    const Humanoid &h = ps.base.humanoid;
+    const Ball &b = w.match.ball;
+    const Team &team = TeamOfPlayer(w, p);
+    const Team &opp = OpponentTeamOfPlayer(w, p);
+    const Vec3 pos = h.spatial.position, mov = h.spatial.movement;
+    const float maxVel = GetMaximumVelocity(sd, p);
+    ps.timeToBallPreviousMs = ps.timeToBallMs;
+    uint32_t start = 0;
+    const bool touchPending = h.anim.frameNum < h.anim.touchFrame;
+    if (IsPassOrShot(h.anim.functionType) && !touchPending) start = 500;
+    bool precise = team.designatedTeamPossessionPlayer == p;
+    ScanResult s = PossessionScan(b.predictions, b.lazyFlip, pos, mov, maxVel, precise, start);
+    ps.timeToBallMs = s.timeToBall;
+    ps.timeToBallOptimisticMs = s.timeToBallOptimistic;
+    if (h.anim.touchFrame != -1 && touchPending) {
+        uint32_t at = (uint32_t)((h.anim.touchFrame - h.anim.frameNum) * 10);
+        if (at < ps.timeToBallMs) ps.timeToBallMs = at;
+        ps.timeToBallOptimisticMs = ps.timeToBallMs;
+    }
+    if (ps.timeToBallMs < kDefaultTouchOffsetMs) {
+        ps.timeToBallMs = TruncToUint32(
+            NormalizedClamp(((pos + mov * (float)(kDefaultTouchOffsetMs * 0.001)) - BallPredict(b, kDefaultTouchOffsetMs).Get2D()).Length(),
+                            0.0f, 0.6f) *
+            kDefaultTouchOffsetMs);
+        ps.timeToBallOptimisticMs = ps.timeToBallMs;
+    }
+    if (IsPassOrShot(h.anim.functionType) && !touchPending) ps.hasPossession = false;
+    else ps.hasPossession = HasPossession(w, p);
+    ps.hasBestPossession = ps.hasPossession && opp.timeToBallMs > (int32_t)ps.timeToBallMs;
+    ps.hasUniquePossession = ps.hasPossession && !opp.hasPossession;
+    if (w.match.ballRetainer == p) {
+        ps.timeToBallMs = 1;
+        ps.timeToBallOptimisticMs = 1;
+        ps.desiredTimeToBallMs = (int32_t)ps.timeToBallMs;
+        ps.hasPossession = ps.hasBestPossession = ps.hasUniquePossession = true;
+    } else if (w.match.ballRetainer != -1) {
+        ps.hasPossession = ps.hasBestPossession = ps.hasUniquePossession = false;
+    }
+}
+
+HDN void TeamUpdatePossessionStatistics(World &w, const Ctx &c, int teamID) {
+    for (int p = 0; p < w.match.playerCount; p++)
+        if (w.playerTeamID[p] == teamID && w.match.players[p].base.isActive) PlayerUpdatePossessionStatistics(w, *c.sd, p);
+    Team &t = TeamByID(w, teamID);
+    t.hasPossession = false;
+    t.timeToBallMs = 100000;
+    for (int p = 0; p < w.match.playerCount; p++) {
+        if (w.playerTeamID[p] != teamID || !w.match.players[p].base.isActive) continue;
+        const Player &ps = w.match.players[p];
+        if (ps.hasPossession) t.hasPossession = true;
+        if ((int)ps.timeToBallMs < t.timeToBallMs) t.timeToBallMs = (int)ps.timeToBallMs;
+    }
+}
+
+HDN void BallTouch(World &w, const Ctx &c, const Vec3 &target) {
+    Ball &b = w.match.ball;
+    b.validPredictions = 0;
+    if (b.positionBuffer.v[2] < 0.11f) b.positionBuffer.v[2] = 0.11f;
+    b.momentum = target;
+    // GRF: the predictions run twice, and each run changes the count of valid cached ones.
+    BallRecalculatePrediction(w);
+    BallRecalculatePrediction(w);
+    if (w.match.mentalImages.count > 0) {
+        MentalImage &m = w.match.mentalImages[0];
+        m.ballPredictions.count = kBallPredictionSpanMs / 10;
+        for (int i = 0; i < (int)(kBallPredictionSpanMs / 10); i++) m.ballPredictions[i] = b.predictions[i];
+        m.lazyFlip = b.lazyFlip;
+    }
+    TeamUpdatePossessionStatistics(w, c, w.FirstTeamID());
+    TeamUpdatePossessionStatistics(w, c, 1 - w.FirstTeamID());
+}
+
+HD void BallSetRotation(World &w, float x, float y, float z, float bias = 1.0f) {
+    Quat rx, ry, rz;
+    rx.SetAngleAxis(Clamp(x * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(-1, 0, 0));
+    ry.SetAngleAxis(Clamp(y * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(0, 1, 0));
+    rz.SetAngleAxis(Clamp(z * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(0, 0, 1));
+    Quat tmp = rx * ry * rz;
+    Ball &b = w.match.ball;
+    b.rotationPerMs = b.rotationPerMs.Slerp(bias, tmp);
+    BallRecalculatePrediction(w);
+}
+
+HD void BallSetPosition(World &w, const Vec3 &target) {
+    Ball &b = w.match.ball;
+    b.validPredictions = 0;
+    b.positionBuffer = target;
+    b.momentum = Vec3(0);
+    BallSetRotation(w, 0, 0, 0, 1.0f);
+    b.positionHistory.count = 0;
+}
+
+}  // namespace eng

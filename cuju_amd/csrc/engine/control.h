@@ -1,0 +1,223 @@
+// Keyboard input of the gamers (agents), and which player each gamer controls.
+// Semantics: include/cuju/simulation/human_controller.h:11-117,
+// include/cuju/simulation/team_select.h:13-207, include/cuju/batch/agent_setup.h:15-70.
+#pragma once
+
+#include "world.h"
+
+namespace eng {
+
+enum Button {
+    kBtnLongPass,
+    kBtnHighPass,
+    kBtnShortPass,
+    kBtnShot,
+    kBtnKeeperRush,
+    kBtnSliding,
+    kBtnPressure,
+    kBtnTeamPressure,
+    kBtnSwitch,
+    kBtnSprint,
+    kBtnDribble,
+    kBtnCount
+};
+constexpr float kStickDeadzone = 0.75f;
+constexpr int kTeamControllers = 11;
+
+HD HumanGamer &HumanGamerOf(World &w, int p) { return GamerByGlobal(w, w.match.players[p].base.externalController); }
+// The keyboard stores its direction times its mirror sign and reports it the same way.
+HD Vec3 KeyboardDirection(const KeyboardState &k) { return k.direction; }
+
+HD float GetLastSwitchBias(World &w, PlayerControllerState &c) {
+    if (!w.match.inPlay || w.match.inSetPiece) c.lastSwitchTimeMs = (uint64_t)(int64_t)-10000;
+    if (c.lastSwitchTimeDurationMs > 0)
+        return 1.0f - Clamp((w.match.actualTimeMs - c.lastSwitchTimeMs) / (float)c.lastSwitchTimeDurationMs, 0.0f, 1.0f);
+    return 0.0f;
+}
+
+HDN void HumanGetKeyboardInput(World &w, int p, Vec3 &dir, float &vel) {
+    HumanControllerState &hc = HumanGamerOf(w, p).controller;
+    const SpatialState &s = Sp(w, p);
+    dir = KeyboardDirection(hc.keyboard);
+    const Vec3 pos = s.position;
+    float &dx = dir.v[0], &dy = dir.v[1];
+    // Each clamp is std::min(0, x) or std::max(0, x); the expression never gives -0.
+    if (pos.v[0] > kPitchHalfLength) dx = ((dx < 0.0f) ? dx : 0.0f) + 0.0f;
+    if (pos.v[0] < -kPitchHalfLength) dx = (0.0f < dx) ? dx : 0.0f;
+    if (pos.v[1] > kPitchHalfWidth) dy = ((dy < 0.0f) ? dy : 0.0f) + 0.0f;
+    if (pos.v[1] < -kPitchHalfWidth) dy = (0.0f < dy) ? dy : 0.0f;
+    if (dir.Length() < kStickDeadzone) {
+        dir = s.directionVec;
+        vel = kIdleVelocity;
+    } else {
+        const bool *b = hc.keyboard.buttons;
+        if (b[kBtnSprint]) vel = kSprintVelocity;
+        else if (b[kBtnDribble]) vel = kDribbleVelocity;
+        else if (b[kBtnSwitch] && w.match.designatedPossessionPlayer == p) vel = kIdleVelocity;
+        else vel = kWalkVelocity;
+        dir.Normalize();
+    }
+    if (GetLastSwitchBias(w, hc.base) > 0.0f) {
+        float influence = 0.5f;
+        float sb = libm::powf(GetLastSwitchBias(w, hc.base), 0.7f);
+        Vec3 cur = s.directionVec * PlayerFloatVelocity(w, p);
+        Vec3 manual = dir * vel;
+        Vec3 res = cur * sb * influence + manual * (1.0f - sb * influence);
+        dir = res.Normalized(dir);
+        vel = res.Length();
+    }
+}
+HD float HumanGetFloatVelocity(World &w, int p) {
+    Vec3 d;
+    float v = 0;
+    HumanGetKeyboardInput(w, p, d, v);
+    return v;
+}
+HD Vec3 HumanGetDirection(World &w, int p) { return KeyboardDirection(HumanGamerOf(w, p).controller.keyboard).Normalized(Sp(w, p).directionVec); }
+
+// GRF: sprint, dribble and the defensive buttons are sticky; the others release.
+HD void ReleaseNonStickyButtons(KeyboardState &k) {
+    const int bs[6] = {kBtnLongPass, kBtnHighPass, kBtnShortPass, kBtnShot, kBtnSliding, kBtnSwitch};
+    for (int b : bs) k.buttons[b] = false;
+}
+HD void KeyboardReleaseNonStickyButtons(World &w, int g) {
+    ReleaseNonStickyButtons(GamerByGlobal(w, g).controller.keyboard);
+    ReleaseNonStickyButtons(w.match.secondKeyboardCopies[g]);
+}
+
+HDN void HumanControllerReset(World &w, int g) {
+    HumanControllerState &c = GamerByGlobal(w, g).controller;
+    c.actionMode = 0;
+    c.gaugeMs = 0;
+    c.actionButton = kBtnShortPass;
+    c.actionBufferTimeMs = 0;
+    c.base.lastSwitchTimeMs = (uint64_t)(int64_t)-10000;
+    c.base.lastSwitchTimeDurationMs = 300;
+    c.lastSteadyDirectionSnapshotTimeMs = 0;
+    c.steadyDirection = Vec3(0, -1, 0);
+    c.previousDirection = Vec3(0, -1, 0);
+    c.base.fadingTeamPossessionAmount = 1.0;
+    KeyboardReleaseNonStickyButtons(w, g);
+}
+HD void HumanControllerSetPlayer(World &w, int g, int p) {
+    HumanControllerState &c = GamerByGlobal(w, g).controller;
+    c.base.lastSwitchTimeMs = w.match.actualTimeMs;
+    c.base.player = p;
+    // The state stores a team as its slot.
+    c.base.team = TeamSlot(w, w.playerTeamID[p]);
+    c.base.opponentTeam = TeamSlot(w, 1 - w.playerTeamID[p]);
+}
+// `g` is a global gamer index, or -1 to hand the player back to the AI.
+HD void SetExternalController(World &w, int p, int g) {
+    Player &ps = w.match.players[p];
+    ps.base.externalController = g;
+    if (g >= 0) {
+        HumanControllerReset(w, g);
+        HumanControllerSetPlayer(w, g, p);
+    } else {
+        ps.controller.lastDesiredDirection = Vec3(0);
+        ps.controller.lastDesiredVelocity = 0;
+    }
+}
+HDN void HumanGamerSetSelectedPlayer(World &w, int g, int p) {
+    HumanGamer &gm = GamerByGlobal(w, g);
+    if (p >= 0 && w.match.players[p].base.externalController >= 0) return;
+    if (gm.selectedPlayer >= 0) {
+        if (gm.selectedPlayer == p) return;
+        SetExternalController(w, gm.selectedPlayer, -1);
+    }
+    if (p >= 0) {
+        gm.selectedPlayer = p;
+        SetExternalController(w, p, g);
+    } else {
+        gm.selectedPlayer = -1;
+    }
+}
+HDN bool TeamSelectPlayer(World &w, const Ctx &c, int teamID, int p) {
+    Team &t = TeamByID(w, teamID);
+    if (Formation(w, c, p).controllable) {
+        t.mainSelectedPlayer = p;
+        if (w.match.players[p].base.externalController < 0 && t.gamers.count > 0) {
+            auto &sp = t.switchPriority;
+            int g = sp[0];
+            HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), p);
+            for (int i = 0; i + 1 < sp.count; i++) sp[i] = sp[i + 1];
+            sp[sp.count - 1] = g;
+        }
+    }
+    t.designatedTeamPossessionPlayer = p;
+    return true;
+}
+// A tie keeps the player first in the state.
+HDN int GetClosestPlayer(const World &w, const Ctx &c, int teamID, const Vec3 &pos, bool onlyAI, int except = -1,
+                         bool onlySelectable = false) {
+    float best = 10000;
+    int bp = -1;
+    for (int p = 0; p < w.match.playerCount; p++) {
+        if (w.playerTeamID[p] != teamID) continue;
+        if (!w.match.players[p].base.isActive || p == except) continue;
+        float d = (Sp(w, p).position - pos).Length();
+        if (d < best) {
+            if ((!onlyAI || !ExternalControllerActive(w, p)) && (!onlySelectable || Formation(w, c, p).controllable)) {
+                best = d;
+                bp = p;
+            }
+        }
+    }
+    return bp;
+}
+// A time in ms: the shortest of the players that enabled gamers control, or 10000.
+HD int HumanControlledToBallTime(const World &w, int teamID) {
+    const Team &t = TeamByID(w, teamID);
+    int best = 10000;
+    for (int g = 0; g < t.gamers.count; g++) {
+        const HumanGamer &gm = t.gamers[g];
+        if (gm.selectedPlayer >= 0 && !gm.controller.keyboard.disabled) {
+            int tt = (int)w.match.players[gm.selectedPlayer].timeToBallMs;
+            best = (tt < best) ? tt : best;
+        }
+    }
+    return best;
+}
+HDN bool TeamUpdateSwitch(World &w, const Ctx &c, int teamID) {
+    MatchState &m = w.match;
+    Team &t = TeamByID(w, teamID);
+    if (m.inPlay && t.gamers.count > 1) {
+        auto &sp = t.switchPriority;
+        int mine = sp[0];
+        if (t.gamers[mine].selectedPlayer == m.designatedPossessionPlayer) {
+            for (int i = 0; i + 1 < sp.count; i++) sp[i] = sp[i + 1];
+            sp[sp.count - 1] = mine;
+        }
+    }
+    if (m.inPlay && t.gamers.count > 0) {
+        int d = t.designatedTeamPossessionPlayer;
+        if (!ExternalControllerActive(w, d) && 3 * (int)m.players[d].timeToBallMs < HumanControlledToBallTime(w, teamID) &&
+            Formation(w, c, d).role != kRoleGoalkeeper) {
+            if (!TeamSelectPlayer(w, c, teamID, d)) return false;
+        }
+    }
+    if (m.inPlay && t.gamers.count > 0) {
+        int d = t.designatedTeamPossessionPlayer;
+        if (!ExternalControllerActive(w, d) && (m.players[d].hasUniquePossession || m.inSetPiece)) {
+            if (Formation(w, c, d).role != kRoleGoalkeeper)
+                if (!TeamSelectPlayer(w, c, teamID, d)) return false;
+        }
+    }
+    return true;
+}
+HDN void TeamHumanGamersSelectAnyone(World &w, const Ctx &c, int teamID) {
+    MatchState &m = w.match;
+    if (!m.inPlay) return;
+    Team &t = TeamByID(w, teamID);
+    if (t.mainSelectedPlayer == -1)
+        t.mainSelectedPlayer = GetClosestPlayer(w, c, teamID, BallPredict(m.ball, 0).Get2D(), true, -1, true);
+    for (int g = 0; g < t.gamers.count; g++) {
+        if (t.gamers[g].selectedPlayer == -1) {
+            int p = GetClosestPlayer(w, c, teamID, BallPredict(m.ball, 0).Get2D(), true, -1, true);
+            if (p >= 0) HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), p);
+        }
+    }
+}
+
+}  // namespace eng

@@ -1,0 +1,301 @@
+// Read-only tables of the simulation, laid out as flat arrays addressed by index so one host build
+// step produces them and a single copy moves them to HBM (every span is an index range, not a
+// pointer). Semantics follow include/cuju/animation/animation_data.h:21-155,
+// include/cuju/animation/animation_derived.h:54-98, include/cuju/animation/skeleton.h:17-45,
+// include/cuju/simulation/static_data.h:17-60 and the selection records of
+// include/cuju/simulation/select_animation.h:431-533.
+#pragma once
+
+#include "state.h"
+
+namespace eng {
+
+// ---- enumerations (GRF's; a state stores them as integers) ----------------------------------------
+enum Velocity { kVelIdle, kVelDribble, kVelWalk, kVelSprint };
+enum FunctionType {
+    kFnNone,
+    kFnMovement,
+    kFnBallControl,
+    kFnTrap,
+    kFnShortPass,
+    kFnLongPass,
+    kFnHighPass,
+    kFnHeader,
+    kFnShot,
+    kFnDeflect,
+    kFnCatch,
+    kFnInterfere,
+    kFnTrip,
+    kFnSliding,
+    kFnSpecial
+};
+enum TouchType { kTouchKicked, kTouchNonKicked, kTouchAccidental, kTouchNone };
+enum Role {
+    kRoleGoalkeeper,
+    kRoleCentreBack,
+    kRoleLeftBack,
+    kRoleRightBack,
+    kRoleDefensiveMid,
+    kRoleCentralMid,
+    kRoleLeftMid,
+    kRoleRightMid,
+    kRoleAttackingMid,
+    kRoleCentreForward
+};
+enum GameMode { kModeNormal, kModeKickOff, kModeGoalKick, kModeFreeKick, kModeCorner, kModeThrowIn, kModePenalty };
+enum StrictMovement { kStrictFalse, kStrictTrue, kStrictDynamic };
+enum BodyPart {
+    kBpMiddle,
+    kBpNeck,
+    kBpLeftThigh,
+    kBpRightThigh,
+    kBpLeftKnee,
+    kBpRightKnee,
+    kBpLeftAnkle,
+    kBpRightAnkle,
+    kBpLeftShoulder,
+    kBpRightShoulder,
+    kBpLeftElbow,
+    kBpRightElbow,
+    kBpBody,
+    kBpPlayer
+};
+enum Interrupt {
+    kIntNone,
+    kIntSwitch,
+    kIntSliding,
+    kIntBump,
+    kIntTrip,
+    kIntCheat,
+    kIntCancel,
+    kIntReQueue
+};
+// Animation type strings (GRF's e_AnimationString).
+enum AnimType {
+    kAtEmpty = 0,
+    kAtType = 5,
+    kAtTrap = 6,
+    kAtDeflect = 7,
+    kAtInterfere = 8,
+    kAtTrip = 9,
+    kAtShortPass = 10,
+    kAtLongPass = 11,
+    kAtShot = 12,
+    kAtSliding = 13,
+    kAtMovement = 14,
+    kAtSpecial = 15,
+    kAtBallControl = 16,
+    kAtHighPass = 17,
+    kAtCatch = 18
+};
+enum StateString { kStrEmpty, kStrLayBack, kStrLayFront, kStrLeftElbow, kStrRightElbow };
+enum Statistic {
+    kStatBalance,
+    kStatReaction,
+    kStatAcceleration,
+    kStatVelocity,
+    kStatStamina,
+    kStatAgility,
+    kStatShotPower,
+    kStatStandingTackle,
+    kStatSlidingTackle,
+    kStatBallControl,
+    kStatDribble,
+    kStatShortPass,
+    kStatHighPass,
+    kStatHeader,
+    kStatShot,
+    kStatVolley,
+    kStatCalmness,
+    kStatWorkRate,
+    kStatResilience,
+    kStatDefensivePositioning,
+    kStatOffensivePositioning,
+    kStatVision
+};
+constexpr int kStatistics = 22;
+
+// ---- static data of a scenario variant -------------------------------------------------------------
+struct PlayerData {
+    float stats[kStatistics];
+    float velocityStat;
+    float height;
+    int32_t skinColor;
+};
+struct StaticFormation {
+    int32_t role;
+    Vec3 position, startPosition;
+    bool lazy, controllable;
+};
+constexpr int kStaticEntries = kPlayers + 3;
+// Players in state order, then the referee and two linesmen.
+struct StaticData {
+    int32_t count;
+    PlayerData data[kStaticEntries];
+    StaticFormation formation[kStaticEntries];
+    float matchDurationFactor;
+    int32_t stableID[kStaticEntries];
+};
+
+// ---- skeleton -------------------------------------------------------------------------------------
+constexpr int kLocalRelative = 0, kLocalAbsolute = 1;
+struct SkelGeometry {
+    bool footOrLowerLeg;
+    int32_t localMode;
+    Vec3 position;
+    Quat rotation;
+    Vec3 scale;
+    Vec3 boxMin, boxMax;  // mesh space
+};
+struct SkelNode {
+    int32_t parent;
+    int32_t localMode;
+    Vec3 position;
+    Quat rotation;
+    Vec3 scale;
+    int32_t geometryCount;
+    SkelGeometry geometries[2];
+};
+struct Skeleton {
+    int32_t nodeMap[kBodyParts];
+    int32_t nodeCount;
+    SkelNode nodes[kHumanoidNodes];  // pre-order
+};
+
+// ---- animations -----------------------------------------------------------------------------------
+struct KeyFrame {
+    int32_t frame;
+    Quat orientation;
+    Vec3 position;
+};
+struct InterpEntry {
+    Quat orientation;
+    Vec3 position;
+    float angleZ;  // yaw of `orientation` by Quat::Angles
+};
+struct MiddleEntry {
+    Quat orientation;
+    Vec3 position;
+    Quat normalized;
+    bool normalizedKeepsZeros;  // squared length in [1e-6, 2): normalizing keeps every zero
+};
+struct NodeAnim {
+    int32_t bodyPart;
+    int32_t keyFirst, keyCount;
+    int32_t interpFirst;   // into interp[] and middle[], frames 0..frameCount+1
+    int32_t interpFrames;  // frameCount + 2
+};
+struct FootballKey {
+    int32_t frame;
+    Quat orientation;
+    Vec3 position;
+    float power;
+};
+struct Anim {
+    int32_t frameCount, currentFoot, animationType;
+    Vec3 translation, incomingMovement;
+    float incomingVelocity;
+    Vec3 outgoingMovement, outgoingDirection, incomingBodyDirection, outgoingBodyDirection;
+    float outgoingVelocity;
+    Radian outgoingAngle, incomingBodyAngle, outgoingBodyAngle;
+    int32_t outgoingFoot;
+    float idleLevel;
+    int32_t quadrantID;
+    float specialVar1, specialVar2;
+    bool lastDitch, baseAnimation;
+    int32_t outgoingSpecialState, incomingRetainState, incomingSpecialState;
+    int32_t nodeFirst, nodeCount;
+    bool hasFootball;
+    int32_t footballFirst, footballCount;
+    bool hasPositions;
+    int32_t posFirst, posCount;
+};
+struct Quadrant {
+    int32_t id;
+    Vec3 position;
+    int32_t velocity;
+    Radian angle;
+};
+// Values GRF parses from each animation's text variables at every use, parsed once on the host.
+struct AnimDerived {
+    double priorityAbsolute;
+    int32_t touchFrame;
+    float difficultyFactor;
+    bool tripTypeIsOne;
+    int32_t tripTypeRounded;
+    Vec3 bumpDirection, incomingBallDirection, ballDirection;
+    float incomingMaxDeviation, outgoingMaxDeviation;
+    bool outgoingRetainRaw;
+    int32_t outgoingRetainRawValue, incomingRetainRawValue;
+    int32_t outgoingRetainBodyPart, incomingRetainBodyPart;
+    int32_t forcedFootWhich;  // 0 none, 1 strong, 2 weak
+    bool touchFootLeft;
+    int32_t touchType;  // 0 kicked (foot or lower leg), 1 non-kicked
+    float touchMaxPowerFactor, touchDifficultyFactor;
+    // Animation-only terms of the crude selection, computed with the same functions.
+    Vec3 crudeOutDirectionRotated;
+    float crudeTurnAngle, crudeInBodyFixAbsolute;
+    Vec3 crudeOutBodyDirection;
+    bool crudeInBallNonzero;
+    Vec3 crudeInBallAdapted, crudeBallDirectionNormalized;
+};
+// Per-animation terms of the selection sorts, computed on the host with the same expressions.
+struct SelectionRecord {
+    float incomingBodyAngles[6];
+    float bodyTurnAngle;
+    int32_t incomingBodyIndex;
+    Vec3 preferredOutgoingDirection, preferredOutgoingMovement;
+    float preferredOutgoingAngle;
+    float lookAngle;
+    int32_t smoothedFirst;  // into smoothed[], -1 below two positions
+    bool ballDirectionFinite;
+};
+constexpr int kFunctionSlots = 16;
+constexpr int kMaxAnimations = 1536;  // the tables hold 1452
+constexpr int kCameraHistory = 150;
+constexpr int kCameraWeights = kCameraHistory * (kCameraHistory + 1) / 2;
+
+struct Tables {
+    const Anim *anims;
+    int32_t animCount;
+    const NodeAnim *nodes;
+    const KeyFrame *keys;
+    const InterpEntry *interp;
+    const MiddleEntry *middle;
+    const FootballKey *football;
+    const Vec3 *positions;
+    const Quadrant *quadrants;
+    int32_t quadrantCount;
+    Radian maxIncomingBallDeviation, maxOutgoingBallDeviation;
+    const AnimDerived *derived;
+    const SelectionRecord *selection;
+    const Vec3 *smoothed;
+    const int16_t *fnAnims;   // animations accepted per function type, ascending
+    const int32_t *fnOffset;  // kFunctionSlots + 1 entries
+    const float *cameraWeights;
+};
+
+// Per-match working memory for the animation selection: candidate lists, planned positions and
+// sort keys. One block per environment in HBM; every lane of the match's wave addresses the same
+// block, so it replaces the large per-thread stack arrays of a thread-per-match design.
+struct Scratch {
+    int16_t lists[3][kMaxAnimations];
+    int32_t listCount[3];
+    Vec3 plans[2][kAnimPositions];
+    double keys[kMaxAnimations];
+    int16_t order[2][kMaxAnimations];
+};
+
+// Everything a match reads besides its world: the shared tables, its variant's static data and
+// its scratch block.
+struct Ctx {
+    const Tables *t;
+    const StaticData *sd;
+    const Skeleton *skeletons;  // players then officials
+    int32_t ticksPerStep;
+    Scratch *ws;
+    HD const Anim &A(int i) const { return t->anims[i]; }
+    HD const AnimDerived &D(int i) const { return t->derived[i]; }
+};
+
+}  // namespace eng

@@ -1,0 +1,413 @@
+// World access, frame mirroring, the world RNG and the per-player helpers every stage reads.
+// Semantics: include/cuju/simulation/world.h:37-167 (frames and mirrors),
+// include/cuju/simulation/access.h:13-63, include/cuju/simulation/humanoid.h:118-420,
+// include/cuju/rng.h:18-113 (Boost MT19937 + uniform_real in the world's 2512 RNG bytes).
+#pragma once
+
+#include "tables.h"
+
+namespace eng {
+
+// ---- faults ----------------------------------------------------------------------------------------
+// A path GRF leaves undefined. `Fail` returns false for the caller to propagate; `Fatal` marks a
+// state no match reaches (list overflow, a team without players).
+#if ENG_DEVICE
+extern __device__ uint32_t gEngineFault;
+HD void Unsupported(const char *) { gEngineFault = 1; }
+HD void Fatal(const char *) { gEngineFault = 2; }
+#else
+const char *&FailReason();
+void Fatal(const char *message);
+inline void Unsupported(const char *reason) { FailReason() = reason; }
+#endif
+HD bool Fail(const char *reason) {
+    Unsupported(reason);
+    return false;
+}
+
+// A small inline list (GRF's std::vector uses), capacity fixed.
+template <class T, int N>
+struct Small {
+    int32_t count = 0;
+    T e[N];
+    HD int size() const { return count; }
+    HD bool empty() const { return count == 0; }
+    HD void clear() { count = 0; }
+    HD void push_back(const T &x) {
+        if (count >= N) Fatal("a fixed-capacity list outgrows its capacity");
+        else e[count++] = x;
+    }
+    HD T &operator[](int i) { return e[i]; }
+    HD const T &operator[](int i) const { return e[i]; }
+    HD T *begin() { return e; }
+    HD T *end() { return e + count; }
+    HD const T *begin() const { return e; }
+    HD const T *end() const { return e + count; }
+    HD T &back() { return e[count - 1]; }
+};
+using PlayerList = Small<int, kPlayers>;
+
+// ---- RNG: Boost.Random mt19937 and uniform_real<float> over the world's bytes ---------------------
+struct Rng {
+    uint8_t *b;
+    HD uint32_t W(int i) const {
+        uint32_t v;
+        memcpy(&v, b + 4 * i, 4);
+        return v;
+    }
+    HD void SetW(int i, uint32_t v) { memcpy(b + 4 * i, &v, 4); }
+    HD uint64_t Index() const {
+        uint64_t v;
+        memcpy(&v, b + 2496, 8);
+        return v;
+    }
+    HD void SetIndex(uint64_t v) { memcpy(b + 2496, &v, 8); }
+    HD float Lo() const {
+        float v;
+        memcpy(&v, b + 2504, 4);
+        return v;
+    }
+    HD float Hi() const {
+        float v;
+        memcpy(&v, b + 2508, 4);
+        return v;
+    }
+    // Boost's seeding, with its normalization of the first word (an all-zero state becomes 1<<31).
+    HDN void Seed(uint32_t s) {
+        SetW(0, s);
+        for (int i = 1; i < 624; i++) SetW(i, 1812433253u * (W(i - 1) ^ (W(i - 1) >> 30)) + (uint32_t)i);
+        SetIndex(624);
+        uint32_t y = W(396) ^ W(623);
+        y = (y & 0x80000000u) ? (((y ^ 0x9908b0dfu) << 1) | 1) : (y << 1);
+        SetW(0, (W(0) & 0x80000000u) | (y & 0x7fffffffu));
+        for (int i = 0; i < 624; i++)
+            if (W(i) != 0) return;
+        SetW(0, 0x80000000u);
+    }
+    HDN void Twist() {
+        auto mix = [&](int i, int j) { return (W(i) & 0x80000000u) | (W(j) & 0x7fffffffu); };
+        for (int i = 0; i < 227; i++) SetW(i, W(i + 397) ^ (mix(i, i + 1) >> 1) ^ ((W(i + 1) & 1) * 0x9908b0dfu));
+        for (int i = 227; i < 623; i++)
+            SetW(i, W(i - 227) ^ (mix(i, i + 1) >> 1) ^ ((W(i + 1) & 1) * 0x9908b0dfu));
+        SetW(623, W(396) ^ (mix(623, 0) >> 1) ^ ((W(0) & 1) * 0x9908b0dfu));
+        SetIndex(0);
+    }
+    HD uint32_t Next() {
+        if (Index() == 624) Twist();
+        uint64_t i = Index();
+        uint32_t y = W((int)i);
+        SetIndex(i + 1);
+        y ^= (y >> 11);
+        y ^= (y << 7) & 0x9d2c5680u;
+        y ^= (y << 15) & 0xefc60000u;
+        y ^= (y >> 18);
+        return y;
+    }
+    // The division by 2^32 runs in float; a result that rounds up to the maximum draws again.
+    HD float Uniform() {
+        const float lo = Lo(), hi = Hi();
+        for (;;) {
+            float r = (float)Next() / ((float)0xffffffffu + 1) * (hi - lo) + lo;
+            if (r < hi) return r;
+        }
+    }
+};
+HD float RandomInRange(World &w, float lo, float hi) {
+    Rng g{w.rng};
+    float stretch = hi - lo;
+    return lo + (g.Uniform() * stretch);
+}
+
+// ---- mirroring between team frames ----------------------------------------------------------------
+HD void MirrorRadian(Radian &r) { r.rotated = !r.rotated; }
+
+HDN void MirrorHumanoid(Humanoid &h, bool &mirrored) {
+    NodeState &root = h.nodes[0];
+    root.position = root.position * Vec3(-1, -1, 1);
+    Quat q = root.rotation;
+    root.rotation = mirrored ? Quat(q.q[1], q.q[0], -q.q[3], q.q[2]) : Quat(q.q[1], q.q[0], q.q[3], -q.q[2]);
+    mirrored = !mirrored;
+    h.startPos.Mirror();
+    MirrorRadian(h.startAngle);
+    h.nextStartPos.Mirror();
+    MirrorRadian(h.nextStartAngle);
+    SpatialState &s = h.spatial;
+    s.position.Mirror();
+    s.actualMovement.Mirror();
+    s.physicsMovement.Mirror();
+    s.animationMovement.Mirror();
+    s.movement.Mirror();
+    s.actionSmuggleMovement.Mirror();
+    s.movementSmuggleMovement.Mirror();
+    s.positionOffsetMovement.Mirror();
+    h.prevPosition2D.Mirror();
+    h.tripDirection.Mirror();
+    h.decayingPositionOffset.Mirror();
+}
+
+HD void MirrorTeam(World &w, int teamID) {
+    w.flags.teamSide[teamID] *= -1;
+    w.flags.teamMirrored[teamID] = !w.flags.teamMirrored[teamID];
+    for (int p = 0; p < w.match.playerCount; p++)
+        if (w.playerTeamID[p] == teamID) MirrorHumanoid(w.match.players[p].base.humanoid, w.flags.humanoidMirrored[p]);
+}
+
+// Prediction and history arrays mirror lazily: `lazyFlip` says they hold negated x and y.
+HD void MirrorBall(Ball &b) {
+    b.momentum.Mirror();
+    b.lazyFlip = !b.lazyFlip;
+    b.positionBuffer.Mirror();
+}
+HD void BallMaterialize(Ball &b) {
+    if (!b.lazyFlip) return;
+    for (int i = 0; i < 401; i++) b.predictions[i].Mirror();
+    for (int i = 0; i < b.positionHistory.count; i++) b.positionHistory[i].Mirror();
+    b.lazyFlip = false;
+}
+HD void MentalMaterialize(MentalImage &m) {
+    if (!m.lazyFlip) return;
+    for (int i = 0; i < m.ballPredictions.count; i++) m.ballPredictions[i].Mirror();
+    m.lazyFlip = false;
+}
+
+HD void MirrorMentalImage(World &w, int k, bool t0, bool t1, bool ball) {
+    MentalImage &m = w.match.mentalImages[k];
+    for (int i = 0; i < m.players.count; i++) {
+        PlayerImage &p = m.players[i];
+        int team = w.playerTeamID[p.player];
+        if (team == 0 ? t0 : t1) {
+            p.position.Mirror();
+            p.directionVector.Mirror();
+            p.movement.Mirror();
+        }
+    }
+    if (ball) {
+        m.lazyFlip = !m.lazyFlip;
+        w.flags.mentalBallMirrored[k] = !w.flags.mentalBallMirrored[k];
+    }
+}
+
+HDN void MirrorMatch(World &w, bool t0, bool t1, bool ball) {
+    if (t0) MirrorTeam(w, 0);
+    if (t1) MirrorTeam(w, 1);
+    if (ball) {
+        w.flags.ballMirrored = !w.flags.ballMirrored;
+        MirrorBall(w.match.ball);
+    }
+    for (int k = 0; k < w.match.mentalImages.count; k++) MirrorMentalImage(w, k, t0, t1, ball);
+}
+
+// A state stores the ball, last-touch team IDs and referee team/positions in canonical order; the
+// conversion is an involution.
+HDN void CanonicalToRest(World &w) {
+    MatchState &m = w.match;
+    if (w.FirstTeamID() == 1) {
+        for (int i = 0; i < 4; i++)
+            if (m.lastTouchTeamIDs[i] != -1) m.lastTouchTeamIDs[i] = 1 - m.lastTouchTeamIDs[i];
+        if (m.lastTouchTeamID != -1) m.lastTouchTeamID = 1 - m.lastTouchTeamID;
+    }
+    if (!w.scenario.reverseTeamProcessing) return;
+    MirrorBall(m.ball);
+    for (int k = 0; k < m.mentalImages.count; k++) m.mentalImages[k].lazyFlip = !m.mentalImages[k].lazyFlip;
+    m.referee.buffer.teamID = 1 - m.referee.buffer.teamID;
+    m.referee.buffer.restartPos.Mirror();
+    m.referee.foul.foulPosition.Mirror();
+}
+HD void RestToCanonical(World &w) { CanonicalToRest(w); }
+
+// ---- access ---------------------------------------------------------------------------------------
+HD int TeamSlot(const World &w, int teamID) { return teamID == w.FirstTeamID() ? 0 : 1; }
+HD Team &TeamByID(World &w, int teamID) { return w.match.teams[TeamSlot(w, teamID)]; }
+HD const Team &TeamByID(const World &w, int teamID) { return w.match.teams[TeamSlot(w, teamID)]; }
+HD const Team &TeamOfPlayer(const World &w, int p) { return TeamByID(w, w.playerTeamID[p]); }
+HD const Team &OpponentTeamOfPlayer(const World &w, int p) { return TeamByID(w, 1 - w.playerTeamID[p]); }
+HD Humanoid &Hum(World &w, int p) { return w.match.players[p].base.humanoid; }
+HD const Humanoid &Hum(const World &w, int p) { return w.match.players[p].base.humanoid; }
+HD SpatialState &Sp(World &w, int p) { return w.match.players[p].base.humanoid.spatial; }
+HD const SpatialState &Sp(const World &w, int p) { return w.match.players[p].base.humanoid.spatial; }
+
+// GRF: the time compares as unsigned, so a negative time reads the entry at 2990 ms.
+HD Vec3 BallPredictRaw(const Vec3 *pred, int ms) {
+    int i = ms;
+    if ((uint32_t)i >= kBallPredictionSpanMs) i = kBallPredictionSpanMs - 10;
+    i = i / 10;
+    if (i < 0) i = 0;
+    return pred[i];
+}
+HD Vec3 BallPredict(const Ball &b, int ms) {
+    Vec3 v = BallPredictRaw(b.predictions, ms);
+    if (b.lazyFlip) v.Mirror();
+    return v;
+}
+
+HD int HumanGamerCount(const Team &t) {
+    int n = 0;
+    for (int g = 0; g < t.gamers.count; g++)
+        if (!t.gamers[g].controller.keyboard.disabled) n++;
+    return n;
+}
+// Gamers count the first team's, then the second's.
+HD HumanGamer &GamerByGlobal(World &w, int g) {
+    int first = w.match.teams[0].gamers.count;
+    return g < first ? w.match.teams[0].gamers[g] : w.match.teams[1].gamers[g - first];
+}
+HD const HumanGamer &GamerByGlobal(const World &w, int g) {
+    int first = w.match.teams[0].gamers.count;
+    return g < first ? w.match.teams[0].gamers[g] : w.match.teams[1].gamers[g - first];
+}
+HD int GlobalGamerIndex(const World &w, int teamID, int gamer) {
+    return TeamSlot(w, teamID) == 0 ? gamer : w.match.teams[0].gamers.count + gamer;
+}
+
+HD void InitializePlayerTeams(World &w) {
+    int first = w.FirstTeamID();
+    int firstSize = first == 0 ? w.scenario.leftTeamSize : w.scenario.rightTeamSize;
+    for (int p = 0; p < w.match.playerCount; p++) w.playerTeamID[p] = p < firstSize ? first : 1 - first;
+    for (int p = 0; p < kPlayers; p++) w.formationOverride[p] = 0;
+}
+
+HD PlayerList TeamAllPlayers(const World &w, int teamID) {
+    PlayerList l;
+    for (int p = 0; p < w.match.playerCount; p++)
+        if (w.playerTeamID[p] == teamID) l.push_back(p);
+    return l;
+}
+HD PlayerList TeamActivePlayers(const World &w, int teamID) {
+    PlayerList l;
+    for (int p = 0; p < w.match.playerCount; p++)
+        if (w.playerTeamID[p] == teamID && w.match.players[p].base.isActive) l.push_back(p);
+    return l;
+}
+HD int TeamDynamicSide(const World &w, int teamID) { return w.flags.teamSide[teamID]; }
+
+// ---- per-player helpers ----------------------------------------------------------------------------
+HD int FormationSource(const World &w, int p) {
+    int o = w.formationOverride[p];
+    return o ? o - 1 : p;
+}
+HD const StaticFormation &Formation(const World &w, const Ctx &c, int p) {
+    return c.sd->formation[FormationSource(w, p)];
+}
+
+HD float FixAngle(float a) { return ModulateIntoRange(-PI, PI, a + 0.5f * PI); }
+
+HD float RangeVelocity(float v) {
+    float r = kIdleVelocity;
+    if (v >= kIdleDribbleSwitch && v < kDribbleWalkSwitch) r = kDribbleVelocity;
+    else if (v >= kDribbleWalkSwitch && v < kWalkSprintSwitch) r = kWalkVelocity;
+    else if (v >= kWalkSprintSwitch) r = kSprintVelocity;
+    return r;
+}
+HD int VelocityCat(float v) {
+    float r = RangeVelocity(v);
+    if (r == kIdleVelocity) return kVelIdle;
+    if (r == kDribbleVelocity) return kVelDribble;
+    if (r == kWalkVelocity) return kVelWalk;
+    if (r == kSprintVelocity) return kVelSprint;
+    return kVelIdle;
+}
+HD float VelocityFloat(int cat) {
+    switch (cat) {
+        case kVelIdle:
+            return kIdleVelocity;
+        case kVelDribble:
+            return kDribbleVelocity;
+        case kVelWalk:
+            return kWalkVelocity;
+        case kVelSprint:
+            return kSprintVelocity;
+    }
+    return 0;
+}
+// The quantized velocity of a player.
+HD float PlayerFloatVelocity(const World &w, int p) { return VelocityFloat(Sp(w, p).velocityCat); }
+
+// `std::min` operand order: a NaN second operand loses.
+HD float MinF(float a, float b) { return (b < a) ? b : a; }
+// `std::max(a, b)`: `a` wins a tie or a NaN.
+HD float MaxF(float a, float b) { return (a < b) ? b : a; }
+
+HD float TeamDifficulty(const World &w, int teamID) {
+    return teamID == 0 ? w.scenario.leftDifficulty : w.scenario.rightDifficulty;
+}
+HD float GetStatistic(const World &w, const Ctx &c, int p, int stat) {
+    float m = 0.3f + 0.7f * TeamDifficulty(w, w.playerTeamID[p]);
+    m *= 0.7f + 0.3f * w.match.players[p].base.fatigueFactorInverse;
+    return c.sd->data[p].stats[stat] * m;
+}
+HD bool ExternalControllerActive(const World &w, int p) {
+    int ec = w.match.players[p].base.externalController;
+    if (ec < 0) return false;
+    return !GamerByGlobal(w, ec).controller.keyboard.disabled;
+}
+HD int GetReactionTimeMs(const World &w, const Ctx &c, int p) {
+    int r = TruncToInt32(roundf(80.0f - GetStatistic(w, c, p, kStatReaction) * 40.0f));
+    if (ExternalControllerActive(w, p)) return r;
+    return TruncToInt32((float)r + (1.0f - TeamDifficulty(w, w.playerTeamID[p])) * 100);
+}
+HD float GetLastTouchBias(const World &w, int p, int decayMs) {
+    uint64_t t = w.match.actualTimeMs;
+    if (decayMs > 0)
+        return 1.0f - Clamp((float)(t - w.match.players[p].base.lastTouchTimeMs) / (float)decayMs, 0.0f, 1.0f);
+    return 0.0f;
+}
+HD float TeamLastTouchBias(const World &w, int teamID, int decayMs) {
+    int lt = TeamByID(w, teamID).lastTouchPlayer;
+    return lt >= 0 ? GetLastTouchBias(w, lt, decayMs) : 0.0f;
+}
+// GRF: before the first touch, the team processed first counts as the last to touch.
+HD float MatchLastTouchBias(const World &w, int decayMs) {
+    int team = w.match.lastTouchTeamID != -1 ? w.match.lastTouchTeamID : w.FirstTeamID();
+    return TeamLastTouchBias(w, team, decayMs);
+}
+
+HD void OffsetPosition(World &w, int p, const Vec3 &off) {
+    Humanoid &h = Hum(w, p);
+    h.nextStartPos += off;
+    h.startPos += off;
+    h.spatial.position += off;
+    h.spatial.positionOffsetMovement += off * 100.0f;
+    h.decayingPositionOffset += off;
+    if (h.decayingPositionOffset.Length() > 0.1f) h.decayingPositionOffset = h.decayingPositionOffset.Normalized() * 0.1f;
+    h.anim.positionOffset += off;
+}
+
+HD int MentalImageIndex(const World &w, int historyMs) {
+    int i = TruncToInt32(round((double)((float)historyMs / 100.0)));
+    if (i >= w.match.mentalImages.count) i = w.match.mentalImages.count - 1;
+    if (i < 0) i = 0;
+    return i;
+}
+// The offset from the image's stamp wraps as unsigned 32-bit, so one outside the window (a negative
+// one included) reads the last prediction.
+HD Vec3 MentalBallPrediction(const World &w, int k, int ms) {
+    const MentalImage &m = w.match.mentalImages[k];
+    int i = (int)(uint32_t)((uint64_t)(int64_t)ms + w.match.actualTimeMs - (uint64_t)m.timeStampMs);
+    if ((uint32_t)i >= kBallPredictionSpanMs) i = kBallPredictionSpanMs - 10;
+    i = i / 10;
+    if (i < 0) i = 0;
+    Vec3 r = m.ballPredictions[i];
+    if (m.lazyFlip) r.Mirror();
+    Vec3 real = BallPredict(w.match.ball, ms);
+    return r.EnforceMaximumDeviation(real, m.maxDistanceDeviation);
+}
+
+// Exact: float differences whose squares add in double.
+HD float GetDistance(const Vec3 &a, const Vec3 &b) {
+    float dx = a.v[0] - b.v[0], dy = a.v[1] - b.v[1], dz = a.v[2] - b.v[2];
+    if (dx == 0.0f && dy == 0.0f && dz == 0.0f) return 0.0f;
+    double x = dx, y = dy, z = dz;
+    float l = (float)sqrt(x * x + y * y + z * z);
+    if (l < kAboveMillionth) l = 0;
+    return l;
+}
+
+HD float Curve(float s, float bias = 1.0f) {
+    return (libm::sinf((s - 0.5f) * PI) * 0.5f + 0.5f) * bias + s * (1.0f - bias);
+}
+
+HD float GetMaximumVelocity(const StaticData &sd, int p) {
+    return kSprintVelocity * (0.9f + sd.data[p].velocityStat * 0.1f);
+}
+
+}  // namespace eng

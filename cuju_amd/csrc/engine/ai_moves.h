@@ -1,0 +1,786 @@
+// The player AI, first half: the state it reads, the defensive component, the ball commands and
+// the movement towards the ball, the formation and the support positions.
+// Semantics: include/cuju/simulation/ai_controller.h:418-1620.
+#pragma once
+
+#include "ai.h"
+
+namespace eng {
+
+struct AIBase {
+    World &w;
+    const Ctx &c;
+    const int p;
+    MatchState &m;
+    Player &ps;
+    AIControllerState *eliza;  // null under a gamer
+    PlayerControllerState &ctl;
+    const int teamID, oppID, side;  // `side`: the sign of x of the own goal
+    int k = 0;                      // mental image
+    CommandQueue &q;
+
+    HD AIBase(World &world, const Ctx &ctx, int player, CommandQueue &queue, PlayerControllerState &controller,
+              AIControllerState *e)
+        : w(world),
+          c(ctx),
+          p(player),
+          m(world.match),
+          ps(world.match.players[player]),
+          eliza(e),
+          ctl(controller),
+          teamID(world.playerTeamID[player]),
+          oppID(1 - world.playerTeamID[player]),
+          side(TeamDynamicSide(world, world.playerTeamID[player])),
+          q(queue) {}
+
+    HD Vec3 Pos(int o) const { return Sp(w, o).position; }
+    HD Vec3 Mov(int o) const { return Sp(w, o).movement; }
+    HD Vec3 Dir(int o) const { return Sp(w, o).directionVec; }
+    HD Vec3 Pos() const { return Pos(p); }
+    HD Vec3 Mov() const { return Mov(p); }
+    HD Vec3 Dir() const { return Dir(p); }
+    HD float FloatVelocity() const { return PlayerFloatVelocity(w, p); }
+    HD float Stat(int s) const { return GetStatistic(w, c, p, s); }
+    HD int StaticRole(int o) const { return Formation(w, c, o).role; }
+    HD int DynamicRole() const { return ps.dynamicFormationEntry.role; }
+    HD const Team &Own() const { return TeamByID(w, teamID); }
+    HD const Team &Opp() const { return TeamByID(w, oppID); }
+    HD const TeamAI &AI() const { return Own().ai; }
+    HD Vec3 MentalBall(int ms) const { return MentalBallPrediction(w, k, ms); }
+    HD Vec3 BallAt(int ms) const { return BallPredict(m.ball, ms); }
+
+    HD float CouldWinABallDuelLikeliness() const {
+        int o = Opp().designatedTeamPossessionPlayer;
+        Vec3 op = Pos(o) + Mov(o) * 0.1f;
+        Vec3 meToOpp = op - (Pos() + Mov() * 0.1f);
+        Vec3 oppToBall = MentalBall(100).Get2D() - (Pos(o) + Mov(o) * 0.1f);
+        float dot = meToOpp.Normalized(0).Dot(oppToBall.Normalized(0));
+        dot = dot * 0.5f + 0.5f;
+        return (1.0f - dot);
+    }
+
+    // Moves `desired` towards the spot that keeps the marked opponent from a shooting point.
+    HDN void AddDefensiveComponent(Vec3 &desired, float bias, int forcedOpp = -1) const {
+        int o = forcedOpp < 0 ? ps.manMarking : forcedOpp;
+        if (!(m.inPlay && !m.inSetPiece && StaticRole(p) != kRoleGoalkeeper)) return;
+        if (o < 0) return;
+        Vec3 defend = desired;
+        const float possShoot = 24.0f, genericShoot = 8.0f, minDistance = 0.4f, buffer = 4.0f;
+        PlayerImage oi = MentalPlayerImage(w, MentalImageIndex(w, PlayerControllerReactionTime(w, c, p)), o);
+        Vec3 op = oi.position + oi.movement * 0.5f;
+        float shoot = o == m.designatedPossessionPlayer ? possShoot : genericShoot;
+        Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
+        float oppToGoal = (goal - op).Length();
+        float oppToThreshold = Clamp(oppToGoal - shoot, minDistance, kPitchHalfLength);
+        Vec3 shootingPoint = op + (goal - op).Normalized(0) * oppToThreshold;
+        const float trapX = AI().offsideTrapX;
+        if (shootingPoint.v[0] * side > trapX * side) {
+            Line l1(op, goal);
+            Line l2(Vec3(trapX, -kPitchHalfWidth, 0), Vec3(trapX, kPitchHalfWidth, 0));
+            shootingPoint = l1.IntersectionPoint(l2);
+            oppToThreshold = (shootingPoint - op).Length();
+        }
+        Vec3 meToThreshold = shootingPoint - desired;
+        float meDist = meToThreshold.Length();
+        float slack = meDist - (oppToThreshold - buffer);
+        if (slack > 0.0f) defend = desired + meToThreshold.Normalized(0) * Clamp(slack, 0.0f, meDist);
+        Vec3 actual = Pos() + Mov() * 0.14f;
+        float actualSlack = (shootingPoint - actual).Length() - oppToThreshold;
+        if (actualSlack > 0.0f) defend += (goal - defend).Normalized(0) * actualSlack * 0.7f;
+        desired = desired * (1.0f - bias) + defend * bias;
+    }
+    HDN Vec3 GetDefendPosition(int o, float distance = 0.0f) const {
+        PlayerImage oi = MentalPlayerImage(w, k, o);
+        Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
+        Vec3 op = oi.position;
+        Vec3 oppToGoal = goal - op;
+        Line toGoal(op, goal);
+        Line meToOpp(Pos(), op);
+        Vec3 mid = meToOpp.pts[0] * 0.5f + meToOpp.pts[1] * 0.5f;
+        Line perp(mid, mid + (meToOpp.pts[0] - mid).Rotated2D((float)(0.5 * (double)PI)));
+        float f = 0.0f;
+        toGoal.IntersectionPoint(perp, f);
+        f = Clamp(f, 0.0f, 1.0f);
+        Vec3 t = toGoal.pts[0] + (toGoal.pts[1] - toGoal.pts[0]) * f;
+        t += (oppToGoal.Normalized(0) * kSprintVelocity * 0.1f) + (oi.movement * 0.14f) + (oppToGoal.Normalized(0) * distance);
+        return t;
+    }
+
+    // ---- commands ----
+    HDN void KeeperDeflectCommand(bool onlyPickup) {
+        if (StaticRole(p) != kRoleGoalkeeper) return;
+        if (GetDistance(BallAt(400), Pos()) > kBallDistanceOptimizeThreshold + 10.0f) return;
+        if (m.lastTouchTeamID == teamID && MatchLastTouchPlayer(w) != p && m.lastTouchTeamIDs[kTouchKicked] == teamID) return;
+        if (m.ballRetainer >= 0) return;
+        if (fabsf(BallAt(160).v[1]) > 20.05f) return;
+        if ((double)(BallAt(160).v[0] * -side) > -(double)kPitchHalfLength + 16.4) return;
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnDeflect;
+        if (onlyPickup) cmd.onlyDeflectAnimationsThatPickupBall = true;
+        q.push_back(cmd);
+    }
+    HDN void SetPieceCommand() {
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.useDesiredMovement = true;
+        cmd.useDesiredLookAt = true;
+        cmd.desiredDirection = Dir();
+        cmd.desiredVelocityFloat = kIdleVelocity;
+        cmd.desiredLookAt = m.ballRetainer == p ? Pos() + ctl.inputDirection * 10.0f : BallAt(0).Get2D();
+        q.push_back(cmd);
+    }
+    HDN void BallControlCommand(bool idleTurnToGoal = false, bool knockOn = false, bool stickyRun = false,
+                                bool keepBodyDirection = false) {
+        if (GetDistance(BallAt(200), Pos()) > kBallDistanceOptimizeThreshold) return;
+        if (m.ballRetainer >= 0) return;
+        if (!ps.hasPossession && !AllowLastDitchOf(w, p)) {
+            const float strictnessInverse = 3.0f;
+            if (fabsf(m.ball.momentum.v[2]) > 5.0f * strictnessInverse) return;
+            if ((m.ball.momentum.Get2D() - Mov()).Length() > 5.0f * strictnessInverse) return;
+        }
+        if (!(m.designatedPossessionPlayer == p ||
+              (Own().designatedTeamPossessionPlayer == p && CouldWinABallDuelLikeliness() >= 0.25f)))
+            return;
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnBallControl;
+        cmd.useDesiredMovement = true;
+        cmd.desiredDirection = ctl.inputDirection;
+        QuantizeDirection(cmd.desiredDirection, kQuantizedDirectionBias);
+        cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
+        if (VelocityCat(cmd.desiredVelocityFloat) == kVelIdle && idleTurnToGoal) cmd.desiredDirection = Vec3(-side, 0, 0);
+        if (knockOn) cmd.modifier |= kModifierKnockOn;
+        if (ctl.hasPossession && ctl.hasBestPossession && cmd.desiredVelocityFloat > kWalkSprintSwitch &&
+            FloatVelocity() > kDribbleWalkSwitch && stickyRun) {
+            float a = cmd.desiredDirection.Angle2D(Dir());
+            if (fabsf(a) > 0.125f * PI && fabsf(a) < 0.7f * PI) {
+                if (a > 0) cmd.desiredDirection = Dir().Rotated2D(0.125f * PI);
+                if (a < 0) cmd.desiredDirection = Dir().Rotated2D(0.125f * -PI);
+            }
+        }
+        cmd.useDesiredLookAt = true;
+        const int vc = Sp(w, p).velocityCat;
+        if (keepBodyDirection && (vc == kVelWalk || vc == kVelDribble) && VelocityCat(cmd.desiredVelocityFloat) == kVelDribble) {
+            cmd.desiredVelocityFloat = kWalkVelocity;
+            cmd.desiredLookAt = Pos() + Dir() * 10.0f;
+        } else {
+            cmd.desiredLookAt = Pos() + Mov() * 0.2f + cmd.desiredDirection * 10.0f;
+        }
+        q.push_back(cmd);
+    }
+    HDN void TrapCommand(bool idleTurnToGoal = false, bool knockOn = false) {
+        if (m.ball.momentum.Get2D().Length() < 2.0f) return;
+        if (GetDistance(BallAt(200), Pos()) > kBallDistanceOptimizeThreshold) return;
+        if (m.ballRetainer >= 0) return;
+        if (ctl.hasPossession) return;
+        if (!(m.designatedPossessionPlayer == p ||
+              (Own().designatedTeamPossessionPlayer == p && ps.timeToBallOptimisticMs < 1000 &&
+               ctl.oppTimeNeededToGetToBall > 400 && !ctl.oppTeamHasPossession && CouldWinABallDuelLikeliness() >= 0.5f)))
+            return;
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnTrap;
+        cmd.useDesiredMovement = true;
+        cmd.desiredDirection = ctl.inputDirection;
+        QuantizeDirection(cmd.desiredDirection, kQuantizedDirectionBias);
+        cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
+        if (StaticRole(p) == kRoleGoalkeeper && !ExternalControllerActive(w, p)) {
+            cmd.desiredDirection = Vec3(-side, 0, 0);
+            cmd.desiredVelocityFloat = kIdleVelocity;
+        }
+        if (VelocityCat(cmd.desiredVelocityFloat) == kVelIdle && idleTurnToGoal) cmd.desiredDirection = Vec3(-side, 0, 0);
+        if (knockOn) cmd.modifier |= kModifierKnockOn;
+        cmd.useDesiredLookAt = true;
+        cmd.desiredLookAt = Pos() + Mov() * 0.3f + cmd.desiredDirection * 10.0f;
+        q.push_back(cmd);
+    }
+    HDN void InterfereCommand(bool byAnyMeans) {
+        if (GetDistance(BallAt(200), Pos()) > kBallDistanceOptimizeThreshold) return;
+        if (m.ballRetainer >= 0) return;
+        if (ctl.teamHasBestPossession) return;
+        if (!byAnyMeans && CouldWinABallDuelLikeliness() < 0.2f) return;
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnInterfere;
+        cmd.useDesiredMovement = true;
+        cmd.strictMovement = byAnyMeans ? kStrictFalse : kStrictTrue;
+        cmd.desiredDirection = ctl.inputDirection;
+        cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
+        q.push_back(cmd);
+    }
+    HDN void SlidingCommand() {
+        if (HumanGamerCount(Own()) != 0) return;
+        if (m.ballRetainer >= 0) return;
+        if (CouldWinABallDuelLikeliness() < 0.7f) return;
+        if (!(!ctl.teamHasBestPossession && ctl.possessionAmount < 0.6f && m.designatedPossessionPlayer != p &&
+              ctl.oppTeamHasPossession))
+            return;
+        const int o = ctl.opponentPlayer;
+        Vec3 bp = MentalBallPrediction(w, MentalImageIndex(w, 20), 200);
+        Vec3 pp = Pos() + Mov() * (float)0.2;
+        float bd = (pp - bp).Length();
+        const AnimationState &oa = Hum(w, o).anim;
+        if ((bd > 0.7f && bd < 1.6f && ctl.oppTimeNeededToGetToBall > 260) ||
+            (bd > 0.6f && bd < 1.8f && oa.functionType == kFnShot && oa.frameNum < oa.touchFrame)) {
+            PlayerCommand cmd = DefaultPlayerCommand();
+            cmd.desiredFunctionType = kFnSliding;
+            cmd.useDesiredMovement = true;
+            cmd.desiredDirection = ((bp.Get2D() + Mov(o) * 0.2f) - pp).Normalized(Vec3(-side, 0, 0));
+            cmd.desiredVelocityFloat = kSprintVelocity;
+            cmd.useDesiredLookAt = true;
+            cmd.desiredLookAt = Pos() + Mov() * 0.1f + cmd.desiredDirection * 10.0f;
+            q.push_back(cmd);
+        }
+    }
+
+    // ---- movement towards the ball ----
+    HDN unsigned BallControlMovement(float desiredVel, Vec3 &bestDir, float &bestVel, Vec3 &bestLookAt) const {
+        const unsigned desiredMs = 250 + kDefaultTouchOffsetMs;
+        Vec3 toBall = MentalBall((int)desiredMs).Get2D() - Pos();
+        float dist = toBall.Length();
+        float autoBias = 1.0f;
+        if (dist < 0.4f) autoBias = libm::powf(NormalizedClamp(dist, 0.2f, 0.4f), 0.5f);
+        Vec3 autoDir = toBall.Normalized(Dir());
+        Vec3 manualDir = Dir();
+        bestDir = autoDir * autoBias + manualDir * (1.0f - autoBias);
+        bestDir.Normalize(Dir());
+        Vec3 look = bestDir;
+        bestVel = dist * kDistanceToVelocity;
+        // GRF: a velocity not below the dribble velocity, NaN included, takes the clamp.
+        if (!(bestVel < kDribbleVelocity)) {
+            bestVel = Clamp(desiredVel, bestVel, bestVel + 8.0f);
+            if (RangeVelocity(bestVel) < bestVel) bestVel = bestVel * 0.9f + RangeVelocity(bestVel) * 0.1f;
+            if (RangeVelocity(bestVel) > bestVel) bestVel = bestVel * 0.1f + RangeVelocity(bestVel) * 0.9f;
+        }
+        bestLookAt = Pos() + look * 10.0f;
+        return ps.timeToBallMs;
+    }
+
+    // Picks the interception time on the ball's path that best fits the desired movement (or the
+    // earliest reachable one, with haste).
+    HDN unsigned ToBallMovement(const Vec3 &desiredDir, float desiredVel, Vec3 &bestDir, float &bestVel, Vec3 &bestLookAt,
+                                float haste) const {
+        const Vec3 pp = Pos();
+        const float maxVel = GetMaximumVelocity(*c.sd, p);
+        float movementW = 1.0f, timeW = 0.0f, perpW = 0.1f, prevW = 0.0f;
+        Vec3 adDir = desiredDir;
+        Line ballLine(MentalBall(0).Get2D(), MentalBall(1000).Get2D());
+        float frac = 0;
+        ballLine.DistanceToPoint(pp, frac);
+        Vec3 shortest = ballLine.pts[0] + (ballLine.pts[1] - ballLine.pts[0]) * frac;
+        Vec3 ballSpace = (MentalBall(0).Get2D() - MentalBall(1000).Get2D()).Normalized(adDir);
+        float bsAngle = ballSpace.Angle2D();
+        Vec3 adBs = adDir.Rotated2D(-bsAngle);
+        {
+            const int directions = 16;
+            float a = adBs.Angle2D();
+            a /= PI * 2.0f;
+            a = roundf(a * directions);
+            a /= directions;
+            a *= PI * 2.0f;
+            const float bias = 1.0f;
+            adBs = (adBs * (1.0f - bias) + (Vec3(1, 0, 0).Rotated2D(a) * bias)).Normalized(adBs);
+        }
+        adDir = adBs.Rotated2D(bsAngle);
+        Vec3 desiredMov = adDir * desiredVel;
+        if (haste > 0.0f) {
+            movementW = 0.0f;
+            timeW = 1.0f;
+            perpW = 0.0f;
+        }
+        float bestRating = -10000.0f;
+        int bestNeeded = -10, bestTime = -10;
+        const uint32_t ttb = ps.timeToBallMs;
+        unsigned start = TruncToUint32(Clamp((float)ttb, 40, (float)(kBallPredictionSpanMs - 10)));
+        Vec3 bpStart = MentalBall((int)start);
+        if (fabsf(bpStart.v[0]) > kPitchHalfLength - 0.2f || fabsf(bpStart.v[1]) > kPitchHalfWidth - 0.2f) start = 80;
+        const int prevDesired = ps.desiredTimeToBallMs;
+        const int ttbInt = (int)ttb;
+        Vec3 ballMovRough = (MentalBall((int)(ttb + 10)) - MentalBall((int)ttb)).Get2D() * 100.0f;
+        Vec3 ballDirRough = ballMovRough.Normalized(adDir);
+        unsigned step = 1;
+        for (unsigned t = start; t < (unsigned)kBallPredictionSpanMs; t += 10 * step) {
+            bool forced = false;
+            Vec3 target = MentalBall((int)t);
+            if (fabsf(target.v[0]) > kPitchHalfLength - 0.2f || fabsf(target.v[1]) > kPitchHalfWidth - 0.2f) forced = true;
+            if (!forced && target.v[2] >= 1.0f) continue;
+            target = target.Get2D();
+            unsigned needed = GetTimeNeededMs(pp, Mov(), target, maxVel, true, t).usual;
+            int next = TruncToInt32(roundf((float)(int)(needed - t) * 0.05f)) - 5;
+            next = next < 1 ? 1 : next;
+            next = 10 < next ? 10 : next;
+            step = (unsigned)next;
+            if (needed <= t) {
+                float dot = (target - pp).Normalized(0).Dot(ballDirRough);
+                float jit = Clamp((float)ttb / (float)t, 0.0f, 1.0f);
+                if (jit < 0.35f) forced = true;
+                if (dot > 0.0f) forced = true;
+                float td = (target - pp).Length();
+                float tv = Clamp(td * kDistanceToVelocity, kIdleVelocity, kSprintVelocity);
+                Vec3 tm = (target - pp).Normalized(0) * tv;
+                float movementRating = 1.0f - NormalizedClamp((desiredMov - tm).Length(), 0.0f, kSprintVelocity);
+                float directionRating = 1.0f - NormalizedClamp(fabsf(adDir.Angle2D(tm.Normalized(adDir))), 0.0f, 0.5f * PI);
+                movementRating = movementRating * 0.4f + directionRating * 0.6f;
+                float timeRating = 1.0f - NormalizedClamp((float)t, 0, 5000);
+                float perpRating = 1.0f - NormalizedClamp((shortest - target).Length(), 0, 2.0f * kSprintVelocity);
+                float prevRating = 0.0f;
+                if (prevDesired >= ttbInt) {
+                    int diff = prevDesired - ttbInt;
+                    prevRating = 1.0f - (diff < 0 ? -diff : diff) / 500.0f;
+                }
+                float rating = movementRating * movementW + timeRating * timeW + perpRating * perpW + prevRating * prevW;
+                if (rating > bestRating || (forced && bestTime == -10)) {
+                    bestRating = rating;
+                    bestTime = (int)t;
+                    bestNeeded = (int)needed;
+                }
+            }
+            if (forced) {
+                if (bestTime == -10) {
+                    bestTime = (int)t;
+                    bestNeeded = (int)t;
+                }
+                break;
+            }
+        }
+        if (bestTime == -10) bestTime = bestNeeded = kBallPredictionSpanMs - 10;
+        Vec3 target = MentalBall(bestTime).Get2D();
+        bestDir = (target - pp).Normalized(Dir());
+        bestVel = Clamp(((float)bestNeeded / (float)bestTime) * maxVel, kIdleVelocity, kSprintVelocity);
+        if (bestTime > 250) bestVel = bestVel * 0.97f + FloatVelocity() * 0.03f;
+        Vec3 lookBall = (MentalBall(20).Get2D() - pp).Normalized(adDir);
+        Vec3 lookDesired;
+        if (bestTime < 100) lookDesired = adDir;
+        else if (VelocityCat(bestVel) != kVelIdle) lookDesired = GetClamped2D(adDir, lookBall, bestDir);
+        else lookDesired = adDir;
+        bestLookAt = pp + lookBall.Rotated2D(Clamp(lookDesired.Angle2D(lookBall) * 1.0f, -0.25f * PI, 0.25f * PI)) * 10.0f;
+        return (unsigned)bestTime;
+    }
+
+    HDN void MovementCommand(bool forceMagnet, bool extraHaste) {
+        const int lookMs = 40;
+        Vec3 qin = ctl.inputDirection;
+        QuantizeDirection(qin, kQuantizedDirectionBias);
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.useDesiredMovement = true;
+        cmd.useDesiredLookAt = true;
+        Vec3 manualDir = qin;
+        float manualVel = ctl.inputVelocityFloat;
+        float dvf = 1.0f - libm::powf(NormalizedClamp(MinF(ctl.inputVelocityFloat, FloatVelocity()), kIdleDribbleSwitch,
+                                                      kSprintVelocity),
+                                      0.5f) *
+                               0.3f;
+        Vec3 focus = MentalBall(lookMs).Get2D();
+        focus += Dir() * 0.5f;
+        float toFocus = (focus - Pos()).Normalized(manualDir).Angle2D(manualDir);
+        Vec3 defaultLook = manualDir.Rotated2D(toFocus * libm::powf(dvf, 0.7f));
+        cmd.desiredDirection = manualDir;
+        cmd.desiredVelocityFloat = manualVel;
+        Vec3 autoDir = cmd.desiredDirection;
+        float autoVel = cmd.desiredVelocityFloat;
+        Vec3 autoLook = defaultLook;
+        const float adaptedPossession = ctl.possessionAmount;
+        ps.desiredTimeToBallMs = 0;
+        float autoBias = 0.0f;
+        float ownHalfFactor = NormalizedClamp(ctl.inputDirection.Dot(Vec3(side, 0, 0)), -1.0f, 1.0f);
+        const int teamDesignated = Own().designatedTeamPossessionPlayer;
+        const float poss = ctl.possessionAmount;
+        if (m.ballRetainer == p) {
+            autoBias = 0.0f;
+        } else if (forceMagnet || m.designatedPossessionPlayer == p ||
+                   ((GetLastTouchBias(w, p, 2000) > 0.01f && poss > 0.5f) && teamDesignated == p) ||
+                   ((!ctl.oppTeamHasPossession && poss > 0.5f) && teamDesignated == p) || (poss > 0.99f && teamDesignated == p) ||
+                   (ctl.hasBestPossession && teamDesignated == p)) {
+            if (ctl.hasBestPossession) {
+                Vec3 la;
+                ps.desiredTimeToBallMs = (int)BallControlMovement(ctl.inputVelocityFloat, autoDir, autoVel, la);
+                autoLook = (la - Pos()).Normalized(0);
+                autoBias = 1.0f;
+            } else {
+                float haste = 0.0f;
+                if (extraHaste || forceMagnet) haste = 1.0f;
+                else if (adaptedPossession < 1.1f) haste = 1.0f;
+                Vec3 la;
+                ps.desiredTimeToBallMs = (int)ToBallMovement(qin, ctl.inputVelocityFloat, autoDir, autoVel, la, haste);
+                autoLook = (la - Pos()).Normalized(0);
+                autoBias = 1.0f;
+                if (m.designatedPossessionPlayer != p) {
+                    float same = 1.0f - Clamp(fabsf(autoDir.Angle2D(manualDir)) / PI, 0.0f, 1.0f);
+                    same = same * 0.5f + 0.5f;
+                    autoBias = 0.0f;
+                    if (GetLastTouchBias(w, p, 2000) > 0.01f && ps.timeToBallMs < 1700)
+                        autoBias = libm::powf(GetLastTouchBias(w, p, 2000), 0.4f) * libm::powf(same, 0.5f);
+                    if (!ctl.oppTeamHasPossession && ps.base.externalController >= 0) {
+                        float sb = GetLastSwitchBias(w, ctl);
+                        float magnet = MaxF(Curve(same, 0.8f), libm::powf(sb, 0.5f));
+                        magnet *= 1.0f - ownHalfFactor;
+                        autoBias = Clamp(libm::powf((MaxF(poss, 0.5f) - 0.5f) * 2.0f, 0.5f) * magnet, autoBias, 1.0f);
+                    }
+                    if (forceMagnet) autoBias = 1.0f;
+                }
+            }
+        } else if (w.playerTeamID[m.designatedPossessionPlayer] != teamID && teamDesignated == p) {
+            PlayerImage oi = MentalPlayerImage(w, k, ctl.opponentPlayer);
+            Vec3 op = oi.position + oi.movement * 0.14f + oi.directionVector * 0.6f;
+            Vec3 oppToGoal = (Vec3(kPitchHalfLength * side, 0, 0) - op).Normalized(0);
+            const float radius = 5.0f;
+            Vec3 fp = op + (oppToGoal * radius * 0.7f);
+            float actionBias = 1.0f - Curve(NormalizedClamp((Pos() - fp).Length(), 0.0f, radius), 0.7f);
+            if (ExternalControllerActive(w, p)) autoBias = actionBias * 0.0f + GetLastSwitchBias(w, ctl) * 0.3f;
+            else autoBias = actionBias * 0.0f;
+            autoBias *= 1.0f - ownHalfFactor;
+            if (autoBias > 0.0f) {
+                float pod = (op - Pos()).Length();
+                float mmBias = libm::powf(1.0f - Curve(NormalizedClamp(pod, 0.0f, 7.0f), 0.7f), 1.2f);
+                Vec3 mmDir = oi.movement.Normalized(ctl.inputDirection);
+                float mmVel = VelocityFloat(oi.velocity);
+                Vec3 mmLook = (MentalBall(lookMs).Get2D() - Pos()).Normalized(0);
+                Vec3 hunt = op + oppToGoal * pod * 0.3f;
+                Vec3 huntMov = hunt - Pos();
+                Vec3 huntDir = huntMov.Normalized(ctl.inputDirection);
+                float huntVel = Clamp(huntMov.Length() * kDistanceToVelocity, kIdleVelocity, kSprintVelocity);
+                Vec3 huntLook = (MentalBall(lookMs).Get2D() - Pos()).Normalized(0);
+                autoDir = (mmDir * mmBias + huntDir * (1.0f - mmBias)).Normalized(ctl.inputDirection);
+                autoVel = Clamp(mmVel * mmBias + huntVel * (1.0f - mmBias), kIdleVelocity, kSprintVelocity);
+                autoLook = ((mmLook * mmBias + huntLook * (1.0f - mmBias))).Normalized(0);
+            }
+        }
+        Vec3 autoMov = autoDir * autoVel;
+        Vec3 manualMov = manualDir * manualVel;
+        Vec3 res = manualMov * (1.0f - autoBias) + autoMov * autoBias;
+        cmd.desiredDirection = res.Normalized(qin);
+        cmd.desiredVelocityFloat = Clamp(res.Length(), kIdleVelocity, kSprintVelocity);
+        if (cmd.desiredVelocityFloat < kIdleDribbleSwitch) cmd.desiredDirection = autoLook;
+        cmd.desiredLookAt = Pos() + autoLook * 10.0f;
+        q.push_back(cmd);
+    }
+
+    // Slows players far from the action, by role, possession and recent running.
+    HDN float GetLazyVelocity(float desiredVel) const {
+        float v = desiredVel;
+        if (v > kSprintVelocity) v = kSprintVelocity + (v - kSprintVelocity) * 0.1f;
+        const float fi = ps.base.fatigueFactorInverse;
+        float startLazy = 20.0f * (fi * 0.8f + 0.2f);
+        float endLazy = 65.0f * (fi * 0.5f + 0.5f);
+        Vec3 op = Pos(Opp().designatedTeamPossessionPlayer);
+        float actionDistance = (Pos() - op).Length();
+        float teamPoss = Clamp(ctl.fadingTeamPossessionAmount - 0.5f, 0.0f, 1.0f);
+        float mind = GetMindSet(DynamicRole());
+        float byRole = mind + teamPoss * (1.0f - mind * 2.0f);
+        float byPosition = NormalizedClamp(actionDistance, startLazy, endLazy);
+        float lazy = byPosition * (0.5f + byRole * 0.5f);
+        float r = v * (1.0f - lazy);
+        if (desiredVel >= kDribbleVelocity && r < kDribbleVelocity) r = kDribbleVelocity;
+        float breath = 1.0f - NormalizedClamp(PlayerAverageVelocity(w, p, 10), kIdleVelocity, kSprintVelocity);
+        float workRate = Stat(kStatWorkRate);
+        breath = libm::powf(breath, 0.8f - workRate * 0.2f);
+        breath = Clamp(breath * 1.2f, 0.0f, 1.0f);
+        breath = breath * lazy + 1.0f * (1.0f - lazy);
+        return MinF(r, kSprintVelocity * breath);
+    }
+
+    HDN Vec3 GetSupportPositionForceField(const Vec3 &base, bool makeRun) const {
+        const int designated = Own().designatedTeamPossessionPlayer;
+        Vec3 cur = Pos() + Mov() * 0.1f;
+        Vec3 mainMan = Pos(designated) + Mov(designated) * 0.1f;
+        ForceField ff;
+        float mind = GetMindSet(DynamicRole());
+        const bool forceNoOffside = true;
+        const float baseW = 0.7f, overall = 1.0f;
+        float oppRepelW = 0.3f * overall;
+        const float mateRepelW = 0.4f * overall, ballRepelW = 1.0f * overall, runW = 1.0f * overall,
+                    flockW = 0.45f * overall, webScale = 0.75f;
+        switch (DynamicRole()) {
+            case kRoleCentreBack:
+            case kRoleLeftBack:
+            case kRoleRightBack: oppRepelW *= 2.2f; break;
+            case kRoleDefensiveMid: oppRepelW *= 2.0f; break;
+            case kRoleCentralMid:
+            case kRoleLeftMid:
+            case kRoleRightMid: oppRepelW *= 1.6f; break;
+            case kRoleAttackingMid: oppRepelW *= 1.2f; break;
+            case kRoleCentreForward: oppRepelW *= 1.0f; break;
+            default: break;
+        }
+        float offsideX = GetOffsideLine(w, k, oppID, 240);
+        {
+            ForceSpot s;
+            s.origin = base;
+            if (p == AI().forwardSupportPlayer) {
+                s.origin.v[0] += -side * (0.3f + 0.7f * mind) * 12.0f;
+            } else {
+                float amount = 22.0f;
+                float laneY = -SignSide(mainMan.v[1]) * 8.0f;
+                amount *= Curve(1.0f - NormalizedClamp(fabsf(laneY - cur.v[1]), 0.0f, 30.0f), 1.0f);
+                s.origin.v[0] += -side * libm::powf(mind, 1.5f) * amount;
+            }
+            s.power = 1.0f * baseW;
+            s.power *= 0.3f + 0.7f * NormalizedClamp((s.origin - cur).Length(), 0.0f, 20.0f);
+            ff.push_back(s);
+        }
+        if (makeRun) ff.push_back(MakeSpot(Vec3(-side * kPitchHalfLength, cur.v[1] * 0.5f, 0.0f), kAttract, kDecayConstant, 2.0f * runW));
+        // GRF adds 0.7 to every coordinate of the focus here.
+        PlayerList opps = GetClosestPlayers(w, c, oppID, mainMan * 0.3f + cur + 0.7f, false, 3);
+        for (int i = 0; i < opps.count; i++) {
+            PlayerImage oi = MentalPlayerImage(w, k, opps[i]);
+            Vec3 op = oi.position + oi.movement * 0.1f;
+            ForceSpot s = MakeSpot(op + (op - mainMan).Normalized(0) * 2.0f, kRepel, kDecayVariable, 1.0f * oppRepelW, 5.0f, 0.7f);
+            if (makeRun) {
+                s.scale = 2.0f;
+                s.power *= 0.5f;
+            }
+            ff.push_back(s);
+        }
+        if (Own().fadingTeamPossessionAmount >= 1.02f) {
+            PlayerList mates = GetClosestPlayers(w, c, teamID, cur, false, 6);
+            for (int i = 0; i < mates.count; i++) {
+                if (mates[i] == p) continue;
+                PlayerImage mi = MentalPlayerImage(w, k, mates[i]);
+                ff.push_back(MakeSpot(mi.position + mi.movement * 0.1f, kRepel, kDecayVariable, 1.0f * mateRepelW, 14.0f * webScale, 1.0f));
+            }
+        }
+        if (p != designated && Own().fadingTeamPossessionAmount >= 1.06f) {
+            const int times[4] = {200, 350, 500, 650};
+            for (int i = 0; i < 4; i++)
+                ff.push_back(MakeSpot(MentalBall(times[i]).Get2D(), kRepel, kDecayVariable, 1.0f * ballRepelW, 2.0f, 0.5f));
+        }
+        if (p != designated) {
+            ff.push_back(MakeSpot(mainMan, kAttract, kDecayVariable, 1.0f * flockW, 28.0f * webScale, 1.0f));
+            ff.push_back(MakeSpot(mainMan, kRepel, kDecayVariable, 1.0f * flockW, 16.0f * webScale, 1.0f));
+        }
+        Vec3 r = cur + GetForceFieldMovement(ff, cur, 7);
+        const float margin = 0.08f;
+        if (forceNoOffside && r.v[0] * -side > (offsideX * -side) - margin) r.v[0] = offsideX - (margin * -side);
+        r.v[0] = Clamp(r.v[0], -kPitchHalfLength, kPitchHalfLength);
+        r.v[1] = Clamp(r.v[1], -kPitchHalfWidth, kPitchHalfWidth);
+        return r;
+    }
+
+    enum StrategyKind { kDefense, kMidfield, kOffense };
+    HDN void FieldStrategyRequestInput(int kind, Vec3 &dir, float &vel) const {
+        const float staticFactor[3] = {1.0f, 0.9f, 0.8f};
+        const float attackLow[3] = {0.2f, 0.1f, 0.1f}, attackHigh[3] = {0.9f, 0.7f, 0.6f};
+        const float runThreshold[3] = {0.0f, 0.9f, 0.7f};
+        const float defensiveBase[3] = {1.9f, 1.5f, 1.3f};
+        Vec3 st = TeamAdaptedFormationPosition(w, c, p, false);
+        Vec3 dy = TeamAdaptedFormationPosition(w, c, p, true);
+        float ad = NormalizedClamp(GetDistance(Pos(), Pos(m.designatedPossessionPlayer)), 15.0f, 20.0f);
+        float sb = Curve(staticFactor[kind] * ad, 1.0f);
+        Vec3 desired = st * sb + dy * (1.0f - sb);
+        {
+            float attackBias = NormalizedClamp((ctl.fadingTeamPossessionAmount - 0.5f) * 1.0f, attackLow[kind], attackHigh[kind]);
+            bool makeRun = kind != kDefense && attackBias > runThreshold[kind] &&
+                           AI().endApplyAttackingRunMs > m.actualTimeMs && AI().attackingRunPlayer == p;
+            Vec3 support = GetSupportPositionForceField(desired, makeRun);
+            desired = desired * (1.0f - attackBias) + support * attackBias;
+        }
+        {
+            float mind = GetMindSet(DynamicRole());
+            AddDefensiveComponent(desired,
+                                  libm::powf(Clamp(defensiveBase[kind] - mind - ctl.fadingTeamPossessionAmount, 0.0f, 1.0f), 0.7f));
+            if (kind != kOffense) TeamApplyOffsideTrap(w, teamID, desired);
+        }
+        dir = (desired - Pos()).Normalized(Dir());
+        float v = (desired - Pos()).Length() * kDistanceToVelocity;
+        v = GetLazyVelocity(v);
+        vel = Clamp(v, 0, kSprintVelocity);
+    }
+
+    HDN void CalculateIfBallIsBoundForGoal() {
+        eliza->ballBoundForGoal = false;
+        eliza->ballBoundForGoalY = 0;
+        float panic = 1.02f + (1.0f - (Stat(kStatDefensivePositioning) * 0.6f + Stat(kStatVision) * 0.4f)) * 0.5f;
+        if (MentalBall(4000).v[0] * side > kPitchHalfLength && (Pos() - MentalBall(250)).Length() < 32.0f) {
+            Line toGoal(MentalBall(0).Get2D(), MentalBall(800).Get2D());
+            Line goalLine(Vec3(kPitchHalfLength * side, -kPitchHalfWidth, 0), Vec3(kPitchHalfLength * side, kPitchHalfWidth, 0));
+            Vec3 ip = toGoal.IntersectionPoint(goalLine).Get2D();
+            if (!((double)fabsf(ip.v[1]) > 3.7 * (double)panic)) {
+                eliza->ballBoundForGoalY = ip.v[1];
+                eliza->ballBoundForGoal = true;
+            }
+        }
+    }
+
+    // How far an opponent is from a shot, scaled down close to goal.
+    HD float ToThreshold(const Vec3 &goal, const Vec3 &from, float threshold) const {
+        float d = (goal - from).Length();
+        return Clamp(d - threshold * NormalizedClamp(d, 0.0f, threshold * 2.0f), 0.0f, kPitchHalfLength);
+    }
+    HDN void GoalieRequestInput(Vec3 &dir, float &vel) {
+        const float lineDistance = 10.0f;
+        Vec3 bp = MentalBall(TruncToInt32(600 + (float)ps.timeToBallMs * 0.2f)).Get2D();
+        Vec3 target = Vec3((kPitchHalfLength - lineDistance) * side, 0, 0);
+        Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
+        float maxVel = kSprintVelocity;
+        if (bp.v[0] * side > 0) {
+            CalculateIfBallIsBoundForGoal();
+            if (!eliza->ballBoundForGoal) {
+                maxVel = kSprintVelocity;
+                Vec3 post1 = Vec3(kPitchHalfLength * side, 3.7f, 0) - bp;
+                Vec3 post2 = Vec3(kPitchHalfLength * side, -3.7f, 0) - bp;
+                float a = post2.Angle2D(post1);
+                Vec3 middle = post1.Rotated2D(a * 0.5f).Normalized(Vec3(side, 0, 0));
+                Line toGoal(bp, bp + middle);
+                Line back(Vec3((kPitchHalfLength - 0.7f) * side, -kPitchHalfWidth, 0), Vec3((kPitchHalfLength - 0.7f) * side, kPitchHalfWidth, 0));
+                Vec3 is = toGoal.IntersectionPoint(back).Get2D();
+                is.v[1] = Clamp(is.v[1], -3.7f, 3.7f);
+                toGoal.pts[1] = is;
+                float awayOffset = 0.7f;
+                float awayBias = 0.3f;
+                awayBias *= NormalizedClamp(ctl.fadingTeamPossessionAmount, 1.0f, 1.5f);
+                if (ctl.fadingTeamPossessionAmount < 1.0f) {
+                    const int o = Opp().designatedTeamPossessionPlayer;
+                    Vec3 op = Pos(o) + Mov(o) * 0.32f;
+                    if (m.players[o].hasPossession == false) toGoal.pts[0] = op * 0.6f + bp * 0.4f;
+                    else toGoal.pts[0] = op * 0.4f + bp * 0.6f;
+                    float oppTh = ToThreshold(goal, op, 20.0f);
+                    Vec3 shootingPoint = op + (goal - op).Normalized(0) * oppTh;
+                    int mate = GetClosestPlayer(w, c, teamID, shootingPoint, false, p);
+                    float mateTh = 99999;
+                    if (mate >= 0) mateTh = (shootingPoint - (Pos(mate) + Mov(mate) * 0.24f)).Length();
+                    if (mateTh > oppTh + 1.0f) {
+                        awayBias = 1.0f;
+                        int helper = GetClosestPlayer(w, c, oppID, goal, false, o);
+                        if (helper >= 0) {
+                            Vec3 hp = Pos(helper) + Mov(helper) * 0.32f;
+                            float helperTh = ToThreshold(goal, hp, 24.0f);
+                            Vec3 hsp = hp + (goal - hp).Normalized(0) * helperTh;
+                            int mateHelper = GetClosestPlayer(w, c, teamID, hsp, false, p);
+                            float mateHelperTh = 99999;
+                            if (mateHelper >= 0) mateHelperTh = (hsp - (Pos(mateHelper) + Mov(mateHelper) * 0.24f)).Length();
+                            float second = 0.0f;
+                            if (mateHelperTh > helperTh) second = NormalizedClamp(mateHelperTh - helperTh, 0.0f, 2.0f);
+                            float ratio = 1.0f - NormalizedClamp(helperTh / (oppTh + 0.0001f), 1.0f, 1.5f);
+                            ratio *= 0.7f;
+                            awayBias = Clamp(1.0f - (second * ratio), 0.0f, 1.0f);
+                        }
+                    }
+                }
+                if (AI().endApplyKeeperRushMs > m.actualTimeMs) awayBias = 1.0f;
+                float d = MaxF(toGoal.Length() - 0.5f, 0.0f);
+                awayOffset = Clamp(d * awayBias, awayOffset, kPitchHalfLength);
+                target = toGoal.pts[1] + (toGoal.pts[0] - toGoal.pts[1]).Normalized(0) * awayOffset;
+                float f = 0.0f;
+                float dl = toGoal.DistanceToPoint(Pos(), f);
+                if ((target - goal).Length() < (Pos() - goal).Length() && dl < 1.0f && f > 0.0f) maxVel = kWalkVelocity;
+                target.v[0] = Clamp(target.v[0], -kPitchHalfLength + 0.2f, kPitchHalfLength - 0.2f);
+            } else {
+                maxVel = kSprintVelocity;
+                Line toGoal;
+                toGoal.pts[0] = MentalBall(10).Get2D();
+                const float minGoalLine = 0.4f;
+                Vec3 over = Vec3(kPitchHalfLength * side, eliza->ballBoundForGoalY, 0);
+                over += (toGoal.pts[0] - over).Normalized(0) * minGoalLine;
+                toGoal.pts[1] = over;
+                float f = 0.0f;
+                toGoal.DistanceToPoint(Pos() + Mov() * 0.05f, f);
+                float f1 = 0.0f;
+                toGoal.DistanceToPoint(MentalBall(1010).Get2D(), f1);
+                bool runsToGoal = false;
+                if ((double)f1 > 1e-4) {
+                    float tr = f / f1;
+                    Vec3 atKeeper = MentalBall(TruncToInt32(10 + 1000 * tr));
+                    if ((double)atKeeper.v[2] > 2.5) runsToGoal = true;
+                }
+                f = Clamp(f, 0.0f, 1.0f);
+                if (runsToGoal) {
+                    target = over;
+                } else {
+                    target = toGoal.pts[0] + (toGoal.pts[1] - toGoal.pts[0]) * f;
+                    target.v[2] = 0.0f;
+                    target.v[0] = Clamp(target.v[0], -kPitchHalfLength + 0.2f, kPitchHalfLength - 0.2f);
+                }
+            }
+        }
+        dir = target - Pos();
+        vel = Clamp(dir.Length() * kDistanceToVelocity, kIdleVelocity, maxVel);
+        dir.Normalize(Dir());
+    }
+
+    // ---- passes ----
+    HDN float PassingOdds(const Vec3 &target, int passType, const ImageList &opps, float ballVelMul = 1.0f) const {
+        const float secondScale = 1.0f;
+        Vec3 origin = Pos() + Mov() * 0.12f;
+        Line line(origin, target);
+        float danger = 0.0f;
+        for (int i = 0; i < opps.count; i++) {
+            Vec3 op = opps[i].position + opps[i].movement * 0.2f;
+            float f = 0.0f;
+            float od = line.DistanceToPoint(op, f);
+            if (!(f >= 0.0f && f <= 1.0f + 0.2f)) continue;
+            if (passType == kFnHighPass && !(f < 0.2f || f > 0.65f)) continue;
+            float cf = Clamp(f, 0.0f, 1.0f);
+            Vec3 is = origin * (1.0f - cf) + target * cf;
+            float oppSeconds = (od + 1.0f) / kSprintVelocity;
+            Vec3 originToBall = (is - origin);
+            float penalty = (passType == kFnHighPass && f > 0.5f) ? 2.5f : 0.0f;
+            float ballSeconds = 0.7f + originToBall.Length() * f * 0.03f + penalty;
+            ballSeconds *= 1.0f / ballVelMul;
+            danger += Clamp(ballSeconds - oppSeconds + (secondScale * 0.5f), 0.0f, secondScale);
+        }
+        if (passType == kFnHighPass) danger += 0.4f;
+        danger = NormalizedClamp(danger, 0.0f, secondScale);
+        return 1.0f - danger;
+    }
+    HDN float PassingOddsTo(int target, int passType, const ImageList &opps) const {
+        float d = (Pos(target) - Pos()).Length();
+        if (passType == kFnHighPass && d < 10.0f) return 0.0f;
+        float est = 0.7f + d * 0.03f;
+        Vec3 tp = Pos(target) + Mov(target) * Clamp(est, 0.0f, 0.5f);
+        if (passType == kFnLongPass) tp += Vec3(-side * d * 0.2f, 0, 0);
+        return PassingOdds(tp, passType, opps);
+    }
+    HDN void AddPass(int target, int passType) {
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = passType;
+        TouchInformation &t = cmd.touchInfo;
+        t.targetPlayer = -1;
+        t.forcedTargetPlayer = target;
+        t.inputDirection = Vec3(0);
+        t.inputPower = 0;
+        t.autoDirectionBias = 1.0f;
+        t.autoPowerBias = 1.0f;
+        GetPass(w, p, passType, t.inputDirection, t.inputPower, t.autoDirectionBias, t.autoPowerBias, t.desiredDirection,
+                t.desiredPower, t.targetPlayer, t.forcedTargetPlayer);
+        q.push_back(cmd);
+    }
+    HDN void AddPanicPass() {
+        int ySide = SignSide(Dir().v[1]);
+        Vec3 away = ((Dir() * Vec3(0.8f, 1.0f, 0.0f)).Normalized() + Vec3(-side * 0.7f, ySide * 0.5f, 0)).Normalized(0) +
+                    Vec3(0, 0, 0.3f);
+        away.Normalize(Dir());
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.touchInfo.inputDirection = away;
+        cmd.touchInfo.desiredDirection = away;
+        cmd.touchInfo.autoDirectionBias = 0.0f;
+        cmd.touchInfo.autoPowerBias = 0.0f;
+        const int types[3] = {kFnHighPass, kFnShot, kFnLongPass};
+        const float powers[3] = {0.7f, 0.6f, 0.8f};
+        for (int i = 0; i < 3; i++) {
+            cmd.desiredFunctionType = types[i];
+            cmd.touchInfo.inputPower = powers[i];
+            cmd.touchInfo.desiredPower = powers[i];
+            q.push_back(cmd);
+        }
+    }
+    HDN void BestDribbleMovement(Vec3 &desiredDir, float &desiredVel) const {
+        Vec3 mp = Pos(), mm = Mov();
+        float offense = 0.7f + kDribbleOffensiveness * 0.05f + GetMindSet(DynamicRole()) * 0.05f;
+        const float powerMul = 1.0f, futureS = 0.25f;
+        PlayerList opps = GetClosestPlayers(w, c, oppID, mp, false, 5);
+        ForceField ff;
+        float nearBackline = NormalizedClamp(fabsf(mp.v[0]) / kPitchHalfLength, 0.0f, 1.0f);
+        float centerInv = 1.0f - nearBackline * nearBackline;
+        centerInv *= 0.5f;
+        Vec3 oppGoal = Vec3(-side * kPitchHalfLength, mp.v[1] * (1.0f - kDribbleCenterMagnet) * centerInv, 0);
+        for (int i = 0; i < opps.count; i++) {
+            PlayerImage oi = MentalPlayerImage(w, k, opps[i]);
+            ff.push_back(MakeSpot(oi.position + oi.movement * futureS, kRepel, kDecayVariable, 2.0f * powerMul, 10.0f, 1.0f));
+        }
+        ff.push_back(MakeSpot(Vec3(mp.v[0], (kPitchHalfWidth + 5.0f) * SignSide(mp.v[1]), 0), kRepel, kDecayVariable, 4.0f * powerMul, 20.0f, 0.7f));
+        ff.push_back(MakeSpot(Vec3((kPitchHalfLength + 5.0f) * SignSide(mp.v[0]), mp.v[1], 0), kRepel, kDecayVariable, 4.0f * powerMul, 20.0f, 0.7f));
+        ff.push_back(MakeSpot(oppGoal, kAttract, kDecayConstant, offense * powerMul));
+        Vec3 mv = GetForceFieldMovement(ff, mp + mm * futureS, 1.0f);
+        desiredDir = mv.Normalized(Dir());
+        desiredVel = Clamp(mv.Length() * kDistanceToVelocity, kIdleVelocity, kSprintVelocity);
+        desiredVel = RangeVelocity(desiredVel);
+    }
+};
+
+}  // namespace eng

@@ -343,7 +343,7 @@ HDN void ApplyNode(const Ctx &c, const Anim &a, const Skeleton &sk, Humanoid &h,
                         for (int k = 0; k < 4; k++) {
                             const float own = middle->normalized.q[k];
                             ori.q[k] = own != 0.0f ? own
-                                       : (signbit(own) && signbit(target.q[k]) != signbit(curBias)) ? -0.0f
+                                       : (SignBit(own) && SignBit(target.q[k]) != SignBit(curBias)) ? -0.0f
                                                                                                      : 0.0f;
                         }
                         steady = true;

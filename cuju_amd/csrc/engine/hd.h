@@ -7,6 +7,10 @@
 #include <cstdint>
 #include <cstring>
 
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#endif
+
 #if defined(__FAST_MATH__)
 #error "the engine needs IEEE 754 semantics, without fast math"
 #endif
@@ -39,6 +43,7 @@ HD uint32_t BitsOf(float v) {
     memcpy(&b, &v, 4);
     return b;
 }
+HD bool SignBit(float v) { return (BitsOf(v) >> 31) != 0; }
 HD float FloatOf(uint32_t b) {
     float v;
     memcpy(&v, &b, 4);

@@ -1,0 +1,273 @@
+// One tick of a match: each stage runs in the frame it expects, between two MirrorMatch calls.
+// Semantics: include/cuju/simulation/match_process.h:17-374.
+#pragma once
+
+#include "setpiece.h"
+#include "camera.h"
+
+namespace eng {
+
+// Slot 0 holds the newest of at most three mental images.
+HDN void PushMentalImage(World &w) {
+    MatchState &m = w.match;
+    const int n = m.mentalImages.count < 3 ? m.mentalImages.count + 1 : 3;
+    for (int i = n - 1; i > 0; i--) {
+        m.mentalImages[i] = m.mentalImages[i - 1];
+        w.flags.mentalBallMirrored[i] = w.flags.mentalBallMirrored[i - 1];
+    }
+    MentalImage &mi = m.mentalImages[0];
+    memset(&mi, 0, sizeof(MentalImage));
+    mi.timeStampMs = (uint32_t)m.actualTimeMs;
+    mi.maxDistanceDeviation = 2.5f;
+    mi.maxMovementDeviation = kWalkVelocity;
+    for (int slot = 0; slot < 2; slot++) {
+        PlayerList ps = TeamActivePlayers(w, slot == 0 ? w.FirstTeamID() : 1 - w.FirstTeamID());
+        for (int i = 0; i < ps.count; i++) {
+            const SpatialState &s = Sp(w, ps[i]);
+            PlayerImage im{};
+            im.player = ps[i];
+            im.position = s.position;
+            im.directionVector = s.directionVec;
+            im.velocity = s.velocityCat;
+            im.movement = s.movement;
+            im.role = m.players[ps[i]].dynamicFormationEntry.role;
+            mi.players.push_back(im);
+        }
+    }
+    const int np = kBallPredictionSpanMs / 10;
+    mi.ballPredictions.count = np;
+    for (int i = 0; i < np; i++) mi.ballPredictions[i] = m.ball.predictions[i];
+    mi.lazyFlip = m.ball.lazyFlip;
+    w.flags.mentalBallMirrored[0] = false;
+    m.mentalImages.count = n;
+}
+
+HDN void CalculateBestPossessionTeamID(World &w) {
+    MatchState &m = w.match;
+    if (m.ballRetainer != -1) {
+        m.bestPossessionTeam = TeamSlot(w, w.playerTeamID[m.ballRetainer]);
+        return;
+    }
+    const int first = w.FirstTeamID();
+    int a = TeamByID(w, first).timeToBallMs, b = TeamByID(w, 1 - first).timeToBallMs;
+    m.bestPossessionTeam = a < b ? TeamSlot(w, first) : a > b ? TeamSlot(w, 1 - first) : -1;
+}
+
+// Parameter bounds compare in double.
+HDN bool TriangleIntersectsLine(const Vec3 *v, const Vec3 &normal, const Vec3 &start, const Vec3 &end) {
+    Vec3 e1 = v[1] - v[0], e2 = v[2] - v[0];
+    Vec3 dir = end - start;
+    Vec3 so = start - v[0];
+    float num = -normal.Dot(so);
+    float den = normal.Dot(dir);
+    if (fabsf(den) < 0.000001f) return false;
+    float r = num / den;
+    if ((double)r <= 0.0 || (double)r >= 1.0) return false;
+    Vec3 iv = start + dir * r;
+    float uu = e1.Dot(e1), uv = e1.Dot(e2), vv = e2.Dot(e2);
+    Vec3 wv = iv - v[0];
+    float wu = wv.Dot(e1), wv2 = wv.Dot(e2);
+    float d = uv * uv - uu * vv;
+    float s = (uv * wv2 - vv * wu) / d;
+    if ((double)s < 0.0 || (double)s > 1.0) return false;
+    float t = (uv * wu - uu * wv2) / d;
+    if ((double)t < 0.0 || (double)(s + t) > 1.0) return false;
+    return true;
+}
+// Whether the ball crossed the goal mouth on `side` this tick.
+HDN bool CheckForGoal(const World &w, int side, const Vec3 &prev) {
+    const Ball &b = w.match.ball;
+    if ((double)fabsf(BallPredict(b, 10).v[0]) < (double)kPitchHalfLength - 1.0) return false;
+    const Vec3 end = BallPredict(b, 0);
+    const float x = (kPitchHalfLength + kLineHalfWidth + 0.11f) * side;
+    const Vec3 normal(-side, 0, 0);
+    const Vec3 lower[3] = {Vec3(x, 3.7f, 0), Vec3(x, -3.7f, 0), Vec3(x, 3.7f, 2.5f)};
+    const Vec3 upper[3] = {Vec3(x, -3.7f, 0), Vec3(x, -3.7f, 2.5f), Vec3(x, 3.7f, 2.5f)};
+    bool lo = TriangleIntersectsLine(lower, normal, prev, end);
+    bool hi = TriangleIntersectsLine(upper, normal, prev, end);
+    if ((double)fabsf(prev.v[1]) > 3.7 && (double)fabsf(prev.v[0]) > (double)(kPitchHalfLength - kLineHalfWidth) - 0.11) return false;
+    return lo || hi;
+}
+
+// False when the tick ends early: while play waits for a restart (the clock still advances), or
+// on an unsupported path, which also clears `ok`.
+HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
+    MatchState &m = w.match;
+    ok = true;
+    const bool rev = w.scenario.reverseTeamProcessing;
+    const int first = w.FirstTeamID(), second = 1 - first;
+    MirrorMatch(w, rev, !rev, rev);
+    if (m.inPlay && !CheckBallCollisions(w, c)) return ok = false;
+    if (!RefereeProcess(w, c)) return ok = false;
+    Vec3 prevBall = BallPredict(m.ball, 0);
+    MirrorMatch(w, rev, !rev, rev);
+    if (!m.inPlay && m.referee.buffer.prepareTime + 10 < m.actualTimeMs) {
+        BumpActualTime(w, c, 10);
+        return false;
+    }
+    MirrorMatch(w, false, false, rev);
+    BallProcess(m.ball, m.ballIsInGoal);
+    MirrorMatch(w, false, false, rev);
+    if (m.mentalImages.count == 0 || m.actualTimeMs % 100 == 0) PushMentalImage(w);
+    if (!TeamUpdateSwitch(w, c, first)) return ok = false;
+    if (!TeamUpdateSwitch(w, c, second)) return ok = false;
+    MirrorMatch(w, first == 1, first == 0, first == 1);
+    if (!TeamProcess(w, c, first)) return ok = false;
+    MirrorMatch(w, true, true, true);
+    if (!TeamProcess(w, c, second)) return ok = false;
+    MirrorMatch(w, first == 0, first == 1, first == 0);
+    MirrorMatch(w, rev, !rev, rev);
+    if (!OfficialsProcess(w, c)) return ok = false;
+    MirrorMatch(w, rev, !rev, rev);
+    MirrorMatch(w, first == 1, first == 0, first == 1);
+    TeamUpdatePossessionStatistics(w, c, first);
+    MirrorMatch(w, true, true, true);
+    TeamUpdatePossessionStatistics(w, c, second);
+    MirrorMatch(w, first == 0, first == 1, first == 0);
+    CalculateBestPossessionTeamID(w);
+    if (m.ballRetainer == -1) {
+        if (m.bestPossessionTeam != -1) {
+            const int bt = m.bestPossessionTeam == 0 ? first : second;
+            int cand = TeamByID(w, bt).designatedTeamPossessionPlayer;
+            if (cand != m.designatedPossessionPlayer) {
+                uint32_t dt = m.players[m.designatedPossessionPlayer].timeToBallMs;
+                uint32_t ct = m.players[cand].timeToBallMs;
+                if ((float)(ct + 10) / (float)(dt + 10) < 0.85f) m.designatedPossessionPlayer = cand;
+            }
+        } else {
+            m.designatedPossessionPlayer = TeamByID(w, w.playerTeamID[m.designatedPossessionPlayer]).designatedTeamPossessionPlayer;
+        }
+    } else {
+        m.designatedPossessionPlayer = m.ballRetainer;
+    }
+    MirrorMatch(w, rev, !rev, rev);
+    if (!CheckHumanoidCollisions(w, c)) return ok = false;
+    BumpActualTime(w, c, 10);
+    bool g1 = false, g2 = false;
+    if (m.inPlay) {
+        g1 = CheckForGoal(w, TeamDynamicSide(w, first), prevBall);
+        g2 = CheckForGoal(w, TeamDynamicSide(w, second), prevBall);
+    }
+    bool goal = g1 | g2;
+    m.ballIsInGoal |= goal;
+    MirrorMatch(w, rev, !rev, rev);
+    if (m.inPlay) {
+        if (goal) {
+            // The ball entered one team's goal, so the other team scores.
+            const int scorer = g1 ? second : first;
+            m.goalCount[scorer == first ? 0 : 1] += 1;
+            m.goalScored = true;
+            m.lastGoalTeam = TeamSlot(w, scorer);
+            TeamUpdateTactics(w, scorer);
+            const int gt = m.lastGoalTeam == 0 ? first : second;
+            bool own = !(m.lastTouchTeamIDs[kTouchKicked] == gt || m.lastTouchTeamIDs[kTouchNonKicked] == gt);
+            m.lastGoalScorer = TeamByID(w, own ? 1 - gt : gt).lastTouchPlayer;
+        }
+    }
+    if (m.inPlay && m.bestPossessionTeam != -1) {
+        float sv = 0;
+        sv += (TeamByID(w, 0).fadingTeamPossessionAmount - 0.5f) * TeamDynamicSide(w, 0);
+        sv += (TeamByID(w, 1).fadingTeamPossessionAmount - 0.5f) * TeamDynamicSide(w, 1);
+        auto &h = m.possessionSideHistory;
+        if (h.count == 600) {
+            for (int i = 0; i + 1 < h.count; i++) h[i] = h[i + 1];
+            h[h.count - 1] = sv;
+        } else {
+            h.push_back(sv);
+        }
+    }
+    Referee &ref = m.referee;
+    if (ref.buffer.active && (ref.foul.foulType == 2 || ref.foul.foulType == 3) && ref.buffer.stopTime < m.actualTimeMs - 1000) {
+        // The camera frames the referee showing the card.
+        auto setAuto = [&](bool a) {
+            if (a != m.autoUpdateInGameCamera) {
+                m.cameraPosition.count = 0;
+                m.autoUpdateInGameCamera = a;
+            }
+        };
+        if (ref.buffer.prepareTime > m.actualTimeMs) {
+            setAuto(false);
+            Vec3 rp = m.officials[0].humanoid.spatial.position;
+            if (rev) rp.Mirror();
+            const Vec3 target = rp + Vec3(0, 0, 0.8f);
+            const float zoom = 1.5f;
+            m.cameraOrientation.SetAngleAxis(0.4f * PI, Vec3(1, 0, 0));
+            m.cameraNodeOrientation.SetAngleAxis((float)((double)target.Angle2D() + 1.5 * (double)PI), Vec3(0, 0, 1));
+            m.cameraNodePosition = target - target.Get2D().Normalized(Vec3(0, -1, 0)) * 10 * (1.0f / zoom) + Vec3(0, 0, 3);
+            m.cameraFov = 60.0f;
+            m.cameraNearCap = 1;
+            m.cameraFarCap = 220;
+            if (m.officials[0].humanoid.anim.functionType == kFnSpecial && ref.buffer.active) {
+                ref.buffer.prepareTime = m.actualTimeMs + 1000;
+                ref.buffer.startTime = ref.buffer.prepareTime + 2000;
+            }
+        } else {
+            setAuto(true);
+        }
+    }
+    return true;
+}
+
+HDN void PlayerPreparePutBuffers(World &w, int p) {
+    CalculateGeometryOffsets(w, p);
+    Player &ps = w.match.players[p];
+    const Team &t = TeamByID(w, w.playerTeamID[p]);
+    const bool ext = ExternalControllerActive(w, p);
+    ps.bufferNameCaptionShowCondition = ext;
+    int gamers = 0;
+    for (int g = 0; g < t.gamers.count; g++)
+        if (!t.gamers[g].controller.keyboard.disabled) gamers++;
+    if (gamers == 0) ps.bufferNameCaptionShowCondition = t.designatedTeamPossessionPlayer == p;
+    int color = 5;
+    const HumanGamer *gm = nullptr;
+    if (ps.base.externalController >= 0) {
+        gm = &GamerByGlobal(w, ps.base.externalController);
+        color = gm->keyboardIndex % 6;
+    }
+    const float colors[6][3] = {{100, 140, 255}, {100, 255, 140}, {255, 110, 110}, {255, 255, 60}, {200, 80, 200}, {200, 200, 200}};
+    ps.bufferPlayerColor = Vec3(colors[color][0], colors[color][1], colors[color][2]);
+    if (ext && gm->controller.actionMode == 2)
+        ps.bufferPlayerColor = ps.bufferPlayerColor * (libm::sinf(w.match.actualTimeMs * 0.02f) * 0.3f + 0.7f);
+}
+HDN void MatchPreparePutBuffers(World &w) {
+    const int first = w.FirstTeamID(), second = 1 - first;
+    MirrorMatch(w, false, false, first == 1);
+    PlayerList a = TeamActivePlayers(w, first);
+    for (int i = 0; i < a.count; i++) PlayerPreparePutBuffers(w, a[i]);
+    MirrorMatch(w, false, false, true);
+    PlayerList b = TeamActivePlayers(w, second);
+    for (int i = 0; i < b.count; i++) PlayerPreparePutBuffers(w, b[i]);
+    MirrorMatch(w, false, false, first == 0);
+}
+HDN void MatchFetchPutBuffers(World &w, const Ctx &c) {
+    const int first = w.FirstTeamID();
+    const Skeleton *skels[kPlayers + 3];
+    Humanoid *hums[kPlayers + 3];
+    int n = 0;
+    for (int t = 0; t < 2; t++) {
+        PlayerList ps = TeamActivePlayers(w, t == 0 ? first : 1 - first);
+        for (int i = 0; i < ps.count; i++) {
+            skels[n] = &c.skeletons[ps[i]];
+            hums[n++] = &w.match.players[ps[i]].base.humanoid;
+        }
+    }
+    for (int o = 0; o < 3; o++) {
+        skels[n] = &c.skeletons[w.match.playerCount + o];
+        hums[n++] = &w.match.officials[o].humanoid;
+    }
+    FetchPutBuffers(c, skels, hums, n);
+}
+// One 10 ms tick of the game.
+HDN bool GameTick(World &w, const Ctx &c) {
+    bool ok;
+    bool process = MatchProcess(w, c, ok);
+    if (!ok) return false;
+    UpdateCamera(w, c);
+    if (process) {
+        MatchPreparePutBuffers(w);
+        MatchFetchPutBuffers(w, c);
+    }
+    return true;
+}
+
+}  // namespace eng

@@ -1,0 +1,516 @@
+// The team AI (tactics, offside trap, danger ranking, attacking runs, dynamic roles, man marking)
+// and the tick of a team (possession amounts, players, gamer switches, designated player).
+// Semantics: include/cuju/simulation/team_ai.h:15-533, include/cuju/simulation/team_process.h:134-312.
+#pragma once
+
+#include "ai_requests.h"
+
+namespace eng {
+
+// Defined with the set pieces.
+HDN bool PlayerSendOff(World &w, const Ctx &c, int p);
+
+// Goals and the possession of the last minute are stored in processing order; these take IDs.
+HD int MatchGoalCount(const World &w, int teamID) { return w.match.goalCount[teamID == w.FirstTeamID() ? 0 : 1]; }
+HD float MatchPossessionLastMinute(const World &w) {
+    return w.FirstTeamID() == 1 ? -w.match.possessionLastMinute : w.match.possessionLastMinute;
+}
+
+// GRF's user tactics, shared by every team, in the alphabetical order of their names; a negative
+// id marks the two dribble settings, which the update skips.
+struct UserTactic {
+    int32_t id;
+    float value, modifierMultiplier;
+};
+constexpr int kUserTactics = 12;
+HD UserTactic UserTacticAt(int i) {
+    switch (i) {
+        case 0: return {-1, 0.72f, 0.0f};
+        case 1: return {-1, 0.5f, 0.0f};
+        case 2: return {kDefenseDepth, 0.3f, 0.1f};
+        case 3: return {kDefenseMicroFocusStrength, 0.96f, 0.15f};
+        case 4: return {kDefenseMidfieldFocus, 0.96f, 0.3f};
+        case 5: return {kDefenseSideFocusStrength, 0.16f, 0.1f};
+        case 6: return {kDefenseWidth, 0.7f, 0.1f};
+        case 7: return {kOffenseDepth, 0.34f, 0.1f};
+        case 8: return {kOffenseMicroFocusStrength, 0.92f, 0.15f};
+        case 9: return {kOffenseMidfieldFocus, 0.88f, 0.3f};
+        case 10: return {kOffenseSideFocusStrength, 0.88f, 0.1f};
+        default: return {kOffenseWidth, 0.74f, 0.1f};
+    }
+}
+HDN void TeamUpdateTactics(World &w, int teamID) {
+    TeamAI &ai = TeamByID(w, teamID).ai;
+    const MatchState &m = w.match;
+    int goals = MatchGoalCount(w, teamID), oppGoals = MatchGoalCount(w, 1 - teamID);
+    ai.liveTactics = ai.baseTactics;
+    float goalFactor = Clamp((float)(0.5 + (double)((oppGoals - goals) * 0.25f)), 0.0f, 1.0f);
+    float timeFactor = 0.5f + 0.5f * Clamp((float)m.matchTimeMs / 6300000.0f, 0.0f, 1.0f);
+    float offenseBias = Clamp(0.5f + (goalFactor - 0.5f) * (timeFactor * 1.0f), 0.0f, 1.0f);
+    float pf = MatchPossessionLastMinute(w) / 60.0f;
+    float recent = teamID == 0 ? (float)(0.5 - (double)(pf * 0.5f)) : (float)(0.5 + (double)(pf * 0.5f));
+    ai.offensivenessBias = offenseBias * 0.5f + recent * 0.5f;
+    for (int i = 0; i < kUserTactics; i++) {
+        const UserTactic ut = UserTacticAt(i);
+        // A stored tactic passes through six-decimal text.
+        float mul = ut.modifierMultiplier == 0.0f ? 0.0f : RoundTripSixDecimals(ut.modifierMultiplier);
+        float offset = (RoundTripSixDecimals(ut.value) - 0.5f) * 2.0f * mul;
+        float base = ut.id < 0 ? -1.0f : PropertiesGetReal(ai.baseTactics, ut.id, -1.0f);
+        if (base >= 0.0f) PropertiesSet(ai.liveTactics, ut.id, Clamp(base + offset, 0.0f, 1.0f));
+    }
+}
+// The closest player without a gamer to a point 26 m ahead of the team's possession player.
+HD int SelectAttackingRunPlayer(const World &w, const Ctx &c, int teamID) {
+    int pp = TeamByID(w, teamID).designatedTeamPossessionPlayer;
+    Vec3 focus = Sp(w, pp).position + Vec3(-TeamDynamicSide(w, teamID) * 26.0f, 0, 0);
+    return GetClosestPlayer(w, c, teamID, focus, true, pp);
+}
+HDN void TeamApplyAttackingRun(World &w, const Ctx &c, int teamID, int manualPlayer) {
+    TeamAI &ai = TeamByID(w, teamID).ai;
+    ai.endApplyAttackingRunMs = w.match.actualTimeMs + 4000;
+    ai.attackingRunPlayer = manualPlayer >= 0 ? manualPlayer : SelectAttackingRunPlayer(w, c, teamID);
+}
+
+HDN bool TeamAIProcess(World &w, const Ctx &c, int teamID) {
+    MatchState &m = w.match;
+    Team &team = TeamByID(w, teamID);
+    const Team &opp = TeamByID(w, 1 - teamID);
+    TeamAI &ai = team.ai;
+    const int side = TeamDynamicSide(w, teamID);
+    auto pos = [&](int p) { return Sp(w, p).position; };
+    auto mov = [&](int p) { return Sp(w, p).movement; };
+    if (m.actualTimeMs % 1000 == 0) TeamUpdateTactics(w, teamID);
+    ai.teamHasPossession = team.hasPossession;
+    ai.teamHasUniquePossession = TeamHasUniquePossession(w, teamID);
+    ai.oppTeamHasPossession = opp.hasPossession;
+    ai.oppTeamHasUniquePossession = TeamHasUniquePossession(w, 1 - teamID);
+    ai.teamHasBestPossession = m.bestPossessionTeam == TeamSlot(w, teamID);
+    ai.teamPossessionAmount = team.teamPossessionAmount;
+    ai.fadingTeamPossessionAmount = team.fadingTeamPossessionAmount;
+    ai.timeNeededToGetToBall = team.timeToBallMs;
+    ai.oppTimeNeededToGetToBall = opp.timeToBallMs;
+    // The offside trap line: the deepest of the danger, the ball, the opponent on the ball and
+    // the slackened offside line.
+    const float ob = ai.offensivenessBias;
+    float startDistance = 30.0f + 20.0f * ob;
+    const float forceDistance = 6.0f;
+    float deepest = (kPitchHalfLength - startDistance) * side;
+    float bx = BallPredict(m.ball, 0).v[0];
+    bx *= side;
+    float offsetX = 20.0f + 10.0f * (1.0f - ob);
+    float stf = NormalizedClamp(bx, kPitchHalfLength - startDistance - offsetX, kPitchHalfLength - forceDistance);
+    bx += offsetX * (1.0f - stf);
+    bx *= side;
+    if (bx * side > deepest * side) deepest = bx;
+    if (BallPredict(m.ball, 700).v[0] * side > deepest * side) deepest = BallPredict(m.ball, 700).v[0];
+    const int opp_p = opp.designatedTeamPossessionPlayer;
+    if (opp_p < 0) return Fail("the team AI finds no opponent possession player");
+    float caution = 4.0f * side;
+    // GRF: the comparison predicts 0.15 s ahead, the stored danger 0.1 s.
+    if ((pos(opp_p).v[0] + mov(opp_p).v[0] * 0.15f + caution) * side > deepest * side)
+        deepest = pos(opp_p).v[0] + mov(opp_p).v[0] * 0.1f + caution;
+    float lineX = GetOffsideLine(w, MentalImageIndex(w, 0), teamID);
+    const float slack = 4.0f;
+    if (lineX * side - slack > deepest * side) deepest = lineX - slack * side;
+    ai.offsideTrapX = deepest;
+    // Opponents ranked by danger, a stable insertion sort (GRF's std::sort below 17 elements).
+    PlayerList opps = TeamActivePlayers(w, 1 - teamID);
+    Vec3 dangerous = Vec3((float)(((double)kPitchHalfLength - 2.0) * side), 0, 0);
+    dangerous = dangerous * 0.8f + BallPredict(m.ball, 100).Get2D() * 0.2f;
+    Small<TacticalOpponent, kTeamPlayers> info;
+    for (int i = 0; i < opps.count; i++) {
+        TacticalOpponent e;
+        e.player = opps[i];
+        e.dangerFactor = (1.0f - NormalizedClamp((pos(opps[i]) - dangerous).Length(), 0, kPitchHalfLength * 2));
+        e.dangerFactor *= 0.95f;
+        if (opps[i] == opp.designatedTeamPossessionPlayer) e.dangerFactor += 0.05f;
+        info.push_back(e);
+    }
+    for (int n = 1; n < info.count; n++) {
+        TacticalOpponent mv = info[n];
+        int s = n;
+        while (s > 0 && mv.dangerFactor > info[s - 1].dangerFactor) {
+            info[s] = info[s - 1];
+            s--;
+        }
+        info[s] = mv;
+    }
+    ai.tacticalOpponents.count = 0;
+    for (int i = 0; i < info.count; i++) ai.tacticalOpponents.push_back(info[i]);
+    if (m.actualTimeMs % 500 == 0 && ai.endApplyAttackingRunMs <= m.actualTimeMs && HumanGamerCount(team) < 2 &&
+        m.bestPossessionTeam == TeamSlot(w, teamID)) {
+        int runner = SelectAttackingRunPlayer(w, c, teamID);
+        if (runner >= 0) {
+            float d = (pos(runner) - pos(team.designatedTeamPossessionPlayer)).Length();
+            float dr = libm::powf(1.0f - NormalizedClamp(d, 0, 40), 0.5f);
+            Vec3 spot = pos(runner) * Vec3(1.0f, 0.8f, 0.0f) + Vec3(side * 10.0f, 0, 0);
+            PlayerList near = GetClosestPlayers(w, c, 1 - teamID, spot, false, 4);
+            float density = 1.0f;
+            for (int i = 0; i < near.count; i++) {
+                float od = (pos(near[i]) - spot).Length();
+                density -= libm::powf(Curve(1.0f - NormalizedClamp(od, 0, 15), 1.0f), 0.5f) * 0.3f;
+            }
+            if (dr * density >= 0.5f) TeamApplyAttackingRun(w, c, teamID, -1);
+        }
+    }
+    if (m.actualTimeMs % 1500 == 0) {
+        const int d = team.designatedTeamPossessionPlayer;
+        ai.forwardSupportPlayer = GetClosestPlayer(w, c, teamID, pos(d) * Vec3(1.0f, 1.0f, 0.0f) + Vec3(-side * 1.5f, 0, 0), false, d);
+    }
+    return true;
+}
+
+// ---- dynamic roles: an integer assignment problem (GRF's libhungarian) -----------------------------
+constexpr int kHungarianMax = kTeamPlayers;
+// Reduces `cost` (size x size, row-major) in place and returns the total cost, or -1 when the
+// reduced costs fail to prove the assignment optimal. `colOfRow` is written only on success.
+// The steps follow the published Hungarian method of libhungarian so ties resolve alike.
+HDN int HungarianSolve(int *cost, int n, int *colOfRow) {
+    const int kInf = 0x7FFFFFFF;
+    auto C = [&](int r, int c) -> int & { return cost[r * n + c]; };
+    int col_of[kHungarianMax], unchosen[kHungarianMax], rowDec[kHungarianMax], slackRow[kHungarianMax],
+        rowOf[kHungarianMax], parent[kHungarianMax], colInc[kHungarianMax], slack[kHungarianMax];
+    for (int i = 0; i < n; i++) col_of[i] = unchosen[i] = rowDec[i] = slackRow[i] = rowOf[i] = parent[i] = colInc[i] = slack[i] = 0;
+    int total = 0, r = 0, c = 0, t = 0, q = 0, unmatched = 0, s = 0;
+    for (c = 0; c < n; c++) {
+        s = C(0, c);
+        for (r = 1; r < n; r++)
+            if (C(r, c) < s) s = C(r, c);
+        total += s;
+        if (s != 0)
+            for (r = 0; r < n; r++) C(r, c) -= s;
+    }
+    for (c = 0; c < n; c++) {
+        rowOf[c] = -1;
+        parent[c] = -1;
+        colInc[c] = 0;
+        slack[c] = kInf;
+    }
+    for (r = 0; r < n; r++) {
+        s = C(r, 0);
+        for (c = 1; c < n; c++)
+            if (C(r, c) < s) s = C(r, c);
+        rowDec[r] = s;
+        bool matched = false;
+        for (c = 0; c < n; c++)
+            if (s == C(r, c) && rowOf[c] < 0) {
+                col_of[r] = c;
+                rowOf[c] = r;
+                matched = true;
+                break;
+            }
+        if (!matched) {
+            col_of[r] = -1;
+            unchosen[t++] = r;
+        }
+    }
+    if (t != 0) {
+        unmatched = t;
+        for (;;) {
+            // Grow the alternating tree until an unmatched column is reached.
+            q = 0;
+            bool breakthrough = false;
+            while (!breakthrough) {
+                while (q < t && !breakthrough) {
+                    r = unchosen[q];
+                    s = rowDec[r];
+                    for (c = 0; c < n; c++) {
+                        if (!slack[c]) continue;
+                        int del = C(r, c) - s + colInc[c];
+                        if (del < slack[c]) {
+                            if (del == 0) {
+                                if (rowOf[c] < 0) {
+                                    breakthrough = true;
+                                    break;
+                                }
+                                slack[c] = 0;
+                                parent[c] = r;
+                                unchosen[t++] = rowOf[c];
+                            } else {
+                                slack[c] = del;
+                                slackRow[c] = r;
+                            }
+                        }
+                    }
+                    if (!breakthrough) q++;
+                }
+                if (breakthrough) break;
+                s = kInf;
+                for (c = 0; c < n; c++)
+                    if (slack[c] && slack[c] < s) s = slack[c];
+                for (q = 0; q < t; q++) rowDec[unchosen[q]] += s;
+                for (c = 0; c < n; c++) {
+                    if (slack[c]) {
+                        slack[c] -= s;
+                        if (slack[c] == 0) {
+                            r = slackRow[c];
+                            if (rowOf[c] < 0) {
+                                for (int j = c + 1; j < n; j++)
+                                    if (slack[j] == 0) colInc[j] += s;
+                                breakthrough = true;
+                                break;
+                            }
+                            parent[c] = r;
+                            unchosen[t++] = rowOf[c];
+                        }
+                    } else {
+                        colInc[c] += s;
+                    }
+                }
+            }
+            // Augment along the tree from (r, c).
+            for (;;) {
+                int j = col_of[r];
+                col_of[r] = c;
+                rowOf[c] = r;
+                if (j < 0) break;
+                r = parent[j];
+                c = j;
+            }
+            if (--unmatched == 0) break;
+            t = 0;
+            for (c = 0; c < n; c++) {
+                parent[c] = -1;
+                slack[c] = kInf;
+            }
+            for (r = 0; r < n; r++)
+                if (col_of[r] < 0) unchosen[t++] = r;
+        }
+    }
+    for (r = 0; r < n; r++)
+        for (c = 0; c < n; c++)
+            if (C(r, c) < rowDec[r] - colInc[c]) return -1;
+    for (r = 0; r < n; r++) {
+        c = col_of[r];
+        if (c < 0 || C(r, c) != rowDec[r] - colInc[c]) return -1;
+    }
+    r = 0;
+    for (c = 0; c < n; c++)
+        if (colInc[c]) r++;
+    if (r > n) return -1;
+    for (int i = 0; i < n; i++) colOfRow[i] = col_of[i];
+    for (int i = 0; i < n; i++) total += rowDec[i];
+    for (int i = 0; i < n; i++) total -= colInc[i];
+    return total;
+}
+
+// Assigns the outfield formation slots to the players nearest them: costs are decimeters, and
+// pairs beyond a growing cutoff cost 50000 until an assignment stays under it.
+HDN bool TeamCalculateDynamicRoles(World &w, const Ctx &c, int teamID) {
+    PlayerList all = TeamActivePlayers(w, teamID);
+    PlayerList ps;
+    if (!all.empty()) {
+        // GRF: removes the first goalkeeper; only one listed first is supported.
+        if (Formation(w, c, all[0]).role != kRoleGoalkeeper) return Fail("the dynamic roles need the goalkeeper first");
+        for (int i = 1; i < all.count; i++) ps.push_back(all[i]);
+    }
+    const unsigned n = (unsigned)ps.count;
+    Vec3 slots[kTeamPlayers];
+    for (unsigned s = 0; s < n; s++) slots[s] = TeamAdaptedFormationPosition(w, c, ps[s], false);
+    auto cost = [&](unsigned pi, unsigned si) {
+        Vec3 pp = Sp(w, ps[pi]).position + Sp(w, ps[pi]).movement * 0.5f;
+        return TruncToInt32(roundf((pp - slots[si]).Length() * 10));
+    };
+    int sorted[kTeamPlayers * kTeamPlayers];
+    int count = 0;
+    for (unsigned pi = 0; pi < n; pi++)
+        for (unsigned si = 0; si < n; si++) sorted[count++] = cost(pi, si);
+    for (int u = 1; u < count; u++)
+        for (int s = u; s > 0 && sorted[s] < sorted[s - 1]; s--) {
+            int x = sorted[s];
+            sorted[s] = sorted[s - 1];
+            sorted[s - 1] = x;
+        }
+    for (unsigned cutoff = n; cutoff < (unsigned)count; cutoff += 5) {
+        // A row is a formation slot, a column a player.
+        int m[kTeamPlayers * kTeamPlayers];
+        for (unsigned pi = 0; pi < n; pi++)
+            for (unsigned si = 0; si < n; si++) {
+                int e = cost(pi, si);
+                if (e >= sorted[cutoff]) e = 50000;
+                m[pi + si * n] = e;
+            }
+        int colOfRow[kTeamPlayers];
+        int total = HungarianSolve(m, (int)n, colOfRow);
+        if (total != -1 && (total < 50000 || cutoff >= (unsigned)count - 5)) {
+            for (unsigned pi = 0; pi < n; pi++)
+                for (unsigned si = 0; si < n; si++)
+                    if (colOfRow[si] == (int)pi) {
+                        const StaticFormation &f = Formation(w, c, ps[si]);
+                        FormationEntry &e = w.match.players[ps[pi]].dynamicFormationEntry;
+                        e.role = f.role;
+                        e.position = f.position;
+                        e.startPosition = f.startPosition;
+                        e.lazy = f.lazy;
+                        e.controllable = f.controllable;
+                    }
+            break;
+        }
+    }
+    return true;
+}
+
+// How well `p` stands between `o` and the own goal: a line across the goal direction in front of
+// `p`, with the opponent's side, distance from it and position along it.
+HDN float TeamCalculateMarkingQuality(const World &w, int teamID, int p, int o) {
+    const int side = TeamDynamicSide(w, teamID);
+    const SpatialState &s = Sp(w, p), &os = Sp(w, o);
+    Vec3 op = os.position + os.movement * 0.1f;
+    Vec3 pp = s.position + s.movement * 0.1f;
+    Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
+    Vec3 toGoal = goal - pp;
+    float ll = Clamp((toGoal).Length(), 4.0f, 14.0f);
+    Vec3 tgd = toGoal.Normalized(Vec3(side, 0, 0));
+    Vec3 safety = -tgd * 0.5f;
+    Line line(pp + safety + tgd.Rotated2D((float)(-0.5 * (double)PI)) * ll, pp + safety + tgd.Rotated2D((float)(0.5 * (double)PI)) * ll);
+    bool rightSide = ((line.pts[1].v[0] - line.pts[0].v[0]) * (op.v[1] - line.pts[0].v[1]) -
+                      (line.pts[1].v[1] - line.pts[0].v[1]) * (op.v[0] - line.pts[0].v[0])) > 0;
+    float f = 0.0f;
+    float fromLine = line.DistanceToPoint(op, f);
+    float adapted = fromLine;
+    if (rightSide) adapted = fabsf(fromLine - 2.0f);
+    float fromFactor = libm::powf(NormalizedClamp(adapted, 0.0f, 60.0f), 0.5f);
+    float onFactor = libm::powf(Clamp(fabsf(f * 2.0f - 1.0f), 0.0f, 1.0f), 0.5f);
+    float r = 1.0f;
+    r -= fromFactor * 0.5f;
+    r -= onFactor * 0.5f;
+    r = Clamp(r, 0.0f, 1.0f);
+    if (!rightSide) r *= 0.6f;
+    float od = (1.0f - NormalizedClamp((pp - op).Length(), 0.0f, kPitchHalfLength * 2.0f));
+    return r * 0.8f + od * 0.2f;
+}
+// The three most dangerous opponents get the best-placed outfield marker each, in danger order.
+HDN bool TeamCalculateManMarking(World &w, const Ctx &c, int teamID) {
+    const int marked = 3;
+    const TeamAI &ai = TeamByID(w, teamID).ai;
+    PlayerList ps = TeamActivePlayers(w, teamID);
+    for (int i = 0; i < ps.count; i++) w.match.players[ps[i]].manMarking = -1;
+    const int mc = ai.tacticalOpponents.count < marked ? ai.tacticalOpponents.count : marked;
+    for (int rank = 0; rank < mc; rank++) {
+        int best = -1, bestIndex = 0;
+        float bestQ = -1.0f;
+        const int o = ai.tacticalOpponents[rank].player;
+        for (int i = 0; i < ps.count; i++) {
+            if (Formation(w, c, ps[i]).role == kRoleGoalkeeper) continue;
+            float qv = TeamCalculateMarkingQuality(w, teamID, ps[i], o);
+            if (qv > bestQ) {
+                best = ps[i];
+                bestQ = qv;
+                bestIndex = i;
+            }
+        }
+        if (best >= 0) {
+            w.match.players[best].manMarking = o;
+            for (int i = bestIndex; i + 1 < ps.count; i++) ps[i] = ps[i + 1];
+            ps.count--;
+        }
+        if (ps.empty()) break;
+    }
+    return true;
+}
+
+// ---- the tick of a team -----------------------------------------------------------------------------
+HDN bool PlayerProcess(World &w, const Ctx &c, int p) {
+    MatchState &m = w.match;
+    Player &ps = m.players[p];
+    if (!ps.base.isActive) return true;
+    ps.desiredTimeToBallMs = (ps.desiredTimeToBallMs - 10 < 0) ? 0 : ps.desiredTimeToBallMs - 10;
+    if (ExternalControllerActive(w, p) && !HumanControllerProcess(w, c, p)) return false;
+    ElizaControllerProcess(w, c, p);
+    if (m.inPlay) {
+        if (m.actualTimeMs % 1000 == 0) ps.base.positionHistoryPerSecond.push_back(ps.base.humanoid.spatial.position);
+        if (ps.hasPossession) ps.possessionDurationMs += 10;
+        else ps.possessionDurationMs = 0;
+        if ((m.actualTimeMs + (uint64_t)(c.sd->stableID[p] * 10)) % 100 == 0) CalculateTacticalSituation(w, p);
+    }
+    Vec3 before = ps.base.humanoid.spatial.position;
+    if (!HumanoidProcess(w, c, p)) return false;
+    if (m.inPlay) {
+        float d = (ps.base.humanoid.spatial.position - before).Length();
+        // GRF: the raw statistic, without the difficulty and fatigue scaling.
+        const float stamina = c.sd->data[p].stats[kStatStamina];
+        ps.base.fatigueFactorInverse -= d * 0.00003f * (2.0f - stamina) * (1.0f / c.sd->matchDurationFactor);
+        ps.base.fatigueFactorInverse = Clamp(ps.base.fatigueFactorInverse, 0.01f, 1.0f);
+    }
+    if (ps.cards > 1 && ps.cardEffectiveTimeMs <= m.actualTimeMs && TeamActivePlayers(w, w.playerTeamID[p]).size() > 1)
+        return PlayerSendOff(w, c, p);
+    return true;
+}
+
+HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
+    MatchState &m = w.match;
+    Team &t = TeamByID(w, teamID);
+    const Team &opp = TeamByID(w, 1 - teamID);
+    t.teamPossessionAmount = (float)(opp.timeToBallMs + 1500) / (float)(t.timeToBallMs + 1500);
+    float fading = t.fadingTeamPossessionAmount * 0.995f + Clamp(t.teamPossessionAmount, 0.5f, 1.5f) * 0.005f;
+    t.fadingTeamPossessionAmount += Clamp(fading - t.fadingTeamPossessionAmount, -0.005f, 0.005f);
+    if (!m.inPlay || m.inSetPiece || m.ballRetainer != -1) {
+        float amount;
+        if (m.ballRetainer != -1) amount = (w.playerTeamID[m.ballRetainer] == teamID) ? 1.5f : 0.5f;
+        else amount = (m.bestPossessionTeam == TeamSlot(w, teamID)) ? 1.5f : 0.5f;
+        t.fadingTeamPossessionAmount = t.teamPossessionAmount = amount;
+    }
+    TeamHumanGamersSelectAnyone(w, c, teamID);
+    if (m.inPlay && !m.inSetPiece) {
+        if (!TeamAIProcess(w, c, teamID)) return false;
+        uint64_t off = teamID == (1 - w.FirstTeamID()) ? 200 : 0;
+        if ((m.actualTimeMs + off) % 400 == 0 && !TeamCalculateDynamicRoles(w, c, teamID)) return false;
+        if ((m.actualTimeMs + off + 100) % 400 == 0 && !TeamCalculateManMarking(w, c, teamID)) return false;
+    }
+    for (int p = 0; p < m.playerCount; p++)
+        if (w.playerTeamID[p] == teamID && m.players[p].base.isActive && !PlayerProcess(w, c, p)) return false;
+    if (m.inPlay) {
+        for (int g = 0; g < t.gamers.count; g++) {
+            HumanGamer &gm = t.gamers[g];
+            int sel = gm.selectedPlayer;
+            int best = TeamBestPossessionPlayer(w, teamID);
+            const bool *b = gm.controller.keyboard.buttons;
+            // GRF: a held switch reads as a fresh press every tick.
+            const bool sw = b[kBtnSwitch] &&
+                            (!(sel == best && sel == t.designatedTeamPossessionPlayer) || t.teamPossessionAmount < 1.0f);
+            if (sw && sel < 0) return Fail("the switch of a gamer that controls no player");
+            if (sw && !m.players[sel].hasUniquePossession) {
+                int target = -1;
+                const bool bestTeam = m.bestPossessionTeam == TeamSlot(w, teamID);
+                if (m.players[t.designatedTeamPossessionPlayer].base.externalController < 0 && bestTeam) {
+                    target = t.designatedTeamPossessionPlayer;
+                } else if (m.players[best].base.externalController < 0 && bestTeam) {
+                    target = best;
+                } else {
+                    target = GetBestSwitchTargetPlayer(w, c, teamID);
+                    if (target >= 0 && m.players[target].base.externalController >= 0) target = -1;
+                }
+                if (target == TeamGoalie(w, c, teamID)) target = -1;
+                if (target >= 0 && Formation(w, c, target).controllable) {
+                    t.mainSelectedPlayer = target;
+                    HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), target);
+                }
+            }
+        }
+    } else if (m.actualTimeMs >= 2000) {
+        if (DynamicPlayerSelection(w))
+            for (int g = 0; g < t.gamers.count; g++)
+                if (t.gamers[g].selectedPlayer >= 0) HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), -1);
+        t.mainSelectedPlayer = -1;
+    }
+    // The designated player changes to the best one when clearly quicker to the ball.
+    int dt = (int)m.players[t.designatedTeamPossessionPlayer].timeToBallMs;
+    int best = TeamBestPossessionPlayer(w, teamID);
+    int ot = opp.timeToBallMs;
+    if (t.designatedTeamPossessionPlayer != best) {
+        int d = t.designatedTeamPossessionPlayer;
+        float r = (float)((int)m.players[best].timeToBallMs + 500) / (float)(dt + 500);
+        if (m.players[best].hasPossession) r *= 0.5f;
+        if (m.players[d].hasPossession) r /= 0.5f;
+        if (ExternalControllerActive(w, best)) r *= 0.8f;
+        if (ExternalControllerActive(w, d)) r /= 0.8f;
+        if (!ExternalControllerActive(w, best) && dt < ot - 100) {
+            r += 0.2f;
+            r *= 1.2f;
+        }
+        if (r < 0.8f) t.designatedTeamPossessionPlayer = best;
+    }
+    return true;
+}
+
+}  // namespace eng

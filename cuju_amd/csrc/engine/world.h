@@ -11,15 +11,30 @@ namespace eng {
 // ---- faults ----------------------------------------------------------------------------------------
 // A path GRF leaves undefined. `Fail` returns false for the caller to propagate; `Fatal` marks a
 // state no match reaches (list overflow, a team without players).
-#if ENG_DEVICE
+#if defined(__HIPCC__)
+// 1 = a path GRF leaves undefined, 2 = a state no match reaches; the batch reads it after a launch.
 extern __device__ uint32_t gEngineFault;
-HD void Unsupported(const char *) { gEngineFault = 1; }
-HD void Fatal(const char *) { gEngineFault = 2; }
-#else
-const char *&FailReason();
-void Fatal(const char *message);
-inline void Unsupported(const char *reason) { FailReason() = reason; }
 #endif
+#if !ENG_DEVICE
+const char *&FailReason();
+[[noreturn]] void FatalHost(const char *message);
+#endif
+HD void Unsupported(const char *reason) {
+#if ENG_DEVICE
+    (void)reason;
+    gEngineFault = 1;
+#else
+    FailReason() = reason;
+#endif
+}
+HD void Fatal(const char *reason) {
+#if ENG_DEVICE
+    (void)reason;
+    gEngineFault = 2;
+#else
+    FatalHost(reason);
+#endif
+}
 HD bool Fail(const char *reason) {
     Unsupported(reason);
     return false;

@@ -468,6 +468,8 @@ inline void VWorld(Archive &a, World &w, int freeControllerCount) {
     VScenarioHead(a, w);
     MatchState &m = w.match;
     m.playerCount = w.scenario.leftTeamSize + w.scenario.rightTeamSize;
+    if (w.scenario.leftTeamSize < 0 || w.scenario.rightTeamSize < 0 || m.playerCount > kPlayers)
+        throw std::runtime_error("the state holds more players than a match holds");
     F(w.step);
     a.push("match");
     F(m.firstTeam);

@@ -1,0 +1,194 @@
+// The C ABI over the batch runtime: the entry points of the reference's src/environment_api.h
+// (cited per function in include/cuju_amd.h) with its argument meaning and error convention:
+// -1 or null with a per-thread message, -2 for an action out of range.
+#include <cstring>
+#include <exception>
+#include <stdexcept>
+#include <string>
+
+#include "../../../include/cuju_amd.h"
+#include "runtime.h"
+
+namespace eng {
+namespace host {
+// Defined by each library: its device and backend name.
+std::unique_ptr<Device> MakeLibraryDevice(int threads);
+extern const char *const kBackendName;
+}  // namespace host
+}  // namespace eng
+
+using eng::host::BatchRuntime;
+
+namespace {
+thread_local std::string lastError;
+thread_local std::string stateBytes;
+thread_local unsigned long long *memoryEstimate = nullptr;
+int Fail(const std::exception &e) {
+    lastError = e.what();
+    return -1;
+}
+BatchRuntime *Of(void *e) { return static_cast<BatchRuntime *>(e); }
+}  // namespace
+
+#pragma GCC visibility push(default)
+extern "C" {
+
+const char *cuju_last_error(void) { return lastError.c_str(); }
+const char *cuju_backend(void) { return eng::host::kBackendName; }
+
+void *cuju_environment_create(const struct cuju_configuration *s) {
+    try {
+        if (!s) throw std::invalid_argument("expected a configuration");
+        if (s->version != CUJU_CONFIGURATION_VERSION)
+            throw std::invalid_argument("expected the configuration version " + std::to_string(CUJU_CONFIGURATION_VERSION) + ", found " +
+                                        std::to_string(s->version));
+        if (s->environment_count < 1) throw std::invalid_argument("expected at least one environment, found " + std::to_string(s->environment_count));
+        if (s->allocate || s->release) throw std::invalid_argument("this build allocates its own device memory");
+        eng::host::Configuration c;
+        for (int i = 0; i < s->asset_count; i++) c.assets.push_back(s->assets[i]);
+        if (s->assignment) c.assignment.assign(s->assignment, s->assignment + s->environment_count);
+        c.animations = s->animations ? s->animations : "";
+        c.count = s->environment_count;
+        c.seed = s->seed;
+        c.actionSet = s->action_set;
+        c.observation = s->observation;
+        c.checkpoints = s->checkpoints != 0;
+        c.numpyLegacy = s->numpy_legacy != 0;
+        c.autoReset = s->auto_reset != 0;
+        c.threads = s->threads;
+        c.ticksPerStep = s->ticks_per_step;
+        c.smmWidth = s->smm_width;
+        c.smmHeight = s->smm_height;
+        c.stack = s->stack;
+        if (s->fixed_seeds) c.fixedSeeds.assign(s->fixed_seeds, s->fixed_seeds + s->environment_count);
+        if (s->agent_counts) c.agentCounts.assign(s->agent_counts, s->agent_counts + 2 * s->asset_count);
+        c.episodeNumber = s->episode_number;
+        // A larger value fails the range check rather than wrapping.
+        c.firstIndex = (int64_t)(s->first_index < (1ULL << 62) ? s->first_index : (1ULL << 62));
+        lastError.clear();
+        auto *b = new BatchRuntime(c, eng::host::MakeLibraryDevice(s->threads));
+        if (memoryEstimate) {
+            *memoryEstimate = b->MemoryBytes();
+            delete b;
+            return nullptr;
+        }
+        return b;
+    } catch (const std::exception &e) {
+        Fail(e);
+        return nullptr;
+    }
+}
+
+int cuju_memory_estimate(const struct cuju_configuration *settings, unsigned long long *bytes) {
+    memoryEstimate = bytes;
+    cuju_environment_create(settings);
+    memoryEstimate = nullptr;
+    return lastError.empty() ? 0 : -1;
+}
+int cuju_local_memory_bytes(unsigned long long *bytes) {
+    *bytes = 0;
+    return 0;
+}
+unsigned long long cuju_environment_memory_bytes(void *e) { return Of(e)->MemoryBytes(); }
+void cuju_environment_destroy(void *e) { delete Of(e); }
+int cuju_environment_count(void *e) { return Of(e)->Count(); }
+int cuju_environment_threads(void *e) { return Of(e)->Dev().Threads(); }
+int cuju_environment_agents(void *e, int *left, int *right) {
+    BatchRuntime *b = Of(e);
+    for (int i = 0; i < b->Count(); i++) {
+        if (left) left[i] = b->LeftAgents(i);
+        if (right) right[i] = b->RightAgents(i);
+    }
+    return b->Agents();
+}
+int cuju_environment_players(void *e, int *left, int *right) {
+    BatchRuntime *b = Of(e);
+    for (int i = 0; i < b->Count(); i++) {
+        if (left) left[i] = b->LeftPlayers(i);
+        if (right) right[i] = b->RightPlayers(i);
+    }
+    return b->Players();
+}
+int cuju_environment_set_difficulty(void *e, const float *difficulty) {
+    try {
+        Of(e)->SetDifficulty(difficulty);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+void cuju_environment_difficulty(void *e, float *difficulty) {
+    BatchRuntime *b = Of(e);
+    for (int i = 0; i < b->Count(); i++)
+        for (int s = 0; s < 2; s++) difficulty[i * 2 + s] = b->Difficulty(i, s);
+}
+int cuju_environment_reset(void *e, const unsigned int *seeds, const int *reverse, void *stream) {
+    try {
+        Of(e)->Reset(seeds, reverse, stream);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+int cuju_environment_reset_masked(void *e, const unsigned char *mask, int mask_on_device, const int64_t *seeds, const int *reverse,
+                                  void *stream, int synchronize) {
+    try {
+        Of(e)->ResetMasked(mask, mask_on_device != 0, seeds, reverse, stream);
+        if (synchronize) Of(e)->Synchronize(stream);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+int cuju_environment_reset_done(void *e, void *stream) {
+    try {
+        Of(e)->ResetDone(stream);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+int cuju_environment_step(void *e, const int *actions, int on_device, void *stream, int synchronize) {
+    try {
+        Of(e)->Step(actions, on_device != 0, stream, synchronize != 0);
+        return 0;
+    } catch (const std::out_of_range &ex) {
+        Fail(ex);
+        return -2;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+int cuju_environment_step_async(void *e, const int *actions, int on_device, void *stream) {
+    return cuju_environment_step(e, actions, on_device, stream, 0);
+}
+int cuju_environment_step_wait(void *e) {
+    (void)e;
+    return 0;
+}
+int cuju_environment_synchronize(void *e, void *stream) {
+    try {
+        Of(e)->Synchronize(stream);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+const char *cuju_environment_get_state(void *e, int index, unsigned long long *size, int *episode) {
+    try {
+        stateBytes = Of(e)->GetState(index, episode);
+        *size = stateBytes.size();
+        return stateBytes.data();
+    } catch (const std::exception &ex) {
+        Fail(ex);
+        return nullptr;
+    }
+}
+void *cuju_environment_buffer(void *e, const char *name) {
+    void *p = Of(e)->Buffer(name ? name : "");
+    if (!p) lastError = std::string("no buffer named ") + (name ? name : "(null)");
+    return p;
+}
+
+}  // extern "C"
+#pragma GCC visibility pop

@@ -1,0 +1,386 @@
+// The batch runtime. Semantics: include/cuju/batch/batch_environment.h:36-230 (creation and
+// checks), :254-330 (resets and steps), :384-395 (state export).
+#include "runtime.h"
+
+#include <algorithm>
+#include <stdexcept>
+#include <thread>
+
+namespace eng {
+namespace host {
+
+BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> device) : cfg_(cfg), dev_(std::move(device)) {
+    try {
+        if ((cfg.observation & kObsSimple115) && (cfg.observation & kObsSimple115v2))
+            throw std::invalid_argument("simple115 and simple115v2 are exclusive");
+        if (cfg.observation & (kObsSmm | kObsRaw))
+            throw std::invalid_argument("this build emits the simple115 and simple115v2 representations only");
+        if (cfg.assets.empty()) throw std::invalid_argument("expected an asset bundle");
+        if (cfg.count < 1) throw std::invalid_argument("expected at least one environment, found " + std::to_string(cfg.count));
+        if (cfg.ticksPerStep < 1) throw std::invalid_argument("expected at least one tick in a step");
+        if (!cfg.fixedSeeds.empty()) {
+            if ((int)cfg.fixedSeeds.size() != cfg.count) throw std::invalid_argument("expected one fixed seed for each environment");
+            for (int64_t s : cfg.fixedSeeds)
+                if (s < -1 || s > 4294967295LL) throw std::invalid_argument("expected a fixed seed from 0 to 4294967295, found " + std::to_string(s));
+        }
+        if (cfg.firstIndex < 0 || cfg.firstIndex + cfg.count > (int64_t(1) << 32))
+            throw std::invalid_argument("expected a first index from 0 to 2**32 minus the environment count");
+        if (cfg.episodeNumber < 0) throw std::invalid_argument("expected an episode number of at least 0");
+        if (cfg.stack != 1 && cfg.stack != 4) throw std::invalid_argument("expected a stack of 1 or 4 observations, found " + std::to_string(cfg.stack));
+        if (cfg.actionSet < 0 || cfg.actionSet > 2) throw std::invalid_argument("expected an action set from 0 to 2");
+        const int count = cfg.count;
+        std::vector<int32_t> assignment = cfg.assignment;
+        if (assignment.empty()) assignment.assign(count, 0);
+        if ((int)assignment.size() != count) throw std::invalid_argument("expected one bundle for each environment");
+        for (int32_t a : assignment)
+            if (a < 0 || a >= (int)cfg.assets.size()) throw std::invalid_argument("expected a bundle from 0 to " + std::to_string(cfg.assets.size() - 1) + ", found " + std::to_string(a));
+        if (!cfg.agentCounts.empty() && cfg.agentCounts.size() != 2 * cfg.assets.size())
+            throw std::invalid_argument("expected a left and a right agent count for each bundle");
+        for (size_t i = 0; i < cfg.assets.size(); i++) {
+            const int l = cfg.agentCounts.empty() ? -1 : cfg.agentCounts[2 * i];
+            const int r = cfg.agentCounts.empty() ? -1 : cfg.agentCounts[2 * i + 1];
+            bundles_.push_back(LoadBundle(cfg.assets[i], l, r));
+        }
+        tables_ = LoadAnimationTables(cfg.animations);
+        for (const Anim &a : tables_->anims)
+            if (a.frameCount > kAnimPositions) throw std::invalid_argument("expected animations of at most 320 frames");
+
+        // Shared tables: one device copy, addressed through a device Tables record.
+        const AnimationTables &T = *tables_;
+        Tables dt = T.View();
+        dt.anims = Upload(T.anims);
+        dt.nodes = Upload(T.nodes);
+        dt.keys = Upload(T.keys);
+        dt.interp = Upload(T.interp);
+        dt.middle = Upload(T.middle);
+        dt.football = Upload(T.football);
+        dt.positions = Upload(T.positions);
+        dt.quadrants = Upload(T.quadrants);
+        dt.derived = Upload(T.derived);
+        dt.selection = Upload(T.selection);
+        dt.smoothed = Upload(T.smoothed);
+        dt.fnAnims = Upload(T.fnAnims);
+        dt.fnOffset = Upload(T.fnOffset);
+        dt.cameraWeights = Upload(T.cameraWeights);
+        const Tables *dTables = Upload(&dt, 1);
+
+        std::vector<Ctx> contexts;
+        std::vector<const World *> templates;
+        int agents = 0;
+        for (const auto &bundle : bundles_) {
+            if (bundle->leftAgents < 0 || bundle->rightAgents < 0 || bundle->leftAgents + bundle->rightAgents > kMaxAgents)
+                throw std::runtime_error("expected at most 22 agents in a bundle");
+            agents = std::max(agents, bundle->leftAgents + bundle->rightAgents);
+            for (const Variant &v : bundle->variants) {
+                Ctx c{};
+                c.t = dTables;
+                c.sd = Upload(&v.staticData, 1);
+                c.skeletons = Upload(v.skeletons);
+                c.ticksPerStep = cfg.ticksPerStep;
+                c.ws = nullptr;
+                contexts.push_back(c);
+                templates.push_back(Upload(v.world.get(), 1));
+                const Scenario &sc = v.world->scenario;
+                players_ = std::max({players_, sc.leftTeamSize, sc.rightTeamSize});
+                if (sc.controlAllPlayers && DynamicPlayerSelection(*v.world))
+                    throw std::invalid_argument("a scenario with control_all_players needs 0 or all of the controllable players of a side as agents");
+                // The per-second position history of a player holds 512 entries.
+                const int64_t seconds = (int64_t)sc.gameDuration * cfg.ticksPerStep / 100 + 1;
+                if (seconds > 512) throw std::invalid_argument("a match longer than the position history of a player");
+            }
+        }
+        b_.contexts = Upload(contexts);
+        b_.templates = Upload(templates);
+        b_.count = count;
+        b_.agents = agents;
+        b_.actionSet = cfg.actionSet;
+        b_.observation = cfg.observation;
+        b_.checkpoints = cfg.checkpoints;
+        b_.numpyLegacy = cfg.numpyLegacy;
+        b_.autoReset = cfg.autoReset;
+        b_.stack = cfg.stack;
+        b_.worlds = Alloc<World>(count);
+        b_.cores = Alloc<EnvCore>(count);
+        b_.slots = Alloc<EnvSlot>(count);
+        b_.scratch = Alloc<Scratch>(count);
+        b_.reward = Alloc<float>((size_t)count * agents);
+        b_.done = Alloc<uint8_t>(count);
+        b_.scoreReward = Alloc<int32_t>(count);
+        if (cfg.observation & (kObsSimple115 | kObsSimple115v2)) {
+            b_.simple115 = Alloc<float>((size_t)count * agents * kSimple115 * cfg.stack);
+            b_.finalSimple115 = Alloc<float>((size_t)count * agents * kSimple115 * cfg.stack);
+        }
+        b_.teamDifficulty = nullptr;
+        if (!dev_->HostMemory()) actions_ = Alloc<int32_t>((size_t)count * agents);
+        seeds_ = Alloc<int64_t>(count);
+        reverse_ = Alloc<int32_t>(count);
+        mask_ = Alloc<uint8_t>(count);
+        slots_.resize(count);
+        std::vector<uint8_t> agentMask((size_t)count * agents, 0);
+        for (int e = 0; e < count; e++) {
+            EnvSlot &s = slots_[e];
+            memset(&s, 0, sizeof(EnvSlot));
+            SeedEpisodeGenerator(s.gen, cfg.seed, (uint32_t)(cfg.firstIndex + e));
+            s.fixedSeed = cfg.fixedSeeds.empty() ? -1 : cfg.fixedSeeds[e];
+            s.episodeOffset = cfg.episodeNumber;
+            s.bundle = assignment[e];
+            s.leftAgents = bundles_[s.bundle]->leftAgents;
+            s.rightAgents = bundles_[s.bundle]->rightAgents;
+            for (int a = 0; a < s.leftAgents + s.rightAgents; a++) agentMask[(size_t)e * agents + a] = 1;
+        }
+        dev_->ToDevice(b_.slots, slots_.data(), sizeof(EnvSlot) * count);
+        agentMask_ = Upload(agentMask);
+        started_.assign(count, false);
+        unstarted_ = count;
+    } catch (...) {
+        for (void *p : owned_) dev_->Release(p);
+        owned_.clear();
+        throw;
+    }
+}
+
+BatchRuntime::~BatchRuntime() {
+    try {
+        dev_->Synchronize(nullptr);
+    } catch (...) {
+    }
+    for (void *p : owned_) dev_->Release(p);
+}
+
+int BatchRuntime::LeftPlayers(int env) const { return VariantAt(slots_[env].bundle * 4).world->scenario.leftTeamSize; }
+int BatchRuntime::RightPlayers(int env) const { return VariantAt(slots_[env].bundle * 4).world->scenario.rightTeamSize; }
+
+void BatchRuntime::CheckStarted() const {
+    if (unstarted_ > 0) throw std::logic_error("expected a reset of the batch, or a state for every environment, before its first step");
+}
+void BatchRuntime::CheckEnvironment(int env) const {
+    if (env < 0 || env >= b_.count)
+        throw std::invalid_argument("expected an environment from 0 to " + std::to_string(b_.count - 1) + ", found " + std::to_string(env));
+}
+
+void BatchRuntime::Reset(const uint32_t *seeds, const int32_t *reverse, void *stream) {
+    const int n = b_.count;
+    const int64_t *ds = nullptr;
+    const int32_t *dr = nullptr;
+    if (seeds) {
+        std::vector<int64_t> wide(seeds, seeds + n);
+        dev_->ToDevice(seeds_, wide.data(), sizeof(int64_t) * n);
+        ds = seeds_;
+    }
+    if (reverse) {
+        for (int e = 0; e < n; e++)
+            if (reverse[e] != 0 && reverse[e] != 1) throw std::invalid_argument("the reverse flag of environment " + std::to_string(e) + " is not 0 or 1");
+        dev_->ToDevice(reverse_, reverse, sizeof(int32_t) * n);
+        dr = reverse_;
+    }
+    dev_->Reset(b_, nullptr, ds, dr, stream);
+    dev_->Synchronize(stream);
+    dev_->CheckFault();
+    started_.assign(n, true);
+    unstarted_ = 0;
+}
+
+void BatchRuntime::ResetMasked(const uint8_t *mask, bool maskOnDevice, const int64_t *seeds, const int32_t *reverse, void *stream) {
+    const int n = b_.count;
+    if (seeds)
+        for (int e = 0; e < n; e++)
+            if (seeds[e] < -1 || seeds[e] > 4294967295LL)
+                throw std::invalid_argument("expected seeds from 0 to 4294967295, or -1 to draw, found " + std::to_string(seeds[e]) +
+                                            " for environment " + std::to_string(e));
+    if (reverse)
+        for (int e = 0; e < n; e++)
+            if (reverse[e] != 0 && reverse[e] != 1) throw std::invalid_argument("the reverse flag of environment " + std::to_string(e) + " is not 0 or 1");
+    // Host arrays are copied on the stream before the launch reads them; the call waits for those
+    // copies, so the caller may free its arrays on return.
+    const uint8_t *dm = mask;
+    if (mask && !maskOnDevice) {
+        dev_->ToDeviceAsync(mask_, mask, n, stream);
+        dm = mask_;
+    }
+    const int64_t *ds = nullptr;
+    const int32_t *dr = nullptr;
+    if (seeds) {
+        dev_->ToDeviceAsync(seeds_, seeds, sizeof(int64_t) * n, stream);
+        ds = seeds_;
+    }
+    if (reverse) {
+        dev_->ToDeviceAsync(reverse_, reverse, sizeof(int32_t) * n, stream);
+        dr = reverse_;
+    }
+    if (unstarted_ > 0) {
+        std::vector<uint8_t> started(n, 1);
+        if (mask && maskOnDevice && !dev_->HostMemory()) {
+            dev_->Synchronize(stream);
+            dev_->ToHost(started.data(), mask, n);
+        } else if (mask) {
+            started.assign(mask, mask + n);
+        }
+        for (int e = 0; e < n; e++)
+            if (started[e] && !started_[e]) {
+                started_[e] = true;
+                unstarted_--;
+            }
+    }
+    dev_->Reset(b_, dm, ds, dr, stream);
+    if ((mask && !maskOnDevice) || seeds || reverse) dev_->Synchronize(stream);
+}
+
+void BatchRuntime::ResetDone(void *stream) {
+    CheckStarted();
+    dev_->Reset(b_, b_.done, nullptr, nullptr, stream);
+}
+
+void BatchRuntime::Step(const int32_t *actions, bool onDevice, void *stream, bool synchronize) {
+    CheckStarted();
+    const int n = ActionSetSize(b_.actionSet);
+    if (!onDevice || dev_->HostMemory()) {
+        // GRF: an action indexes a Python list, which raises outside [-n, n).
+        for (int e = 0; e < b_.count; e++) {
+            const int32_t *row = actions + (size_t)e * b_.agents;
+            for (int a = 0; a < slots_[e].leftAgents + slots_[e].rightAgents; a++)
+                if (row[a] < -n || row[a] >= n)
+                    throw std::out_of_range("expected action indices from " + std::to_string(-n) + " to " + std::to_string(n - 1) +
+                                            ", found " + std::to_string(row[a]));
+        }
+    }
+    const int32_t *da = actions;
+    if (!onDevice && !dev_->HostMemory()) {
+        dev_->ToDeviceAsync(actions_, actions, sizeof(int32_t) * b_.count * b_.agents, stream);
+        da = actions_;
+    }
+    dev_->Step(b_, da, stream);
+    if (synchronize || (!onDevice && !dev_->HostMemory())) {
+        dev_->Synchronize(stream);
+        dev_->CheckFault();
+    }
+}
+
+void BatchRuntime::Synchronize(void *stream) {
+    dev_->Synchronize(stream);
+    dev_->CheckFault();
+}
+
+void BatchRuntime::SetDifficulty(const float *difficulty) {
+    const size_t n = (size_t)b_.count * 2;
+    for (size_t i = 0; i < n; i++)
+        if (!(difficulty[i] <= 1)) throw std::invalid_argument("expected a difficulty from 0 to 1, found " + std::to_string(difficulty[i]));
+    if (!b_.teamDifficulty) b_.teamDifficulty = Alloc<float>(n);
+    dev_->ToDevice(const_cast<float *>(b_.teamDifficulty), difficulty, n * sizeof(float));
+    hostDifficulty_.assign(difficulty, difficulty + n);
+}
+
+float BatchRuntime::Difficulty(int env, int side) const {
+    if (!hostDifficulty_.empty() && hostDifficulty_[env * 2 + side] >= 0.0f) return hostDifficulty_[env * 2 + side];
+    // GRF: episode_number is the episode before the first, so its parity is the first's.
+    const Scenario &sc = VariantAt(slots_[env].bundle * 4 + (cfg_.episodeNumber & 1)).world->scenario;
+    return side == 0 ? sc.leftDifficulty : sc.rightDifficulty;
+}
+
+std::string BatchRuntime::GetState(int env, int *episode) {
+    CheckEnvironment(env);
+    dev_->Synchronize(nullptr);
+    dev_->CheckFault();
+    auto w = std::make_unique<World>();
+    auto core = std::make_unique<EnvCore>();
+    auto slot = std::make_unique<EnvSlot>();
+    dev_->ToHost(w.get(), b_.worlds + env, sizeof(World));
+    dev_->ToHost(core.get(), b_.cores + env, sizeof(EnvCore));
+    dev_->ToHost(slot.get(), b_.slots + env, sizeof(EnvSlot));
+    StateCodec codec;
+    codec.freeControllerCount = VariantAt(slot->variant).freeControllerCount;
+    std::string bytes = codec.SaveFrame(*w, 0);
+    if (episode) {
+        episode[0] = core->prevScoreDiff;
+        episode[1] = core->prevGameMode;
+        episode[2] = core->prevBallOwnedTeam;
+        for (int a = 0; a < b_.agents; a++) episode[3 + a] = slot->collected[a];
+    }
+    return bytes;
+}
+
+void *BatchRuntime::Buffer(const std::string &name) {
+    if (name == "simple115") return b_.simple115;
+    if (name == "final_simple115") return b_.finalSimple115;
+    if (name == "reward") return b_.reward;
+    if (name == "done") return b_.done;
+    if (name == "score_reward") return b_.scoreReward;
+    if (name == "agent_mask") return agentMask_;
+    return nullptr;
+}
+
+// ---- the host device: the engine on host threads -------------------------------------------------------
+namespace {
+class HostDevice : public Device {
+public:
+    explicit HostDevice(int threads) {
+        threads_ = threads > 0 ? threads : (int)std::max(1u, std::thread::hardware_concurrency());
+    }
+    const char *Name() const override { return "host"; }
+    bool HostMemory() const override { return true; }
+    void *Allocate(size_t n) override {
+        void *p = calloc(1, n);
+        if (!p) throw std::bad_alloc();
+        return p;
+    }
+    void Release(void *p) override { free(p); }
+    void ToDevice(void *d, const void *s, size_t n) override { memcpy(d, s, n); }
+    void ToHost(void *d, const void *s, size_t n) override { memcpy(d, s, n); }
+    void ToDeviceAsync(void *d, const void *s, size_t n, void *) override { memcpy(d, s, n); }
+    void Fill(void *d, int v, size_t n) override { memset(d, v, n); }
+    void Synchronize(void *) override {}
+    void CheckFault() override {
+        if (!fault_.empty()) {
+            std::string f = fault_;
+            fault_.clear();
+            throw std::runtime_error(f);
+        }
+    }
+    int Threads() const override { return threads_; }
+    void Reset(const Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *) override {
+        ForEach(b.count, [&](int e) {
+            if (mask && !mask[e]) return true;
+            return ResetAndWriteEnvironment(b, e, seeds, reverse);
+        });
+    }
+    void Step(const Batch &b, const int32_t *actions, void *) override {
+        ForEach(b.count, [&](int e) { return StepEnvironment(b, e, actions); });
+    }
+
+private:
+    template <class F>
+    void ForEach(int count, F body) {
+        const int workers = std::min(threads_, count);
+        std::vector<std::string> faults(workers);
+        auto run = [&](int w) {
+            for (int e = w; e < count; e += workers) {
+                try {
+                    FailReason() = "";
+                    if (!body(e)) {
+                        faults[w] = "environment " + std::to_string(e) + " reached a path that GRF leaves undefined: " + FailReason();
+                        return;
+                    }
+                } catch (const std::exception &ex) {
+                    faults[w] = "environment " + std::to_string(e) + ": " + ex.what();
+                    return;
+                }
+            }
+        };
+        if (workers == 1) {
+            run(0);
+        } else {
+            std::vector<std::thread> pool;
+            for (int w = 0; w < workers; w++) pool.emplace_back(run, w);
+            for (auto &t : pool) t.join();
+        }
+        for (auto &f : faults)
+            if (!f.empty() && fault_.empty()) fault_ = f;
+    }
+    int threads_;
+    std::string fault_;
+};
+}  // namespace
+
+std::unique_ptr<Device> MakeHostDevice(int threads) { return std::make_unique<HostDevice>(threads); }
+
+}  // namespace host
+}  // namespace eng

@@ -1,0 +1,134 @@
+// The batch runtime behind the C ABI: creation from bundles and animation tables, the buffers in
+// device memory, resets, steps and state export. The work on the environments runs on a
+// `Device`: the HIP device for the product, or the host (a debugging build of the same engine
+// code that tests use to locate a divergence tick by tick).
+// Semantics: include/cuju/batch/batch_environment.h:30-621, src/environment_api.h.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "assets.h"
+
+namespace eng {
+namespace host {
+
+class Device {
+public:
+    virtual ~Device() = default;
+    virtual const char *Name() const = 0;
+    // True when device memory is host memory.
+    virtual bool HostMemory() const = 0;
+    // Zero-filled memory.
+    virtual void *Allocate(size_t bytes) = 0;
+    virtual void Release(void *p) = 0;
+    virtual void ToDevice(void *dst, const void *src, size_t bytes) = 0;
+    virtual void ToHost(void *dst, const void *src, size_t bytes) = 0;
+    virtual void ToDeviceAsync(void *dst, const void *src, size_t bytes, void *stream) = 0;
+    virtual void Fill(void *dst, int value, size_t bytes) = 0;
+    virtual void Synchronize(void *stream) = 0;
+    // Resets every environment whose mask byte is nonzero (all when `mask` is null). Arrays are in
+    // device memory.
+    virtual void Reset(const Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *stream) = 0;
+    virtual void Step(const Batch &b, const int32_t *actions, void *stream) = 0;
+    // Throws when a launch since the last check reached an undefined path.
+    virtual void CheckFault() = 0;
+    virtual int Threads() const { return 0; }
+};
+std::unique_ptr<Device> MakeHostDevice(int threads);
+
+struct Configuration {
+    std::vector<std::string> assets;
+    std::vector<int32_t> assignment;
+    std::string animations;
+    int count = 1;
+    uint64_t seed = 0;
+    int actionSet = 0;
+    int observation = kObsSimple115v2;
+    bool checkpoints = false, numpyLegacy = true, autoReset = true;
+    int threads = 0;
+    int ticksPerStep = 10;
+    int smmWidth = 96, smmHeight = 72;
+    int stack = 1;
+    std::vector<int64_t> fixedSeeds;
+    std::vector<int32_t> agentCounts;
+    int episodeNumber = 0;
+    int64_t firstIndex = 0;
+};
+
+class BatchRuntime {
+public:
+    BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> device);
+    ~BatchRuntime();
+    BatchRuntime(const BatchRuntime &) = delete;
+    BatchRuntime &operator=(const BatchRuntime &) = delete;
+
+    int Count() const { return b_.count; }
+    int Agents() const { return b_.agents; }
+    int LeftAgents(int env) const { return slots_[env].leftAgents; }
+    int RightAgents(int env) const { return slots_[env].rightAgents; }
+    int Players() const { return players_; }
+    int LeftPlayers(int env) const;
+    int RightPlayers(int env) const;
+    size_t MemoryBytes() const { return allocated_; }
+    Device &Dev() { return *dev_; }
+    const Batch &Buffers() const { return b_; }
+
+    void Reset(const uint32_t *seeds, const int32_t *reverse, void *stream);
+    void ResetMasked(const uint8_t *mask, bool maskOnDevice, const int64_t *seeds, const int32_t *reverse, void *stream);
+    void ResetDone(void *stream);
+    void Step(const int32_t *actions, bool onDevice, void *stream, bool synchronize);
+    void Synchronize(void *stream);
+    void SetDifficulty(const float *difficulty);
+    float Difficulty(int env, int side) const;
+    // The engine bytes of one environment; `episode` gets the score difference, game mode and
+    // ball-owning team after the last step, then each agent's checkpoints.
+    std::string GetState(int env, int *episode);
+    // The buffer of an output name, or null.
+    void *Buffer(const std::string &name);
+
+private:
+    template <class T>
+    T *Alloc(size_t n) {
+        void *p = dev_->Allocate(sizeof(T) * (n ? n : 1));
+        owned_.push_back(p);
+        allocated_ += sizeof(T) * (n ? n : 1);
+        return static_cast<T *>(p);
+    }
+    template <class T>
+    T *Upload(const T *src, size_t n) {
+        T *d = Alloc<T>(n);
+        if (n) dev_->ToDevice(d, src, sizeof(T) * n);
+        return d;
+    }
+    template <class T>
+    T *Upload(const std::vector<T> &v) {
+        return Upload(v.data(), v.size());
+    }
+    const Variant &VariantAt(int v) const { return bundles_[v / 4]->variants[v % 4]; }
+    void CheckStarted() const;
+    void CheckEnvironment(int env) const;
+
+    Configuration cfg_;
+    std::unique_ptr<Device> dev_;
+    std::vector<void *> owned_;
+    size_t allocated_ = 0;
+    std::vector<std::unique_ptr<Bundle>> bundles_;
+    std::unique_ptr<AnimationTables> tables_;
+    std::vector<EnvSlot> slots_;  // as created: bundles and agent counts
+    std::vector<float> hostDifficulty_;
+    std::vector<bool> started_;
+    int unstarted_ = 0;
+    int players_ = 0;
+    Batch b_{};
+    uint8_t *agentMask_ = nullptr;
+    int32_t *actions_ = nullptr;
+    int64_t *seeds_ = nullptr;
+    int32_t *reverse_ = nullptr;
+    uint8_t *mask_ = nullptr;
+};
+
+}  // namespace host
+}  // namespace eng

@@ -1,0 +1,102 @@
+/*
+ * The C ABI of the MI355X batched football step engine (libcuju_amd.so). Each entry point is the
+ * one the reference's Python binding calls for the same operation, with the same arguments and
+ * error convention, so a ctypes binding written for the reference binds this library unchanged.
+ *
+ * Calls are synchronous unless noted. A failure returns -1 or null, and cuju_last_error() gives
+ * the message (per thread). A `stream` is a HIP stream (hipStream_t), or null for the default
+ * stream. Device pointers are HIP device memory of the current device.
+ */
+#ifndef CUJU_AMD_H
+#define CUJU_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CUJU_CONFIGURATION_VERSION 2
+
+/* The batch configuration, version 2: src/environment_api.h:49-95 of the reference. */
+struct cuju_configuration {
+    int version; /* CUJU_CONFIGURATION_VERSION */
+    const char *const *assets; /* [asset_count] paths of .cjb bundles */
+    int asset_count;
+    const int *assignment; /* [environment_count] bundle indices, or null for bundle 0 */
+    const char *animations; /* path of animations.bin */
+    int environment_count;
+    unsigned long long seed; /* env i plays GRF after random.seed(seed * 2**32 + first_index + i) */
+    int action_set; /* 0 default, 1 v2, 2 full */
+    int observation; /* bit mask: 1 simple115, 2 simple115v2 (4 SMM and 8 raw are refused) */
+    int checkpoints; /* nonzero adds the checkpoint reward */
+    int numpy_legacy; /* nonzero adds it as numpy before 2.0 does */
+    int auto_reset; /* nonzero resets every environment whose episode ended within the step */
+    int threads; /* host threads of the debugging backend; ignored by the GPU */
+    int ticks_per_step; /* GRF physics_steps_per_frame, 10 there */
+    int smm_width, smm_height; /* GRF channel_dimensions */
+    int stack; /* 4 stacks observations as GRF's `stacked`, else 1 */
+    const long long *fixed_seeds; /* [environment_count] GRF game_engine_random_seed, -1 draws; null draws all */
+    const int *agent_counts; /* [asset_count][2] left/right agents, -1 keeps the bundle's; null keeps all */
+    int episode_number; /* GRF episode_number */
+    unsigned long long first_index; /* seed-rule index of environment 0 */
+    void *(*allocate)(size_t bytes, void *context); /* reserved, must be null */
+    void (*release)(void *pointer, void *context); /* reserved, must be null */
+    void *allocator_context;
+    int pin_threads; /* CPU-only options of the reference, ignored */
+    int numa;
+    int page_aligned;
+};
+
+/* src/environment_api.h:41 */
+const char *cuju_last_error(void);
+/* src/environment_api.h:44; "hip" for this library */
+const char *cuju_backend(void);
+/* src/environment_api.h:98 */
+void *cuju_environment_create(const struct cuju_configuration *settings);
+/* src/environment_api.h:161 */
+int cuju_memory_estimate(const struct cuju_configuration *settings, unsigned long long *bytes);
+/* src/environment_api.h:172 */
+int cuju_local_memory_bytes(unsigned long long *bytes);
+/* src/environment_api.h:186 */
+unsigned long long cuju_environment_memory_bytes(void *environment);
+/* src/environment_api.h:191 */
+void cuju_environment_destroy(void *environment);
+/* src/environment_api.h:195 */
+int cuju_environment_count(void *environment);
+/* src/environment_api.h:200 */
+int cuju_environment_threads(void *environment);
+/* src/environment_api.h:206 */
+int cuju_environment_agents(void *environment, int *left, int *right);
+/* src/environment_api.h:218 */
+int cuju_environment_players(void *environment, int *left, int *right);
+/* src/environment_api.h:229 */
+int cuju_environment_set_difficulty(void *environment, const float *difficulty);
+/* src/environment_api.h:240 */
+void cuju_environment_difficulty(void *environment, float *difficulty);
+/* src/environment_api.h:250 */
+int cuju_environment_reset(void *environment, const unsigned int *seeds, const int *reverse, void *stream);
+/* src/environment_api.h:269 */
+int cuju_environment_reset_masked(void *environment, const unsigned char *mask, int mask_on_device, const int64_t *seeds,
+                                  const int *reverse, void *stream, int synchronize);
+/* src/environment_api.h:287 */
+int cuju_environment_reset_done(void *environment, void *stream);
+/* src/environment_api.h:302; -2 for a host action outside [-n, n) */
+int cuju_environment_step(void *environment, const int *actions, int on_device, void *stream, int synchronize);
+/* src/environment_api.h:323 */
+int cuju_environment_step_async(void *environment, const int *actions, int on_device, void *stream);
+/* src/environment_api.h:341 */
+int cuju_environment_step_wait(void *environment);
+/* src/environment_api.h:353 */
+int cuju_environment_synchronize(void *environment, void *stream);
+/* src/environment_api.h:367 */
+const char *cuju_environment_get_state(void *environment, int index, unsigned long long *size, int *episode);
+/* src/environment_api.h:430; simple115, final_simple115, reward, done, score_reward */
+void *cuju_environment_buffer(void *environment, const char *name);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

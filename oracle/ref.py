@@ -70,15 +70,17 @@ def available() -> bool:
     return os.path.isfile(LIBRARY)
 
 
-_library = None
+_libraries = {}
 
 
-def library():
-    global _library
-    if _library is None:
-        if not available():
-            raise FileNotFoundError(f'the reference CPU library is not built: {LIBRARY}')
-        lib = ctypes.CDLL(LIBRARY)
+def library(path=None):
+    """The reference library, or another library with the same C ABI at `path` (the tests drive
+    the engine's host debugging build through the same calls)."""
+    path = path or LIBRARY
+    if path not in _libraries:
+        if not os.path.isfile(path):
+            raise FileNotFoundError(f'the library is not built: {path}')
+        lib = ctypes.CDLL(path)
         lib.cuju_last_error.restype = ctypes.c_char_p
         lib.cuju_environment_create.restype = ctypes.c_void_p
         lib.cuju_environment_create.argtypes = [ctypes.POINTER(Configuration)]
@@ -100,8 +102,8 @@ def library():
         lib.cuju_environment_buffer.restype = ctypes.c_void_p
         lib.cuju_environment_buffer.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
         lib.cuju_environment_set_difficulty.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        _library = lib
-    return _library
+        _libraries[path] = lib
+    return _libraries[path]
 
 
 def resolve_asset(name: str):
@@ -149,8 +151,8 @@ class ReferenceBatch:
                  rewards='scoring', action_set='default', stacked=False, auto_reset=True,
                  threads=0, assignment=None, agent_counts=None, first_index=0,
                  difficulty=None, numpy_legacy=True, episode_number=0,
-                 physics_steps_per_frame=10, game_engine_random_seed=None):
-        lib = library()
+                 physics_steps_per_frame=10, game_engine_random_seed=None, library_path=None):
+        lib = library(library_path)
         self._lib = lib
         names = [assets] if isinstance(assets, str) else list(assets)
         resolved = [resolve_asset(n) for n in names]

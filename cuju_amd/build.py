@@ -1,0 +1,80 @@
+"""Builds the native libraries in-tree.
+
+* ``lib/libcuju_amd.so``: the product, the engine compiled for gfx950 behind the C ABI of
+  ``include/cuju_amd.h``.
+* ``lib/libcuju_amd_host.so``: the same engine and C ABI on host threads, a debugging build that
+  tests use to follow a match tick by tick. The package never loads it.
+
+Every source compiles with IEEE semantics and no contraction of multiply-adds, which the engine's
+bit-exactness needs. ``python -m cuju_amd.build`` runs the same steps.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SOURCE = os.path.join(HERE, 'csrc')
+OUT = os.path.join(HERE, 'lib')
+BUILD = os.path.join(HERE, 'lib', 'obj')
+ARCH = 'gfx950'
+HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
+CXX = os.environ.get('CXX', 'g++')
+
+PRODUCT = os.path.join(OUT, 'libcuju_amd.so')
+HOST = os.path.join(OUT, 'libcuju_amd_host.so')
+
+HOST_SOURCES = ['host/assets.cpp', 'host/runtime.cpp', 'host/api.cpp']
+COMMON = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math', '-fvisibility=hidden', '-w']
+# Packed FP32 instructions stay off: plain float code only.
+HIP_FLAGS = ['-std=c++17', '-O3', '-fPIC', '-ffp-contract=off', '-fno-fast-math', '-fvisibility=hidden', '-w',
+             f'--offload-arch={ARCH}', '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops']
+
+
+def _run(command):
+    result = subprocess.run(command, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if result.returncode != 0:
+        raise RuntimeError('build failed: ' + ' '.join(command) + '\n' + result.stdout[-6000:])
+    return result.stdout
+
+
+def _object(source, tag):
+    return os.path.join(BUILD, tag + '_' + os.path.basename(source).replace('.', '_') + '.o')
+
+
+def build(host=True, product=True, jobs=8):
+    """Compiles both libraries (each source every time) and returns their paths."""
+    os.makedirs(BUILD, exist_ok=True)
+    tasks = []
+    if product:
+        for s in HOST_SOURCES:
+            tasks.append([CXX, *COMMON, '-c', os.path.join(SOURCE, s), '-o', _object(s, 'p')])
+        tasks.append([HIPCC, *HIP_FLAGS, '-c', os.path.join(SOURCE, 'hip_device.hip'),
+                      '-o', _object('hip_device.hip', 'p')])
+    if host:
+        for s in HOST_SOURCES + ['host/host_library.cpp']:
+            tasks.append([CXX, *COMMON, '-c', os.path.join(SOURCE, s), '-o', _object(s, 'h')])
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        for f in [pool.submit(_run, t) for t in tasks]:
+            f.result()
+    built = []
+    if product:
+        objects = [_object(s, 'p') for s in HOST_SOURCES] + [_object('hip_device.hip', 'p')]
+        _run([HIPCC, f'--offload-arch={ARCH}', '-shared', '-fPIC', '-o', PRODUCT, *objects])
+        built.append(PRODUCT)
+    if host:
+        objects = [_object(s, 'h') for s in HOST_SOURCES + ['host/host_library.cpp']]
+        _run([CXX, '-shared', '-fPIC', '-o', HOST, *objects, '-lpthread'])
+        built.append(HOST)
+    shutil.rmtree(BUILD, ignore_errors=True)
+    return built
+
+
+if __name__ == '__main__':
+    for path in build():
+        print(path)
+    sys.exit(0)

@@ -17,7 +17,7 @@
 
 #if defined(__HIPCC__)
 #define HD __host__ __device__ inline
-#define HDN __host__ __device__ __attribute__((noinline))
+#define HDN __host__ __device__ __attribute__((noinline)) inline
 #else
 #define HD inline
 #define HDN inline

@@ -1,0 +1,108 @@
+// The MI355X device of the batch runtime: device memory, copies and the two kernels (reset and
+// step). Each environment runs on one lane; a launch maps environments to lanes in blocks of
+// `kEnvironmentsPerBlock`, so with one environment per block each match owns a wavefront.
+#include <hip/hip_runtime.h>
+
+#include <stdexcept>
+#include <string>
+
+#include "host/runtime.h"
+
+namespace eng {
+__device__ uint32_t gEngineFault;
+}  // namespace eng
+
+namespace {
+
+__device__ int32_t gFaultEnvironment;
+
+// Environments per workgroup. One keeps every match on a wavefront of its own, whose other lanes
+// idle; the match code is a long sequential chain with data-dependent branches, so lanes of one
+// wavefront running different matches would serialize on divergence anyway.
+constexpr int kEnvironmentsPerBlock = 1;
+
+__device__ void RecordFault(int env) {
+    if (eng::gEngineFault == 0) eng::gEngineFault = 1;
+    atomicMin(&gFaultEnvironment, env);
+}
+
+__global__ void __launch_bounds__(kEnvironmentsPerBlock) ResetKernel(eng::Batch b, const uint8_t *mask, const int64_t *seeds,
+                                                                     const int32_t *reverse) {
+    const int env = blockIdx.x * blockDim.x + threadIdx.x;
+    if (env >= b.count) return;
+    if (mask && !mask[env]) return;
+    if (!eng::ResetAndWriteEnvironment(b, env, seeds, reverse)) RecordFault(env);
+}
+
+__global__ void __launch_bounds__(kEnvironmentsPerBlock) StepKernel(eng::Batch b, const int32_t *actions) {
+    const int env = blockIdx.x * blockDim.x + threadIdx.x;
+    if (env >= b.count) return;
+    if (!eng::StepEnvironment(b, env, actions)) RecordFault(env);
+}
+
+void Check(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+class HipDevice : public eng::host::Device {
+public:
+    HipDevice() {
+        int n = 0;
+        Check(hipGetDeviceCount(&n), "hipGetDeviceCount");
+        if (n < 1) throw std::runtime_error("no HIP device");
+        ClearFault();
+    }
+    const char *Name() const override { return "hip"; }
+    bool HostMemory() const override { return false; }
+    void *Allocate(size_t n) override {
+        void *p = nullptr;
+        Check(hipMalloc(&p, n), "hipMalloc");
+        Check(hipMemset(p, 0, n), "hipMemset");
+        return p;
+    }
+    void Release(void *p) override { (void)hipFree(p); }
+    void ToDevice(void *d, const void *s, size_t n) override { Check(hipMemcpy(d, s, n, hipMemcpyHostToDevice), "hipMemcpy"); }
+    void ToHost(void *d, const void *s, size_t n) override { Check(hipMemcpy(d, s, n, hipMemcpyDeviceToHost), "hipMemcpy"); }
+    void ToDeviceAsync(void *d, const void *s, size_t n, void *stream) override {
+        Check(hipMemcpyAsync(d, s, n, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream)), "hipMemcpyAsync");
+    }
+    void Fill(void *d, int v, size_t n) override { Check(hipMemset(d, v, n), "hipMemset"); }
+    void Synchronize(void *stream) override { Check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize"); }
+    void Reset(const eng::Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *stream) override {
+        const int blocks = (b.count + kEnvironmentsPerBlock - 1) / kEnvironmentsPerBlock;
+        hipLaunchKernelGGL(ResetKernel, dim3(blocks), dim3(kEnvironmentsPerBlock), 0, static_cast<hipStream_t>(stream), b, mask, seeds,
+                           reverse);
+        Check(hipGetLastError(), "reset launch");
+    }
+    void Step(const eng::Batch &b, const int32_t *actions, void *stream) override {
+        const int blocks = (b.count + kEnvironmentsPerBlock - 1) / kEnvironmentsPerBlock;
+        hipLaunchKernelGGL(StepKernel, dim3(blocks), dim3(kEnvironmentsPerBlock), 0, static_cast<hipStream_t>(stream), b, actions);
+        Check(hipGetLastError(), "step launch");
+    }
+    void CheckFault() override {
+        uint32_t fault = 0;
+        int32_t env = 0;
+        Check(hipMemcpyFromSymbol(&fault, HIP_SYMBOL(eng::gEngineFault), sizeof(fault)), "hipMemcpyFromSymbol");
+        if (!fault) return;
+        Check(hipMemcpyFromSymbol(&env, HIP_SYMBOL(gFaultEnvironment), sizeof(env)), "hipMemcpyFromSymbol");
+        ClearFault();
+        throw std::runtime_error("environment " + std::to_string(env) + (fault == 2 ? " reached a state that no match reaches" : " reached a path that GRF leaves undefined"));
+    }
+
+private:
+    void ClearFault() {
+        const uint32_t zero = 0;
+        const int32_t none = 0x7fffffff;
+        Check(hipMemcpyToSymbol(HIP_SYMBOL(eng::gEngineFault), &zero, sizeof(zero)), "hipMemcpyToSymbol");
+        Check(hipMemcpyToSymbol(HIP_SYMBOL(gFaultEnvironment), &none, sizeof(none)), "hipMemcpyToSymbol");
+    }
+};
+
+}  // namespace
+
+namespace eng {
+namespace host {
+std::unique_ptr<Device> MakeLibraryDevice(int) { return std::make_unique<HipDevice>(); }
+extern const char *const kBackendName = "hip";
+}  // namespace host
+}  // namespace eng

@@ -2,9 +2,85 @@
 // a match tick by tick; the package never loads it.
 #include "runtime.h"
 
+#include <algorithm>
+#include <stdexcept>
+#include <thread>
+
 namespace eng {
 namespace host {
-std::unique_ptr<Device> MakeLibraryDevice(int threads) { return MakeHostDevice(threads); }
+// ---- the host device: the engine on host threads -------------------------------------------------------
+namespace {
+class HostDevice : public Device {
+public:
+    explicit HostDevice(int threads) {
+        threads_ = threads > 0 ? threads : (int)std::max(1u, std::thread::hardware_concurrency());
+    }
+    const char *Name() const override { return "host"; }
+    bool HostMemory() const override { return true; }
+    void *Allocate(size_t n) override {
+        void *p = calloc(1, n);
+        if (!p) throw std::bad_alloc();
+        return p;
+    }
+    void Release(void *p) override { free(p); }
+    void ToDevice(void *d, const void *s, size_t n) override { memcpy(d, s, n); }
+    void ToHost(void *d, const void *s, size_t n) override { memcpy(d, s, n); }
+    void ToDeviceAsync(void *d, const void *s, size_t n, void *) override { memcpy(d, s, n); }
+    void Fill(void *d, int v, size_t n) override { memset(d, v, n); }
+    void Synchronize(void *) override {}
+    void CheckFault() override {
+        if (!fault_.empty()) {
+            std::string f = fault_;
+            fault_.clear();
+            throw std::runtime_error(f);
+        }
+    }
+    int Threads() const override { return threads_; }
+    void Reset(const Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *) override {
+        ForEach(b.count, [&](int e) {
+            if (mask && !mask[e]) return true;
+            return ResetAndWriteEnvironment(b, e, seeds, reverse);
+        });
+    }
+    void Step(const Batch &b, const int32_t *actions, void *) override {
+        ForEach(b.count, [&](int e) { return StepEnvironment(b, e, actions); });
+    }
+
+private:
+    template <class F>
+    void ForEach(int count, F body) {
+        const int workers = std::min(threads_, count);
+        std::vector<std::string> faults(workers);
+        auto run = [&](int w) {
+            for (int e = w; e < count; e += workers) {
+                try {
+                    FailReason() = "";
+                    if (!body(e)) {
+                        faults[w] = "environment " + std::to_string(e) + " reached a path that GRF leaves undefined: " + FailReason();
+                        return;
+                    }
+                } catch (const std::exception &ex) {
+                    faults[w] = "environment " + std::to_string(e) + ": " + ex.what();
+                    return;
+                }
+            }
+        };
+        if (workers == 1) {
+            run(0);
+        } else {
+            std::vector<std::thread> pool;
+            for (int w = 0; w < workers; w++) pool.emplace_back(run, w);
+            for (auto &t : pool) t.join();
+        }
+        for (auto &f : faults)
+            if (!f.empty() && fault_.empty()) fault_ = f;
+    }
+    int threads_;
+    std::string fault_;
+};
+}  // namespace
+
+std::unique_ptr<Device> MakeLibraryDevice(int threads) { return std::make_unique<HostDevice>(threads); }
 extern const char *const kBackendName = "host";
 }  // namespace host
 }  // namespace eng
@@ -29,4 +105,12 @@ extern "C" __attribute__((visibility("default"))) const char *cuju_debug_state_s
     } catch (...) {
         return nullptr;
     }
+}
+
+// The first `count` episode seeds that environment `index` of a batch with `seed` draws.
+extern "C" __attribute__((visibility("default"))) void cuju_debug_episode_seeds(unsigned long long seed, unsigned int index, int count,
+                                                                                  unsigned int *out) {
+    auto g = std::make_unique<eng::EpisodeGenerator>();
+    eng::SeedEpisodeGenerator(*g, seed, index);
+    for (int i = 0; i < count; i++) out[i] = eng::DrawEpisodeSeed(*g);
 }

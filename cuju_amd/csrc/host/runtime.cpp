@@ -4,7 +4,6 @@
 
 #include <algorithm>
 #include <stdexcept>
-#include <thread>
 
 namespace eng {
 namespace host {
@@ -308,79 +307,6 @@ void *BatchRuntime::Buffer(const std::string &name) {
     return nullptr;
 }
 
-// ---- the host device: the engine on host threads -------------------------------------------------------
-namespace {
-class HostDevice : public Device {
-public:
-    explicit HostDevice(int threads) {
-        threads_ = threads > 0 ? threads : (int)std::max(1u, std::thread::hardware_concurrency());
-    }
-    const char *Name() const override { return "host"; }
-    bool HostMemory() const override { return true; }
-    void *Allocate(size_t n) override {
-        void *p = calloc(1, n);
-        if (!p) throw std::bad_alloc();
-        return p;
-    }
-    void Release(void *p) override { free(p); }
-    void ToDevice(void *d, const void *s, size_t n) override { memcpy(d, s, n); }
-    void ToHost(void *d, const void *s, size_t n) override { memcpy(d, s, n); }
-    void ToDeviceAsync(void *d, const void *s, size_t n, void *) override { memcpy(d, s, n); }
-    void Fill(void *d, int v, size_t n) override { memset(d, v, n); }
-    void Synchronize(void *) override {}
-    void CheckFault() override {
-        if (!fault_.empty()) {
-            std::string f = fault_;
-            fault_.clear();
-            throw std::runtime_error(f);
-        }
-    }
-    int Threads() const override { return threads_; }
-    void Reset(const Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *) override {
-        ForEach(b.count, [&](int e) {
-            if (mask && !mask[e]) return true;
-            return ResetAndWriteEnvironment(b, e, seeds, reverse);
-        });
-    }
-    void Step(const Batch &b, const int32_t *actions, void *) override {
-        ForEach(b.count, [&](int e) { return StepEnvironment(b, e, actions); });
-    }
-
-private:
-    template <class F>
-    void ForEach(int count, F body) {
-        const int workers = std::min(threads_, count);
-        std::vector<std::string> faults(workers);
-        auto run = [&](int w) {
-            for (int e = w; e < count; e += workers) {
-                try {
-                    FailReason() = "";
-                    if (!body(e)) {
-                        faults[w] = "environment " + std::to_string(e) + " reached a path that GRF leaves undefined: " + FailReason();
-                        return;
-                    }
-                } catch (const std::exception &ex) {
-                    faults[w] = "environment " + std::to_string(e) + ": " + ex.what();
-                    return;
-                }
-            }
-        };
-        if (workers == 1) {
-            run(0);
-        } else {
-            std::vector<std::thread> pool;
-            for (int w = 0; w < workers; w++) pool.emplace_back(run, w);
-            for (auto &t : pool) t.join();
-        }
-        for (auto &f : faults)
-            if (!f.empty() && fault_.empty()) fault_ = f;
-    }
-    int threads_;
-    std::string fault_;
-};
-}  // namespace
-
-std::unique_ptr<Device> MakeHostDevice(int threads) { return std::make_unique<HostDevice>(threads); }
 
 }  // namespace host
 }  // namespace eng

@@ -37,7 +37,6 @@ public:
     virtual void CheckFault() = 0;
     virtual int Threads() const { return 0; }
 };
-std::unique_ptr<Device> MakeHostDevice(int threads);
 
 struct Configuration {
     std::vector<std::string> assets;

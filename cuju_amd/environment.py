@@ -1,0 +1,344 @@
+"""`BatchEnvironment`: many GRF matches stepped together on one MI355X.
+
+The surface follows the reference's `cuju.BatchEnvironment` (python/cuju/_batch/environment.py:220
+onward): the same constructor arguments for the options this build supports, `reset`, `step`,
+`reset_done`, `observation`, `get_state` and `close`, and outputs that are PyTorch tensors viewing
+the library's device buffers without a copy. Every call overwrites the same tensors, so a caller
+clones what it keeps.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import struct
+from typing import Any
+
+import numpy as np
+import torch
+
+from . import library as _library
+from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, ConfigurationError,
+                     EnvironmentIndexError, MissingFileError, from_library)
+
+REPRESENTATIONS = {'simple115': 1, 'simple115v2': 2}
+ACTION_SETS = {'default': 0, 'v2': 1, 'full': 2}
+ACTION_COUNTS = {'default': 19, 'v2': 20, 'full': 33}
+MAXIMUM_AGENTS = 22
+
+
+def resolve_assets(name: str) -> tuple[str, tuple[int, int]]:
+    """`<scenario>_l<L>_r<R>` to a shipped bundle and the agents per side; a path stays a path.
+    The bundle with the fewest agents serves any counts (python/cuju/_batch/assets.py:39-68)."""
+    if os.path.sep in name or name.endswith('.cjb'):
+        if not os.path.isfile(name):
+            raise MissingFileError(f'no asset bundle at {name}')
+        return name, (-1, -1)
+    directory = os.path.join(_library.DATA, 'assets')
+    shipped = os.path.join(directory, name + '.cjb')
+    if os.path.isfile(shipped):
+        return shipped, (-1, -1)
+    match = re.fullmatch(r'(.+)_l(\d+)_r(\d+)', name)
+    if match is None:
+        path, counts = os.path.join(directory, name + '_l0_r0.cjb'), (1, 0)
+    else:
+        path = os.path.join(directory, match.group(1) + '_l0_r0.cjb')
+        counts = (int(match.group(2)), int(match.group(3)))
+    if not os.path.isfile(path):
+        raise MissingFileError(f'no shipped bundle for {name}')
+    return path, counts
+
+
+def _pickle_text(value: str) -> bytes:
+    data = value.encode()
+    return b'X' + struct.pack('<I', len(data)) + data
+
+
+def _pickle_int(value: int) -> bytes:
+    return b'J' + struct.pack('<i', value)
+
+
+def episode_pickle(episode, collected=None) -> bytes:
+    """GRF's pickle of the episode logic that precedes the engine bytes of a state: the core's
+    previous score difference, game mode and ball-owning team, then the checkpoints per agent
+    (python/cuju/_batch/state.py:38-77)."""
+    keys = ('previous_score_diff', 'previous_game_mode', 'prev_ball_owned_team')
+    logic = b''.join(_pickle_text(k) + _pickle_int(v) for k, v in zip(keys, episode))
+    data = (b'\x80\x02}(' + _pickle_text('FootballEnvCore')
+            + b'cgfootball.env.football_env_core\nEnvState\n' + b')\x81}(' + logic + b'ub')
+    if collected is not None:
+        data += (_pickle_text('CheckpointRewardWrapper') + b'}('
+                 + b''.join(_pickle_int(a) + _pickle_int(c) for a, c in enumerate(collected) if c)
+                 + b'u')
+    return data + b'u.'
+
+
+class _DeviceArray:
+    """A device buffer that `torch.as_tensor` reads through `__cuda_array_interface__`."""
+
+    _TYPES = {torch.float32: '<f4', torch.int32: '<i4', torch.uint8: '|u1'}
+
+    def __init__(self, pointer, shape, dtype, owner):
+        self.owner = owner
+        self.__cuda_array_interface__ = {'data': (pointer, False), 'shape': tuple(shape),
+                                         'typestr': self._TYPES[dtype], 'version': 2,
+                                         'strides': None}
+
+
+class _Native:
+    """The library handle, kept alive by every tensor that views the batch's memory."""
+
+    def __init__(self, lib, device):
+        self.lib, self.device, self.handle = lib, device, None
+
+    def free(self):
+        if self.handle:
+            with torch.cuda.device(self.device):
+                self.lib.cuju_environment_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class BatchEnvironment:
+    """A batch of GRF environments on one HIP device."""
+
+    def __init__(self, assets: str | list[str], animations: str | None = None, environment_count: int = 1024,
+                 representation: str = 'simple115v2', rewards: str = 'scoring', action_set: str = 'default',
+                 seed: int = 0, numpy_legacy: bool = True, auto_reset: bool = True, assignment=None,
+                 difficulty=None, device: str | int | torch.device = 'cuda', physics_steps_per_frame: int = 10,
+                 stacked: bool = False, game_engine_random_seed=None, squeeze: bool = False, agent_counts=None,
+                 episode_number: int = 0, first_index: int = 0, check_actions: bool = False,
+                 library: str | None = None):
+        if representation not in REPRESENTATIONS:
+            raise ChoiceError(f'expected a representation of {sorted(REPRESENTATIONS)}, found {representation!r}')
+        if action_set not in ACTION_SETS:
+            raise ChoiceError(f'expected an action set of {sorted(ACTION_SETS)}, found {action_set!r}')
+        reward_parts = set(rewards.split(','))
+        if not reward_parts <= {'scoring', 'checkpoints'} or 'scoring' not in reward_parts:
+            raise ChoiceError(f"expected rewards 'scoring' or 'scoring,checkpoints', found {rewards!r}")
+        if environment_count < 1:
+            raise ConfigurationError(f'expected at least one environment, found {environment_count}')
+        self._torch_device = torch.device(device) if not isinstance(device, int) else torch.device('cuda', device)
+        if self._torch_device.type != 'cuda':
+            raise ConfigurationError('this build steps environments on a HIP device only')
+        if self._torch_device.index is None:
+            self._torch_device = torch.device('cuda', torch.cuda.current_device())
+        lib = _library.load(library)
+        if lib.cuju_backend().decode() != 'hip':
+            raise ConfigurationError('expected the HIP library')
+        names = [assets] if isinstance(assets, str) else list(assets)
+        resolved = [resolve_assets(n) for n in names]
+        counts = [pair for _, pair in resolved]
+        if agent_counts is not None:
+            counts = [tuple(c) for c in agent_counts]
+            if len(counts) != len(names):
+                raise ConfigurationError('expected one agent count pair per bundle')
+        self.checkpoints = 'checkpoints' in reward_parts
+        self.stack = 4 if stacked else 1
+        self.stacked = bool(stacked)
+        self.squeeze = bool(squeeze)
+        self.representation = representation
+        self.action_count = ACTION_COUNTS[action_set]
+        self.environment_count = environment_count
+        self._check_actions = check_actions
+        self._paths = (ctypes.c_char_p * len(names))(*(p.encode() for p, _ in resolved))
+        self._counts = np.ascontiguousarray([c for pair in counts for c in pair], dtype=np.int32)
+        self._assignment = None if assignment is None else np.ascontiguousarray(assignment, dtype=np.int32)
+        self._fixed = None
+        if game_engine_random_seed is not None:
+            self._fixed = np.ascontiguousarray(np.broadcast_to(
+                np.asarray(game_engine_random_seed, dtype=np.int64), (environment_count,)))
+        animations = animations or os.path.join(_library.DATA, 'animations.bin')
+        if not os.path.isfile(animations):
+            raise MissingFileError(f'no animation tables at {animations}')
+        cfg = _library.Configuration(
+            version=2, assets=self._paths, asset_count=len(names),
+            assignment=None if self._assignment is None else self._assignment.ctypes.data,
+            animations=animations.encode(), environment_count=environment_count, seed=seed,
+            action_set=ACTION_SETS[action_set], observation=REPRESENTATIONS[representation],
+            checkpoints=int(self.checkpoints), numpy_legacy=int(numpy_legacy), auto_reset=int(auto_reset),
+            threads=0, ticks_per_step=physics_steps_per_frame, smm_width=96, smm_height=72, stack=self.stack,
+            fixed_seeds=None if self._fixed is None else self._fixed.ctypes.data,
+            agent_counts=self._counts.ctypes.data, episode_number=episode_number, first_index=first_index,
+            allocate=None, release=None, allocator_context=None, pin_threads=0, numa=0, page_aligned=0)
+        self._native = _Native(lib, self._torch_device)
+        with torch.cuda.device(self._torch_device):
+            handle = lib.cuju_environment_create(ctypes.byref(cfg))
+        if not handle:
+            raise ConfigurationError(lib.cuju_last_error().decode())
+        self._native.handle = handle
+        self._lib = lib
+        left = np.zeros(environment_count, dtype=np.int32)
+        right = np.zeros(environment_count, dtype=np.int32)
+        self.agents = lib.cuju_environment_agents(handle, left.ctypes.data, right.ctypes.data)
+        self.left_agents, self.right_agents = left, right
+        pl = np.zeros(environment_count, dtype=np.int32)
+        pr = np.zeros(environment_count, dtype=np.int32)
+        self.players = lib.cuju_environment_players(handle, pl.ctypes.data, pr.ctypes.data)
+        self.agent_mask = torch.as_tensor(
+            np.arange(self.agents)[None, :] < (left + right)[:, None], device=self._torch_device)
+        if difficulty is not None:
+            values = np.ascontiguousarray(np.broadcast_to(np.asarray(difficulty, dtype=np.float32),
+                                                          (environment_count, 2)))
+            self._check(lib.cuju_environment_set_difficulty(handle, values.ctypes.data))
+        width = 115 * self.stack
+        self._observation = self._buffer('simple115', (environment_count, self.agents, width), torch.float32)
+        self._final = self._buffer('final_simple115', (environment_count, self.agents, width), torch.float32)
+        self._reward = self._buffer('reward', (environment_count, self.agents), torch.float32)
+        self._done = self._buffer('done', (environment_count,), torch.uint8)
+        self._score_reward = self._buffer('score_reward', (environment_count,), torch.int32)
+
+    # ---- plumbing ----
+    @property
+    def device(self) -> str:
+        return 'cuda'
+
+    @property
+    def torch_device(self) -> torch.device:
+        return self._torch_device
+
+    def _handle(self):
+        if not self._native.handle:
+            raise ClosedError('the batch is closed')
+        return self._native.handle
+
+    def _check(self, status):
+        if status == -2:
+            raise ActionRangeError(self._lib.cuju_last_error().decode())
+        if status != 0:
+            raise from_library(self._lib.cuju_last_error().decode())
+
+    def _buffer(self, name, shape, dtype):
+        pointer = self._lib.cuju_environment_buffer(self._handle(), name.encode())
+        if not pointer:
+            raise from_library(self._lib.cuju_last_error().decode())
+        return torch.as_tensor(_DeviceArray(pointer, shape, dtype, self._native), device=self._torch_device)
+
+    def _stream(self):
+        return torch.cuda.current_stream(self._torch_device).cuda_stream
+
+    def _view(self, tensor):
+        return tensor[:, 0] if self.squeeze and self.agents == 1 else tensor
+
+    def _outputs(self):
+        return (self._view(self._observation), self._view(self._reward), self._done.bool(),
+                self._view(self._final))
+
+    # ---- the environment ----
+    def reset(self, seeds: Any = None, reverse: Any = None, mask: Any = None):
+        """Starts the next episode of every environment, or of those that `mask` selects."""
+        n = self.environment_count
+        seed_array = reverse_array = None
+        if seeds is not None:
+            seed_array = self._integers(seeds, 'seeds')
+            if ((seed_array < -1) | (seed_array > 4294967295)).any():
+                raise ArgumentError(f'expected seeds from 0 to 4294967295, or -1 to draw, found {seed_array.tolist()}')
+        if reverse is not None:
+            reverse_array = self._integers(reverse, 'reverse')
+            if ((reverse_array != 0) & (reverse_array != 1)).any():
+                raise ArgumentError(f'expected reverse flags of 0 or 1, found {reverse_array.tolist()}')
+            reverse_array = np.ascontiguousarray(reverse_array, dtype=np.int32)
+        with torch.cuda.device(self._torch_device):
+            if mask is not None or (seed_array is not None and (seed_array == -1).any()):
+                device_mask = None
+                host_mask = None
+                on_device = 0
+                if mask is not None:
+                    if isinstance(mask, torch.Tensor) and mask.device == self._torch_device:
+                        device_mask = mask.to(torch.uint8).reshape(n).contiguous()
+                        on_device = 1
+                    else:
+                        host_mask = np.ascontiguousarray(np.broadcast_to(np.asarray(
+                            mask.cpu() if isinstance(mask, torch.Tensor) else mask, dtype=bool), (n,)), dtype=np.uint8)
+                seeds64 = None if seed_array is None else np.ascontiguousarray(seed_array, dtype=np.int64)
+                pointer = (device_mask.data_ptr() if device_mask is not None
+                           else None if host_mask is None else host_mask.ctypes.data)
+                self._check(self._lib.cuju_environment_reset_masked(
+                    self._handle(), pointer, on_device, None if seeds64 is None else seeds64.ctypes.data,
+                    None if reverse_array is None else reverse_array.ctypes.data, self._stream(),
+                    int(mask is None)))
+            else:
+                seeds32 = None if seed_array is None else np.ascontiguousarray(seed_array, dtype=np.uint32)
+                self._check(self._lib.cuju_environment_reset(
+                    self._handle(), None if seeds32 is None else seeds32.ctypes.data,
+                    None if reverse_array is None else reverse_array.ctypes.data, self._stream()))
+        return self._outputs()[0]
+
+    def _integers(self, values, name):
+        array = values.cpu().numpy() if isinstance(values, torch.Tensor) else np.asarray(values)
+        if array.dtype.kind not in 'iub':
+            raise TypeError(f'expected integer {name}, found {array.dtype}')
+        try:
+            return np.ascontiguousarray(np.broadcast_to(array.astype(np.int64), (self.environment_count,)))
+        except ValueError:
+            raise ArgumentError(f'expected one {name} value or one per environment, found shape {array.shape}') from None
+
+    def reset_done(self) -> None:
+        """Starts the next episode of every environment whose done flag is set."""
+        with torch.cuda.device(self._torch_device):
+            self._check(self._lib.cuju_environment_reset_done(self._handle(), self._stream()))
+
+    def observation(self):
+        return self._outputs()[0]
+
+    def step(self, actions: Any):
+        """Runs one step of every environment on the current stream, without waiting for it."""
+        shape = (self.environment_count, self.agents)
+        if not isinstance(actions, torch.Tensor):
+            actions = torch.as_tensor(actions)
+        if actions.is_floating_point() or actions.is_complex():
+            raise TypeError(f'expected integer action indices, found {actions.dtype}')
+        if tuple(actions.shape) != shape and not (self.agents == 1 and tuple(actions.shape) == (shape[0],)):
+            raise ArgumentError(f'expected actions of the shape {shape}, found {tuple(actions.shape)}')
+        with torch.cuda.device(self._torch_device):
+            if actions.device == self._torch_device:
+                staged = actions.to(torch.int32).reshape(shape).contiguous()
+                if self._check_actions and bool(((staged < -self.action_count) | (staged >= self.action_count)).any()):
+                    raise ActionRangeError(f'expected action indices from {-self.action_count} to {self.action_count - 1}')
+                status = self._lib.cuju_environment_step(self._handle(), staged.data_ptr(), 1, self._stream(), 0)
+            else:
+                staged = np.ascontiguousarray(actions.numpy(), dtype=np.int32).reshape(shape)
+                status = self._lib.cuju_environment_step(self._handle(), staged.ctypes.data, 0, self._stream(), 0)
+        self._check(status)
+        observation, reward, done, final = self._outputs()
+        return observation, reward, done, {'final_observation': final, 'score_reward': self._score_reward}
+
+    def synchronize(self) -> None:
+        """Waits for the batch's work and reports a fault of any environment."""
+        with torch.cuda.device(self._torch_device):
+            self._check(self._lib.cuju_environment_synchronize(self._handle(), self._stream()))
+
+    def get_state(self, index: int) -> bytes:
+        """GRF's state of environment `index`: an int32 pickle length, the pickle of the episode
+        logic, then the engine bytes."""
+        if not 0 <= index < self.environment_count:
+            raise EnvironmentIndexError(f'expected an environment from 0 to {self.environment_count - 1}, found {index}')
+        size = ctypes.c_ulonglong()
+        episode = (ctypes.c_int * (3 + MAXIMUM_AGENTS))()
+        with torch.cuda.device(self._torch_device):
+            torch.cuda.current_stream(self._torch_device).synchronize()
+            pointer = self._lib.cuju_environment_get_state(self._handle(), index, ctypes.byref(size), episode)
+        if not pointer:
+            raise from_library(self._lib.cuju_last_error().decode())
+        match = ctypes.string_at(pointer, size.value)
+        collected = list(episode)[3:3 + self.agents] if self.checkpoints else None
+        data = episode_pickle(list(episode)[:3], collected)
+        return struct.pack('<i', len(data)) + data + match
+
+    def memory_bytes(self) -> int:
+        return int(self._lib.cuju_environment_memory_bytes(self._handle()))
+
+    def close(self) -> None:
+        self._native.free()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exception):
+        self.close()

@@ -1,0 +1,96 @@
+"""Loads the native library and declares its C ABI (include/cuju_amd.h) for ctypes.
+
+The package calls only the HIP library `lib/libcuju_amd.so`. Without it every call fails with
+`MissingFileError`: there is no other implementation to fall back to.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+from .errors import MissingFileError
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PRODUCT = os.path.join(HERE, 'lib', 'libcuju_amd.so')
+DATA = os.path.join(HERE, 'data')
+
+
+class Configuration(ctypes.Structure):
+    """`struct cuju_configuration`, version 2."""
+
+    _fields_ = [
+        ('version', ctypes.c_int),
+        ('assets', ctypes.POINTER(ctypes.c_char_p)),
+        ('asset_count', ctypes.c_int),
+        ('assignment', ctypes.c_void_p),
+        ('animations', ctypes.c_char_p),
+        ('environment_count', ctypes.c_int),
+        ('seed', ctypes.c_ulonglong),
+        ('action_set', ctypes.c_int),
+        ('observation', ctypes.c_int),
+        ('checkpoints', ctypes.c_int),
+        ('numpy_legacy', ctypes.c_int),
+        ('auto_reset', ctypes.c_int),
+        ('threads', ctypes.c_int),
+        ('ticks_per_step', ctypes.c_int),
+        ('smm_width', ctypes.c_int),
+        ('smm_height', ctypes.c_int),
+        ('stack', ctypes.c_int),
+        ('fixed_seeds', ctypes.c_void_p),
+        ('agent_counts', ctypes.c_void_p),
+        ('episode_number', ctypes.c_int),
+        ('first_index', ctypes.c_ulonglong),
+        ('allocate', ctypes.c_void_p),
+        ('release', ctypes.c_void_p),
+        ('allocator_context', ctypes.c_void_p),
+        ('pin_threads', ctypes.c_int),
+        ('numa', ctypes.c_int),
+        ('page_aligned', ctypes.c_int),
+    ]
+
+
+# Every entry point of include/cuju_amd.h: (name, result, arguments).
+P, I, U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_ulonglong
+SIGNATURES = [
+    ('cuju_last_error', ctypes.c_char_p, []),
+    ('cuju_backend', ctypes.c_char_p, []),
+    ('cuju_environment_create', P, [ctypes.POINTER(Configuration)]),
+    ('cuju_memory_estimate', I, [ctypes.POINTER(Configuration), ctypes.POINTER(U64)]),
+    ('cuju_local_memory_bytes', I, [ctypes.POINTER(U64)]),
+    ('cuju_environment_memory_bytes', U64, [P]),
+    ('cuju_environment_destroy', None, [P]),
+    ('cuju_environment_count', I, [P]),
+    ('cuju_environment_threads', I, [P]),
+    ('cuju_environment_agents', I, [P, P, P]),
+    ('cuju_environment_players', I, [P, P, P]),
+    ('cuju_environment_set_difficulty', I, [P, P]),
+    ('cuju_environment_difficulty', None, [P, P]),
+    ('cuju_environment_reset', I, [P, P, P, P]),
+    ('cuju_environment_reset_masked', I, [P, P, I, P, P, P, I]),
+    ('cuju_environment_reset_done', I, [P, P]),
+    ('cuju_environment_step', I, [P, P, I, P, I]),
+    ('cuju_environment_step_async', I, [P, P, I, P]),
+    ('cuju_environment_step_wait', I, [P]),
+    ('cuju_environment_synchronize', I, [P, P]),
+    ('cuju_environment_get_state', P, [P, I, ctypes.POINTER(U64), P]),
+    ('cuju_environment_buffer', P, [P, ctypes.c_char_p]),
+]
+
+_loaded = {}
+
+
+def load(path: str | None = None):
+    """The library at `path`, by default the in-tree HIP build, with its signatures declared."""
+    path = os.path.abspath(path or PRODUCT)
+    if path not in _loaded:
+        if not os.path.isfile(path):
+            raise MissingFileError(
+                f'the HIP library is not built: {path} (run `python -m cuju_amd.build`)')
+        lib = ctypes.CDLL(path)
+        for name, result, arguments in SIGNATURES:
+            function = getattr(lib, name)
+            function.restype = result
+            function.argtypes = arguments
+        _loaded[path] = lib
+    return _loaded[path]

@@ -70,14 +70,19 @@ def cpu_baseline(environments, steps, seed):
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument('--gpus', type=int, default=1)
-    parser.add_argument('--steps', type=int, default=20)
-    parser.add_argument('--warmup', type=int, default=3)
+    parser.add_argument('--steps', type=int, default=30)
+    parser.add_argument('--warmup', type=int, default=5)
     parser.add_argument('--environments', type=int, default=ENVIRONMENTS)
     parser.add_argument('--seed', type=int, default=0)
-    parser.add_argument('--cpu-environments', type=int, default=512)
-    parser.add_argument('--cpu-steps', type=int, default=20)
+    parser.add_argument('--cpu-environments', type=int, default=4096)
+    parser.add_argument('--cpu-steps', type=int, default=40)
     parser.add_argument('--no-cpu', action='store_true')
+    parser.add_argument('--lanes', type=int, default=None, help='environments per workgroup, 1 to 64')
+    parser.add_argument('--copy-probe', action='store_true',
+                        help='also run a 1 GiB device-to-device copy, the calibration of HBM byte counters')
     args = parser.parse_args()
+    if args.lanes is not None:
+        os.environ['CUJU_AMD_LANES'] = str(args.lanes)
     if args.gpus != 1:
         print(f'bench.py measures one GPU: every GPU box here has one, and the engine has no multi-GPU path '
               f'(environments shard by first_index with no exchange); asked for --gpus {args.gpus}.', file=sys.stderr)
@@ -123,6 +128,13 @@ def main():
     print(f'[bench] {args.steps} steps in {wall:.2f} s, mean step kernel {mean_launch_s * 1000:.1f} ms', file=sys.stderr,
           flush=True)
     env.close()
+    if args.copy_probe:
+        source = torch.empty(1 << 28, dtype=torch.float32, device=device).fill_(1.0)
+        target = torch.empty_like(source)
+        torch.cuda.synchronize()
+        target.copy_(source)
+        torch.cuda.synchronize()
+        print('[bench] copy probe: 1 GiB read, 1 GiB written', file=sys.stderr, flush=True)
 
     baseline = None
     if not args.no_cpu:

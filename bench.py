@@ -32,6 +32,9 @@ HBM_PEAK_GBS = 8000.0
 # Algorithmic bytes of one environment step: the world read and written once (2 x 373,552 B)
 # plus the compulsory I/O of this configuration (actions, observations, reward, done, score).
 BYTES_PER_ENV_STEP = 752_257
+# HBM bytes one step launch moves at 16,384 environments, read + written, from rocprofv3
+# FETCH_SIZE and WRITE_SIZE passes scaled by a 1 GiB copy (profiles/step_kernel_11v11_hard_16384.md).
+MEASURED_TRAFFIC = {16384: 102_427_793_892 + 39_220_378_224}
 
 
 def counter_actions(torch, seed, step, environments, agents, device):
@@ -75,7 +78,7 @@ def main():
     parser.add_argument('--environments', type=int, default=ENVIRONMENTS)
     parser.add_argument('--seed', type=int, default=0)
     parser.add_argument('--cpu-environments', type=int, default=4096)
-    parser.add_argument('--cpu-steps', type=int, default=40)
+    parser.add_argument('--cpu-steps', type=int, default=60)
     parser.add_argument('--no-cpu', action='store_true')
     parser.add_argument('--lanes', type=int, default=None, help='environments per workgroup, 1 to 64')
     parser.add_argument('--copy-probe', action='store_true',
@@ -158,7 +161,7 @@ def main():
                                f'3000-step episodes, auto reset', 'environments': args.environments,
                    'agents': AGENTS, 'reset_seconds': reset_seconds},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': achieved / HBM_PEAK_GBS, 'traffic': None},
+                     'frac': achieved / HBM_PEAK_GBS, 'traffic': MEASURED_TRAFFIC.get(args.environments)},
         'cpu_baseline': baseline,
     }
     print(json.dumps(line))

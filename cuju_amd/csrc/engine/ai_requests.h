@@ -556,6 +556,7 @@ HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
 }
 
 HDN bool PlayerRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
+    ENG_SCOPE(13);
     if (ExternalControllerActive(w, p)) return HumanRequestCommand(w, c, p, q);
     AIControllerState &e = w.match.players[p].controller;
     AIController ai(w, c, p, q, e.base, &e);

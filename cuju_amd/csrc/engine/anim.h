@@ -469,6 +469,7 @@ HDN Vec3 MovementAtFrame(const Vec3 *pos, int count, uint32_t frame, uint32_t sm
 }
 
 HDN void CalculateSpatialState(const Ctx &c, Humanoid &h) {
+    ENG_SCOPE(29);
     AnimationState &cur = h.anim;
     const Anim &a = c.A(cur.anim);
     SpatialState &s = h.spatial;

@@ -197,6 +197,7 @@ HD void BallRecalculatePrediction(World &w) {
 }
 
 HDN void BallProcess(Ball &b, bool inGoal) {
+    ENG_SCOPE(7);
     BallMaterialize(b);
     BallSpatial s = BallCalculatePrediction(b, inGoal);
     b.momentum = s.momentum;
@@ -398,6 +399,7 @@ HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p)
 }
 
 HDN void TeamUpdatePossessionStatistics(World &w, const Ctx &c, int teamID) {
+    ENG_SCOPE(16);
     for (int p = 0; p < w.match.playerCount; p++)
         if (w.playerTeamID[p] == teamID && w.match.players[p].base.isActive) PlayerUpdatePossessionStatistics(w, *c.sd, p);
     Team &t = TeamByID(w, teamID);

@@ -85,6 +85,7 @@ HDN void UpdateInGameCamera(World &w, const Ctx &c) {
 
 // The camera works on the unmirrored pitch, so team 1 is mirrored around its update.
 HDN void UpdateCamera(World &w, const Ctx &c) {
+    ENG_SCOPE(19);
     MatchState &m = w.match;
     if (m.autoUpdateInGameCamera) {
         MirrorMatch(w, false, true, false);

@@ -180,6 +180,7 @@ HD int HumanControlledToBallTime(const World &w, int teamID) {
     return best;
 }
 HDN bool TeamUpdateSwitch(World &w, const Ctx &c, int teamID) {
+    ENG_SCOPE(9);
     MatchState &m = w.match;
     Team &t = TeamByID(w, teamID);
     if (m.inPlay && t.gamers.count > 1) {

@@ -32,6 +32,12 @@
 #define CUJU_DATA(T, name, n) static const T name[n]
 #endif
 
+// A timing hook at the top of each stage of the tick (`ENG_SCOPE(stage number)`). It expands to
+// nothing unless a profiling build defines it before this header.
+#ifndef ENG_SCOPE
+#define ENG_SCOPE(stage)
+#endif
+
 namespace eng {
 
 // A path GRF leaves undefined. The host aborts the call with an exception; the device raises the

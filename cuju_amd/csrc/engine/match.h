@@ -9,6 +9,7 @@ namespace eng {
 
 // Slot 0 holds the newest of at most three mental images.
 HDN void PushMentalImage(World &w) {
+    ENG_SCOPE(8);
     MatchState &m = w.match;
     const int n = m.mentalImages.count < 3 ? m.mentalImages.count + 1 : 3;
     for (int i = n - 1; i > 0; i--) {
@@ -92,6 +93,7 @@ HDN bool CheckForGoal(const World &w, int side, const Vec3 &prev) {
 // False when the tick ends early: while play waits for a restart (the clock still advances), or
 // on an unsupported path, which also clears `ok`.
 HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
+    ENG_SCOPE(4);
     MatchState &m = w.match;
     ok = true;
     const bool rev = w.scenario.reverseTeamProcessing;
@@ -230,6 +232,7 @@ HDN void PlayerPreparePutBuffers(World &w, int p) {
         ps.bufferPlayerColor = ps.bufferPlayerColor * (libm::sinf(w.match.actualTimeMs * 0.02f) * 0.3f + 0.7f);
 }
 HDN void MatchPreparePutBuffers(World &w) {
+    ENG_SCOPE(20);
     const int first = w.FirstTeamID(), second = 1 - first;
     MirrorMatch(w, false, false, first == 1);
     PlayerList a = TeamActivePlayers(w, first);
@@ -240,6 +243,7 @@ HDN void MatchPreparePutBuffers(World &w) {
     MirrorMatch(w, false, false, first == 0);
 }
 HDN void MatchFetchPutBuffers(World &w, const Ctx &c) {
+    ENG_SCOPE(21);
     const int first = w.FirstTeamID();
     const Skeleton *skels[kPlayers + 3];
     Humanoid *hums[kPlayers + 3];

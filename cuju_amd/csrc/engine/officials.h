@@ -314,6 +314,7 @@ HDN bool OfficialHumanoidProcess(World &w, const Ctx &c, int official) {
     return true;
 }
 HDN bool OfficialsProcess(World &w, const Ctx &c) {
+    ENG_SCOPE(15);
     for (int o = 0; o < 3; o++)
         if (!OfficialHumanoidProcess(w, c, o)) return false;
     return true;

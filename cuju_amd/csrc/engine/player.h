@@ -349,6 +349,7 @@ HDN bool AnimationTouch(World &w, const Ctx &c, int p, const Anim &a, const Anim
 }
 
 HDN bool HumanoidProcess(World &w, const Ctx &c, int p) {
+    ENG_SCOPE(12);
     Player &ps = w.match.players[p];
     Humanoid &h = ps.base.humanoid;
     AnimationState &cur = h.anim;

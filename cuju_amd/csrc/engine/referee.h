@@ -135,6 +135,7 @@ HDN bool RefereeCheckFoul(World &w, const Ctx &c) {
 }
 
 HDN bool RefereeProcess(World &w, const Ctx &c) {
+    ENG_SCOPE(6);
     MatchState &m = w.match;
     Referee &ref = m.referee;
     RefereeBuffer &b = ref.buffer;
@@ -305,6 +306,7 @@ HD PlayerList PlayersInProcessingOrder(const World &w) {
 }
 
 HDN bool CheckBallCollisions(World &w, const Ctx &c) {
+    ENG_SCOPE(5);
     MatchState &m = w.match;
     if (m.actualTimeMs <= (uint64_t)(uint32_t)(m.lastBodyBallCollisionTimeMs + 150)) return true;
     PlayerList ps = PlayersInProcessingOrder(w);
@@ -631,6 +633,7 @@ HDN void CheckHumanoidCollision(World &w, const Ctx &c, int p1, int p2, PlayerBo
 }
 
 HDN bool CheckHumanoidCollisions(World &w, const Ctx &c) {
+    ENG_SCOPE(17);
     PlayerList ps = PlayersInProcessingOrder(w);
     PlayerBounceList bounces[kPlayers];
     for (int i = 0; i + 1 < ps.count; i++)

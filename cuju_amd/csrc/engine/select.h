@@ -297,6 +297,7 @@ HD int AllowedBodyDirectionEntry(const Vec3 &d) {
 }
 
 HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
+    ENG_SCOPE(28);
     out.count = 0;
     const Tables &T = *c.t;
     const float margin = 0.06f * PI;
@@ -985,6 +986,7 @@ struct Selector {
     }
 
     HDN void CalculatePredictedSituation(Vec3 &predPos, float &predAngle) {
+        ENG_SCOPE(22);
         AnimationState &cur = H().anim;
         const Anim &a = A(cur.anim);
         SpatialState &s = S();
@@ -1391,6 +1393,7 @@ struct Selector {
     }
 
     HDN SelectResult SelectAnimation(const PlayerCommand &cmd, int interrupt, bool preferPassAndShot) {
+        ENG_SCOPE(14);
         Player &player = P();
         Humanoid &h = H();
         AnimationState &cur = h.anim;

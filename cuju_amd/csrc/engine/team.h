@@ -72,6 +72,7 @@ HDN void TeamApplyAttackingRun(World &w, const Ctx &c, int teamID, int manualPla
 }
 
 HDN bool TeamAIProcess(World &w, const Ctx &c, int teamID) {
+    ENG_SCOPE(10);
     MatchState &m = w.match;
     Team &team = TeamByID(w, teamID);
     const Team &opp = TeamByID(w, 1 - teamID);
@@ -297,6 +298,7 @@ HDN int HungarianSolve(int *cost, int n, int *colOfRow) {
 // Assigns the outfield formation slots to the players nearest them: costs are decimeters, and
 // pairs beyond a growing cutoff cost 50000 until an assignment stays under it.
 HDN bool TeamCalculateDynamicRoles(World &w, const Ctx &c, int teamID) {
+    ENG_SCOPE(26);
     PlayerList all = TeamActivePlayers(w, teamID);
     PlayerList ps;
     if (!all.empty()) {
@@ -381,6 +383,7 @@ HDN float TeamCalculateMarkingQuality(const World &w, int teamID, int p, int o) 
 }
 // The three most dangerous opponents get the best-placed outfield marker each, in danger order.
 HDN bool TeamCalculateManMarking(World &w, const Ctx &c, int teamID) {
+    ENG_SCOPE(27);
     const int marked = 3;
     const TeamAI &ai = TeamByID(w, teamID).ai;
     PlayerList ps = TeamActivePlayers(w, teamID);
@@ -411,6 +414,7 @@ HDN bool TeamCalculateManMarking(World &w, const Ctx &c, int teamID) {
 
 // ---- the tick of a team -----------------------------------------------------------------------------
 HDN bool PlayerProcess(World &w, const Ctx &c, int p) {
+    ENG_SCOPE(11);
     MatchState &m = w.match;
     Player &ps = m.players[p];
     if (!ps.base.isActive) return true;
@@ -438,6 +442,7 @@ HDN bool PlayerProcess(World &w, const Ctx &c, int p) {
 }
 
 HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
+    ENG_SCOPE(25);
     MatchState &m = w.match;
     Team &t = TeamByID(w, teamID);
     const Team &opp = TeamByID(w, 1 - teamID);

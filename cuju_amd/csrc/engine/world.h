@@ -203,6 +203,7 @@ HD void MirrorMentalImage(World &w, int k, bool t0, bool t1, bool ball) {
 }
 
 HDN void MirrorMatch(World &w, bool t0, bool t1, bool ball) {
+    ENG_SCOPE(18);
     if (t0) MirrorTeam(w, 0);
     if (t1) MirrorTeam(w, 1);
     if (ball) {

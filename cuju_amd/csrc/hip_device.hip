@@ -43,6 +43,8 @@ __global__ void __launch_bounds__(kMaxLanes) StepKernel(eng::Batch b, const int3
     if (!eng::StepEnvironment(b, env, actions)) RecordFault(env);
 }
 
+__global__ void __launch_bounds__(1) OutputKernel(eng::Batch b, int env) { eng::WriteEnvironmentOutputs(b, env, false); }
+
 void Check(hipError_t e, const char *what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -84,6 +86,11 @@ public:
         hipLaunchKernelGGL(StepKernel, dim3(blocks), dim3(lanes_), 0, static_cast<hipStream_t>(stream), b, actions);
         Check(hipGetLastError(), "step launch");
     }
+    void Outputs(const eng::Batch &b, int env, void *stream) override {
+        if (env < 0 || env >= b.count) throw std::out_of_range("no environment " + std::to_string(env));
+        hipLaunchKernelGGL(OutputKernel, dim3(1), dim3(1), 0, static_cast<hipStream_t>(stream), b, env);
+        Check(hipGetLastError(), "output launch");
+    }
     void CheckFault() override {
         uint32_t fault = 0;
         int32_t env = 0;
@@ -109,6 +116,8 @@ private:
 namespace eng {
 namespace host {
 std::unique_ptr<Device> MakeLibraryDevice(int) { return std::make_unique<HipDevice>(); }
-extern const char *const kBackendName = "hip";
+// torch names a HIP device "cuda" on ROCm; the reference binding compares this name with the
+// device type it was asked for (python/cuju/_batch/library.py:217-222).
+extern const char *const kBackendName = "cuda";
 }  // namespace host
 }  // namespace eng

@@ -184,6 +184,33 @@ const char *cuju_environment_get_state(void *e, int index, unsigned long long *s
         return nullptr;
     }
 }
+int cuju_environment_set_state(void *e, int index, const char *bytes, unsigned long long size, const int *episode) {
+    try {
+        if (!bytes || !episode) throw std::invalid_argument("expected state bytes and the episode values");
+        Of(e)->SetState(index, std::string(bytes, size), episode[0], episode[1], episode[2], episode + 3);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+int cuju_environment_set_stack(void *e, int index, const char *name, const void *frames, unsigned long long size) {
+    try {
+        if (!frames) throw std::invalid_argument("expected frames");
+        Of(e)->SetStack(index, name ? name : "", frames, size);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+const char *cuju_environment_raw_field(void *e, int field, int *type, int *dimensions, unsigned long long *offset) {
+    // The batch emits no raw observation, so it describes no raw array.
+    (void)e;
+    (void)field;
+    (void)type;
+    (void)dimensions;
+    (void)offset;
+    return nullptr;
+}
 void *cuju_environment_buffer(void *e, const char *name) {
     void *p = Of(e)->Buffer(name ? name : "");
     if (!p) lastError = std::string("no buffer named ") + (name ? name : "(null)");

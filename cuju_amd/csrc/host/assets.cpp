@@ -377,7 +377,8 @@ StaticData ParseStatic(const std::string &b) {
     return sd;
 }
 
-// Scenario bytes without the per-episode seed and the batch-set difficulties.
+}  // namespace
+
 std::string ScenarioKey(const World &w) {
     Scenario s = w.scenario;
     s.gameEngineRandomSeed = 0;
@@ -388,7 +389,6 @@ std::string ScenarioKey(const World &w) {
     return a.bytes();
 }
 
-}  // namespace
 
 Tables AnimationTables::View() const {
     Tables t{};

@@ -70,6 +70,8 @@ struct StateCodec {
     std::string SaveFrame(World &w, int mirror, std::vector<codec::SchemaEntry> *schema = nullptr);
 };
 void ResetWorld(World &w);
+// The scenario bytes of a world without the per-episode seed and the batch-set difficulties.
+std::string ScenarioKey(const World &w);
 // Gives a rest-frame template `left` and `right` agents as GRF's reset does.
 void SetupAgents(World &w, const StaticData &sd, int left, int right, const std::string &bundle);
 

@@ -45,6 +45,7 @@ public:
     void Step(const Batch &b, const int32_t *actions, void *) override {
         ForEach(b.count, [&](int e) { return StepEnvironment(b, e, actions); });
     }
+    void Outputs(const Batch &b, int env, void *) override { WriteEnvironmentOutputs(b, env, false); }
 
 private:
     template <class F>

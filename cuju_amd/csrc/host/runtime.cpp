@@ -297,6 +297,87 @@ std::string BatchRuntime::GetState(int env, int *episode) {
     return bytes;
 }
 
+void BatchRuntime::SetState(int env, const std::string &bytes, int prevScoreDiff, int prevGameMode, int prevBallOwnedTeam,
+                            const int32_t *collected) {
+    CheckEnvironment(env);
+    dev_->Synchronize(nullptr);
+    dev_->CheckFault();
+    auto w = std::make_unique<World>();
+    StateCodec codec;
+    codec.animationCount = (int)tables_->anims.size();
+    const int bundle = slots_[env].bundle;
+    if (!codec.LoadFrame(bytes, 0, *w)) throw std::invalid_argument("expected the bytes of a state, found bytes that do not load");
+    // GRF compares scenarios without `real_time`, so the bundle's stands in for the comparison.
+    const bool realTime = w->scenario.realTime;
+    w->scenario.realTime = bundles_[bundle]->variants[0].world->scenario.realTime;
+    const std::string key = ScenarioKey(*w);
+    int index = 0;
+    while (index < 4 && bundles_[bundle]->variants[index].scenario != key) index++;
+    if (index == 4) throw std::invalid_argument("expected a state of the scenario of the environment, found another");
+    w->scenario.realTime = realTime;
+    // An environment continues a state only under the difficulties it plays.
+    const Scenario &expected = bundles_[bundle]->variants[index].world->scenario;
+    float want[2] = {expected.leftDifficulty, expected.rightDifficulty};
+    for (int side = 0; side < 2; side++)
+        if (!hostDifficulty_.empty() && hostDifficulty_[env * 2 + side] >= 0.0f) want[side] = hostDifficulty_[env * 2 + side];
+    if (memcmp(&w->scenario.leftDifficulty, &want[0], 4) != 0 || memcmp(&w->scenario.rightDifficulty, &want[1], 4) != 0)
+        throw std::invalid_argument("expected a state of the difficulties of the environment, " + std::to_string(want[0]) + " and " +
+                                    std::to_string(want[1]) + ", found " + std::to_string(w->scenario.leftDifficulty) + " and " +
+                                    std::to_string(w->scenario.rightDifficulty));
+    const int variant = bundle * 4 + index;
+    const Variant &v = VariantAt(variant);
+    const Tables hostTables = tables_->View();
+    Ctx c{};
+    c.t = &hostTables;
+    c.sd = &v.staticData;
+    c.skeletons = v.skeletons.data();
+    c.ticksPerStep = cfg_.ticksPerStep;
+    auto core = std::make_unique<EnvCore>();
+    memset(core.get(), 0, sizeof(EnvCore));
+    core->prevScoreDiff = prevScoreDiff;
+    core->prevGameMode = prevGameMode;
+    core->prevBallOwnedTeam = prevBallOwnedTeam;
+    EnvironmentGetState(*w, c, core->obs);
+    auto slot = std::make_unique<EnvSlot>();
+    dev_->ToHost(slot.get(), b_.slots + env, sizeof(EnvSlot));
+    slot->variant = variant;
+    const int agents = slot->leftAgents + slot->rightAgents;
+    for (int a = 0; a < kMaxAgents; a++) slot->collected[a] = collected && a < agents ? collected[a] : 0;
+    for (int a = 0; a < agents; a++) {
+        const bool left = a < slot->leftAgents;
+        StickyActions(*w, b_.actionSet, left, left ? a : a - slot->leftAgents, slot->sticky[a]);
+    }
+    // A sent-off keeper's replacement lives outside the state bytes, so it carries over.
+    dev_->ToHost(w->formationOverride, b_.worlds[env].formationOverride, sizeof(w->formationOverride));
+    dev_->ToDevice(b_.worlds + env, w.get(), sizeof(World));
+    dev_->ToDevice(b_.cores + env, core.get(), sizeof(EnvCore));
+    dev_->ToDevice(b_.slots + env, slot.get(), sizeof(EnvSlot));
+    dev_->Fill(b_.reward + (size_t)env * b_.agents, 0, sizeof(float) * b_.agents);
+    dev_->Fill(b_.done + env, 0, 1);
+    dev_->Fill(b_.scoreReward + env, 0, sizeof(int32_t));
+    dev_->Outputs(b_, env, nullptr);
+    dev_->Synchronize(nullptr);
+    dev_->CheckFault();
+    if (!started_[env]) {
+        started_[env] = true;
+        unstarted_--;
+    }
+}
+
+void BatchRuntime::SetStack(int env, const std::string &name, const void *frames, size_t bytes) {
+    CheckEnvironment(env);
+    if (b_.stack < 2) throw std::invalid_argument("expected a batch that stacks its observations");
+    if (name != "simple115" || !b_.simple115) throw std::invalid_argument("expected the stack simple115 of the batch, found " + name);
+    const size_t agents = (size_t)(slots_[env].leftAgents + slots_[env].rightAgents);
+    const size_t width = (size_t)kSimple115 * b_.stack;
+    const size_t expected = agents * width * sizeof(float);
+    if (bytes != expected)
+        throw std::invalid_argument("expected a stack of " + std::to_string(expected) + " bytes for the agents of environment " +
+                                    std::to_string(env) + ", found " + std::to_string(bytes));
+    dev_->Synchronize(nullptr);
+    dev_->ToDevice(b_.simple115 + (size_t)env * b_.agents * width, frames, bytes);
+}
+
 void *BatchRuntime::Buffer(const std::string &name) {
     if (name == "simple115") return b_.simple115;
     if (name == "final_simple115") return b_.finalSimple115;

@@ -33,6 +33,8 @@ public:
     // device memory.
     virtual void Reset(const Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *stream) = 0;
     virtual void Step(const Batch &b, const int32_t *actions, void *stream) = 0;
+    // Writes the outputs of environment `env` after a reset or a loaded state.
+    virtual void Outputs(const Batch &b, int env, void *stream) = 0;
     // Throws when a launch since the last check reached an undefined path.
     virtual void CheckFault() = 0;
     virtual int Threads() const { return 0; }
@@ -85,6 +87,13 @@ public:
     // The engine bytes of one environment; `episode` gets the score difference, game mode and
     // ball-owning team after the last step, then each agent's checkpoints.
     std::string GetState(int env, int *episode);
+    // Loads engine bytes of GRF's state into environment `env` and writes its outputs; the reward
+    // is 0 and done clear until the next step. `collected` may be null.
+    void SetState(int env, const std::string &bytes, int prevScoreDiff, int prevGameMode, int prevBallOwnedTeam,
+                  const int32_t *collected);
+    // Writes the observation stack of environment `env`: `[agents][115 * stack]` floats, oldest
+    // frame first.
+    void SetStack(int env, const std::string &name, const void *frames, size_t bytes);
     // The buffer of an output name, or null.
     void *Buffer(const std::string &name);
 

@@ -10,7 +10,9 @@ clones what it keeps.
 from __future__ import annotations
 
 import ctypes
+import io
 import os
+import pickle
 import re
 import struct
 from typing import Any
@@ -20,7 +22,7 @@ import torch
 
 from . import library as _library
 from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, ConfigurationError,
-                     EnvironmentIndexError, MissingFileError, from_library)
+                     EnvironmentIndexError, MissingFileError, StateError, from_library)
 
 REPRESENTATIONS = {'simple115': 1, 'simple115v2': 2}
 ACTION_SETS = {'default': 0, 'v2': 1, 'full': 2}
@@ -72,6 +74,21 @@ def episode_pickle(episode, collected=None) -> bytes:
                  + b''.join(_pickle_int(a) + _pickle_int(c) for a, c in enumerate(collected) if c)
                  + b'u')
     return data + b'u.'
+
+
+class _EpisodeLogic:
+    """Stands in for GRF's `EnvState` while the pickle of a state loads."""
+
+
+class _StateUnpickler(pickle.Unpickler):
+    """Loads the pickle of a state, resolving GRF's episode-logic class to a plain stand-in and
+    refusing every other global, so that loading constructs nothing else
+    (python/cuju/_batch/state.py:20-32)."""
+
+    def find_class(self, module, name):
+        if (module, name) == ('gfootball.env.football_env_core', 'EnvState'):
+            return _EpisodeLogic
+        raise pickle.UnpicklingError(f'expected only the episode logic, found `{module}.{name}`')
 
 
 class _DeviceArray:
@@ -130,7 +147,7 @@ class BatchEnvironment:
         if self._torch_device.index is None:
             self._torch_device = torch.device('cuda', torch.cuda.current_device())
         lib = _library.load(library)
-        if lib.cuju_backend().decode() != 'hip':
+        if lib.cuju_backend().decode() != 'cuda':
             raise ConfigurationError('expected the HIP library')
         names = [assets] if isinstance(assets, str) else list(assets)
         resolved = [resolve_assets(n) for n in names]
@@ -330,6 +347,40 @@ class BatchEnvironment:
         collected = list(episode)[3:3 + self.agents] if self.checkpoints else None
         data = episode_pickle(list(episode)[:3], collected)
         return struct.pack('<i', len(data)) + data + match
+
+    def set_state(self, index: int, state: bytes, stacked: bool = False) -> None:
+        """Sets environment `index` to a state that `get_state` returned; its observation and sticky
+        actions follow from the state, the reward is 0 and done clear until the next step
+        (python/cuju/_batch/environment.py:1540-1620). States that carry GRF's frame stack are not
+        read."""
+        if not 0 <= index < self.environment_count:
+            raise EnvironmentIndexError(f'expected an environment from 0 to {self.environment_count - 1}, found {index}')
+        if stacked:
+            raise StateError('this build reads states without a frame stack only')
+        if len(state) < 4 or not 0 < struct.unpack_from('<i', state)[0] <= len(state) - 4:
+            raise StateError(f'expected the bytes of a state: a pickle length, the pickle and the match, '
+                             f'found {len(state)} bytes that hold none')
+        (length,) = struct.unpack_from('<i', state)
+        try:
+            unpickled = _StateUnpickler(io.BytesIO(state[4:4 + length])).load()
+            logic = unpickled['FootballEnvCore'].__dict__
+            episode = (ctypes.c_int * (3 + MAXIMUM_AGENTS))(
+                logic['previous_score_diff'], logic['previous_game_mode'], logic['prev_ball_owned_team'])
+        except (pickle.UnpicklingError, KeyError, AttributeError, EOFError, TypeError) as error:
+            raise StateError(f'expected the pickle of the episode logic in the state, found {error}') from error
+        if self.checkpoints and 'CheckpointRewardWrapper' not in unpickled:
+            raise StateError('expected the checkpoints of the checkpoint reward in the state')
+        for agent, count in unpickled.get('CheckpointRewardWrapper', {}).items():
+            episode[3 + agent] = count
+        match = state[4 + length:]
+        with torch.cuda.device(self._torch_device):
+            torch.cuda.current_stream(self._torch_device).synchronize()
+            status = self._lib.cuju_environment_set_state(self._handle(), index, match, len(match), episode)
+        if status != 0:
+            message = self._lib.cuju_last_error().decode()
+            if message.startswith('expected'):
+                raise StateError(message)
+            raise from_library(message)
 
     def memory_bytes(self) -> int:
         return int(self._lib.cuju_environment_memory_bytes(self._handle()))

@@ -74,6 +74,9 @@ SIGNATURES = [
     ('cuju_environment_step_wait', I, [P]),
     ('cuju_environment_synchronize', I, [P, P]),
     ('cuju_environment_get_state', P, [P, I, ctypes.POINTER(U64), P]),
+    ('cuju_environment_set_state', I, [P, I, ctypes.c_char_p, U64, P]),
+    ('cuju_environment_set_stack', I, [P, I, ctypes.c_char_p, P, U64]),
+    ('cuju_environment_raw_field', ctypes.c_char_p, [P, I, P, P, P]),
     ('cuju_environment_buffer', P, [P, ctypes.c_char_p]),
 ]
 

@@ -51,7 +51,7 @@ struct cuju_configuration {
 
 /* src/environment_api.h:41 */
 const char *cuju_last_error(void);
-/* src/environment_api.h:44; "hip" for this library */
+/* src/environment_api.h:44; "cuda", the torch device type of a HIP device on ROCm */
 const char *cuju_backend(void);
 /* src/environment_api.h:98 */
 void *cuju_environment_create(const struct cuju_configuration *settings);
@@ -92,6 +92,12 @@ int cuju_environment_step_wait(void *environment);
 int cuju_environment_synchronize(void *environment, void *stream);
 /* src/environment_api.h:367 */
 const char *cuju_environment_get_state(void *environment, int index, unsigned long long *size, int *episode);
+/* src/environment_api.h:392; `bytes` are engine bytes of get_state, `episode` as get_state writes it */
+int cuju_environment_set_state(void *environment, int index, const char *bytes, unsigned long long size, const int *episode);
+/* src/environment_api.h:410; simple115 only: [agents][115 * stack] float32, oldest frame first */
+int cuju_environment_set_stack(void *environment, int index, const char *name, const void *frames, unsigned long long size);
+/* src/environment_api.h:449; null: the batch emits no raw observation */
+const char *cuju_environment_raw_field(void *environment, int field, int *type, int *dimensions, unsigned long long *offset);
 /* src/environment_api.h:430; simple115, final_simple115, reward, done, score_reward */
 void *cuju_environment_buffer(void *environment, const char *name);
 

@@ -102,6 +102,8 @@ def library(path=None):
         lib.cuju_environment_buffer.restype = ctypes.c_void_p
         lib.cuju_environment_buffer.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
         lib.cuju_environment_set_difficulty.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        lib.cuju_environment_set_state.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p,
+                                                   ctypes.c_ulonglong, ctypes.c_void_p]
         _libraries[path] = lib
     return _libraries[path]
 
@@ -255,6 +257,12 @@ class ReferenceBatch:
         if not pointer:
             raise RuntimeError(self._lib.cuju_last_error().decode())
         return ctypes.string_at(pointer, size.value), list(episode)
+
+    def set_raw_state(self, index, match, episode):
+        """`cuju_environment_set_state` (`src/environment_api.h:392-404`) with engine bytes and
+        the episode words `raw_state` returned."""
+        words = (ctypes.c_int * (3 + MAXIMUM_AGENTS))(*episode[:3 + MAXIMUM_AGENTS])
+        self._check(self._lib.cuju_environment_set_state(self._handle, index, match, len(match), words))
 
     def get_state(self, index):
         """`BatchEnvironment.get_state` bytes: pickle length, pickle, then the match bytes."""

@@ -31,7 +31,7 @@ def test_product_library_exports_every_declared_symbol():
     missing = [n for n in declared() if not hasattr(lib, n)]
     assert not missing
     lib.cuju_backend.restype = ctypes.c_char_p
-    assert lib.cuju_backend() == b'hip'
+    assert lib.cuju_backend() == b'cuda'
 
 
 def test_package_binds_the_declared_symbols():

@@ -81,3 +81,41 @@ def test_gpu_masked_reset_and_episode_end(reference_library):
     finally:
         mine.close()
         theirs.close()
+
+
+def test_gpu_set_state_continues_as_the_reference(reference_library):
+    """States of a reference batch (with checkpoint counts) load into the HIP batch through
+    `set_state`, shuffled across environments; the outputs right after and every later step and
+    state match the reference given the same states."""
+    assets, environments, played, after = '11_vs_11_hard_stochastic_l11_r0', 4, 30, 15
+    options = dict(environment_count=environments, rewards='scoring,checkpoints')
+    source = ref.ReferenceBatch(assets, seed=7, threads=0, library_path=reference_library, **options)
+    source.reset()
+    for step in range(played):
+        source.step(digest_actions(step, environments, source.agents, source.action_count))
+    states = [source.get_state(i) for i in range(environments)]
+    raw = [source.raw_state(i) for i in range(environments)]
+    source.close()
+    mine = gpu_batch(assets, seed=11, **options)
+    theirs = ref.ReferenceBatch(assets, seed=11, threads=0, library_path=reference_library, **options)
+    try:
+        mine.reset()
+        theirs.reset()
+        for index in range(environments):
+            mine.set_state(index, states[(index + 1) % environments])
+            match, episode = raw[(index + 1) % environments]
+            theirs.set_raw_state(index, match, episode)
+        assert host(mine.observation()).tobytes() == theirs.observation().tobytes()
+        for index in range(environments):
+            assert mine.get_state(index) == states[(index + 1) % environments]
+        for step in range(after):
+            actions = digest_actions(step + 5, environments, theirs.agents, theirs.action_count)
+            a = mine.step(torch.as_tensor(actions, device='cuda:0'))
+            b = theirs.step(actions)
+            for x, y in zip(a[:3], b):
+                assert host(x).astype(y.dtype).tobytes() == y.tobytes(), f'step {step}'
+        for index in range(environments):
+            assert mine.get_state(index) == theirs.get_state(index)
+    finally:
+        mine.close()
+        theirs.close()

@@ -10,6 +10,7 @@ import pytest
 
 from conftest import digest_actions, play, short_cases
 from oracle import ref
+from oracle.ref import ReferenceBatch
 
 
 @pytest.mark.parametrize('name,case', short_cases(), ids=[n for n, _ in short_cases()])
@@ -76,3 +77,51 @@ def test_episode_seeds_follow_cpython_random(host_library):
         lib.cuju_debug_episode_seeds(seed, index, 8, out.ctypes.data)
         rng = random.Random(seed * 2**32 + index)
         assert out.tolist() == [rng.randint(0, 2000000000) for _ in range(8)]
+
+
+@pytest.mark.parametrize('assets', ['11_vs_11_hard_stochastic_l11_r0', 'academy_corner_l1_r0'])
+def test_set_state_continues_as_the_reference(assets, reference_library, host_library):
+    """States of a played batch load into another batch (environments shuffled) in the reference
+    and in the engine; both then agree byte for byte on the outputs and on every later state
+    (reference `cuju_environment_set_state`, src/environment_api.h:390-404)."""
+    environments, played, after = 3, 25, 12
+    source = ReferenceBatch(assets, environment_count=environments, seed=7, library_path=reference_library)
+    source.reset()
+    for step in range(played):
+        source.step(digest_actions(step, environments, source.agents, source.action_count))
+    states = [source.raw_state(i) for i in range(environments)]
+    source.close()
+    targets = [ReferenceBatch(assets, environment_count=environments, seed=11, library_path=path)
+               for path in (reference_library, host_library)]
+    for batch in targets:
+        batch.reset()
+        for index in range(environments):
+            match, episode = states[(index + 1) % environments]
+            batch.set_raw_state(index, match, episode)
+    reference, engine = targets
+    assert np.array_equal(reference.observation(), engine.observation())
+    for index in range(environments):
+        assert engine.raw_state(index) == reference.raw_state(index)
+        assert engine.raw_state(index)[0] == states[(index + 1) % environments][0]
+    for step in range(after):
+        actions = digest_actions(step + 3, environments, reference.agents, reference.action_count)
+        for a, b in zip(reference.step(actions), engine.step(actions)):
+            assert np.array_equal(a, b)
+    for index in range(environments):
+        assert engine.get_state(index) == reference.get_state(index)
+    for batch in targets:
+        batch.close()
+
+
+def test_set_state_refuses_another_scenario(reference_library, host_library):
+    source = ReferenceBatch('academy_corner_l1_r0', environment_count=1, seed=7, library_path=host_library)
+    source.reset()
+    match, episode = source.raw_state(0)
+    source.close()
+    target = ReferenceBatch('academy_empty_goal_l1_r0', environment_count=1, seed=7, library_path=host_library)
+    target.reset()
+    with pytest.raises(RuntimeError, match='scenario'):
+        target.set_raw_state(0, match, episode)
+    with pytest.raises(RuntimeError, match='do not load'):
+        target.set_raw_state(0, b'\x00' * 16, episode)
+    target.close()

@@ -16,6 +16,7 @@ struct BallSpatial {
 // Entry k of `predictions` is the position after 10k ms. When the first step lands where the last
 // tick predicted, the predictions shift down one entry instead, at most `validPredictions` times.
 HDN BallSpatial BallCalculatePrediction(Ball &ball, bool ballIsInGoal) {
+    ENG_SCOPE(37);
     const float bounce = 0.62f, linearBounce = 0.06f, drag = 0.015f, friction = 0.04f,
                 linearFriction = 1.6f, gravity = -9.81f, grassHeight = 0.025f, dt = 0.01f;
     BallSpatial out;
@@ -227,6 +228,7 @@ HD uint32_t DirectTimeMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &target, f
 // Velocities in m/s; `maxTime` is UINT32_MAX for no limit.
 HDN TimeNeeded GetTimeNeededMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &target, float maxVel,
                                bool precise, uint32_t maxTime) {
+    ENG_SCOPE(36);
     TimeNeeded r;
     if ((pos - target).Length() > (precise ? 48.0f : 16.0f)) {
         r.usual = DirectTimeMs(pos, mov, target, maxVel);
@@ -300,6 +302,7 @@ HD Vec3 PredFlip(const Vec3 *pred, bool flip, int ms) {
 
 HDN ScanResult PossessionScan(const Vec3 *pred, bool flip, const Vec3 &pos, const Vec3 &mov, float maxVel,
                               bool precise, uint32_t start) {
+    ENG_SCOPE(35);
     ScanResult s;
     {
         uint32_t latest = kBallPredictionSpanMs;

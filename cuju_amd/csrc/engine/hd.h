@@ -66,6 +66,18 @@ HD double DoubleOf(uint64_t b) {
     return v;
 }
 
+// Whether `x` holds in any lane of the wavefront that executes the call (the lanes of a wavefront
+// run different matches). The host runs one match at a time, so there it is `x`. Being a
+// wavefront-wide operation, a call is a point where those lanes meet: none passes it before all
+// have reached it.
+HD bool AnyLane(bool x) {
+#if ENG_DEVICE
+    return __builtin_amdgcn_ballot_w64(x) != 0;
+#else
+    return x;
+#endif
+}
+
 // x86-64 float-to-integer conversions (cvttss2si / cvttsd2si), which GRF's build performs. NaN and
 // out-of-range inputs give the "integer indefinite" value where a GPU conversion would saturate.
 HD int32_t TruncToInt32(float v) {

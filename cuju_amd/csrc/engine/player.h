@@ -348,13 +348,16 @@ HDN bool AnimationTouch(World &w, const Ctx &c, int p, const Anim &a, const Anim
     return true;
 }
 
-HDN bool HumanoidProcess(World &w, const Ctx &c, int p) {
+// A humanoid's tick (humanoid_process.h:89-681) in three parts: the frame advance that decides
+// whether the animation is interrupted, the interruption (command request and animation
+// selection, the expensive part), and the rest. Run in that order they are the whole tick; the
+// team loop lets the matches of a wavefront meet at the interruption.
+HDN void HumanoidProcessBegin(World &w, const Ctx &c, int p) {
     ENG_SCOPE(12);
     Player &ps = w.match.players[p];
     Humanoid &h = ps.base.humanoid;
     AnimationState &cur = h.anim;
     const int t = w.playerTeamID[p];
-    const Ball &ball = w.match.ball;
     const int k = MentalImageIndex(w, h.mentalImageTime);
     h.decayingPositionOffset *= 0.95f;
     if ((double)h.decayingPositionOffset.Length() < 0.005) h.decayingPositionOffset = Vec3(0);
@@ -369,7 +372,12 @@ HDN bool HumanoidProcess(World &w, const Ctx &c, int p) {
         if (cur.frameNum == a.frameCount - 1 && h.interruptAnim == kIntNone) h.interruptAnim = kIntSwitch;
         if (h.interruptAnim == kIntNone && MayRequeue(w, c, p, a, k)) h.interruptAnim = kIntReQueue;
     }
-    if (h.interruptAnim != kIntNone) {
+}
+HDN bool HumanoidProcessInterrupt(World &w, const Ctx &c, int p) {
+    Humanoid &h = w.match.players[p].base.humanoid;
+    AnimationState &cur = h.anim;
+    {
+        ENG_SCOPE(30);
         CommandQueue q;
         if (h.interruptAnim == kIntTrip && h.tripType != 0) {
             AddTripCommandToQueue(h, q, h.tripType);
@@ -415,6 +423,14 @@ HDN bool HumanoidProcess(World &w, const Ctx &c, int p) {
             if (h.interruptAnim == kIntReQueue && h.prevAnimFunctionType == fn) h.requeueDelayFrames = 22;
         }
     }
+    return true;
+}
+HDN bool HumanoidProcessEnd(World &w, const Ctx &c, int p) {
+    Player &ps = w.match.players[p];
+    Humanoid &h = ps.base.humanoid;
+    AnimationState &cur = h.anim;
+    const int t = w.playerTeamID[p];
+    const Ball &ball = w.match.ball;
     h.requeueDelayFrames = h.requeueDelayFrames - 1 > 0 ? h.requeueDelayFrames - 1 : 0;
     h.interruptAnim = kIntNone;
     const Anim &a = c.A(cur.anim);

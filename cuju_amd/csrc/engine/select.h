@@ -174,6 +174,7 @@ HD Vec3 GetFrontOfFootOffsetRelative(float velocity, float bodyAngleRel, float h
 // them orders as on the original type). Any stable sort of a strict weak order without NaN gives
 // GRF's std::stable_sort order.
 HDN void StableSortByKeys(const Ctx &c, AList &list) {
+    ENG_SCOPE(33);
     const int n = list.count;
     double *keys = c.ws->keys;
     int16_t *a = c.ws->order[0], *b = c.ws->order[1];
@@ -642,6 +643,7 @@ struct Selector {
     // The first element after a chain of stable sorts: the smallest key tuple, the earliest on ties.
     template <class KeysFn>
     HD int FirstOfSortChain(const AList &l, int keyCount, KeysFn keys) {
+        ENG_SCOPE(34);
         if (l.count < 2) return l[0];
         int best = -1;
         double bk[kMaxChainKeys];
@@ -675,6 +677,7 @@ struct Selector {
 
     HDN void KeepBestDirectionAnimations(AList &l, const PlayerCommand &cmd, bool strict, float allowedAngle = 0,
                                          int allowedVelocitySteps = 0, int forcedQuadrant = -1) {
+        ENG_SCOPE(32);
         int bestQ = forcedQuadrant;
         if (bestQ == -1) {
             Sort(l, [&](int i) { return MovementSimilarityKey(i); });
@@ -703,6 +706,7 @@ struct Selector {
     }
 
     HDN void KeepBestBodyDirectionAnimations(AList &l, const PlayerCommand &cmd, bool strict, float allowedAngle = 0) {
+        ENG_SCOPE(32);
         Vec3 relLookAt;
         if (l.count > 1) relLookAt = RelativeLookAt();
         Sort(l, [&](int i) { return DirectionSimilarityRating(A(i), pred, relLookAt); });
@@ -749,6 +753,7 @@ struct Selector {
 
     HDN Vec3 CalculatePhysicsVector(int ai, bool useDesiredMovement, const Vec3 &desiredMovement, bool useDesiredBody,
                                     const Vec3 &desiredBodyRel, PList &out, float &rotationOffset) {
+        ENG_SCOPE(38);
         (void)useDesiredBody;
         const Anim &a = A(ai);
         const AnimDerived &d = D(ai);
@@ -1109,6 +1114,7 @@ struct Selector {
                                         bool useDesiredBody, const Vec3 &desiredBodyRel, PList &positions, int &touchFrameOut,
                                         Vec3 &touchPosOut, Vec3 &actionSmuggleOut, float &rotationSmuggleOut,
                                         bool preferPassAndShot = false) {
+        ENG_SCOPE(31);
         const MatchState &m = w.match;
         SpatialState &s = S();
         const float angle = s.angle.value();

@@ -413,11 +413,12 @@ HDN bool TeamCalculateManMarking(World &w, const Ctx &c, int teamID) {
 }
 
 // ---- the tick of a team -----------------------------------------------------------------------------
-HDN bool PlayerProcess(World &w, const Ctx &c, int p) {
+// A player's tick (team_process.h, PlayerProcess) around its humanoid's: the part before the
+// humanoid's interruption, which returns the position the fatigue measures from, and the part after.
+HDN bool PlayerProcessBegin(World &w, const Ctx &c, int p, Vec3 &before) {
     ENG_SCOPE(11);
     MatchState &m = w.match;
     Player &ps = m.players[p];
-    if (!ps.base.isActive) return true;
     ps.desiredTimeToBallMs = (ps.desiredTimeToBallMs - 10 < 0) ? 0 : ps.desiredTimeToBallMs - 10;
     if (ExternalControllerActive(w, p) && !HumanControllerProcess(w, c, p)) return false;
     ElizaControllerProcess(w, c, p);
@@ -427,8 +428,14 @@ HDN bool PlayerProcess(World &w, const Ctx &c, int p) {
         else ps.possessionDurationMs = 0;
         if ((m.actualTimeMs + (uint64_t)(c.sd->stableID[p] * 10)) % 100 == 0) CalculateTacticalSituation(w, p);
     }
-    Vec3 before = ps.base.humanoid.spatial.position;
-    if (!HumanoidProcess(w, c, p)) return false;
+    before = ps.base.humanoid.spatial.position;
+    HumanoidProcessBegin(w, c, p);
+    return true;
+}
+HDN bool PlayerProcessEnd(World &w, const Ctx &c, int p, const Vec3 &before) {
+    MatchState &m = w.match;
+    Player &ps = m.players[p];
+    if (!HumanoidProcessEnd(w, c, p)) return false;
     if (m.inPlay) {
         float d = (ps.base.humanoid.spatial.position - before).Length();
         // GRF: the raw statistic, without the difficulty and fatigue scaling.
@@ -462,8 +469,32 @@ HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
         if ((m.actualTimeMs + off) % 400 == 0 && !TeamCalculateDynamicRoles(w, c, teamID)) return false;
         if ((m.actualTimeMs + off + 100) % 400 == 0 && !TeamCalculateManMarking(w, c, teamID)) return false;
     }
-    for (int p = 0; p < m.playerCount; p++)
-        if (w.playerTeamID[p] == teamID && m.players[p].base.isActive && !PlayerProcess(w, c, p)) return false;
+    // The active players of the team in state order, each checked when its turn comes. A match
+    // whose next humanoid needs a new animation stops there until every match of the wavefront has
+    // stopped or finished, so that the interruptions run together; each match still processes
+    // its players in order.
+    auto next = [&](int from) {
+        while (from < m.playerCount && !(w.playerTeamID[from] == teamID && m.players[from].base.isActive)) from++;
+        return from;
+    };
+    int p = next(0);
+    bool interrupted = false;
+    Vec3 before;
+    for (;;) {
+        while (!interrupted && p < m.playerCount) {
+            if (!PlayerProcessBegin(w, c, p, before)) return false;
+            interrupted = Hum(w, p).interruptAnim != kIntNone;
+            if (interrupted) break;
+            if (!PlayerProcessEnd(w, c, p, before)) return false;
+            p = next(p + 1);
+        }
+        if (!AnyLane(interrupted)) break;
+        if (interrupted) {
+            if (!HumanoidProcessInterrupt(w, c, p) || !PlayerProcessEnd(w, c, p, before)) return false;
+            interrupted = false;
+            p = next(p + 1);
+        }
+    }
     if (m.inPlay) {
         for (int g = 0; g < t.gamers.count; g++) {
             HumanGamer &gm = t.gamers[g];

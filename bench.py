@@ -80,12 +80,12 @@ def main():
     parser.add_argument('--cpu-environments', type=int, default=4096)
     parser.add_argument('--cpu-steps', type=int, default=60)
     parser.add_argument('--no-cpu', action='store_true')
-    parser.add_argument('--lanes', type=int, default=None, help='environments per workgroup, 1 to 64')
+    parser.add_argument('--matches', type=int, default=None, help='environments per workgroup (one wavefront)')
     parser.add_argument('--copy-probe', action='store_true',
                         help='also run a 1 GiB device-to-device copy, the calibration of HBM byte counters')
     args = parser.parse_args()
-    if args.lanes is not None:
-        os.environ['CUJU_AMD_LANES'] = str(args.lanes)
+    if args.matches is not None:
+        os.environ['CUJU_AMD_MATCHES'] = str(args.matches)
     if args.gpus != 1:
         print(f'bench.py measures one GPU: every GPU box here has one, and the engine has no multi-GPU path '
               f'(environments shard by first_index with no exchange); asked for --gpus {args.gpus}.', file=sys.stderr)

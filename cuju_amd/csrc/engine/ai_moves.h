@@ -231,6 +231,7 @@ struct AIBase {
 
     // ---- movement towards the ball ----
     HDN unsigned BallControlMovement(float desiredVel, Vec3 &bestDir, float &bestVel, Vec3 &bestLookAt) const {
+        ENG_SCOPE(47);
         const unsigned desiredMs = 250 + kDefaultTouchOffsetMs;
         Vec3 toBall = MentalBall((int)desiredMs).Get2D() - Pos();
         float dist = toBall.Length();
@@ -256,6 +257,7 @@ struct AIBase {
     // earliest reachable one, with haste).
     HDN unsigned ToBallMovement(const Vec3 &desiredDir, float desiredVel, Vec3 &bestDir, float &bestVel, Vec3 &bestLookAt,
                                 float haste) const {
+        ENG_SCOPE(39);
         const Vec3 pp = Pos();
         const float maxVel = GetMaximumVelocity(*c.sd, p);
         float movementW = 1.0f, timeW = 0.0f, perpW = 0.1f, prevW = 0.0f;
@@ -354,6 +356,7 @@ struct AIBase {
     }
 
     HDN void MovementCommand(bool forceMagnet, bool extraHaste) {
+        ENG_SCOPE(40);
         const int lookMs = 40;
         Vec3 qin = ctl.inputDirection;
         QuantizeDirection(qin, kQuantizedDirectionBias);
@@ -476,6 +479,7 @@ struct AIBase {
     }
 
     HDN Vec3 GetSupportPositionForceField(const Vec3 &base, bool makeRun) const {
+        ENG_SCOPE(41);
         const int designated = Own().designatedTeamPossessionPlayer;
         Vec3 cur = Pos() + Mov() * 0.1f;
         Vec3 mainMan = Pos(designated) + Mov(designated) * 0.1f;
@@ -603,6 +607,7 @@ struct AIBase {
         return Clamp(d - threshold * NormalizedClamp(d, 0.0f, threshold * 2.0f), 0.0f, kPitchHalfLength);
     }
     HDN void GoalieRequestInput(Vec3 &dir, float &vel) {
+        ENG_SCOPE(46);
         const float lineDistance = 10.0f;
         Vec3 bp = MentalBall(TruncToInt32(600 + (float)ps.timeToBallMs * 0.2f)).Get2D();
         Vec3 target = Vec3((kPitchHalfLength - lineDistance) * side, 0, 0);
@@ -695,6 +700,7 @@ struct AIBase {
 
     // ---- passes ----
     HDN float PassingOdds(const Vec3 &target, int passType, const ImageList &opps, float ballVelMul = 1.0f) const {
+        ENG_SCOPE(42);
         const float secondScale = 1.0f;
         Vec3 origin = Pos() + Mov() * 0.12f;
         Line line(origin, target);
@@ -760,6 +766,7 @@ struct AIBase {
         }
     }
     HDN void BestDribbleMovement(Vec3 &desiredDir, float &desiredVel) const {
+        ENG_SCOPE(43);
         Vec3 mp = Pos(), mm = Mov();
         float offense = 0.7f + kDribbleOffensiveness * 0.05f + GetMindSet(DynamicRole()) * 0.05f;
         const float powerMul = 1.0f, futureS = 0.25f;

@@ -20,6 +20,7 @@ struct AIController : AIBase {
     // Pass to the best-placed team mate, a panic clearance near the own goal, a shot when placed
     // for one, and a dribble direction from a force field.
     HDN void GetOnTheBallCommands(Vec3 &rawDir, float &rawVel) {
+        ENG_SCOPE(44);
         float movDiff = NormalizedClamp((m.ball.momentum - Mov()).Length(), 0.0f, 10.0f);
         float oneTouchIsHard = movDiff - Stat(kStatShortPass) * movDiff * 0.8f;
         ImageList opps;
@@ -404,6 +405,7 @@ HD void TeamApplyKeeperRush(World &w, int teamID) { TeamByID(w, teamID).ai.endAp
 // The commands of a gamer's player: the armed action, then ball control, trap, interference and a
 // movement that follows the stick (steady direction) with the default gameplay settings.
 HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
+    ENG_SCOPE(45);
     HumanControllerState &hc = HumanGamerOf(w, p).controller;
     PlayerControllerState &ctl = hc.base;
     AIController ai(w, c, p, q, ctl, nullptr);

@@ -391,7 +391,9 @@ HDN void ApplyNode(const Ctx &c, const Anim &a, const Skeleton &sk, Humanoid &h,
 
 // Applies every humanoid's buffered frame; humanoids are independent.
 HDN void FetchPutBuffers(const Ctx &c, const Skeleton *const *skels, Humanoid *const *hums, int count) {
-    for (int k = 0; k < count; k++) {
+    // A humanoid's pose reads and writes only its own state, so the lanes of the match take the
+    // humanoids in turn.
+    for (int k = GroupRank(); k < count; k += kGroupLanes) {
         Humanoid &h = *hums[k];
         AnimApplyBuffer &buf = h.applyBuf;
         const Anim &a = c.A(buf.anim);
@@ -401,6 +403,7 @@ HDN void FetchPutBuffers(const Ctx &c, const Skeleton *const *skels, Humanoid *c
             ApplyNode(c, a, *skels[k], h, n, buf.frameNum, buf.smooth, buf.smoothFactor, buf.position,
                       buf.orientation.value(), buf.offsets, 10, buf.noPos, plan);
     }
+    GroupSync();
 }
 
 // ---- spatial state --------------------------------------------------------------------------------

@@ -403,8 +403,13 @@ HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p)
 
 HDN void TeamUpdatePossessionStatistics(World &w, const Ctx &c, int teamID) {
     ENG_SCOPE(16);
+    // A player's statistics read only the ball, the opposing team and its own fields, so the lanes
+    // of the match take the players in turn.
+    int players[kPlayers], n = 0;
     for (int p = 0; p < w.match.playerCount; p++)
-        if (w.playerTeamID[p] == teamID && w.match.players[p].base.isActive) PlayerUpdatePossessionStatistics(w, *c.sd, p);
+        if (w.playerTeamID[p] == teamID && w.match.players[p].base.isActive) players[n++] = p;
+    for (int i = GroupRank(); i < n; i += kGroupLanes) PlayerUpdatePossessionStatistics(w, *c.sd, players[i]);
+    GroupSync();
     Team &t = TeamByID(w, teamID);
     t.hasPossession = false;
     t.timeToBallMs = 100000;

@@ -78,6 +78,89 @@ HD bool AnyLane(bool x) {
 #endif
 }
 
+// ---- the lanes of one match ------------------------------------------------------------------------
+// On the device a match runs on a group of kGroupLanes adjacent lanes of a wavefront. Every lane
+// of the group runs the match's sequential code with the same data, so the group never diverges
+// there and its loads and stores of one address merge. Loops whose iterations are independent split
+// their iterations over the group ("rank" = the lane's place in it) and combine the results in
+// iteration order, so a match computes exactly what one lane alone would. The host runs a match
+// on one lane.
+#ifndef ENG_GROUP_LANES
+#define ENG_GROUP_LANES 4
+#endif
+#if ENG_DEVICE
+constexpr int kGroupLanes = ENG_GROUP_LANES;
+static_assert(kGroupLanes == 1 || kGroupLanes == 2 || kGroupLanes == 4 || kGroupLanes == 8 || kGroupLanes == 16,
+              "a group is a power of two of lanes within a wavefront");
+#else
+constexpr int kGroupLanes = 1;
+#endif
+// Groups never exceed this, which sizes per-lane working memory.
+constexpr int kMaxGroupLanes = 16;
+
+HD int LaneId() {
+#if ENG_DEVICE
+    return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+#else
+    return 0;
+#endif
+}
+HD int GroupRank() { return LaneId() & (kGroupLanes - 1); }
+// Bit r: `x` in the group's lane of rank r. Every lane of the group must make the call.
+HD uint32_t GroupBallot(bool x) {
+#if ENG_DEVICE
+    const uint64_t all = __builtin_amdgcn_ballot_w64(x);
+    return (uint32_t)(all >> (LaneId() & ~(kGroupLanes - 1))) & ((1u << kGroupLanes) - 1u);
+#else
+    return x ? 1u : 0u;
+#endif
+}
+HD int PopCount(uint32_t x) {
+#if ENG_DEVICE
+    return __builtin_popcount(x);
+#else
+    int n = 0;
+    for (; x; x &= x - 1) n++;
+    return n;
+#endif
+}
+HD int LowestBit(uint32_t x) {
+    int i = 0;
+    while (!(x & 1u)) {
+        x >>= 1;
+        i++;
+    }
+    return i;
+}
+// The value of the group's lane of rank `rank`. Every lane of the group must make the call.
+HD uint32_t GroupShuffle(uint32_t v, int rank) {
+#if ENG_DEVICE
+    const int src = (LaneId() & ~(kGroupLanes - 1)) + rank;
+    return (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)v);
+#else
+    (void)rank;
+    return v;
+#endif
+}
+HD int32_t GroupShuffle(int32_t v, int rank) { return (int32_t)GroupShuffle((uint32_t)v, rank); }
+HD bool GroupShuffle(bool v, int rank) { return GroupShuffle((uint32_t)v, rank) != 0; }
+HD float GroupShuffle(float v, int rank) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    b = GroupShuffle(b, rank);
+    float r;
+    memcpy(&r, &b, 4);
+    return r;
+}
+// Orders the group's memory operations: what a lane stored before the call is what every lane of
+// the group loads after it (one wavefront's memory operations complete in order).
+HD void GroupSync() {
+#if ENG_DEVICE
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#endif
+}
+
 // x86-64 float-to-integer conversions (cvttss2si / cvttsd2si), which GRF's build performs. NaN and
 // out-of-range inputs give the "integer indefinite" value where a GPU conversion would saturate.
 HD int32_t TruncToInt32(float v) {

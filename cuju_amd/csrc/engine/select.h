@@ -331,22 +331,24 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
     const Vec3 qOut2D = q.outgoingBallDirection.Get2D();
     const bool qOutNull = fabsf(qOut2D.v[0]) < 0.000001f && fabsf(qOut2D.v[1]) < 0.000001f && fabsf(qOut2D.v[2]) < 0.000001f;
     const Vec3 qOutNormalized = qOutNull ? Vec3(0) : qOut2D.Normalized(Vec3(0));
-    for (int k = 0; k < n; k++) {
+    // Each animation passes or fails on its own, so the lanes of the match test consecutive ones
+    // and append the passing ones in list order.
+    auto accepts = [&](int k) -> bool {
         const int ai = list ? list[k] : k;
         const Anim &a = T.anims[ai];
         const AnimDerived &d = T.derived[ai];
         const int at = a.animationType;
-        if (q.byFunctionType && !list && !CheckFunctionType(at, q.functionType)) continue;
+        if (q.byFunctionType && !list && !CheckFunctionType(at, q.functionType)) return false;
         if (q.byIncomingVelocity) {
             int aIn = VelocityCat(a.incomingVelocity);
             if (!q.incomingVelocityStrict) {
-                if (q.incomingVelocityNoDribbleToIdle && aIn == kVelIdle && q.incomingVelocity == kVelDribble) continue;
-                if (aIn == kVelIdle && q.incomingVelocity == kVelWalk) continue;
-                if (aIn == kVelIdle && q.incomingVelocity == kVelSprint) continue;
-                if (aIn == kVelDribble && q.incomingVelocity == kVelIdle) continue;
-                if (aIn == kVelWalk && q.incomingVelocity == kVelIdle) continue;
-                if (aIn == kVelSprint && q.incomingVelocity == kVelIdle) continue;
-                if (q.incomingVelocityNoDribbleToSprint && aIn == kVelSprint && q.incomingVelocity == kVelDribble) continue;
+                if (q.incomingVelocityNoDribbleToIdle && aIn == kVelIdle && q.incomingVelocity == kVelDribble) return false;
+                if (aIn == kVelIdle && q.incomingVelocity == kVelWalk) return false;
+                if (aIn == kVelIdle && q.incomingVelocity == kVelSprint) return false;
+                if (aIn == kVelDribble && q.incomingVelocity == kVelIdle) return false;
+                if (aIn == kVelWalk && q.incomingVelocity == kVelIdle) return false;
+                if (aIn == kVelSprint && q.incomingVelocity == kVelIdle) return false;
+                if (q.incomingVelocityNoDribbleToSprint && aIn == kVelSprint && q.incomingVelocity == kVelDribble) return false;
                 if (q.incomingVelocityForceLinearity) {
                     float ain = RangeVelocity(a.incomingVelocity), aout = RangeVelocity(a.outgoingVelocity);
                     float qin = VelocityFloat(q.incomingVelocity);
@@ -355,14 +357,14 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
                     if (VelocityCat(qin) == kVelDribble) qin = kWalkVelocity;
                     float upper = (qin < aout) ? aout : qin;
                     float lower = (aout < qin) ? aout : qin;
-                    if (ain > upper) continue;
-                    if (ain < lower) continue;
+                    if (ain > upper) return false;
+                    if (ain < lower) return false;
                 }
             } else if (aIn != q.incomingVelocity) {
-                continue;
+                return false;
             }
         }
-        if (q.byOutgoingVelocity && VelocityCat(a.outgoingVelocity) != q.outgoingVelocity) continue;
+        if (q.byOutgoingVelocity && VelocityCat(a.outgoingVelocity) != q.outgoingVelocity) return false;
         if (q.bySide) {
             const Vec3 &aIn = a.incomingBodyDirection;
             const Vec3 &aOut = d.crudeOutDirectionRotated;
@@ -374,36 +376,36 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
                 int aInToFenceSide = (aInToFence > 0) ? 0 : 1;
                 int qInToFenceSide = (queryInToFence > 0) ? 0 : 1;
                 int fenceToOutSide = (fenceToOut > 0) ? 0 : 1;
-                if (aInToFenceSide == aSide && fenceToOutSide == aSide && fabsf(aInToFence + fenceToOut) < PI) continue;
+                if (aInToFenceSide == aSide && fenceToOutSide == aSide && fabsf(aInToFence + fenceToOut) < PI) return false;
                 // GRF: adds the side number 0 or 1 to an angle in radians.
                 if (qInToFenceSide == aSide && fenceToOutSide == aSide && fabsf((float)qInToFenceSide + fenceToOut) < PI)
-                    continue;
+                    return false;
             }
         }
         if (q.byPickupBall) {
-            if ((!d.outgoingRetainRaw && q.pickupBall) || (d.outgoingRetainRaw && !q.pickupBall)) continue;
+            if ((!d.outgoingRetainRaw && q.pickupBall) || (d.outgoingRetainRaw && !q.pickupBall)) return false;
         }
-        if (!q.allowLastDitch && a.lastDitch) continue;
+        if (!q.allowLastDitch && a.lastDitch) return false;
         if (byBody) {
             if (VelocityCat(a.incomingVelocity) != kVelIdle) {
-                if (d.crudeInBodyFixAbsolute > queryInBodyFixAbs + margin) continue;
+                if (d.crudeInBodyFixAbsolute > queryInBodyFixAbs + margin) return false;
                 const float qOff = queryBodyEntry >= 0 ? T.selection[ai].incomingBodyAngles[queryBodyEntry]
                                                        : a.incomingBodyDirection.Angle2D(q.incomingBodyDirection);
                 if (q.incomingBodyDirectionStrict) {
-                    if (fabsf(qOff) > margin) continue;
+                    if (fabsf(qOff) > margin) return false;
                 } else {
-                    if (fabsf(qOff) > 0.5f * PI + margin) continue;
+                    if (fabsf(qOff) > 0.5f * PI + margin) return false;
                 }
                 if (q.incomingBodyDirectionForceLinearity) {
                     float bt = T.selection[ai].bodyTurnAngle;
-                    if ((bt > margin && qOff > margin) || (bt < -margin && qOff < -margin)) continue;
-                    if (fabsf(bt) + fabsf(qOff) > PI + margin) continue;
+                    if ((bt > margin && qOff > margin) || (bt < -margin && qOff < -margin)) return false;
+                    if (fabsf(bt) + fabsf(qOff) > PI + margin) return false;
                 }
             } else {
                 if (q.incomingBodyDirectionStrict) {
-                    if (queryIdleBodyAbs > margin) continue;
+                    if (queryIdleBodyAbs > margin) return false;
                 } else {
-                    if (queryIdleBodyAbs > 0.25f * PI + margin) continue;
+                    if (queryIdleBodyAbs > 0.25f * PI + margin) return false;
                 }
             }
         }
@@ -414,7 +416,7 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
                 maxDev = T.maxIncomingBallDeviation.value();
                 if (at == kAtDeflect) maxDev = 0.4f * PI;
             }
-            if (ang > maxDev) continue;
+            if (ang > maxDev) return false;
         }
         if (q.byOutgoingBallDirection) {
             const Vec3 &abd = d.crudeBallDirectionNormalized;
@@ -423,24 +425,32 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
                             : fabsf((qOutNull ? abd : qOutNormalized).Angle2D(abd));
             float maxDev = d.outgoingMaxDeviation;
             if ((double)maxDev == 0.0) maxDev = T.maxOutgoingBallDeviation.value();
-            if (ang > maxDev) continue;
+            if (ang > maxDev) return false;
         }
-        if (q.incomingSpecialState != a.incomingSpecialState) continue;
+        if (q.incomingSpecialState != a.incomingSpecialState) return false;
         if ((q.functionType == kFnDeflect ||
              ((q.incomingRetainState != kStrEmpty) != (a.incomingRetainState != kStrEmpty))) &&
             q.incomingRetainState != a.incomingRetainState)
-            continue;
-        if (q.specialVar1 != a.specialVar1) continue;
-        if (q.specialVar2 != a.specialVar2) continue;
-        if (q.byTripType && d.tripTypeRounded != q.tripType) continue;
+            return false;
+        if (q.specialVar1 != a.specialVar1) return false;
+        if (q.specialVar2 != a.specialVar2) return false;
+        if (q.byTripType && d.tripTypeRounded != q.tripType) return false;
         if (q.heedForcedFoot && d.forcedFootWhich != 0) {
             int foot = d.touchFootLeft ? 0 : 1;
             if (a.currentFoot == 0) foot = foot == 0 ? 1 : 0;
-            if (d.forcedFootWhich == 1 && q.strongFoot != foot) continue;
-            if (d.forcedFootWhich == 2 && q.strongFoot == foot) continue;
+            if (d.forcedFootWhich == 1 && q.strongFoot != foot) return false;
+            if (d.forcedFootWhich == 2 && q.strongFoot == foot) return false;
         }
-        out.e[out.count++] = (int16_t)ai;
+        return true;
+    };
+    for (int k0 = 0; k0 < n; k0 += kGroupLanes) {
+        const int k = k0 + GroupRank();
+        const bool keep = k < n && accepts(k);
+        const uint32_t kept = GroupBallot(keep);
+        if (keep) out.e[out.count + PopCount(kept & ((1u << GroupRank()) - 1u))] = (int16_t)(list ? list[k] : k);
+        out.count += PopCount(kept);
     }
+    GroupSync();
 }
 
 // Directions relative to the humanoid's angle; velocities are categories.
@@ -634,7 +644,8 @@ struct Selector {
     template <class KeyFn>
     HD void Sort(AList &l, KeyFn key) {
         if (l.count < 2) return;
-        for (int i = 0; i < l.count; i++) c.ws->keys[i] = (double)key((int)l[i]);
+        for (int i = GroupRank(); i < l.count; i += kGroupLanes) c.ws->keys[i] = (double)key((int)l[i]);
+        GroupSync();
         StableSortByKeys(c, l);
     }
     HD void SortBaseAnimation(AList &l) {
@@ -1130,23 +1141,26 @@ struct Selector {
         float tmpRotSmuggle = 0, predAngle = 0;
         Vec3 adaptedOut;
         bool found = false;
-        for (int entry = 0; entry < sorted.count && !found; entry++) {
-            const int ai = sorted[entry];
+        // One candidate: its physics plan into `plan`, then its ball keys from the middle one down,
+        // then up; true with the touch at the first key the body reaches.
+        auto evaluate = [&](int ai, PList &plan, float &rotSmuggle, float &predAngleOut, Vec3 &adaptedOutOut, Vec3 &smuggleOut,
+                            int &touchFrame) -> bool {
+            bool hit = false;
             const Anim &a = A(ai);
             bool isBase = a.baseAnimation;
-            CalculatePhysicsVector(ai, useDesiredMovement, desiredMovement, useDesiredBody, desiredBodyRel, positions, tmpRotSmuggle);
-            predAngle = a.outgoingAngle.value() + tmpRotSmuggle;
-            predAngle = ModulateIntoRange(-PI, PI, predAngle);
+            CalculatePhysicsVector(ai, useDesiredMovement, desiredMovement, useDesiredBody, desiredBodyRel, plan, rotSmuggle);
+            predAngleOut = a.outgoingAngle.value() + rotSmuggle;
+            predAngleOut = ModulateIntoRange(-PI, PI, predAngleOut);
+            const float predAngle = predAngleOut;
+            PList &positions = plan;
             Vec3 outMov = RotatedBy(OutgoingMovementOf(positions), bk);
-            adaptedOut = outMov;
+            adaptedOutOut = outMov;
+            const Vec3 adaptedOut = outMov;
             const int total = a.footballCount;
-            AList ids{c.ws->lists[2], 0};
-            for (int t = total / 2; t > -1; t--) ids.push_back(t);
-            for (int t = total / 2 + 1; t < total; t++) ids.push_back(t);
             int defaultTouchFrame = D(ai).touchFrame;
-            for (int tn = 0; tn < total && !found; tn++) {
-                if (ids[tn] >= total) Fatal("a touch of an animation lies past its ball keys");
-                const FootballKey &fk = c.t->football[a.footballFirst + ids[tn]];
+            for (int tn = 0; tn < total && !hit; tn++) {
+                const int key = tn <= total / 2 ? total / 2 - tn : tn;
+                const FootballKey &fk = c.t->football[a.footballFirst + key];
                 Vec3 animBall = fk.position;
                 int tf = fk.frame;
                 if (!retainerIsMe) {
@@ -1224,13 +1238,44 @@ struct Selector {
                     float adv = BodyBallDistanceAdvantage(a, touchMov, inMov, adaptedOut, predAngle, bodyPos, foot, animBall.Get2D(),
                                                           ballPos.Get2D(), rf * tff, cheatOff);
                     if (adv >= 1.0f || retainerIsMe) {
-                        found = true;
-                        best = ai;
-                        bestSmuggle2D = smuggle2D;
-                        touchFrameOut = tf;
+                        hit = true;
+                        smuggleOut = smuggle2D;
+                        touchFrame = tf;
                     }
                 }
             }
+            return hit;
+        };
+        // The lanes of the match evaluate consecutive candidates; the earliest that passes wins.
+        // Without one, the plan and rotation of the last candidate remain, as a sequential search
+        // leaves them.
+        for (int e0 = 0; e0 < sorted.count && !found; e0 += kGroupLanes) {
+            const int entry = e0 + GroupRank();
+            PList mine{kGroupLanes == 1 ? positions.e : c.ws->lanePlans[GroupRank()], 0};
+            float rot = 0, pa = 0;
+            Vec3 ao, sm;
+            int tf = 0;
+            const bool ok = entry < sorted.count && evaluate(sorted[entry], mine, rot, pa, ao, sm, tf);
+            const uint32_t passed = GroupBallot(ok);
+            const int last = sorted.count - 1 - e0;
+            const int from = passed ? LowestBit(passed) : (last < kGroupLanes - 1 ? last : kGroupLanes - 1);
+            tmpRotSmuggle = GroupShuffle(rot, from);
+            const int count = GroupShuffle((int32_t)mine.count, from);
+            if (passed) {
+                found = true;
+                best = sorted[e0 + from];
+                predAngle = GroupShuffle(pa, from);
+                adaptedOut = GroupShuffle(ao, from);
+                bestSmuggle2D = GroupShuffle(sm, from);
+                touchFrameOut = GroupShuffle((int32_t)tf, from);
+            }
+            if (kGroupLanes > 1 && (passed || e0 + kGroupLanes >= sorted.count)) {
+                GroupSync();
+                const Vec3 *src = c.ws->lanePlans[from];
+                for (int i = GroupRank(); i < count; i += kGroupLanes) positions.e[i] = src[i];
+                GroupSync();
+            }
+            positions.count = count;
         }
         if (found) {
             touchPosOut = MentalBallAt(touchFrameOut * 10);

@@ -275,13 +275,17 @@ struct Tables {
     const float *cameraWeights;
 };
 
-// Per-match working memory for the animation selection: candidate lists, planned positions and
-// sort keys. One block per environment in HBM; every lane of the match's wave addresses the same
-// block, so it replaces the large per-thread stack arrays of a thread-per-match design.
+// Lanes of one match with a plan of their own in the candidate search.
+constexpr int kPlanLanes = 8;
+static_assert(kGroupLanes <= kPlanLanes, "every lane of a match needs a candidate plan");
+// Per-match working memory for the animation selection: candidate lists, planned positions, sort
+// keys and one candidate plan per lane of the match. One block per environment in HBM, which every
+// lane of the match addresses, in place of large per-lane stack arrays.
 struct Scratch {
     int16_t lists[3][kMaxAnimations];
     int32_t listCount[3];
     Vec3 plans[2][kAnimPositions];
+    Vec3 lanePlans[kPlanLanes][kAnimPositions];
     double keys[kMaxAnimations];
     int16_t order[2][kMaxAnimations];
 };

@@ -1,9 +1,11 @@
-// The MI355X device of the batch runtime: device memory, copies and the two kernels (reset and
-// step). Each environment runs on one lane, and a workgroup (one wavefront) holds `lanes_` of them.
-// A match is a long chain of dependent loads with data-dependent branches: one match per
-// wavefront leaves the latency of each load exposed, while 64 per wavefront serialize on
-// divergence. 16 measured best on gfx950 for the 11-a-side scenarios (1: 9.1k, 4: 16.9k,
-// 16: 33.5k, 64: 22.9k env-steps/s at 16,384 environments).
+// The MI355X device of the batch runtime: device memory, copies and the kernels (reset, step and
+// the outputs of one environment). Each environment runs on a group of kGroupLanes adjacent lanes
+// (engine/hd.h), and a workgroup (one wavefront) holds `matches_` environments. A match is a long
+// chain of dependent loads with data-dependent branches: one match per wavefront leaves the latency
+// of each load exposed, while many matches per wavefront serialize on divergence. With one lane
+// per match, 16 per wavefront measured best on gfx950 for the 11-a-side scenarios (1: 9.1k,
+// 4: 16.9k, 16: 33.5k, 64: 22.9k env-steps/s at 16,384 environments, early steps); groups of four
+// lanes fill the wavefront with the same 16 matches.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -21,29 +23,40 @@ namespace {
 
 __device__ int32_t gFaultEnvironment;
 
-// The most environments a workgroup holds: one per lane of a wavefront.
-constexpr int kMaxLanes = 64;
+// A workgroup is one wavefront. The launch geometry is host code, where the engine's own
+// eng::kGroupLanes is the host's single lane, so it reads the device group size from the macro
+// both compilation passes share.
+constexpr int kWaveLanes = 64;
+constexpr int kDeviceGroupLanes = ENG_GROUP_LANES;
+constexpr int kMaxMatches = kWaveLanes / kDeviceGroupLanes;
+#if defined(__HIP_DEVICE_COMPILE__)
+static_assert(eng::kGroupLanes == kDeviceGroupLanes, "the launch and the engine agree on the lanes of a match");
+#endif
 
 __device__ void RecordFault(int env) {
     if (eng::gEngineFault == 0) eng::gEngineFault = 1;
     atomicMin(&gFaultEnvironment, env);
 }
 
-__global__ void __launch_bounds__(kMaxLanes) ResetKernel(eng::Batch b, const uint8_t *mask, const int64_t *seeds,
-                                                                     const int32_t *reverse) {
-    const int env = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ int MatchIndex() { return (int)(blockIdx.x * (blockDim.x / kDeviceGroupLanes) + threadIdx.x / kDeviceGroupLanes); }
+
+__global__ void __launch_bounds__(kWaveLanes) ResetKernel(eng::Batch b, const uint8_t *mask, const int64_t *seeds,
+                                                                      const int32_t *reverse) {
+    const int env = MatchIndex();
     if (env >= b.count) return;
     if (mask && !mask[env]) return;
     if (!eng::ResetAndWriteEnvironment(b, env, seeds, reverse)) RecordFault(env);
 }
 
-__global__ void __launch_bounds__(kMaxLanes) StepKernel(eng::Batch b, const int32_t *actions) {
-    const int env = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void __launch_bounds__(kWaveLanes) StepKernel(eng::Batch b, const int32_t *actions) {
+    const int env = MatchIndex();
     if (env >= b.count) return;
     if (!eng::StepEnvironment(b, env, actions)) RecordFault(env);
 }
 
-__global__ void __launch_bounds__(1) OutputKernel(eng::Batch b, int env) { eng::WriteEnvironmentOutputs(b, env, false); }
+__global__ void __launch_bounds__(kDeviceGroupLanes) OutputKernel(eng::Batch b, int env) {
+    eng::WriteEnvironmentOutputs(b, env, false);
+}
 
 void Check(hipError_t e, const char *what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
@@ -52,8 +65,8 @@ void Check(hipError_t e, const char *what) {
 class HipDevice : public eng::host::Device {
 public:
     HipDevice() {
-        // Environments per workgroup (each on its own lane), 1 to 64.
-        if (const char *v = getenv("CUJU_AMD_LANES")) lanes_ = std::max(1, std::min(kMaxLanes, atoi(v)));
+        // Environments per workgroup, 1 to 64 / kGroupLanes.
+        if (const char *v = getenv("CUJU_AMD_MATCHES")) matches_ = std::max(1, std::min(kMaxMatches, atoi(v)));
         int n = 0;
         Check(hipGetDeviceCount(&n), "hipGetDeviceCount");
         if (n < 1) throw std::runtime_error("no HIP device");
@@ -76,19 +89,20 @@ public:
     void Fill(void *d, int v, size_t n) override { Check(hipMemset(d, v, n), "hipMemset"); }
     void Synchronize(void *stream) override { Check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize"); }
     void Reset(const eng::Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *stream) override {
-        const int blocks = (b.count + lanes_ - 1) / lanes_;
-        hipLaunchKernelGGL(ResetKernel, dim3(blocks), dim3(lanes_), 0, static_cast<hipStream_t>(stream), b, mask, seeds,
-                           reverse);
+        const int blocks = (b.count + matches_ - 1) / matches_;
+        hipLaunchKernelGGL(ResetKernel, dim3(blocks), dim3(matches_ * kDeviceGroupLanes), 0, static_cast<hipStream_t>(stream), b,
+                           mask, seeds, reverse);
         Check(hipGetLastError(), "reset launch");
     }
     void Step(const eng::Batch &b, const int32_t *actions, void *stream) override {
-        const int blocks = (b.count + lanes_ - 1) / lanes_;
-        hipLaunchKernelGGL(StepKernel, dim3(blocks), dim3(lanes_), 0, static_cast<hipStream_t>(stream), b, actions);
+        const int blocks = (b.count + matches_ - 1) / matches_;
+        hipLaunchKernelGGL(StepKernel, dim3(blocks), dim3(matches_ * kDeviceGroupLanes), 0, static_cast<hipStream_t>(stream), b,
+                           actions);
         Check(hipGetLastError(), "step launch");
     }
     void Outputs(const eng::Batch &b, int env, void *stream) override {
         if (env < 0 || env >= b.count) throw std::out_of_range("no environment " + std::to_string(env));
-        hipLaunchKernelGGL(OutputKernel, dim3(1), dim3(1), 0, static_cast<hipStream_t>(stream), b, env);
+        hipLaunchKernelGGL(OutputKernel, dim3(1), dim3(kDeviceGroupLanes), 0, static_cast<hipStream_t>(stream), b, env);
         Check(hipGetLastError(), "output launch");
     }
     void CheckFault() override {
@@ -102,7 +116,7 @@ public:
     }
 
 private:
-    int lanes_ = 16;
+    int matches_ = kMaxMatches < 16 ? kMaxMatches : 16;
     void ClearFault() {
         const uint32_t zero = 0;
         const int32_t none = 0x7fffffff;

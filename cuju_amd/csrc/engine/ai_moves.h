@@ -297,13 +297,23 @@ struct AIBase {
         Vec3 ballMovRough = (MentalBall((int)(ttb + 10)) - MentalBall((int)ttb)).Get2D() * 100.0f;
         Vec3 ballDirRough = ballMovRough.Normalized(adDir);
         unsigned step = 1;
+        const Vec3 mov = Mov();
+        const bool walks = TimeWalkApplies(mov);
+        TimeWalk &walk = c.ws->walk;
+        bool built = false;
         for (unsigned t = start; t < (unsigned)kBallPredictionSpanMs; t += 10 * step) {
             bool forced = false;
             Vec3 target = MentalBall((int)t);
             if (fabsf(target.v[0]) > kPitchHalfLength - 0.2f || fabsf(target.v[1]) > kPitchHalfWidth - 0.2f) forced = true;
             if (!forced && target.v[2] >= 1.0f) continue;
             target = target.Get2D();
-            unsigned needed = GetTimeNeededMs(pp, Mov(), target, maxVel, true, t).usual;
+            if (walks && !built) {
+                BuildTimeWalk(walk, pp, mov, maxVel);
+                GroupSync();
+                built = true;
+            }
+            unsigned needed =
+                (walks ? WalkTimeNeeded(walk, pp, mov, target, maxVel, true, t, true) : GetTimeNeededMs(pp, mov, target, maxVel, true, t)).usual;
             int next = TruncToInt32(roundf((float)(int)(needed - t) * 0.05f)) - 5;
             next = next < 1 ? 1 : next;
             next = 10 < next ? 10 : next;

@@ -214,8 +214,18 @@ HDN void BallProcess(Ball &b, bool inGoal) {
     }
 }
 
-// `clamp((float)(10 k) / (float)700, 0, 1)`, computed in float once per step index.
-HD float TimeNeededBias(uint32_t step) { return Clamp((float)(step * 10) / (float)700, 0, 1); }
+// `clamp((float)(10 k) / (float)700, 0, 1)`, computed in float once per step index. The device
+// divides by a reciprocal product and one fused correction, which rounds exactly as the division
+// for every step index below 200 (the walks end at 70).
+HD float TimeNeededBias(uint32_t step) {
+#if ENG_DEVICE
+    const float x = (float)(step * 10), r = 1.0f / 700.0f;
+    const float q = x * r;
+    return Clamp(fmaf(fmaf(-q, 700.0f, x), r, q), 0, 1);
+#else
+    return Clamp((float)(step * 10) / (float)700, 0, 1);
+#endif
+}
 
 struct TimeNeeded {
     uint32_t usual = 0, optimistic = 0;
@@ -247,8 +257,8 @@ HDN TimeNeeded GetTimeNeededMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &tar
     float usualR = 0.28f, optR = 0.9f, resultingUsualR = usualR;
     bool foundOpt = false;
     float amv = maxVel * 0.94f;
-    while (true) {
-        float bias = TimeNeededBias(time / step);
+    for (uint32_t k = 0;; k++) {
+        float bias = TimeNeededBias(k);  // k = time / step
         if (bias >= 1.0f) {
             float rem = Clamp((target - cur).Length() - usualR, 0.0f, 100000.0f);
             r.usual = TruncToUint32((float)time + (rem / amv) * 1000);
@@ -278,6 +288,99 @@ HDN TimeNeeded GetTimeNeededMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &tar
         time += step;
     }
     if (maxTime != (uint32_t)-1 && time > maxTime) {
+        uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
+        r.usual = def > ext ? def : ext;
+        if (!foundOpt) r.optimistic = r.usual;
+        return r;
+    }
+    if (r.usual == 0) {
+        r.usual = (uint32_t)TruncToInt32(roundf(Clamp((target - pos).Length() / resultingUsualR, 0.0f, 1.0f) * 10));
+        r.optimistic = r.usual;
+    }
+    return r;
+}
+
+// GetTimeNeededMs split in two for a player whose movement exceeds the idle threshold: the walk,
+// which every target shares, and the search along it for one target. The search gives the same
+// result as GetTimeNeededMs. With `cooperative` the lanes of the match (all running the same
+// sequential code) test consecutive steps of the walk together.
+HD bool TimeWalkApplies(const Vec3 &mov) { return mov.Length() > kIdleDribbleSwitch; }
+HDN void BuildTimeWalk(TimeWalk &wk, const Vec3 &pos, const Vec3 &mov, float maxVel) {
+    Vec3 cur = pos, cm = mov;
+    cur += cm.Normalized() * 0.1f;
+    cur += cm * 0.01f;
+    wk.z = cur.v[2];
+    const uint32_t step = 10;
+    float usualR = 0.28f, optR = 0.9f;
+    const float amv = maxVel * 0.94f;
+    for (int k = 0; k < kTimeWalkSteps; k++) {
+        const float bias = TimeNeededBias((uint32_t)k);
+        cm.v[0] = mov.v[0] * (1.0f - bias);
+        cm.v[1] = mov.v[1] * (1.0f - bias);
+        cur.v[0] += cm.v[0] * step * 0.001f;
+        cur.v[1] += cm.v[1] * step * 0.001f;
+        usualR += amv * bias * step * 0.001f;
+        optR += amv * bias * step * 0.001f;
+        wk.x[k] = cur.v[0];
+        wk.y[k] = cur.v[1];
+        wk.usual[k] = usualR;
+        wk.optimistic[k] = optR;
+        wk.usualSquared[k] = usualR * usualR;
+        wk.optimisticSquared[k] = optR * optR;
+    }
+}
+HDN TimeNeeded WalkTimeNeeded(const TimeWalk &wk, const Vec3 &pos, const Vec3 &mov, const Vec3 &target, float maxVel,
+                              bool precise, uint32_t maxTime, bool cooperative) {
+    TimeNeeded r;
+    if ((pos - target).Length() > (precise ? 48.0f : 16.0f)) {
+        r.usual = DirectTimeMs(pos, mov, target, maxVel);
+        r.optimistic = r.usual - 200;
+        return r;
+    }
+    const bool limited = maxTime != (uint32_t)-1;
+    const int stride = cooperative ? kGroupLanes : 1, rank = cooperative ? GroupRank() : 0;
+    int reach = -1, optimistic = -1;
+    for (int k0 = 0; k0 < kTimeWalkSteps && reach < 0; k0 += stride) {
+        const int k = k0 + rank;
+        bool u = false, o = false;
+        if (k < kTimeWalkSteps) {
+            const bool late = limited && (uint32_t)(k * 10) > maxTime;
+            const Vec3 cur(wk.x[k], wk.y[k], wk.z);
+            const float d2 = (target - cur).SquaredLength();
+            o = d2 < wk.optimisticSquared[k] || late;
+            u = d2 < wk.usualSquared[k] || late;
+        }
+        uint32_t um = cooperative ? GroupBallot(u) : (uint32_t)u;
+        uint32_t om = cooperative ? GroupBallot(o) : (uint32_t)o;
+        if (um) {
+            reach = k0 + LowestBit(um);
+            om &= (2u << LowestBit(um)) - 1u;  // the optimistic test comes first within a step
+        }
+        if (optimistic < 0 && om) optimistic = k0 + LowestBit(om);
+    }
+    const bool foundOpt = optimistic >= 0;
+    if (foundOpt) r.optimistic = (uint32_t)(optimistic * 10);
+    uint32_t time;
+    float resultingUsualR;
+    if (reach >= 0) {
+        time = (uint32_t)(reach * 10);
+        resultingUsualR = wk.usual[reach];
+        r.usual = time;
+    } else {
+        // The bias reaches 1 at 700 ms; the rest of the way runs at 94% of the maximum velocity.
+        time = (uint32_t)(kTimeWalkSteps * 10);
+        const int last = kTimeWalkSteps - 1;
+        const Vec3 cur(wk.x[last], wk.y[last], wk.z);
+        const float amv = maxVel * 0.94f;
+        float rem = Clamp((target - cur).Length() - wk.usual[last], 0.0f, 100000.0f);
+        r.usual = TruncToUint32((float)time + (rem / amv) * 1000);
+        resultingUsualR = wk.usual[last] + rem;
+        if (!foundOpt) {
+            float ro = Clamp((target - cur).Length() - wk.optimistic[last], 0.0f, 100000.0f);
+            r.optimistic = TruncToUint32((float)time + (ro / amv) * 1000);
+        }
+    }
+    if (limited && time > maxTime) {
         uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
         r.usual = def > ext ? def : ext;
         if (!foundOpt) r.optimistic = r.usual;

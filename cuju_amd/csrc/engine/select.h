@@ -182,22 +182,28 @@ HDN void StableSortByKeys(const Ctx &c, AList &list) {
     for (int i = 0; i < n; i++)
         if (keys[i] != keys[i]) Fatal("an animation sort key is NaN");
 #endif
-    for (int i = 0; i < n; i++) a[i] = (int16_t)i;
+    // Bottom-up merge sort; the merges of one pass are independent, so the lanes of the match take
+    // them in turn.
+    for (int i = GroupRank(); i < n; i += kGroupLanes) a[i] = (int16_t)i;
+    GroupSync();
     for (int width = 1; width < n; width *= 2) {
-        for (int lo = 0; lo < n; lo += 2 * width) {
+        for (int lo = GroupRank() * 2 * width; lo < n; lo += kGroupLanes * 2 * width) {
             int mid = lo + width < n ? lo + width : n, hi = lo + 2 * width < n ? lo + 2 * width : n;
             int l = lo, r = mid, o = lo;
             while (l < mid && r < hi) b[o++] = (keys[a[r]] < keys[a[l]]) ? a[r++] : a[l++];
             while (l < mid) b[o++] = a[l++];
             while (r < hi) b[o++] = a[r++];
         }
+        GroupSync();
         int16_t *t = a;
         a = b;
         b = t;
     }
     // `a` holds the order; gather through `b`.
-    for (int i = 0; i < n; i++) b[i] = list.e[a[i]];
-    for (int i = 0; i < n; i++) list.e[i] = b[i];
+    for (int i = GroupRank(); i < n; i += kGroupLanes) b[i] = list.e[a[i]];
+    GroupSync();
+    for (int i = GroupRank(); i < n; i += kGroupLanes) list.e[i] = b[i];
+    GroupSync();
 }
 
 constexpr int kMaxChainKeys = 8;
@@ -1653,7 +1659,10 @@ struct Selector {
                 k[n++] = D(i).priorityAbsolute;
             });
             Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
-            CalculatePhysicsVector(sel, cmd.useDesiredMovement, dm, cmd.useDesiredLookAt, dbr, plan, tmpRot);
+            {
+                ENG_SCOPE(48);
+                CalculatePhysicsVector(sel, cmd.useDesiredMovement, dm, cmd.useDesiredLookAt, dbr, plan, tmpRot);
+            }
         } else if (fn == kFnBallControl) {
             if (NeedTouch(l[0], cmd))
                 sel = GetBestCheatableAnimationID(l, cmd.useDesiredMovement, cmd.desiredDirection, cmd.desiredVelocityFloat,

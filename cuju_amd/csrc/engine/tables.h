@@ -275,6 +275,16 @@ struct Tables {
     const float *cameraWeights;
 };
 
+// The walk that GRF's time-to-target estimate takes from a moving player (ai_time.h:170-200):
+// position, reach and optimistic reach after each 10 ms step while the acceleration bias grows
+// below 1. It depends on the player's position, movement and speed, not on the target.
+constexpr int kTimeWalkSteps = 70;
+struct TimeWalk {
+    float z;  // the walk moves in x and y only
+    float x[kTimeWalkSteps], y[kTimeWalkSteps];
+    float usual[kTimeWalkSteps], optimistic[kTimeWalkSteps];
+    float usualSquared[kTimeWalkSteps], optimisticSquared[kTimeWalkSteps];
+};
 // Lanes of one match with a plan of their own in the candidate search.
 constexpr int kPlanLanes = 8;
 static_assert(kGroupLanes <= kPlanLanes, "every lane of a match needs a candidate plan");
@@ -286,6 +296,7 @@ struct Scratch {
     int32_t listCount[3];
     Vec3 plans[2][kAnimPositions];
     Vec3 lanePlans[kPlanLanes][kAnimPositions];
+    TimeWalk walk;  // the match's sequential code
     double keys[kMaxAnimations];
     int16_t order[2][kMaxAnimations];
 };

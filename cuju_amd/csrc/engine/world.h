@@ -160,10 +160,12 @@ HDN void MirrorHumanoid(Humanoid &h, bool &mirrored) {
     h.decayingPositionOffset.Mirror();
 }
 
+// Each humanoid mirrors on its own, so the lanes of the match take the players in turn; the caller
+// synchronizes the group before the mirrored state is read.
 HD void MirrorTeam(World &w, int teamID) {
     w.flags.teamSide[teamID] *= -1;
     w.flags.teamMirrored[teamID] = !w.flags.teamMirrored[teamID];
-    for (int p = 0; p < w.match.playerCount; p++)
+    for (int p = GroupRank(); p < w.match.playerCount; p += kGroupLanes)
         if (w.playerTeamID[p] == teamID) MirrorHumanoid(w.match.players[p].base.humanoid, w.flags.humanoidMirrored[p]);
 }
 
@@ -187,7 +189,7 @@ HD void MentalMaterialize(MentalImage &m) {
 
 HD void MirrorMentalImage(World &w, int k, bool t0, bool t1, bool ball) {
     MentalImage &m = w.match.mentalImages[k];
-    for (int i = 0; i < m.players.count; i++) {
+    for (int i = GroupRank(); i < m.players.count; i += kGroupLanes) {
         PlayerImage &p = m.players[i];
         int team = w.playerTeamID[p.player];
         if (team == 0 ? t0 : t1) {
@@ -211,6 +213,7 @@ HDN void MirrorMatch(World &w, bool t0, bool t1, bool ball) {
         MirrorBall(w.match.ball);
     }
     for (int k = 0; k < w.match.mentalImages.count; k++) MirrorMentalImage(w, k, t0, t1, ball);
+    GroupSync();
 }
 
 // A state stores the ball, last-touch team IDs and referee team/positions in canonical order; the

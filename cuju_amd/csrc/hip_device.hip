@@ -27,6 +27,10 @@ __device__ int32_t gFaultEnvironment;
 // eng::kGroupLanes is the host's single lane, so it reads the device group size from the macro
 // both compilation passes share.
 constexpr int kWaveLanes = 64;
+// Wavefronts each SIMD must be able to hold, which bounds the registers of a lane.
+#ifndef ENG_WAVES_PER_SIMD
+#define ENG_WAVES_PER_SIMD 1
+#endif
 constexpr int kDeviceGroupLanes = ENG_GROUP_LANES;
 constexpr int kMaxMatches = kWaveLanes / kDeviceGroupLanes;
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -40,7 +44,7 @@ __device__ void RecordFault(int env) {
 
 __device__ int MatchIndex() { return (int)(blockIdx.x * (blockDim.x / kDeviceGroupLanes) + threadIdx.x / kDeviceGroupLanes); }
 
-__global__ void __launch_bounds__(kWaveLanes) ResetKernel(eng::Batch b, const uint8_t *mask, const int64_t *seeds,
+__global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) ResetKernel(eng::Batch b, const uint8_t *mask, const int64_t *seeds,
                                                                       const int32_t *reverse) {
     const int env = MatchIndex();
     if (env >= b.count) return;
@@ -48,7 +52,7 @@ __global__ void __launch_bounds__(kWaveLanes) ResetKernel(eng::Batch b, const ui
     if (!eng::ResetAndWriteEnvironment(b, env, seeds, reverse)) RecordFault(env);
 }
 
-__global__ void __launch_bounds__(kWaveLanes) StepKernel(eng::Batch b, const int32_t *actions) {
+__global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) StepKernel(eng::Batch b, const int32_t *actions) {
     const int env = MatchIndex();
     if (env >= b.count) return;
     if (!eng::StepEnvironment(b, env, actions)) RecordFault(env);

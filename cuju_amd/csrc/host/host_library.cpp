@@ -115,3 +115,26 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_episode_seeds(
     eng::SeedEpisodeGenerator(*g, seed, index);
     for (int i = 0; i < count; i++) out[i] = eng::DrawEpisodeSeed(*g);
 }
+
+// GRF's time-to-target estimate for `count` cases, directly and along the shared walk (both usual
+// and optimistic times per case, direct first); tests compare the two.
+extern "C" __attribute__((visibility("default"))) void cuju_debug_time_needed(const float *cases, int count, unsigned int *out) {
+    auto walk = std::make_unique<eng::TimeWalk>();
+    for (int i = 0; i < count; i++) {
+        const float *q = cases + (size_t)i * 12;
+        const eng::Vec3 pos(q[0], q[1], q[2]), mov(q[3], q[4], q[5]), target(q[6], q[7], q[8]);
+        const float maxVel = q[9];
+        const bool precise = q[10] != 0.0f;
+        const uint32_t maxTime = q[11] < 0 ? (uint32_t)-1 : (uint32_t)q[11];
+        const eng::TimeNeeded a = eng::GetTimeNeededMs(pos, mov, target, maxVel, precise, maxTime);
+        eng::TimeNeeded b = a;
+        if (eng::TimeWalkApplies(mov)) {
+            eng::BuildTimeWalk(*walk, pos, mov, maxVel);
+            b = eng::WalkTimeNeeded(*walk, pos, mov, target, maxVel, precise, maxTime, false);
+        }
+        out[(size_t)i * 4 + 0] = a.usual;
+        out[(size_t)i * 4 + 1] = a.optimistic;
+        out[(size_t)i * 4 + 2] = b.usual;
+        out[(size_t)i * 4 + 3] = b.optimistic;
+    }
+}

@@ -125,3 +125,48 @@ def test_set_state_refuses_another_scenario(reference_library, host_library):
     with pytest.raises(RuntimeError, match='do not load'):
         target.set_raw_state(0, b'\x00' * 16, episode)
     target.close()
+
+
+def test_time_walk_matches_the_direct_estimate(host_library):
+    """The time-to-target estimate along the precomputed walk equals GRF's direct loop
+    (ai_time.h:102-409) on random players, movements, targets and time limits, near and far."""
+    lib = ctypes.CDLL(host_library)
+    rng = np.random.default_rng(5)
+    n = 200_000
+    pos = np.column_stack([rng.uniform(-55, 55, n), rng.uniform(-36, 36, n), rng.choice([0.0, 0.1], n)])
+    speed = rng.choice([0.0, 1.0, 1.8, 1.80001, 3.0, 6.0, 9.0], n) * rng.uniform(0.5, 1.5, n)
+    angle = rng.uniform(-np.pi, np.pi, n)
+    mov = np.column_stack([speed * np.cos(angle), speed * np.sin(angle), rng.choice([0.0, 0.3], n)])
+    reach = rng.choice([0.5, 3.0, 10.0, 20.0, 40.0, 60.0], n) * rng.uniform(0, 1, n)
+    turn = rng.uniform(-np.pi, np.pi, n)
+    target = np.column_stack([pos[:, 0] + reach * np.cos(turn), pos[:, 1] + reach * np.sin(turn), np.zeros(n)])
+    limit = np.where(rng.uniform(size=n) < 0.3, -1.0, rng.integers(0, 3000, n).astype(float))
+    cases = np.column_stack([pos, mov, target, rng.uniform(5, 9.5, n), rng.integers(0, 2, n), limit]).astype(np.float32)
+    out = np.zeros((n, 4), dtype=np.uint32)
+    lib.cuju_debug_time_needed(ctypes.c_void_p(cases.ctypes.data), n, ctypes.c_void_p(out.ctypes.data))
+    assert np.array_equal(out[:, :2], out[:, 2:])
+    walked = np.linalg.norm(mov[:, :2], axis=1) > 2.0
+    assert walked.sum() > n // 3
+
+
+def test_device_time_bias_rounds_as_the_division():
+    """The device computes GRF's acceleration bias (10 k) / 700 as a reciprocal product with one
+    fused correction (engine/ball.h, TimeNeededBias); for every step index the walks use (k < 200)
+    that rounds exactly as the float division."""
+    from fractions import Fraction
+
+    def fma(a, b, c):
+        exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+        near = np.float32(float(exact))
+        best = near
+        for d in (np.nextafter(near, np.float32(-np.inf)), near, np.nextafter(near, np.float32(np.inf))):
+            e, b0 = abs(Fraction(float(d)) - exact), abs(Fraction(float(best)) - exact)
+            if e < b0 or (e == b0 and int(np.float32(d).view(np.int32)) % 2 == 0):
+                best = d
+        return np.float32(best)
+
+    r = np.float32(1) / np.float32(700)
+    for k in range(200):
+        x = np.float32(10 * k)
+        q = x * r
+        assert fma(fma(-q, np.float32(700), x), r, q) == x / np.float32(700), k

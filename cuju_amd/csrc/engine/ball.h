@@ -236,7 +236,7 @@ HD uint32_t DirectTimeMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &target, f
 }
 
 // Velocities in m/s; `maxTime` is UINT32_MAX for no limit.
-HDN TimeNeeded GetTimeNeededMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &target, float maxVel,
+HD TimeNeeded GetTimeNeededMs(const Vec3 &pos, const Vec3 &mov, const Vec3 &target, float maxVel,
                                bool precise, uint32_t maxTime) {
     ENG_SCOPE(36);
     TimeNeeded r;

@@ -112,7 +112,7 @@ HD bool SinCosReduce(float y, double *xr, double *sgn, int *n, int *set) {
     return true;
 }
 
-HDN float sinf(float y) {
+HD float sinf(float y) {
     uint32_t top = Top12f(y);
     if (top >= Top12f(INFINITY)) return (y - y) / (y - y);
     if (top < Top12f(0x1.921FB6p-1f)) {
@@ -126,7 +126,7 @@ HDN float sinf(float y) {
     return SinCosPoly(x * s, x * x, LoadSinCos(set), n);
 }
 
-HDN float cosf(float y) {
+HD float cosf(float y) {
     uint32_t top = Top12f(y);
     if (top >= Top12f(INFINITY)) return (y - y) / (y - y);
     if (top < Top12f(0x1.921FB6p-1f)) {
@@ -141,7 +141,7 @@ HDN float cosf(float y) {
 }
 
 // sinf and cosf of one argument sharing the reduction; each result equals the single function's.
-HDN SinCos sincosf(float y) {
+HD SinCos sincosf(float y) {
     uint32_t top = Top12f(y);
     if (top >= Top12f(INFINITY)) {
         float v = (y - y) / (y - y);
@@ -222,7 +222,7 @@ HD bool SignalingF(float x) {
     return 2 * (i ^ 0x00400000) > 2u * 0x7fc00000;
 }
 
-HDN float powf(float x, float y) {
+HD float powf(float x, float y) {
     uint32_t sign_bias = 0;
     uint32_t ix = BitsOf(x), iy = BitsOf(y);
     if (ix - 0x00800000 >= 0x7f800000 - 0x00800000 || Powf_ZeroInfNan(iy)) {
@@ -442,7 +442,7 @@ HD float RationalAcos(float z) {
     return p / q;
 }
 
-HDN float acosf(float x) {
+HD float acosf(float x) {
     const float pi = 3.1415925026e+00f, pio2_hi = 1.5707962513e+00f, pio2_lo = 7.5497894159e-08f;
     int32_t hx = (int32_t)BitsOf(x), ix = hx & 0x7fffffff;
     if (ix == 0x3f800000) {
@@ -474,7 +474,7 @@ HDN float acosf(float x) {
 
 HDN float asinf(float x);
 
-HDN float atanf(float x) {
+HD float atanf(float x) {
     const float atanhi[4] = {4.6364760399e-01f, 7.8539812565e-01f, 9.8279368877e-01f,
                              1.5707962513e+00f};
     const float atanlo[4] = {5.0121582440e-09f, 3.7748947079e-08f, 3.4473217170e-08f,
@@ -521,7 +521,7 @@ HDN float atanf(float x) {
     return (hx < 0) ? -z : z;
 }
 
-HDN float atan2f(float y, float x) {
+HD float atan2f(float y, float x) {
     const float tiny = 1.0e-30f, pi_o_4 = 7.8539818525e-01f, pi_o_2 = 1.5707963705e+00f,
                 pi = 3.1415927410e+00f, pi_lo = -8.7422776573e-08f;
     int32_t hx = (int32_t)BitsOf(x), hy = (int32_t)BitsOf(y);
@@ -588,7 +588,7 @@ HDN float atan2f(float y, float x) {
 
 // ---- asinf: glibc 2.39 flt-32 e_asinf.c ----------------------------------------------------------
 // Reference: include/cuju/libm/asinf.h:40-95.
-HDN float asinf(float x) {
+HD float asinf(float x) {
     const float pio2_hi = 1.57079637050628662109375f, pio2_lo = -4.37113900018624283e-8f,
                 pio4_hi = 0.785398185253143310546875f, p0 = 1.666675248e-1f, p1 = 7.495297643e-2f,
                 p2 = 4.547037598e-2f, p3 = 2.417951451e-2f, p4 = 4.216630880e-2f;

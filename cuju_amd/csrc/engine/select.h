@@ -339,14 +339,11 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
     const Vec3 qOutNormalized = qOutNull ? Vec3(0) : qOut2D.Normalized(Vec3(0));
     // Each animation passes or fails on its own, so the lanes of the match test consecutive ones
     // and append the passing ones in list order.
-    auto accepts = [&](int k) -> bool {
-        const int ai = list ? list[k] : k;
-        const Anim &a = T.anims[ai];
-        const AnimDerived &d = T.derived[ai];
-        const int at = a.animationType;
+    auto accepts = [&](const CrudeRecord &r) -> bool {
+        const int at = r.animationType;
         if (q.byFunctionType && !list && !CheckFunctionType(at, q.functionType)) return false;
         if (q.byIncomingVelocity) {
-            int aIn = VelocityCat(a.incomingVelocity);
+            int aIn = VelocityCat(r.incomingVelocity);
             if (!q.incomingVelocityStrict) {
                 if (q.incomingVelocityNoDribbleToIdle && aIn == kVelIdle && q.incomingVelocity == kVelDribble) return false;
                 if (aIn == kVelIdle && q.incomingVelocity == kVelWalk) return false;
@@ -356,7 +353,7 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
                 if (aIn == kVelSprint && q.incomingVelocity == kVelIdle) return false;
                 if (q.incomingVelocityNoDribbleToSprint && aIn == kVelSprint && q.incomingVelocity == kVelDribble) return false;
                 if (q.incomingVelocityForceLinearity) {
-                    float ain = RangeVelocity(a.incomingVelocity), aout = RangeVelocity(a.outgoingVelocity);
+                    float ain = RangeVelocity(r.incomingVelocity), aout = RangeVelocity(r.outgoingVelocity);
                     float qin = VelocityFloat(q.incomingVelocity);
                     if (VelocityCat(ain) == kVelDribble) ain = kWalkVelocity;
                     if (VelocityCat(aout) == kVelDribble) aout = kWalkVelocity;
@@ -370,11 +367,11 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
                 return false;
             }
         }
-        if (q.byOutgoingVelocity && VelocityCat(a.outgoingVelocity) != q.outgoingVelocity) return false;
+        if (q.byOutgoingVelocity && VelocityCat(r.outgoingVelocity) != q.outgoingVelocity) return false;
         if (q.bySide) {
-            const Vec3 &aIn = a.incomingBodyDirection;
-            const Vec3 &aOut = d.crudeOutDirectionRotated;
-            const float turn = d.crudeTurnAngle;
+            const Vec3 &aIn = r.incomingBodyDirection;
+            const Vec3 &aOut = r.outDirectionRotated;
+            const float turn = r.turnAngle;
             if (fabsf(turn) > 0.06f * PI) {
                 int aSide = (turn > 0) ? 0 : 1;
                 float aInToFence = fenced.Angle2D(aIn);
@@ -388,22 +385,23 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
                     return false;
             }
         }
+        const bool retains = r.flags & 1;
         if (q.byPickupBall) {
-            if ((!d.outgoingRetainRaw && q.pickupBall) || (d.outgoingRetainRaw && !q.pickupBall)) return false;
+            if ((!retains && q.pickupBall) || (retains && !q.pickupBall)) return false;
         }
-        if (!q.allowLastDitch && a.lastDitch) return false;
+        if (!q.allowLastDitch && (r.flags & 2)) return false;
         if (byBody) {
-            if (VelocityCat(a.incomingVelocity) != kVelIdle) {
-                if (d.crudeInBodyFixAbsolute > queryInBodyFixAbs + margin) return false;
-                const float qOff = queryBodyEntry >= 0 ? T.selection[ai].incomingBodyAngles[queryBodyEntry]
-                                                       : a.incomingBodyDirection.Angle2D(q.incomingBodyDirection);
+            if (VelocityCat(r.incomingVelocity) != kVelIdle) {
+                if (r.inBodyFixAbsolute > queryInBodyFixAbs + margin) return false;
+                const float qOff = queryBodyEntry >= 0 ? r.incomingBodyAngles[queryBodyEntry]
+                                                       : r.incomingBodyDirection.Angle2D(q.incomingBodyDirection);
                 if (q.incomingBodyDirectionStrict) {
                     if (fabsf(qOff) > margin) return false;
                 } else {
                     if (fabsf(qOff) > 0.5f * PI + margin) return false;
                 }
                 if (q.incomingBodyDirectionForceLinearity) {
-                    float bt = T.selection[ai].bodyTurnAngle;
+                    float bt = r.bodyTurnAngle;
                     if ((bt > margin && qOff > margin) || (bt < -margin && qOff < -margin)) return false;
                     if (fabsf(bt) + fabsf(qOff) > PI + margin) return false;
                 }
@@ -415,9 +413,9 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
                 }
             }
         }
-        if (q.byIncomingBallDirection && d.crudeInBallNonzero && qInBallNonzero) {
-            float ang = fabsf(qInBallAdapted.Angle2D(d.crudeInBallAdapted));
-            float maxDev = d.incomingMaxDeviation;
+        if (q.byIncomingBallDirection && (r.flags & 4) && qInBallNonzero) {
+            float ang = fabsf(qInBallAdapted.Angle2D(r.inBallAdapted));
+            float maxDev = r.incomingMaxDeviation;
             if (maxDev == 0.0f) {
                 maxDev = T.maxIncomingBallDeviation.value();
                 if (at == kAtDeflect) maxDev = 0.4f * PI;
@@ -425,35 +423,34 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
             if (ang > maxDev) return false;
         }
         if (q.byOutgoingBallDirection) {
-            const Vec3 &abd = d.crudeBallDirectionNormalized;
-            float ang = qOutNull && T.selection[ai].ballDirectionFinite
-                            ? 0.0f
-                            : fabsf((qOutNull ? abd : qOutNormalized).Angle2D(abd));
-            float maxDev = d.outgoingMaxDeviation;
+            const Vec3 &abd = r.ballDirectionNormalized;
+            float ang = qOutNull && (r.flags & 8) ? 0.0f : fabsf((qOutNull ? abd : qOutNormalized).Angle2D(abd));
+            float maxDev = r.outgoingMaxDeviation;
             if ((double)maxDev == 0.0) maxDev = T.maxOutgoingBallDeviation.value();
             if (ang > maxDev) return false;
         }
-        if (q.incomingSpecialState != a.incomingSpecialState) return false;
+        if (q.incomingSpecialState != r.incomingSpecialState) return false;
         if ((q.functionType == kFnDeflect ||
-             ((q.incomingRetainState != kStrEmpty) != (a.incomingRetainState != kStrEmpty))) &&
-            q.incomingRetainState != a.incomingRetainState)
+             ((q.incomingRetainState != kStrEmpty) != (r.incomingRetainState != kStrEmpty))) &&
+            q.incomingRetainState != r.incomingRetainState)
             return false;
-        if (q.specialVar1 != a.specialVar1) return false;
-        if (q.specialVar2 != a.specialVar2) return false;
-        if (q.byTripType && d.tripTypeRounded != q.tripType) return false;
-        if (q.heedForcedFoot && d.forcedFootWhich != 0) {
-            int foot = d.touchFootLeft ? 0 : 1;
-            if (a.currentFoot == 0) foot = foot == 0 ? 1 : 0;
-            if (d.forcedFootWhich == 1 && q.strongFoot != foot) return false;
-            if (d.forcedFootWhich == 2 && q.strongFoot == foot) return false;
+        if (q.specialVar1 != r.specialVar1) return false;
+        if (q.specialVar2 != r.specialVar2) return false;
+        if (q.byTripType && r.tripTypeRounded != q.tripType) return false;
+        if (q.heedForcedFoot && r.forcedFootWhich != 0) {
+            int foot = (r.flags & 16) ? 0 : 1;
+            if (r.currentFoot == 0) foot = foot == 0 ? 1 : 0;
+            if (r.forcedFootWhich == 1 && q.strongFoot != foot) return false;
+            if (r.forcedFootWhich == 2 && q.strongFoot == foot) return false;
         }
         return true;
     };
+    const CrudeRecord *records = list ? T.crude + T.fnOffset[q.functionType] : T.crudeByIndex;
     for (int k0 = 0; k0 < n; k0 += kGroupLanes) {
         const int k = k0 + GroupRank();
-        const bool keep = k < n && accepts(k);
+        const bool keep = k < n && accepts(records[k]);
         const uint32_t kept = GroupBallot(keep);
-        if (keep) out.e[out.count + PopCount(kept & ((1u << GroupRank()) - 1u))] = (int16_t)(list ? list[k] : k);
+        if (keep) out.e[out.count + PopCount(kept & ((1u << GroupRank()) - 1u))] = records[k].index;
         out.count += PopCount(kept);
     }
     GroupSync();

@@ -250,6 +250,21 @@ struct SelectionRecord {
     int32_t smoothedFirst;  // into smoothed[], -1 below two positions
     bool ballDirectionFinite;
 };
+// Every term the crude selection reads of one animation, copied from Anim, AnimDerived and
+// SelectionRecord into one 128-byte line: the filter tests hundreds of animations per query, and
+// one line each is what it moves. `flags`: bit 0 outgoing retain, 1 last ditch, 2 nonzero
+// incoming ball direction, 3 finite outgoing ball direction, 4 touching foot left.
+struct alignas(128) CrudeRecord {
+    Vec3 incomingBodyDirection, outDirectionRotated, inBallAdapted, ballDirectionNormalized;
+    float incomingVelocity, outgoingVelocity, turnAngle, inBodyFixAbsolute;
+    float incomingBodyAngles[6];
+    float bodyTurnAngle;
+    float incomingMaxDeviation, outgoingMaxDeviation, specialVar1, specialVar2;
+    int16_t index, animationType, incomingSpecialState, incomingRetainState, tripTypeRounded;
+    int8_t forcedFootWhich, currentFoot;
+    uint8_t flags;
+};
+static_assert(sizeof(CrudeRecord) == 128, "one crude record per cache line");
 constexpr int kFunctionSlots = 16;
 constexpr int kMaxAnimations = 1536;  // the tables hold 1452
 constexpr int kCameraHistory = 150;
@@ -272,6 +287,8 @@ struct Tables {
     const Vec3 *smoothed;
     const int16_t *fnAnims;   // animations accepted per function type, ascending
     const int32_t *fnOffset;  // kFunctionSlots + 1 entries
+    const CrudeRecord *crude;         // parallel to fnAnims
+    const CrudeRecord *crudeByIndex;  // one per animation
     const float *cameraWeights;
 };
 

@@ -299,6 +299,42 @@ void BuildSelection(AnimationTables &t) {
             if (CheckFunctionType(t.anims[i].animationType, fn)) t.fnAnims.push_back((int16_t)i);
     }
     t.fnOffset[kFunctionSlots] = (int32_t)t.fnAnims.size();
+    auto small = [](int v, int lo, int hi, const char *what) {
+        if (v < lo || v > hi) throw std::runtime_error(std::string("animation tables: a crude record cannot hold ") + what);
+        return v;
+    };
+    t.crudeByIndex.assign(t.anims.size(), CrudeRecord{});
+    for (size_t i = 0; i < t.anims.size(); i++) {
+        const Anim &a = t.anims[i];
+        const AnimDerived &d = t.derived[i];
+        const SelectionRecord &sr = t.selection[i];
+        CrudeRecord &r = t.crudeByIndex[i];
+        r.incomingBodyDirection = a.incomingBodyDirection;
+        r.outDirectionRotated = d.crudeOutDirectionRotated;
+        r.inBallAdapted = d.crudeInBallAdapted;
+        r.ballDirectionNormalized = d.crudeBallDirectionNormalized;
+        r.incomingVelocity = a.incomingVelocity;
+        r.outgoingVelocity = a.outgoingVelocity;
+        r.turnAngle = d.crudeTurnAngle;
+        r.inBodyFixAbsolute = d.crudeInBodyFixAbsolute;
+        for (int j = 0; j < 6; j++) r.incomingBodyAngles[j] = sr.incomingBodyAngles[j];
+        r.bodyTurnAngle = sr.bodyTurnAngle;
+        r.incomingMaxDeviation = d.incomingMaxDeviation;
+        r.outgoingMaxDeviation = d.outgoingMaxDeviation;
+        r.specialVar1 = a.specialVar1;
+        r.specialVar2 = a.specialVar2;
+        r.index = (int16_t)small((int)i, 0, 32767, "the animation index");
+        r.animationType = (int16_t)small(a.animationType, -32768, 32767, "the animation type");
+        r.incomingSpecialState = (int16_t)small(a.incomingSpecialState, -32768, 32767, "the special state");
+        r.incomingRetainState = (int16_t)small(a.incomingRetainState, -32768, 32767, "the retain state");
+        r.tripTypeRounded = (int16_t)small(d.tripTypeRounded, -32768, 32767, "the trip type");
+        r.forcedFootWhich = (int8_t)small(d.forcedFootWhich, -128, 127, "the forced foot");
+        r.currentFoot = (int8_t)small(a.currentFoot, -128, 127, "the current foot");
+        r.flags = (uint8_t)((d.outgoingRetainRaw ? 1 : 0) | (a.lastDitch ? 2 : 0) | (d.crudeInBallNonzero ? 4 : 0) |
+                            (sr.ballDirectionFinite ? 8 : 0) | (d.touchFootLeft ? 16 : 0));
+    }
+    t.crude.clear();
+    for (int16_t i : t.fnAnims) t.crude.push_back(t.crudeByIndex[i]);
     t.cameraWeights.assign(kCameraWeights, 0.0f);
     for (int n = 1; n <= kCameraHistory; n++)
         for (int i = 0; i < n; i++) t.cameraWeights[n * (n - 1) / 2 + i] = CameraWeight(i, n);
@@ -409,6 +445,8 @@ Tables AnimationTables::View() const {
     t.smoothed = smoothed.data();
     t.fnAnims = fnAnims.data();
     t.fnOffset = fnOffset.data();
+    t.crude = crude.data();
+    t.crudeByIndex = crudeByIndex.data();
     t.cameraWeights = cameraWeights.data();
     return t;
 }

@@ -60,6 +60,8 @@ BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> dev
         dt.smoothed = Upload(T.smoothed);
         dt.fnAnims = Upload(T.fnAnims);
         dt.fnOffset = Upload(T.fnOffset);
+        dt.crude = Upload(T.crude);
+        dt.crudeByIndex = Upload(T.crudeByIndex);
         dt.cameraWeights = Upload(T.cameraWeights);
         const Tables *dTables = Upload(&dt, 1);
 

@@ -303,6 +303,70 @@ HD int AllowedBodyDirectionEntry(const Vec3 &d) {
     return -1;
 }
 
+// The incoming-velocity test of the crude selection that GRF's selection sets for each function
+// type (humanoid_base.cpp, SelectAnimation): strict for movement and ball control, otherwise
+// lenient, with the dribble, sprint and linearity refinements of passes, shots and the rest.
+struct VelocityRule {
+    bool strict = false, noDribbleToIdle = false, noDribbleToSprint = false, forceLinearity = false;
+};
+HD VelocityRule FunctionVelocityRule(int fn) {
+    VelocityRule r;
+    if (fn == kFnMovement || fn == kFnBallControl) {
+        r.strict = true;
+    } else if (fn != kFnDeflect) {
+        r.noDribbleToSprint = true;
+        if (fn != kFnShortPass && fn != kFnLongPass && fn != kFnHighPass && fn != kFnShot) {
+            r.forceLinearity = true;
+            r.noDribbleToIdle = true;
+        }
+    }
+    return r;
+}
+HD bool VelocityRuleOf(const CrudeQuery &q, const VelocityRule &r) {
+    return q.incomingVelocityStrict == r.strict && q.incomingVelocityNoDribbleToIdle == r.noDribbleToIdle &&
+           q.incomingVelocityNoDribbleToSprint == r.noDribbleToSprint && q.incomingVelocityForceLinearity == r.forceLinearity;
+}
+// The incoming-velocity test of one animation (`q.byIncomingVelocity` set).
+HD bool IncomingVelocityPasses(const CrudeQuery &q, float incomingVelocity, float outgoingVelocity) {
+    int aIn = VelocityCat(incomingVelocity);
+    if (!q.incomingVelocityStrict) {
+        if (q.incomingVelocityNoDribbleToIdle && aIn == kVelIdle && q.incomingVelocity == kVelDribble) return false;
+        if (aIn == kVelIdle && q.incomingVelocity == kVelWalk) return false;
+        if (aIn == kVelIdle && q.incomingVelocity == kVelSprint) return false;
+        if (aIn == kVelDribble && q.incomingVelocity == kVelIdle) return false;
+        if (aIn == kVelWalk && q.incomingVelocity == kVelIdle) return false;
+        if (aIn == kVelSprint && q.incomingVelocity == kVelIdle) return false;
+        if (q.incomingVelocityNoDribbleToSprint && aIn == kVelSprint && q.incomingVelocity == kVelDribble) return false;
+        if (q.incomingVelocityForceLinearity) {
+            float ain = RangeVelocity(incomingVelocity), aout = RangeVelocity(outgoingVelocity);
+            float qin = VelocityFloat(q.incomingVelocity);
+            if (VelocityCat(ain) == kVelDribble) ain = kWalkVelocity;
+            if (VelocityCat(aout) == kVelDribble) aout = kWalkVelocity;
+            if (VelocityCat(qin) == kVelDribble) qin = kWalkVelocity;
+            float upper = (qin < aout) ? aout : qin;
+            float lower = (aout < qin) ? aout : qin;
+            if (ain > upper) return false;
+            if (ain < lower) return false;
+        }
+    } else if (aIn != q.incomingVelocity) {
+        return false;
+    }
+    return true;
+}
+// The canonical query of a function type's velocity rule, which the prefiltered record lists
+// (Tables::crudeVelocity) were built with.
+HD CrudeQuery VelocityRuleQuery(int fn, int incomingVelocity) {
+    CrudeQuery q;
+    const VelocityRule r = FunctionVelocityRule(fn);
+    q.byIncomingVelocity = true;
+    q.incomingVelocity = incomingVelocity;
+    q.incomingVelocityStrict = r.strict;
+    q.incomingVelocityNoDribbleToIdle = r.noDribbleToIdle;
+    q.incomingVelocityNoDribbleToSprint = r.noDribbleToSprint;
+    q.incomingVelocityForceLinearity = r.forceLinearity;
+    return q;
+}
+
 HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
     ENG_SCOPE(28);
     out.count = 0;
@@ -339,34 +403,12 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
     const Vec3 qOutNormalized = qOutNull ? Vec3(0) : qOut2D.Normalized(Vec3(0));
     // Each animation passes or fails on its own, so the lanes of the match test consecutive ones
     // and append the passing ones in list order.
+    bool velocityTested = false;
     auto accepts = [&](const CrudeRecord &r) -> bool {
         const int at = r.animationType;
         if (q.byFunctionType && !list && !CheckFunctionType(at, q.functionType)) return false;
-        if (q.byIncomingVelocity) {
-            int aIn = VelocityCat(r.incomingVelocity);
-            if (!q.incomingVelocityStrict) {
-                if (q.incomingVelocityNoDribbleToIdle && aIn == kVelIdle && q.incomingVelocity == kVelDribble) return false;
-                if (aIn == kVelIdle && q.incomingVelocity == kVelWalk) return false;
-                if (aIn == kVelIdle && q.incomingVelocity == kVelSprint) return false;
-                if (aIn == kVelDribble && q.incomingVelocity == kVelIdle) return false;
-                if (aIn == kVelWalk && q.incomingVelocity == kVelIdle) return false;
-                if (aIn == kVelSprint && q.incomingVelocity == kVelIdle) return false;
-                if (q.incomingVelocityNoDribbleToSprint && aIn == kVelSprint && q.incomingVelocity == kVelDribble) return false;
-                if (q.incomingVelocityForceLinearity) {
-                    float ain = RangeVelocity(r.incomingVelocity), aout = RangeVelocity(r.outgoingVelocity);
-                    float qin = VelocityFloat(q.incomingVelocity);
-                    if (VelocityCat(ain) == kVelDribble) ain = kWalkVelocity;
-                    if (VelocityCat(aout) == kVelDribble) aout = kWalkVelocity;
-                    if (VelocityCat(qin) == kVelDribble) qin = kWalkVelocity;
-                    float upper = (qin < aout) ? aout : qin;
-                    float lower = (aout < qin) ? aout : qin;
-                    if (ain > upper) return false;
-                    if (ain < lower) return false;
-                }
-            } else if (aIn != q.incomingVelocity) {
-                return false;
-            }
-        }
+        if (q.byIncomingVelocity && !velocityTested && !IncomingVelocityPasses(q, r.incomingVelocity, r.outgoingVelocity))
+            return false;
         if (q.byOutgoingVelocity && VelocityCat(r.outgoingVelocity) != q.outgoingVelocity) return false;
         if (q.bySide) {
             const Vec3 &aIn = r.incomingBodyDirection;
@@ -446,6 +488,15 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
         return true;
     };
     const CrudeRecord *records = list ? T.crude + T.fnOffset[q.functionType] : T.crudeByIndex;
+    // A query with its function type's velocity rule reads the animations of that type that pass
+    // the velocity test, prefiltered in list order.
+    if (list && q.byIncomingVelocity && q.incomingVelocity >= kVelIdle && q.incomingVelocity <= kVelSprint &&
+        VelocityRuleOf(q, FunctionVelocityRule(q.functionType))) {
+        const int slot = q.functionType * 4 + q.incomingVelocity;
+        records = T.crudeVelocity + T.crudeVelocityOffset[slot];
+        n = T.crudeVelocityOffset[slot + 1] - T.crudeVelocityOffset[slot];
+        velocityTested = true;
+    }
     for (int k0 = 0; k0 < n; k0 += kGroupLanes) {
         const int k = k0 + GroupRank();
         const bool keep = k < n && accepts(records[k]);
@@ -1511,25 +1562,12 @@ struct Selector {
         q.byIncomingVelocity = true;
         q.incomingVelocity = s.velocityCat;
         if (q.functionType != kFnMovement && q.incomingVelocity == kVelDribble) q.incomingVelocity = kVelWalk;
-        q.incomingVelocityStrict = false;
-        if (q.functionType != kFnMovement && q.functionType != kFnBallControl) {
-            q.incomingVelocityForceLinearity = false;
-            if (q.functionType != kFnDeflect) {
-                q.incomingVelocityNoDribbleToSprint = true;
-                if (q.functionType != kFnShortPass && q.functionType != kFnLongPass && q.functionType != kFnHighPass &&
-                    q.functionType != kFnShot) {
-                    q.incomingVelocityForceLinearity = true;
-                    q.incomingVelocityNoDribbleToIdle = true;
-                } else {
-                    q.incomingVelocityForceLinearity = false;
-                    q.incomingVelocityNoDribbleToIdle = false;
-                }
-            } else {
-                q.incomingVelocityNoDribbleToSprint = false;
-                q.incomingVelocityNoDribbleToIdle = false;
-            }
-        } else {
-            q.incomingVelocityStrict = true;
+        {
+            const VelocityRule rule = FunctionVelocityRule(q.functionType);
+            q.incomingVelocityStrict = rule.strict;
+            q.incomingVelocityNoDribbleToIdle = rule.noDribbleToIdle;
+            q.incomingVelocityNoDribbleToSprint = rule.noDribbleToSprint;
+            q.incomingVelocityForceLinearity = rule.forceLinearity;
         }
         q.byIncomingBodyDirection = true;
         q.incomingBodyDirection = s.relBodyDirectionVec;

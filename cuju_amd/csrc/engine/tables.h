@@ -289,6 +289,10 @@ struct Tables {
     const int32_t *fnOffset;  // kFunctionSlots + 1 entries
     const CrudeRecord *crude;         // parallel to fnAnims
     const CrudeRecord *crudeByIndex;  // one per animation
+    // Per function type and incoming velocity (slot fn * 4 + velocity), the records of the type
+    // that pass its velocity rule, in list order; kFunctionSlots * 4 + 1 offsets.
+    const CrudeRecord *crudeVelocity;
+    const int32_t *crudeVelocityOffset;
     const float *cameraWeights;
 };
 

@@ -335,6 +335,17 @@ void BuildSelection(AnimationTables &t) {
     }
     t.crude.clear();
     for (int16_t i : t.fnAnims) t.crude.push_back(t.crudeByIndex[i]);
+    t.crudeVelocity.clear();
+    t.crudeVelocityOffset.assign(kFunctionSlots * 4 + 1, 0);
+    for (int fn = 0; fn < kFunctionSlots; fn++)
+        for (int v = kVelIdle; v <= kVelSprint; v++) {
+            t.crudeVelocityOffset[fn * 4 + v] = (int32_t)t.crudeVelocity.size();
+            const CrudeQuery q = VelocityRuleQuery(fn, v);
+            for (int j = t.fnOffset[fn]; j < t.fnOffset[fn + 1]; j++)
+                if (IncomingVelocityPasses(q, t.crude[j].incomingVelocity, t.crude[j].outgoingVelocity))
+                    t.crudeVelocity.push_back(t.crude[j]);
+        }
+    t.crudeVelocityOffset[kFunctionSlots * 4] = (int32_t)t.crudeVelocity.size();
     t.cameraWeights.assign(kCameraWeights, 0.0f);
     for (int n = 1; n <= kCameraHistory; n++)
         for (int i = 0; i < n; i++) t.cameraWeights[n * (n - 1) / 2 + i] = CameraWeight(i, n);
@@ -447,6 +458,8 @@ Tables AnimationTables::View() const {
     t.fnOffset = fnOffset.data();
     t.crude = crude.data();
     t.crudeByIndex = crudeByIndex.data();
+    t.crudeVelocity = crudeVelocity.data();
+    t.crudeVelocityOffset = crudeVelocityOffset.data();
     t.cameraWeights = cameraWeights.data();
     return t;
 }

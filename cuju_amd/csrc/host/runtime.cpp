@@ -62,6 +62,8 @@ BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> dev
         dt.fnOffset = Upload(T.fnOffset);
         dt.crude = Upload(T.crude);
         dt.crudeByIndex = Upload(T.crudeByIndex);
+        dt.crudeVelocity = Upload(T.crudeVelocity);
+        dt.crudeVelocityOffset = Upload(T.crudeVelocityOffset);
         dt.cameraWeights = Upload(T.cameraWeights);
         const Tables *dTables = Upload(&dt, 1);
 

@@ -24,9 +24,40 @@ struct SinCosCoeffs {
     double hpi_inv, hpi, c0, c1, s1, c2, s2, c3, s3, c4;
 };
 
+// The tables the float routines index with a per-lane value. On the device each workgroup reads
+// them from its LDS, where StageMathTables copies them before any engine code runs; the host
+// reads the constant tables.
+#if ENG_DEVICE
+__shared__ uint64_t gLdsSinCosfCoefficients[28];
+__shared__ uint64_t gLdsPowfLog2Table[32];
+__shared__ uint64_t gLdsExp2fTable[32];
+#endif
+#if defined(__HIPCC__)
+// Every thread of the workgroup calls it at the start of a kernel.
+__device__ inline void StageMathTables() {
+#if ENG_DEVICE
+    for (int i = threadIdx.x; i < 32; i += blockDim.x) {
+        gLdsPowfLog2Table[i] = kPowfLog2Table[i];
+        gLdsExp2fTable[i] = kExp2fTable[i];
+        if (i < 28) gLdsSinCosfCoefficients[i] = kSinCosfCoefficients[i];
+    }
+    __syncthreads();
+#endif
+}
+#endif
+#if ENG_DEVICE
+#define LIBM_SINCOSF_TABLE gLdsSinCosfCoefficients
+#define LIBM_POWF_LOG2_TABLE gLdsPowfLog2Table
+#define LIBM_EXP2F_TABLE gLdsExp2fTable
+#else
+#define LIBM_SINCOSF_TABLE kSinCosfCoefficients
+#define LIBM_POWF_LOG2_TABLE kPowfLog2Table
+#define LIBM_EXP2F_TABLE kExp2fTable
+#endif
+
 HD SinCosCoeffs LoadSinCos(int set) {
     SinCosCoeffs k;
-    const uint64_t *t = kSinCosfCoefficients + 14 * set;
+    const uint64_t *t = LIBM_SINCOSF_TABLE + 14 * set;
     k.sign[0] = DoubleOf(t[0]);
     k.sign[1] = DoubleOf(t[1]);
     k.sign[2] = DoubleOf(t[2]);
@@ -42,6 +73,11 @@ HD SinCosCoeffs LoadSinCos(int set) {
     k.s3 = DoubleOf(t[12]);
     k.c4 = DoubleOf(t[13]);
     return k;
+}
+
+// sign[j] for j in 0..3, selected rather than indexed.
+HD double SignOf(const SinCosCoeffs &k, int j) {
+    return j == 0 ? k.sign[0] : j == 1 ? k.sign[1] : j == 2 ? k.sign[2] : k.sign[3];
 }
 
 // Exponent and top 3 mantissa bits of |x|.
@@ -100,13 +136,13 @@ HD bool SinCosReduce(float y, double *xr, double *sgn, int *n, int *set) {
     SinCosCoeffs k0 = LoadSinCos(0);
     if (top < Top12f(120.0f)) {
         *xr = ReduceFast((double)y, k0, n);
-        *sgn = k0.sign[*n & 3];
+        *sgn = SignOf(k0, *n & 3);
         *set = (*n & 2) ? 1 : 0;
     } else {
         uint32_t b = BitsOf(y);
         int s = b >> 31;
         *xr = ReduceLarge(b, n);
-        *sgn = k0.sign[(*n + s) & 3];
+        *sgn = SignOf(k0, (*n + s) & 3);
         *set = ((*n + s) & 2) ? 1 : 0;
     }
     return true;
@@ -142,6 +178,7 @@ HD float cosf(float y) {
 
 // sinf and cosf of one argument sharing the reduction; each result equals the single function's.
 HD SinCos sincosf(float y) {
+    ENG_SCOPE(50);
     uint32_t top = Top12f(y);
     if (top >= Top12f(INFINITY)) {
         float v = (y - y) / (y - y);
@@ -170,8 +207,8 @@ HD double Powf_Log2(uint32_t ix) {
     uint32_t top = tmp & 0xff800000;
     uint32_t iz = ix - top;
     int k = (int32_t)top >> 23;
-    double invc = DoubleOf(kPowfLog2Table[2 * i]);
-    double logc = DoubleOf(kPowfLog2Table[2 * i + 1]);
+    double invc = DoubleOf(LIBM_POWF_LOG2_TABLE[2 * i]);
+    double logc = DoubleOf(LIBM_POWF_LOG2_TABLE[2 * i + 1]);
     double z = (double)FloatOf(iz);
     double A0 = DoubleOf(kPowfLog2Poly[0]), A1 = DoubleOf(kPowfLog2Poly[1]),
            A2 = DoubleOf(kPowfLog2Poly[2]), A3 = DoubleOf(kPowfLog2Poly[3]),
@@ -194,7 +231,7 @@ HD float Powf_Exp2(double xd, uint32_t sign_bias) {
     uint64_t ki = BitsOf(kd);
     kd -= SHIFT;
     double r = xd - kd;
-    uint64_t t = kExp2fTable[ki % 32];
+    uint64_t t = LIBM_EXP2F_TABLE[ki % 32];
     uint64_t ski = ki + sign_bias;
     t += ski << (52 - 5);
     double s = DoubleOf(t);
@@ -223,6 +260,7 @@ HD bool SignalingF(float x) {
 }
 
 HD float powf(float x, float y) {
+    ENG_SCOPE(49);
     uint32_t sign_bias = 0;
     uint32_t ix = BitsOf(x), iy = BitsOf(y);
     if (ix - 0x00800000 >= 0x7f800000 - 0x00800000 || Powf_ZeroInfNan(iy)) {
@@ -517,11 +555,15 @@ HD float atanf(float x) {
     float s1 = z * (aT[0] + w * (aT[2] + w * (aT[4] + w * (aT[6] + w * (aT[8] + w * aT[10])))));
     float s2 = w * (aT[1] + w * (aT[3] + w * (aT[5] + w * (aT[7] + w * aT[9]))));
     if (id < 0) return x - x * (s1 + s2);
-    z = atanhi[id] - ((x * (s1 + s2) - atanlo[id]) - x);
+    // Selected rather than indexed, so the device reads no table memory.
+    const float hi = id == 0 ? atanhi[0] : id == 1 ? atanhi[1] : id == 2 ? atanhi[2] : atanhi[3];
+    const float lo = id == 0 ? atanlo[0] : id == 1 ? atanlo[1] : id == 2 ? atanlo[2] : atanlo[3];
+    z = hi - ((x * (s1 + s2) - lo) - x);
     return (hx < 0) ? -z : z;
 }
 
 HD float atan2f(float y, float x) {
+    ENG_SCOPE(51);
     const float tiny = 1.0e-30f, pi_o_4 = 7.8539818525e-01f, pi_o_2 = 1.5707963705e+00f,
                 pi = 3.1415927410e+00f, pi_lo = -8.7422776573e-08f;
     int32_t hx = (int32_t)BitsOf(x), hy = (int32_t)BitsOf(y);

@@ -46,6 +46,7 @@ __device__ int MatchIndex() { return (int)(blockIdx.x * (blockDim.x / kDeviceGro
 
 __global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) ResetKernel(eng::Batch b, const uint8_t *mask, const int64_t *seeds,
                                                                       const int32_t *reverse) {
+    eng::libm::StageMathTables();
     const int env = MatchIndex();
     if (env >= b.count) return;
     if (mask && !mask[env]) return;
@@ -53,12 +54,14 @@ __global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) ResetKernel(en
 }
 
 __global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) StepKernel(eng::Batch b, const int32_t *actions) {
+    eng::libm::StageMathTables();
     const int env = MatchIndex();
     if (env >= b.count) return;
     if (!eng::StepEnvironment(b, env, actions)) RecordFault(env);
 }
 
 __global__ void __launch_bounds__(kDeviceGroupLanes) OutputKernel(eng::Batch b, int env) {
+    eng::libm::StageMathTables();
     eng::WriteEnvironmentOutputs(b, env, false);
 }
 

@@ -521,41 +521,27 @@ HD float atanf(float x) {
                           -1.1111110449e-01f, 9.0908870101e-02f,  -7.6918758452e-02f,
                           6.6610731184e-02f,  -5.8335702866e-02f, 4.9768779427e-02f,
                           -3.6531571299e-02f, 1.6285819933e-02f};
-    int32_t hx = (int32_t)BitsOf(x), ix = hx & 0x7fffffff, id;
+    int32_t hx = (int32_t)BitsOf(x), ix = hx & 0x7fffffff;
     if (ix >= 0x4c000000) {
         if (ix > 0x7f800000) return x + x;
         if (hx > 0) return atanhi[3] + atanlo[3];
         return -atanhi[3] - atanlo[3];
     }
-    if (ix < 0x3ee00000) {
-        if (ix < 0x31000000) {
-            if (1.0e30f + x > 1.0f) return x;
-        }
-        id = -1;
-    } else {
-        x = fabsf(x);
-        if (ix < 0x3f980000) {
-            if (ix < 0x3f300000) {
-                id = 0;
-                x = (2.0f * x - 1.0f) / (2.0f + x);
-            } else {
-                id = 1;
-                x = (x - 1.0f) / (x + 1.0f);
-            }
-        } else if (ix < 0x401c0000) {
-            id = 2;
-            x = (x - 1.5f) / (1.0f + 1.5f * x);
-        } else {
-            id = 3;
-            x = -1.0f / x;
-        }
-    }
+    if (ix < 0x31000000 && 1.0e30f + x > 1.0f) return x;
+    // fdlibm's four argument reductions, (2|x| - 1) / (2 + |x|), (|x| - 1) / (|x| + 1),
+    // (|x| - 1.5) / (1 + 1.5|x|) and -1 / |x|, as one selected quotient: the same operations on
+    // each lane, so lanes in different ranges share one division.
+    const bool reduced = ix >= 0x3ee00000;
+    const int id = ix < 0x3f300000 ? 0 : ix < 0x3f980000 ? 1 : ix < 0x401c0000 ? 2 : 3;
+    const float ax = fabsf(x);
+    const float num = id == 0 ? 2.0f * ax - 1.0f : id == 1 ? ax - 1.0f : id == 2 ? ax - 1.5f : -1.0f;
+    const float den = id == 0 ? 2.0f + ax : id == 1 ? ax + 1.0f : id == 2 ? 1.0f + 1.5f * ax : ax;
+    if (reduced) x = num / den;
     float z = x * x;
     float w = z * z;
     float s1 = z * (aT[0] + w * (aT[2] + w * (aT[4] + w * (aT[6] + w * (aT[8] + w * aT[10])))));
     float s2 = w * (aT[1] + w * (aT[3] + w * (aT[5] + w * (aT[7] + w * aT[9]))));
-    if (id < 0) return x - x * (s1 + s2);
-    // Selected rather than indexed, so the device reads no table memory.
+    if (!reduced) return x - x * (s1 + s2);
     const float hi = id == 0 ? atanhi[0] : id == 1 ? atanhi[1] : id == 2 ? atanhi[2] : atanhi[3];
     const float lo = id == 0 ? atanlo[0] : id == 1 ? atanlo[1] : id == 2 ? atanlo[2] : atanlo[3];
     z = hi - ((x * (s1 + s2) - lo) - x);
@@ -616,16 +602,9 @@ HD float atan2f(float y, float x) {
         z = 0.0f;
     else
         z = atanf(fabsf(y / x));
-    switch (m) {
-        case 0:
-            return z;
-        case 1:
-            return FloatOf(BitsOf(z) ^ 0x80000000u);
-        case 2:
-            return pi - (z - pi_lo);
-        default:
-            return (z - pi_lo) - pi;
-    }
+    // The quadrant, selected rather than branched.
+    const float zl = z - pi_lo;
+    return m == 0 ? z : m == 1 ? FloatOf(BitsOf(z) ^ 0x80000000u) : m == 2 ? pi - zl : zl - pi;
 }
 
 // ---- asinf: glibc 2.39 flt-32 e_asinf.c ----------------------------------------------------------

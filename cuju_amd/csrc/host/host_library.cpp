@@ -138,3 +138,20 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_time_needed(co
         out[(size_t)i * 4 + 3] = b.optimistic;
     }
 }
+
+// The engine's float math routines on arrays, for tests against the C library: `which` is 0 sinf,
+// 1 cosf, 2 powf(x, y), 3 atan2f(x, y), 4 atanf, 5 acosf, 6 asinf.
+extern "C" __attribute__((visibility("default"))) void cuju_debug_libm(int which, const float *x, const float *y, float *out,
+                                                                         int count) {
+    for (int i = 0; i < count; i++) {
+        switch (which) {
+            case 0: out[i] = eng::libm::sinf(x[i]); break;
+            case 1: out[i] = eng::libm::cosf(x[i]); break;
+            case 2: out[i] = eng::libm::powf(x[i], y[i]); break;
+            case 3: out[i] = eng::libm::atan2f(x[i], y[i]); break;
+            case 4: out[i] = eng::libm::atanf(x[i]); break;
+            case 5: out[i] = eng::libm::acosf(x[i]); break;
+            default: out[i] = eng::libm::asinf(x[i]); break;
+        }
+    }
+}

@@ -367,6 +367,49 @@ HD CrudeQuery VelocityRuleQuery(int fn, int incomingVelocity) {
     return q;
 }
 
+// The incoming-body-direction test that GRF's selection sets for each function type: strict for
+// movement; otherwise lenient, with the linearity refinement except for deflections and ball
+// control.
+struct BodyRule {
+    bool strict = false, forceLinearity = false;
+};
+HD BodyRule FunctionBodyRule(int fn) {
+    BodyRule r;
+    if (fn != kFnMovement) r.forceLinearity = fn != kFnDeflect ? fn != kFnBallControl : false;
+    else r.strict = true;
+    return r;
+}
+// The incoming-body-direction test of one animation, for a query body direction given by its
+// absolute angles and either its allowed-direction entry (`entry` >= 0) or the direction itself.
+HD bool IncomingBodyPasses(const BodyRule &rule, int entry, const Vec3 &direction, float queryInBodyFixAbs,
+                           float queryIdleBodyAbs, const CrudeRecord &r) {
+    const float margin = 0.06f * PI;
+    if (VelocityCat(r.incomingVelocity) != kVelIdle) {
+        if (r.inBodyFixAbsolute > queryInBodyFixAbs + margin) return false;
+        const float qOff = entry >= 0 ? r.incomingBodyAngles[entry] : r.incomingBodyDirection.Angle2D(direction);
+        if (rule.strict) {
+            if (fabsf(qOff) > margin) return false;
+        } else {
+            if (fabsf(qOff) > 0.5f * PI + margin) return false;
+        }
+        if (rule.forceLinearity) {
+            float bt = r.bodyTurnAngle;
+            if ((bt > margin && qOff > margin) || (bt < -margin && qOff < -margin)) return false;
+            if (fabsf(bt) + fabsf(qOff) > PI + margin) return false;
+        }
+    } else {
+        if (rule.strict) {
+            if (queryIdleBodyAbs > margin) return false;
+        } else {
+            if (queryIdleBodyAbs > 0.25f * PI + margin) return false;
+        }
+    }
+    return true;
+}
+// Allowed body-direction entries of a query (AllowedBodyDirectionEntry), which index the
+// body-prefiltered record lists (Tables::crudeBody).
+constexpr int kBodyEntries = 6;
+
 HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
     ENG_SCOPE(28);
     out.count = 0;
@@ -403,7 +446,10 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
     const Vec3 qOutNormalized = qOutNull ? Vec3(0) : qOut2D.Normalized(Vec3(0));
     // Each animation passes or fails on its own, so the lanes of the match test consecutive ones
     // and append the passing ones in list order.
-    bool velocityTested = false;
+    bool velocityTested = false, bodyTested = false;
+    BodyRule bodyRule;
+    bodyRule.strict = q.incomingBodyDirectionStrict;
+    bodyRule.forceLinearity = q.incomingBodyDirectionForceLinearity;
     auto accepts = [&](const CrudeRecord &r) -> bool {
         const int at = r.animationType;
         if (q.byFunctionType && !list && !CheckFunctionType(at, q.functionType)) return false;
@@ -432,29 +478,9 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
             if ((!retains && q.pickupBall) || (retains && !q.pickupBall)) return false;
         }
         if (!q.allowLastDitch && (r.flags & 2)) return false;
-        if (byBody) {
-            if (VelocityCat(r.incomingVelocity) != kVelIdle) {
-                if (r.inBodyFixAbsolute > queryInBodyFixAbs + margin) return false;
-                const float qOff = queryBodyEntry >= 0 ? r.incomingBodyAngles[queryBodyEntry]
-                                                       : r.incomingBodyDirection.Angle2D(q.incomingBodyDirection);
-                if (q.incomingBodyDirectionStrict) {
-                    if (fabsf(qOff) > margin) return false;
-                } else {
-                    if (fabsf(qOff) > 0.5f * PI + margin) return false;
-                }
-                if (q.incomingBodyDirectionForceLinearity) {
-                    float bt = r.bodyTurnAngle;
-                    if ((bt > margin && qOff > margin) || (bt < -margin && qOff < -margin)) return false;
-                    if (fabsf(bt) + fabsf(qOff) > PI + margin) return false;
-                }
-            } else {
-                if (q.incomingBodyDirectionStrict) {
-                    if (queryIdleBodyAbs > margin) return false;
-                } else {
-                    if (queryIdleBodyAbs > 0.25f * PI + margin) return false;
-                }
-            }
-        }
+        if (byBody && !bodyTested &&
+            !IncomingBodyPasses(bodyRule, queryBodyEntry, q.incomingBodyDirection, queryInBodyFixAbs, queryIdleBodyAbs, r))
+            return false;
         if (q.byIncomingBallDirection && (r.flags & 4) && qInBallNonzero) {
             float ang = fabsf(qInBallAdapted.Angle2D(r.inBallAdapted));
             float maxDev = r.incomingMaxDeviation;
@@ -496,6 +522,16 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
         records = T.crudeVelocity + T.crudeVelocityOffset[slot];
         n = T.crudeVelocityOffset[slot + 1] - T.crudeVelocityOffset[slot];
         velocityTested = true;
+        // With its function type's body rule and an allowed body direction too, the list is
+        // prefiltered by the body test as well.
+        const BodyRule canonical = FunctionBodyRule(q.functionType);
+        if (q.byIncomingBodyDirection && queryBodyEntry >= 0 && canonical.strict == bodyRule.strict &&
+            canonical.forceLinearity == bodyRule.forceLinearity) {
+            const int body = slot * kBodyEntries + queryBodyEntry;
+            records = T.crudeBody + T.crudeBodyOffset[body];
+            n = T.crudeBodyOffset[body + 1] - T.crudeBodyOffset[body];
+            bodyTested = true;
+        }
     }
     for (int k0 = 0; k0 < n; k0 += kGroupLanes) {
         const int k = k0 + GroupRank();
@@ -1571,11 +1607,10 @@ struct Selector {
         }
         q.byIncomingBodyDirection = true;
         q.incomingBodyDirection = s.relBodyDirectionVec;
-        if (q.functionType != kFnMovement) {
-            q.incomingBodyDirectionStrict = false;
-            q.incomingBodyDirectionForceLinearity = q.functionType != kFnDeflect ? q.functionType != kFnBallControl : false;
-        } else {
-            q.incomingBodyDirectionStrict = true;
+        {
+            const BodyRule rule = FunctionBodyRule(q.functionType);
+            q.incomingBodyDirectionStrict = rule.strict;
+            q.incomingBodyDirectionForceLinearity = rule.forceLinearity;
         }
         q.bySide = false;
         if (cmd.useDesiredLookAt && (current.outgoingSpecialState == kStrEmpty) && !retainerIsMe) {

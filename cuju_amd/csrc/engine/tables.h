@@ -293,6 +293,10 @@ struct Tables {
     // that pass its velocity rule, in list order; kFunctionSlots * 4 + 1 offsets.
     const CrudeRecord *crudeVelocity;
     const int32_t *crudeVelocityOffset;
+    // The same lists prefiltered by the body rule of the function type for each allowed body
+    // direction (slot (fn * 4 + velocity) * 6 + entry); kFunctionSlots * 4 * 6 + 1 offsets.
+    const CrudeRecord *crudeBody;
+    const int32_t *crudeBodyOffset;
     const float *cameraWeights;
 };
 

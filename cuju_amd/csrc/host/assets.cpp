@@ -346,6 +346,23 @@ void BuildSelection(AnimationTables &t) {
                     t.crudeVelocity.push_back(t.crude[j]);
         }
     t.crudeVelocityOffset[kFunctionSlots * 4] = (int32_t)t.crudeVelocity.size();
+    t.crudeBody.clear();
+    t.crudeBodyOffset.assign(kFunctionSlots * 4 * kBodyEntries + 1, 0);
+    for (int slot = 0; slot < kFunctionSlots * 4; slot++) {
+        const int fn = slot / 4, v = slot % 4;
+        const BodyRule rule = FunctionBodyRule(fn);
+        for (int e = 0; e < kBodyEntries; e++) {
+            t.crudeBodyOffset[slot * kBodyEntries + e] = (int32_t)t.crudeBody.size();
+            for (int j = t.crudeVelocityOffset[slot]; j < t.crudeVelocityOffset[slot + 1]; j++) {
+                const CrudeRecord &r = t.crudeVelocity[j];
+                // An idle query velocity turns the body test off (CrudeSelection, byBody).
+                if (v == kVelIdle || IncomingBodyPasses(rule, e, AllowedBodyDir(e), AllowedBodyFixAbsolute(e),
+                                                        AllowedBodyIdleAbsolute(e), r))
+                    t.crudeBody.push_back(r);
+            }
+        }
+    }
+    t.crudeBodyOffset[kFunctionSlots * 4 * kBodyEntries] = (int32_t)t.crudeBody.size();
     t.cameraWeights.assign(kCameraWeights, 0.0f);
     for (int n = 1; n <= kCameraHistory; n++)
         for (int i = 0; i < n; i++) t.cameraWeights[n * (n - 1) / 2 + i] = CameraWeight(i, n);
@@ -460,6 +477,8 @@ Tables AnimationTables::View() const {
     t.crudeByIndex = crudeByIndex.data();
     t.crudeVelocity = crudeVelocity.data();
     t.crudeVelocityOffset = crudeVelocityOffset.data();
+    t.crudeBody = crudeBody.data();
+    t.crudeBodyOffset = crudeBodyOffset.data();
     t.cameraWeights = cameraWeights.data();
     return t;
 }

@@ -33,8 +33,8 @@ struct AnimationTables {
     std::vector<Vec3> smoothed;  // parallels `positions`
     std::vector<int16_t> fnAnims;
     std::vector<int32_t> fnOffset;
-    std::vector<CrudeRecord> crude, crudeByIndex, crudeVelocity;
-    std::vector<int32_t> crudeVelocityOffset;
+    std::vector<CrudeRecord> crude, crudeByIndex, crudeVelocity, crudeBody;
+    std::vector<int32_t> crudeVelocityOffset, crudeBodyOffset;
     std::vector<float> cameraWeights;
     // Tables whose pointers index the vectors above.
     Tables View() const;

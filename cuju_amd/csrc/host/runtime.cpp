@@ -64,6 +64,8 @@ BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> dev
         dt.crudeByIndex = Upload(T.crudeByIndex);
         dt.crudeVelocity = Upload(T.crudeVelocity);
         dt.crudeVelocityOffset = Upload(T.crudeVelocityOffset);
+        dt.crudeBody = Upload(T.crudeBody);
+        dt.crudeBodyOffset = Upload(T.crudeBodyOffset);
         dt.cameraWeights = Upload(T.cameraWeights);
         const Tables *dTables = Upload(&dt, 1);
 

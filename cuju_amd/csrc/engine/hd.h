@@ -152,6 +152,15 @@ HD float GroupShuffle(float v, int rank) {
     memcpy(&r, &b, 4);
     return r;
 }
+HD double GroupShuffle(double v, int rank) {
+    uint64_t b;
+    memcpy(&b, &v, 8);
+    const uint32_t lo = GroupShuffle((uint32_t)b, rank), hi = GroupShuffle((uint32_t)(b >> 32), rank);
+    b = ((uint64_t)hi << 32) | lo;
+    double r;
+    memcpy(&r, &b, 8);
+    return r;
+}
 // Orders the group's memory operations: what a lane stored before the call is what every lane of
 // the group loads after it (one wavefront's memory operations complete in order).
 HD void GroupSync() {

@@ -741,6 +741,54 @@ struct Selector {
     HD void SortBaseAnimation(AList &l) {
         Sort(l, [&](int i) { return A(i).baseAnimation ? 0 : 1; });
     }
+    // The position of the element that a stable sort of `l` by `key`, followed (with `byBase`) by
+    // the stable sort by base animation, puts first: the smallest (base key, key), the earliest on
+    // ties. The lanes of the match scan every fourth element and combine their bests.
+    template <class KeyFn>
+    HD int StableFirst(const AList &l, KeyFn key, bool byBase) {
+        double bestKey = 0, bestBase = 0;
+        int best = -1;
+        for (int i = GroupRank(); i < l.count; i += kGroupLanes) {
+            const double k = (double)key((int)l[i]);
+            const double b = byBase ? (A(l[i]).baseAnimation ? 0 : 1) : 0;
+#if !ENG_DEVICE
+            if (k != k) Fatal("an animation sort key is NaN");
+#endif
+            if (best < 0 || b < bestBase || (b == bestBase && k < bestKey)) {
+                best = i;
+                bestKey = k;
+                bestBase = b;
+            }
+        }
+        for (int r = 1; r < kGroupLanes; r++) {
+            const int other = GroupShuffle((int32_t)best, r);
+            const double ok = GroupShuffle(bestKey, r), ob = GroupShuffle(bestBase, r);
+            if (other >= 0 && (best < 0 || ob < bestBase || (ob == bestBase && (ok < bestKey || (ok == bestKey && other < best))))) {
+                best = other;
+                bestKey = ok;
+                bestBase = ob;
+            }
+        }
+        // Every lane now holds the group's first; lane 0's combination is taken for all.
+        return GroupShuffle((int32_t)best, 0);
+    }
+    // Keeps, in order, the elements of `l` for which `keep` holds (the lanes of the match test
+    // consecutive elements and compact the list in place).
+    template <class KeepFn>
+    HD void KeepInOrder(AList &l, KeepFn keep) {
+        int kept = 0;
+        for (int k0 = 0; k0 < l.count; k0 += kGroupLanes) {
+            const int k = k0 + GroupRank();
+            const int16_t e = k < l.count ? l[k] : 0;
+            const bool ok = k < l.count && keep((int)e);
+            const uint32_t mask = GroupBallot(ok);
+            GroupSync();
+            if (ok) l.e[kept + PopCount(mask & ((1u << GroupRank()) - 1u))] = e;
+            kept += PopCount(mask);
+            GroupSync();
+        }
+        l.count = kept;
+    }
     // The first element after a chain of stable sorts: the smallest key tuple, the earliest on ties.
     template <class KeysFn>
     HD int FirstOfSortChain(const AList &l, int keyCount, KeysFn keys) {
@@ -779,47 +827,54 @@ struct Selector {
     HDN void KeepBestDirectionAnimations(AList &l, const PlayerCommand &cmd, bool strict, float allowedAngle = 0,
                                          int allowedVelocitySteps = 0, int forcedQuadrant = -1) {
         ENG_SCOPE(32);
+        if (l.empty()) return;
         int bestQ = forcedQuadrant;
+        auto keeps = [&](int ai) {
+            const Anim &a = A(ai);
+            if (strict) return a.quadrantID == bestQ;
+            const Quadrant &bq = c.t->quadrants[bestQ];
+            const Quadrant &qd = c.t->quadrants[a.quadrantID];
+            bool keep = true;
+            if (!a.lastDitch) {
+                int dv = GetVelocityID(qd.velocity, true) - GetVelocityID(bq.velocity, true);
+                if ((dv < 0 ? -dv : dv) > allowedVelocitySteps) keep = false;
+            }
+            if (fabsf(qd.angle.value() - bq.angle.value()) > allowedAngle) keep = false;
+            return keep;
+        };
         if (bestQ == -1) {
-            Sort(l, [&](int i) { return MovementSimilarityKey(i); });
-            if (strict && cmd.desiredFunctionType != kFnMovement) SortBaseAnimation(l);
-            bestQ = A(l[0]).quadrantID;
+            // GRF sorts by similarity (then base animation), takes the first element's quadrant
+            // and keeps the sorted elements near it. The first element passes its own test and the
+            // test depends on the element alone, so filtering first and sorting the kept ones
+            // gives the same list.
+            auto key = [&](int i) { return MovementSimilarityKey(i); };
+            const bool byBase = strict && cmd.desiredFunctionType != kFnMovement;
+            bestQ = A(l[StableFirst(l, key, byBase)]).quadrantID;
+            KeepInOrder(l, keeps);
+            Sort(l, key);
+            if (byBase) SortBaseAnimation(l);
+            return;
         }
         int kept = 1;
-        for (int k = 1; k < l.count; k++) {
-            const Anim &a = A(l[k]);
-            bool keep;
-            if (strict) {
-                keep = a.quadrantID == bestQ;
-            } else {
-                const Quadrant &bq = c.t->quadrants[bestQ];
-                const Quadrant &qd = c.t->quadrants[a.quadrantID];
-                keep = true;
-                if (!a.lastDitch) {
-                    int dv = GetVelocityID(qd.velocity, true) - GetVelocityID(bq.velocity, true);
-                    if ((dv < 0 ? -dv : dv) > allowedVelocitySteps) keep = false;
-                }
-                if (fabsf(qd.angle.value() - bq.angle.value()) > allowedAngle) keep = false;
-            }
-            if (keep) l[kept++] = l[k];
-        }
+        for (int k = 1; k < l.count; k++)
+            if (keeps(l[k])) l[kept++] = l[k];
         l.count = kept;
     }
 
     HDN void KeepBestBodyDirectionAnimations(AList &l, const PlayerCommand &cmd, bool strict, float allowedAngle = 0) {
         ENG_SCOPE(32);
+        if (l.empty()) return;
         Vec3 relLookAt;
         if (l.count > 1) relLookAt = RelativeLookAt();
-        Sort(l, [&](int i) { return DirectionSimilarityRating(A(i), pred, relLookAt); });
-        if (strict && cmd.desiredFunctionType != kFnMovement) SortBaseAnimation(l);
-        float bestLook = LookAngle(l[0]);
-        int kept = 1;
-        for (int k = 1; k < l.count; k++) {
-            float la = LookAngle(l[k]);
-            float allowed = strict ? 0.06f * PI : allowedAngle;
-            if (fabsf(la - bestLook) <= allowed) l[kept++] = l[k];
-        }
-        l.count = kept;
+        // As in KeepBestDirectionAnimations: the first element of GRF's sorted list passes its
+        // own test, so the kept elements are filtered first and sorted after.
+        auto key = [&](int i) { return DirectionSimilarityRating(A(i), pred, relLookAt); };
+        const bool byBase = strict && cmd.desiredFunctionType != kFnMovement;
+        const float bestLook = LookAngle(l[StableFirst(l, key, byBase)]);
+        const float allowed = strict ? 0.06f * PI : allowedAngle;
+        KeepInOrder(l, [&](int ai) { return fabsf(LookAngle(ai) - bestLook) <= allowed; });
+        Sort(l, key);
+        if (byBase) SortBaseAnimation(l);
     }
 
     HDN int GetIdleMovementAnimationID() {

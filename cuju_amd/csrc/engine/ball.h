@@ -393,6 +393,82 @@ HDN TimeNeeded WalkTimeNeeded(const TimeWalk &wk, const Vec3 &pos, const Vec3 &m
     return r;
 }
 
+// GetTimeNeededMs for the targets of one player (position, movement and velocity fixed), with a
+// shortcut for targets the walk cannot reach (ai_time.h:133). Over its 70 steps the walk moves at
+// most 0.355 |movement| (in the plane) from where it starts, and its optimistic radius grows to
+// at most 0.9 + 0.345 amv. A target farther from the start than their sum, with a margin over the
+// rounding of the walk, fails every step's test. Its result then follows from the step at which
+// the walk stops: one step past the time limit, or the end of the bias at 700 ms. The walk's
+// state there is the same for every target of a moving player, and is computed once. Every other
+// target runs GetTimeNeededMs itself, so the results are GetTimeNeededMs's.
+struct TimeNeededScan {
+    Vec3 pos, mov, start, end;
+    float maxVel, amv, reach, endUsual = 0, endOptimistic = 0;
+    bool moving, ended = false;
+
+    HD TimeNeededScan(const Vec3 &p, const Vec3 &m, float velocity) : pos(p), mov(m), maxVel(velocity) {
+        amv = maxVel * 0.94f;
+        moving = mov.Length() > kIdleDribbleSwitch;
+        start = pos;
+        if (moving) {
+            start += mov.Normalized() * 0.1f;
+            start += mov * 0.01f;
+        }
+        reach = (sqrtf(mov.v[0] * mov.v[0] + mov.v[1] * mov.v[1]) * 0.36f + 0.9f + 0.35f * amv) * 1.001f + 0.01f;
+    }
+    // The walk of a moving player to the end of the bias, as GetTimeNeededMs steps it.
+    HD void WalkToEnd() {
+        Vec3 cur = start;
+        float usualR = 0.28f, optR = 0.9f;
+        const uint32_t step = 10;
+        for (uint32_t k = 0; k < kTimeWalkSteps; k++) {
+            const float bias = TimeNeededBias(k);
+            const float cx = mov.v[0] * (1.0f - bias), cy = mov.v[1] * (1.0f - bias);
+            cur.v[0] += cx * step * 0.001f;
+            cur.v[1] += cy * step * 0.001f;
+            usualR += amv * bias * step * 0.001f;
+            optR += amv * bias * step * 0.001f;
+        }
+        end = cur;
+        endUsual = usualR;
+        endOptimistic = optR;
+        ended = true;
+    }
+    HD TimeNeeded Get(const Vec3 &target, bool precise, uint32_t maxTime) {
+        if ((pos - target).Length() <= (precise ? 48.0f : 16.0f)) {
+            const Vec3 from = moving ? start : pos + (target - pos).Normalized(0) * 0.1f;
+            const float margin = (fabsf(from.v[0]) + fabsf(from.v[1])) * 1e-5f;
+            if ((target - from).Length() > reach + margin) {
+                const bool limited = maxTime != (uint32_t)-1;
+                TimeNeeded r;
+                if (limited && maxTime < (kTimeWalkSteps - 1) * 10) {
+                    // Stopped by the limit one step past it, the optimistic time found there.
+                    const uint32_t time = (maxTime / 10 + 1) * 10;
+                    const uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
+                    r.optimistic = time;
+                    r.usual = def > ext ? def : ext;
+                    return r;
+                }
+                if (moving) {
+                    if (!ended) WalkToEnd();
+                    const uint32_t time = kTimeWalkSteps * 10;
+                    const float d = (target - end).Length();
+                    const float rem = Clamp(d - endUsual, 0.0f, 100000.0f), ro = Clamp(d - endOptimistic, 0.0f, 100000.0f);
+                    r.usual = TruncToUint32((float)time + (rem / amv) * 1000);
+                    r.optimistic = TruncToUint32((float)time + (ro / amv) * 1000);
+                    if (limited && time > maxTime) {
+                        const uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
+                        r.usual = def > ext ? def : ext;
+                        r.optimistic = r.usual;
+                    }
+                    return r;
+                }
+            }
+        }
+        return GetTimeNeededMs(pos, mov, target, maxVel, precise, maxTime);
+    }
+};
+
 struct ScanResult {
     uint32_t timeToBall, timeToBallOptimistic;
 };
@@ -417,10 +493,11 @@ HDN ScanResult PossessionScan(const Vec3 *pred, bool flip, const Vec3 &pos, cons
     s.timeToBallOptimistic = s.timeToBall;
     bool refine = false;
     uint32_t stepMs = 10, prev = 0;
+    TimeNeededScan times(pos, mov, maxVel);
     for (uint32_t ms = start; ms < kBallPredictionSpanMs; ms += stepMs) {
         if (PredFlip(pred, flip, ms).v[2] < 1.5f) {
             const Vec3 target = PredFlip(pred, flip, ms).Get2D();
-            TimeNeeded r = GetTimeNeededMs(pos, mov, target, maxVel, precise, ms);
+            TimeNeeded r = times.Get(target, precise, ms);
             if (r.optimistic <= ms && ms < s.timeToBallOptimistic) s.timeToBallOptimistic = ms;
             if (r.usual <= ms) {
                 if (!refine) {

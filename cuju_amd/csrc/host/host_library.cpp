@@ -116,10 +116,11 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_episode_seeds(
     for (int i = 0; i < count; i++) out[i] = eng::DrawEpisodeSeed(*g);
 }
 
-// GRF's time-to-target estimate for `count` cases, directly and along the shared walk (both usual
-// and optimistic times per case, direct first); tests compare the two.
+// GRF's time-to-target estimate for `count` cases: directly, along the shared walk, and by the
+// possession scan's shortcut (usual and optimistic times of each, direct first); tests compare them.
 extern "C" __attribute__((visibility("default"))) void cuju_debug_time_needed(const float *cases, int count, unsigned int *out) {
     auto walk = std::make_unique<eng::TimeWalk>();
+    std::unique_ptr<eng::TimeNeededScan> scan;
     for (int i = 0; i < count; i++) {
         const float *q = cases + (size_t)i * 12;
         const eng::Vec3 pos(q[0], q[1], q[2]), mov(q[3], q[4], q[5]), target(q[6], q[7], q[8]);
@@ -132,10 +133,16 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_time_needed(co
             eng::BuildTimeWalk(*walk, pos, mov, maxVel);
             b = eng::WalkTimeNeeded(*walk, pos, mov, target, maxVel, precise, maxTime, false);
         }
-        out[(size_t)i * 4 + 0] = a.usual;
-        out[(size_t)i * 4 + 1] = a.optimistic;
-        out[(size_t)i * 4 + 2] = b.usual;
-        out[(size_t)i * 4 + 3] = b.optimistic;
+        // Consecutive cases of one player share a scan, as the targets of a possession scan do.
+        if (!scan || !(scan->pos == pos) || !(scan->mov == mov) || scan->maxVel != maxVel)
+            scan = std::make_unique<eng::TimeNeededScan>(pos, mov, maxVel);
+        const eng::TimeNeeded c = scan->Get(target, precise, maxTime);
+        out[(size_t)i * 6 + 0] = a.usual;
+        out[(size_t)i * 6 + 1] = a.optimistic;
+        out[(size_t)i * 6 + 2] = b.usual;
+        out[(size_t)i * 6 + 3] = b.optimistic;
+        out[(size_t)i * 6 + 4] = c.usual;
+        out[(size_t)i * 6 + 5] = c.optimistic;
     }
 }
 

@@ -128,23 +128,36 @@ def test_set_state_refuses_another_scenario(reference_library, host_library):
 
 
 def test_time_walk_matches_the_direct_estimate(host_library):
-    """The time-to-target estimate along the precomputed walk equals GRF's direct loop
-    (ai_time.h:102-409) on random players, movements, targets and time limits, near and far."""
+    """The time-to-target estimate along the precomputed walk, and the possession scan's shortcut
+    for targets the walk cannot reach, equal GRF's direct loop (ai_time.h:102-409) on random
+    players, movements, targets and time limits, near and far. Each player takes eight targets in
+    a row, as a possession scan does, and a third of the targets sit within a metre of the
+    shortcut's bound."""
     lib = ctypes.CDLL(host_library)
     rng = np.random.default_rng(5)
-    n = 200_000
-    pos = np.column_stack([rng.uniform(-55, 55, n), rng.uniform(-36, 36, n), rng.choice([0.0, 0.1], n)])
-    speed = rng.choice([0.0, 1.0, 1.8, 1.80001, 3.0, 6.0, 9.0], n) * rng.uniform(0.5, 1.5, n)
-    angle = rng.uniform(-np.pi, np.pi, n)
-    mov = np.column_stack([speed * np.cos(angle), speed * np.sin(angle), rng.choice([0.0, 0.3], n)])
+    players, per = 25_000, 8
+    n = players * per
+    pos = np.column_stack([rng.uniform(-55, 55, players), rng.uniform(-36, 36, players), rng.choice([0.0, 0.1], players)])
+    speed = rng.choice([0.0, 1.0, 1.8, 1.80001, 3.0, 6.0, 9.0], players) * rng.uniform(0.5, 1.5, players)
+    angle = rng.uniform(-np.pi, np.pi, players)
+    mov = np.column_stack([speed * np.cos(angle), speed * np.sin(angle), rng.choice([0.0, 0.3], players)])
+    velocity = rng.uniform(5, 9.5, players)
+    precise = rng.integers(0, 2, players)
+    pos, mov, velocity, precise = (np.repeat(x, per, axis=0) for x in (pos, mov, velocity, precise))
+    # The shortcut's bound: 0.36 |movement| + 0.9 + 0.35 (0.94 maximum velocity), from the start.
+    bound = np.linalg.norm(mov[:, :2], axis=1) * 0.36 + 0.9 + 0.35 * 0.94 * velocity
     reach = rng.choice([0.5, 3.0, 10.0, 20.0, 40.0, 60.0], n) * rng.uniform(0, 1, n)
+    near = rng.uniform(size=n) < 1 / 3
+    reach[near] = bound[near] + rng.uniform(-0.5, 0.5, near.sum())
     turn = rng.uniform(-np.pi, np.pi, n)
     target = np.column_stack([pos[:, 0] + reach * np.cos(turn), pos[:, 1] + reach * np.sin(turn), np.zeros(n)])
     limit = np.where(rng.uniform(size=n) < 0.3, -1.0, rng.integers(0, 3000, n).astype(float))
-    cases = np.column_stack([pos, mov, target, rng.uniform(5, 9.5, n), rng.integers(0, 2, n), limit]).astype(np.float32)
-    out = np.zeros((n, 4), dtype=np.uint32)
+    limit[rng.uniform(size=n) < 0.1] = rng.choice([680.0, 689.0, 690.0, 695.0, 699.0, 700.0])
+    cases = np.column_stack([pos, mov, target, velocity, precise, limit]).astype(np.float32)
+    out = np.zeros((n, 6), dtype=np.uint32)
     lib.cuju_debug_time_needed(ctypes.c_void_p(cases.ctypes.data), n, ctypes.c_void_p(out.ctypes.data))
-    assert np.array_equal(out[:, :2], out[:, 2:])
+    assert np.array_equal(out[:, :2], out[:, 2:4])
+    assert np.array_equal(out[:, :2], out[:, 4:])
     walked = np.linalg.norm(mov[:, :2], axis=1) > 2.0
     assert walked.sum() > n // 3
 

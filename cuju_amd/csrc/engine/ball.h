@@ -398,9 +398,10 @@ HDN TimeNeeded WalkTimeNeeded(const TimeWalk &wk, const Vec3 &pos, const Vec3 &m
 // most 0.355 |movement| (in the plane) from where it starts, and its optimistic radius grows to
 // at most 0.9 + 0.345 amv. A target farther from the start than their sum, with a margin over the
 // rounding of the walk, fails every step's test. Its result then follows from the step at which
-// the walk stops: one step past the time limit, or the end of the bias at 700 ms. The walk's
-// state there is the same for every target of a moving player, and is computed once. Every other
-// target runs GetTimeNeededMs itself, so the results are GetTimeNeededMs's.
+// the walk stops: one step past the time limit, or the end of the bias at 700 ms. The radii there
+// are the same for every target, and so is the position for a moving player; an idle player
+// starts a tenth of a metre towards the target, so its position is walked per target, without
+// the tests. Every other target runs GetTimeNeededMs itself, so the results are GetTimeNeededMs's.
 struct TimeNeededScan {
     Vec3 pos, mov, start, end;
     float maxVel, amv, reach, endUsual = 0, endOptimistic = 0;
@@ -416,22 +417,30 @@ struct TimeNeededScan {
         }
         reach = (sqrtf(mov.v[0] * mov.v[0] + mov.v[1] * mov.v[1]) * 0.36f + 0.9f + 0.35f * amv) * 1.001f + 0.01f;
     }
-    // The walk of a moving player to the end of the bias, as GetTimeNeededMs steps it.
-    HD void WalkToEnd() {
-        Vec3 cur = start;
-        float usualR = 0.28f, optR = 0.9f;
+    // The position after the 70 steps from `from`, as GetTimeNeededMs steps it.
+    HD Vec3 WalkFrom(const Vec3 &from) const {
+        Vec3 cur = from;
         const uint32_t step = 10;
         for (uint32_t k = 0; k < kTimeWalkSteps; k++) {
             const float bias = TimeNeededBias(k);
             const float cx = mov.v[0] * (1.0f - bias), cy = mov.v[1] * (1.0f - bias);
             cur.v[0] += cx * step * 0.001f;
             cur.v[1] += cy * step * 0.001f;
+        }
+        return cur;
+    }
+    // The radii after the 70 steps, and a moving player's position.
+    HD void WalkToEnd() {
+        float usualR = 0.28f, optR = 0.9f;
+        const uint32_t step = 10;
+        for (uint32_t k = 0; k < kTimeWalkSteps; k++) {
+            const float bias = TimeNeededBias(k);
             usualR += amv * bias * step * 0.001f;
             optR += amv * bias * step * 0.001f;
         }
-        end = cur;
         endUsual = usualR;
         endOptimistic = optR;
+        if (moving) end = WalkFrom(start);
         ended = true;
     }
     HD TimeNeeded Get(const Vec3 &target, bool precise, uint32_t maxTime) {
@@ -449,20 +458,18 @@ struct TimeNeededScan {
                     r.usual = def > ext ? def : ext;
                     return r;
                 }
-                if (moving) {
-                    if (!ended) WalkToEnd();
-                    const uint32_t time = kTimeWalkSteps * 10;
-                    const float d = (target - end).Length();
-                    const float rem = Clamp(d - endUsual, 0.0f, 100000.0f), ro = Clamp(d - endOptimistic, 0.0f, 100000.0f);
-                    r.usual = TruncToUint32((float)time + (rem / amv) * 1000);
-                    r.optimistic = TruncToUint32((float)time + (ro / amv) * 1000);
-                    if (limited && time > maxTime) {
-                        const uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
-                        r.usual = def > ext ? def : ext;
-                        r.optimistic = r.usual;
-                    }
-                    return r;
+                if (!ended) WalkToEnd();
+                const uint32_t time = kTimeWalkSteps * 10;
+                const float d = (target - (moving ? end : WalkFrom(from))).Length();
+                const float rem = Clamp(d - endUsual, 0.0f, 100000.0f), ro = Clamp(d - endOptimistic, 0.0f, 100000.0f);
+                r.usual = TruncToUint32((float)time + (rem / amv) * 1000);
+                r.optimistic = TruncToUint32((float)time + (ro / amv) * 1000);
+                if (limited && time > maxTime) {
+                    const uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
+                    r.usual = def > ext ? def : ext;
+                    r.optimistic = r.usual;
                 }
+                return r;
             }
         }
         return GetTimeNeededMs(pos, mov, target, maxVel, precise, maxTime);

@@ -993,7 +993,17 @@ struct Selector {
         const float adaptedDesiredVel = adaptedDesired.Length();
         const Vec3 adaptedDesiredDir = adaptedDesired.Normalized(0);
         if (a.frameCount > kAnimPositions) Fatal("a fixed-capacity list outgrows its capacity");
-        for (int frame = 0; frame < a.frameCount; frame++) {
+        // The frames read only these values of the animation, held in registers across the
+        // plan's stores.
+        const int frameCount = a.frameCount, lastFramesMs = (a.frameCount - 2) * 10;
+        const bool outgoingIdle = VelocityCat(a.outgoingVelocity) == kVelIdle;
+        const Vec3 outgoingTurned = RotatedBy(a.outgoingMovement, turn);
+        const int32_t smoothedFirst = c.t->selection[ai].smoothedFirst;
+        const Vec3 *const smoothed = c.t->smoothed + (smoothedFirst >= 0 ? smoothedFirst : 0);
+        const Vec3 *const animPositions = c.t->positions + a.posFirst;
+        const int posCount = a.posCount;
+        Vec3 *const plan = out.e;
+        for (int frame = 0; frame < frameCount; frame++) {
             const int tms = frame * stepMs;
             float frameBias = (tms + 10) / (float)((effFrames + 1) * 10);
             // The frame's part independent of the carried movement.
@@ -1008,7 +1018,11 @@ struct Selector {
                 lagExp = lagExp * physicsBias + 1.0f * (1.0f - physicsBias);
             }
             float adaptedFrameBias = lagExp == 1.0f ? frameBias : libm::powf(frameBias, lagExp);
-            Vec3 animMov = RotatedBy(SmoothedMovement(ai, TruncToUint32(effFrames * adaptedFrameBias)), turn);
+            const uint32_t animFrame = TruncToUint32(effFrames * adaptedFrameBias);
+            Vec3 animMov = RotatedBy(smoothedFirst >= 0 && animFrame < (uint32_t)posCount
+                                         ? smoothed[animFrame]
+                                         : MovementAtFrame(animPositions, posCount, animFrame, 1),
+                                     turn);
             float animVel = animMov.Length();
             Vec3 adaptedAnimMov = animMov;
             float adaptedAnimVel = animVel;
@@ -1102,16 +1116,16 @@ struct Selector {
                 }
             }
             Vec3 tmp = temporal + toDesired;
-            if (tms >= (a.frameCount - 2) * 10) {
-                if (VelocityCat(a.outgoingVelocity) == kVelIdle && VelocityCat(tmp.Length()) != kVelIdle)
+            if (tms >= lastFramesMs) {
+                if (outgoingIdle && VelocityCat(tmp.Length()) != kVelIdle)
                     tmp = Vec3(0);
-                else if (VelocityCat(a.outgoingVelocity) != kVelIdle && VelocityCat(tmp.Length()) == kVelIdle)
-                    tmp = NormalizedTo(RotatedBy(a.outgoingMovement, turn), kDribbleVelocity);
+                else if (!outgoingIdle && VelocityCat(tmp.Length()) == kVelIdle)
+                    tmp = NormalizedTo(outgoingTurned, kDribbleVelocity);
             }
             temporal = tmp;
-            if (tms >= (a.frameCount - 2) * 10) penaltyBreak = 0.0f;
+            if (tms >= lastFramesMs) penaltyBreak = 0.0f;
             curPos += temporal * (1.0f - penaltyBreak) * (stepMs / 1000.0f);
-            out[frame] = curPos;
+            plan[frame] = curPos;
         }
         out.count = a.frameCount > 0 ? a.frameCount : 0;
         Vec3 resulting = temporal;
@@ -1286,6 +1300,14 @@ struct Selector {
         float tmpRotSmuggle = 0, predAngle = 0;
         Vec3 adaptedOut;
         bool found = false;
+        // What the keys read of the match, which the evaluations leave unchanged.
+        const MentalBallView mental(w, MentalImg());
+        const Vec3 position = s.position;
+        const Vec3 *const ballPredictions = m.ball.predictions;
+        const bool ballFlip = m.ball.lazyFlip;
+        const FootballKey *const footballKeys = c.t->football;
+        const float ballControl = Statistic(kStatBallControl);
+        const uint64_t now = m.actualTimeMs;
         // One candidate: its physics plan into `plan`, then its ball keys from the middle one down,
         // then up; true with the touch at the first key the body reaches.
         auto evaluate = [&](int ai, PList &plan, float &rotSmuggle, float &predAngleOut, Vec3 &adaptedOutOut, Vec3 &smuggleOut,
@@ -1305,19 +1327,20 @@ struct Selector {
             int defaultTouchFrame = D(ai).touchFrame;
             for (int tn = 0; tn < total && !hit; tn++) {
                 const int key = tn <= total / 2 ? total / 2 - tn : tn;
-                const FootballKey &fk = c.t->football[a.footballFirst + key];
+                const FootballKey &fk = footballKeys[a.footballFirst + key];
                 Vec3 animBall = fk.position;
                 int tf = fk.frame;
                 if (!retainerIsMe) {
-                    Vec3 abs = BallPredict(m.ball, tf * 10);
+                    Vec3 abs = BallPredictRaw(ballPredictions, tf * 10);
+                    if (ballFlip) abs.Mirror();
                     if (fabsf(abs.v[0]) > kPitchHalfLength + kLineHalfWidth + 0.11f ||
                         fabsf(abs.v[1]) > kPitchHalfWidth + kLineHalfWidth + 0.11f)
                         continue;
                 }
                 Vec3 touchMov = RotatedBy(MovementAtFrame(positions.e, positions.count, tf, 0), bk);
-                Vec3 ballPos = MentalBallAt(tf * 10);
-                Vec3 ballMov = (MentalBallAt(tf * 10 + 10) - MentalBallAt(tf * 10)) * 100.0f;
-                ballPos = RotatedBy(ballPos - s.position, bk);
+                Vec3 ballPos = mental.At(tf * 10);
+                Vec3 ballMov = (mental.At(tf * 10 + 10) - ballPos) * 100.0f;
+                ballPos = RotatedBy(ballPos - position, bk);
                 ballMov = RotatedBy(ballMov, bk);
                 const Vec3 touchPos = RotatedBy(positions[tf], bk);
                 Vec3 bodyPos = touchPos;
@@ -1374,9 +1397,9 @@ struct Selector {
                     float tv = touchMov.Length();
                     Vec3 foot = GetFrontOfFootOffsetRelative(tv, z, ballPos.v[2]);
                     if (VelocityCat(tv) != kVelIdle) foot.Rotate2D(FixAngle(touchMov.Normalized(Vec3(0, -1, 0)).Angle2D()));
-                    float ltb = Curve(LastTouchBiasAt(600, m.actualTimeMs + (uint64_t)(int64_t)(tf * 10)), 1.0f);
+                    float ltb = Curve(LastTouchBiasAt(600, now + (uint64_t)(int64_t)(tf * 10)), 1.0f);
                     if (ltb > 0.0f) {
-                        float f = 1.0f - ltb * 0.97f * (1.0f - Statistic(kStatBallControl) * 0.1f);
+                        float f = 1.0f - ltb * 0.97f * (1.0f - ballControl * 0.1f);
                         rf *= f;
                         cheatOff *= f;
                     }

@@ -399,17 +399,36 @@ HD int MentalImageIndex(const World &w, int historyMs) {
 }
 // The offset from the image's stamp wraps as unsigned 32-bit, so one outside the window (a negative
 // one included) reads the last prediction.
-HD Vec3 MentalBallPrediction(const World &w, int k, int ms) {
-    const MentalImage &m = w.match.mentalImages[k];
-    int i = (int)(uint32_t)((uint64_t)(int64_t)ms + w.match.actualTimeMs - (uint64_t)m.timeStampMs);
-    if ((uint32_t)i >= kBallPredictionSpanMs) i = kBallPredictionSpanMs - 10;
-    i = i / 10;
-    if (i < 0) i = 0;
-    Vec3 r = m.ballPredictions[i];
-    if (m.lazyFlip) r.Mirror();
-    Vec3 real = BallPredict(w.match.ball, ms);
-    return r.EnforceMaximumDeviation(real, m.maxDistanceDeviation);
-}
+// The fields one image's predictions read, looked up once for the many times a caller asks.
+struct MentalBallView {
+    const Vec3 *image, *ball;
+    uint64_t now;
+    uint32_t stamp;
+    float maxDeviation;
+    bool imageFlip, ballFlip;
+    HD MentalBallView(const World &w, int k) {
+        const MentalImage &m = w.match.mentalImages[k];
+        image = m.ballPredictions.e;
+        ball = w.match.ball.predictions;
+        now = w.match.actualTimeMs;
+        stamp = m.timeStampMs;
+        maxDeviation = m.maxDistanceDeviation;
+        imageFlip = m.lazyFlip;
+        ballFlip = w.match.ball.lazyFlip;
+    }
+    HD Vec3 At(int ms) const {
+        int i = (int)(uint32_t)((uint64_t)(int64_t)ms + now - (uint64_t)stamp);
+        if ((uint32_t)i >= kBallPredictionSpanMs) i = kBallPredictionSpanMs - 10;
+        i = i / 10;
+        if (i < 0) i = 0;
+        Vec3 r = image[i];
+        if (imageFlip) r.Mirror();
+        Vec3 real = BallPredictRaw(ball, ms);
+        if (ballFlip) real.Mirror();
+        return r.EnforceMaximumDeviation(real, maxDeviation);
+    }
+};
+HD Vec3 MentalBallPrediction(const World &w, int k, int ms) { return MentalBallView(w, k).At(ms); }
 
 // Exact: float differences whose squares add in double.
 HD float GetDistance(const Vec3 &a, const Vec3 &b) {

@@ -301,19 +301,24 @@ struct AIBase {
         const bool walks = TimeWalkApplies(mov);
         TimeWalk &walk = c.ws->walk;
         bool built = false;
+        const MentalBallView mental(w, k);
+        TimeNeededScan scan(pp, mov, maxVel);
         for (unsigned t = start; t < (unsigned)kBallPredictionSpanMs; t += 10 * step) {
             bool forced = false;
-            Vec3 target = MentalBall((int)t);
+            Vec3 target = mental.At((int)t);
             if (fabsf(target.v[0]) > kPitchHalfLength - 0.2f || fabsf(target.v[1]) > kPitchHalfWidth - 0.2f) forced = true;
             if (!forced && target.v[2] >= 1.0f) continue;
             target = target.Get2D();
-            if (walks && !built) {
-                BuildTimeWalk(walk, pp, mov, maxVel);
-                GroupSync();
-                built = true;
+            TimeNeeded tn;
+            if (!scan.Unreachable(target, true, t, tn)) {
+                if (walks && !built) {
+                    BuildTimeWalk(walk, pp, mov, maxVel);
+                    GroupSync();
+                    built = true;
+                }
+                tn = walks ? WalkTimeNeeded(walk, pp, mov, target, maxVel, true, t, true) : GetTimeNeededMs(pp, mov, target, maxVel, true, t);
             }
-            unsigned needed =
-                (walks ? WalkTimeNeeded(walk, pp, mov, target, maxVel, true, t, true) : GetTimeNeededMs(pp, mov, target, maxVel, true, t)).usual;
+            unsigned needed = tn.usual;
             int next = TruncToInt32(roundf((float)(int)(needed - t) * 0.05f)) - 5;
             next = next < 1 ? 1 : next;
             next = 10 < next ? 10 : next;

@@ -13,6 +13,24 @@ struct BallSpatial {
     Quat rotationPerMs;
 };
 
+// The cached ticks' shift: entries 2..399 take entries 3..400, as the ticks copy them one after
+// another in increasing order. The lanes of the match copy four entries each per round, all reads
+// of a round before its writes (a lane's first entry overwrites the last one the lane before it
+// reads).
+HD void ShiftPredictions(Ball &ball) {
+    constexpr int kFirst = 2, kCount = 398, kPerLane = 4;
+    for (int base = 0; base < kCount; base += kPerLane * kGroupLanes) {
+        const int first = base + GroupRank() * kPerLane;
+        Vec3 v[kPerLane];
+        for (int j = 0; j < kPerLane; j++)
+            if (first + j < kCount) v[j] = ball.predictions[kFirst + first + j + 1];
+        GroupSync();
+        for (int j = 0; j < kPerLane; j++)
+            if (first + j < kCount) ball.predictions[kFirst + first + j] = v[j];
+        GroupSync();
+    }
+}
+
 // Entry k of `predictions` is the position after 10k ms. When the first step lands where the last
 // tick predicted, the predictions shift down one entry instead, at most `validPredictions` times.
 HDN BallSpatial BallCalculatePrediction(Ball &ball, bool ballIsInGoal) {
@@ -39,8 +57,8 @@ HDN BallSpatial BallCalculatePrediction(Ball &ball, bool ballIsInGoal) {
     for (uint32_t t = 10; t < kBallPredictionSpanMs + kCachedPredictions * 10; t += 10) {
         if (useCache) {
             // GRF: the last shift reads predictions[400], which no tick writes.
-            ball.predictions[t / 10] = ball.predictions[t / 10 + 1];
-            continue;
+            ShiftPredictions(ball);
+            break;
         }
         float frictionFactor = 0.0f;
         mom.v[2] = mom.v[2] + gravity * dt;
@@ -443,35 +461,38 @@ struct TimeNeededScan {
         if (moving) end = WalkFrom(start);
         ended = true;
     }
-    HD TimeNeeded Get(const Vec3 &target, bool precise, uint32_t maxTime) {
-        if ((pos - target).Length() <= (precise ? 48.0f : 16.0f)) {
-            const Vec3 from = moving ? start : pos + (target - pos).Normalized(0) * 0.1f;
-            const float margin = (fabsf(from.v[0]) + fabsf(from.v[1])) * 1e-5f;
-            if ((target - from).Length() > reach + margin) {
-                const bool limited = maxTime != (uint32_t)-1;
-                TimeNeeded r;
-                if (limited && maxTime < (kTimeWalkSteps - 1) * 10) {
-                    // Stopped by the limit one step past it, the optimistic time found there.
-                    const uint32_t time = (maxTime / 10 + 1) * 10;
-                    const uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
-                    r.optimistic = time;
-                    r.usual = def > ext ? def : ext;
-                    return r;
-                }
-                if (!ended) WalkToEnd();
-                const uint32_t time = kTimeWalkSteps * 10;
-                const float d = (target - (moving ? end : WalkFrom(from))).Length();
-                const float rem = Clamp(d - endUsual, 0.0f, 100000.0f), ro = Clamp(d - endOptimistic, 0.0f, 100000.0f);
-                r.usual = TruncToUint32((float)time + (rem / amv) * 1000);
-                r.optimistic = TruncToUint32((float)time + (ro / amv) * 1000);
-                if (limited && time > maxTime) {
-                    const uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
-                    r.usual = def > ext ? def : ext;
-                    r.optimistic = r.usual;
-                }
-                return r;
-            }
+    // True with the result in `r` for a target the walk cannot reach; false for a far target (the
+    // direct estimate) and for one within reach.
+    HD bool Unreachable(const Vec3 &target, bool precise, uint32_t maxTime, TimeNeeded &r) {
+        if ((pos - target).Length() > (precise ? 48.0f : 16.0f)) return false;
+        const Vec3 from = moving ? start : pos + (target - pos).Normalized(0) * 0.1f;
+        const float margin = (fabsf(from.v[0]) + fabsf(from.v[1])) * 1e-5f;
+        if (!((target - from).Length() > reach + margin)) return false;
+        const bool limited = maxTime != (uint32_t)-1;
+        if (limited && maxTime < (kTimeWalkSteps - 1) * 10) {
+            // Stopped by the limit one step past it, the optimistic time found there.
+            const uint32_t time = (maxTime / 10 + 1) * 10;
+            const uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
+            r.optimistic = time;
+            r.usual = def > ext ? def : ext;
+            return true;
         }
+        if (!ended) WalkToEnd();
+        const uint32_t time = kTimeWalkSteps * 10;
+        const float d = (target - (moving ? end : WalkFrom(from))).Length();
+        const float rem = Clamp(d - endUsual, 0.0f, 100000.0f), ro = Clamp(d - endOptimistic, 0.0f, 100000.0f);
+        r.usual = TruncToUint32((float)time + (rem / amv) * 1000);
+        r.optimistic = TruncToUint32((float)time + (ro / amv) * 1000);
+        if (limited && time > maxTime) {
+            const uint32_t def = DirectTimeMs(pos, mov, target, maxVel), ext = (time + 100) * 2;
+            r.usual = def > ext ? def : ext;
+            r.optimistic = r.usual;
+        }
+        return true;
+    }
+    HD TimeNeeded Get(const Vec3 &target, bool precise, uint32_t maxTime) {
+        TimeNeeded r;
+        if (Unreachable(target, precise, maxTime, r)) return r;
         return GetTimeNeededMs(pos, mov, target, maxVel, precise, maxTime);
     }
 };

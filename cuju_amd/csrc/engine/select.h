@@ -386,7 +386,11 @@ HD bool IncomingBodyPasses(const BodyRule &rule, int entry, const Vec3 &directio
     const float margin = 0.06f * PI;
     if (VelocityCat(r.incomingVelocity) != kVelIdle) {
         if (r.inBodyFixAbsolute > queryInBodyFixAbs + margin) return false;
-        const float qOff = entry >= 0 ? r.incomingBodyAngles[entry] : r.incomingBodyDirection.Angle2D(direction);
+        // Selected with constant indices, so a record copied into registers stays there.
+        float entryAngle = r.incomingBodyAngles[0];
+        for (int i = 1; i < 6; i++)
+            if (entry == i) entryAngle = r.incomingBodyAngles[i];
+        const float qOff = entry >= 0 ? entryAngle : r.incomingBodyDirection.Angle2D(direction);
         if (rule.strict) {
             if (fabsf(qOff) > margin) return false;
         } else {
@@ -410,10 +414,15 @@ HD bool IncomingBodyPasses(const BodyRule &rule, int entry, const Vec3 &directio
 // body-prefiltered record lists (Tables::crudeBody).
 constexpr int kBodyEntries = 6;
 
-HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
+HDN void CrudeSelection(const Ctx &c, const CrudeQuery &query, AList &out) {
     ENG_SCOPE(28);
-    out.count = 0;
+    // The query, the tables' bounds and the list held in registers across the list's stores.
+    const CrudeQuery q = query;
     const Tables &T = *c.t;
+    const float maxIncomingBallDeviation = T.maxIncomingBallDeviation.value();
+    const float maxOutgoingBallDeviation = T.maxOutgoingBallDeviation.value();
+    int16_t *const kept = out.e;
+    int count = 0;
     const float margin = 0.06f * PI;
     Vec3 fenced;
     float queryInToFence = 0.0f;
@@ -485,7 +494,7 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
             float ang = fabsf(qInBallAdapted.Angle2D(r.inBallAdapted));
             float maxDev = r.incomingMaxDeviation;
             if (maxDev == 0.0f) {
-                maxDev = T.maxIncomingBallDeviation.value();
+                maxDev = maxIncomingBallDeviation;
                 if (at == kAtDeflect) maxDev = 0.4f * PI;
             }
             if (ang > maxDev) return false;
@@ -494,7 +503,7 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
             const Vec3 &abd = r.ballDirectionNormalized;
             float ang = qOutNull && (r.flags & 8) ? 0.0f : fabsf((qOutNull ? abd : qOutNormalized).Angle2D(abd));
             float maxDev = r.outgoingMaxDeviation;
-            if ((double)maxDev == 0.0) maxDev = T.maxOutgoingBallDeviation.value();
+            if ((double)maxDev == 0.0) maxDev = maxOutgoingBallDeviation;
             if (ang > maxDev) return false;
         }
         if (q.incomingSpecialState != r.incomingSpecialState) return false;
@@ -535,11 +544,14 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &q, AList &out) {
     }
     for (int k0 = 0; k0 < n; k0 += kGroupLanes) {
         const int k = k0 + GroupRank();
+        // The whole record at once, field by field into registers: the tests read its fields
+        // one after another.
         const bool keep = k < n && accepts(records[k]);
-        const uint32_t kept = GroupBallot(keep);
-        if (keep) out.e[out.count + PopCount(kept & ((1u << GroupRank()) - 1u))] = records[k].index;
-        out.count += PopCount(kept);
+        const uint32_t passed = GroupBallot(keep);
+        if (keep) kept[count + PopCount(passed & ((1u << GroupRank()) - 1u))] = records[k].index;
+        count += PopCount(passed);
     }
+    out.count = count;
     GroupSync();
 }
 

@@ -203,13 +203,8 @@ int cuju_environment_set_stack(void *e, int index, const char *name, const void 
     }
 }
 const char *cuju_environment_raw_field(void *e, int field, int *type, int *dimensions, unsigned long long *offset) {
-    // The batch emits no raw observation, so it describes no raw array.
-    (void)e;
-    (void)field;
-    (void)type;
-    (void)dimensions;
-    (void)offset;
-    return nullptr;
+    if (!e || !type || !dimensions || !offset) return nullptr;
+    return Of(e)->RawField(field, type, dimensions, offset);
 }
 void *cuju_environment_buffer(void *e, const char *name) {
     void *p = Of(e)->Buffer(name ? name : "");

@@ -12,8 +12,11 @@ BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> dev
     try {
         if ((cfg.observation & kObsSimple115) && (cfg.observation & kObsSimple115v2))
             throw std::invalid_argument("simple115 and simple115v2 are exclusive");
-        if (cfg.observation & (kObsSmm | kObsRaw))
-            throw std::invalid_argument("this build emits the simple115 and simple115v2 representations only");
+        if ((cfg.observation & kObsSmm) && (cfg.smmWidth < 1 || cfg.smmHeight < 1))
+            throw std::invalid_argument("expected an SMM of at least 1 by 1, found " + std::to_string(cfg.smmWidth) + " by " +
+                                        std::to_string(cfg.smmHeight));
+        if (!(cfg.observation & (kObsSimple115 | kObsSimple115v2 | kObsSmm | kObsRaw)))
+            throw std::invalid_argument("expected at least one representation");
         if (cfg.assets.empty()) throw std::invalid_argument("expected an asset bundle");
         if (cfg.count < 1) throw std::invalid_argument("expected at least one environment, found " + std::to_string(cfg.count));
         if (cfg.ticksPerStep < 1) throw std::invalid_argument("expected at least one tick in a step");
@@ -114,6 +117,21 @@ BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> dev
         if (cfg.observation & (kObsSimple115 | kObsSimple115v2)) {
             b_.simple115 = Alloc<float>((size_t)count * agents * kSimple115 * cfg.stack);
             b_.finalSimple115 = Alloc<float>((size_t)count * agents * kSimple115 * cfg.stack);
+        }
+        b_.smmWidth = cfg.smmWidth;
+        b_.smmHeight = cfg.smmHeight;
+        if (cfg.observation & kObsSmm) {
+            const size_t maps = (size_t)count * agents * cfg.smmWidth * cfg.smmHeight * kSmmLayers * cfg.stack;
+            const size_t rows = (size_t)count * agents * kSmmMarkRow * cfg.stack;
+            b_.smm = Alloc<uint8_t>(maps);
+            b_.finalSmm = Alloc<uint8_t>(maps);
+            b_.smmMarks = Alloc<int32_t>(rows);
+            b_.finalSmmMarks = Alloc<int32_t>(rows);
+        }
+        if (cfg.observation & kObsRaw) {
+            b_.rawLayout = MakeRawLayout((size_t)count * agents, players_, StickyActionCount(cfg.actionSet));
+            b_.raw = Alloc<uint8_t>(b_.rawLayout.bytes);
+            b_.finalRaw = Alloc<uint8_t>(b_.rawLayout.bytes);
         }
         b_.teamDifficulty = nullptr;
         if (!dev_->HostMemory()) actions_ = Alloc<int32_t>((size_t)count * agents);
@@ -384,9 +402,62 @@ void BatchRuntime::SetStack(int env, const std::string &name, const void *frames
     dev_->ToDevice(b_.simple115 + (size_t)env * b_.agents * width, frames, bytes);
 }
 
+// GRF's raw keys, in the order of the arrays (observation.py).
+static const char *const kRawFieldNames[kRawFields] = {
+    "ball", "ball_direction", "ball_rotation", "ball_owned_team", "ball_owned_player",
+    "left_team", "left_team_direction", "left_team_tired_factor", "left_team_yellow_card", "left_team_active", "left_team_roles",
+    "right_team", "right_team_direction", "right_team_tired_factor", "right_team_yellow_card", "right_team_active", "right_team_roles",
+    "score", "steps_left", "game_mode", "active", "designated", "sticky_actions"};
+
+RawLayout MakeRawLayout(size_t outputs, int players, int sticky) {
+    RawLayout L{};
+    L.players = players;
+    L.sticky = sticky;
+    auto set = [&](int field, int type, int d0, int d1) {
+        L.type[field] = type;
+        L.shape[field][0] = d0;
+        L.shape[field][1] = d1;
+        L.elements[field] = (d0 ? d0 : 1) * (d1 ? d1 : 1);
+    };
+    for (int f : {kRawBall, kRawBallDirection, kRawBallRotation}) set(f, kRawFloat32, 3, 0);
+    set(kRawBallOwnedTeam, kRawInt32, 0, 0);
+    set(kRawBallOwnedPlayer, kRawInt32, 0, 0);
+    for (int base : {kRawLeftTeam, kRawRightTeam}) {
+        set(base, kRawFloat32, players, 2);
+        set(base + 1, kRawFloat32, players, 2);
+        set(base + 2, kRawFloat32, players, 0);
+        set(base + 3, kRawBool, players, 0);
+        set(base + 4, kRawBool, players, 0);
+        set(base + 5, kRawInt32, players, 0);
+    }
+    set(kRawScore, kRawInt32, 2, 0);
+    for (int f : {kRawStepsLeft, kRawGameMode, kRawActive, kRawDesignated}) set(f, kRawInt32, 0, 0);
+    set(kRawStickyActions, kRawUint8, sticky, 0);
+    uint64_t offset = 0;
+    for (int f = 0; f < kRawFields; f++) {
+        L.offset[f] = offset;
+        offset += (outputs * L.elements[f] * RawTypeBytes(L.type[f]) + 255) / 256 * 256;
+    }
+    L.bytes = offset;
+    return L;
+}
+
+const char *BatchRuntime::RawField(int field, int *type, int *dimensions, unsigned long long *offset) const {
+    if (!b_.raw || field < 0 || field >= kRawFields) return nullptr;
+    *type = b_.rawLayout.type[field];
+    dimensions[0] = b_.rawLayout.shape[field][0];
+    dimensions[1] = b_.rawLayout.shape[field][1];
+    *offset = b_.rawLayout.offset[field];
+    return kRawFieldNames[field];
+}
+
 void *BatchRuntime::Buffer(const std::string &name) {
     if (name == "simple115") return b_.simple115;
     if (name == "final_simple115") return b_.finalSimple115;
+    if (name == "smm") return b_.smm;
+    if (name == "final_smm") return b_.finalSmm;
+    if (name == "raw") return b_.raw;
+    if (name == "final_raw") return b_.finalRaw;
     if (name == "reward") return b_.reward;
     if (name == "done") return b_.done;
     if (name == "score_reward") return b_.scoreReward;

@@ -59,6 +59,9 @@ struct Configuration {
     int64_t firstIndex = 0;
 };
 
+// The raw arrays of `outputs` agent views in one buffer, each at a multiple of 256 bytes.
+RawLayout MakeRawLayout(size_t outputs, int players, int sticky);
+
 class BatchRuntime {
 public:
     BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> device);
@@ -96,6 +99,9 @@ public:
     void SetStack(int env, const std::string &name, const void *frames, size_t bytes);
     // The buffer of an output name, or null.
     void *Buffer(const std::string &name);
+    // Raw array `field`: its name, element type, the two dimensions after the agent axis (0 when
+    // absent) and its byte offset into `raw` and `final_raw`; null past the last or without raw.
+    const char *RawField(int field, int *type, int *dimensions, unsigned long long *offset) const;
 
 private:
     template <class T>

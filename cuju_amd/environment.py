@@ -24,7 +24,10 @@ from . import library as _library
 from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, ConfigurationError,
                      EnvironmentIndexError, MissingFileError, StateError, from_library)
 
-REPRESENTATIONS = {'simple115': 1, 'simple115v2': 2}
+REPRESENTATIONS = {'simple115': 1, 'simple115v2': 2, 'extracted': 4, 'raw': 8}
+# By the type code of `cuju_environment_raw_field`.
+RAW_TYPES = (torch.float32, torch.int32, torch.bool, torch.uint8)
+SMM_HEIGHT, SMM_WIDTH = 72, 96
 ACTION_SETS = {'default': 0, 'v2': 1, 'full': 2}
 ACTION_COUNTS = {'default': 19, 'v2': 20, 'full': 33}
 MAXIMUM_AGENTS = 22
@@ -94,7 +97,7 @@ class _StateUnpickler(pickle.Unpickler):
 class _DeviceArray:
     """A device buffer that `torch.as_tensor` reads through `__cuda_array_interface__`."""
 
-    _TYPES = {torch.float32: '<f4', torch.int32: '<i4', torch.uint8: '|u1'}
+    _TYPES = {torch.float32: '<f4', torch.int32: '<i4', torch.uint8: '|u1', torch.bool: '|b1'}
 
     def __init__(self, pointer, shape, dtype, owner):
         self.owner = owner
@@ -131,9 +134,11 @@ class BatchEnvironment:
                  difficulty=None, device: str | int | torch.device = 'cuda', physics_steps_per_frame: int = 10,
                  stacked: bool = False, game_engine_random_seed=None, squeeze: bool = False, agent_counts=None,
                  episode_number: int = 0, first_index: int = 0, check_actions: bool = False,
-                 library: str | None = None):
+                 with_raw: bool = False, library: str | None = None):
         if representation not in REPRESENTATIONS:
             raise ChoiceError(f'expected a representation of {sorted(REPRESENTATIONS)}, found {representation!r}')
+        if stacked and representation == 'raw':
+            raise ConfigurationError('expected simple115, simple115v2 or extracted for a stack, found raw')
         if action_set not in ACTION_SETS:
             raise ChoiceError(f'expected an action set of {sorted(ACTION_SETS)}, found {action_set!r}')
         reward_parts = set(rewards.split(','))
@@ -178,9 +183,11 @@ class BatchEnvironment:
             version=2, assets=self._paths, asset_count=len(names),
             assignment=None if self._assignment is None else self._assignment.ctypes.data,
             animations=animations.encode(), environment_count=environment_count, seed=seed,
-            action_set=ACTION_SETS[action_set], observation=REPRESENTATIONS[representation],
+            action_set=ACTION_SETS[action_set],
+            observation=REPRESENTATIONS[representation] | (REPRESENTATIONS['raw'] if with_raw else 0),
             checkpoints=int(self.checkpoints), numpy_legacy=int(numpy_legacy), auto_reset=int(auto_reset),
-            threads=0, ticks_per_step=physics_steps_per_frame, smm_width=96, smm_height=72, stack=self.stack,
+            threads=0, ticks_per_step=physics_steps_per_frame, smm_width=SMM_WIDTH, smm_height=SMM_HEIGHT,
+            stack=self.stack,
             fixed_seeds=None if self._fixed is None else self._fixed.ctypes.data,
             agent_counts=self._counts.ctypes.data, episode_number=episode_number, first_index=first_index,
             allocate=None, release=None, allocator_context=None, pin_threads=0, numa=0, page_aligned=0)
@@ -204,9 +211,17 @@ class BatchEnvironment:
             values = np.ascontiguousarray(np.broadcast_to(np.asarray(difficulty, dtype=np.float32),
                                                           (environment_count, 2)))
             self._check(lib.cuju_environment_set_difficulty(handle, values.ctypes.data))
-        width = 115 * self.stack
-        self._observation = self._buffer('simple115', (environment_count, self.agents, width), torch.float32)
-        self._final = self._buffer('final_simple115', (environment_count, self.agents, width), torch.float32)
+        self._raw_fields = self._describe_raw()
+        if representation == 'raw':
+            self._observation, self._final = self._raw('raw'), self._raw('final_raw')
+        elif representation == 'extracted':
+            shape = (environment_count, self.agents, SMM_HEIGHT, SMM_WIDTH, 4 * self.stack)
+            self._observation = self._buffer('smm', shape, torch.uint8)
+            self._final = self._buffer('final_smm', shape, torch.uint8)
+        else:
+            width = 115 * self.stack
+            self._observation = self._buffer('simple115', (environment_count, self.agents, width), torch.float32)
+            self._final = self._buffer('final_simple115', (environment_count, self.agents, width), torch.float32)
         self._reward = self._buffer('reward', (environment_count, self.agents), torch.float32)
         self._done = self._buffer('done', (environment_count,), torch.uint8)
         self._score_reward = self._buffer('score_reward', (environment_count,), torch.int32)
@@ -237,10 +252,42 @@ class BatchEnvironment:
             raise from_library(self._lib.cuju_last_error().decode())
         return torch.as_tensor(_DeviceArray(pointer, shape, dtype, self._native), device=self._torch_device)
 
+    def _describe_raw(self):
+        """Name, type, shape and byte offset of each raw array (src/environment_api.h:446-460)."""
+        fields = []
+        element_type, offset = ctypes.c_int(), ctypes.c_ulonglong()
+        dimensions = (ctypes.c_int * 2)()
+        for field in range(64):
+            name = self._lib.cuju_environment_raw_field(self._handle(), field, ctypes.byref(element_type), dimensions,
+                                                        ctypes.byref(offset))
+            if name is None:
+                break
+            shape = (self.environment_count, self.agents, *(d for d in dimensions if d))
+            fields.append((name.decode(), RAW_TYPES[element_type.value], shape, offset.value))
+        return fields
+
+    def _raw(self, name):
+        """The raw arrays of a buffer as tensors that share it."""
+        pointer = self._lib.cuju_environment_buffer(self._handle(), name.encode())
+        if not pointer:
+            raise from_library(self._lib.cuju_last_error().decode())
+        return {field: torch.as_tensor(_DeviceArray(pointer + offset, shape, dtype, self._native), device=self._torch_device)
+                for field, dtype, shape, offset in self._raw_fields}
+
+    def raw(self) -> dict:
+        """GRF's raw observation of every agent as `[environment_count, agents, ...]` tensors, for
+        a batch of the `raw` representation or one made `with_raw`."""
+        if not self._raw_fields:
+            raise ConfigurationError('expected a batch with the raw representation or with_raw')
+        return self._raw('raw')
+
     def _stream(self):
         return torch.cuda.current_stream(self._torch_device).cuda_stream
 
     def _view(self, tensor):
+        # GRF: the raw observation of one agent keeps its agent axis.
+        if isinstance(tensor, dict):
+            return tensor
         return tensor[:, 0] if self.squeeze and self.agents == 1 else tensor
 
     def _outputs(self):

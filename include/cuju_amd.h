@@ -29,7 +29,7 @@ struct cuju_configuration {
     int environment_count;
     unsigned long long seed; /* env i plays GRF after random.seed(seed * 2**32 + first_index + i) */
     int action_set; /* 0 default, 1 v2, 2 full */
-    int observation; /* bit mask: 1 simple115, 2 simple115v2 (4 SMM and 8 raw are refused) */
+    int observation; /* bit mask: 1 simple115, 2 simple115v2, 4 SMM (extracted), 8 raw */
     int checkpoints; /* nonzero adds the checkpoint reward */
     int numpy_legacy; /* nonzero adds it as numpy before 2.0 does */
     int auto_reset; /* nonzero resets every environment whose episode ended within the step */
@@ -96,9 +96,12 @@ const char *cuju_environment_get_state(void *environment, int index, unsigned lo
 int cuju_environment_set_state(void *environment, int index, const char *bytes, unsigned long long size, const int *episode);
 /* src/environment_api.h:410; simple115 only: [agents][115 * stack] float32, oldest frame first */
 int cuju_environment_set_stack(void *environment, int index, const char *name, const void *frames, unsigned long long size);
-/* src/environment_api.h:449; null: the batch emits no raw observation */
+/* src/environment_api.h:449; raw array `field` from 0: its name, type (0 float32, 1 int32, 2 bool,
+   3 uint8), the two dimensions after the agent axis (0 if absent) and its byte offset into raw and
+   final_raw; null past the last array or without the raw representation */
 const char *cuju_environment_raw_field(void *environment, int field, int *type, int *dimensions, unsigned long long *offset);
-/* src/environment_api.h:430; simple115, final_simple115, reward, done, score_reward */
+/* src/environment_api.h:430; simple115, final_simple115, smm, final_smm (uint8
+   [E][A][smm_height][smm_width][4 * stack]), raw, final_raw, reward, done, score_reward */
 void *cuju_environment_buffer(void *environment, const char *name);
 
 #ifdef __cplusplus

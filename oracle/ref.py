@@ -102,10 +102,40 @@ def library(path=None):
         lib.cuju_environment_buffer.restype = ctypes.c_void_p
         lib.cuju_environment_buffer.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
         lib.cuju_environment_set_difficulty.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        lib.cuju_environment_raw_field.restype = ctypes.c_char_p
+        lib.cuju_environment_raw_field.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                                   ctypes.c_void_p, ctypes.POINTER(ctypes.c_ulonglong)]
         lib.cuju_environment_set_state.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p,
                                                    ctypes.c_ulonglong, ctypes.c_void_p]
         _libraries[path] = lib
     return _libraries[path]
+
+
+# By the type code of `cuju_environment_raw_field` (`src/environment_api.h:446-460`).
+RAW_TYPES = (np.float32, np.int32, np.bool_, np.uint8)
+
+
+def describe_raw(lib, handle, environments, agents):
+    """Name, type, shape and byte offset of each raw array of a batch, empty without raw."""
+    fields = []
+    element_type, offset = ctypes.c_int(), ctypes.c_ulonglong()
+    dimensions = (ctypes.c_int * 2)()
+    for field in range(64):
+        name = lib.cuju_environment_raw_field(handle, field, ctypes.byref(element_type), dimensions,
+                                              ctypes.byref(offset))
+        if name is None:
+            break
+        shape = (environments, agents, *(d for d in dimensions if d))
+        fields.append((name.decode(), RAW_TYPES[element_type.value], shape, offset.value))
+    return fields
+
+
+def observation_bytes(observation):
+    """The bytes a digest hashes of an observation: a raw dictionary by sorted name
+    (`python/cuju/check.py:81-87`)."""
+    if isinstance(observation, dict):
+        return b''.join(np.ascontiguousarray(observation[name]).tobytes() for name in sorted(observation))
+    return np.ascontiguousarray(observation).tobytes()
 
 
 def resolve_asset(name: str):
@@ -153,7 +183,8 @@ class ReferenceBatch:
                  rewards='scoring', action_set='default', stacked=False, auto_reset=True,
                  threads=0, assignment=None, agent_counts=None, first_index=0,
                  difficulty=None, numpy_legacy=True, episode_number=0,
-                 physics_steps_per_frame=10, game_engine_random_seed=None, library_path=None):
+                 physics_steps_per_frame=10, game_engine_random_seed=None, library_path=None,
+                 with_raw=False):
         lib = library(library_path)
         self._lib = lib
         names = [assets] if isinstance(assets, str) else list(assets)
@@ -177,7 +208,8 @@ class ReferenceBatch:
             assignment=None if self._assignment is None else self._assignment.ctypes.data,
             animations=os.path.join(DATA, 'animations.bin').encode(),
             environment_count=environment_count, seed=seed,
-            action_set=ACTION_SETS[action_set], observation=REPRESENTATIONS[representation],
+            action_set=ACTION_SETS[action_set],
+            observation=REPRESENTATIONS[representation] | (REPRESENTATIONS['raw'] if with_raw else 0),
             checkpoints=int(self.checkpoints), numpy_legacy=int(numpy_legacy),
             auto_reset=int(auto_reset), threads=threads,
             ticks_per_step=physics_steps_per_frame, smm_width=96, smm_height=72,
@@ -201,6 +233,25 @@ class ReferenceBatch:
             values = np.ascontiguousarray(difficulty, dtype=np.float32).reshape(
                 environment_count, 2)
             self._check(lib.cuju_environment_set_difficulty(handle, values.ctypes.data))
+        self.raw_fields = describe_raw(lib, handle, environment_count, self.agents)
+
+    def _raw(self, name):
+        pointer = self._lib.cuju_environment_buffer(self._handle, name.encode())
+        out = {}
+        for field, dtype, shape, offset in self.raw_fields:
+            count = int(np.prod(shape))
+            buffer = (ctypes.c_char * (count * np.dtype(dtype).itemsize)).from_address(pointer + offset)
+            out[field] = np.frombuffer(buffer, dtype=dtype).reshape(shape)
+        return out
+
+    def _observation(self, final):
+        prefix = 'final_' if final else ''
+        if self.representation == 'raw':
+            return self._raw(prefix + 'raw')
+        if self.representation == 'extracted':
+            return self._array(prefix + 'smm', np.uint8, (self.environment_count, self.agents, 72, 96, 4 * self.stack))
+        return self._array(prefix + 'simple115', np.float32,
+                           (self.environment_count, self.agents, 115 * self.stack))
 
     def _check(self, status):
         if status != 0:
@@ -215,8 +266,9 @@ class ReferenceBatch:
         return np.frombuffer(buffer, dtype=dtype).reshape(shape)
 
     def observation(self):
-        return self._array('simple115', np.float32,
-                           (self.environment_count, self.agents, 115 * self.stack))
+        """The observation of the batch's representation: `[E][A][115 * stack]` float32, the SMM
+        `[E][A][72][96][4 * stack]` uint8, or for `raw` a dictionary of `[E][A]...` arrays."""
+        return self._observation(False)
 
     def reward(self):
         return self._array('reward', np.float32, (self.environment_count, self.agents))
@@ -228,8 +280,11 @@ class ReferenceBatch:
         return self._array('score_reward', np.int32, (self.environment_count,))
 
     def final_observation(self):
-        return self._array('final_simple115', np.float32,
-                           (self.environment_count, self.agents, 115 * self.stack))
+        return self._observation(True)
+
+    def raw(self, final=False):
+        """The raw arrays of a batch of the raw representation or made `with_raw`."""
+        return self._raw('final_raw' if final else 'raw')
 
     def reset(self, seeds=None, mask=None):
         if mask is None and seeds is None:
@@ -295,11 +350,11 @@ def play_digest(batch_factory, assets, steps, seed=7, environments=4, **options)
     either a `ReferenceBatch` or any object with the same methods."""
     batch = batch_factory(assets, environment_count=environments, seed=seed, **options)
     digest = hashlib.sha256()
-    digest.update(np.ascontiguousarray(batch.reset()).tobytes())
+    digest.update(observation_bytes(batch.reset()))
     for step in range(steps):
         actions = actions_at(step, environments, batch.agents, batch.action_count)
         observation, reward, done = batch.step(actions)
-        digest.update(np.ascontiguousarray(observation).tobytes())
+        digest.update(observation_bytes(observation))
         digest.update(np.ascontiguousarray(reward).tobytes())
         digest.update(np.ascontiguousarray(done).tobytes())
     if batch.stack == 1:

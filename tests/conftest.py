@@ -28,7 +28,7 @@ def load_digests():
         return json.load(f)
 
 
-def short_cases(formats=('simple115', 'simple115v2')):
+def short_cases(formats=('simple115', 'simple115v2', 'extracted', 'raw')):
     """The reference's short digest cases whose representation this build emits."""
     digests = load_digests()
     out = []
@@ -49,6 +49,9 @@ def play(batch, steps, environments):
     """SHA-256 over the reset observation, every step's observation, reward and done, then every
     environment's state. `batch` exposes reset/step/get_state returning array-likes."""
     def raw(x):
+        # A raw observation is a dictionary, hashed by sorted name as the reference's check does.
+        if isinstance(x, dict):
+            return b''.join(raw(x[name]) for name in sorted(x))
         x = x.detach().cpu().numpy() if hasattr(x, 'detach') else np.asarray(x)
         return np.ascontiguousarray(x).tobytes()
     digest = hashlib.sha256()

@@ -119,3 +119,48 @@ def test_gpu_set_state_continues_as_the_reference(reference_library):
     finally:
         mine.close()
         theirs.close()
+
+
+def _host_observation(x):
+    if isinstance(x, dict):
+        return {k: host(v) for k, v in x.items()}
+    return host(x)
+
+
+def _same(a, b):
+    if isinstance(a, dict):
+        return sorted(a) == sorted(b) and all(_same(a[k], b[k]) for k in a)
+    return np.ascontiguousarray(a).tobytes() == np.ascontiguousarray(b).tobytes()
+
+
+@pytest.mark.parametrize('representation,stacked,with_raw', [('extracted', False, True), ('extracted', True, False),
+                                                             ('raw', False, False)])
+def test_gpu_smm_and_raw_match_reference(representation, stacked, with_raw, reference_library):
+    """The SMM (one frame and a stack of four) and the raw arrays on the device, with the final
+    observations of episodes that end, byte for byte against the reference CPU library on short
+    academy episodes mixed with 5-a-side games."""
+    environments = 24
+    assets = ['academy_empty_goal_close_l1_r0', '5_vs_5_l4_r4']
+    options = dict(environment_count=environments, seed=5, representation=representation, stacked=stacked,
+                   with_raw=with_raw, assignment=[0, 1] * (environments // 2))
+    mine = gpu_batch(assets, **options)
+    theirs = ref.ReferenceBatch(assets, threads=0, library_path=reference_library, **options)
+    try:
+        assert _same(_host_observation(mine.reset()), theirs.reset())
+        ended = 0
+        for step in range(70):
+            actions = digest_actions(step, environments, mine.agents, mine.action_count)
+            a = mine.step(torch.as_tensor(actions, device='cuda:0'))
+            b = theirs.step(actions)
+            assert _same(_host_observation(a[0]), b[0]), f'observation at step {step}'
+            assert host(a[1]).tobytes() == b[1].tobytes(), f'reward at step {step}'
+            assert host(a[2]).astype(np.uint8).tobytes() == b[2].tobytes(), f'done at step {step}'
+            if b[2].any():
+                ended += 1
+                assert _same(_host_observation(a[3]['final_observation']), theirs.final_observation()), f'final at {step}'
+            if with_raw:
+                assert _same(_host_observation(mine.raw()), theirs.raw()), f'raw at step {step}'
+        assert ended > 0
+    finally:
+        mine.close()
+        theirs.close()

@@ -214,3 +214,42 @@ def test_engine_float_math_matches_the_c_library(name, which, binary, host_libra
     want = np.array([fn(float(a), float(b)) if binary else fn(float(a)) for a, b in zip(x, y)], dtype=np.float32)
     same = (out.view(np.uint32) == want.view(np.uint32)) | (np.isnan(out) & np.isnan(want))
     assert same.all(), f'{name}: {(~same).sum()} differ, first at {x[~same][0]!r}, {y[~same][0]!r}'
+
+
+def _same(a, b):
+    """Byte equality of two observations, arrays or raw dictionaries of arrays."""
+    if isinstance(a, dict):
+        return sorted(a) == sorted(b) and all(_same(a[k], b[k]) for k in a)
+    return np.ascontiguousarray(a).tobytes() == np.ascontiguousarray(b).tobytes()
+
+
+@pytest.mark.parametrize('representation,stacked,with_raw', [('extracted', False, True), ('extracted', True, False),
+                                                             ('raw', False, False)])
+def test_host_engine_smm_and_raw_match_reference(representation, stacked, with_raw, reference_library, host_library):
+    """The SMM (one frame and a stack of four) and the raw arrays, with the final observations of
+    episodes that end, against the reference library on short academy episodes and a 5-a-side game
+    in one batch (observation_encoding.h:119-148, batch_core.h:52-210)."""
+    options = dict(environment_count=6, seed=5, threads=2, representation=representation, stacked=stacked,
+                   with_raw=with_raw, assignment=[0, 1, 0, 1, 0, 1])
+    assets = ['academy_empty_goal_close_l1_r0', '5_vs_5_l4_r4']
+    mine = ref.ReferenceBatch(assets, library_path=host_library, **options)
+    theirs = ref.ReferenceBatch(assets, library_path=reference_library, **options)
+    try:
+        assert _same(mine.reset(), theirs.reset())
+        ended = 0
+        for step in range(70):
+            actions = digest_actions(step, 6, mine.agents, mine.action_count)
+            a, b = mine.step(actions), theirs.step(actions)
+            for x, y, what in zip(a, b, ('observation', 'reward', 'done')):
+                assert _same(x, y), f'{what} at step {step}'
+            if b[2].any():
+                ended += 1
+                assert _same(mine.final_observation(), theirs.final_observation()), f'final at step {step}'
+                if with_raw:
+                    assert _same(mine.raw(final=True), theirs.raw(final=True)), f'final raw at step {step}'
+            if with_raw:
+                assert _same(mine.raw(), theirs.raw()), f'raw at step {step}'
+        assert ended > 0
+    finally:
+        mine.close()
+        theirs.close()

@@ -1426,30 +1426,68 @@ struct Selector {
             }
             return hit;
         };
+        // A candidate passes only at a key where the ball is on the pitch and passes the height
+        // test (dz < 0.22). The plan moves the ball's height at a key only between its heights just
+        // before and just after the key, so a key whose ball height lies far enough from that span
+        // fails the test whatever the plan. The lanes keep, in list order, the candidates with a
+        // key that may pass; the others fail without a plan. The bound's factors are the smallest
+        // the test can apply, with margins over the rounding.
+        auto mayPass = [&](int ai) -> bool {
+            if (retainerIsMe) return true;
+            const Anim &a = A(ai);
+            for (int key = 0; key < a.footballCount; key++) {
+                const FootballKey &fk = footballKeys[a.footballFirst + key];
+                const int tf = fk.frame;
+                Vec3 abs = BallPredictRaw(ballPredictions, tf * 10);
+                if (ballFlip) abs.Mirror();
+                if (fabsf(abs.v[0]) > kPitchHalfLength + kLineHalfWidth + 0.11f ||
+                    fabsf(abs.v[1]) > kPitchHalfWidth + kLineHalfWidth + 0.11f)
+                    continue;
+                const float m0 = mental.At(tf * 10).v[2], m1 = mental.At(tf * 10 + 10).v[2];
+                const float z = m0 - position.v[2], dzdt = (m1 - m0) * 100.0f;
+                const float zBefore = z - dzdt * 0.006f, zAfter = z + dzdt * 0.003f;
+                const float slack = (fabsf(zBefore) + fabsf(zAfter)) * 1e-5f + 1e-6f;
+                const float lo = MinF(zBefore, zAfter) - slack, hi = MaxF(zBefore, zAfter) + slack;
+                const float az = fk.position.v[2] * (height / kDefaultPlayerHeight);
+                const float gap = az < lo ? lo - az : az > hi ? az - hi : 0.0f;
+                float bound = gap * (1.0f - Clamp((float)(((double)az - 0.11) * (double)0.3f), 0.0f, 0.2f)) * 0.69f;
+                if (fn == kFnDeflect) bound *= 0.8f;
+                if (a.baseAnimation && lo < 0.5f) bound -= 0.15f;
+                if (!(bound > 0.2201f)) return true;
+            }
+            return false;
+        };
+        AList candidates{c.ws->lists[2], 0};
+        for (int k0 = 0; k0 < sorted.count; k0 += kGroupLanes) {
+            const int k = k0 + GroupRank();
+            const bool keep = k < sorted.count && mayPass(sorted[k]);
+            const uint32_t kept = GroupBallot(keep);
+            if (keep) candidates.e[candidates.count + PopCount(kept & ((1u << GroupRank()) - 1u))] = sorted[k];
+            candidates.count += PopCount(kept);
+        }
+        GroupSync();
         // The lanes of the match evaluate consecutive candidates; the earliest that passes wins.
-        // Without one, the plan and rotation of the last candidate remain, as a sequential search
-        // leaves them.
-        for (int e0 = 0; e0 < sorted.count && !found; e0 += kGroupLanes) {
+        // Without one the caller reads neither the plan nor the rotation.
+        positions.count = 0;
+        for (int e0 = 0; e0 < candidates.count && !found; e0 += kGroupLanes) {
             const int entry = e0 + GroupRank();
             PList mine{kGroupLanes == 1 ? positions.e : c.ws->lanePlans[GroupRank()], 0};
             float rot = 0, pa = 0;
             Vec3 ao, sm;
             int tf = 0;
-            const bool ok = entry < sorted.count && evaluate(sorted[entry], mine, rot, pa, ao, sm, tf);
+            const bool ok = entry < candidates.count && evaluate(candidates[entry], mine, rot, pa, ao, sm, tf);
             const uint32_t passed = GroupBallot(ok);
-            const int last = sorted.count - 1 - e0;
-            const int from = passed ? LowestBit(passed) : (last < kGroupLanes - 1 ? last : kGroupLanes - 1);
+            if (!passed) continue;
+            const int from = LowestBit(passed);
             tmpRotSmuggle = GroupShuffle(rot, from);
             const int count = GroupShuffle((int32_t)mine.count, from);
-            if (passed) {
-                found = true;
-                best = sorted[e0 + from];
-                predAngle = GroupShuffle(pa, from);
-                adaptedOut = GroupShuffle(ao, from);
-                bestSmuggle2D = GroupShuffle(sm, from);
-                touchFrameOut = GroupShuffle((int32_t)tf, from);
-            }
-            if (kGroupLanes > 1 && (passed || e0 + kGroupLanes >= sorted.count)) {
+            found = true;
+            best = candidates[e0 + from];
+            predAngle = GroupShuffle(pa, from);
+            adaptedOut = GroupShuffle(ao, from);
+            bestSmuggle2D = GroupShuffle(sm, from);
+            touchFrameOut = GroupShuffle((int32_t)tf, from);
+            if (kGroupLanes > 1) {
                 GroupSync();
                 const Vec3 *src = c.ws->lanePlans[from];
                 for (int i = GroupRank(); i < count; i += kGroupLanes) positions.e[i] = src[i];

@@ -313,41 +313,54 @@ HDN bool TeamCalculateDynamicRoles(World &w, const Ctx &c, int teamID) {
         Vec3 pp = Sp(w, ps[pi]).position + Sp(w, ps[pi]).movement * 0.5f;
         return TruncToInt32(roundf((pp - slots[si]).Length() * 10));
     };
-    int sorted[kTeamPlayers * kTeamPlayers];
+    int costs[kTeamPlayers * kTeamPlayers], sorted[kTeamPlayers * kTeamPlayers];
     int count = 0;
     for (unsigned pi = 0; pi < n; pi++)
-        for (unsigned si = 0; si < n; si++) sorted[count++] = cost(pi, si);
+        for (unsigned si = 0; si < n; si++) sorted[count++] = costs[pi * n + si] = cost(pi, si);
     for (int u = 1; u < count; u++)
         for (int s = u; s > 0 && sorted[s] < sorted[s - 1]; s--) {
             int x = sorted[s];
             sorted[s] = sorted[s - 1];
             sorted[s - 1] = x;
         }
-    for (unsigned cutoff = n; cutoff < (unsigned)count; cutoff += 5) {
-        // A row is a formation slot, a column a player.
-        int m[kTeamPlayers * kTeamPlayers];
-        for (unsigned pi = 0; pi < n; pi++)
-            for (unsigned si = 0; si < n; si++) {
-                int e = cost(pi, si);
-                if (e >= sorted[cutoff]) e = 50000;
-                m[pi + si * n] = e;
-            }
+    // GRF tries the cutoffs n, n + 5, ... in turn and keeps the first assignment that succeeds.
+    // Each solve is independent of the others, so the lanes of the match solve consecutive
+    // cutoffs together and the lowest that succeeds wins.
+    const int cutoffs = (unsigned)count > n ? (int)(((unsigned)count - 1 - n) / 5 + 1) : 0;
+    for (int c0 = 0; c0 < cutoffs; c0 += kGroupLanes) {
+        const int ci = c0 + GroupRank();
         int colOfRow[kTeamPlayers];
-        int total = HungarianSolve(m, (int)n, colOfRow);
-        if (total != -1 && (total < 50000 || cutoff >= (unsigned)count - 5)) {
+        bool ok = false;
+        if (ci < cutoffs) {
+            const unsigned cutoff = n + 5 * (unsigned)ci;
+            // A row is a formation slot, a column a player.
+            int m[kTeamPlayers * kTeamPlayers];
             for (unsigned pi = 0; pi < n; pi++)
-                for (unsigned si = 0; si < n; si++)
-                    if (colOfRow[si] == (int)pi) {
-                        const StaticFormation &f = Formation(w, c, ps[si]);
-                        FormationEntry &e = w.match.players[ps[pi]].dynamicFormationEntry;
-                        e.role = f.role;
-                        e.position = f.position;
-                        e.startPosition = f.startPosition;
-                        e.lazy = f.lazy;
-                        e.controllable = f.controllable;
-                    }
-            break;
+                for (unsigned si = 0; si < n; si++) {
+                    int e = costs[pi * n + si];
+                    if (e >= sorted[cutoff]) e = 50000;
+                    m[pi + si * n] = e;
+                }
+            const int total = HungarianSolve(m, (int)n, colOfRow);
+            ok = total != -1 && (total < 50000 || cutoff >= (unsigned)count - 5);
         }
+        const uint32_t solved = GroupBallot(ok);
+        if (!solved) continue;
+        const int from = LowestBit(solved);
+        int chosen[kTeamPlayers];
+        for (unsigned si = 0; si < n; si++) chosen[si] = GroupShuffle((int32_t)colOfRow[si], from);
+        for (unsigned pi = 0; pi < n; pi++)
+            for (unsigned si = 0; si < n; si++)
+                if (chosen[si] == (int)pi) {
+                    const StaticFormation &f = Formation(w, c, ps[si]);
+                    FormationEntry &e = w.match.players[ps[pi]].dynamicFormationEntry;
+                    e.role = f.role;
+                    e.position = f.position;
+                    e.startPosition = f.startPosition;
+                    e.lazy = f.lazy;
+                    e.controllable = f.controllable;
+                }
+        break;
     }
     return true;
 }

@@ -14,22 +14,8 @@ struct BallSpatial {
 };
 
 // The cached ticks' shift: entries 2..399 take entries 3..400, as the ticks copy them one after
-// another in increasing order. The lanes of the match copy four entries each per round, all reads
-// of a round before its writes (a lane's first entry overwrites the last one the lane before it
-// reads).
-HD void ShiftPredictions(Ball &ball) {
-    constexpr int kFirst = 2, kCount = 398, kPerLane = 4;
-    for (int base = 0; base < kCount; base += kPerLane * kGroupLanes) {
-        const int first = base + GroupRank() * kPerLane;
-        Vec3 v[kPerLane];
-        for (int j = 0; j < kPerLane; j++)
-            if (first + j < kCount) v[j] = ball.predictions[kFirst + first + j + 1];
-        GroupSync();
-        for (int j = 0; j < kPerLane; j++)
-            if (first + j < kCount) ball.predictions[kFirst + first + j] = v[j];
-        GroupSync();
-    }
-}
+// another in increasing order.
+HD void ShiftPredictions(Ball &ball) { GroupShiftDown<4>(ball.predictions + 2, 398); }
 
 // Entry k of `predictions` is the position after 10k ms. When the first step lands where the last
 // tick predicted, the predictions shift down one entry instead, at most `validPredictions` times.
@@ -227,7 +213,7 @@ HDN void BallProcess(Ball &b, bool inGoal) {
     if (h.count < (int)kBallHistorySize) {
         h.push_back(b.positionBuffer);
     } else {
-        for (int i = 1; i < h.count; i++) h[i - 1] = h[i];
+        GroupShiftDown<4>(h.e, h.count - 1);
         h[h.count - 1] = b.positionBuffer;
     }
 }
@@ -640,7 +626,7 @@ HDN void BallTouch(World &w, const Ctx &c, const Vec3 &target) {
     if (w.match.mentalImages.count > 0) {
         MentalImage &m = w.match.mentalImages[0];
         m.ballPredictions.count = kBallPredictionSpanMs / 10;
-        for (int i = 0; i < (int)(kBallPredictionSpanMs / 10); i++) m.ballPredictions[i] = b.predictions[i];
+        GroupCopy<4>(m.ballPredictions.e, b.predictions, (int)(kBallPredictionSpanMs / 10));
         m.lazyFlip = b.lazyFlip;
     }
     TeamUpdatePossessionStatistics(w, c, w.FirstTeamID());

@@ -41,7 +41,7 @@ HDN void UpdateInGameCamera(World &w, const Ctx &c) {
     auto &cp = m.cameraPosition;
     Vec3 add = bp + shudder * ((float)cp.count / (float)kCameraHistory);
     if (cp.count == kCameraHistory) {
-        for (int i = 0; i + 1 < cp.count; i++) cp[i] = cp[i + 1];
+        GroupShiftDown<4>(cp.e, cp.count - 1);
         cp[cp.count - 1] = add;
     } else {
         cp.push_back(add);

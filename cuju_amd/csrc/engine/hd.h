@@ -169,6 +169,36 @@ HD void GroupSync() {
     __builtin_amdgcn_wave_barrier();
 #endif
 }
+// dst[i] = src[i] for i below `count`, for arrays that do not overlap; the lanes of the match take
+// `Run` entries each per round. Every lane of the match calls it; it ends synchronized.
+template <int Run, class T>
+HD void GroupCopy(T *dst, const T *src, int count) {
+    for (int base = GroupRank() * Run; base < count; base += Run * kGroupLanes) {
+        T v[Run];
+        for (int j = 0; j < Run; j++)
+            if (base + j < count) v[j] = src[base + j];
+        for (int j = 0; j < Run; j++)
+            if (base + j < count) dst[base + j] = v[j];
+    }
+    GroupSync();
+}
+// a[i] = a[i + 1] for i from 0 to count - 1, as a loop in increasing i leaves it. The lanes of the
+// match copy `Run` entries each per round, every read of a round before its writes (a lane's first
+// entry overwrites the last one the lane before it reads), so the reads of a round overlap in
+// flight instead of following one another. Every lane of the match calls it.
+template <int Run, class T>
+HD void GroupShiftDown(T *a, int count) {
+    for (int base = 0; base < count; base += Run * kGroupLanes) {
+        const int first = base + GroupRank() * Run;
+        T v[Run];
+        for (int j = 0; j < Run; j++)
+            if (first + j < count) v[j] = a[first + j + 1];
+        GroupSync();
+        for (int j = 0; j < Run; j++)
+            if (first + j < count) a[first + j] = v[j];
+        GroupSync();
+    }
+}
 
 // x86-64 float-to-integer conversions (cvttss2si / cvttsd2si), which GRF's build performs. NaN and
 // out-of-range inputs give the "integer indefinite" value where a GPU conversion would saturate.

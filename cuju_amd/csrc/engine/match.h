@@ -37,7 +37,7 @@ HDN void PushMentalImage(World &w) {
     }
     const int np = kBallPredictionSpanMs / 10;
     mi.ballPredictions.count = np;
-    for (int i = 0; i < np; i++) mi.ballPredictions[i] = m.ball.predictions[i];
+    GroupCopy<4>(mi.ballPredictions.e, m.ball.predictions, np);
     mi.lazyFlip = m.ball.lazyFlip;
     w.flags.mentalBallMirrored[0] = false;
     m.mentalImages.count = n;
@@ -172,7 +172,7 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
         sv += (TeamByID(w, 1).fadingTeamPossessionAmount - 0.5f) * TeamDynamicSide(w, 1);
         auto &h = m.possessionSideHistory;
         if (h.count == 600) {
-            for (int i = 0; i + 1 < h.count; i++) h[i] = h[i + 1];
+            GroupShiftDown<8>(h.e, h.count - 1);
             h[h.count - 1] = sv;
         } else {
             h.push_back(sv);

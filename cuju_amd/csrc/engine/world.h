@@ -175,10 +175,26 @@ HD void MirrorBall(Ball &b) {
     b.lazyFlip = !b.lazyFlip;
     b.positionBuffer.Mirror();
 }
+// Negates x and y of `count` stored vectors; the lanes of the match take four entries each per
+// round, so their reads overlap in flight. Every lane of the match calls it.
+HD void MirrorStored(Vec3 *a, int count) {
+    constexpr int kRun = 4;
+    for (int base = GroupRank() * kRun; base < count; base += kRun * kGroupLanes) {
+        Vec3 v[kRun];
+        for (int j = 0; j < kRun; j++)
+            if (base + j < count) v[j] = a[base + j];
+        for (int j = 0; j < kRun; j++)
+            if (base + j < count) {
+                v[j].Mirror();
+                a[base + j] = v[j];
+            }
+    }
+}
 HD void BallMaterialize(Ball &b) {
     if (!b.lazyFlip) return;
-    for (int i = 0; i < 401; i++) b.predictions[i].Mirror();
-    for (int i = 0; i < b.positionHistory.count; i++) b.positionHistory[i].Mirror();
+    MirrorStored(b.predictions, 401);
+    MirrorStored(b.positionHistory.e, b.positionHistory.count);
+    GroupSync();
     b.lazyFlip = false;
 }
 HD void MentalMaterialize(MentalImage &m) {

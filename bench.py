@@ -5,8 +5,9 @@ with all 11 left players under agents (the right team is the built-in AI at diff
 3,000-step episodes, `simple115v2` observations [16384, 11, 115] and automatic resets. A step is
 one `BatchEnvironment.step` of every environment. Actions are uniform integers in [0, 19) from a
 counter-based hash of (seed, step, environment, agent), computed on the device inside the timed
-loop (a few microseconds). The value is environment steps per second over the timed steps, with
-the inputs resident in HBM.
+loop (a few microseconds). As the reference's benchmark does, the first 100 steps after the reset
+are discarded: early steps are cheaper (few stoppages, short histories). The value is environment
+steps per second over the timed steps, with the inputs resident in HBM.
 
 Beside it the line reports the roofline of the step kernel (algorithmic HBM bytes per launch over
 its measured duration, against 8 TB/s) and the reference's own CPU thread pool on this host's
@@ -48,8 +49,9 @@ def counter_actions(torch, seed, step, environments, agents, device):
     return (x % ACTIONS).to(torch.int32)
 
 
-def cpu_baseline(environments, steps, seed):
-    """The reference CPU library (its own thread pool, every core it may use) on a sample."""
+def cpu_baseline(environments, steps, warmup, seed):
+    """The reference CPU library (its own thread pool, every core it may use) on a sample, timed
+    after the same warm-up as the device."""
     from oracle import ref
     import numpy as np
     if not os.path.isfile(ref.LIBRARY):
@@ -57,8 +59,9 @@ def cpu_baseline(environments, steps, seed):
     batch = ref.ReferenceBatch(ASSETS, environment_count=environments, seed=seed, threads=0)
     batch.reset()
     rng = np.random.default_rng(seed)
-    actions = [rng.integers(0, ACTIONS, size=(environments, AGENTS), dtype=np.int32) for _ in range(steps + 1)]
-    batch.step(actions[-1])
+    for _ in range(warmup):
+        batch.step(rng.integers(0, ACTIONS, size=(environments, AGENTS), dtype=np.int32))
+    actions = [rng.integers(0, ACTIONS, size=(environments, AGENTS), dtype=np.int32) for _ in range(steps)]
     start = time.perf_counter()
     for step in range(steps):
         batch.step(actions[step])
@@ -66,18 +69,18 @@ def cpu_baseline(environments, steps, seed):
     threads = batch.threads
     batch.close()
     return {'value': environments * steps / seconds, 'unit': 'env_steps/s', 'cores': threads, 'kind': 'reference',
-            'sample': f'{environments} environments of {ASSETS}, {steps} timed steps after a reset and one warm-up '
-                      f'step, uniform random actions'}
+            'sample': f'{environments} environments of {ASSETS}, {steps} timed steps after a reset and {warmup} '
+                      f'warm-up steps, uniform random actions'}
 
 
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument('--gpus', type=int, default=1)
     parser.add_argument('--steps', type=int, default=30)
-    parser.add_argument('--warmup', type=int, default=5)
+    parser.add_argument('--warmup', type=int, default=100)
     parser.add_argument('--environments', type=int, default=ENVIRONMENTS)
     parser.add_argument('--seed', type=int, default=0)
-    parser.add_argument('--cpu-environments', type=int, default=4096)
+    parser.add_argument('--cpu-environments', type=int, default=2048)
     parser.add_argument('--cpu-steps', type=int, default=60)
     parser.add_argument('--no-cpu', action='store_true')
     parser.add_argument('--matches', type=int, default=None, help='environments per workgroup (one wavefront)')
@@ -105,9 +108,12 @@ def main():
     reset_seconds = time.perf_counter() - start
     print(f'[bench] reset took {reset_seconds:.2f} s', file=sys.stderr, flush=True)
     step = 0
-    for _ in range(args.warmup):
+    for k in range(args.warmup):
         env.step(counter_actions(torch, args.seed, step, args.environments, AGENTS, device))
         step += 1
+        if k % 25 == 24:
+            env.synchronize()
+            print(f'[bench] {k + 1} warm-up steps', file=sys.stderr, flush=True)
     env.synchronize()
     print(f'[bench] {args.warmup} warm-up steps done', file=sys.stderr, flush=True)
 
@@ -142,7 +148,7 @@ def main():
     baseline = None
     if not args.no_cpu:
         print('[bench] timing the reference CPU thread pool', file=sys.stderr, flush=True)
-        baseline = cpu_baseline(args.cpu_environments, args.cpu_steps, args.seed)
+        baseline = cpu_baseline(args.cpu_environments, args.cpu_steps, args.warmup, args.seed)
 
     line = {
         'metric': 'env steps/sec on 1 MI355X (11v11, 16384 envs) + bit-exact digest match',

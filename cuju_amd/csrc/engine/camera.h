@@ -13,19 +13,28 @@ HD float CameraWeight(int index, int count) {
     return w;
 }
 
+// GRF updates the camera with team 1 mirrored. Of what the update reads, the mirror changes only
+// the positions of team 1's players (x and y negated) and team 1's side (negated), so it reads
+// those through `position` and `side` instead of mirroring the team there and back.
 HDN void UpdateInGameCamera(World &w, const Ctx &c) {
     MatchState &m = w.match;
     const int first = w.FirstTeamID(), second = 1 - first;
+    auto position = [&](int p) {
+        Vec3 v = Sp(w, p).position;
+        if (w.playerTeamID[p] == 1) v.Mirror();
+        return v;
+    };
+    auto side = [&](int t) { return t == 1 ? -TeamDynamicSide(w, t) : TeamDynamicSide(w, t); };
     const float fovDefault = 0.4f, zoomDefault = 0.5f, heightDefault = 0.3f, angleDefault = 0.0f;
     float fov = 0.5f + fovDefault * 0.5f;
     float zoom = zoomDefault;
     float height = heightDefault * 1.5f;
     float playerBias = 0.6f;
     const SpatialState &ds = Sp(w, m.designatedPossessionPlayer);
-    Vec3 bp = BallPredict(m.ball, 0) * (1.0f - playerBias) + ds.position * playerBias;
+    Vec3 bp = BallPredict(m.ball, 0) * (1.0f - playerBias) + position(m.designatedPossessionPlayer) * playerBias;
     bp += ds.directionVec * 1.0f;
-    bp += Vec3(((TeamByID(w, first).fadingTeamPossessionAmount - 1.0f) * -TeamDynamicSide(w, first) +
-                (TeamByID(w, second).fadingTeamPossessionAmount - 1.0f) * -TeamDynamicSide(w, second)) *
+    bp += Vec3(((TeamByID(w, first).fadingTeamPossessionAmount - 1.0f) * -side(first) +
+                (TeamByID(w, second).fadingTeamPossessionAmount - 1.0f) * -side(second)) *
                    4.0f,
                0, 0);
     bp.v[2] *= 0.1f;
@@ -50,10 +59,21 @@ HDN void UpdateInGameCamera(World &w, const Ctx &c) {
     float n = 0;
     const int pc = cp.count;
     const float *table = c.t->cameraWeights + pc * (pc - 1) / 2;
-    for (int i = 0; i < pc; i++) {
-        float wt = table[i];
-        avg += cp[i] * wt;
-        n += wt;
+    // The sums run in order; the entries load eight at a time, so their loads overlap in flight.
+    constexpr int kChunk = 8;
+    for (int i0 = 0; i0 < pc; i0 += kChunk) {
+        float wt[kChunk];
+        Vec3 at[kChunk];
+        for (int j = 0; j < kChunk; j++)
+            if (i0 + j < pc) {
+                wt[j] = table[i0 + j];
+                at[j] = cp[i0 + j];
+            }
+        for (int j = 0; j < kChunk; j++)
+            if (i0 + j < pc) {
+                avg += at[j] * wt[j];
+                n += wt[j];
+            }
     }
     avg /= Vec3(n);
     float angleFactor = 1.0f - angleDefault * 0.4f;
@@ -72,7 +92,7 @@ HDN void UpdateInGameCamera(World &w, const Ctx &c) {
         m.cameraFarCap = 200;
     } else {
         Vec3 target = BallPredict(m.ball, 0).Get2D();
-        if (m.lastGoalScorer >= 0) target = Sp(w, m.lastGoalScorer).position;
+        if (m.lastGoalScorer >= 0) target = position(m.lastGoalScorer);
         float rot = (float)m.goalScoredTimer * 0.0005f;
         m.cameraOrientation.SetAngleAxis(0.45f * PI, Vec3(1, 0, 0));
         m.cameraNodeOrientation.SetAngleAxis(rot, Vec3(0, 0, 1));
@@ -83,15 +103,12 @@ HDN void UpdateInGameCamera(World &w, const Ctx &c) {
     }
 }
 
-// The camera works on the unmirrored pitch, so team 1 is mirrored around its update.
+// The camera works on the unmirrored pitch: GRF mirrors team 1 around its update, which
+// UpdateInGameCamera reads in place.
 HDN void UpdateCamera(World &w, const Ctx &c) {
     ENG_SCOPE(19);
     MatchState &m = w.match;
-    if (m.autoUpdateInGameCamera) {
-        MirrorMatch(w, false, true, false);
-        UpdateInGameCamera(w, c);
-        MirrorMatch(w, false, true, false);
-    }
+    if (m.autoUpdateInGameCamera) UpdateInGameCamera(w, c);
     const unsigned zoomTime = 2000, startTime = 0;
     if (m.actualTimeMs < zoomTime + startTime) {
         Quat init(0, 0, 0, 1);

@@ -98,6 +98,17 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
     ok = true;
     const bool rev = w.scenario.reverseTeamProcessing;
     const int first = w.FirstTeamID(), second = 1 - first;
+    // Between the set piece's preparation and its start a tick only advances the clocks: the
+    // referee touches nothing that a team frame changes, so the frame changes around it, which
+    // cancel exactly, are left out.
+    {
+        const RefereeBuffer &rb = m.referee.buffer;
+        if (!m.inPlay && !m.inSetPiece && rb.active && rb.prepareTime + 10 < m.actualTimeMs && rb.startTime != m.actualTimeMs) {
+            if (!RefereeProcess(w, c)) return ok = false;
+            BumpActualTime(w, c, 10);
+            return false;
+        }
+    }
     MirrorMatch(w, rev, !rev, rev);
     if (m.inPlay && !CheckBallCollisions(w, c)) return ok = false;
     if (!RefereeProcess(w, c)) return ok = false;

@@ -555,6 +555,18 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &query, AList &out) {
     GroupSync();
 }
 
+// The crude query of GetIdleMovementAnimationID: movement from idle to idle.
+HD CrudeQuery IdleMovementQuery() {
+    CrudeQuery q;
+    q.byFunctionType = true;
+    q.functionType = kFnMovement;
+    q.byIncomingVelocity = true;
+    q.incomingVelocity = kVelIdle;
+    q.byOutgoingVelocity = true;
+    q.outgoingVelocity = kVelIdle;
+    return q;
+}
+
 // Directions relative to the humanoid's angle; velocities are categories.
 struct Predicates {
     int desiredFoot = 0;
@@ -806,21 +818,51 @@ struct Selector {
     HD int FirstOfSortChain(const AList &l, int keyCount, KeysFn keys) {
         ENG_SCOPE(34);
         if (l.count < 2) return l[0];
+        // The first element with the least keys. The lanes of the match each take every
+        // kGroupLanes-th element, keeping their first least, and combine in element order: the
+        // same element for keys that order totally. A NaN key (which the host build rejects)
+        // takes the sequential scan.
         int best = -1;
         double bk[kMaxChainKeys];
-        for (int e = 0; e < l.count; e++) {
+        bool nan = false;
+        for (int e = GroupRank(); e < l.count; e += kGroupLanes) {
             double k[kMaxChainKeys];
             keys((int)l[e], k);
-#if !ENG_DEVICE
             for (int j = 0; j < keyCount; j++)
-                if (k[j] != k[j]) Fatal("an animation sort key is NaN");
+                if (k[j] != k[j]) nan = true;
+#if !ENG_DEVICE
+            if (nan) Fatal("an animation sort key is NaN");
 #endif
             if (best < 0 || ChainPrecedes(k, bk, keyCount)) {
                 best = e;
                 for (int j = 0; j < keyCount; j++) bk[j] = k[j];
             }
         }
-        return l[best];
+        if (GroupBallot(nan)) {
+            best = -1;
+            for (int e = 0; e < l.count; e++) {
+                double k[kMaxChainKeys];
+                keys((int)l[e], k);
+                if (best < 0 || ChainPrecedes(k, bk, keyCount)) {
+                    best = e;
+                    for (int j = 0; j < keyCount; j++) bk[j] = k[j];
+                }
+            }
+            return l[best];
+        }
+        int winner = -1;
+        double wk[kMaxChainKeys];
+        for (int r = 0; r < kGroupLanes; r++) {
+            const int e = GroupShuffle((int32_t)best, r);
+            if (e < 0) continue;
+            double k[kMaxChainKeys];
+            for (int j = 0; j < keyCount; j++) k[j] = GroupShuffle(bk[j], r);
+            if (winner < 0 || ChainPrecedes(k, wk, keyCount) || (!ChainPrecedes(wk, k, keyCount) && e < winner)) {
+                winner = e;
+                for (int j = 0; j < keyCount; j++) wk[j] = k[j];
+            }
+        }
+        return l[winner];
     }
 
     HD bool AllowLastDitch(bool withPossessionAmount = true) {
@@ -890,15 +932,8 @@ struct Selector {
     }
 
     HDN int GetIdleMovementAnimationID() {
-        CrudeQuery q;
-        q.byFunctionType = true;
-        q.functionType = kFnMovement;
-        q.byIncomingVelocity = true;
-        q.incomingVelocity = kVelIdle;
-        q.byOutgoingVelocity = true;
-        q.outgoingVelocity = kVelIdle;
-        AList l{c.ws->lists[1], 0};
-        CrudeSelection(c, q, l);
+        // The crude selection of IdleMovementQuery, made once from the tables; only read here.
+        const AList l{const_cast<int16_t *>(c.t->idleMovement), c.t->idleMovementCount};
         pred.idle = 1;
         pred.relIncomingBodyDirection = Vec3(0, -1, 0);
         pred.incomingVelocity = kVelIdle;

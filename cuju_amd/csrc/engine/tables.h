@@ -298,6 +298,10 @@ struct Tables {
     const CrudeRecord *crudeBody;
     const int32_t *crudeBodyOffset;
     const float *cameraWeights;
+    // The crude selection of idle movement in and out (GetIdleMovementAnimationID), which reads
+    // only the tables: one list for every call.
+    const int16_t *idleMovement;
+    int32_t idleMovementCount;
 };
 
 // The walk that GRF's time-to-target estimate takes from a moving player (ai_time.h:170-200):

@@ -1239,9 +1239,7 @@ struct Selector {
         if (DesiredTimeToBallMs() > (int)ttb) ttb = (uint32_t)DesiredTimeToBallMs();
         uint32_t animMs = (uint32_t)a.frameCount * 10;
         uint32_t future = animMs + kDefaultTouchOffsetMs > ttb ? animMs + kDefaultTouchOffsetMs : ttb;
-        PList pl{c.ws->plans[1], 0};
-        for (int i = 0; i < cur.positions.count; i++) pl[pl.count++] = cur.positions[i];
-        Vec3 predOut = OutgoingMovementOf(pl);
+        Vec3 predOut = OutgoingMovementOf(PList{cur.positions.e, cur.positions.count});
         Vec3 predPos;
         float predAngle;
         CalculatePredictedSituation(predPos, predAngle);
@@ -1591,8 +1589,9 @@ struct Selector {
         cur.movementSmuggleOffset = Vec3(0);
         cur.incomingMovement = s.movement;
         cur.outgoingMovement = OutgoingMovementOf(positions);
-        cur.positions.count = 0;
-        for (int i = 0; i < positions.count; i++) cur.positions.push_back(positions[i]);
+        // The plan fits the list: both hold kAnimPositions entries.
+        GroupCopy<4>(cur.positions.e, positions.e, positions.count);
+        cur.positions.count = positions.count;
         cur.positionOffset = Vec3(0);
         cur.originatingCommand = cmd;
     }

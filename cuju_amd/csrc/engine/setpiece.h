@@ -50,8 +50,10 @@ HDN bool HumanoidResetPosition(World &w, const Ctx &c, int hi, const Vec3 &pos, 
     AnimationState &cur = h.anim;
     cur.id = idle;
     cur.anim = idle;
-    cur.positions.count = 0;
-    for (int i = 0; i < ia.posCount; i++) cur.positions.push_back(c.t->positions[ia.posFirst + i]);
+    if (ia.posCount > cur.positions.kCapacity) Unsupported("a state list outgrows its capacity");
+    const int copied = ia.posCount < cur.positions.kCapacity ? ia.posCount : cur.positions.kCapacity;
+    GroupCopy<4>(cur.positions.e, c.t->positions + ia.posFirst, copied);
+    cur.positions.count = copied;
     // GRF: the frame draws below the effective frame count, one less than the frame count.
     cur.frameNum = TruncToInt32(RandomInRange(w, 0, (float)(ia.frameCount - 1 - 1)));
     cur.touchFrame = -1;

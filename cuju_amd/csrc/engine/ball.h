@@ -620,9 +620,12 @@ HDN void BallTouch(World &w, const Ctx &c, const Vec3 &target) {
     b.validPredictions = 0;
     if (b.positionBuffer.v[2] < 0.11f) b.positionBuffer.v[2] = 0.11f;
     b.momentum = target;
-    // GRF: the predictions run twice, and each run changes the count of valid cached ones.
+    // GRF: the predictions run twice, and each run changes the count of valid cached ones. The
+    // second run starts from the same ball, so its first step lands on the first run's entry 1:
+    // unless that equals entry 2 (the cached path, which shifts), it recomputes exactly what the
+    // first run left, and is skipped.
     BallRecalculatePrediction(w);
-    BallRecalculatePrediction(w);
+    if (b.validPredictions > 0 && b.predictions[2] == b.predictions[1]) BallRecalculatePrediction(w);
     if (w.match.mentalImages.count > 0) {
         MentalImage &m = w.match.mentalImages[0];
         m.ballPredictions.count = kBallPredictionSpanMs / 10;
@@ -633,7 +636,9 @@ HDN void BallTouch(World &w, const Ctx &c, const Vec3 &target) {
     TeamUpdatePossessionStatistics(w, c, 1 - w.FirstTeamID());
 }
 
-HD void BallSetRotation(World &w, float x, float y, float z, float bias = 1.0f) {
+// With `predict` false the predictions stay as they are, for a caller whose next step recomputes
+// every output of the prediction before anything reads it.
+HD void BallSetRotation(World &w, float x, float y, float z, float bias = 1.0f, bool predict = true) {
     Quat rx, ry, rz;
     rx.SetAngleAxis(Clamp(x * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(-1, 0, 0));
     ry.SetAngleAxis(Clamp(y * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(0, 1, 0));
@@ -641,7 +646,7 @@ HD void BallSetRotation(World &w, float x, float y, float z, float bias = 1.0f) 
     Quat tmp = rx * ry * rz;
     Ball &b = w.match.ball;
     b.rotationPerMs = b.rotationPerMs.Slerp(bias, tmp);
-    BallRecalculatePrediction(w);
+    if (predict) BallRecalculatePrediction(w);
 }
 
 HD void BallSetPosition(World &w, const Vec3 &target) {

@@ -499,7 +499,9 @@ HDN bool HumanoidProcessEnd(World &w, const Ctx &c, int p) {
             DeriveNodes(sk, h.nodes, der);
             const Derived &node = der[sk.nodeMap[bp]];
             BallTouch(w, c, Vec3(0));
-            BallSetRotation(w, 0, 0, 0, 1.0f);
+            // BallSetPosition predicts again from its own position before anything reads the
+            // predictions, so this rotation's prediction is left out.
+            BallSetRotation(w, 0, 0, 0, 1.0f, false);
             BallSetPosition(w, node.position + node.rotation * Vec3(0, 0, -0.36f));
             if (!TeamSetLastTouchPlayer(w, c, p, kTouchNonKicked)) return false;
         } else {

@@ -19,8 +19,33 @@ HD void ShiftPredictions(Ball &ball) { GroupShiftDown<4>(ball.predictions + 2, 3
 
 // Entry k of `predictions` is the position after 10k ms. When the first step lands where the last
 // tick predicted, the predictions shift down one entry instead, at most `validPredictions` times.
+HD bool SameBits(const Vec3 &a, const Vec3 &b) {
+    return BitsOf(a.v[0]) == BitsOf(b.v[0]) && BitsOf(a.v[1]) == BitsOf(b.v[1]) && BitsOf(a.v[2]) == BitsOf(b.v[2]);
+}
+HD bool SameBits(const Quat &a, const Quat &b) {
+    return BitsOf(a.q[0]) == BitsOf(b.q[0]) && BitsOf(a.q[1]) == BitsOf(b.q[1]) && BitsOf(a.q[2]) == BitsOf(b.q[2]) &&
+           BitsOf(a.q[3]) == BitsOf(b.q[3]);
+}
+
+// The prediction is a function of the ball's position, orientation, momentum and rotation and of
+// whether it is in the goal. When those match the last full prediction bit for bit, its first step
+// lands on entry 1; unless the cached path applies, the full path would write exactly what the
+// arrays already hold, so only its other results are restored.
 HDN BallSpatial BallCalculatePrediction(Ball &ball, bool ballIsInGoal) {
     ENG_SCOPE(37);
+    if (ball.memoValid && ball.memoInGoal == ballIsInGoal && SameBits(ball.memoPosition, ball.positionBuffer) &&
+        SameBits(ball.memoMomentum, ball.momentum) && SameBits(ball.memoOrientation, ball.orientationBuffer) &&
+        SameBits(ball.memoRotation, ball.rotationPerMs) &&
+        !(ball.validPredictions > 0 && ball.predictions[2] == ball.predictions[1])) {
+        ball.validPredictions = kCachedPredictions;
+        ball.touchesNet = ball.memoTouchesNet;
+        BallSpatial out;
+        out.momentum = ball.memoOutMomentum;
+        out.rotationPerMs = ball.memoOutRotation;
+        return out;
+    }
+    const Vec3 inPosition = ball.positionBuffer, inMomentum = ball.momentum;
+    const Quat inOrientation = ball.orientationBuffer, inRotation = ball.rotationPerMs;
     const float bounce = 0.62f, linearBounce = 0.06f, drag = 0.015f, friction = 0.04f,
                 linearFriction = 1.6f, gravity = -9.81f, grassHeight = 0.025f, dt = 0.01f;
     BallSpatial out;
@@ -192,6 +217,17 @@ HDN BallSpatial BallCalculatePrediction(Ball &ball, bool ballIsInGoal) {
         }
         ball.predictions[t / 10] = nextPos;
         firstTime = false;
+    }
+    ball.memoValid = !useCache;
+    if (!useCache) {
+        ball.memoInGoal = ballIsInGoal;
+        ball.memoTouchesNet = ball.touchesNet;
+        ball.memoPosition = inPosition;
+        ball.memoMomentum = inMomentum;
+        ball.memoOrientation = inOrientation;
+        ball.memoRotation = inRotation;
+        ball.memoOutMomentum = out.momentum;
+        ball.memoOutRotation = out.rotationPerMs;
     }
     return out;
 }

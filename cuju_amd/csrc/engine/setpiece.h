@@ -201,6 +201,7 @@ HD void BallResetSituation(Ball &b, const Vec3 &focus) {
     b.momentum = Vec3(0);
     b.rotationPerMs = Quat();
     for (int i = 0; i < kBallPredictionSpanMs / 10; i++) b.predictions[i] = focus + Vec3(0, 0, 0.11f);
+    b.memoValid = false;
     b.orientationPrediction = Quat();
     b.positionHistory.count = 0;
     b.positionBuffer = focus + Vec3(0, 0, 0.11f);

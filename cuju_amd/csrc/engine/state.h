@@ -310,6 +310,12 @@ struct Ball {
     Quat orientationBuffer;
     bool touchesNet;
     bool lazyFlip;  // not in the state: predictions and history hold negated x and y
+    // Not in the state: the inputs and first-step results of the last full prediction, which a
+    // prediction from the same inputs recomputes bit for bit. Every other write of `predictions`
+    // clears `memoValid`.
+    bool memoValid, memoInGoal, memoTouchesNet;
+    Vec3 memoPosition, memoMomentum, memoOutMomentum;
+    Quat memoOrientation, memoRotation, memoOutRotation;
 };
 
 struct RefereeBuffer {

@@ -28,7 +28,7 @@ CXX = os.environ.get('CXX', 'g++')
 PRODUCT = os.path.join(OUT, 'libcuju_amd.so')
 HOST = os.path.join(OUT, 'libcuju_amd_host.so')
 
-HOST_SOURCES = ['host/assets.cpp', 'host/runtime.cpp', 'host/api.cpp']
+HOST_SOURCES = ['host/assets.cpp', 'host/runtime.cpp', 'host/api.cpp', 'host/scenario.cpp']
 COMMON = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math', '-fvisibility=hidden', '-w']
 # Packed FP32 instructions stay off: plain float code only. -O2 measured about 1% faster than -O3
 # for the step kernel on gfx950 (289 against 292 ms per step at 16,384 environments). Runtime

@@ -2,12 +2,14 @@
 // (cited per function in include/cuju_amd.h) with its argument meaning and error convention:
 // -1 or null with a per-thread message, -2 for an action out of range.
 #include <cstring>
+#include <fstream>
 #include <exception>
 #include <stdexcept>
 #include <string>
 
 #include "../../../include/cuju_amd.h"
 #include "runtime.h"
+#include "scenario.h"
 
 namespace eng {
 namespace host {
@@ -210,6 +212,53 @@ void *cuju_environment_buffer(void *e, const char *name) {
     void *p = Of(e)->Buffer(name ? name : "");
     if (!p) lastError = std::string("no buffer named ") + (name ? name : "(null)");
     return p;
+}
+
+int cuju_scenario_build_bundle(const struct cuju_scenario_description *even, const struct cuju_scenario_description *odd,
+                               const char *name, const char *animations, const char *out) {
+    try {
+        if (!even || !odd || !name || !animations || !out) throw std::invalid_argument("expected two descriptions, a name and two paths");
+        const cuju_scenario_description *sources[2] = {even, odd};
+        eng::host::ScenarioDescription parity[2];
+        for (int i = 0; i < 2; i++) {
+            const cuju_scenario_description &s = *sources[i];
+            if (s.version != CUJU_SCENARIO_VERSION)
+                throw std::invalid_argument("expected the scenario description version " + std::to_string(CUJU_SCENARIO_VERSION) +
+                                            ", found " + std::to_string(s.version));
+            if (s.left_size < 0 || s.right_size < 0) throw std::invalid_argument("expected team sizes of zero or more");
+            if ((s.left_size > 0 && !s.left_team) || (s.right_size > 0 && !s.right_team)) throw std::invalid_argument("expected the players of each team");
+            eng::host::ScenarioDescription &d = parity[i];
+            d.ballX = s.ball_x;
+            d.ballY = s.ball_y;
+            for (int side = 0; side < 2; side++) {
+                const cuju_scenario_player *players = side ? s.right_team : s.left_team;
+                std::vector<eng::host::ScenarioPlayer> &team = side ? d.rightTeam : d.leftTeam;
+                for (int p = 0, n = side ? s.right_size : s.left_size; p < n; p++)
+                    team.push_back({players[p].x, players[p].y, players[p].role, players[p].lazy != 0, players[p].controllable != 0});
+            }
+            d.useMagnet = s.use_magnet != 0;
+            d.offsides = s.offsides != 0;
+            d.realTime = s.real_time != 0;
+            d.leftTeamDifficulty = s.left_team_difficulty;
+            d.rightTeamDifficulty = s.right_team_difficulty;
+            d.deterministic = s.deterministic != 0;
+            d.endOnScore = s.end_episode_on_score != 0;
+            d.endOnPossessionChange = s.end_episode_on_possession_change != 0;
+            d.endOnOutOfPlay = s.end_episode_on_out_of_play != 0;
+            d.gameDuration = s.game_duration;
+            d.secondHalf = s.second_half;
+            d.controlAllPlayers = s.control_all_players != 0;
+            d.gameEngineRandomSeed = s.game_engine_random_seed;
+        }
+        const std::string bundle = eng::host::BuildScenarioBundle(name, parity, animations);
+        std::ofstream file(out, std::ios::binary);
+        if (!file) throw std::runtime_error(std::string("cannot write ") + out);
+        file.write(bundle.data(), (std::streamsize)bundle.size());
+        if (!file) throw std::runtime_error(std::string("cannot write ") + out);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
 }
 
 }  // extern "C"

@@ -368,6 +368,8 @@ void BuildSelection(AnimationTables &t) {
         for (int i = 0; i < n; i++) t.cameraWeights[n * (n - 1) / 2 + i] = CameraWeight(i, n);
 }
 
+}  // namespace
+
 std::vector<Skeleton> ParseSkeletons(const std::string &bytes) {
     if (bytes.compare(0, 7, "CUJHUM1") != 0) throw std::runtime_error("expected the skeletons of a bundle");
     Reader r(bytes, "the skeletons", 7);
@@ -441,8 +443,6 @@ StaticData ParseStatic(const std::string &b) {
     return sd;
 }
 
-}  // namespace
-
 std::string ScenarioKey(const World &w) {
     Scenario s = w.scenario;
     s.gameEngineRandomSeed = 0;
@@ -480,6 +480,8 @@ Tables AnimationTables::View() const {
     t.crudeBody = crudeBody.data();
     t.crudeBodyOffset = crudeBodyOffset.data();
     t.cameraWeights = cameraWeights.data();
+    t.idleMovement = idleMovement.data();
+    t.idleMovementCount = (int32_t)idleMovement.size();
     return t;
 }
 
@@ -490,6 +492,19 @@ std::unique_ptr<AnimationTables> LoadAnimationTables(const std::string &path) {
     BuildInterpolation(*t);
     BuildDerived(*t, p);
     BuildSelection(*t);
+    {
+        // The idle-movement candidates: the idle query has fixed inputs, so its crude selection
+        // runs once here instead of at every idle request.
+        const Tables view = t->View();
+        auto scratch = std::make_unique<Scratch>();
+        Ctx c{};
+        c.t = &view;
+        c.ws = scratch.get();
+        AList idle{scratch->lists[1], 0};
+        CrudeSelection(c, IdleMovementQuery(), idle);
+        if (idle.count < 1) throw std::invalid_argument("expected animations of idle movement");
+        t->idleMovement.assign(idle.e, idle.e + idle.count);
+    }
     return t;
 }
 

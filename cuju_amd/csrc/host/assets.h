@@ -36,10 +36,16 @@ struct AnimationTables {
     std::vector<CrudeRecord> crude, crudeByIndex, crudeVelocity, crudeBody;
     std::vector<int32_t> crudeVelocityOffset, crudeBodyOffset;
     std::vector<float> cameraWeights;
+    std::vector<int16_t> idleMovement;  // the crude selection of the idle query
     // Tables whose pointers index the vectors above.
     Tables View() const;
 };
 std::unique_ptr<AnimationTables> LoadAnimationTables(const std::string &path);
+
+// The sections of a bundle variant: the skeletons ("CUJHUM1") and the static data (the
+// PlayerData of every entry, then FORM, MDUR and SIDS).
+std::vector<Skeleton> ParseSkeletons(const std::string &bytes);
+StaticData ParseStatic(const std::string &bytes);
 
 // One team order and episode parity of a bundle.
 struct Variant {

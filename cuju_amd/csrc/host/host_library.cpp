@@ -86,6 +86,8 @@ extern const char *const kBackendName = "host";
 }  // namespace host
 }  // namespace eng
 
+#include <cmath>
+#include <cstring>
 #include <sstream>
 
 // The field layout of a state, one line per field: byte position, size and path. Tests use it to
@@ -160,5 +162,72 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_libm(int which
             case 5: out[i] = eng::libm::acosf(x[i]); break;
             default: out[i] = eng::libm::asinf(x[i]); break;
         }
+    }
+}
+
+// The description a scenario builder needs to rebuild a bundle's variant (reverse 0, `parity`),
+// read back from its template: the flags, difficulties and player entries as stored, and for
+// each coordinate the float whose scaling gives the stored value (any one does: the builder
+// reads the description only through that scaling). Tests rebuild the shipped bundles from it.
+#include "../../../include/cuju_amd.h"
+namespace {
+template <class F>
+float Preimage(float stored, double estimate, F scale) {
+    auto same = [&](float f) {
+        const float v = scale(f);
+        return memcmp(&v, &stored, sizeof(float)) == 0;
+    };
+    float up = (float)estimate, down = up;
+    if (same(up)) return up;
+    for (int k = 0; k < 32; k++) {
+        up = nextafterf(up, INFINITY);
+        if (same(up)) return up;
+        down = nextafterf(down, -INFINITY);
+        if (same(down)) return down;
+    }
+    throw std::runtime_error("no float scales to the stored coordinate");
+}
+}  // namespace
+extern "C" __attribute__((visibility("default"))) int cuju_debug_bundle_description(const char *path, int parity, cuju_scenario_description *out,
+                                                                                      cuju_scenario_player *left, cuju_scenario_player *right) {
+    try {
+        const auto bundle = eng::host::LoadBundle(path);
+        const eng::Scenario &s = bundle->variants[parity & 1].world->scenario;
+        memset(out, 0, sizeof(*out));
+        out->version = CUJU_SCENARIO_VERSION;
+        out->ball_x = Preimage(s.ballPosition.v[0], s.ballPosition.v[0] / 54.4, [](float f) { return (float)((double)f * 54.4); });
+        out->ball_y = Preimage(s.ballPosition.v[1], s.ballPosition.v[1] / -83.6, [](float f) { return (float)((double)f * -83.6); });
+        for (int side = 0; side < 2; side++) {
+            const eng::FormationEntry *team = side ? s.rightTeam : s.leftTeam;
+            const int n = side ? s.rightTeamSize : s.leftTeamSize;
+            cuju_scenario_player *players = side ? right : left;
+            for (int p = 0; p < n; p++) {
+                const eng::Vec3 &at = team[p].startPosition;
+                players[p].x = at.v[0];
+                players[p].y = Preimage(at.v[1], (double)at.v[1] / -2.36, [](float f) { return f * -2.36f; });
+                players[p].role = team[p].role;
+                players[p].lazy = team[p].lazy;
+                players[p].controllable = team[p].controllable;
+            }
+            (side ? out->right_size : out->left_size) = n;
+        }
+        out->left_team = left;
+        out->right_team = right;
+        out->use_magnet = s.useMagnet;
+        out->offsides = s.offsides;
+        out->real_time = s.realTime;
+        out->left_team_difficulty = s.leftDifficulty;
+        out->right_team_difficulty = s.rightDifficulty;
+        out->deterministic = s.deterministic;
+        out->end_episode_on_score = s.endOnScore;
+        out->end_episode_on_possession_change = s.endOnPossessionChange;
+        out->end_episode_on_out_of_play = s.endOnOutOfPlay;
+        out->game_duration = s.gameDuration;
+        out->second_half = s.secondHalf;
+        out->control_all_players = s.controlAllPlayers;
+        out->game_engine_random_seed = s.deterministic ? s.gameEngineRandomSeed : 42;
+        return 0;
+    } catch (...) {
+        return -1;
     }
 }

@@ -70,19 +70,8 @@ BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> dev
         dt.crudeBody = Upload(T.crudeBody);
         dt.crudeBodyOffset = Upload(T.crudeBodyOffset);
         dt.cameraWeights = Upload(T.cameraWeights);
-        {
-            // The idle-movement candidates, selected once on the host from the host tables.
-            const Tables hostTables = T.View();
-            auto scratch = std::make_unique<Scratch>();
-            Ctx hc{};
-            hc.t = &hostTables;
-            hc.ws = scratch.get();
-            AList idle{scratch->lists[1], 0};
-            CrudeSelection(hc, IdleMovementQuery(), idle);
-            if (idle.count < 1) throw std::invalid_argument("expected animations of idle movement");
-            dt.idleMovement = Upload(std::vector<int16_t>(idle.e, idle.e + idle.count));
-            dt.idleMovementCount = idle.count;
-        }
+        dt.idleMovement = Upload(T.idleMovement);
+        dt.idleMovementCount = (int32_t)T.idleMovement.size();
         const Tables *dTables = Upload(&dt, 1);
 
         std::vector<Ctx> contexts;

@@ -15,6 +15,7 @@ import os
 import pickle
 import re
 import struct
+import tempfile
 from typing import Any
 
 import numpy as np
@@ -34,12 +35,13 @@ MAXIMUM_AGENTS = 22
 
 
 def resolve_assets(name: str) -> tuple[str, tuple[int, int]]:
-    """`<scenario>_l<L>_r<R>` to a shipped bundle and the agents per side; a path stays a path.
+    """`<scenario>_l<L>_r<R>` to a shipped bundle and the agents per side; a path stays a path,
+    and a GRF scenario file (`.py`) gets one left agent, as GRF's `create_environment` gives it.
     The bundle with the fewest agents serves any counts (python/cuju/_batch/assets.py:39-68)."""
-    if os.path.sep in name or name.endswith('.cjb'):
-        if not os.path.isfile(name):
-            raise MissingFileError(f'no asset bundle at {name}')
-        return name, (-1, -1)
+    if os.path.isfile(name):
+        return name, ((1, 0) if name.endswith('.py') else (-1, -1))
+    if os.path.sep in name or '/' in name or name.endswith(('.cjb', '.py')):
+        raise MissingFileError(f'expected a scenario file or an asset bundle at {name!r}, found no file')
     directory = os.path.join(_library.DATA, 'assets')
     shipped = os.path.join(directory, name + '.cjb')
     if os.path.isfile(shipped):
@@ -156,6 +158,22 @@ class BatchEnvironment:
             raise ConfigurationError('expected the HIP library')
         names = [assets] if isinstance(assets, str) else list(assets)
         resolved = [resolve_assets(n) for n in names]
+        # A scenario file becomes an agentless bundle, built with this batch's animation tables;
+        # the library reads bundles at creation only, so a temporary one goes with the batch.
+        self._scenario_directory = None
+        for index, (path, pair) in enumerate(resolved):
+            if not path.endswith('.py'):
+                continue
+            from . import scenarios
+            if scenarios.cache_directory() is not None:
+                built = scenarios.cached_bundle(path, library=library, animations=animations)
+            else:
+                if self._scenario_directory is None:
+                    self._scenario_directory = tempfile.TemporaryDirectory(prefix='cuju_amd-')
+                stem = os.path.splitext(os.path.basename(path))[0]
+                built = scenarios.build_bundle(path, os.path.join(self._scenario_directory.name, f'{index}_{stem}_l0_r0.cjb'),
+                                               library=library, animations=animations)
+            resolved[index] = (built, pair)
         counts = [pair for _, pair in resolved]
         if agent_counts is not None:
             counts = [tuple(c) for c in agent_counts]

@@ -50,6 +50,27 @@ class Configuration(ctypes.Structure):
     ]
 
 
+class ScenarioPlayer(ctypes.Structure):
+    """`struct cuju_scenario_player` (src/scenario_api.h:22-28)."""
+    _fields_ = [('x', ctypes.c_double), ('y', ctypes.c_double), ('role', ctypes.c_int), ('lazy', ctypes.c_int),
+                ('controllable', ctypes.c_int)]
+
+
+class ScenarioDescription(ctypes.Structure):
+    """`struct cuju_scenario_description`, version 1 (src/scenario_api.h:30-47)."""
+    _fields_ = [
+        ('version', ctypes.c_int), ('ball_x', ctypes.c_double), ('ball_y', ctypes.c_double),
+        ('left_team', ctypes.POINTER(ScenarioPlayer)), ('left_size', ctypes.c_int),
+        ('right_team', ctypes.POINTER(ScenarioPlayer)), ('right_size', ctypes.c_int),
+        ('use_magnet', ctypes.c_int), ('offsides', ctypes.c_int), ('real_time', ctypes.c_int),
+        ('left_team_difficulty', ctypes.c_double), ('right_team_difficulty', ctypes.c_double),
+        ('deterministic', ctypes.c_int), ('end_episode_on_score', ctypes.c_int),
+        ('end_episode_on_possession_change', ctypes.c_int), ('end_episode_on_out_of_play', ctypes.c_int),
+        ('game_duration', ctypes.c_int), ('second_half', ctypes.c_int), ('control_all_players', ctypes.c_int),
+        ('game_engine_random_seed', ctypes.c_uint),
+    ]
+
+
 # Every entry point of include/cuju_amd.h: (name, result, arguments).
 P, I, U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_ulonglong
 SIGNATURES = [
@@ -78,6 +99,8 @@ SIGNATURES = [
     ('cuju_environment_set_stack', I, [P, I, ctypes.c_char_p, P, U64]),
     ('cuju_environment_raw_field', ctypes.c_char_p, [P, I, P, P, P]),
     ('cuju_environment_buffer', P, [P, ctypes.c_char_p]),
+    ('cuju_scenario_build_bundle', I, [ctypes.POINTER(ScenarioDescription), ctypes.POINTER(ScenarioDescription),
+                                       ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
 ]
 
 _loaded = {}

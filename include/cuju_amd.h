@@ -104,6 +104,42 @@ const char *cuju_environment_raw_field(void *environment, int field, int *type, 
    [E][A][smm_height][smm_width][4 * stack]), raw, final_raw, reward, done, score_reward */
 void *cuju_environment_buffer(void *environment, const char *name);
 
+/* The scenario builder (src/scenario_api.h:19-51). `cuju_scenario_build_bundle` refuses a
+   description of another version. */
+#define CUJU_SCENARIO_VERSION 1
+
+/* One `AddPlayer` call of a GRF scenario file (src/scenario_api.h:22-28): the start position in
+   environment coordinates, an `e_PlayerRole` from 0 (goalkeeper) to 9, and two flags. */
+struct cuju_scenario_player {
+    double x, y;
+    int role;
+    int lazy;
+    int controllable;
+};
+
+/* What a scenario file builds for one parity of the episode number, in the fields of GRF's
+   `ScenarioConfig` (src/scenario_api.h:30-47). An empty team is refused: the caller adds GRF's
+   lazy goalkeeper first. */
+struct cuju_scenario_description {
+    int version;
+    double ball_x, ball_y;
+    const struct cuju_scenario_player *left_team;
+    int left_size;
+    const struct cuju_scenario_player *right_team;
+    int right_size;
+    int use_magnet, offsides, real_time;
+    double left_team_difficulty, right_team_difficulty;
+    int deterministic, end_episode_on_score, end_episode_on_possession_change, end_episode_on_out_of_play;
+    int game_duration, second_half;
+    int control_all_players;
+    unsigned int game_engine_random_seed;
+};
+
+/* src/scenario_api.h:52; writes the agentless bundle of a scenario (its even and odd episodes) to
+   `out`, with the animation tables at `animations`; 0, or -1 with cuju_last_error() */
+int cuju_scenario_build_bundle(const struct cuju_scenario_description *even, const struct cuju_scenario_description *odd,
+                               const char *name, const char *animations, const char *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -140,7 +140,10 @@ def observation_bytes(observation):
 
 def resolve_asset(name: str):
     """`<scenario>_l<L>_r<R>` to the shipped bundle and the agents per side
-    (`python/cuju/_batch/assets.py:39-68`): the bundle with the fewest agents serves any counts."""
+    (`python/cuju/_batch/assets.py:39-68`): the bundle with the fewest agents serves any counts.
+    The path of a bundle file keeps its own agents."""
+    if os.path.isfile(name):
+        return name, (-1, -1)
     directory = os.path.join(DATA, 'assets')
     shipped = os.path.join(directory, name + '.cjb')
     if os.path.isfile(shipped):

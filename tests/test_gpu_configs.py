@@ -12,14 +12,17 @@ sides consume identical inputs:
 4. `11_vs_11_stochastic_l11_r11`, both sides controlled, 4-frame stacked observations, 10% of the
    environments reset every 40 steps with fresh int64 seeds.
 5. A mixed batch: half `academy_3_vs_1_with_keeper_l3_r0` drills, a quarter `5_vs_5_l4_r0`, a
-   quarter `11_vs_11_stochastic_l1_r0`.
+   quarter `11_vs_11_stochastic_l1_r0`; and the same mix with the drills of a GRF scenario file
+   (three attackers 25 m out), built by the scenario builder.
 """
+
+import os
 
 import numpy as np
 import pytest
 import torch
 
-from conftest import PRODUCT
+from conftest import PRODUCT, ROOT
 from oracle import ref
 
 pytestmark = pytest.mark.gpu
@@ -46,11 +49,12 @@ def host(x):
     return x.detach().cpu().numpy()
 
 
-def compare(assets, environments, steps, seed=0, reset_every=None, states=True, **options):
+def compare(assets, environments, steps, seed=0, reset_every=None, states=True, their_assets=None, **options):
     import cuju_amd
     mine = cuju_amd.BatchEnvironment(assets, library=PRODUCT, device='cuda:0', environment_count=environments,
                                      seed=seed, **options)
-    theirs = ref.ReferenceBatch(assets, environment_count=environments, seed=seed, threads=0, **options)
+    theirs = ref.ReferenceBatch(their_assets or assets, environment_count=environments, seed=seed, threads=0,
+                                **options)
     try:
         assert host(mine.reset()).tobytes() == theirs.reset().tobytes(), 'reset'
         agents = theirs.agents
@@ -93,3 +97,13 @@ def test_config5_mixed_batch(reference_library):
     assignment = [0, 0, 1, 2] * 16
     compare(['academy_3_vs_1_with_keeper_l3_r0', '5_vs_5_l4_r0', '11_vs_11_stochastic_l1_r0'], 64, 150,
             seed=5, assignment=assignment)
+
+
+def test_config5_drills_from_a_scenario_file(reference_library, tmp_path):
+    from cuju_amd import scenarios
+    source = os.path.join(ROOT, 'tests', 'golden', 'scenarios', 'drill_3_vs_1_with_keeper.py')
+    bundle = scenarios.build_bundle(source, str(tmp_path / 'drill_l0_r0.cjb'))
+    others = ['5_vs_5_l0_r0', '11_vs_11_stochastic_l0_r0']
+    assignment = [0, 0, 1, 2] * 16
+    compare([source] + others, 64, 150, seed=9, assignment=assignment, their_assets=[bundle] + others,
+            agent_counts=[(3, 0), (4, 0), (1, 0)])

@@ -214,6 +214,16 @@ void *cuju_environment_buffer(void *e, const char *name) {
     return p;
 }
 
+int cuju_environment_episode(void *e, int index, long long *values, float *difficulty) {
+    try {
+        if (!values) throw std::invalid_argument("expected room for the episode values");
+        Of(e)->Episode(index, values, difficulty);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
+const char *cuju_environment_scenario(void *e, int bundle) { return Of(e)->ScenarioName(bundle); }
 int cuju_scenario_build_bundle(const struct cuju_scenario_description *even, const struct cuju_scenario_description *odd,
                                const char *name, const char *animations, const char *out) {
     try {

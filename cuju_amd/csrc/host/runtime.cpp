@@ -301,6 +301,35 @@ float BatchRuntime::Difficulty(int env, int side) const {
     return side == 0 ? sc.leftDifficulty : sc.rightDifficulty;
 }
 
+void BatchRuntime::Episode(int env, long long *values, float *difficulty) {
+    CheckEnvironment(env);
+    dev_->Synchronize(nullptr);
+    dev_->CheckFault();
+    auto slot = std::make_unique<EnvSlot>();
+    dev_->ToHost(slot.get(), b_.slots + env, sizeof(EnvSlot));
+    auto obs = std::make_unique<Observation>();
+    dev_->ToHost(obs.get(), &b_.cores[env].obs, sizeof(Observation));
+    // The variant without reverse processing orders the teams as the observation does.
+    const Scenario &sc = VariantAt(slot->bundle * 4).world->scenario;
+    const long long out[17] = {slot->seed, slot->reverse, slot->episode, slot->episodeOffset, slot->bundle, obs->step,
+                               slot->fixedSeed, sc.deterministic, cfg_.ticksPerStep, slot->leftAgents, slot->rightAgents,
+                               sc.leftTeamSize, sc.rightTeamSize, obs->team[0].designatedPlayer, obs->team[1].designatedPlayer,
+                               slot->finalDesignated[0], slot->finalDesignated[1]};
+    memcpy(values, out, sizeof(out));
+    if (difficulty) {
+        dev_->ToHost(&difficulty[0], &b_.worlds[env].scenario.leftDifficulty, sizeof(float));
+        dev_->ToHost(&difficulty[1], &b_.worlds[env].scenario.rightDifficulty, sizeof(float));
+        const Scenario &own = VariantAt(slot->variant).world->scenario;
+        difficulty[2] = own.leftDifficulty;
+        difficulty[3] = own.rightDifficulty;
+    }
+}
+
+const char *BatchRuntime::ScenarioName(int bundle) const {
+    if (bundle < 0 || bundle >= (int)bundles_.size()) return nullptr;
+    return bundles_[bundle]->scenario.c_str();
+}
+
 std::string BatchRuntime::GetState(int env, int *episode) {
     CheckEnvironment(env);
     dev_->Synchronize(nullptr);

@@ -97,6 +97,13 @@ public:
     // Writes the observation stack of environment `env`: `[agents][115 * stack]` floats, oldest
     // frame first.
     void SetStack(int env, const std::string &name, const void *frames, size_t bytes);
+    // The current episode of environment `env`, synchronously: 17 values (seed, team order,
+    // resets so far, episode_number, bundle, last observation's step, fixed seed or -1,
+    // deterministic, ticks per step, agents, players and designated players per side, now and at
+    // the last episode end) and, unless null, the played then the scenario's difficulties.
+    void Episode(int env, long long *values, float *difficulty);
+    // The scenario name bundle `bundle` records, or null past the last bundle.
+    const char *ScenarioName(int bundle) const;
     // The buffer of an output name, or null.
     void *Buffer(const std::string &name);
     // Raw array `field`: its name, element type, the two dimensions after the agent axis (0 when

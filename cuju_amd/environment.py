@@ -175,6 +175,13 @@ class BatchEnvironment:
                                                library=library, animations=animations)
             resolved[index] = (built, pair)
         counts = [pair for _, pair in resolved]
+        if difficulty is not None:
+            pairs = list(difficulty)
+            if len(pairs) != len(names) or not all(isinstance(p, (tuple, list)) and len(p) == 2 for p in pairs):
+                raise ConfigurationError(f'expected a (left, right) pair of difficulties for each of the {len(names)} '
+                                         f'bundles, such as [(None, 0.5)] for one, found {difficulty!r}')
+            if any(v is not None and not 0 <= v <= 1 for p in pairs for v in p):
+                raise ConfigurationError(f"expected difficulties from 0 to 1, or None for the scenario's, found {difficulty!r}")
         if agent_counts is not None:
             counts = [tuple(c) for c in agent_counts]
             if len(counts) != len(names):
@@ -225,10 +232,19 @@ class BatchEnvironment:
         self.players = lib.cuju_environment_players(handle, pl.ctypes.data, pr.ctypes.data)
         self.agent_mask = torch.as_tensor(
             np.arange(self.agents)[None, :] < (left + right)[:, None], device=self._torch_device)
-        if difficulty is not None:
-            values = np.ascontiguousarray(np.broadcast_to(np.asarray(difficulty, dtype=np.float32),
-                                                          (environment_count, 2)))
-            self._check(lib.cuju_environment_set_difficulty(handle, values.ctypes.data))
+        # One (left, right) pair per bundle, None keeping the scenario's; the library takes a
+        # negative value for the scenario's (python/cuju/_batch/environment.py:496-507, 640-657).
+        bundles = np.zeros(environment_count, dtype=np.int64) if self._assignment is None else self._assignment
+        chosen = np.full((environment_count, 2), -1.0, dtype=np.float32)
+        for bundle, pair in enumerate(difficulty or []):
+            for side, value in enumerate(pair):
+                if value is not None:
+                    chosen[bundles == bundle, side] = value
+        if (chosen >= 0).any():
+            self._check(lib.cuju_environment_set_difficulty(handle, chosen.ctypes.data))
+        # The difficulty each environment plays, [environment_count, 2] float32 on the host.
+        self.difficulty = torch.empty((environment_count, 2), dtype=torch.float32)
+        lib.cuju_environment_difficulty(handle, self.difficulty.data_ptr())
         self._raw_fields = self._describe_raw()
         if representation == 'raw':
             self._observation, self._final = self._raw('raw'), self._raw('final_raw')

@@ -99,6 +99,8 @@ SIGNATURES = [
     ('cuju_environment_set_stack', I, [P, I, ctypes.c_char_p, P, U64]),
     ('cuju_environment_raw_field', ctypes.c_char_p, [P, I, P, P, P]),
     ('cuju_environment_buffer', P, [P, ctypes.c_char_p]),
+    ('cuju_environment_episode', I, [P, I, P, P]),
+    ('cuju_environment_scenario', ctypes.c_char_p, [P, I]),
     ('cuju_scenario_build_bundle', I, [ctypes.POINTER(ScenarioDescription), ctypes.POINTER(ScenarioDescription),
                                        ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
 ]

@@ -103,6 +103,14 @@ const char *cuju_environment_raw_field(void *environment, int field, int *type, 
 /* src/environment_api.h:430; simple115, final_simple115, smm, final_smm (uint8
    [E][A][smm_height][smm_width][4 * stack]), raw, final_raw, reward, done, score_reward */
 void *cuju_environment_buffer(void *environment, const char *name);
+/* src/environment_api.h:470; the current episode of environment `index`, synchronously: 17 values
+   (seed, reverse, resets so far, episode_number, bundle, step of the last observation or -1,
+   fixed seed or -1, deterministic, ticks per step, left and right agents, left and right players,
+   the designated player of each team now and at the last episode end) and, unless null, the
+   played left/right difficulty then the scenario's */
+int cuju_environment_episode(void *environment, int index, long long *values, float *difficulty);
+/* src/environment_api.h:519; the scenario name that bundle `bundle` records, or null past the last */
+const char *cuju_environment_scenario(void *environment, int bundle);
 
 /* The scenario builder (src/scenario_api.h:19-51). `cuju_scenario_build_bundle` refuses a
    description of another version. */

@@ -107,3 +107,38 @@ def test_config5_drills_from_a_scenario_file(reference_library, tmp_path):
     assignment = [0, 0, 1, 2] * 16
     compare([source] + others, 64, 150, seed=9, assignment=assignment, their_assets=[bundle] + others,
             agent_counts=[(3, 0), (4, 0), (1, 0)])
+
+
+def test_difficulty_reports_and_overrides(reference_library):
+    """`difficulty` takes one (left, right) pair per bundle, None keeping the scenario's, and
+    `batch.difficulty` reports what each environment plays (tests/test_difficulty.py of the
+    reference); the overridden batch then plays as the reference with the same difficulties."""
+    import cuju_amd
+    batch = cuju_amd.BatchEnvironment(['5_vs_5_l1_r0', '11_vs_11_easy_stochastic_l1_r0', '1_vs_1_easy_l1_r0'],
+                                      library=PRODUCT, device='cuda:0', environment_count=3, assignment=[0, 1, 2])
+    try:
+        assert batch.difficulty.dtype == torch.float32
+        assert torch.equal(batch.difficulty, torch.tensor([[0.05, 0.05], [1.0, 0.05], [0.0, 0.0]]))
+    finally:
+        batch.close()
+    assets = ['11_vs_11_stochastic_l1_r0', '5_vs_5_l1_r0']
+    assignment = [0, 1] * 16
+    mine = cuju_amd.BatchEnvironment(assets, library=PRODUCT, device='cuda:0', environment_count=32,
+                                     assignment=assignment, difficulty=[(None, 0.25), (0.75, None)], seed=4)
+    per_environment = np.array([[-1.0, 0.25], [0.75, -1.0]] * 16, dtype=np.float32)
+    theirs = ref.ReferenceBatch(assets, environment_count=32, seed=4, threads=0, assignment=assignment,
+                                difficulty=per_environment)
+    try:
+        assert torch.equal(mine.difficulty, torch.tensor([[1.0, 0.25], [0.75, 0.05]] * 16))
+        assert host(mine.reset()).tobytes() == theirs.reset().tobytes()
+        for step in range(80):
+            actions = counter(4, step, 32, theirs.agents, theirs.action_count).astype(np.int32)
+            a = mine.step(torch.as_tensor(actions, device='cuda:0'))
+            b = theirs.step(actions)
+            for x, y, name in zip(a[:3], b, ('observation', 'reward', 'done')):
+                assert host(x).astype(y.dtype).tobytes() == y.tobytes(), f'{name} at step {step}'
+        for e in range(32):
+            assert mine.get_state(e) == theirs.get_state(e), f'state of environment {e}'
+    finally:
+        mine.close()
+        theirs.close()

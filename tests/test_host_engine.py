@@ -253,3 +253,50 @@ def test_host_engine_smm_and_raw_match_reference(representation, stacked, with_r
     finally:
         mine.close()
         theirs.close()
+
+
+def test_difficulty_override_plays_as_the_reference(reference_library, host_library):
+    """Per-environment difficulties (negative keeps the scenario's) change the AI identically."""
+    difficulty = np.array([[-1.0, 0.25], [0.75, -1.0], [0.1, 0.9]], dtype=np.float32)
+    digests = []
+    for path in (host_library, reference_library):
+        batch = ref.ReferenceBatch('11_vs_11_stochastic_l1_r0', environment_count=3, seed=8, threads=2,
+                                   library_path=path, difficulty=difficulty)
+        try:
+            digests.append(play(batch, 60, 3))
+        finally:
+            batch.close()
+    assert digests[0] == digests[1]
+
+
+def test_episode_values_and_scenario_names_match_the_reference(reference_library, host_library):
+    """`cuju_environment_episode` and `cuju_environment_scenario`, after episodes have ended."""
+    import ctypes
+    assets = ['academy_empty_goal_close_l1_r0', '5_vs_5_l2_r1']
+    options = dict(environment_count=4, seed=3, threads=2, assignment=[0, 1, 0, 1], episode_number=5,
+                   difficulty=np.array([[-1.0, 0.5]] * 4, dtype=np.float32))
+    results = []
+    for path in (host_library, reference_library):
+        batch = ref.ReferenceBatch(assets, library_path=path, **options)
+        lib = batch._lib
+        lib.cuju_environment_episode.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        lib.cuju_environment_scenario.restype = ctypes.c_char_p
+        lib.cuju_environment_scenario.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        try:
+            batch.reset()
+            seen = []
+            for step in range(90):
+                batch.step(digest_actions(step, 4, batch.agents, batch.action_count))
+                if step % 30 == 29:
+                    for e in range(4):
+                        values = np.zeros(17, dtype=np.int64)
+                        difficulty = np.zeros(4, dtype=np.float32)
+                        assert lib.cuju_environment_episode(batch._handle, e, values.ctypes.data, difficulty.ctypes.data) == 0
+                        seen.append((values.tolist(), difficulty.tolist()))
+            names = [lib.cuju_environment_scenario(batch._handle, k) for k in range(3)]
+            results.append((seen, names))
+        finally:
+            batch.close()
+    assert results[0] == results[1]
+    assert results[0][1] == [b'academy_empty_goal_close', b'5_vs_5', None]
+    assert any(values[2] > 1 for values, _ in results[0][0])  # some environment has reset since

@@ -422,15 +422,43 @@ void BatchRuntime::SetState(int env, const std::string &bytes, int prevScoreDiff
 void BatchRuntime::SetStack(int env, const std::string &name, const void *frames, size_t bytes) {
     CheckEnvironment(env);
     if (b_.stack < 2) throw std::invalid_argument("expected a batch that stacks its observations");
-    if (name != "simple115" || !b_.simple115) throw std::invalid_argument("expected the stack simple115 of the batch, found " + name);
     const size_t agents = (size_t)(slots_[env].leftAgents + slots_[env].rightAgents);
-    const size_t width = (size_t)kSimple115 * b_.stack;
-    const size_t expected = agents * width * sizeof(float);
-    if (bytes != expected)
-        throw std::invalid_argument("expected a stack of " + std::to_string(expected) + " bytes for the agents of environment " +
-                                    std::to_string(env) + ", found " + std::to_string(bytes));
+    auto checkBytes = [&](size_t expected) {
+        if (bytes != expected)
+            throw std::invalid_argument("expected a stack of " + std::to_string(expected) + " bytes for the agents of environment " +
+                                        std::to_string(env) + ", found " + std::to_string(bytes));
+    };
+    if (name == "simple115" && b_.simple115) {
+        const size_t width = (size_t)kSimple115 * b_.stack;
+        checkBytes(agents * width * sizeof(float));
+        dev_->Synchronize(nullptr);
+        dev_->ToDevice(b_.simple115 + (size_t)env * b_.agents * width, frames, bytes);
+        return;
+    }
+    if (name != "smm" || !b_.smm) throw std::invalid_argument("expected the stack simple115 or smm of the batch, found " + name);
+    // A minimap is zero but for its marks, and each frame keeps the list of its marks so that the
+    // next step erases exactly them: rebuild those lists from the cells of 255.
+    const size_t cells = (size_t)b_.smmWidth * b_.smmHeight * kSmmLayers;  // marks of one frame
+    const size_t agentBytes = cells * b_.stack;
+    checkBytes(agents * agentBytes);
+    const uint8_t *in = static_cast<const uint8_t *>(frames);
+    const int rowsPerAgent = kSmmMarkRow * b_.stack;
+    std::vector<int32_t> marks(agents * rowsPerAgent, 0);
+    for (size_t a = 0; a < agents; a++)
+        for (int f = 0; f < b_.stack; f++) {
+            int32_t *row = marks.data() + a * rowsPerAgent + f * kSmmMarkRow;
+            for (size_t m = 0; m < cells; m++) {
+                const uint8_t v = in[a * agentBytes + (m / kSmmLayers) * kSmmLayers * b_.stack + kSmmLayers * f + m % kSmmLayers];
+                if (v == 0) continue;
+                if (v != 255 || row[0] == kSmmMarks)
+                    throw std::invalid_argument("expected a minimap of GRF, zeros and at most " + std::to_string(kSmmMarks) +
+                                                " cells of 255 a frame, found a cell of " + std::to_string(v));
+                row[1 + row[0]++] = (int32_t)m;
+            }
+        }
     dev_->Synchronize(nullptr);
-    dev_->ToDevice(b_.simple115 + (size_t)env * b_.agents * width, frames, bytes);
+    dev_->ToDevice(b_.smm + (size_t)env * b_.agents * agentBytes, frames, bytes);
+    dev_->ToDevice(b_.smmMarks + (size_t)env * b_.agents * rowsPerAgent, marks.data(), marks.size() * sizeof(int32_t));
 }
 
 // GRF's raw keys, in the order of the arrays (observation.py).

@@ -21,6 +21,7 @@ from typing import Any
 import numpy as np
 import torch
 
+from . import frame_stack as _frame_stack
 from . import library as _library
 from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, ConfigurationError,
                      EnvironmentIndexError, MissingFileError, StateError, from_library)
@@ -66,10 +67,12 @@ def _pickle_int(value: int) -> bytes:
     return b'J' + struct.pack('<i', value)
 
 
-def episode_pickle(episode, collected=None) -> bytes:
+def episode_pickle(episode, collected=None, frames=None) -> bytes:
     """GRF's pickle of the episode logic that precedes the engine bytes of a state: the core's
-    previous score difference, game mode and ball-owning team, then the checkpoints per agent
-    (python/cuju/_batch/state.py:38-77)."""
+    previous score difference, game mode and ball-owning team, then the checkpoints per agent,
+    then the opcodes of GRF's `FrameStack` deque when `frames` holds them
+    (python/cuju/_batch/state.py:38-77). The pickle keeps no memo of its own, so the deque's
+    opcodes keep their memo indices."""
     keys = ('previous_score_diff', 'previous_game_mode', 'prev_ball_owned_team')
     logic = b''.join(_pickle_text(k) + _pickle_int(v) for k, v in zip(keys, episode))
     data = (b'\x80\x02}(' + _pickle_text('FootballEnvCore')
@@ -78,6 +81,8 @@ def episode_pickle(episode, collected=None) -> bytes:
         data += (_pickle_text('CheckpointRewardWrapper') + b'}('
                  + b''.join(_pickle_int(a) + _pickle_int(c) for a, c in enumerate(collected) if c)
                  + b'u')
+    if frames is not None:
+        data += _pickle_text('FrameStack') + frames
     return data + b'u.'
 
 
@@ -87,12 +92,17 @@ class _EpisodeLogic:
 
 class _StateUnpickler(pickle.Unpickler):
     """Loads the pickle of a state, resolving GRF's episode-logic class to a plain stand-in and
-    refusing every other global, so that loading constructs nothing else
-    (python/cuju/_batch/state.py:20-32)."""
+    refusing every other global but those of a pickled frame stack in a stacked state, so that
+    loading constructs nothing else (python/cuju/_batch/state.py:20-32)."""
+
+    stacked = False
 
     def find_class(self, module, name):
         if (module, name) == ('gfootball.env.football_env_core', 'EnvState'):
             return _EpisodeLogic
+        found = _frame_stack.find_class(module, name) if self.stacked else None
+        if found is not None:
+            return found
         raise pickle.UnpicklingError(f'expected only the episode logic, found `{module}.{name}`')
 
 
@@ -412,11 +422,27 @@ class BatchEnvironment:
         with torch.cuda.device(self._torch_device):
             self._check(self._lib.cuju_environment_synchronize(self._handle(), self._stream()))
 
-    def get_state(self, index: int) -> bytes:
+    def _check_stack(self, stacked: bool) -> None:
+        """GRF pickles its frame stack with the state, so the option must match the batch."""
+        if self.stacked and not stacked:
+            raise StateError("expected stacked=True for the state of a batch that stacks its observations, whose "
+                             "state holds GRF's FrameStack")
+        if stacked and not self.stacked:
+            raise StateError('expected a batch with stacked=True for a stacked state')
+
+    def _frame_shape(self):
+        """One agent's frame of the stack and its element type."""
+        shape = tuple(self._observation.shape[2:])
+        dtype = 'uint8' if self._observation.dtype == torch.uint8 else 'float32'
+        return (*shape[:-1], shape[-1] // _frame_stack.FRAMES), dtype
+
+    def get_state(self, index: int, stacked: bool = False) -> bytes:
         """GRF's state of environment `index`: an int32 pickle length, the pickle of the episode
-        logic, then the engine bytes."""
+        logic (with GRF's `FrameStack` deque when `stacked`), then the engine bytes
+        (python/cuju/_batch/environment.py:1487-1538)."""
         if not 0 <= index < self.environment_count:
             raise EnvironmentIndexError(f'expected an environment from 0 to {self.environment_count - 1}, found {index}')
+        self._check_stack(stacked)
         size = ctypes.c_ulonglong()
         episode = (ctypes.c_int * (3 + MAXIMUM_AGENTS))()
         with torch.cuda.device(self._torch_device):
@@ -426,24 +452,30 @@ class BatchEnvironment:
             raise from_library(self._lib.cuju_last_error().decode())
         match = ctypes.string_at(pointer, size.value)
         collected = list(episode)[3:3 + self.agents] if self.checkpoints else None
-        data = episode_pickle(list(episode)[:3], collected)
+        frames = None
+        if stacked:
+            agents = int(self.left_agents[index] + self.right_agents[index])
+            stack = self._observation[index, :agents].cpu().numpy()
+            frames = _frame_stack.pickled_frames(_frame_stack.frames_of(stack, agents))
+        data = episode_pickle(list(episode)[:3], collected, frames)
         return struct.pack('<i', len(data)) + data + match
 
     def set_state(self, index: int, state: bytes, stacked: bool = False) -> None:
-        """Sets environment `index` to a state that `get_state` returned; its observation and sticky
-        actions follow from the state, the reward is 0 and done clear until the next step
-        (python/cuju/_batch/environment.py:1540-1620). States that carry GRF's frame stack are not
-        read."""
+        """Sets environment `index` to a state that `get_state` (or GRF) wrote; its observation and
+        sticky actions follow from the state, the reward is 0 and done clear until the next step.
+        With `stacked`, the state's `FrameStack` becomes the observation stack
+        (python/cuju/_batch/environment.py:1540-1620)."""
         if not 0 <= index < self.environment_count:
             raise EnvironmentIndexError(f'expected an environment from 0 to {self.environment_count - 1}, found {index}')
-        if stacked:
-            raise StateError('this build reads states without a frame stack only')
+        self._check_stack(stacked)
         if len(state) < 4 or not 0 < struct.unpack_from('<i', state)[0] <= len(state) - 4:
             raise StateError(f'expected the bytes of a state: a pickle length, the pickle and the match, '
                              f'found {len(state)} bytes that hold none')
         (length,) = struct.unpack_from('<i', state)
         try:
-            unpickled = _StateUnpickler(io.BytesIO(state[4:4 + length])).load()
+            unpickler = _StateUnpickler(io.BytesIO(state[4:4 + length]))
+            unpickler.stacked = stacked
+            unpickled = unpickler.load()
             logic = unpickled['FootballEnvCore'].__dict__
             episode = (ctypes.c_int * (3 + MAXIMUM_AGENTS))(
                 logic['previous_score_diff'], logic['previous_game_mode'], logic['prev_ball_owned_team'])
@@ -453,6 +485,17 @@ class BatchEnvironment:
             raise StateError('expected the checkpoints of the checkpoint reward in the state')
         for agent, count in unpickled.get('CheckpointRewardWrapper', {}).items():
             episode[3 + agent] = count
+        stack = None
+        if stacked:
+            # GRF: `FrameStack.set_state` takes the state's deque as its observations.
+            if 'FrameStack' not in unpickled:
+                raise StateError("expected GRF's FrameStack in the stacked state")
+            shape, dtype = self._frame_shape()
+            agents = int(self.left_agents[index] + self.right_agents[index])
+            try:
+                stack = _frame_stack.stack_bytes(unpickled['FrameStack'], agents, shape, dtype)
+            except ValueError as error:
+                raise StateError(str(error)) from error
         match = state[4 + length:]
         with torch.cuda.device(self._torch_device):
             torch.cuda.current_stream(self._torch_device).synchronize()
@@ -462,6 +505,10 @@ class BatchEnvironment:
             if message.startswith('expected'):
                 raise StateError(message)
             raise from_library(message)
+        if stack is not None:
+            name = b'smm' if self.representation == 'extracted' else b'simple115'
+            with torch.cuda.device(self._torch_device):
+                self._check(self._lib.cuju_environment_set_stack(self._handle(), index, name, stack, len(stack)))
 
     def memory_bytes(self) -> int:
         return int(self._lib.cuju_environment_memory_bytes(self._handle()))

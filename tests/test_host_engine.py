@@ -300,3 +300,59 @@ def test_episode_values_and_scenario_names_match_the_reference(reference_library
     assert results[0] == results[1]
     assert results[0][1] == [b'academy_empty_goal_close', b'5_vs_5', None]
     assert any(values[2] > 1 for values, _ in results[0][0])  # some environment has reset since
+
+
+@pytest.mark.parametrize('representation', ['extracted', 'simple115v2'])
+def test_set_stack_continues_as_the_reference(representation, reference_library, host_library):
+    """A stack set from outside (`cuju_environment_set_stack`), an SMM one included, whose marks the
+    library rebuilds so the next steps erase exactly them, continues as the reference continues."""
+    import ctypes
+    name = b'smm' if representation == 'extracted' else b'simple115'
+    outputs = []
+    for path in (host_library, reference_library):
+        batch = ref.ReferenceBatch('5_vs_5_l2_r1', environment_count=2, seed=6, threads=2, library_path=path,
+                                   representation=representation, stacked=True)
+        lib = batch._lib
+        lib.cuju_environment_set_stack.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p,
+                                                   ctypes.c_ulonglong]
+        try:
+            batch.reset()
+            seen = []
+            for step in range(12):
+                batch.step(digest_actions(step, 2, batch.agents, batch.action_count))
+            # Environment 1 takes environment 0's match and a stack of env 0's frames, oldest last.
+            match, episode = batch.raw_state(0)
+            batch.set_raw_state(1, match, episode)
+            frames = np.ascontiguousarray(batch.observation()[0])
+            width = frames.shape[-1] // 4
+            reordered = np.concatenate([frames[..., width * f:width * (f + 1)] for f in (3, 1, 2, 0)], axis=-1)
+            stack = np.ascontiguousarray(reordered).tobytes()
+            assert lib.cuju_environment_set_stack(batch._handle, 1, name, stack, len(stack)) == 0
+            seen.append(np.ascontiguousarray(batch.observation()).tobytes())
+            for step in range(12, 24):
+                out = batch.step(digest_actions(step, 2, batch.agents, batch.action_count))
+                seen.append(b''.join(np.ascontiguousarray(x).tobytes() for x in out))
+            outputs.append(seen)
+        finally:
+            batch.close()
+    assert outputs[0] == outputs[1]
+
+
+def test_set_stack_refuses_what_no_minimap_holds(host_library):
+    import ctypes
+    batch = ref.ReferenceBatch('5_vs_5_l1_r0', environment_count=1, seed=6, threads=1, library_path=host_library,
+                               representation='extracted', stacked=True)
+    lib = batch._lib
+    lib.cuju_environment_set_stack.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p,
+                                               ctypes.c_ulonglong]
+    try:
+        batch.reset()
+        frames = np.ascontiguousarray(batch.observation()[0]).copy()
+        frames.reshape(-1)[5] = 7
+        stack = frames.tobytes()
+        assert lib.cuju_environment_set_stack(batch._handle, 0, b'smm', stack, len(stack)) == -1
+        assert b'minimap' in lib.cuju_last_error()
+        assert lib.cuju_environment_set_stack(batch._handle, 0, b'smm', stack, len(stack) - 1) == -1
+        assert b'bytes' in lib.cuju_last_error()
+    finally:
+        batch.close()

@@ -22,6 +22,7 @@ import numpy as np
 import torch
 
 from . import frame_stack as _frame_stack
+from . import operators as _operators
 from . import library as _library
 from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, ConfigurationError,
                      EnvironmentIndexError, MissingFileError, StateError, from_library)
@@ -269,6 +270,9 @@ class BatchEnvironment:
         self._reward = self._buffer('reward', (environment_count, self.agents), torch.float32)
         self._done = self._buffer('done', (environment_count,), torch.uint8)
         self._score_reward = self._buffer('score_reward', (environment_count,), torch.int32)
+        self._pending = None
+        # The key under which torch.compile's operators find this batch.
+        self._operator = _operators.register(self)
 
     # ---- plumbing ----
     @property
@@ -389,8 +393,46 @@ class BatchEnvironment:
 
     def reset_done(self) -> None:
         """Starts the next episode of every environment whose done flag is set."""
+        if torch.compiler.is_compiling():
+            torch.ops.cuju_amd.reset_done(self._operator_key(), self._operator_outputs())
+            return
         with torch.cuda.device(self._torch_device):
             self._check(self._lib.cuju_environment_reset_done(self._handle(), self._stream()))
+
+    # ---- torch.compile: the operators of operators.py (python/cuju/_batch/environment.py:983-1056) ----
+    def _operator_key(self) -> int:
+        return self._operator
+
+    def _operator_outputs(self) -> list:
+        """Every tensor a step writes, which the operators declare as mutated."""
+        outputs = []
+        for tensor in (self._observation, self._reward, self._done, self._final, self._score_reward):
+            outputs.extend(tensor.values() if isinstance(tensor, dict) else (tensor,))
+        return outputs
+
+    def _copy_operator_outputs(self, outputs) -> None:
+        # The compiler may hand copies of the buffers; each takes the step's values.
+        for given, own in zip(outputs, self._operator_outputs()):
+            if given.data_ptr() != own.data_ptr():
+                given.copy_(own)
+
+    def _operator_step(self, actions, outputs) -> None:
+        with torch.cuda.device(self._torch_device):
+            if self._check_actions and bool(((actions < -self.action_count) | (actions >= self.action_count)).any()):
+                raise ActionRangeError(f'expected action indices from {-self.action_count} to {self.action_count - 1}')
+            self._check(self._lib.cuju_environment_step(self._handle(), actions.data_ptr(), 1, self._stream(), 0))
+        self._copy_operator_outputs(outputs)
+
+    def _operator_reset_done(self, outputs) -> None:
+        with torch.cuda.device(self._torch_device):
+            self._check(self._lib.cuju_environment_reset_done(self._handle(), self._stream()))
+        self._copy_operator_outputs(outputs)
+
+    def _compiled_step(self, actions: torch.Tensor, shape):
+        actions = actions.to(self._torch_device, torch.int32).reshape(shape).contiguous()
+        torch.ops.cuju_amd.step(self._operator_key(), actions, self._operator_outputs())
+        observation, reward, done, final = self._outputs()
+        return observation, reward, done, {'final_observation': final, 'score_reward': self._score_reward}
 
     def observation(self):
         return self._outputs()[0]
@@ -404,6 +446,8 @@ class BatchEnvironment:
             raise TypeError(f'expected integer action indices, found {actions.dtype}')
         if tuple(actions.shape) != shape and not (self.agents == 1 and tuple(actions.shape) == (shape[0],)):
             raise ArgumentError(f'expected actions of the shape {shape}, found {tuple(actions.shape)}')
+        if torch.compiler.is_compiling():
+            return self._compiled_step(actions, shape)
         with torch.cuda.device(self._torch_device):
             if actions.device == self._torch_device:
                 staged = actions.to(torch.int32).reshape(shape).contiguous()
@@ -416,6 +460,18 @@ class BatchEnvironment:
         self._check(status)
         observation, reward, done, final = self._outputs()
         return observation, reward, done, {'final_observation': final, 'score_reward': self._score_reward}
+
+    def step_async(self, actions: Any) -> None:
+        """Starts a step of every environment on the current stream and returns at once; on the
+        device this is `step` without reading its outputs (python/cuju/_batch/environment.py:1418)."""
+        self._pending = self.step(actions)
+
+    def step_wait(self):
+        """The outputs of the step `step_async` started (python/cuju/_batch/environment.py:1466)."""
+        if self._pending is None:
+            raise ArgumentError('expected a step_async before step_wait')
+        outputs, self._pending = self._pending, None
+        return outputs
 
     def synchronize(self) -> None:
         """Waits for the batch's work and reports a fault of any environment."""

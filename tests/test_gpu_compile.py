@@ -1,0 +1,85 @@
+"""`torch.compile` traces a step whole, through the `cuju_amd::step` and `cuju_amd::reset_done`
+operators, and gives the outputs of an eager step (tests/test_compile.py of the reference)."""
+
+import pytest
+import torch
+
+from conftest import PRODUCT, digest_actions
+
+pytestmark = pytest.mark.gpu
+STEPS = 40
+
+
+def outputs_bytes(observation, reward, done, information):
+    tensors = (observation, reward, done, information['final_observation'], information['score_reward'])
+    return b''.join(t.detach().cpu().numpy().tobytes() for t in tensors)
+
+
+def step(batch, actions):
+    return batch.step(actions)
+
+
+def reset_done(batch):
+    batch.reset_done()
+
+
+def play(step, reset_done, **options):
+    import cuju_amd
+    batch = cuju_amd.BatchEnvironment('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=3, **options)
+    try:
+        batch.reset()
+        found = []
+        for index in range(STEPS):
+            actions = torch.as_tensor(digest_actions(index, 3, batch.agents, batch.action_count), device='cuda:0')
+            found.append(outputs_bytes(*step(batch, actions)))
+            if not options.get('auto_reset', True):
+                reset_done(batch)
+        return found
+    finally:
+        batch.close()
+
+
+@pytest.mark.parametrize('auto_reset', [True, False])
+def test_a_compiled_step_equals_an_eager_one(auto_reset):
+    torch._dynamo.reset()
+    compiled = (torch.compile(step, fullgraph=True, backend='aot_eager'),
+                torch.compile(reset_done, fullgraph=True, backend='aot_eager'))
+    options = {'auto_reset': auto_reset, 'seed': 11}
+    assert play(*compiled, **options) == play(step, reset_done, **options)
+
+
+def test_a_squeezed_batch_compiles():
+    import cuju_amd
+    torch._dynamo.reset()
+
+    def run(step):
+        batch = cuju_amd.BatchEnvironment('academy_empty_goal_close', library=PRODUCT, device='cuda:0',
+                                          environment_count=2, squeeze=True)
+        try:
+            batch.reset()
+            return [outputs_bytes(*step(batch, torch.full((2,), index % 19, device='cuda:0'))) for index in range(10)]
+        finally:
+            batch.close()
+
+    assert run(torch.compile(step, fullgraph=True, backend='aot_eager')) == run(step)
+
+
+def test_step_async_then_wait_equals_step():
+    import cuju_amd
+    found = []
+    for use_async in (False, True):
+        batch = cuju_amd.BatchEnvironment('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=3, seed=2)
+        try:
+            batch.reset()
+            seen = []
+            for index in range(20):
+                actions = torch.as_tensor(digest_actions(index, 3, batch.agents, batch.action_count), device='cuda:0')
+                if use_async:
+                    batch.step_async(actions)
+                    seen.append(outputs_bytes(*batch.step_wait()))
+                else:
+                    seen.append(outputs_bytes(*batch.step(actions)))
+            found.append(seen)
+        finally:
+            batch.close()
+    assert found[0] == found[1]

@@ -636,8 +636,19 @@ HDN bool CheckHumanoidCollisions(World &w, const Ctx &c) {
     ENG_SCOPE(17);
     PlayerList ps = PlayersInProcessingOrder(w);
     PlayerBounceList bounces[kPlayers];
-    for (int i = 0; i + 1 < ps.count; i++)
-        for (int j = i + 1; j < ps.count; j++) CheckHumanoidCollision(w, c, ps[i], ps[j], bounces[i], bounces[j]);
+    // A pair farther apart than both contact radii changes nothing, so only near pairs make the
+    // call; the test is the one the pair's own check starts with, on the same values.
+    const float bounceRadius = 0.5f * 0.72f, similarRadius = 0.8f * 0.72f;
+    for (int i = 0; i + 1 < ps.count; i++) {
+        Vec3 pi = Sp(w, ps[i]).position;
+        for (int j = i + 1; j < ps.count; j++) {
+            const float dist = (pi - Sp(w, ps[j]).position).Length();
+            if (dist < bounceRadius * 2.0f || dist < (bounceRadius + similarRadius) * 2.0f) {
+                CheckHumanoidCollision(w, c, ps[i], ps[j], bounces[i], bounces[j]);
+                pi = Sp(w, ps[i]).position;  // the call may push the player aside
+            }
+        }
+    }
     for (int i = 0; i < ps.count; i++) {
         float total = 0.0f;
         for (int k = 0; k < bounces[i].count; k++) total += bounces[i][k].force;

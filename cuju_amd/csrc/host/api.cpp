@@ -45,7 +45,7 @@ void *cuju_environment_create(const struct cuju_configuration *s) {
             throw std::invalid_argument("expected the configuration version " + std::to_string(CUJU_CONFIGURATION_VERSION) + ", found " +
                                         std::to_string(s->version));
         if (s->environment_count < 1) throw std::invalid_argument("expected at least one environment, found " + std::to_string(s->environment_count));
-        if (s->allocate || s->release) throw std::invalid_argument("this build allocates its own device memory");
+        if (!s->allocate != !s->release) throw std::invalid_argument("expected both allocate and release, or neither");
         eng::host::Configuration c;
         for (int i = 0; i < s->asset_count; i++) c.assets.push_back(s->assets[i]);
         if (s->assignment) c.assignment.assign(s->assignment, s->assignment + s->environment_count);
@@ -58,6 +58,9 @@ void *cuju_environment_create(const struct cuju_configuration *s) {
         c.numpyLegacy = s->numpy_legacy != 0;
         c.autoReset = s->auto_reset != 0;
         c.threads = s->threads;
+        c.allocate = s->allocate;
+        c.release = s->release;
+        c.allocatorContext = s->allocator_context;
         c.ticksPerStep = s->ticks_per_step;
         c.smmWidth = s->smm_width;
         c.smmHeight = s->smm_height;

@@ -158,7 +158,10 @@ BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> dev
         started_.assign(count, false);
         unstarted_ = count;
     } catch (...) {
-        for (void *p : owned_) dev_->Release(p);
+        for (void *p : owned_) {
+            if (UsesCallerAllocator()) cfg_.release(p, cfg_.allocatorContext);
+            else dev_->Release(p);
+        }
         owned_.clear();
         throw;
     }
@@ -169,7 +172,27 @@ BatchRuntime::~BatchRuntime() {
         dev_->Synchronize(nullptr);
     } catch (...) {
     }
-    for (void *p : owned_) dev_->Release(p);
+    for (void *p : owned_) {
+        if (UsesCallerAllocator()) cfg_.release(p, cfg_.allocatorContext);
+        else dev_->Release(p);
+    }
+}
+
+bool BatchRuntime::UsesCallerAllocator() const { return cfg_.allocate != nullptr && !dev_->HostMemory(); }
+
+void *BatchRuntime::AllocateBytes(size_t bytes) {
+    void *p = nullptr;
+    if (UsesCallerAllocator()) {
+        p = cfg_.allocate(bytes, cfg_.allocatorContext);
+        if (!p) throw std::runtime_error("the allocator of the configuration has no " + std::to_string(bytes) + " bytes of device memory");
+        owned_.push_back(p);
+        dev_->Fill(p, 0, bytes);
+    } else {
+        p = dev_->Allocate(bytes);
+        owned_.push_back(p);
+    }
+    allocated_ += bytes;
+    return p;
 }
 
 int BatchRuntime::LeftPlayers(int env) const { return VariantAt(slots_[env].bundle * 4).world->scenario.leftTeamSize; }

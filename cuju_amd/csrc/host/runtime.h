@@ -57,6 +57,12 @@ struct Configuration {
     std::vector<int32_t> agentCounts;
     int episodeNumber = 0;
     int64_t firstIndex = 0;
+    // Device memory from the caller's allocator (src/environment_api.h:81-86): `allocate` returns
+    // null when it has none, and `release` gets each block back once the device is idle. Null
+    // takes the device's own allocation.
+    void *(*allocate)(size_t bytes, void *context) = nullptr;
+    void (*release)(void *pointer, void *context) = nullptr;
+    void *allocatorContext = nullptr;
 };
 
 // The raw arrays of `outputs` agent views in one buffer, each at a multiple of 256 bytes.
@@ -111,12 +117,12 @@ public:
     const char *RawField(int field, int *type, int *dimensions, unsigned long long *offset) const;
 
 private:
+    // Zero-filled device memory, from the caller's allocator when the configuration names one.
+    void *AllocateBytes(size_t bytes);
+    bool UsesCallerAllocator() const;
     template <class T>
     T *Alloc(size_t n) {
-        void *p = dev_->Allocate(sizeof(T) * (n ? n : 1));
-        owned_.push_back(p);
-        allocated_ += sizeof(T) * (n ? n : 1);
-        return static_cast<T *>(p);
+        return static_cast<T *>(AllocateBytes(sizeof(T) * (n ? n : 1)));
     }
     template <class T>
     T *Upload(const T *src, size_t n) {

@@ -119,11 +119,40 @@ class _DeviceArray:
                                          'strides': None}
 
 
+class _TorchAllocator:
+    """`allocate` and `release` over PyTorch's caching allocator (python/cuju/_batch/allocator.py):
+    the batch's device memory then shows in torch's statistics. Blocks come from the device's
+    default stream; the library returns them only once the device is idle."""
+
+    ALLOCATE = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p)
+    RELEASE = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_void_p)
+
+    def __init__(self, device):
+        stream = torch.cuda.default_stream(device)
+        self.errors = []
+
+        def allocate(size, _context):
+            try:
+                return torch.cuda.caching_allocator_alloc(size, device, stream)
+            except Exception as error:  # an exception cannot cross the library
+                self.errors.append(error)
+                return None
+
+        def release(pointer, _context):
+            torch.cuda.caching_allocator_delete(pointer)
+
+        self.allocate, self.release = self.ALLOCATE(allocate), self.RELEASE(release)
+
+    def pointers(self):
+        return (ctypes.cast(self.allocate, ctypes.c_void_p).value, ctypes.cast(self.release, ctypes.c_void_p).value)
+
+
 class _Native:
     """The library handle, kept alive by every tensor that views the batch's memory."""
 
     def __init__(self, lib, device):
         self.lib, self.device, self.handle = lib, device, None
+        self.allocator = None
 
     def free(self):
         if self.handle:
@@ -147,7 +176,14 @@ class BatchEnvironment:
                  difficulty=None, device: str | int | torch.device = 'cuda', physics_steps_per_frame: int = 10,
                  stacked: bool = False, game_engine_random_seed=None, squeeze: bool = False, agent_counts=None,
                  episode_number: int = 0, first_index: int = 0, check_actions: bool = False,
-                 with_raw: bool = False, library: str | None = None):
+                 with_raw: bool = False, library: str | None = None, threads: int = 0, allocator: str = 'cuda',
+                 pin_threads: bool = False, numa: bool = False, pin_memory: bool = False, debug: bool = False):
+        # threads, pin_threads, numa and pin_memory shape the reference's CPU batches; a device batch
+        # takes them and has no use for them, as the reference's GPU batch does.
+        del threads, pin_threads, numa, pin_memory
+        if allocator not in ('cuda', 'torch'):
+            raise ChoiceError(f'expected the allocator cuda or torch, found {allocator!r}')
+        self.debug = bool(debug)
         if representation not in REPRESENTATIONS:
             raise ChoiceError(f'expected a representation of {sorted(REPRESENTATIONS)}, found {representation!r}')
         if stacked and representation == 'raw':
@@ -204,7 +240,7 @@ class BatchEnvironment:
         self.representation = representation
         self.action_count = ACTION_COUNTS[action_set]
         self.environment_count = environment_count
-        self._check_actions = check_actions
+        self._check_actions = check_actions or self.debug
         self._paths = (ctypes.c_char_p * len(names))(*(p.encode() for p, _ in resolved))
         self._counts = np.ascontiguousarray([c for pair in counts for c in pair], dtype=np.int32)
         self._assignment = None if assignment is None else np.ascontiguousarray(assignment, dtype=np.int32)
@@ -228,9 +264,15 @@ class BatchEnvironment:
             agent_counts=self._counts.ctypes.data, episode_number=episode_number, first_index=first_index,
             allocate=None, release=None, allocator_context=None, pin_threads=0, numa=0, page_aligned=0)
         self._native = _Native(lib, self._torch_device)
+        if allocator == 'torch':
+            # The callbacks live on the handle's owner, which outlives every buffer they gave out.
+            self._native.allocator = _TorchAllocator(self._torch_device)
+            cfg.allocate, cfg.release = self._native.allocator.pointers()
         with torch.cuda.device(self._torch_device):
             handle = lib.cuju_environment_create(ctypes.byref(cfg))
         if not handle:
+            if self._native.allocator is not None and self._native.allocator.errors:
+                raise self._native.allocator.errors[0]
             raise ConfigurationError(lib.cuju_last_error().decode())
         self._native.handle = handle
         self._lib = lib
@@ -380,6 +422,7 @@ class BatchEnvironment:
                 self._check(self._lib.cuju_environment_reset(
                     self._handle(), None if seeds32 is None else seeds32.ctypes.data,
                     None if reverse_array is None else reverse_array.ctypes.data, self._stream()))
+        self._wait_in_debug()
         return self._outputs()[0]
 
     def _integers(self, values, name):
@@ -398,6 +441,7 @@ class BatchEnvironment:
             return
         with torch.cuda.device(self._torch_device):
             self._check(self._lib.cuju_environment_reset_done(self._handle(), self._stream()))
+        self._wait_in_debug()
 
     # ---- torch.compile: the operators of operators.py (python/cuju/_batch/environment.py:983-1056) ----
     def _operator_key(self) -> int:
@@ -458,8 +502,14 @@ class BatchEnvironment:
                 staged = np.ascontiguousarray(actions.numpy(), dtype=np.int32).reshape(shape)
                 status = self._lib.cuju_environment_step(self._handle(), staged.ctypes.data, 0, self._stream(), 0)
         self._check(status)
+        self._wait_in_debug()
         observation, reward, done, final = self._outputs()
         return observation, reward, done, {'final_observation': final, 'score_reward': self._score_reward}
+
+    def _wait_in_debug(self) -> None:
+        """In a `debug` batch every call waits for the device, so a failure raises at its call."""
+        if self.debug:
+            self.synchronize()
 
     def step_async(self, actions: Any) -> None:
         """Starts a step of every environment on the current stream and returns at once; on the

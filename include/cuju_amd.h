@@ -41,8 +41,10 @@ struct cuju_configuration {
     const int *agent_counts; /* [asset_count][2] left/right agents, -1 keeps the bundle's; null keeps all */
     int episode_number; /* GRF episode_number */
     unsigned long long first_index; /* seed-rule index of environment 0 */
-    void *(*allocate)(size_t bytes, void *context); /* reserved, must be null */
-    void (*release)(void *pointer, void *context); /* reserved, must be null */
+    /* device memory from the caller: null when it has none; released once the device is idle.
+       Both null take hipMalloc and hipFree (src/environment_api.h:81-86) */
+    void *(*allocate)(size_t bytes, void *context);
+    void (*release)(void *pointer, void *context);
     void *allocator_context;
     int pin_threads; /* CPU-only options of the reference, ignored */
     int numa;

@@ -83,3 +83,33 @@ def test_step_async_then_wait_equals_step():
         finally:
             batch.close()
     assert found[0] == found[1]
+
+
+def test_torch_allocator_and_debug_give_the_same_steps():
+    """`allocator='torch'` takes the batch's memory from PyTorch's caching allocator (it shows in
+    torch's statistics and returns at close), and a `debug` batch waits at every call; both step
+    as the default batch does."""
+    import cuju_amd
+    found = []
+    for options in ({}, {'allocator': 'torch'}, {'debug': True, 'threads': 4, 'pin_memory': True}):
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated()
+        batch = cuju_amd.BatchEnvironment('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=3, seed=2,
+                                          **options)
+        try:
+            if options.get('allocator') == 'torch':
+                assert torch.cuda.memory_allocated() - before >= 3 * 370_000
+            batch.reset()
+            seen = []
+            for index in range(20):
+                actions = torch.as_tensor(digest_actions(index, 3, batch.agents, batch.action_count), device='cuda:0')
+                seen.append(outputs_bytes(*batch.step(actions)))
+            found.append(seen)
+        finally:
+            batch.close()
+        torch.cuda.synchronize()
+        # Only the last actions tensor may remain; the batch's memory went back.
+        assert torch.cuda.memory_allocated() - before < 1 << 20
+    assert found[0] == found[1] == found[2]
+    with pytest.raises(ValueError, match='allocator'):
+        cuju_amd.BatchEnvironment('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=1, allocator='numa')

@@ -177,10 +177,18 @@ class BatchEnvironment:
                  stacked: bool = False, game_engine_random_seed=None, squeeze: bool = False, agent_counts=None,
                  episode_number: int = 0, first_index: int = 0, check_actions: bool = False,
                  with_raw: bool = False, library: str | None = None, threads: int = 0, allocator: str = 'cuda',
-                 pin_threads: bool = False, numa: bool = False, pin_memory: bool = False, debug: bool = False):
+                 pin_threads: bool = False, numa: bool = False, pin_memory: bool = False, debug: bool = False,
+                 channel_dimensions=(SMM_WIDTH, SMM_HEIGHT)):
         # threads, pin_threads, numa and pin_memory shape the reference's CPU batches; a device batch
         # takes them and has no use for them, as the reference's GPU batch does.
         del threads, pin_threads, numa, pin_memory
+        # GRF's `channel_dimensions`: the SMM's width and height.
+        if (not isinstance(channel_dimensions, (tuple, list)) or len(channel_dimensions) != 2
+                or not all(isinstance(v, int) and v >= 1 for v in channel_dimensions)):
+            raise ConfigurationError(f'expected channel_dimensions of two positive integers (width, height), found '
+                                     f'{channel_dimensions!r}')
+        self._smm_width, self._smm_height = int(channel_dimensions[0]), int(channel_dimensions[1])
+        self.channel_dimensions = (self._smm_width, self._smm_height)
         if allocator not in ('cuda', 'torch'):
             raise ChoiceError(f'expected the allocator cuda or torch, found {allocator!r}')
         self.debug = bool(debug)
@@ -258,7 +266,7 @@ class BatchEnvironment:
             action_set=ACTION_SETS[action_set],
             observation=REPRESENTATIONS[representation] | (REPRESENTATIONS['raw'] if with_raw else 0),
             checkpoints=int(self.checkpoints), numpy_legacy=int(numpy_legacy), auto_reset=int(auto_reset),
-            threads=0, ticks_per_step=physics_steps_per_frame, smm_width=SMM_WIDTH, smm_height=SMM_HEIGHT,
+            threads=0, ticks_per_step=physics_steps_per_frame, smm_width=self._smm_width, smm_height=self._smm_height,
             stack=self.stack,
             fixed_seeds=None if self._fixed is None else self._fixed.ctypes.data,
             agent_counts=self._counts.ctypes.data, episode_number=episode_number, first_index=first_index,
@@ -302,7 +310,7 @@ class BatchEnvironment:
         if representation == 'raw':
             self._observation, self._final = self._raw('raw'), self._raw('final_raw')
         elif representation == 'extracted':
-            shape = (environment_count, self.agents, SMM_HEIGHT, SMM_WIDTH, 4 * self.stack)
+            shape = (environment_count, self.agents, self._smm_height, self._smm_width, 4 * self.stack)
             self._observation = self._buffer('smm', shape, torch.uint8)
             self._final = self._buffer('final_smm', shape, torch.uint8)
         else:

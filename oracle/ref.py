@@ -187,7 +187,7 @@ class ReferenceBatch:
                  threads=0, assignment=None, agent_counts=None, first_index=0,
                  difficulty=None, numpy_legacy=True, episode_number=0,
                  physics_steps_per_frame=10, game_engine_random_seed=None, library_path=None,
-                 with_raw=False):
+                 with_raw=False, channel_dimensions=(96, 72)):
         lib = library(library_path)
         self._lib = lib
         names = [assets] if isinstance(assets, str) else list(assets)
@@ -206,6 +206,7 @@ class ReferenceBatch:
         self.checkpoints = 'checkpoints' in rewards.split(',')
         self.stack = 4 if stacked else 1
         self.representation = representation
+        self.channel_dimensions = tuple(channel_dimensions)
         cfg = Configuration(
             version=2, assets=self._paths, asset_count=len(names),
             assignment=None if self._assignment is None else self._assignment.ctypes.data,
@@ -215,7 +216,8 @@ class ReferenceBatch:
             observation=REPRESENTATIONS[representation] | (REPRESENTATIONS['raw'] if with_raw else 0),
             checkpoints=int(self.checkpoints), numpy_legacy=int(numpy_legacy),
             auto_reset=int(auto_reset), threads=threads,
-            ticks_per_step=physics_steps_per_frame, smm_width=96, smm_height=72,
+            ticks_per_step=physics_steps_per_frame, smm_width=channel_dimensions[0],
+            smm_height=channel_dimensions[1],
             stack=self.stack,
             fixed_seeds=None if self._fixed is None else self._fixed.ctypes.data,
             agent_counts=ctypes.addressof(self._counts), episode_number=episode_number,
@@ -252,7 +254,8 @@ class ReferenceBatch:
         if self.representation == 'raw':
             return self._raw(prefix + 'raw')
         if self.representation == 'extracted':
-            return self._array(prefix + 'smm', np.uint8, (self.environment_count, self.agents, 72, 96, 4 * self.stack))
+            width, height = self.channel_dimensions
+            return self._array(prefix + 'smm', np.uint8, (self.environment_count, self.agents, height, width, 4 * self.stack))
         return self._array(prefix + 'simple115', np.float32,
                            (self.environment_count, self.agents, 115 * self.stack))
 

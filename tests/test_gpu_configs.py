@@ -142,3 +142,9 @@ def test_difficulty_reports_and_overrides(reference_library):
     finally:
         mine.close()
         theirs.close()
+
+
+def test_smm_of_other_dimensions(reference_library):
+    """`channel_dimensions` resizes the SMM on the device as on the reference, stacked."""
+    compare('5_vs_5_l2_r1', 16, 60, seed=4, states=False, representation='extracted', stacked=True,
+            channel_dimensions=(37, 21))

@@ -356,3 +356,17 @@ def test_set_stack_refuses_what_no_minimap_holds(host_library):
         assert b'bytes' in lib.cuju_last_error()
     finally:
         batch.close()
+
+
+def test_smm_of_other_dimensions_matches_the_reference(reference_library, host_library):
+    """GRF's `channel_dimensions` sets the SMM's size; marks fall into the smaller or larger grid as
+    the reference puts them."""
+    digests = []
+    for path in (host_library, reference_library):
+        batch = ref.ReferenceBatch('5_vs_5_l2_r1', environment_count=3, seed=4, threads=2, library_path=path,
+                                   representation='extracted', stacked=True, channel_dimensions=(37, 21))
+        try:
+            digests.append(play(batch, 60, 3))
+        finally:
+            batch.close()
+    assert digests[0] == digests[1]

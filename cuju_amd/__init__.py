@@ -5,11 +5,11 @@ CPU engine for the same seeds and actions. The native library is built in-tree b
 `python -m cuju_amd.build`.
 """
 
-from .environment import BatchEnvironment, episode_pickle, resolve_assets
+from .environment import BatchEnvironment, episode_pickle, memory_estimate, resolve_assets
 from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, ConfigurationError,
                      DeviceError, EnvironmentIndexError, Error, LibraryError, MissingFileError,
                      StateError, UndefinedPathError)
 
-__all__ = ['BatchEnvironment', 'episode_pickle', 'resolve_assets', 'Error', 'ConfigurationError',
+__all__ = ['BatchEnvironment', 'episode_pickle', 'memory_estimate', 'resolve_assets', 'Error', 'ConfigurationError',
            'ChoiceError', 'ArgumentError', 'ActionRangeError', 'EnvironmentIndexError', 'StateError',
            'ClosedError', 'DeviceError', 'UndefinedPathError', 'LibraryError', 'MissingFileError']

@@ -635,3 +635,20 @@ class BatchEnvironment:
 
     def __exit__(self, *exception):
         self.close()
+
+
+class _Bytes(int):
+    """An int of bytes with the attribute `local_memory_bytes`."""
+    local_memory_bytes = 0
+
+
+def memory_estimate(assets, **options) -> int:
+    """The device bytes `BatchEnvironment(assets, **options)` requests, the figure `memory_bytes`
+    reports right after creation (python/cuju/_batch/environment.py:1622-1660). This build sizes
+    the batch by creating it and freeing it at once, so the estimate needs that memory for an
+    instant; `local_memory_bytes` is 0, since the kernels' per-lane stack comes with the launch."""
+    batch = BatchEnvironment(assets, **options)
+    try:
+        return _Bytes(batch.memory_bytes())
+    finally:
+        batch.close()

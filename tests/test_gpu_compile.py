@@ -113,3 +113,14 @@ def test_torch_allocator_and_debug_give_the_same_steps():
     assert found[0] == found[1] == found[2]
     with pytest.raises(ValueError, match='allocator'):
         cuju_amd.BatchEnvironment('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=1, allocator='numa')
+
+
+def test_memory_estimate_is_what_the_batch_reports():
+    import cuju_amd
+    estimate = cuju_amd.memory_estimate('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=8)
+    batch = cuju_amd.BatchEnvironment('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=8)
+    try:
+        assert estimate == batch.memory_bytes() > 8 * 373_552
+        assert estimate.local_memory_bytes == 0
+    finally:
+        batch.close()

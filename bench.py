@@ -35,7 +35,7 @@ HBM_PEAK_GBS = 8000.0
 BYTES_PER_ENV_STEP = 752_257
 # HBM bytes one step launch moves at 16,384 environments, read + written, from rocprofv3
 # FETCH_SIZE and WRITE_SIZE passes scaled by a 1 GiB copy (profiles/step_kernel_11v11_hard_16384.md).
-MEASURED_TRAFFIC = {16384: 143_254_406_073 + 52_734_074_080}
+MEASURED_TRAFFIC = {16384: 144_371_218_771 + 53_184_601_872}
 
 
 def counter_actions(torch, seed, step, environments, agents, device):

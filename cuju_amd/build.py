@@ -34,9 +34,12 @@ COMMON = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math', '
 # for the step kernel on gfx950 (289 against 292 ms per step at 16,384 environments). Runtime
 # unrolling lets loops of unknown trip count issue several iterations' loads together, which the
 # latency-bound step kernel gains about 3% from (331 against 343 ms per step after 100 steps).
+# The instruction scheduler's max-ILP strategy spreads independent work between dependent loads:
+# 276-279 against 280-283 ms per step; the memory-clause strategy and promoting stack arrays to
+# registers measured no better.
 HIP_FLAGS = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math', '-fvisibility=hidden', '-w',
              f'--offload-arch={ARCH}', '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
-             '-mllvm', '-unroll-runtime']
+             '-mllvm', '-unroll-runtime', '-mllvm', '-amdgpu-sched-strategy=max-ilp']
 
 
 def _run(command):

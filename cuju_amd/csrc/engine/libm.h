@@ -912,5 +912,34 @@ HD void sincos(double x, double *s, double *c) {
     *c = cos(x);
 }
 
+// The routines by code, for the checks of tests (the host build's debugging entry points and the
+// device's): float 0 sinf, 1 cosf, 2 powf(x, y), 3 atan2f(x, y), 4 atanf, 5 acosf, 6 asinf,
+// 7 and 8 the sine and cosine of sincosf; double 0 sin, 1 cos, 2 pow(x, y), 3 acos, 4 and 5 the
+// sine and cosine of sincos.
+HD float EvaluateFloat(int which, float x, float y) {
+    switch (which) {
+        case 0: return sinf(x);
+        case 1: return cosf(x);
+        case 2: return powf(x, y);
+        case 3: return atan2f(x, y);
+        case 4: return atanf(x);
+        case 5: return acosf(x);
+        case 6: return asinf(x);
+        case 7: return sincosf(x).s;
+        default: return sincosf(x).c;
+    }
+}
+HD double EvaluateDouble(int which, double x, double y) {
+    double s = 0, c = 0;
+    switch (which) {
+        case 0: return sin(x);
+        case 1: return cos(x);
+        case 2: return pow(x, y);
+        case 3: return acos(x);
+        case 4: sincos(x, &s, &c); return s;
+        default: sincos(x, &s, &c); return c;
+    }
+}
+
 }  // namespace libm
 }  // namespace eng

@@ -65,6 +65,27 @@ __global__ void __launch_bounds__(kDeviceGroupLanes) OutputKernel(eng::Batch b, 
     eng::WriteEnvironmentOutputs(b, env, false);
 }
 
+// The math routines over an index range, for the checks of tests: consecutive float bit patterns
+// from `first` (kind 0), float arrays (kind 1) or double arrays (kind 2). Every lane reads the
+// tables from its workgroup's LDS, as the step does.
+constexpr int kLibmThreads = 256;
+__global__ void __launch_bounds__(kLibmThreads) LibmKernel(int kind, int which, uint32_t first, long long count, const void *x,
+                                                            const void *y, void *out) {
+    eng::libm::StageMathTables();
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        if (kind == 0) {
+            static_cast<float *>(out)[i] = eng::libm::EvaluateFloat(which, eng::FloatOf(first + (uint32_t)i), 0.0f);
+        } else if (kind == 1) {
+            static_cast<float *>(out)[i] =
+                eng::libm::EvaluateFloat(which, static_cast<const float *>(x)[i], static_cast<const float *>(y)[i]);
+        } else {
+            static_cast<double *>(out)[i] =
+                eng::libm::EvaluateDouble(which, static_cast<const double *>(x)[i], static_cast<const double *>(y)[i]);
+        }
+    }
+}
+
 void Check(hipError_t e, const char *what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -95,6 +116,7 @@ public:
     }
     void Fill(void *d, int v, size_t n) override { Check(hipMemset(d, v, n), "hipMemset"); }
     void Synchronize(void *stream) override { Check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize"); }
+    void SynchronizeAll() override { Check(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
     void Reset(const eng::Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *stream) override {
         const int blocks = (b.count + matches_ - 1) / matches_;
         hipLaunchKernelGGL(ResetKernel, dim3(blocks), dim3(matches_ * kDeviceGroupLanes), 0, static_cast<hipStream_t>(stream), b,
@@ -133,6 +155,18 @@ private:
 };
 
 }  // namespace
+
+extern "C" __attribute__((visibility("default"))) int cuju_debug_libm_device(int kind, int which, unsigned int first,
+                                                                            long long count, const void *x, const void *y,
+                                                                            void *out, void *stream) {
+    if (kind < 0 || kind > 2 || which < 0 || which > (kind == 2 ? 5 : 8) || count < 0 || !out || (kind != 0 && (!x || !y)))
+        return -1;
+    if (count == 0) return 0;
+    const long long blocks = std::min<long long>((count + kLibmThreads - 1) / kLibmThreads, 8192);
+    hipLaunchKernelGGL(LibmKernel, dim3((unsigned)blocks), dim3(kLibmThreads), 0, static_cast<hipStream_t>(stream), kind, which,
+                       first, count, x, y, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 namespace eng {
 namespace host {

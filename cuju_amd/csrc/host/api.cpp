@@ -24,12 +24,45 @@ using eng::host::BatchRuntime;
 namespace {
 thread_local std::string lastError;
 thread_local std::string stateBytes;
-thread_local unsigned long long *memoryEstimate = nullptr;
 int Fail(const std::exception &e) {
     lastError = e.what();
     return -1;
 }
 BatchRuntime *Of(void *e) { return static_cast<BatchRuntime *>(e); }
+
+eng::host::Configuration ConfigurationOf(const struct cuju_configuration *s) {
+    if (!s) throw std::invalid_argument("expected a configuration");
+    if (s->version != CUJU_CONFIGURATION_VERSION)
+        throw std::invalid_argument("expected the configuration version " + std::to_string(CUJU_CONFIGURATION_VERSION) + ", found " +
+                                    std::to_string(s->version));
+    if (s->environment_count < 1) throw std::invalid_argument("expected at least one environment, found " + std::to_string(s->environment_count));
+    if (!s->allocate != !s->release) throw std::invalid_argument("expected both allocate and release, or neither");
+    eng::host::Configuration c;
+    for (int i = 0; i < s->asset_count; i++) c.assets.push_back(s->assets[i]);
+    if (s->assignment) c.assignment.assign(s->assignment, s->assignment + s->environment_count);
+    c.animations = s->animations ? s->animations : "";
+    c.count = s->environment_count;
+    c.seed = s->seed;
+    c.actionSet = s->action_set;
+    c.observation = s->observation;
+    c.checkpoints = s->checkpoints != 0;
+    c.numpyLegacy = s->numpy_legacy != 0;
+    c.autoReset = s->auto_reset != 0;
+    c.threads = s->threads;
+    c.allocate = s->allocate;
+    c.release = s->release;
+    c.allocatorContext = s->allocator_context;
+    c.ticksPerStep = s->ticks_per_step;
+    c.smmWidth = s->smm_width;
+    c.smmHeight = s->smm_height;
+    c.stack = s->stack;
+    if (s->fixed_seeds) c.fixedSeeds.assign(s->fixed_seeds, s->fixed_seeds + s->environment_count);
+    if (s->agent_counts) c.agentCounts.assign(s->agent_counts, s->agent_counts + 2 * s->asset_count);
+    c.episodeNumber = s->episode_number;
+    // A larger value fails the range check rather than wrapping.
+    c.firstIndex = (int64_t)(s->first_index < (1ULL << 62) ? s->first_index : (1ULL << 62));
+    return c;
+}
 }  // namespace
 
 #pragma GCC visibility push(default)
@@ -40,44 +73,9 @@ const char *cuju_backend(void) { return eng::host::kBackendName; }
 
 void *cuju_environment_create(const struct cuju_configuration *s) {
     try {
-        if (!s) throw std::invalid_argument("expected a configuration");
-        if (s->version != CUJU_CONFIGURATION_VERSION)
-            throw std::invalid_argument("expected the configuration version " + std::to_string(CUJU_CONFIGURATION_VERSION) + ", found " +
-                                        std::to_string(s->version));
-        if (s->environment_count < 1) throw std::invalid_argument("expected at least one environment, found " + std::to_string(s->environment_count));
-        if (!s->allocate != !s->release) throw std::invalid_argument("expected both allocate and release, or neither");
-        eng::host::Configuration c;
-        for (int i = 0; i < s->asset_count; i++) c.assets.push_back(s->assets[i]);
-        if (s->assignment) c.assignment.assign(s->assignment, s->assignment + s->environment_count);
-        c.animations = s->animations ? s->animations : "";
-        c.count = s->environment_count;
-        c.seed = s->seed;
-        c.actionSet = s->action_set;
-        c.observation = s->observation;
-        c.checkpoints = s->checkpoints != 0;
-        c.numpyLegacy = s->numpy_legacy != 0;
-        c.autoReset = s->auto_reset != 0;
-        c.threads = s->threads;
-        c.allocate = s->allocate;
-        c.release = s->release;
-        c.allocatorContext = s->allocator_context;
-        c.ticksPerStep = s->ticks_per_step;
-        c.smmWidth = s->smm_width;
-        c.smmHeight = s->smm_height;
-        c.stack = s->stack;
-        if (s->fixed_seeds) c.fixedSeeds.assign(s->fixed_seeds, s->fixed_seeds + s->environment_count);
-        if (s->agent_counts) c.agentCounts.assign(s->agent_counts, s->agent_counts + 2 * s->asset_count);
-        c.episodeNumber = s->episode_number;
-        // A larger value fails the range check rather than wrapping.
-        c.firstIndex = (int64_t)(s->first_index < (1ULL << 62) ? s->first_index : (1ULL << 62));
         lastError.clear();
-        auto *b = new BatchRuntime(c, eng::host::MakeLibraryDevice(s->threads));
-        if (memoryEstimate) {
-            *memoryEstimate = b->MemoryBytes();
-            delete b;
-            return nullptr;
-        }
-        return b;
+        const eng::host::Configuration c = ConfigurationOf(s);
+        return new BatchRuntime(c, eng::host::MakeLibraryDevice(s->threads));
     } catch (const std::exception &e) {
         Fail(e);
         return nullptr;
@@ -85,10 +83,18 @@ void *cuju_environment_create(const struct cuju_configuration *s) {
 }
 
 int cuju_memory_estimate(const struct cuju_configuration *settings, unsigned long long *bytes) {
-    memoryEstimate = bytes;
-    cuju_environment_create(settings);
-    memoryEstimate = nullptr;
-    return lastError.empty() ? 0 : -1;
+    try {
+        lastError.clear();
+        eng::host::Configuration c = ConfigurationOf(settings);
+        // The estimate takes nothing from the caller's allocator.
+        c.allocate = nullptr;
+        c.release = nullptr;
+        BatchRuntime sized(c, eng::host::MakeSizingDevice());
+        *bytes = sized.MemoryBytes();
+        return 0;
+    } catch (const std::exception &e) {
+        return Fail(e);
+    }
 }
 int cuju_local_memory_bytes(unsigned long long *bytes) {
     *bytes = 0;

@@ -148,21 +148,18 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_time_needed(co
     }
 }
 
-// The engine's float math routines on arrays, for tests against the C library: `which` is 0 sinf,
-// 1 cosf, 2 powf(x, y), 3 atan2f(x, y), 4 atanf, 5 acosf, 6 asinf.
+// The engine's math routines for tests, by the codes of eng::libm::EvaluateFloat and
+// EvaluateDouble: on arrays, and on the consecutive float bit patterns from `first`.
 extern "C" __attribute__((visibility("default"))) void cuju_debug_libm(int which, const float *x, const float *y, float *out,
-                                                                         int count) {
-    for (int i = 0; i < count; i++) {
-        switch (which) {
-            case 0: out[i] = eng::libm::sinf(x[i]); break;
-            case 1: out[i] = eng::libm::cosf(x[i]); break;
-            case 2: out[i] = eng::libm::powf(x[i], y[i]); break;
-            case 3: out[i] = eng::libm::atan2f(x[i], y[i]); break;
-            case 4: out[i] = eng::libm::atanf(x[i]); break;
-            case 5: out[i] = eng::libm::acosf(x[i]); break;
-            default: out[i] = eng::libm::asinf(x[i]); break;
-        }
-    }
+                                                                         long long count) {
+    for (long long i = 0; i < count; i++) out[i] = eng::libm::EvaluateFloat(which, x[i], y[i]);
+}
+extern "C" __attribute__((visibility("default"))) void cuju_debug_libm_range(int which, uint32_t first, long long count, float *out) {
+    for (long long i = 0; i < count; i++) out[i] = eng::libm::EvaluateFloat(which, eng::FloatOf(first + (uint32_t)i), 0.0f);
+}
+extern "C" __attribute__((visibility("default"))) void cuju_debug_libm_double(int which, const double *x, const double *y,
+                                                                                double *out, long long count) {
+    for (long long i = 0; i < count; i++) out[i] = eng::libm::EvaluateDouble(which, x[i], y[i]);
 }
 
 // The description a scenario builder needs to rebuild a bundle's variant (reverse 0, `parity`),

@@ -168,8 +168,10 @@ BatchRuntime::BatchRuntime(const Configuration &cfg, std::unique_ptr<Device> dev
 }
 
 BatchRuntime::~BatchRuntime() {
+    // Blocks go back to a caller's allocator, which may hand them out at once, so every stream that
+    // may still run this batch's work (a caller's non-blocking stream among them) must be idle.
     try {
-        dev_->Synchronize(nullptr);
+        dev_->SynchronizeAll();
     } catch (...) {
     }
     for (void *p : owned_) {
@@ -194,6 +196,31 @@ void *BatchRuntime::AllocateBytes(size_t bytes) {
     allocated_ += bytes;
     return p;
 }
+
+namespace {
+class SizingDevice : public Device {
+public:
+    const char *Name() const override { return "sizing"; }
+    bool HostMemory() const override { return false; }
+    // Every block is the same placeholder: nothing reads or writes it.
+    void *Allocate(size_t) override { return &placeholder_; }
+    void Release(void *) override {}
+    void ToDevice(void *, const void *, size_t) override {}
+    void ToHost(void *, const void *, size_t) override { throw std::logic_error("a sizing device holds no data"); }
+    void ToDeviceAsync(void *, const void *, size_t, void *) override {}
+    void Fill(void *, int, size_t) override {}
+    void Synchronize(void *) override {}
+    void Reset(const Batch &, const uint8_t *, const int64_t *, const int32_t *, void *) override {}
+    void Step(const Batch &, const int32_t *, void *) override {}
+    void Outputs(const Batch &, int, void *) override {}
+    void CheckFault() override {}
+
+private:
+    alignas(256) unsigned char placeholder_[256] = {};
+};
+}  // namespace
+
+std::unique_ptr<Device> MakeSizingDevice() { return std::make_unique<SizingDevice>(); }
 
 int BatchRuntime::LeftPlayers(int env) const { return VariantAt(slots_[env].bundle * 4).world->scenario.leftTeamSize; }
 int BatchRuntime::RightPlayers(int env) const { return VariantAt(slots_[env].bundle * 4).world->scenario.rightTeamSize; }

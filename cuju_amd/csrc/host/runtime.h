@@ -29,6 +29,8 @@ public:
     virtual void ToDeviceAsync(void *dst, const void *src, size_t bytes, void *stream) = 0;
     virtual void Fill(void *dst, int value, size_t bytes) = 0;
     virtual void Synchronize(void *stream) = 0;
+    // Waits for all work on the device, whichever stream it was enqueued on.
+    virtual void SynchronizeAll() { Synchronize(nullptr); }
     // Resets every environment whose mask byte is nonzero (all when `mask` is null). Arrays are in
     // device memory.
     virtual void Reset(const Batch &b, const uint8_t *mask, const int64_t *seeds, const int32_t *reverse, void *stream) = 0;
@@ -64,6 +66,11 @@ struct Configuration {
     void (*release)(void *pointer, void *context) = nullptr;
     void *allocatorContext = nullptr;
 };
+
+// A device that holds no memory and runs nothing: a batch created on it checks its configuration,
+// loads its bundles and tables on the host and counts the bytes it would allocate on a HIP device
+// (src/environment_api.h:148-152, the reference's EstimateMemory).
+std::unique_ptr<Device> MakeSizingDevice();
 
 // The raw arrays of `outputs` agent views in one buffer, each at a multiple of 256 bytes.
 RawLayout MakeRawLayout(size_t outputs, int players, int sticky);

@@ -189,7 +189,7 @@ class BatchEnvironment:
                                      f'{channel_dimensions!r}')
         self._smm_width, self._smm_height = int(channel_dimensions[0]), int(channel_dimensions[1])
         self.channel_dimensions = (self._smm_width, self._smm_height)
-        if allocator not in ('cuda', 'torch'):
+        if allocator not in ('cuda', 'torch') and allocator is not _SIZING:
             raise ChoiceError(f'expected the allocator cuda or torch, found {allocator!r}')
         self.debug = bool(debug)
         if representation not in REPRESENTATIONS:
@@ -271,6 +271,13 @@ class BatchEnvironment:
             fixed_seeds=None if self._fixed is None else self._fixed.ctypes.data,
             agent_counts=self._counts.ctypes.data, episode_number=episode_number, first_index=first_index,
             allocate=None, release=None, allocator_context=None, pin_threads=0, numa=0, page_aligned=0)
+        if allocator is _SIZING:
+            # memory_estimate: the library sizes the configuration without creating the batch.
+            size = ctypes.c_ulonglong()
+            if lib.cuju_memory_estimate(ctypes.byref(cfg), ctypes.byref(size)) != 0:
+                raise ConfigurationError(lib.cuju_last_error().decode())
+            self.estimated_bytes = int(size.value)
+            return
         self._native = _Native(lib, self._torch_device)
         if allocator == 'torch':
             # The callbacks live on the handle's owner, which outlives every buffer they gave out.
@@ -642,13 +649,17 @@ class _Bytes(int):
     local_memory_bytes = 0
 
 
+# The allocator value by which memory_estimate asks a batch to size itself instead of existing.
+_SIZING = object()
+
+
 def memory_estimate(assets, **options) -> int:
     """The device bytes `BatchEnvironment(assets, **options)` requests, the figure `memory_bytes`
-    reports right after creation (python/cuju/_batch/environment.py:1622-1660). This build sizes
-    the batch by creating it and freeing it at once, so the estimate needs that memory for an
-    instant; `local_memory_bytes` is 0, since the kernels' per-lane stack comes with the launch."""
-    batch = BatchEnvironment(assets, **options)
-    try:
-        return _Bytes(batch.memory_bytes())
-    finally:
-        batch.close()
+    reports right after creation (python/cuju/_batch/environment.py:1622-1660). The library checks
+    the configuration and loads the bundles and tables on the host, but allocates nothing, so a
+    batch too large for the device still gets its size. `local_memory_bytes` is 0: the kernels'
+    per-lane stack comes with the launch."""
+    options = dict(options)
+    options['allocator'] = _SIZING
+    sized = BatchEnvironment(assets, **options)
+    return _Bytes(sized.estimated_bytes)

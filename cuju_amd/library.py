@@ -103,6 +103,7 @@ SIGNATURES = [
     ('cuju_environment_scenario', ctypes.c_char_p, [P, I]),
     ('cuju_scenario_build_bundle', I, [ctypes.POINTER(ScenarioDescription), ctypes.POINTER(ScenarioDescription),
                                        ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]),
+    ('cuju_debug_libm_device', I, [I, I, ctypes.c_uint, ctypes.c_longlong, P, P, P, P]),
 ]
 
 _loaded = {}
@@ -117,6 +118,10 @@ def load(path: str | None = None):
                 f'the HIP library is not built: {path} (run `python -m cuju_amd.build`)')
         lib = ctypes.CDLL(path)
         for name, result, arguments in SIGNATURES:
+            # Another library with the reference ABI (the reference's own, for its scenario
+            # builder) lacks this build's debugging entry points.
+            if not hasattr(lib, name):
+                continue
             function = getattr(lib, name)
             function.restype = result
             function.argtypes = arguments

@@ -150,6 +150,17 @@ struct cuju_scenario_description {
 int cuju_scenario_build_bundle(const struct cuju_scenario_description *even, const struct cuju_scenario_description *odd,
                                const char *name, const char *animations, const char *out);
 
+/* No counterpart in the reference: a check of the device's math routines for tests. It evaluates
+   the routines the step calls (glibc 2.39's algorithms, tables read from LDS as in the step) on
+   `count` inputs: the consecutive float bit patterns from `first` (kind 0), the float arrays `x`
+   and `y` (kind 1) or the double arrays `x` and `y` (kind 2), into `out`. Pointers are device
+   memory; the work is enqueued on `stream`. `which`: float 0 sinf, 1 cosf, 2 powf(x, y),
+   3 atan2f(x, y), 4 atanf, 5 acosf, 6 asinf, 7 and 8 the sine and cosine of sincosf; double 0 sin,
+   1 cos, 2 pow(x, y), 3 acos, 4 and 5 the sine and cosine of sincos. 0, or -1 for arguments out of
+   range or a failed launch. */
+int cuju_debug_libm_device(int kind, int which, unsigned int first, long long count, const void *x, const void *y, void *out,
+                           void *stream);
+
 #ifdef __cplusplus
 }
 #endif

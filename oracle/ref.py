@@ -107,6 +107,9 @@ def library(path=None):
                                                    ctypes.c_void_p, ctypes.POINTER(ctypes.c_ulonglong)]
         lib.cuju_environment_set_state.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p,
                                                    ctypes.c_ulonglong, ctypes.c_void_p]
+        lib.cuju_environment_set_stack.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p,
+                                                   ctypes.c_ulonglong]
+        lib.cuju_environment_episode.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
         _libraries[path] = lib
     return _libraries[path]
 
@@ -324,6 +327,22 @@ class ReferenceBatch:
         the episode words `raw_state` returned."""
         words = (ctypes.c_int * (3 + MAXIMUM_AGENTS))(*episode[:3 + MAXIMUM_AGENTS])
         self._check(self._lib.cuju_environment_set_state(self._handle, index, match, len(match), words))
+
+    def set_stack(self, index, name, frames):
+        """`cuju_environment_set_stack` (`src/environment_api.h:406-419`): the observation stack of
+        environment `index`, `[agents][115 * stack]` float32 or the SMM's uint8 frames."""
+        frames = np.ascontiguousarray(frames)
+        self._check(self._lib.cuju_environment_set_stack(self._handle, index, name.encode(), frames.ctypes.data,
+                                                         frames.nbytes))
+
+    def episode(self, index):
+        """`cuju_environment_episode` (`src/environment_api.h:470-516`): 17 episode values and the
+        played then the scenario's (left, right) difficulties."""
+        values = np.zeros(17, dtype=np.int64)
+        difficulty = np.zeros(4, dtype=np.float32)
+        self._check(self._lib.cuju_environment_episode(self._handle, index, values.ctypes.data,
+                                                       difficulty.ctypes.data))
+        return values, difficulty
 
     def get_state(self, index):
         """`BatchEnvironment.get_state` bytes: pickle length, pickle, then the match bytes."""

@@ -1,63 +1,174 @@
-"""The reference's long digests on the MI355X: full 3,010-step matches and long drill runs with the
-raw, SMM and checkpoint outputs (python/cuju/data/digests.json `long_cases`). A step of four
-environments costs about as much as a full batch, so the five cases play at once, each batch on a
-stream of its own. Opt-in, as the reference's tests/test_long.py is: CUJU_AMD_LONG=1."""
+"""Long horizons on the MI355X, in one loop so that every batch runs at once, each on a stream of
+its own:
+
+* the reference's five long digests (python/cuju/data/digests.json `long_cases`): full 3,010-step
+  matches and 1,500-2,000-step drill runs with raw, SMM and checkpoint outputs, 4 environments each
+  (the reference's tests/test_long.py:59-69);
+* a full 3,000-step episode of each of the five benchmark workloads on two ranges of environments,
+  at the start and at the end of the workload's index range (`first_index`), against
+  per-environment digests of the reference CPU library (`tests/golden/episodes.json`, written by
+  `tests/golden/make_episodes.py`). `CUJU_AMD_EPISODE_STEPS=10000` plays them to 10,000 steps.
+
+These batches put four environments in a wavefront rather than the default sixteen: the sample's
+few environments then spread over more compute units, and a step of a batch takes less time. A
+wavefront's environments are independent, so the geometry changes no result; the other GPU tests
+run the default geometry.
+"""
 
 import hashlib
+import json
 import os
 
 import numpy as np
 import pytest
 import torch
 
-from conftest import PRODUCT, digest_actions, load_digests
+from conftest import PRODUCT, ROOT, digest_actions, load_digests
+import episodes
+from cuju_amd import workloads
 
-pytestmark = [pytest.mark.gpu,
-              pytest.mark.skipif(os.environ.get('CUJU_AMD_LONG') != '1', reason='long digests run with CUJU_AMD_LONG=1')]
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(ROOT, 'tests', 'golden', 'episodes.json')
+
+
+def host(x):
+    return x.detach().cpu().numpy()
 
 
 def raw_bytes(x):
     if isinstance(x, dict):
         return b''.join(raw_bytes(x[name]) for name in sorted(x))
-    return np.ascontiguousarray(x.detach().cpu().numpy()).tobytes()
+    return np.ascontiguousarray(host(x)).tobytes()
 
 
-def test_gpu_reproduces_long_digests():
-    import cuju_amd
+class DeviceSide:
+    """A `cuju_amd.BatchEnvironment` of one workload range on its own stream."""
+
+    def __init__(self, workload, first_index, count, drill_paths):
+        import cuju_amd
+        options = workload.batch_options(first_index, count, drill_paths)
+        assets = options.pop('assets')
+        self.batch = cuju_amd.BatchEnvironment(assets, library=PRODUCT, device='cuda:0', seed=episodes.seed_of(workload),
+                                               **options)
+        self.stream = torch.cuda.Stream()
+        self.stacked = workload.stacked
+
+    def reset(self):
+        with torch.cuda.stream(self.stream):
+            obs = self.batch.reset()
+        self.stream.synchronize()
+        return host(obs)
+
+    def reset_masked(self, mask, seeds):
+        with torch.cuda.stream(self.stream):
+            obs = self.batch.reset(seeds=seeds, mask=torch.as_tensor(mask.astype(bool)))
+        self.stream.synchronize()
+        return host(obs)
+
+    def launch(self, actions):
+        with torch.cuda.stream(self.stream):
+            self.out = self.batch.step(torch.as_tensor(actions, device='cuda:0'))
+
+    def collect(self):
+        self.stream.synchronize()
+        obs, reward, done, info = self.out
+        done = host(done).astype(np.uint8)
+        final = host(info['final_observation']) if done.any() else None
+        return host(obs), host(reward), done, final
+
+    def state(self, index):
+        state = self.batch.get_state(index, stacked=self.stacked)
+        return episodes.engine_bytes(state) if self.stacked else state
+
+    def close(self):
+        self.batch.close()
+
+
+class LongDigestRun:
+    """One of the reference's long digest cases, hashed as its self-check does."""
+
+    def __init__(self, name, case, environments, seed):
+        import cuju_amd
+        self.name, self.case, self.environments = name, case, environments
+        self.batch = cuju_amd.BatchEnvironment(case['assets'], library=PRODUCT, device='cuda:0',
+                                               environment_count=environments, seed=seed, **dict(case['options']))
+        self.stream = torch.cuda.Stream()
+        self.step = 0
+
+    def start(self):
+        with torch.cuda.stream(self.stream):
+            first = self.batch.reset()
+        self.stream.synchronize()
+        self.digest = hashlib.sha256(raw_bytes(first))
+
+    def launch(self):
+        with torch.cuda.stream(self.stream):
+            actions = torch.as_tensor(digest_actions(self.step, self.environments, self.batch.agents,
+                                                     self.batch.action_count), device='cuda:0')
+            self.out = self.batch.step(actions)
+
+    def collect(self):
+        self.stream.synchronize()
+        for x in self.out[:3]:
+            self.digest.update(raw_bytes(x))
+        self.step += 1
+        if self.done and self.batch.stack == 1:
+            for index in range(self.environments):
+                self.digest.update(self.batch.get_state(index))
+
+    @property
+    def done(self):
+        return self.step >= self.case['steps']
+
+    def close(self):
+        self.batch.close()
+
+
+def test_long_horizons_match_the_reference(tmp_path, monkeypatch):
+    with open(GOLDEN) as f:
+        golden = json.load(f)
+    horizon = int(os.environ.get('CUJU_AMD_EPISODE_STEPS', '3000'))
+    checkpoints = [c for c in golden['checkpoints'] if c <= horizon]
+    assert checkpoints, f'no golden checkpoint at or below {horizon} steps'
+    drill_paths = workloads.drill_bundles(str(tmp_path / 'drills'))
+    built = {os.path.basename(p): hashlib.sha256(open(p, 'rb').read()).hexdigest() for p in drill_paths}
+    assert built == golden['drill_bundles'], 'the drill bundles differ from the reference builder\'s'
+
+    monkeypatch.setenv('CUJU_AMD_MATCHES', '4')
     digests = load_digests()
-    environments = digests['environments']
-    cases = sorted(digests['long_cases'].items())
     runs = []
-    for name, case in cases:
-        batch = cuju_amd.BatchEnvironment(case['assets'], library=PRODUCT, device='cuda:0', environment_count=environments,
-                                          seed=digests['seed'], **dict(case['options']))
-        stream = torch.cuda.Stream()
-        with torch.cuda.stream(stream):
-            first = batch.reset()
-        stream.synchronize()
-        digest = hashlib.sha256(raw_bytes(first))
-        runs.append(dict(name=name, case=case, batch=batch, stream=stream, digest=digest))
     try:
-        longest = max(case['steps'] for _, case in cases)
-        for step in range(longest):
-            live = [r for r in runs if step < r['case']['steps']]
-            for r in live:
-                with torch.cuda.stream(r['stream']):
-                    actions = torch.as_tensor(digest_actions(step, environments, r['batch'].agents,
-                                                             r['batch'].action_count), device='cuda:0')
-                    r['out'] = r['batch'].step(actions)
-            for r in live:
-                r['stream'].synchronize()
-                for x in r['out'][:3]:
-                    r['digest'].update(raw_bytes(x))
-            if step % 250 == 249:
-                print(f'long digests: step {step + 1} of {longest}', flush=True)
+        for name, case in sorted(digests['long_cases'].items()):
+            runs.append(LongDigestRun(name, case, digests['environments'], digests['seed']))
+        for number in sorted(workloads.WORKLOADS):
+            w = workloads.WORKLOADS[number]
+            for first, count in episodes.sample_ranges(w):
+                runs.append(episodes.EpisodeRun(w, first, count, DeviceSide(w, first, count, drill_paths),
+                                                checkpoints=checkpoints))
         for r in runs:
-            if r['batch'].stack == 1:
-                for index in range(environments):
-                    r['digest'].update(r['batch'].get_state(index))
-        failed = [r['name'] for r in runs if r['digest'].hexdigest() != r['case']['digest']]
-        assert not failed, f'long digests that differ: {failed}'
+            r.start()
+        step = 0
+        while True:
+            live = [r for r in runs if not r.done]
+            if not live:
+                break
+            for r in live:
+                r.launch()
+            for r in live:
+                r.collect()
+            step += 1
+            if step % 250 == 0:
+                print(f'long horizons: step {step}, {len(live)} batches running', flush=True)
+        failed = [r.name for r in runs if isinstance(r, LongDigestRun) and r.digest.hexdigest() != r.case['digest']]
+        for r in runs:
+            if isinstance(r, episodes.EpisodeRun):
+                expected = golden['workloads'][str(r.workload.number)][str(r.first_index)]
+                for checkpoint in checkpoints:
+                    for i, (got, want) in enumerate(zip(r.digests[checkpoint], expected[str(checkpoint)])):
+                        if got != want:
+                            failed.append(f'{r.name}: environment {r.first_index + i} at step {checkpoint}')
+        assert not failed, f'digests that differ from the reference: {failed}'
     finally:
         for r in runs:
-            r['batch'].close()
+            (r.side if isinstance(r, episodes.EpisodeRun) else r).close()

@@ -3,12 +3,15 @@ the shipped digests and, tick by tick, against the reference library on the same
 actions. The product never loads this build; it locates divergences on the CPU."""
 
 import ctypes
+import json
+import os
 import random
 
 import numpy as np
 import pytest
 
-from conftest import digest_actions, play, short_cases
+import libm_cases
+from conftest import ROOT, digest_actions, play, short_cases
 from oracle import ref
 from oracle.ref import ReferenceBatch
 
@@ -185,35 +188,96 @@ def test_device_time_bias_rounds_as_the_division():
         assert fma(fma(-q, np.float32(700), x), r, q) == x / np.float32(700), k
 
 
-@pytest.mark.parametrize('name,which,binary', [('sinf', 0, False), ('cosf', 1, False), ('powf', 2, True),
-                                               ('atan2f', 3, True), ('atanf', 4, False), ('acosf', 5, False),
-                                               ('asinf', 6, False)])
-def test_engine_float_math_matches_the_c_library(name, which, binary, host_library):
-    """The engine's float routines (restatements of glibc's, which GRF's build links) give the C
-    library's results bit for bit on random finite inputs of every magnitude and on the special
-    values."""
+LIBM_GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden', 'libm.json')
+LIBM_PORTS = os.path.join(ROOT, 'oracle', '_ref', 'liblibm_ports.so')
+
+
+def _libm_golden():
+    with open(LIBM_GOLDEN) as f:
+        return json.load(f)
+
+
+def _host_libm(host_library):
     lib = ctypes.CDLL(host_library)
-    libm = ctypes.CDLL('libm.so.6')
-    fn = getattr(libm, name)
-    fn.restype = ctypes.c_float
-    fn.argtypes = [ctypes.c_float, ctypes.c_float] if binary else [ctypes.c_float]
-    rng = np.random.default_rng(which)
-    n = 20_000
-    bits = rng.integers(0, 1 << 32, size=n, dtype=np.uint64).astype(np.uint32)
-    x = bits.view(np.float32).copy()
-    x[: n // 2] = rng.uniform(-8.0, 8.0, n // 2).astype(np.float32)
-    y = rng.integers(0, 1 << 32, size=n, dtype=np.uint64).astype(np.uint32).view(np.float32).copy()
-    y[: n // 2] = rng.uniform(-4.0, 4.0, n // 2).astype(np.float32)
-    special = np.array([0.0, -0.0, 1.0, -1.0, 0.5, 2.0, np.inf, -np.inf, 1e-40, -1e-40, 3.4e38], dtype=np.float32)
-    x = np.concatenate([x, np.repeat(special, len(special))])
-    y = np.concatenate([y, np.tile(special, len(special))])
-    x, y = np.ascontiguousarray(x[np.isfinite(x) | np.isinf(x)]), np.ascontiguousarray(y[: len(x)])
-    out = np.zeros(len(x), dtype=np.float32)
-    lib.cuju_debug_libm(which, ctypes.c_void_p(x.ctypes.data), ctypes.c_void_p(y.ctypes.data),
-                        ctypes.c_void_p(out.ctypes.data), len(x))
-    want = np.array([fn(float(a), float(b)) if binary else fn(float(a)) for a, b in zip(x, y)], dtype=np.float32)
-    same = (out.view(np.uint32) == want.view(np.uint32)) | (np.isnan(out) & np.isnan(want))
-    assert same.all(), f'{name}: {(~same).sum()} differ, first at {x[~same][0]!r}, {y[~same][0]!r}'
+    lib.cuju_debug_libm_range.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_longlong, ctypes.c_void_p]
+    lib.cuju_debug_libm.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong]
+    lib.cuju_debug_libm_double.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                           ctypes.c_longlong]
+    return lib
+
+
+@pytest.mark.parametrize('name', sorted(libm_cases.UNARY_FLOAT))
+def test_engine_unary_float_math_is_the_reference_port_on_every_input(name, host_library):
+    """sinf, cosf, atanf, acosf and asinf of the engine give the reference ports' bits
+    (include/cuju/libm/sincosf.h:61-212, inverse_trigonometric_float.h:32-272, asinf.h:40-95) on all
+    2**32 inputs: the checksum over every output equals the one the ports wrote
+    (tests/golden/make_libm.py)."""
+    lib = _host_libm(host_library)
+    which = libm_cases.UNARY_FLOAT[name]
+    digest = libm_cases.exhaustive_digest(
+        lambda first, out: lib.cuju_debug_libm_range(which, first, len(out), out.ctypes.data))
+    assert digest == _libm_golden()['exhaustive'][name]
+
+
+def _compare_with_ports(name, got, want):
+    kind = np.uint32 if got.dtype == np.float32 else np.uint64
+    a = np.frombuffer(libm_cases.canonical(got), dtype=kind)
+    b = np.frombuffer(libm_cases.canonical(want), dtype=kind)
+    differ = np.flatnonzero(a != b)
+    assert differ.size == 0, f'{name}: {differ.size} outputs differ from the reference port, the first at sample {differ[0]}'
+
+
+@pytest.mark.parametrize('name', sorted(libm_cases.SAMPLED_FLOAT))
+def test_engine_float_math_is_the_reference_port_on_samples(name, host_library):
+    """powf (include/cuju/libm/powf.h:93-198), atan2f and sincosf on special values, every pair of
+    exponents, random bit patterns and the step's ranges: the checksum equals the ports', and
+    output for output equals them where the port library is built."""
+    lib = _host_libm(host_library)
+    which = libm_cases.SAMPLED_FLOAT[name]
+    x, y = libm_cases.float_pairs(name)
+    out = np.empty_like(x)
+    lib.cuju_debug_libm(which, x.ctypes.data, y.ctypes.data, out.ctypes.data, len(x))
+    if os.path.isfile(LIBM_PORTS):
+        ports = ctypes.CDLL(LIBM_PORTS)
+        ports.oracle_libm_float.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 3 + [ctypes.c_longlong]
+        want = np.empty_like(x)
+        ports.oracle_libm_float(which, x.ctypes.data, y.ctypes.data, want.ctypes.data, len(x))
+        _compare_with_ports(name, out, want)
+    assert libm_cases.sample_digest(out) == _libm_golden()['sampled_float'][name]
+
+
+@pytest.mark.parametrize('name', sorted(libm_cases.SAMPLED_DOUBLE))
+def test_engine_double_math_is_the_reference_port_on_samples(name, host_library):
+    """Double sin, cos (include/cuju/libm/sin_double.h:30-266), pow (pow.h:447-651), acos
+    (acos_double.h:29-143) and sincos on special values, every exponent, random bit patterns, large
+    reduction arguments and the step's ranges, as the ports compute them."""
+    lib = _host_libm(host_library)
+    which = libm_cases.SAMPLED_DOUBLE[name]
+    x, y = libm_cases.double_pairs(name)
+    out = np.empty_like(x)
+    lib.cuju_debug_libm_double(which, x.ctypes.data, y.ctypes.data, out.ctypes.data, len(x))
+    if os.path.isfile(LIBM_PORTS):
+        ports = ctypes.CDLL(LIBM_PORTS)
+        ports.oracle_libm_double.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 3 + [ctypes.c_longlong]
+        want = np.empty_like(x)
+        ports.oracle_libm_double(which, x.ctypes.data, y.ctypes.data, want.ctypes.data, len(x))
+        _compare_with_ports(name, out, want)
+    assert libm_cases.sample_digest(out) == _libm_golden()['sampled_double'][name]
+
+
+def test_libm_checks_catch_a_one_bit_change():
+    """The checksums see a change of the last bit of one output of one block, and NaN payloads
+    and signs do not count."""
+    def fill(first, out, flip=None):
+        out[:] = np.arange(first, first + len(out), dtype=np.uint64).astype(np.uint32).view(np.float32)
+        if flip is not None and first <= flip < first + len(out):
+            out.view(np.uint32)[flip - first] ^= 1
+    base = libm_cases.exhaustive_digest(fill, threads=8)
+    assert base != libm_cases.exhaustive_digest(lambda f, o: fill(f, o, flip=0x3F800000), threads=8)
+    nan_a = np.array([np.nan, 1.0], dtype=np.float32)
+    nan_b = nan_a.copy()
+    nan_b.view(np.uint32)[0] = 0xFFC00001
+    assert libm_cases.sample_digest(nan_a) == libm_cases.sample_digest(nan_b)
 
 
 def _same(a, b):

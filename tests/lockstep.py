@@ -1,0 +1,106 @@
+"""Plays many small device batches at once: each on a stream of its own, all stepped in lockstep
+from the host, so that their kernels run side by side on the GPU. A step of a small batch takes
+about as long as the step of one match, so the batches cost together what one costs alone.
+
+A run has `start()`, `launch()` (enqueue one step), `collect()` (wait for it and absorb its
+outputs) and `done`. `one_match_per_wavefront()` makes the batches created inside it put a single
+environment in each wavefront: a wavefront then follows one match's control flow, and a step of a
+small batch takes the least time. The environments of a wavefront are independent, so the
+geometry changes no result; the tests that run the default geometry (16 environments in a
+wavefront) cover the code where matches of a wavefront wait for each other.
+"""
+
+from __future__ import annotations
+
+import contextlib
+import hashlib
+import os
+import time
+
+import numpy as np
+import torch
+
+from conftest import PRODUCT, digest_actions
+
+
+@contextlib.contextmanager
+def one_match_per_wavefront():
+    before = os.environ.get('CUJU_AMD_MATCHES')
+    os.environ['CUJU_AMD_MATCHES'] = '1'
+    try:
+        yield
+    finally:
+        if before is None:
+            os.environ.pop('CUJU_AMD_MATCHES', None)
+        else:
+            os.environ['CUJU_AMD_MATCHES'] = before
+
+
+def raw_bytes(x):
+    if isinstance(x, dict):
+        return b''.join(raw_bytes(x[name]) for name in sorted(x))
+    return np.ascontiguousarray(x.detach().cpu().numpy()).tobytes()
+
+
+class DigestRun:
+    """A digest case of the reference's self-check (tests/conftest.py:69-98 of the reference):
+    SHA-256 over the reset observation, every step's observation, reward and done, then every
+    environment's state."""
+
+    def __init__(self, name, case, environments, seed, steps):
+        import cuju_amd
+        self.name, self.case, self.environments, self.steps = name, case, environments, steps
+        self.batch = cuju_amd.BatchEnvironment(case['assets'], library=PRODUCT, device='cuda:0',
+                                               environment_count=environments, seed=seed, **dict(case['options']))
+        self.stream = torch.cuda.Stream()
+        self.step = 0
+
+    def start(self):
+        with torch.cuda.stream(self.stream):
+            first = self.batch.reset()
+        self.stream.synchronize()
+        self.digest = hashlib.sha256(raw_bytes(first))
+
+    def launch(self):
+        with torch.cuda.stream(self.stream):
+            actions = torch.as_tensor(digest_actions(self.step, self.environments, self.batch.agents,
+                                                     self.batch.action_count), device='cuda:0')
+            self.out = self.batch.step(actions)
+
+    def collect(self):
+        self.stream.synchronize()
+        for x in self.out[:3]:
+            self.digest.update(raw_bytes(x))
+        self.step += 1
+        if self.done and self.batch.stack == 1:
+            for index in range(self.environments):
+                self.digest.update(self.batch.get_state(index))
+
+    @property
+    def done(self):
+        return self.step >= self.steps
+
+    def hexdigest(self):
+        return self.digest.hexdigest()
+
+    def close(self):
+        self.batch.close()
+
+
+def play(runs, label='lockstep', every=250):
+    """Starts every run, then steps the live ones together until all are done."""
+    for r in runs:
+        r.start()
+    begin = time.time()
+    step = 0
+    while True:
+        live = [r for r in runs if not r.done]
+        if not live:
+            return
+        for r in live:
+            r.launch()
+        for r in live:
+            r.collect()
+        step += 1
+        if every and step % every == 0:
+            print(f'{label}: step {step}, {len(live)} batches running, {time.time() - begin:.0f} s', flush=True)

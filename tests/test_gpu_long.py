@@ -9,10 +9,8 @@ its own:
   per-environment digests of the reference CPU library (`tests/golden/episodes.json`, written by
   `tests/golden/make_episodes.py`). `CUJU_AMD_EPISODE_STEPS=10000` plays them to 10,000 steps.
 
-These batches put four environments in a wavefront rather than the default sixteen: the sample's
-few environments then spread over more compute units, and a step of a batch takes less time. A
-wavefront's environments are independent, so the geometry changes no result; the other GPU tests
-run the default geometry.
+These batches put one environment in a wavefront rather than the default sixteen
+(`lockstep.one_match_per_wavefront`): a step of a small batch then takes the time of one match.
 """
 
 import hashlib
@@ -23,8 +21,9 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import PRODUCT, ROOT, digest_actions, load_digests
 import episodes
+import lockstep
+from conftest import PRODUCT, ROOT, load_digests
 from cuju_amd import workloads
 
 pytestmark = pytest.mark.gpu
@@ -34,12 +33,6 @@ GOLDEN = os.path.join(ROOT, 'tests', 'golden', 'episodes.json')
 
 def host(x):
     return x.detach().cpu().numpy()
-
-
-def raw_bytes(x):
-    if isinstance(x, dict):
-        return b''.join(raw_bytes(x[name]) for name in sorted(x))
-    return np.ascontiguousarray(host(x)).tobytes()
 
 
 class DeviceSide:
@@ -85,47 +78,7 @@ class DeviceSide:
         self.batch.close()
 
 
-class LongDigestRun:
-    """One of the reference's long digest cases, hashed as its self-check does."""
-
-    def __init__(self, name, case, environments, seed):
-        import cuju_amd
-        self.name, self.case, self.environments = name, case, environments
-        self.batch = cuju_amd.BatchEnvironment(case['assets'], library=PRODUCT, device='cuda:0',
-                                               environment_count=environments, seed=seed, **dict(case['options']))
-        self.stream = torch.cuda.Stream()
-        self.step = 0
-
-    def start(self):
-        with torch.cuda.stream(self.stream):
-            first = self.batch.reset()
-        self.stream.synchronize()
-        self.digest = hashlib.sha256(raw_bytes(first))
-
-    def launch(self):
-        with torch.cuda.stream(self.stream):
-            actions = torch.as_tensor(digest_actions(self.step, self.environments, self.batch.agents,
-                                                     self.batch.action_count), device='cuda:0')
-            self.out = self.batch.step(actions)
-
-    def collect(self):
-        self.stream.synchronize()
-        for x in self.out[:3]:
-            self.digest.update(raw_bytes(x))
-        self.step += 1
-        if self.done and self.batch.stack == 1:
-            for index in range(self.environments):
-                self.digest.update(self.batch.get_state(index))
-
-    @property
-    def done(self):
-        return self.step >= self.case['steps']
-
-    def close(self):
-        self.batch.close()
-
-
-def test_long_horizons_match_the_reference(tmp_path, monkeypatch):
+def test_long_horizons_match_the_reference(tmp_path):
     with open(GOLDEN) as f:
         golden = json.load(f)
     horizon = int(os.environ.get('CUJU_AMD_EPISODE_STEPS', '3000'))
@@ -135,32 +88,19 @@ def test_long_horizons_match_the_reference(tmp_path, monkeypatch):
     built = {os.path.basename(p): hashlib.sha256(open(p, 'rb').read()).hexdigest() for p in drill_paths}
     assert built == golden['drill_bundles'], 'the drill bundles differ from the reference builder\'s'
 
-    monkeypatch.setenv('CUJU_AMD_MATCHES', '4')
     digests = load_digests()
     runs = []
     try:
-        for name, case in sorted(digests['long_cases'].items()):
-            runs.append(LongDigestRun(name, case, digests['environments'], digests['seed']))
-        for number in sorted(workloads.WORKLOADS):
-            w = workloads.WORKLOADS[number]
-            for first, count in episodes.sample_ranges(w):
-                runs.append(episodes.EpisodeRun(w, first, count, DeviceSide(w, first, count, drill_paths),
-                                                checkpoints=checkpoints))
-        for r in runs:
-            r.start()
-        step = 0
-        while True:
-            live = [r for r in runs if not r.done]
-            if not live:
-                break
-            for r in live:
-                r.launch()
-            for r in live:
-                r.collect()
-            step += 1
-            if step % 250 == 0:
-                print(f'long horizons: step {step}, {len(live)} batches running', flush=True)
-        failed = [r.name for r in runs if isinstance(r, LongDigestRun) and r.digest.hexdigest() != r.case['digest']]
+        with lockstep.one_match_per_wavefront():
+            for name, case in sorted(digests['long_cases'].items()):
+                runs.append(lockstep.DigestRun(name, case, digests['environments'], digests['seed'], case['steps']))
+            for number in sorted(workloads.WORKLOADS):
+                w = workloads.WORKLOADS[number]
+                for first, count in episodes.sample_ranges(w):
+                    runs.append(episodes.EpisodeRun(w, first, count, DeviceSide(w, first, count, drill_paths),
+                                                    checkpoints=checkpoints))
+        lockstep.play(runs, label='long horizons')
+        failed = [r.name for r in runs if isinstance(r, lockstep.DigestRun) and r.hexdigest() != r.case['digest']]
         for r in runs:
             if isinstance(r, episodes.EpisodeRun):
                 expected = golden['workloads'][str(r.workload.number)][str(r.first_index)]

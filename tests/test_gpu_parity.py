@@ -6,7 +6,8 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import PRODUCT, digest_actions, play, short_cases
+import lockstep
+from conftest import PRODUCT, digest_actions, short_cases
 from oracle import ref
 
 pytestmark = pytest.mark.gpu
@@ -21,13 +22,24 @@ def host(x):
     return x.detach().cpu().numpy()
 
 
-@pytest.mark.parametrize('name,case', short_cases(), ids=[n for n, _ in short_cases()])
-def test_gpu_reproduces_shipped_digest(name, case, digests):
-    batch = gpu_batch(case['assets'], environment_count=digests['environments'], seed=7, **dict(case['options']))
+@pytest.fixture(scope='module')
+def shipped_digests_on_device(digests):
+    """Every short digest case played at once, each batch on a stream of its own."""
+    runs = []
     try:
-        assert play(batch, digests['steps'], digests['environments']) == case['digest']
+        with lockstep.one_match_per_wavefront():
+            for name, case in short_cases():
+                runs.append(lockstep.DigestRun(name, case, digests['environments'], digests['seed'], digests['steps']))
+        lockstep.play(runs, label='short digests', every=0)
+        return {r.name: r.hexdigest() for r in runs}
     finally:
-        batch.close()
+        for r in runs:
+            r.close()
+
+
+@pytest.mark.parametrize('name,case', short_cases(), ids=[n for n, _ in short_cases()])
+def test_gpu_reproduces_shipped_digest(name, case, shipped_digests_on_device):
+    assert shipped_digests_on_device[name] == case['digest']
 
 
 def test_gpu_matches_reference_on_headline_scenario(reference_library):

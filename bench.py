@@ -1,17 +1,25 @@
 """Throughput of the step engine on one MI355X.
 
-The workload is the headline configuration: 16,384 environments of `11_vs_11_hard_stochastic`
-with all 11 left players under agents (the right team is the built-in AI at difficulty 0.95),
-3,000-step episodes, `simple115v2` observations [16384, 11, 115] and automatic resets. A step is
-one `BatchEnvironment.step` of every environment. Actions are uniform integers in [0, 19) from a
-counter-based hash of (seed, step, environment, agent), computed on the device inside the timed
-loop (a few microseconds). As the reference's benchmark does, the first 100 steps after the reset
-are discarded: early steps are cheaper (few stoppages, short histories). The value is environment
-steps per second over the timed steps, with the inputs resident in HBM.
+The default workload is the headline configuration (workload 3 of `cuju_amd.workloads`): 16,384
+environments of `11_vs_11_hard_stochastic` with all 11 left players under agents (the right team
+is the built-in AI at difficulty 0.95), 3,000-step episodes, `simple115v2` observations
+[16384, 11, 115] and automatic resets. `--config N` runs workload N instead (1: 5-a-side, 64
+environments; 2: 11-a-side with one agent, 4,096; 4: self-play stacked with masked resets, 8,192;
+5: the mixed batch of drills, 5-a-side and 11-a-side, 32,768).
 
-Beside it the line reports the roofline of the step kernel (algorithmic HBM bytes per launch over
-its measured duration, against 8 TB/s) and the reference's own CPU thread pool on this host's
-cores, timed on a bounded sample of the same workload.
+A step is one `BatchEnvironment.step` of every environment. Actions are uniform integers in
+[0, 19) from the workloads' counter hash of (seed, step, environment, agent), computed on the
+device before the timed steps; workload 4's masked resets (every 512 steps, 10% of the
+environments, drawn seeds) run inside the timed loop when they fall in it. `--warmup` steps run
+untimed after the reset; the reference's own benchmark discards 100, and the first steps after a
+reset are cheaper than open play, so a line with fewer says so. The value is environment steps
+per second over the timed steps (wall clock, inputs resident in HBM).
+
+Beside it the line reports the per-launch step-kernel durations (HIP events on the stream the
+kernel runs on; median and spread over three rounds of the timed steps), the roofline of the step
+kernel (algorithmic HBM bytes per launch over its mean duration, against 8 TB/s) with the HBM
+traffic rocprofv3 measured for the same window where one was profiled, and the reference's own
+CPU thread pool on this host's cores, timed on a bounded sample of the same workload.
 """
 
 from __future__ import annotations
@@ -19,69 +27,83 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-ASSETS = '11_vs_11_hard_stochastic_l11_r0'
-ENVIRONMENTS = 16384
-AGENTS = 11
-ACTIONS = 19
 HBM_PEAK_GBS = 8000.0
-# Algorithmic bytes of one environment step: the world read and written once (2 x 373,552 B)
-# plus the compulsory I/O of this configuration (actions, observations, reward, done, score).
-BYTES_PER_ENV_STEP = 752_257
-# HBM bytes one step launch moves at 16,384 environments, read + written, from rocprofv3
-# FETCH_SIZE and WRITE_SIZE passes scaled by a 1 GiB copy (profiles/step_kernel_11v11_hard_16384.md).
-MEASURED_TRAFFIC = {16384: 144_371_218_771 + 53_184_601_872}
+WORLD_BYTES = 373_552
+STEADY_WARMUP = 100
+
+# HBM bytes one step launch moves, read + written, from rocprofv3 FETCH_SIZE and WRITE_SIZE passes
+# (each scaled by what the counter reads for a 1 GiB device copy), keyed by (workload,
+# environments, warm-up steps, timed steps): the window of launches the profile averaged.
+MEASURED_TRAFFIC = {
+    (3, 16384, 100, 2): (144_371_218_771 + 53_184_601_872, 'profiles/step_kernel_11v11_hard_16384.md'),
+}
 
 
-def counter_actions(torch, seed, step, environments, agents, device):
-    """SplitMix64 of (seed, step, environment, agent), reduced to [0, 19)."""
-    env = torch.arange(environments, device=device, dtype=torch.int64)[:, None]
-    agent = torch.arange(agents, device=device, dtype=torch.int64)[None, :]
-    x = (seed * 0x9E3779B9 + step * 0x632BE5AB + env * 0x85EBCA77 + agent * 0xC2B2AE3D) & 0x7FFFFFFFFFFFFFFF
-    x = (x ^ (x >> 30)) * 0x3F58476D1CE4E5B9 & 0x7FFFFFFFFFFFFFFF
-    x = (x ^ (x >> 27)) * 0x14AF1C8B9A4A5E1D & 0x7FFFFFFFFFFFFFFF
-    x = x ^ (x >> 31)
-    return (x % ACTIONS).to(torch.int32)
+def algorithmic_bytes(workload, agents_present, agent_axis):
+    """The compulsory HBM bytes of one environment step: the world read and written once, the
+    actions read, the observation written (the stacked frames shifted: 3 of 4 read back), the
+    reward, done and score written."""
+    stack = 4 if workload.stacked else 1
+    io = agents_present * (4 + 460 * stack) + (345 * agents_present * 4 if stack == 4 else 0) + 4 * agent_axis + 5
+    return 2 * WORLD_BYTES + io
 
 
-def cpu_baseline(environments, steps, warmup, seed):
-    """The reference CPU library (its own thread pool, every core it may use) on a sample, timed
-    after the same warm-up as the device."""
+def cpu_model():
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
+def cpu_baseline(workload, environments, steps, warmup, seed, drill_paths):
+    """The reference CPU library (its own thread pool, every core it may use) on a sample of the
+    workload's environments, timed after the same warm-up as the device, on the same inputs."""
+    from cuju_amd import workloads
     from oracle import ref
-    import numpy as np
     if not os.path.isfile(ref.LIBRARY):
         return None
-    batch = ref.ReferenceBatch(ASSETS, environment_count=environments, seed=seed, threads=0)
+    options = workload.batch_options(0, environments, drill_paths)
+    assets = options.pop('assets')
+    batch = ref.ReferenceBatch(assets, seed=seed, threads=0, **options)
     batch.reset()
-    rng = np.random.default_rng(seed)
-    for _ in range(warmup):
-        batch.step(rng.integers(0, ACTIONS, size=(environments, AGENTS), dtype=np.int32))
-    actions = [rng.integers(0, ACTIONS, size=(environments, AGENTS), dtype=np.int32) for _ in range(steps)]
+    agents = batch.agents
+    for step in range(warmup):
+        batch.step(workloads.actions(seed, step, 0, environments, agents))
+    inputs = [workloads.actions(seed, warmup + k, 0, environments, agents) for k in range(steps)]
     start = time.perf_counter()
-    for step in range(steps):
-        batch.step(actions[step])
+    for k in range(steps):
+        batch.step(inputs[k])
     seconds = time.perf_counter() - start
     threads = batch.threads
     batch.close()
     return {'value': environments * steps / seconds, 'unit': 'env_steps/s', 'cores': threads, 'kind': 'reference',
-            'sample': f'{environments} environments of {ASSETS}, {steps} timed steps after a reset and {warmup} '
-                      f'warm-up steps, uniform random actions'}
+            'cpu': cpu_model(),
+            'sample': f'environments 0-{environments - 1} of workload {workload.number}, {steps} timed steps after a '
+                      f'reset and {warmup} warm-up steps, the same counter-hash actions as the device'}
 
 
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument('--gpus', type=int, default=1)
     parser.add_argument('--steps', type=int, default=30)
-    parser.add_argument('--warmup', type=int, default=100)
-    parser.add_argument('--environments', type=int, default=ENVIRONMENTS)
+    parser.add_argument('--warmup', type=int, default=STEADY_WARMUP)
+    parser.add_argument('--config', type=int, default=3, choices=[1, 2, 3, 4, 5])
+    parser.add_argument('--environments', type=int, default=None, help='default: the workload\'s')
     parser.add_argument('--seed', type=int, default=0)
-    parser.add_argument('--cpu-environments', type=int, default=2048)
-    parser.add_argument('--cpu-steps', type=int, default=60)
+    parser.add_argument('--cpu-environments', type=int, default=None)
+    parser.add_argument('--cpu-steps', type=int, default=None)
     parser.add_argument('--no-cpu', action='store_true')
     parser.add_argument('--matches', type=int, default=None, help='environments per workgroup (one wavefront)')
     parser.add_argument('--copy-probe', action='store_true',
@@ -94,22 +116,41 @@ def main():
               f'(environments shard by first_index with no exchange); asked for --gpus {args.gpus}.', file=sys.stderr)
         sys.exit(2)
 
+    import numpy as np
     import torch
     import cuju_amd
+    from cuju_amd import workloads
 
+    workload = workloads.WORKLOADS[args.config]
+    environments = args.environments or workload.environments
     device = torch.device('cuda', 0)
     torch.cuda.set_device(device)
-    print(f'[bench] creating {args.environments} environments of {ASSETS}', file=sys.stderr, flush=True)
-    env = cuju_amd.BatchEnvironment(ASSETS, environment_count=args.environments, seed=args.seed, device=device)
+    drill_paths = None
+    if workload.number == 5:
+        drill_paths = workloads.drill_bundles(os.path.join(tempfile.gettempdir(), 'cuju_amd_drills'))
+    options = workload.batch_options(0, environments, drill_paths)
+    assets = options.pop('assets')
+    print(f'[bench] creating {environments} environments of workload {workload.number}', file=sys.stderr, flush=True)
+    env = cuju_amd.BatchEnvironment(assets, device=device, seed=args.seed, **options)
+    agents = env.agents
+    present = (env.left_agents + env.right_agents).astype(np.float64)
+    bytes_per_step = float(np.mean([algorithmic_bytes(workload, a, agents) for a in present]))
     torch.cuda.synchronize()
     start = time.perf_counter()
     env.reset()
     env.synchronize()
     reset_seconds = time.perf_counter() - start
     print(f'[bench] reset took {reset_seconds:.2f} s', file=sys.stderr, flush=True)
+
+    def masked_reset(step):
+        if workload.reset_every and (step + 1) % workload.reset_every == 0:
+            mask, seeds = workloads.masked_reset(args.seed, step + 1, 0, environments, workload.reset_percent)
+            env.reset(seeds=seeds, mask=torch.as_tensor(mask.astype(bool)))
+
     step = 0
     for k in range(args.warmup):
-        env.step(counter_actions(torch, args.seed, step, args.environments, AGENTS, device))
+        env.step(workloads.actions_torch(torch, args.seed, step, 0, environments, agents, device))
+        masked_reset(step)
         step += 1
         if k % 25 == 24:
             env.synchronize()
@@ -118,7 +159,8 @@ def main():
     print(f'[bench] {args.warmup} warm-up steps done', file=sys.stderr, flush=True)
 
     stream = torch.cuda.current_stream(device)
-    actions = [counter_actions(torch, args.seed, step + k, args.environments, AGENTS, device) for k in range(args.steps)]
+    actions = [workloads.actions_torch(torch, args.seed, step + k, 0, environments, agents, device)
+               for k in range(args.steps)]
     begin = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     end = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -127,13 +169,16 @@ def main():
         begin[k].record(stream)
         env.step(actions[k])
         end[k].record(stream)
+        masked_reset(step + k)
     env.synchronize()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall
     launch_ms = [b.elapsed_time(e) for b, e in zip(begin, end)]
     mean_launch_s = sum(launch_ms) / len(launch_ms) / 1000.0
-    value = args.environments * args.steps / wall
-    achieved = BYTES_PER_ENV_STEP * args.environments / mean_launch_s / 1e9
+    rounds = [chunk for chunk in np.array_split(np.array(launch_ms), min(3, args.steps)) if len(chunk)]
+    round_rates = [environments * len(chunk) / (chunk.sum() / 1000.0) for chunk in rounds]
+    value = environments * args.steps / wall
+    achieved = bytes_per_step * environments / mean_launch_s / 1e9
     print(f'[bench] {args.steps} steps in {wall:.2f} s, mean step kernel {mean_launch_s * 1000:.1f} ms', file=sys.stderr,
           flush=True)
     env.close()
@@ -148,8 +193,11 @@ def main():
     baseline = None
     if not args.no_cpu:
         print('[bench] timing the reference CPU thread pool', file=sys.stderr, flush=True)
-        baseline = cpu_baseline(args.cpu_environments, args.cpu_steps, args.warmup, args.seed)
+        cpu_environments = args.cpu_environments or min(environments, 2048)
+        cpu_steps = args.cpu_steps or (60 if workload.number != 1 else 600)
+        baseline = cpu_baseline(workload, cpu_environments, cpu_steps, args.warmup, args.seed, drill_paths)
 
+    traffic = MEASURED_TRAFFIC.get((workload.number, environments, args.warmup, args.steps))
     line = {
         'metric': 'env steps/sec on 1 MI355X (11v11, 16384 envs) + bit-exact digest match',
         'value': value,
@@ -162,14 +210,25 @@ def main():
         'scaling': 'weak',
         'vs_baseline': None,
         'dtype': 'f32',
-        'data': 'synthetic: counter-hash uniform actions in [0, 19) on the shipped 11_vs_11_hard_stochastic bundle',
-        'config': {'workload': f'{ASSETS}: {args.environments} environments x {AGENTS} agents, simple115v2, '
-                               f'3000-step episodes, auto reset', 'environments': args.environments,
-                   'agents': AGENTS, 'reset_seconds': reset_seconds},
+        'data': 'synthetic: counter-hash uniform actions in [0, 19) on the shipped bundles (workload 5: drills built '
+                'by the scenario builder)',
+        'config': {'workload': workload.description, 'number': workload.number, 'environments': environments,
+                   'agents': agents, 'reset_seconds': reset_seconds,
+                   'steady_state': args.warmup >= STEADY_WARMUP},
+        'launch_ms': {'mean': mean_launch_s * 1000.0, 'median': statistics.median(launch_ms), 'min': min(launch_ms),
+                      'max': max(launch_ms)},
+        'rounds': {'env_steps_per_s': round_rates, 'median': statistics.median(round_rates),
+                   'spread': (max(round_rates) - min(round_rates)) / statistics.median(round_rates)},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': achieved / HBM_PEAK_GBS, 'traffic': MEASURED_TRAFFIC.get(args.environments)},
+                     'frac': achieved / HBM_PEAK_GBS, 'bytes_per_env_step': bytes_per_step,
+                     'traffic': traffic[0] if traffic else None,
+                     'traffic_window': (f'warm-up {args.warmup}, timed {args.steps}: {traffic[1]}' if traffic
+                                        else 'not profiled for this window')},
         'cpu_baseline': baseline,
     }
+    if args.warmup < STEADY_WARMUP:
+        line['config']['note'] = (f'{args.warmup} warm-up steps: the timed steps include early ones, which are '
+                                  f'cheaper than open play; the reference discards {STEADY_WARMUP}')
     print(json.dumps(line))
 
 

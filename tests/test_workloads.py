@@ -1,0 +1,49 @@
+"""The workloads' inputs: the counter hash gives the same draws as Python integers, numpy and torch
+(so the host, the oracle and the device consume identical inputs), a slice of a workload gets the
+inputs of the same environments in the full batch, and workload 5's drill family and assignment."""
+
+import numpy as np
+import torch
+
+from cuju_amd import workloads
+
+
+def test_draws_agree_between_python_numpy_and_torch():
+    seed, step, first, count, columns = 1003, 4097, 16376, 8, 11
+    a = workloads.draw(seed, step, np.arange(first, first + count), columns)
+    b = workloads.draw_torch(torch, seed, step, first, count, columns, 'cpu').numpy()
+    c = np.array([[workloads.draw_scalar(seed, step, first + i, j) for j in range(columns)] for i in range(count)])
+    assert a.dtype == np.int64 and (a >= 0).all() and (a < 2 ** 31).all()
+    assert np.array_equal(a, b) and np.array_equal(a, c)
+    t = workloads.actions_torch(torch, seed, step, first, count, columns, 'cpu').numpy()
+    assert np.array_equal(t, workloads.actions(seed, step, first, count, columns))
+
+
+def test_actions_are_uniform_and_slices_agree():
+    full = workloads.actions(3, 12, 0, 4096, 11)
+    assert full.min() == 0 and full.max() == 18
+    counts = np.bincount(full.reshape(-1), minlength=19)
+    assert counts.min() > 0.9 * full.size / 19 and counts.max() < 1.1 * full.size / 19
+    assert np.array_equal(workloads.actions(3, 12, 1000, 24, 11), full[1000:1024])
+
+
+def test_masked_resets_draw_a_tenth_with_seeds_in_range():
+    mask, seeds = workloads.masked_reset(4, 512, 0, 8192, 10)
+    assert 0.08 < mask.mean() < 0.12
+    assert seeds.min() >= 0 and seeds.max() <= 0xFFFFFFFF
+    m2, s2 = workloads.masked_reset(4, 512, 100, 50, 10)
+    assert np.array_equal(m2, mask[100:150]) and np.array_equal(s2, seeds[100:150])
+
+
+def test_drill_family_and_the_mixed_assignment():
+    assert len(workloads.DRILLS) == 36
+    distances = sorted({d.metres for d in workloads.DRILLS})
+    assert distances[0] == 20 and distances[-1] == 35
+    assert 0.36 < workloads.ball_x(35) < workloads.ball_x(20) < 0.65
+    w = workloads.WORKLOADS[5]
+    assignment = w.assignment(0, 32768)
+    drills = len(workloads.DRILLS)
+    assert (assignment < drills).mean() == 0.5
+    assert (assignment == drills).mean() == 0.25 and (assignment == drills + 1).mean() == 0.25
+    assert len(set(assignment[assignment < drills].tolist())) == drills
+    assert np.array_equal(w.assignment(32760, 8), assignment[32760:])

@@ -44,6 +44,7 @@ STEADY_WARMUP = 100
 # environments, warm-up steps, timed steps): the window of launches the profile averaged.
 MEASURED_TRAFFIC = {
     (3, 16384, 100, 2): (144_371_218_771 + 53_184_601_872, 'profiles/step_kernel_11v11_hard_16384.md'),
+    (3, 16384, 5, 20): (142_132_616_184 + 53_741_422_392, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
 }
 
 

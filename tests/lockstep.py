@@ -36,6 +36,14 @@ def one_match_per_wavefront():
             os.environ['CUJU_AMD_MATCHES'] = before
 
 
+def uncaptured(capsys):
+    """A report function that prints to the terminal whatever pytest captures."""
+    def report(line):
+        with capsys.disabled():
+            print(line, flush=True)
+    return report
+
+
 def raw_bytes(x):
     if isinstance(x, dict):
         return b''.join(raw_bytes(x[name]) for name in sorted(x))
@@ -87,8 +95,10 @@ class DigestRun:
         self.batch.close()
 
 
-def play(runs, label='lockstep', every=250):
-    """Starts every run, then steps the live ones together until all are done."""
+def play(runs, label='lockstep', every=250, report=print):
+    """Starts every run, then steps the live ones together until all are done. Every `every`
+    steps `report` gets a progress line: a test passes one that writes past pytest's capture, so
+    that a long run keeps printing."""
     for r in runs:
         r.start()
     begin = time.time()
@@ -103,4 +113,4 @@ def play(runs, label='lockstep', every=250):
             r.collect()
         step += 1
         if every and step % every == 0:
-            print(f'{label}: step {step}, {len(live)} batches running, {time.time() - begin:.0f} s', flush=True)
+            report(f'{label}: step {step}, {len(live)} batches running, {time.time() - begin:.0f} s')

@@ -78,7 +78,7 @@ class DeviceSide:
         self.batch.close()
 
 
-def test_long_horizons_match_the_reference(tmp_path):
+def test_long_horizons_match_the_reference(tmp_path, capsys):
     with open(GOLDEN) as f:
         golden = json.load(f)
     horizon = int(os.environ.get('CUJU_AMD_EPISODE_STEPS', '3000'))
@@ -99,7 +99,7 @@ def test_long_horizons_match_the_reference(tmp_path):
                 for first, count in episodes.sample_ranges(w):
                     runs.append(episodes.EpisodeRun(w, first, count, DeviceSide(w, first, count, drill_paths),
                                                     checkpoints=checkpoints))
-        lockstep.play(runs, label='long horizons')
+        lockstep.play(runs, label='long horizons', report=lockstep.uncaptured(capsys))
         failed = [r.name for r in runs if isinstance(r, lockstep.DigestRun) and r.hexdigest() != r.case['digest']]
         for r in runs:
             if isinstance(r, episodes.EpisodeRun):

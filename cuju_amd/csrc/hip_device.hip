@@ -10,8 +10,10 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "host/runtime.h"
 
@@ -90,6 +92,32 @@ void Check(hipError_t e, const char *what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// The working memory of the step that allocates nothing (cuju_environment_step_no_alloc): the
+// per-environment Scratch blocks of at most kStaticScratchEnvironments environments, 4.3 MB, one
+// copy on each GPU for the life of the process. Every such call on a GPU shares it: calls that
+// overlap on one GPU race. Nothing in it needs to start at zero, since the step builds every
+// list, plan, key array and time walk before reading it.
+constexpr int kStaticScratchEnvironments = 64;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchEnvironments * sizeof(eng::Scratch)];
+
+// The device address of `scratch` on each GPU. In host code the array's name stands in for the
+// symbol only; its address on a device comes from hipGetSymbolAddress with that device current.
+std::mutex gScratchMutex;
+std::vector<void *> gScratchAddress;
+
+void *StaticScratchOfCurrentDevice() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(gScratchMutex);
+    if ((int)gScratchAddress.size() <= device) gScratchAddress.resize(device + 1, nullptr);
+    if (!gScratchAddress[device]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        gScratchAddress[device] = p;
+    }
+    return gScratchAddress[device];
+}
+
 class HipDevice : public eng::host::Device {
 public:
     HipDevice() {
@@ -99,6 +127,9 @@ public:
         Check(hipGetDeviceCount(&n), "hipGetDeviceCount");
         if (n < 1) throw std::runtime_error("no HIP device");
         ClearFault();
+        // The batch is created with its device current: look the static scratch up now, so the
+        // step that allocates nothing makes no runtime call besides its launch.
+        staticScratch_ = static_cast<eng::Scratch *>(StaticScratchOfCurrentDevice());
     }
     const char *Name() const override { return "hip"; }
     bool HostMemory() const override { return false; }
@@ -134,6 +165,10 @@ public:
         hipLaunchKernelGGL(OutputKernel, dim3(1), dim3(kDeviceGroupLanes), 0, static_cast<hipStream_t>(stream), b, env);
         Check(hipGetLastError(), "output launch");
     }
+    eng::Scratch *StaticScratch(int *environments) override {
+        *environments = staticScratch_ ? kStaticScratchEnvironments : 0;
+        return staticScratch_;
+    }
     void CheckFault() override {
         uint32_t fault = 0;
         int32_t env = 0;
@@ -146,6 +181,7 @@ public:
 
 private:
     int matches_ = kMaxMatches < 16 ? kMaxMatches : 16;
+    eng::Scratch *staticScratch_ = nullptr;
     void ClearFault() {
         const uint32_t zero = 0;
         const int32_t none = 0x7fffffff;

@@ -170,6 +170,14 @@ int cuju_environment_step(void *e, const int *actions, int on_device, void *stre
         return Fail(ex);
     }
 }
+int cuju_environment_step_no_alloc(void *e, const int *actions, void *stream) {
+    try {
+        Of(e)->StepWithStaticScratch(actions, stream);
+        return 0;
+    } catch (const std::exception &ex) {
+        return Fail(ex);
+    }
+}
 int cuju_environment_step_async(void *e, const int *actions, int on_device, void *stream) {
     return cuju_environment_step(e, actions, on_device, stream, 0);
 }

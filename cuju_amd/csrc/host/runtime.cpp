@@ -330,6 +330,19 @@ void BatchRuntime::Step(const int32_t *actions, bool onDevice, void *stream, boo
     }
 }
 
+void BatchRuntime::StepWithStaticScratch(const int32_t *actions, void *stream) {
+    CheckStarted();
+    int capacity = 0;
+    Scratch *scratch = dev_->StaticScratch(&capacity);
+    if (!scratch) throw std::logic_error("expected a device with a static scratch array for a step that allocates nothing");
+    if (b_.count > capacity)
+        throw std::invalid_argument("expected at most " + std::to_string(capacity) +
+                                    " environments for a step that allocates nothing, found " + std::to_string(b_.count));
+    Batch b = b_;
+    b.scratch = scratch;
+    dev_->Step(b, actions, stream);
+}
+
 void BatchRuntime::Synchronize(void *stream) {
     dev_->Synchronize(stream);
     dev_->CheckFault();

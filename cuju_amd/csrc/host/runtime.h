@@ -40,6 +40,12 @@ public:
     // Throws when a launch since the last check reached an undefined path.
     virtual void CheckFault() = 0;
     virtual int Threads() const { return 0; }
+    // The device's own scratch array for a step that allocates nothing, and the environments it
+    // holds; null when the device has none.
+    virtual Scratch *StaticScratch(int *environments) {
+        *environments = 0;
+        return nullptr;
+    }
 };
 
 struct Configuration {
@@ -97,6 +103,9 @@ public:
     void ResetMasked(const uint8_t *mask, bool maskOnDevice, const int64_t *seeds, const int32_t *reverse, void *stream);
     void ResetDone(void *stream);
     void Step(const int32_t *actions, bool onDevice, void *stream, bool synchronize);
+    // A step on device actions whose working memory is the device's static scratch array instead
+    // of the batch's: it allocates nothing and waits for nothing.
+    void StepWithStaticScratch(const int32_t *actions, void *stream);
     void Synchronize(void *stream);
     void SetDifficulty(const float *difficulty);
     float Difficulty(int env, int side) const;

@@ -91,6 +91,7 @@ SIGNATURES = [
     ('cuju_environment_reset_masked', I, [P, P, I, P, P, P, I]),
     ('cuju_environment_reset_done', I, [P, P]),
     ('cuju_environment_step', I, [P, P, I, P, I]),
+    ('cuju_environment_step_no_alloc', I, [P, P, P]),
     ('cuju_environment_step_async', I, [P, P, I, P]),
     ('cuju_environment_step_wait', I, [P]),
     ('cuju_environment_synchronize', I, [P, P]),

@@ -88,6 +88,14 @@ int cuju_environment_reset_done(void *environment, void *stream);
 int cuju_environment_step(void *environment, const int *actions, int on_device, void *stream, int synchronize);
 /* src/environment_api.h:323 */
 int cuju_environment_step_async(void *environment, const int *actions, int on_device, void *stream);
+/* No counterpart in the reference: cuju_environment_step for callers that cannot allocate (code
+   under HIP graph capture, serving loops that forbid device allocation). The step runs on
+   `stream` with device actions int32 [environments][agents], unchecked, and returns without
+   waiting; its working memory is a static array of the library on each GPU instead of the
+   batch's, so the call allocates and frees nothing. It takes batches of at most 64 environments
+   (-1 with cuju_last_error() beyond). Every such call on a GPU shares that GPU's array: calls that
+   overlap on one GPU race, so a caller serializes them (one stream, or events). */
+int cuju_environment_step_no_alloc(void *environment, const int *actions, void *stream);
 /* src/environment_api.h:341 */
 int cuju_environment_step_wait(void *environment);
 /* src/environment_api.h:353 */

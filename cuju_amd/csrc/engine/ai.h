@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The built-in player AI: formation positions, the offside trap, the commands of a player without a
 // gamer and of a gamer's player. Expressions with a double literal run in double, as in GRF.
 // Semantics: include/cuju/simulation/ai_controller.h:16-2494.

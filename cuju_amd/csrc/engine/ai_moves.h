@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The player AI, first half: the state it reads, the defensive component, the ball commands and
 // the movement towards the ball, the formation and the support positions.
 // Semantics: include/cuju/simulation/ai_controller.h:418-1620.

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The player AI, second half: decisions on the ball, celebrations, set pieces, the command queue of
 // a player without a gamer and of a gamer's player.
 // Semantics: include/cuju/simulation/ai_controller.h:1620-2494.

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Keyframe poses, skeleton transforms, and the per-tick application of an animation frame to the
 // nodes of a humanoid with GRF's smoothing. Semantics: include/cuju/animation/keyframes.h:16-194,
 // include/cuju/animation/skeleton.h:98-222, include/cuju/animation/apply.h:16-367,

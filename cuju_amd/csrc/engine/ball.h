@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Ball flight, the earliest reach times of players, and player possession.
 // Semantics: include/cuju/ball.h:23-348 (prediction), include/cuju/ai_time.h:97-239 (time needed,
 // the device form), include/cuju/possession.h:35-123 (scan),

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // GRF's in-game camera. It never affects play, but its pose is part of the state and its shake
 // draws two numbers a tick from the world RNG. Semantics: include/cuju/simulation/camera.h:15-170.
 #pragma once

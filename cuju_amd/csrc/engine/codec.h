@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Host-side codec between GRF's state bytes and a World. GRF's format is the raw little-endian
 // bytes of each field, in the engine's object order (the order of
 // src/environment_state.cpp:11-100 and include/cuju/state/environment_state.h), lists as an int32

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Keyboard input of the gamers (agents), and which player each gamer controls.
 // Semantics: include/cuju/simulation/human_controller.h:11-117,
 // include/cuju/simulation/team_select.h:13-207, include/cuju/batch/agent_setup.h:15-70.

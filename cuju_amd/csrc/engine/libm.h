@@ -1,3 +1,10 @@
+// SPDX-License-Identifier: LGPL-2.1-or-later AND MIT AND SunPro
+// Restates the GNU C Library 2.39's math routines: sin, cos, acos and asinf from the GNU C Library
+// (Copyright (C) 2001-2024 Free Software Foundation, Inc.; Copyright (C) 1993 Sun Microsystems, Inc.;
+// LGPL 2.1 or later), sinf, cosf, powf and pow from Arm Optimized Routines (Copyright (c) 2017-2020
+// Arm Limited; MIT), atanf, atan2f and acosf from fdlibm (Copyright (C) 1993 Sun Microsystems, Inc.:
+// Developed at SunPro, a Sun Microsystems, Inc. business. Permission to use, copy, modify, and
+// distribute this software is freely granted, provided that this notice is preserved); see NOTICE.
 // The math routines GRF calls, computed as glibc 2.39 computes them on x86-64 with FMA, so results
 // agree to the last bit on the host and on gfx950. Each routine follows the published algorithm
 // named above it; "fused" steps are the contractions of glibc's FMA build and are written as

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // One tick of a match: each stage runs in the frame it expects, between two MirrorMatch calls.
 // Semantics: include/cuju/simulation/match_process.h:17-374.
 #pragma once

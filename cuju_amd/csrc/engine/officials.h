@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Player commands, the force fields and offside lines that the AI shares with the officials, and
 // the tick of the referee and the two linesmen.
 // Semantics: include/cuju/simulation/humanoid_process.h:18-83 (commands),

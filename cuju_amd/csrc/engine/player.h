@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The controllers of the players (reaction times, situation ratings, the gamer's buttons) and the
 // tick of a player's humanoid (next frame, next animation, ball touches, smuggles).
 // Semantics: include/cuju/simulation/player_controller.h:15-248,

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The referee (half time, balls out of play, fouls, offside, the start of each set piece), the
 // collisions of the ball with the players and of the players with each other, and the record of a
 // touch. Semantics: include/cuju/simulation/referee.h:15-353,

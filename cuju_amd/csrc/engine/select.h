@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Animation selection of players and officials: a crude filter over the animation table, stable
 // sorts by similarity keys, and the physics plan of the chosen animation.
 // Semantics: include/cuju/simulation/select_animation.h:37-2795 (every expression keeps GRF's

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The reset of the world for a set piece, the placement of the players for it and sending-offs.
 // The placement keeps every conversion between double and float of GRF's arithmetic.
 // Semantics: include/cuju/simulation/reset.h:15-721.

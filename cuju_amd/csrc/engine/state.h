@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The match of one environment: GRF's serialized engine objects (their fields are GRF's state
 // format, include/cuju/state/environment_state.h:91-882) plus the frame bookkeeping a state omits.
 // Each struct lists its fields in GRF's byte order and visits them in that order, so one routine

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Read-only tables of the simulation, laid out as flat arrays addressed by index so one host build
 // step produces them and a single copy moves them to HBM (every span is an index range, not a
 // pointer). Semantics follow include/cuju/animation/animation_data.h:21-155,

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The team AI (tactics, offside trap, danger ranking, attacking runs, dynamic roles, man marking)
 // and the tick of a team (possession amounts, players, gamer switches, designated player).
 // Semantics: include/cuju/simulation/team_ai.h:15-533, include/cuju/simulation/team_process.h:134-312.

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Team queries the player AI and the team AI share: lines, tactic properties, the closest players,
 // the goalkeeper, the best possession player, gamer switch targets, and the pose offsets of a
 // player. Semantics: include/cuju/simulation/ai_controller.h:43-87 (Line),

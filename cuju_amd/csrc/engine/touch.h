@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Touch vectors (the ball momentum a touch gives) and pass/shot aiming.
 // Semantics: include/cuju/simulation/touch.h:15-400 (results depend on the number and order of the
 // RNG draws), include/cuju/simulation/ai_functions.h:27-190.

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // World access, frame mirroring, the world RNG and the per-player helpers every stage reads.
 // Semantics: include/cuju/simulation/world.h:37-167 (frames and mirrors),
 // include/cuju/simulation/access.h:13-63, include/cuju/simulation/humanoid.h:118-420,

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Host loaders. Formats: include/cuju/animation/animation_data.h:210-307 (CUJANIM1),
 // include/cuju/animation/skeleton.h:41-85 (CUJHUM1), include/cuju/simulation/static_data.h:72-105,
 // include/cuju/batch/batch_core.h:660-752 (CUJASSET1). Derived values:

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // Host-side construction of everything a match reads besides its world: the animation tables and
 // their derived records, the skeletons and static data of each scenario variant, the reset
 // templates of a bundle with any agent counts, and the codec between GRF's state bytes and a

@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The scenario builder (include/cuju/assets/scenario_builder.h:570-784). A variant's template is
 // the state GRF's `GameEnv::reset` leaves before the ticks that bring the match into play: every
 // field below is what GRF's constructors set, then this engine's reset from the template draws

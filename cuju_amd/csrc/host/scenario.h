@@ -1,3 +1,6 @@
+// SPDX-License-Identifier: Apache-2.0
+// Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
+// Research Football (Copyright 2019 Google LLC); see NOTICE.
 // The scenario builder: the agentless `l0_r0` bundle ("CUJASSET1") of a GRF scenario, built on the
 // host from a description of what the scenario file sets (include/cuju/assets/scenario_builder.h,
 // src/scenario_api.h). It runs this engine's own reset and kick-off ticks, so a bundle it writes

@@ -107,18 +107,6 @@ class _StateUnpickler(pickle.Unpickler):
         raise pickle.UnpicklingError(f'expected only the episode logic, found `{module}.{name}`')
 
 
-class _DeviceArray:
-    """A device buffer that `torch.as_tensor` reads through `__cuda_array_interface__`."""
-
-    _TYPES = {torch.float32: '<f4', torch.int32: '<i4', torch.uint8: '|u1', torch.bool: '|b1'}
-
-    def __init__(self, pointer, shape, dtype, owner):
-        self.owner = owner
-        self.__cuda_array_interface__ = {'data': (pointer, False), 'shape': tuple(shape),
-                                         'typestr': self._TYPES[dtype], 'version': 2,
-                                         'strides': None}
-
-
 class _TorchAllocator:
     """`allocate` and `release` over PyTorch's caching allocator (python/cuju/_batch/allocator.py):
     the batch's device memory then shows in torch's statistics. Blocks come from the device's
@@ -156,6 +144,7 @@ class _Native:
 
     def free(self):
         if self.handle:
+            _operators.closed(self.handle)
             with torch.cuda.device(self.device):
                 self.lib.cuju_environment_destroy(self.handle)
             self.handle = None
@@ -327,9 +316,13 @@ class BatchEnvironment:
         self._reward = self._buffer('reward', (environment_count, self.agents), torch.float32)
         self._done = self._buffer('done', (environment_count,), torch.uint8)
         self._score_reward = self._buffer('score_reward', (environment_count,), torch.int32)
+        # The library buffer behind each output (raw arrays are located by offset instead).
+        observation_name = 'smm' if representation == 'extracted' else 'simple115'
+        self._buffer_names = {'observation': observation_name, 'final': 'final_' + observation_name,
+                              'reward': 'reward', 'done': 'done', 'score_reward': 'score_reward'}
         self._pending = None
-        # The key under which torch.compile's operators find this batch.
-        self._operator = _operators.register(self)
+        # torch.compile's operator names the batch by its native handle.
+        _operators.opened(handle, lib)
 
     # ---- plumbing ----
     @property
@@ -355,7 +348,7 @@ class BatchEnvironment:
         pointer = self._lib.cuju_environment_buffer(self._handle(), name.encode())
         if not pointer:
             raise from_library(self._lib.cuju_last_error().decode())
-        return torch.as_tensor(_DeviceArray(pointer, shape, dtype, self._native), device=self._torch_device)
+        return torch.as_tensor(_library.DeviceArray(pointer, shape, dtype, self._native), device=self._torch_device)
 
     def _describe_raw(self):
         """Name, type, shape and byte offset of each raw array (src/environment_api.h:446-460)."""
@@ -376,7 +369,7 @@ class BatchEnvironment:
         pointer = self._lib.cuju_environment_buffer(self._handle(), name.encode())
         if not pointer:
             raise from_library(self._lib.cuju_last_error().decode())
-        return {field: torch.as_tensor(_DeviceArray(pointer + offset, shape, dtype, self._native), device=self._torch_device)
+        return {field: torch.as_tensor(_library.DeviceArray(pointer + offset, shape, dtype, self._native), device=self._torch_device)
                 for field, dtype, shape, offset in self._raw_fields}
 
     def raw(self) -> dict:
@@ -452,44 +445,36 @@ class BatchEnvironment:
     def reset_done(self) -> None:
         """Starts the next episode of every environment whose done flag is set."""
         if torch.compiler.is_compiling():
-            torch.ops.cuju_amd.reset_done(self._operator_key(), self._operator_outputs())
+            self._operator_call(True, torch.empty(0, dtype=torch.int32, device=self._torch_device))
             return
         with torch.cuda.device(self._torch_device):
             self._check(self._lib.cuju_environment_reset_done(self._handle(), self._stream()))
         self._wait_in_debug()
 
-    # ---- torch.compile: the operators of operators.py (python/cuju/_batch/environment.py:983-1056) ----
-    def _operator_key(self) -> int:
-        return self._operator
+    # ---- torch.compile: the operator of operators.py (python/cuju/_batch/environment.py:983-1056) ----
+    def _operator_outputs(self):
+        """Every tensor a step writes, with the library location each one views."""
+        tensors, locations = [], []
+        for name, tensor in (('observation', self._observation), ('reward', self._reward), ('done', self._done),
+                             ('final', self._final), ('score_reward', self._score_reward)):
+            if isinstance(tensor, dict):
+                buffer = 'final_raw' if name == 'final' else 'raw'
+                for field, _dtype, _shape, offset in self._raw_fields:
+                    tensors.append(tensor[field])
+                    locations.append(f'{buffer}@{offset}')
+            else:
+                tensors.append(tensor)
+                locations.append(self._buffer_names[name])
+        return tensors, locations
 
-    def _operator_outputs(self) -> list:
-        """Every tensor a step writes, which the operators declare as mutated."""
-        outputs = []
-        for tensor in (self._observation, self._reward, self._done, self._final, self._score_reward):
-            outputs.extend(tensor.values() if isinstance(tensor, dict) else (tensor,))
-        return outputs
-
-    def _copy_operator_outputs(self, outputs) -> None:
-        # The compiler may hand copies of the buffers; each takes the step's values.
-        for given, own in zip(outputs, self._operator_outputs()):
-            if given.data_ptr() != own.data_ptr():
-                given.copy_(own)
-
-    def _operator_step(self, actions, outputs) -> None:
-        with torch.cuda.device(self._torch_device):
-            if self._check_actions and bool(((actions < -self.action_count) | (actions >= self.action_count)).any()):
-                raise ActionRangeError(f'expected action indices from {-self.action_count} to {self.action_count - 1}')
-            self._check(self._lib.cuju_environment_step(self._handle(), actions.data_ptr(), 1, self._stream(), 0))
-        self._copy_operator_outputs(outputs)
-
-    def _operator_reset_done(self, outputs) -> None:
-        with torch.cuda.device(self._torch_device):
-            self._check(self._lib.cuju_environment_reset_done(self._handle(), self._stream()))
-        self._copy_operator_outputs(outputs)
+    def _operator_call(self, reset_done: bool, actions: torch.Tensor) -> None:
+        tensors, locations = self._operator_outputs()
+        what = _operators.packed(reset_done, self.debug, self._check_actions, self.action_count)
+        torch.ops.cuju_amd.advance(self._handle(), what, actions, locations, tensors)
 
     def _compiled_step(self, actions: torch.Tensor, shape):
         actions = actions.to(self._torch_device, torch.int32).reshape(shape).contiguous()
-        torch.ops.cuju_amd.step(self._operator_key(), actions, self._operator_outputs())
+        self._operator_call(False, actions)
         observation, reward, done, final = self._outputs()
         return observation, reward, done, {'final_observation': final, 'score_reward': self._score_reward}
 

@@ -128,3 +128,17 @@ def load(path: str | None = None):
             function.argtypes = arguments
         _loaded[path] = lib
     return _loaded[path]
+
+
+class DeviceArray:
+    """A device buffer of the library that `torch.as_tensor` views without a copy, through
+    `__cuda_array_interface__`; `owner` stays alive as long as any view does."""
+
+    TYPES = {'float32': '<f4', 'int32': '<i4', 'uint8': '|u1', 'bool': '|b1'}
+
+    def __init__(self, pointer, shape, dtype, owner):
+        self.owner = owner
+        self.__cuda_array_interface__ = {'data': (pointer, False), 'shape': tuple(shape),
+                                         'typestr': self.TYPES[str(dtype).replace('torch.', '')], 'version': 2,
+                                         'strides': None}
+

@@ -1,53 +1,98 @@
-"""The `torch.library` operators through which `torch.compile` traces a step without a graph break
-(python/cuju/_batch/operators.py).
+"""`torch.compile` support: the operator `cuju_amd::advance`, through which a compiled program steps
+a batch, or restarts its ended environments, without a graph break (the reference's compiled-step
+surface is python/cuju/_batch/environment.py:983-1056).
 
-`cuju_amd::step` and `cuju_amd::reset_done` find their batch by an integer key and declare the
-batch's output tensors as mutated arguments, so the compiler orders every read of an output after
-the call and never drops it. Each runs the library call the eager method runs.
+The operator carries no Python object. A batch is named by its native handle, the library's
+pointer as an integer, and each output tensor by the library buffer it views: a location string,
+`name` for a whole buffer (`simple115`, `reward`, ...) or `name@offset` for a raw array inside the
+`raw` buffers. A call runs the library on the current stream. Functionalization hands the operator
+stand-ins for its mutated arguments rather than the batch's own tensors, so after the call every
+stand-in gets the bytes of the library buffer it names. The outputs are declared mutated, so the
+compiler orders each later read of them after the call and never drops the call. Handles are
+checked against the open batches: a compiled program that outlives its batch raises instead of
+reaching freed memory.
+
+`what` packs the call: bit 0 selects a reset of the ended environments over a step, bit 1 waits
+for the device after the call (debug batches), bit 2 checks the action range first, and bits 8 and
+up hold the action count that check uses.
 """
 
 from __future__ import annotations
 
-import itertools
-import weakref
+import ctypes
 
 import torch
 
-_BATCHES: weakref.WeakValueDictionary = weakref.WeakValueDictionary()
-_KEYS = itertools.count(1)
+from .errors import ActionRangeError, ClosedError, from_library
+from .library import DeviceArray
+
+RESET_DONE = 1
+SYNCHRONIZE = 2
+CHECK_ACTIONS = 4
+
+# The open batches: native handle -> the loaded library that made it.
+_OPEN: dict[int, ctypes.CDLL] = {}
 
 
-def register(batch) -> int:
-    """A new key under which the operators find `batch`; a dead batch drops out."""
-    key = next(_KEYS)
-    _BATCHES[key] = batch
-    return key
+def opened(handle: int, lib) -> None:
+    _OPEN[handle] = lib
 
 
-def _batch(key: int):
-    batch = _BATCHES.get(key)
-    if batch is None:
-        raise RuntimeError('the batch of this compiled step is gone')
-    return batch
+def closed(handle: int) -> None:
+    _OPEN.pop(handle, None)
 
 
-@torch.library.custom_op('cuju_amd::step', mutates_args=('outputs',))
-def step(batch: int, actions: torch.Tensor, outputs: list[torch.Tensor]) -> None:
-    """Steps the batch of key `batch` with device `actions` and writes its outputs into `outputs`."""
-    _batch(batch)._operator_step(actions, outputs)
+def packed(reset_done: bool, synchronize: bool, check_actions: bool, action_count: int) -> int:
+    return ((RESET_DONE if reset_done else 0) | (SYNCHRONIZE if synchronize else 0) |
+            (CHECK_ACTIONS if check_actions else 0) | (action_count << 8))
 
 
-@step.register_fake
-def _step_fake(batch, actions, outputs):
-    return None
+_NAMESPACE = torch.library.Library('cuju_amd', 'DEF')
+_NAMESPACE.define('advance(int handle, int what, Tensor actions, str[] locations, Tensor(a!)[] outputs) -> ()')
 
 
-@torch.library.custom_op('cuju_amd::reset_done', mutates_args=('outputs',))
-def reset_done(batch: int, outputs: list[torch.Tensor]) -> None:
-    """Resets the ended environments of the batch of key `batch` and writes `outputs`."""
-    _batch(batch)._operator_reset_done(outputs)
+def _check(lib, status):
+    if status == -2:
+        raise ActionRangeError(lib.cuju_last_error().decode())
+    if status != 0:
+        raise from_library(lib.cuju_last_error().decode())
 
 
-@reset_done.register_fake
-def _reset_done_fake(batch, outputs):
+def _library_tensor(lib, handle, location, like):
+    """The library buffer at `location`, viewed with the shape and type of `like`."""
+    name, _, offset = location.partition('@')
+    pointer = lib.cuju_environment_buffer(handle, name.encode())
+    if not pointer:
+        raise from_library(lib.cuju_last_error().decode())
+    return torch.as_tensor(DeviceArray(pointer + int(offset or 0), like.shape, like.dtype, None), device=like.device)
+
+
+def _advance(handle, what, actions, locations, outputs):
+    lib = _OPEN.get(handle)
+    if lib is None:
+        raise ClosedError('the batch of this compiled call is closed')
+    device = outputs[0].device
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        if what & RESET_DONE:
+            status = lib.cuju_environment_reset_done(handle, stream)
+        else:
+            count = what >> 8
+            if what & CHECK_ACTIONS and bool(((actions < -count) | (actions >= count)).any()):
+                raise ActionRangeError(f'expected action indices from {-count} to {count - 1}')
+            status = lib.cuju_environment_step(handle, actions.data_ptr(), 1, stream, 0)
+        _check(lib, status)
+        if what & SYNCHRONIZE:
+            _check(lib, lib.cuju_environment_synchronize(handle, stream))
+    for location, given in zip(locations, outputs):
+        own = _library_tensor(lib, handle, location, given)
+        if given.data_ptr() != own.data_ptr():
+            given.copy_(own)
+
+
+_NAMESPACE.impl('advance', _advance, 'CUDA')
+
+
+@torch.library.register_fake('cuju_amd::advance')
+def _advance_fake(handle, what, actions, locations, outputs):
     return None

@@ -1,5 +1,17 @@
-"""Stacked states on the MI355X: GRF's `FrameStack` pickled beside the state and loaded back
-(tests/test_stacked_state.py of the reference, python/cuju/_batch/frame_stack.py)."""
+"""Stacked states on the MI355X. A stacked batch's state pickles GRF's `FrameStack` (a deque of the
+last four observations, oldest first) beside the episode logic and the engine bytes; loading it
+restores the stack (the reference's surface: python/cuju/_batch/environment.py:1487-1620,
+python/cuju/_batch/frame_stack.py). The checks here:
+
+* a state carried from one batch into an environment of another batch, with another seed, makes
+  that environment continue frame for frame as the original does, for one agent, several agents
+  and the SMM;
+* the pickle holds GRF's deque, with one agent's frames lacking the agent axis, and its frames
+  concatenate to the observation;
+* four foreign frames become the stack, and the next step shifts them by one frame;
+* malformed stacks and mismatched `stacked` options are refused.
+(The continuation against the reference library is in test_gpu_surface.py.)
+"""
 
 import collections
 import pickle
@@ -11,151 +23,154 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import PRODUCT, digest_actions
+from conftest import PRODUCT
+from cuju_amd import workloads
 
 pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture
-def grf_classes(monkeypatch):
-    """A stand-in for GRF's `EnvState`, so that `pickle` reads and writes whole states."""
-    names = ('gfootball', 'gfootball.env', 'gfootball.env.football_env_core')
-    modules = {name: types.ModuleType(name) for name in names}
-
-    class EnvState:
-        pass
-
-    EnvState.__module__, EnvState.__qualname__ = names[-1], 'EnvState'
-    modules[names[-1]].EnvState = EnvState
-    for name, module in modules.items():
+def grf_env_state(monkeypatch):
+    """A module tree standing in for GRF's, so that `pickle` can load and dump whole states."""
+    path = ('gfootball', 'gfootball.env', 'gfootball.env.football_env_core')
+    state_class = type('EnvState', (), {'__module__': path[-1], '__qualname__': 'EnvState'})
+    for name in path:
+        module = types.ModuleType(name)
+        if name == path[-1]:
+            module.EnvState = state_class
         monkeypatch.setitem(sys.modules, name, module)
-    return EnvState
+    return state_class
 
 
-def batch_of(assets, **options):
+def make(assets, **options):
     import cuju_amd
     return cuju_amd.BatchEnvironment(assets, library=PRODUCT, device='cuda:0', **options)
 
 
-def split(state):
+def parts(state):
+    """(unpickled episode logic, engine bytes) of `get_state` bytes."""
     (length,) = struct.unpack_from('<i', state)
     return pickle.loads(state[4:4 + length]), state[4 + length:]
 
 
-def join(unpickled, match):
+def assemble(unpickled, engine):
     data = pickle.dumps(unpickled, protocol=2)
-    return struct.pack('<i', len(data)) + data + match
+    return struct.pack('<i', len(data)) + data + engine
 
 
-def host_bytes(x):
+def as_bytes(x):
     return x.detach().cpu().numpy().tobytes()
 
 
-def steps(batch, start, count):
-    """Steps every environment with the same actions and returns the observations."""
-    seen = []
-    for step in range(start, start + count):
-        actions = np.repeat(digest_actions(step, 1, batch.agents, batch.action_count), batch.environment_count, axis=0)
-        observation, _, _, _ = batch.step(torch.as_tensor(actions, device='cuda:0'))
-        seen.append(observation.clone())
-    return seen
+def advance(batch, seed, first, count):
+    for step in range(first, first + count):
+        batch.step(torch.as_tensor(workloads.actions(seed, step, 0, batch.environment_count, batch.agents),
+                                   device='cuda:0'))
 
 
-@pytest.mark.parametrize('assets,representation', [('5_vs_5_l1_r0', 'simple115v2'), ('5_vs_5_l2_r1', 'simple115v2'),
+@pytest.mark.parametrize('assets,representation', [('5_vs_5_l1_r0', 'simple115v2'), ('5_vs_5_l2_r1', 'simple115'),
                                                    ('5_vs_5_l2_r0', 'extracted')])
-def test_a_stacked_state_continues_the_stack(assets, representation):
-    batch = batch_of(assets, environment_count=2, representation=representation, stacked=True)
+def test_a_carried_state_continues_frame_for_frame(assets, representation):
+    options = dict(environment_count=3, representation=representation, stacked=True)
+    source, target = make(assets, seed=31, **options), make(assets, seed=32, **options)
     try:
-        batch.reset()
-        steps(batch, 0, 25)
-        batch.set_state(1, batch.get_state(0, stacked=True), stacked=True)
-        assert host_bytes(batch.observation()[0]) == host_bytes(batch.observation()[1])
-        for observation in steps(batch, 25, 20):
-            assert host_bytes(observation[0]) == host_bytes(observation[1])
+        source.reset()
+        target.reset()
+        advance(source, 31, 0, 21)
+        advance(target, 32, 0, 9)
+        # Environment 1 of the source goes into environment 2 of the target.
+        target.set_state(2, source.get_state(1, stacked=True), stacked=True)
+        assert as_bytes(target.observation()[2]) == as_bytes(source.observation()[1])
+        for step in range(15):
+            actions = workloads.actions(40, step, 0, 3, source.agents)
+            moved = actions.copy()
+            moved[2] = actions[1]
+            a = source.step(torch.as_tensor(actions, device='cuda:0'))[0]
+            b = target.step(torch.as_tensor(moved, device='cuda:0'))[0]
+            assert as_bytes(b[2]) == as_bytes(a[1]), f'step {step} after the load'
     finally:
-        batch.close()
+        source.close()
+        target.close()
 
 
-def test_the_pickle_holds_grf_frame_stack(grf_classes):
-    batch = batch_of('5_vs_5_l2_r1', environment_count=1, stacked=True)
+@pytest.mark.parametrize('assets,representation,frame_shape', [('5_vs_5_l2_r1', 'simple115v2', (3, 115)),
+                                                               ('5_vs_5_l1_r0', 'simple115v2', (115,)),
+                                                               ('5_vs_5_l1_r0', 'extracted', (72, 96, 4))])
+def test_the_pickle_holds_grf_frame_stack(assets, representation, frame_shape, grf_env_state):
+    batch = make(assets, environment_count=1, stacked=True, representation=representation)
     try:
         batch.reset()
-        steps(batch, 0, 6)
-        unpickled, _ = split(batch.get_state(0, stacked=True))
+        advance(batch, 3, 0, 6)
+        unpickled, _ = parts(batch.get_state(0, stacked=True))
         frames = unpickled['FrameStack']
         assert isinstance(frames, collections.deque) and frames.maxlen == 4 and len(frames) == 4
-        assert all(frame.dtype == np.float32 and frame.shape == (3, 115) for frame in frames)
-        assert np.concatenate(list(frames), axis=-1).tobytes() == host_bytes(batch.observation()[0])
-        assert isinstance(unpickled['FootballEnvCore'], grf_classes)
+        assert {frame.shape for frame in frames} == {frame_shape}
+        assert np.concatenate(list(frames), axis=-1).tobytes() == as_bytes(batch.observation()[0])
+        assert isinstance(unpickled['FootballEnvCore'], grf_env_state)
     finally:
         batch.close()
 
 
-def test_one_agent_frames_drop_the_agent_axis(grf_classes):
-    batch = batch_of('5_vs_5_l1_r0', environment_count=1, stacked=True)
+def test_foreign_frames_become_the_stack_and_shift(grf_env_state):
+    batch = make('5_vs_5_l1_r0', environment_count=1, stacked=True)
     try:
         batch.reset()
-        unpickled, _ = split(batch.get_state(0, stacked=True))
-        assert [frame.shape for frame in unpickled['FrameStack']] == [(115,)] * 4
+        advance(batch, 5, 0, 4)
+        unpickled, engine = parts(batch.get_state(0, stacked=True))
+        frames = [np.full(115, k, dtype=np.float32) + np.arange(115, dtype=np.float32) / 1000 for k in range(4)]
+        unpickled['FrameStack'] = collections.deque(frames, maxlen=4)
+        batch.set_state(0, assemble(unpickled, engine), stacked=True)
+        assert as_bytes(batch.observation()[0]) == np.concatenate(frames).tobytes()
+        observation = batch.step(torch.zeros((1, 1), dtype=torch.int32, device='cuda:0'))[0]
+        # The oldest frame leaves; the other three move down one place.
+        assert observation[0, 0, :345].cpu().numpy().tobytes() == np.concatenate(frames[1:]).tobytes()
     finally:
         batch.close()
 
 
-def test_a_stack_from_elsewhere_sets_the_observation(grf_classes):
-    batch = batch_of('5_vs_5_l1_r0', environment_count=1, stacked=True)
+def test_malformed_stacks_are_refused(grf_env_state):
+    batch = make('5_vs_5_l1_r0', environment_count=1, stacked=True, representation='extracted')
     try:
         batch.reset()
-        steps(batch, 0, 3)
-        unpickled, match = split(batch.get_state(0, stacked=True))
-        frame = np.arange(115, dtype=np.float32)
-        unpickled['FrameStack'] = collections.deque([frame] * 4, maxlen=4)
-        batch.set_state(0, join(unpickled, match), stacked=True)
-        assert host_bytes(batch.observation()[0]) == np.tile(frame, 4).tobytes()
-    finally:
-        batch.close()
-
-
-def test_malformed_stacks(grf_classes):
-    batch = batch_of('5_vs_5_l1_r0', environment_count=1, stacked=True, representation='extracted')
-    try:
-        batch.reset()
-        unpickled, match = split(batch.get_state(0, stacked=True))
+        unpickled, engine = parts(batch.get_state(0, stacked=True))
         frames = list(unpickled['FrameStack'])
-        unpickled['FrameStack'] = collections.deque(frames[:3], maxlen=4)
-        with pytest.raises(ValueError, match='frames'):
-            batch.set_state(0, join(unpickled, match), stacked=True)
-        unpickled['FrameStack'] = collections.deque([frame[:, :10] for frame in frames], maxlen=4)
-        with pytest.raises(ValueError, match='shape'):
-            batch.set_state(0, join(unpickled, match), stacked=True)
-        # GRF's minimap marks a cell with 255 and leaves the others 0.
-        marked = [frame.copy() for frame in frames]
-        marked[0][0, 0, 0] = 7
-        unpickled['FrameStack'] = collections.deque(marked, maxlen=4)
-        with pytest.raises(RuntimeError, match='minimap'):
-            batch.set_state(0, join(unpickled, match), stacked=True)
-        del unpickled['FrameStack']
-        with pytest.raises(ValueError, match='FrameStack'):
-            batch.set_state(0, join(unpickled, match), stacked=True)
+
+        def marked(frame_list):
+            frame_list = [f.copy() for f in frame_list]
+            frame_list[0][0, 0, 0] = 7  # GRF's minimap holds 0 or 255 only
+            return frame_list
+
+        cases = [
+            (collections.deque(frames[:3], maxlen=4), ValueError, 'frames'),
+            (collections.deque([f[:, :10] for f in frames], maxlen=4), ValueError, 'shape'),
+            (collections.deque(marked(frames), maxlen=4), RuntimeError, 'minimap'),
+            (None, ValueError, 'FrameStack'),
+        ]
+        for stack, error, message in cases:
+            variant = dict(unpickled)
+            if stack is None:
+                del variant['FrameStack']
+            else:
+                variant['FrameStack'] = stack
+            with pytest.raises(error, match=message):
+                batch.set_state(0, assemble(variant, engine), stacked=True)
     finally:
         batch.close()
 
 
-def test_the_stack_option_must_match():
-    stacked = batch_of('5_vs_5_l1_r0', environment_count=1, stacked=True)
-    plain = batch_of('5_vs_5_l1_r0', environment_count=1)
+def test_the_stacked_option_must_match_the_batch():
+    stacked = make('5_vs_5_l1_r0', environment_count=1, stacked=True)
+    plain = make('5_vs_5_l1_r0', environment_count=1)
     try:
         stacked.reset()
         plain.reset()
-        with pytest.raises(ValueError, match='stacked=True'):
-            stacked.get_state(0)
-        with pytest.raises(ValueError, match='stacked=True'):
-            plain.get_state(0, stacked=True)
-        with pytest.raises(ValueError, match='stacked=True'):
-            stacked.set_state(0, plain.get_state(0))
-        # The pickle without a stack keeps its bytes, as the digests read them.
-        state = plain.get_state(0)
-        (length,) = struct.unpack_from('<i', state)
-        assert b'FrameStack' not in state[4:4 + length]
+        for call in (lambda: stacked.get_state(0), lambda: plain.get_state(0, stacked=True),
+                     lambda: stacked.set_state(0, plain.get_state(0))):
+            with pytest.raises(ValueError, match='stacked=True'):
+                call()
+        # An unstacked state's pickle holds no frame stack: its bytes are what the digests hash.
+        (length,) = struct.unpack_from('<i', plain.get_state(0))
+        assert b'FrameStack' not in plain.get_state(0)[4:4 + length]
     finally:
         stacked.close()
         plain.close()

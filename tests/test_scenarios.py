@@ -102,7 +102,7 @@ def test_scenario_files_build_as_the_reference(name, reference_library, tmp_path
     out = scenarios.build_bundle(source, str(tmp_path / 'mine.cjb'))
     even, odd = scenarios.describe(source)
     keep = []
-    pair = [scenarios._as_struct(even, keep), scenarios._as_struct(odd, keep)]
+    pair = [scenarios.c_description(even, keep), scenarios.c_description(odd, keep)]
     status, theirs = build_with(reference_library, pair, name, tmp_path / 'theirs.cjb')
     assert status == 0, theirs
     with open(out, 'rb') as f:
@@ -112,19 +112,19 @@ def test_scenario_files_build_as_the_reference(name, reference_library, tmp_path
 def test_describe_follows_the_builder_semantics():
     from cuju_amd import scenarios
     even, odd = scenarios.describe(os.path.join(SCENARIOS, 'drill_3_vs_1_with_keeper.py'))
-    assert even['ball'] == (0.55, 0.12) and odd['ball'] == (0.55, -0.12)
-    assert [p[2] for p in even['left']] == [0, 9, 6, 7]
+    assert even.ball == (0.55, 0.12) and odd.ball == (0.55, -0.12)
+    assert [p.role for p in even.left] == [0, 9, 6, 7]
     # Not deterministic: every episode's seed replaces the scenario's.
-    assert even['values']['game_engine_random_seed'] == 42
+    assert even.values['game_engine_random_seed'] == 42
     duel, _ = scenarios.describe(os.path.join(SCENARIOS, 'keeper_duel_deterministic.py'))
-    assert duel['values']['game_engine_random_seed'] == 1234
-    assert duel['left'][0][4] is False and duel['right'][1][3] is True
+    assert duel.values['game_engine_random_seed'] == 1234
+    assert duel.left[0].controllable is False and duel.right[1].lazy is True
 
     def empty_right(builder):
         builder.AddPlayer(-1.0, 0.0, scenarios.PlayerRole.e_PlayerRole_GK)
     # GRF gives an empty team a lazy goalkeeper.
     even, _ = scenarios.describe(empty_right)
-    assert even['right'] == [(-1.0, 0.42, 0, True, True)]
+    assert even.right == ((-1.0, 0.42, 0, True, True),)
 
 
 def _refused(build, match):

@@ -42,6 +42,16 @@ HIP_FLAGS = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math'
              '-mllvm', '-unroll-runtime', '-mllvm', '-amdgpu-sched-strategy=max-ilp']
 
 
+# The device code is built once per group width (lanes per environment); the first build also
+# holds the geometry choice, the static scratch and the math check kernel.
+GROUP_WIDTHS = (4, 8, 16)
+
+
+def _variant_flags(lanes):
+    return [f'-DENG_GROUP_LANES={lanes}', f'-DENG_DEVICE_FACTORY=MakeHipDevice{lanes}',
+            f'-DENG_PRIMARY_VARIANT={1 if lanes == GROUP_WIDTHS[0] else 0}']
+
+
 def _run(command):
     result = subprocess.run(command, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if result.returncode != 0:
@@ -60,8 +70,9 @@ def build(host=True, product=True, jobs=8):
     if product:
         for s in HOST_SOURCES:
             tasks.append([CXX, *COMMON, '-c', os.path.join(SOURCE, s), '-o', _object(s, 'p')])
-        tasks.append([HIPCC, *HIP_FLAGS, '-c', os.path.join(SOURCE, 'hip_device.hip'),
-                      '-o', _object('hip_device.hip', 'p')])
+        for lanes in GROUP_WIDTHS:
+            tasks.append([HIPCC, *HIP_FLAGS, *_variant_flags(lanes), '-c', os.path.join(SOURCE, 'hip_device.hip'),
+                          '-o', _object(f'hip_device_{lanes}.hip', 'p')])
     if host:
         for s in HOST_SOURCES + ['host/host_library.cpp']:
             tasks.append([CXX, *COMMON, '-c', os.path.join(SOURCE, s), '-o', _object(s, 'h')])
@@ -70,7 +81,7 @@ def build(host=True, product=True, jobs=8):
             f.result()
     built = []
     if product:
-        objects = [_object(s, 'p') for s in HOST_SOURCES] + [_object('hip_device.hip', 'p')]
+        objects = [_object(s, 'p') for s in HOST_SOURCES] + [_object(f'hip_device_{lanes}.hip', 'p') for lanes in GROUP_WIDTHS]
         _run([HIPCC, f'--offload-arch={ARCH}', '-shared', '-fPIC', '-o', PRODUCT, *objects])
         built.append(PRODUCT)
     if host:

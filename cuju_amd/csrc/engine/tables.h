@@ -318,7 +318,7 @@ struct TimeWalk {
     float usualSquared[kTimeWalkSteps], optimisticSquared[kTimeWalkSteps];
 };
 // Lanes of one match with a plan of their own in the candidate search.
-constexpr int kPlanLanes = 8;
+constexpr int kPlanLanes = 16;
 static_assert(kGroupLanes <= kPlanLanes, "every lane of a match needs a candidate plan");
 // Per-match working memory for the animation selection: candidate lists, planned positions, sort
 // keys and one candidate plan per lane of the match. One block per environment in HBM, which every

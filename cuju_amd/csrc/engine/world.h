@@ -16,7 +16,8 @@ namespace eng {
 // state no match reaches (list overflow, a team without players).
 #if defined(__HIPCC__)
 // 1 = a path GRF leaves undefined, 2 = a state no match reaches; the batch reads it after a launch.
-extern __device__ uint32_t gEngineFault;
+// Each device build (one per group width) holds its own.
+static __device__ uint32_t gEngineFault;
 #endif
 #if !ENG_DEVICE
 const char *&FailReason();

@@ -1,11 +1,19 @@
 // The MI355X device of the batch runtime: device memory, copies and the kernels (reset, step and
-// the outputs of one environment). Each environment runs on a group of kGroupLanes adjacent lanes
-// (engine/hd.h), and a workgroup (one wavefront) holds `matches_` environments. A match is a long
-// chain of dependent loads with data-dependent branches: one match per wavefront leaves the latency
-// of each load exposed, while many matches per wavefront serialize on divergence. With one lane
-// per match, 16 per wavefront measured best on gfx950 for the 11-a-side scenarios (1: 9.1k,
-// 4: 16.9k, 16: 33.5k, 64: 22.9k env-steps/s at 16,384 environments, early steps); groups of four
-// lanes fill the wavefront with the same 16 matches.
+// the outputs of one environment).
+//
+// Geometry. Each environment runs on a group of ENG_GROUP_LANES adjacent lanes (engine/hd.h), and a
+// workgroup of one wavefront holds `matches_` environments. A step's cost is the wavefront's: its
+// matches' divergent control flow runs one path after another (16 identical matches step in a
+// quarter of the time of 16 ordinary ones), and a match's own sequential chain of dependent loads
+// sets a floor that wider groups lower, since the loops of independent iterations split over the
+// group. This file is compiled once per group width (4, 8 and 16 lanes), each copy with its own
+// kernels, fault words and device class; MakeLibraryDevice (the copy built with
+// ENG_PRIMARY_VARIANT) picks one per batch: as many matches per wavefront as fill every SIMD with
+// one wavefront, at most 16, and the widest group those matches leave room for. Measured on gfx950
+// (ms per step after 100 steps): 64 environments of 5-a-side 80.4 at 4 lanes x 16 matches, 18.3 at
+// 16 lanes x 1; 4,096 of 11-a-side 219.6 at 4 x 16, 124.1 at 16 x 4; 8,192 of 11-a-side self-play
+// 236.8 at 4 x 16, 176.0 at 8 x 8; 16,384 of 11-a-side 280 at 4 x 16, 352 at 4 x 8 (two wavefronts
+// per SIMD), 356 at 4 x 12.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -17,8 +25,17 @@
 
 #include "host/runtime.h"
 
+#ifndef ENG_DEVICE_FACTORY
+#error "each build of the device names its factory (ENG_DEVICE_FACTORY)"
+#endif
+
 namespace eng {
-__device__ uint32_t gEngineFault;
+namespace host {
+std::unique_ptr<Device> ENG_DEVICE_FACTORY(int matches);
+// The static scratch array of the step that allocates nothing, on the current device (defined by
+// the primary build, which owns the array).
+Scratch *StaticScratchOfCurrentDevice(int *environments);
+}  // namespace host
 }  // namespace eng
 
 namespace {
@@ -67,69 +84,20 @@ __global__ void __launch_bounds__(kDeviceGroupLanes) OutputKernel(eng::Batch b, 
     eng::WriteEnvironmentOutputs(b, env, false);
 }
 
-// The math routines over an index range, for the checks of tests: consecutive float bit patterns
-// from `first` (kind 0), float arrays (kind 1) or double arrays (kind 2). Every lane reads the
-// tables from its workgroup's LDS, as the step does.
-constexpr int kLibmThreads = 256;
-__global__ void __launch_bounds__(kLibmThreads) LibmKernel(int kind, int which, uint32_t first, long long count, const void *x,
-                                                            const void *y, void *out) {
-    eng::libm::StageMathTables();
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
-        if (kind == 0) {
-            static_cast<float *>(out)[i] = eng::libm::EvaluateFloat(which, eng::FloatOf(first + (uint32_t)i), 0.0f);
-        } else if (kind == 1) {
-            static_cast<float *>(out)[i] =
-                eng::libm::EvaluateFloat(which, static_cast<const float *>(x)[i], static_cast<const float *>(y)[i]);
-        } else {
-            static_cast<double *>(out)[i] =
-                eng::libm::EvaluateDouble(which, static_cast<const double *>(x)[i], static_cast<const double *>(y)[i]);
-        }
-    }
-}
-
 void Check(hipError_t e, const char *what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// The working memory of the step that allocates nothing (cuju_environment_step_no_alloc): the
-// per-environment Scratch blocks of at most kStaticScratchEnvironments environments, 4.3 MB, one
-// copy on each GPU for the life of the process. Every such call on a GPU shares it: calls that
-// overlap on one GPU race. Nothing in it needs to start at zero, since the step builds every
-// list, plan, key array and time walk before reading it.
-constexpr int kStaticScratchEnvironments = 64;
-static __device__ __align__(256) unsigned char scratch[kStaticScratchEnvironments * sizeof(eng::Scratch)];
-
-// The device address of `scratch` on each GPU. In host code the array's name stands in for the
-// symbol only; its address on a device comes from hipGetSymbolAddress with that device current.
-std::mutex gScratchMutex;
-std::vector<void *> gScratchAddress;
-
-void *StaticScratchOfCurrentDevice() {
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lock(gScratchMutex);
-    if ((int)gScratchAddress.size() <= device) gScratchAddress.resize(device + 1, nullptr);
-    if (!gScratchAddress[device]) {
-        void *p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
-        gScratchAddress[device] = p;
-    }
-    return gScratchAddress[device];
-}
-
 class HipDevice : public eng::host::Device {
 public:
-    HipDevice() {
-        // Environments per workgroup, 1 to 64 / kGroupLanes.
-        if (const char *v = getenv("CUJU_AMD_MATCHES")) matches_ = std::max(1, std::min(kMaxMatches, atoi(v)));
+    explicit HipDevice(int matches) : matches_(std::max(1, std::min(kMaxMatches, matches))) {
         int n = 0;
         Check(hipGetDeviceCount(&n), "hipGetDeviceCount");
         if (n < 1) throw std::runtime_error("no HIP device");
         ClearFault();
         // The batch is created with its device current: look the static scratch up now, so the
         // step that allocates nothing makes no runtime call besides its launch.
-        staticScratch_ = static_cast<eng::Scratch *>(StaticScratchOfCurrentDevice());
+        staticScratch_ = eng::host::StaticScratchOfCurrentDevice(&staticScratchEnvironments_);
     }
     const char *Name() const override { return "hip"; }
     bool HostMemory() const override { return false; }
@@ -166,7 +134,7 @@ public:
         Check(hipGetLastError(), "output launch");
     }
     eng::Scratch *StaticScratch(int *environments) override {
-        *environments = staticScratch_ ? kStaticScratchEnvironments : 0;
+        *environments = staticScratch_ ? staticScratchEnvironments_ : 0;
         return staticScratch_;
     }
     void CheckFault() override {
@@ -178,10 +146,15 @@ public:
         ClearFault();
         throw std::runtime_error("environment " + std::to_string(env) + (fault == 2 ? " reached a state that no match reaches" : " reached a path that GRF leaves undefined"));
     }
+    int Geometry(int *lanes) const override {
+        *lanes = kDeviceGroupLanes;
+        return matches_;
+    }
 
 private:
-    int matches_ = kMaxMatches < 16 ? kMaxMatches : 16;
+    int matches_;
     eng::Scratch *staticScratch_ = nullptr;
+    int staticScratchEnvironments_ = 0;
     void ClearFault() {
         const uint32_t zero = 0;
         const int32_t none = 0x7fffffff;
@@ -191,6 +164,96 @@ private:
 };
 
 }  // namespace
+
+namespace eng {
+namespace host {
+std::unique_ptr<Device> ENG_DEVICE_FACTORY(int matches) { return std::make_unique<HipDevice>(matches); }
+}  // namespace host
+}  // namespace eng
+
+#if ENG_PRIMARY_VARIANT
+namespace {
+
+// The math routines over an index range, for the checks of tests: consecutive float bit patterns
+// from `first` (kind 0), float arrays (kind 1) or double arrays (kind 2). Every lane reads the
+// tables from its workgroup's LDS, as the step does.
+constexpr int kLibmThreads = 256;
+__global__ void __launch_bounds__(kLibmThreads) LibmKernel(int kind, int which, uint32_t first, long long count, const void *x,
+                                                            const void *y, void *out) {
+    eng::libm::StageMathTables();
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+        if (kind == 0) {
+            static_cast<float *>(out)[i] = eng::libm::EvaluateFloat(which, eng::FloatOf(first + (uint32_t)i), 0.0f);
+        } else if (kind == 1) {
+            static_cast<float *>(out)[i] =
+                eng::libm::EvaluateFloat(which, static_cast<const float *>(x)[i], static_cast<const float *>(y)[i]);
+        } else {
+            static_cast<double *>(out)[i] =
+                eng::libm::EvaluateDouble(which, static_cast<const double *>(x)[i], static_cast<const double *>(y)[i]);
+        }
+    }
+}
+
+// The working memory of the step that allocates nothing (cuju_environment_step_no_alloc): the
+// per-environment Scratch blocks of at most kStaticScratchEnvironments environments, one copy on
+// each GPU for the life of the process. Every such call on a GPU shares it: calls that overlap on
+// one GPU race. Nothing in it needs to start at zero, since the step builds every list, plan, key
+// array and time walk before reading it.
+constexpr int kStaticScratchEnvironments = 64;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchEnvironments * sizeof(eng::Scratch)];
+
+// The device address of `scratch` on each GPU. In host code the array's name stands in for the
+// symbol only; its address on a device comes from hipGetSymbolAddress with that device current.
+std::mutex gScratchMutex;
+std::vector<void *> gScratchAddress;
+
+}  // namespace
+
+namespace eng {
+namespace host {
+
+Scratch *StaticScratchOfCurrentDevice(int *environments) {
+    *environments = 0;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(gScratchMutex);
+    if ((int)gScratchAddress.size() <= device) gScratchAddress.resize(device + 1, nullptr);
+    if (!gScratchAddress[device]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        gScratchAddress[device] = p;
+    }
+    *environments = kStaticScratchEnvironments;
+    return static_cast<Scratch *>(gScratchAddress[device]);
+}
+
+std::unique_ptr<Device> MakeHipDevice4(int matches);
+std::unique_ptr<Device> MakeHipDevice8(int matches);
+std::unique_ptr<Device> MakeHipDevice16(int matches);
+
+// One wavefront for each SIMD where the batch allows it: the matches of a wavefront are the
+// environments over the SIMDs, 1 to 16, and the group is the widest of 16, 8 or 4 lanes that
+// those matches leave room for in 64. CUJU_AMD_MATCHES sets the matches of a wavefront instead.
+std::unique_ptr<Device> MakeLibraryDevice(int, int environments) {
+    int device = 0, units = 0;
+    Check(hipGetDevice(&device), "hipGetDevice");
+    Check(hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
+    const int simds = std::max(1, 4 * units);
+    int matches = (std::max(1, environments) + simds - 1) / simds;
+    if (const char *v = getenv("CUJU_AMD_MATCHES")) matches = atoi(v);
+    matches = std::max(1, std::min(16, matches));
+    if (matches <= 4) return MakeHipDevice16(matches);
+    if (matches <= 8) return MakeHipDevice8(matches);
+    return MakeHipDevice4(matches);
+}
+
+// torch names a HIP device "cuda" on ROCm; the reference binding compares this name with the
+// device type it was asked for (python/cuju/_batch/library.py:217-222).
+extern const char *const kBackendName = "cuda";
+
+}  // namespace host
+}  // namespace eng
 
 extern "C" __attribute__((visibility("default"))) int cuju_debug_libm_device(int kind, int which, unsigned int first,
                                                                             long long count, const void *x, const void *y,
@@ -203,12 +266,4 @@ extern "C" __attribute__((visibility("default"))) int cuju_debug_libm_device(int
                        first, count, x, y, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
-
-namespace eng {
-namespace host {
-std::unique_ptr<Device> MakeLibraryDevice(int) { return std::make_unique<HipDevice>(); }
-// torch names a HIP device "cuda" on ROCm; the reference binding compares this name with the
-// device type it was asked for (python/cuju/_batch/library.py:217-222).
-extern const char *const kBackendName = "cuda";
-}  // namespace host
-}  // namespace eng
+#endif

@@ -14,7 +14,7 @@
 namespace eng {
 namespace host {
 // Defined by each library: its device and backend name.
-std::unique_ptr<Device> MakeLibraryDevice(int threads);
+std::unique_ptr<Device> MakeLibraryDevice(int threads, int environments);
 extern const char *const kBackendName;
 }  // namespace host
 }  // namespace eng
@@ -75,7 +75,7 @@ void *cuju_environment_create(const struct cuju_configuration *s) {
     try {
         lastError.clear();
         const eng::host::Configuration c = ConfigurationOf(s);
-        return new BatchRuntime(c, eng::host::MakeLibraryDevice(s->threads));
+        return new BatchRuntime(c, eng::host::MakeLibraryDevice(s->threads, c.count));
     } catch (const std::exception &e) {
         Fail(e);
         return nullptr;
@@ -104,6 +104,7 @@ unsigned long long cuju_environment_memory_bytes(void *e) { return Of(e)->Memory
 void cuju_environment_destroy(void *e) { delete Of(e); }
 int cuju_environment_count(void *e) { return Of(e)->Count(); }
 int cuju_environment_threads(void *e) { return Of(e)->Dev().Threads(); }
+int cuju_environment_geometry(void *e, int *lanes) { return Of(e)->Dev().Geometry(lanes); }
 int cuju_environment_agents(void *e, int *left, int *right) {
     BatchRuntime *b = Of(e);
     for (int i = 0; i < b->Count(); i++) {

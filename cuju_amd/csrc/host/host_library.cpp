@@ -81,7 +81,7 @@ private:
 };
 }  // namespace
 
-std::unique_ptr<Device> MakeLibraryDevice(int threads) { return std::make_unique<HostDevice>(threads); }
+std::unique_ptr<Device> MakeLibraryDevice(int threads, int) { return std::make_unique<HostDevice>(threads); }
 extern const char *const kBackendName = "host";
 }  // namespace host
 }  // namespace eng

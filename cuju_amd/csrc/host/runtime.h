@@ -40,6 +40,11 @@ public:
     // Throws when a launch since the last check reached an undefined path.
     virtual void CheckFault() = 0;
     virtual int Threads() const { return 0; }
+    // Environments per wavefront, and in `lanes` the lanes of each (1 and 1 off the GPU).
+    virtual int Geometry(int *lanes) const {
+        *lanes = 1;
+        return 1;
+    }
     // The device's own scratch array for a step that allocates nothing, and the environments it
     // holds; null when the device has none.
     virtual Scratch *StaticScratch(int *environments) {

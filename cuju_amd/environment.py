@@ -333,6 +333,15 @@ class BatchEnvironment:
     def torch_device(self) -> torch.device:
         return self._torch_device
 
+    @property
+    def geometry(self) -> tuple:
+        """(environments per wavefront, lanes per environment) of the batch's kernels: the library
+        fills every SIMD with one wavefront where the batch allows, with wider groups for fewer
+        environments per wavefront."""
+        lanes = ctypes.c_int()
+        matches = self._lib.cuju_environment_geometry(self._handle(), ctypes.byref(lanes))
+        return int(matches), int(lanes.value)
+
     def _handle(self):
         if not self._native.handle:
             raise ClosedError('the batch is closed')

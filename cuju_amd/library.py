@@ -82,6 +82,7 @@ SIGNATURES = [
     ('cuju_environment_memory_bytes', U64, [P]),
     ('cuju_environment_destroy', None, [P]),
     ('cuju_environment_count', I, [P]),
+    ('cuju_environment_geometry', I, [P, P]),
     ('cuju_environment_threads', I, [P]),
     ('cuju_environment_agents', I, [P, P, P]),
     ('cuju_environment_players', I, [P, P, P]),

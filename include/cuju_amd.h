@@ -69,6 +69,9 @@ void cuju_environment_destroy(void *environment);
 int cuju_environment_count(void *environment);
 /* src/environment_api.h:200 */
 int cuju_environment_threads(void *environment);
+/* No counterpart in the reference: the launch geometry the library chose for the batch, the
+   environments in each wavefront, and in `lanes` the lanes that run each environment. */
+int cuju_environment_geometry(void *environment, int *lanes);
 /* src/environment_api.h:206 */
 int cuju_environment_agents(void *environment, int *left, int *right);
 /* src/environment_api.h:218 */

@@ -49,10 +49,22 @@ def host(x):
     return x.detach().cpu().numpy()
 
 
-def compare(assets, environments, steps, seed=0, reset_every=None, states=True, their_assets=None, **options):
+def compare(assets, environments, steps, seed=0, reset_every=None, states=True, their_assets=None, matches=None,
+            **options):
+    """`matches` sets the environments per wavefront (and so the group width) of the device batch;
+    by default the library chooses, which for these small batches is one environment of 16 lanes."""
     import cuju_amd
-    mine = cuju_amd.BatchEnvironment(assets, library=PRODUCT, device='cuda:0', environment_count=environments,
-                                     seed=seed, **options)
+    before = os.environ.get('CUJU_AMD_MATCHES')
+    if matches is not None:
+        os.environ['CUJU_AMD_MATCHES'] = str(matches)
+    try:
+        mine = cuju_amd.BatchEnvironment(assets, library=PRODUCT, device='cuda:0', environment_count=environments,
+                                         seed=seed, **options)
+    finally:
+        if before is None:
+            os.environ.pop('CUJU_AMD_MATCHES', None)
+        else:
+            os.environ['CUJU_AMD_MATCHES'] = before
     theirs = ref.ReferenceBatch(their_assets or assets, environment_count=environments, seed=seed, threads=0,
                                 **options)
     try:
@@ -86,17 +98,17 @@ def test_config1_five_a_side(representation, reference_library):
 
 
 def test_config2_eleven_a_side_one_agent(reference_library):
-    compare('11_vs_11_stochastic_l1_r0', 128, 120)
+    compare('11_vs_11_stochastic_l1_r0', 128, 120, matches=4)
 
 
 def test_config4_self_play_stacked_with_masked_resets(reference_library):
-    compare('11_vs_11_stochastic_l11_r11', 32, 120, seed=3, reset_every=40, stacked=True, states=False)
+    compare('11_vs_11_stochastic_l11_r11', 32, 120, seed=3, reset_every=40, stacked=True, states=False, matches=8)
 
 
 def test_config5_mixed_batch(reference_library):
     assignment = [0, 0, 1, 2] * 16
     compare(['academy_3_vs_1_with_keeper_l3_r0', '5_vs_5_l4_r0', '11_vs_11_stochastic_l1_r0'], 64, 150,
-            seed=5, assignment=assignment)
+            seed=5, assignment=assignment, matches=16)
 
 
 def test_config5_drills_from_a_scenario_file(reference_library, tmp_path):

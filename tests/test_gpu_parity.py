@@ -64,6 +64,48 @@ def test_gpu_matches_reference_on_headline_scenario(reference_library):
         theirs.close()
 
 
+@pytest.mark.parametrize('matches,lanes', [(16, 4), (8, 8), (4, 16), (1, 16)])
+def test_every_geometry_matches_the_reference(matches, lanes, reference_library, monkeypatch):
+    """Each build of the kernels (4, 8 and 16 lanes per environment) at the matches per wavefront
+    it serves plays the headline scenario as the reference does: 48 environments, 40 steps, then
+    every state. 16 matches of 4 lanes is the geometry of the headline batch of 16,384."""
+    monkeypatch.setenv('CUJU_AMD_MATCHES', str(matches))
+    environments, steps = 48, 40
+    mine = gpu_batch('11_vs_11_hard_stochastic_l11_r0', environment_count=environments, seed=2)
+    theirs = ref.ReferenceBatch('11_vs_11_hard_stochastic_l11_r0', environment_count=environments, seed=2,
+                                threads=0, library_path=reference_library)
+    try:
+        assert mine.geometry == (matches, lanes)
+        assert host(mine.reset()).tobytes() == theirs.reset().tobytes()
+        for step in range(steps):
+            actions = digest_actions(step, environments, 11, 19)
+            a = mine.step(torch.as_tensor(actions, device='cuda:0'))
+            b = theirs.step(actions)
+            for x, y in zip(a[:3], b):
+                assert host(x).astype(y.dtype).tobytes() == y.tobytes(), f'step {step}'
+        for e in range(environments):
+            assert mine.get_state(e) == theirs.get_state(e), f'state of environment {e}'
+    finally:
+        mine.close()
+        theirs.close()
+
+
+def test_the_geometry_fills_the_simds():
+    """One wavefront for each SIMD where the batch allows: 16 environments of 4 lanes at 16,384,
+    8 of 8 lanes at 8,192, 4 of 16 lanes at 4,096, one of 16 lanes for a small batch
+    (memory_estimate sizes these without allocating)."""
+    import cuju_amd
+    units = torch.cuda.get_device_properties(0).multi_processor_count
+    expected = {16 * 4 * units: (16, 4), 8 * 4 * units: (8, 8), 4 * 4 * units: (4, 16), 64: (1, 16)}
+    for environments, geometry in expected.items():
+        batch = cuju_amd.BatchEnvironment('academy_empty_goal_close', library=PRODUCT, device='cuda:0',
+                                          environment_count=environments)
+        try:
+            assert batch.geometry == geometry, environments
+        finally:
+            batch.close()
+
+
 def test_gpu_masked_reset_and_episode_end(reference_library):
     """Short academy episodes end and reset automatically; a masked reset with explicit and drawn
     seeds restarts a subset."""

@@ -6,14 +6,15 @@
 // matches' divergent control flow runs one path after another (16 identical matches step in a
 // quarter of the time of 16 ordinary ones), and a match's own sequential chain of dependent loads
 // sets a floor that wider groups lower, since the loops of independent iterations split over the
-// group. This file is compiled once per group width (4, 8 and 16 lanes), each copy with its own
+// group. This file is compiled once per group width (2, 4, 8 and 16 lanes), each copy with its own
 // kernels, fault words and device class; MakeLibraryDevice (the copy built with
 // ENG_PRIMARY_VARIANT) picks one per batch: as many matches per wavefront as fill every SIMD with
-// one wavefront, at most 16, and the widest group those matches leave room for. Measured on gfx950
+// one wavefront, at most 32, and the widest group those matches leave room for. Measured on gfx950
 // (ms per step after 100 steps): 64 environments of 5-a-side 80.4 at 4 lanes x 16 matches, 18.3 at
 // 16 lanes x 1; 4,096 of 11-a-side 219.6 at 4 x 16, 124.1 at 16 x 4; 8,192 of 11-a-side self-play
 // 236.8 at 4 x 16, 176.0 at 8 x 8; 16,384 of 11-a-side 280 at 4 x 16, 352 at 4 x 8 (two wavefronts
-// per SIMD), 356 at 4 x 12.
+// per SIMD), 356 at 4 x 12; 32,768 of the mixed batch 377 at 4 x 16 (two wavefronts per SIMD),
+// 365 at 2 x 32.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -228,12 +229,13 @@ Scratch *StaticScratchOfCurrentDevice(int *environments) {
     return static_cast<Scratch *>(gScratchAddress[device]);
 }
 
+std::unique_ptr<Device> MakeHipDevice2(int matches);
 std::unique_ptr<Device> MakeHipDevice4(int matches);
 std::unique_ptr<Device> MakeHipDevice8(int matches);
 std::unique_ptr<Device> MakeHipDevice16(int matches);
 
 // One wavefront for each SIMD where the batch allows it: the matches of a wavefront are the
-// environments over the SIMDs, 1 to 16, and the group is the widest of 16, 8 or 4 lanes that
+// environments over the SIMDs, 1 to 32, and the group is the widest of 16, 8, 4 or 2 lanes that
 // those matches leave room for in 64. CUJU_AMD_MATCHES sets the matches of a wavefront instead.
 std::unique_ptr<Device> MakeLibraryDevice(int, int environments) {
     int device = 0, units = 0;
@@ -242,10 +244,11 @@ std::unique_ptr<Device> MakeLibraryDevice(int, int environments) {
     const int simds = std::max(1, 4 * units);
     int matches = (std::max(1, environments) + simds - 1) / simds;
     if (const char *v = getenv("CUJU_AMD_MATCHES")) matches = atoi(v);
-    matches = std::max(1, std::min(16, matches));
+    matches = std::max(1, std::min(32, matches));
     if (matches <= 4) return MakeHipDevice16(matches);
     if (matches <= 8) return MakeHipDevice8(matches);
-    return MakeHipDevice4(matches);
+    if (matches <= 16) return MakeHipDevice4(matches);
+    return MakeHipDevice2(matches);
 }
 
 // torch names a HIP device "cuda" on ROCm; the reference binding compares this name with the

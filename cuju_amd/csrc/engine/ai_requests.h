@@ -308,18 +308,23 @@ struct AIController : AIBase {
             SetPieceCommands();
             return true;
         }
+        // The field strategy of each line and the on-the-ball commands each have one call site, so
+        // that matches of a wavefront whose players differ in role or situation run them together;
+        // per environment the calls and their order are GRF's.
+        int strategy = -1;
+        bool onTheBall = false;
         if (m.inPlay && !m.inSetPiece && m.ballRetainer != p && m.designatedPossessionPlayer != p && role != kRoleGoalkeeper) {
             if (role == kRoleLeftBack || role == kRoleCentreBack || role == kRoleRightBack)
-                FieldStrategyRequestInput(kDefense, rawDir, rawVel);
+                strategy = kDefense;
             else if (role == kRoleDefensiveMid || role == kRoleLeftMid || role == kRoleCentralMid || role == kRoleRightMid ||
                      role == kRoleAttackingMid)
-                FieldStrategyRequestInput(kMidfield, rawDir, rawVel);
+                strategy = kMidfield;
             else if (role == kRoleCentreForward)
-                FieldStrategyRequestInput(kOffense, rawDir, rawVel);
+                strategy = kOffense;
         } else if (m.inPlay && !m.inSetPiece && m.designatedPossessionPlayer == p &&
                    (HumanGamerCount(Own()) == 0 || (!ExternalControllerActive(w, p) && ps.base.externalController >= 0)) &&
                    role != kRoleGoalkeeper) {
-            if (ps.timeToBallMs < 1000) GetOnTheBallCommands(rawDir, rawVel);
+            onTheBall = ps.timeToBallMs < 1000;
             extraHaste = false;
         } else if (m.inPlay && !m.inSetPiece && role == kRoleGoalkeeper) {
             CalculateIfBallIsBoundForGoal();
@@ -329,8 +334,10 @@ struct AIController : AIBase {
             GoalieRequestInput(manualDir, manualVel);
             if (!ctl.hasUniquePossession || ctl.possessionAmount < 3.4f)
                 KeeperDeflectCommand(!bound && ctl.possessionAmount > 1.3f);
-            if (ps.timeToBallMs < 1000 && m.designatedPossessionPlayer == p) GetOnTheBallCommands(rawDir, rawVel);
+            onTheBall = ps.timeToBallMs < 1000 && m.designatedPossessionPlayer == p;
         }
+        if (strategy >= 0) FieldStrategyRequestInput(strategy, rawDir, rawVel);
+        if (onTheBall) GetOnTheBallCommands(rawDir, rawVel);
         bool forceMagnet = m.inPlay && !m.inSetPiece && (AI().endApplyTeamPressureMs > m.actualTimeMs && AI().teamPressurePlayer == p) &&
                            !ctl.teamHasBestPossession && m.designatedPossessionPlayer != p && role != kRoleGoalkeeper;
         ctl.inputDirection = rawDir;

@@ -256,75 +256,59 @@ HDN bool AnimationTouch(World &w, const Ctx &c, int p, const Anim &a, const Anim
     const Vec3 outMov = OutgoingMovementOf(pl);
     const int fn = cur.functionType;
     const bool knockOn = (cur.originatingCommand.modifier & kModifierKnockOn) != 0;
+    // Each function type computes the ball's new momentum and spin; the touch, the spin and the
+    // last touch then have one call site each, so that matches of a wavefront touching the ball
+    // in different ways run the ball's new prediction together. Per environment the calls and
+    // their order are GRF's.
+    Vec3 tv;
+    bool touch = true, rotate = true;
+    float rx = 0, ry = 0, rz = 0, bias = 1.0f;
+    int touchType = d.touchType;
     if (fn == kFnTrap || (fn == kFnBallControl && !ps.hasPossession)) {
-        float xr = 0, yr = 0;
-        Vec3 tv;
         if (!GetTrapVector(w, c, p, h.nextStartPos, h.nextStartAngle.value(), nba, outMov, cur, cur.frameNum, h.spatial,
-                           h.decayingPositionOffset, xr, yr, tv))
+                           h.decayingPositionOffset, rx, ry, tv))
             return false;
         if (knockOn) tv *= 1.35f;
         tv = tv * (1.0f - bumpy) + bm * bumpy;
-        BallTouch(w, c, tv);
-        BallSetRotation(w, xr, yr, 0, 0.5f * (1.0f - bumpy));
-        return TeamSetLastTouchPlayer(w, c, p, d.touchType);
-    }
-    if (fn == kFnBallControl) {
-        float xr = 0, yr = 0;
-        Vec3 tv;
-        if (!GetBallControlVector(w, c, p, h.nextStartPos, h.nextStartAngle.value(), nba, outMov, cur, cur.frameNum, h.spatial, xr,
-                                  yr, tv))
+        bias = 0.5f * (1.0f - bumpy);
+    } else if (fn == kFnBallControl) {
+        if (!GetBallControlVector(w, c, p, h.nextStartPos, h.nextStartAngle.value(), nba, outMov, cur, cur.frameNum, h.spatial, rx,
+                                  ry, tv))
             return false;
         if (knockOn) tv *= 1.35f;
         tv = tv * (1.0f - bumpy) + bm * bumpy;
-        BallTouch(w, c, tv);
-        BallSetRotation(w, xr, yr, 0, 0.6f * (1.0f - bumpy));
-        return TeamSetLastTouchPlayer(w, c, p, d.touchType);
-    }
-    if (fn == kFnInterfere) {
-        float xr = 0, yr = 0;
-        Vec3 tv;
+        bias = 0.6f * (1.0f - bumpy);
+    } else if (fn == kFnInterfere) {
         if (!GetTrapVector(w, c, p, h.nextStartPos, h.nextStartAngle.value(), nba, outMov, cur, cur.frameNum, h.spatial,
-                           h.decayingPositionOffset, xr, yr, tv))
+                           h.decayingPositionOffset, rx, ry, tv))
             return false;
         tv = tv * 0.5f + (BallPredict(w.match.ball, 0).Get2D() - h.spatial.position).Normalized() * 4.0f +
              Vec3(0, 0, RandomInRange(w, 0.5f, 1.5f));
         tv = tv * (1.0f - bumpy) + bm * bumpy;
-        BallTouch(w, c, tv);
         // GRF passes the bias as the z rotation here, with the default bias of 1.
-        BallSetRotation(w, xr, yr, 0.3f * (1.0f - bumpy));
-        return TeamSetLastTouchPlayer(w, c, p, kTouchAccidental);
-    }
-    if (fn == kFnSliding) {
-        Vec3 tv = d.ballDirection.Rotated2D(h.spatial.angle.value());
+        rz = 0.3f * (1.0f - bumpy);
+        touchType = kTouchAccidental;
+    } else if (fn == kFnSliding) {
+        tv = d.ballDirection.Rotated2D(h.spatial.angle.value());
         tv = tv * 6.0f + w.match.ball.momentum * -0.28f;
         tv += Vec3(0, 0, 6);
         tv = tv * (1.0f - bumpy) + bm * bumpy;
-        BallTouch(w, c, tv);
-        return TeamSetLastTouchPlayer(w, c, p, kTouchAccidental);
-    }
-    if (fn == kFnShortPass || fn == kFnLongPass || fn == kFnHighPass) {
-        Vec3 tv;
-        float zr = 0.0f;
-        if (!PassTouch(w, c, p, cur, tv, zr)) return false;
+        rotate = false;
+        touchType = kTouchAccidental;
+    } else if (fn == kFnShortPass || fn == kFnLongPass || fn == kFnHighPass) {
+        if (!PassTouch(w, c, p, cur, tv, rz)) return false;
         tv = tv * (1.0f - bumpy) + bm * bumpy;
-        BallTouch(w, c, tv);
         float forwardness = fn == kFnHighPass ? -1.3f : 3.5f;
         float tl = Clamp(tv.Length(), 0.0, 15.0);
-        float xr = tv.Normalized(0).v[1] * (tl * forwardness);
-        float yr = tv.Normalized(0).v[0] * (tl * forwardness);
-        BallSetRotation(w, xr, yr, zr, 0.9f * (1.0f - bumpy));
-        return TeamSetLastTouchPlayer(w, c, p, d.touchType);
-    }
-    if (fn == kFnShot) {
+        rx = tv.Normalized(0).v[1] * (tl * forwardness);
+        ry = tv.Normalized(0).v[0] * (tl * forwardness);
+        bias = 0.9f * (1.0f - bumpy);
+    } else if (fn == kFnShot) {
         // GRF computes a shot direction here and discards it; the call has no side effects.
-        float xr = 0, yr = 0, zr = 0;
-        Vec3 tv = GetShotVector(w, c, p, cur, h.spatial, h.decayingPositionOffset, xr, yr, zr);
+        tv = GetShotVector(w, c, p, cur, h.spatial, h.decayingPositionOffset, rx, ry, rz);
         tv = tv * (1.0f - bumpy) + bm * bumpy;
-        BallTouch(w, c, tv);
-        BallSetRotation(w, xr, yr, zr, 0.7f * (1.0f - bumpy));
-        return TeamSetLastTouchPlayer(w, c, p, d.touchType);
-    }
-    if (fn == kFnDeflect) {
+        bias = 0.7f * (1.0f - bumpy);
+    } else if (fn == kFnDeflect) {
         bool canRetain = d.outgoingRetainRawValue != kStrEmpty && w.match.ballRetainer == -1;
         float velDiff = NormalizedClamp((w.match.ball.momentum - h.spatial.movement).Length(), 0.0f, 40.0f);
         float reactDiff = 0.0f;
@@ -335,20 +319,24 @@ HDN bool AnimationTouch(World &w, const Ctx &c, int p, const Anim &a, const Anim
         if ((1.0f - velDiff) * (1.0f - reactDiff) < 0.3f) canRetain = false;
         if (canRetain) {
             w.match.ballRetainer = p;
+            touch = rotate = false;
         } else {
             Vec3 bmov = w.match.ball.momentum.Get2D();
             Vec3 pmov = h.spatial.movement;
             float lateral = RandomInRange(w, -1, 1);
-            Vec3 tv = (-bmov * 0.1f + pmov * 2.0f + Vec3(-TeamDynamicSide(w, t), 0, 0) * 4.0f + Vec3(0, lateral, 0)).Normalized(0) *
-                      (bmov.Length() * 0.3f + pmov.Length() * 2.5f);
+            tv = (-bmov * 0.1f + pmov * 2.0f + Vec3(-TeamDynamicSide(w, t), 0, 0) * 4.0f + Vec3(0, lateral, 0)).Normalized(0) *
+                 (bmov.Length() * 0.3f + pmov.Length() * 2.5f);
             tv.v[2] += 1.2f;
             tv = tv * (1.0f - bumpy) + bm * bumpy;
-            BallTouch(w, c, tv);
-            BallSetRotation(w, 0, 0, 0, 0.2f * (1.0f - bumpy));
+            bias = 0.2f * (1.0f - bumpy);
         }
-        return TeamSetLastTouchPlayer(w, c, p, kTouchAccidental);
+        touchType = kTouchAccidental;
+    } else {
+        return true;
     }
-    return true;
+    if (touch) BallTouch(w, c, tv);
+    if (rotate) BallSetRotation(w, rx, ry, rz, bias);
+    return TeamSetLastTouchPlayer(w, c, p, touchType);
 }
 
 // A humanoid's tick (humanoid_process.h:89-681) in three parts: the frame advance that decides

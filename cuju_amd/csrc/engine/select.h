@@ -1811,38 +1811,41 @@ struct Selector {
             Vec3 rel = RotatedBy(cmd.desiredDirection, BackTurn(angle));
             SetMovementSimilarityPredicate(rel, VelocityCat(cmd.desiredVelocityFloat));
             pred.lookAt = cmd.desiredLookAt;
-            if (fn == kFnMovement) {
-                KeepBestDirectionAnimations(l, cmd, true);
-                if (cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, true);
-            } else if (fn == kFnBallControl) {
-                bool strict = !AllowLastDitch();
-                float allowed = 0.0f * PI;
-                if (cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, strict, allowed);
-                KeepBestDirectionAnimations(l, cmd, strict, allowed, 0);
+            // The keep-best filters of each function type, as one call site per filter: matches of
+            // a wavefront that select for different function types run each filter together. Per
+            // environment the filters run in GRF's order (body direction first for ball control
+            // only).
+            const bool keeps = fn == kFnMovement || fn == kFnBallControl || fn == kFnTrap || fn == kFnInterfere;
+            bool strict = true;
+            float allowed = 0.0f;
+            int velocitySteps = 0;
+            if (fn == kFnBallControl) {
+                strict = !AllowLastDitch();
+                allowed = 0.0f * PI;
             } else if (fn == kFnTrap) {
-                bool hob = HighOrBouncyBall();
-                bool strict = !(AllowLastDitch(false) || hob);
-                float allowed = 0.3f * PI;
-                KeepBestDirectionAnimations(l, cmd, strict, allowed, 2, -1);
-                if (cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, strict, allowed);
-                if (!HighOrBouncyBall() && q.allowLastDitch == false) {
-                    Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
-                    const Anim &ba = A(l[0]);
-                    Vec3 bestOut = RotatedBy(ba.outgoingMovement, Turn(angle));
-                    float cdd = cmd.desiredDirection.Dot(s.directionVec);
-                    bool allow = true;
-                    float ad = fabsf(RotatedBy(ba.outgoingDirection, Turn(angle)).Angle2D(cmd.desiredDirection));
-                    if (ad > 0.375f * PI) allow = false;
-                    Vec3 diff = bestOut - dm;
-                    if ((diff.Length() > kWalkVelocity + 0.5f && cdd > 0.0f) || (diff.Length() > kSprintVelocity + 0.5f && cdd <= 0.0f))
-                        allow = false;
-                    if (!allow) return kSelectFalse;
-                }
+                strict = !(AllowLastDitch(false) || HighOrBouncyBall());
+                allowed = 0.3f * PI;
+                velocitySteps = 2;
             } else if (fn == kFnInterfere) {
-                bool strict = cmd.strictMovement == kStrictTrue;
-                float allowed = 0.3f * PI;
-                KeepBestDirectionAnimations(l, cmd, strict, allowed, 1);
-                if (cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, strict, allowed);
+                strict = cmd.strictMovement == kStrictTrue;
+                allowed = 0.3f * PI;
+                velocitySteps = 1;
+            }
+            if (fn == kFnBallControl && cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, strict, allowed);
+            if (keeps) KeepBestDirectionAnimations(l, cmd, strict, allowed, velocitySteps, -1);
+            if (keeps && fn != kFnBallControl && cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, strict, allowed);
+            if (fn == kFnTrap && !HighOrBouncyBall() && q.allowLastDitch == false) {
+                Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
+                const Anim &ba = A(l[0]);
+                Vec3 bestOut = RotatedBy(ba.outgoingMovement, Turn(angle));
+                float cdd = cmd.desiredDirection.Dot(s.directionVec);
+                bool allow = true;
+                float ad = fabsf(RotatedBy(ba.outgoingDirection, Turn(angle)).Angle2D(cmd.desiredDirection));
+                if (ad > 0.375f * PI) allow = false;
+                Vec3 diff = bestOut - dm;
+                if ((diff.Length() > kWalkVelocity + 0.5f && cdd > 0.0f) || (diff.Length() > kSprintVelocity + 0.5f && cdd <= 0.0f))
+                    allow = false;
+                if (!allow) return kSelectFalse;
             }
         }
         // A movement, trip or special needs only the first of the sort chain.
@@ -1880,6 +1883,10 @@ struct Selector {
         Vec3 dbr = Vec3(0, -1, 0);
         if (cmd.useDesiredLookAt)
             dbr = RotatedBy((cmd.desiredLookAt - (s.position + s.movement * 0.1f)).Normalized(Vec3(0, -1, 0)), BackTurn(angle));
+        // The candidate search of the touch function types and the physics plan of the others, as
+        // one call site each, so that matches selecting for different function types run them
+        // together.
+        bool cheat = false, prefer = false, physics = false;
         if (firstOnly) {
             const bool byTrip = cmd.useDesiredTripDirection, byBase = fn != kFnMovement;
             const int qi = l.count > 1 ? IncomingBodyDirectionQuery() : 0;
@@ -1893,31 +1900,28 @@ struct Selector {
                 k[n++] = KeyIdle(A(i), pred);
                 k[n++] = D(i).priorityAbsolute;
             });
-            Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
-            {
-                ENG_SCOPE(48);
-                CalculatePhysicsVector(sel, cmd.useDesiredMovement, dm, cmd.useDesiredLookAt, dbr, plan, tmpRot);
-            }
+            physics = true;
         } else if (fn == kFnBallControl) {
-            if (NeedTouch(l[0], cmd))
-                sel = GetBestCheatableAnimationID(l, cmd.useDesiredMovement, cmd.desiredDirection, cmd.desiredVelocityFloat,
-                                                  cmd.useDesiredLookAt, dbr, plan, tmpTouchFrame, tmpTouchPos, tmpSmuggle, tmpRot,
-                                                  preferPassAndShot);
+            cheat = NeedTouch(l[0], cmd);
+            prefer = preferPassAndShot;
         } else if (fn == kFnTrap || fn == kFnInterfere || fn == kFnDeflect) {
+            cheat = true;
+            prefer = preferPassAndShot;
+        } else if (fn == kFnShortPass || fn == kFnLongPass || fn == kFnHighPass || fn == kFnShot || fn == kFnSliding) {
+            cheat = true;
+        }
+        if (cheat)
             sel = GetBestCheatableAnimationID(l, cmd.useDesiredMovement, cmd.desiredDirection, cmd.desiredVelocityFloat,
                                               cmd.useDesiredLookAt, dbr, plan, tmpTouchFrame, tmpTouchPos, tmpSmuggle, tmpRot,
-                                              preferPassAndShot);
-        } else if (fn == kFnShortPass || fn == kFnLongPass || fn == kFnHighPass || fn == kFnShot) {
-            sel = GetBestCheatableAnimationID(l, cmd.useDesiredMovement, cmd.desiredDirection, cmd.desiredVelocityFloat,
-                                              cmd.useDesiredLookAt, dbr, plan, tmpTouchFrame, tmpTouchPos, tmpSmuggle, tmpRot);
-        } else if (fn == kFnSliding) {
-            sel = GetBestCheatableAnimationID(l, cmd.useDesiredMovement, cmd.desiredDirection, cmd.desiredVelocityFloat,
-                                              cmd.useDesiredLookAt, dbr, plan, tmpTouchFrame, tmpTouchPos, tmpSmuggle, tmpRot);
-            if (sel == -1 && !l.empty()) {
-                sel = l[0];
-                Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
-                CalculatePhysicsVector(sel, cmd.useDesiredMovement, dm, cmd.useDesiredLookAt, dbr, plan, tmpRot);
-            }
+                                              prefer);
+        if (fn == kFnSliding && sel == -1 && !l.empty()) {
+            sel = l[0];
+            physics = true;
+        }
+        if (physics) {
+            ENG_SCOPE(48);
+            Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
+            CalculatePhysicsVector(sel, cmd.useDesiredMovement, dm, cmd.useDesiredLookAt, dbr, plan, tmpRot);
         }
         if (interrupt == kIntReQueue && sel != -1 && cur.positions.count > 1 && plan.count > 1) {
             const Anim &sa = A(sel);

@@ -480,12 +480,16 @@ HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
                 GetPass(w, p, cmd.desiredFunctionType, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias,
                         ti.desiredDirection, ti.desiredPower, ti.targetPlayer, ti.forcedTargetPlayer);
                 q.push_back(cmd);
-            } else if (hc.actionButton == kBtnShortPass) {
-                pass(kFnShortPass, 0.7f, 0.4f, 0.7f);
-            } else if (hc.actionButton == kBtnLongPass) {
-                pass(kFnLongPass, 0.65f, 0.2f, 0.7f);
-            } else if (hc.actionButton == kBtnHighPass) {
-                pass(kFnHighPass, 0.55f, 0.2f, 0.5f);
+            } else if (hc.actionButton == kBtnShortPass || hc.actionButton == kBtnLongPass || hc.actionButton == kBtnHighPass) {
+                // One call site for the three passes, so that matches of a wavefront passing in
+                // different ways run the pass search together.
+                const int type = hc.actionButton == kBtnShortPass ? kFnShortPass
+                                 : hc.actionButton == kBtnLongPass ? kFnLongPass
+                                                                   : kFnHighPass;
+                const float exponent = type == kFnShortPass ? 0.7f : type == kFnLongPass ? 0.65f : 0.55f;
+                const float autoDir = type == kFnShortPass ? 0.4f : 0.2f;
+                const float autoPower = type == kFnHighPass ? 0.5f : 0.7f;
+                pass(type, exponent, autoDir, autoPower);
             } else if (hc.actionButton == kBtnShot) {
                 PlayerCommand cmd = DefaultPlayerCommand();
                 cmd.desiredFunctionType = kFnShot;

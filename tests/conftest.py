@@ -19,12 +19,6 @@ HOST = os.path.join(ROOT, 'cuju_amd', 'lib', 'libcuju_amd_host.so')
 REFERENCE = os.path.join(ROOT, 'oracle', '_ref', 'libcuju_cpu.so')
 
 
-# The long-horizon test runs fifteen batches at once, each on a stream of its own. HIP maps streams
-# onto this many hardware queues per process (its default is 4), and streams that share a queue run
-# one after another. It must be set before the process first uses the device.
-os.environ.setdefault('GPU_MAX_HW_QUEUES', '16')
-
-
 def pytest_configure(config):
     config.addinivalue_line('markers', 'gpu: needs an MI355X (HIP device)')
 

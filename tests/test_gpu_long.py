@@ -11,6 +11,10 @@ its own:
 
 These batches put one environment in a wavefront rather than the default sixteen
 (`lockstep.one_match_per_wavefront`): a step of a small batch then takes the time of one match.
+HIP spreads the streams over the process's hardware queues (4 by default), and the batches that
+share a queue run one after another, so a lockstep step costs about a quarter of the sum of the
+batches' own step times. `CUJU_AMD_LONG_PARTS` (default `digests,1,2,3,4,5`) names the parts to
+play, so a 10,000-step run can be split over several processes.
 """
 
 import hashlib
@@ -88,13 +92,19 @@ def test_long_horizons_match_the_reference(tmp_path, capsys):
     built = {os.path.basename(p): hashlib.sha256(open(p, 'rb').read()).hexdigest() for p in drill_paths}
     assert built == golden['drill_bundles'], 'the drill bundles differ from the reference builder\'s'
 
+    parts = os.environ.get('CUJU_AMD_LONG_PARTS', 'digests,' + ','.join(map(str, sorted(workloads.WORKLOADS))))
+    parts = {p.strip() for p in parts.split(',') if p.strip()}
+    unknown = parts - {'digests'} - {str(n) for n in workloads.WORKLOADS}
+    assert not unknown, f'CUJU_AMD_LONG_PARTS names no part {sorted(unknown)}'
     digests = load_digests()
     runs = []
     try:
         with lockstep.one_match_per_wavefront():
-            for name, case in sorted(digests['long_cases'].items()):
-                runs.append(lockstep.DigestRun(name, case, digests['environments'], digests['seed'], case['steps']))
-            for number in sorted(workloads.WORKLOADS):
+            if 'digests' in parts:
+                for name, case in sorted(digests['long_cases'].items()):
+                    runs.append(lockstep.DigestRun(name, case, digests['environments'], digests['seed'],
+                                                   case['steps']))
+            for number in sorted(n for n in workloads.WORKLOADS if str(n) in parts):
                 w = workloads.WORKLOADS[number]
                 for first, count in episodes.sample_ranges(w):
                     runs.append(episodes.EpisodeRun(w, first, count, DeviceSide(w, first, count, drill_paths),

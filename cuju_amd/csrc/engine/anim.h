@@ -72,7 +72,7 @@ HDN void ComputeInterpolated(const Anim &a, const KeyFrame *keys, int keyCount, 
 
 HD void Interpolated(const Ctx &c, const Anim &a, const NodeAnim &n, int frame, Quat &ori, Vec3 &pos) {
     if (frame < n.interpFrames) {
-        const InterpEntry &e = c.t->interp[n.interpFirst + (frame < 0 ? 0 : frame)];
+        const InterpEntry &e = c.t->interp[n.interpFirst + (frame < 0 ? 0 : frame) * n.interpStride];
         ori = e.orientation;
         pos = e.position;
         return;
@@ -88,7 +88,7 @@ HD void BlendFrames(Quat at, const Vec3 &pAt, const Quat &next, const Vec3 &pNex
 
 HD void InterpolatedZ(const Ctx &c, const Anim &a, const NodeAnim &n, int frame, Quat &ori, Vec3 &pos, float &z) {
     if (frame < n.interpFrames) {
-        const InterpEntry &e = c.t->interp[n.interpFirst + (frame < 0 ? 0 : frame)];
+        const InterpEntry &e = c.t->interp[n.interpFirst + (frame < 0 ? 0 : frame) * n.interpStride];
         ori = e.orientation;
         pos = e.position;
         z = e.angleZ;
@@ -281,7 +281,7 @@ HDN void ApplyNode(const Ctx &c, const Anim &a, const Skeleton &sk, Humanoid &h,
     // The table's halfway pose while `ori` still equals it, else null.
     const MiddleEntry *middle = nullptr;
     if (frame >= 0 && frame + 1 < na.interpFrames) {
-        middle = &c.t->middle[na.interpFirst + frame];
+        middle = &c.t->middle[na.interpFirst + frame * na.interpStride];
         ori = middle->orientation;
         pos = middle->position;
     } else {

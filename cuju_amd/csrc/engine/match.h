@@ -248,12 +248,16 @@ HDN void PlayerPreparePutBuffers(World &w, int p) {
 HDN void MatchPreparePutBuffers(World &w) {
     ENG_SCOPE(20);
     const int first = w.FirstTeamID(), second = 1 - first;
+    // A player's buffers and pose offsets are its own, and the rest of the match is only read, so
+    // the lanes of the match take a team's players in turn.
     MirrorMatch(w, false, false, first == 1);
     PlayerList a = TeamActivePlayers(w, first);
-    for (int i = 0; i < a.count; i++) PlayerPreparePutBuffers(w, a[i]);
+    for (int i = GroupRank(); i < a.count; i += kGroupLanes) PlayerPreparePutBuffers(w, a[i]);
+    GroupSync();
     MirrorMatch(w, false, false, true);
     PlayerList b = TeamActivePlayers(w, second);
-    for (int i = 0; i < b.count; i++) PlayerPreparePutBuffers(w, b[i]);
+    for (int i = GroupRank(); i < b.count; i += kGroupLanes) PlayerPreparePutBuffers(w, b[i]);
+    GroupSync();
     MirrorMatch(w, false, false, first == 0);
 }
 HDN void MatchFetchPutBuffers(World &w, const Ctx &c) {

@@ -185,8 +185,12 @@ struct MiddleEntry {
 struct NodeAnim {
     int32_t bodyPart;
     int32_t keyFirst, keyCount;
-    int32_t interpFirst;   // into interp[] and middle[], frames 0..frameCount+1
+    // Frame f (0..frameCount+1) of the node is entry interpFirst + f * interpStride of interp[] and
+    // middle[]: an animation's nodes lie side by side frame after frame, so the nodes of a pose
+    // share cache lines.
+    int32_t interpFirst;
     int32_t interpFrames;  // frameCount + 2
+    int32_t interpStride;  // the animation's node count
 };
 struct FootballKey {
     int32_t frame;

@@ -200,20 +200,21 @@ void BuildInterpolation(AnimationTables &t) {
     for (const Anim &a : t.anims) total += (size_t)a.nodeCount * (a.frameCount + 2);
     t.interp.assign(total, InterpEntry{});
     t.middle.assign(total, MiddleEntry{});
-    size_t off = 0;
+    size_t base = 0;
     for (const Anim &a : t.anims) {
-        const int frames = a.frameCount + 2;
+        const int frames = a.frameCount + 2, stride = a.nodeCount;
         for (int k = 0; k < a.nodeCount; k++) {
             NodeAnim &na = t.nodes[a.nodeFirst + k];
+            const size_t off = base + (size_t)k;
             for (int f = 0; f < frames; f++) {
-                InterpEntry &e = t.interp[off + f];
+                InterpEntry &e = t.interp[off + (size_t)f * stride];
                 ComputeInterpolated(a, t.keys.data() + na.keyFirst, na.keyCount, f, e.orientation, e.position);
                 float x, y;
                 e.orientation.Angles(x, y, e.angleZ);
             }
             for (int f = 0; f + 1 < frames; f++) {
-                const InterpEntry &at = t.interp[off + f], &nx = t.interp[off + f + 1];
-                MiddleEntry &m = t.middle[off + f];
+                const InterpEntry &at = t.interp[off + (size_t)f * stride], &nx = t.interp[off + (size_t)(f + 1) * stride];
+                MiddleEntry &m = t.middle[off + (size_t)f * stride];
                 BlendFrames(at.orientation, at.position, nx.orientation, nx.position, 0.5f, m.orientation, m.position);
                 m.normalized = m.orientation.Normalized();
                 const float sq = m.orientation.SquaredMagnitude();
@@ -221,8 +222,9 @@ void BuildInterpolation(AnimationTables &t) {
             }
             na.interpFirst = (int32_t)off;
             na.interpFrames = frames;
-            off += frames;
+            na.interpStride = stride;
         }
+        base += (size_t)a.nodeCount * frames;
     }
 }
 

@@ -36,10 +36,13 @@ COMMON = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math', '
 # latency-bound step kernel gains about 3% from (331 against 343 ms per step after 100 steps).
 # The instruction scheduler's max-ILP strategy spreads independent work between dependent loads:
 # 276-279 against 280-283 ms per step; the memory-clause strategy and promoting stack arrays to
-# registers measured no better.
+# registers measured no better. The step kernel is bounded to two wavefronts per SIMD
+# (hip_device.hip); without AGPR spills it fits that bound in 254 VGPRs, with them it takes 257
+# registers and one wavefront per SIMD.
 HIP_FLAGS = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math', '-fvisibility=hidden', '-w',
              f'--offload-arch={ARCH}', '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
-             '-mllvm', '-unroll-runtime', '-mllvm', '-amdgpu-sched-strategy=max-ilp']
+             '-mllvm', '-unroll-runtime', '-mllvm', '-amdgpu-sched-strategy=max-ilp',
+             '-mllvm', '-amdgpu-spill-vgpr-to-agpr=0']
 
 
 # The device code is built once per group width (lanes per environment); the first build also

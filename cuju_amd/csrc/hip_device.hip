@@ -7,14 +7,20 @@
 // quarter of the time of 16 ordinary ones), and a match's own sequential chain of dependent loads
 // sets a floor that wider groups lower, since the loops of independent iterations split over the
 // group. This file is compiled once per group width (2, 4, 8 and 16 lanes), each copy with its own
-// kernels, fault words and device class; MakeLibraryDevice (the copy built with
-// ENG_PRIMARY_VARIANT) picks one per batch: as many matches per wavefront as fill every SIMD with
-// one wavefront, at most 32, and the widest group those matches leave room for. Measured on gfx950
-// (ms per step after 100 steps): 64 environments of 5-a-side 80.4 at 4 lanes x 16 matches, 18.3 at
-// 16 lanes x 1; 4,096 of 11-a-side 219.6 at 4 x 16, 124.1 at 16 x 4; 8,192 of 11-a-side self-play
-// 236.8 at 4 x 16, 176.0 at 8 x 8; 16,384 of 11-a-side 280 at 4 x 16, 352 at 4 x 8 (two wavefronts
-// per SIMD), 356 at 4 x 12; 32,768 of the mixed batch 377 at 4 x 16 (two wavefronts per SIMD),
-// 365 at 2 x 32.
+// kernels, fault words and device class.
+//
+// Occupancy. The step kernel is bounded to the registers of two wavefronts per SIMD (256 VGPRs,
+// none spilled to AGPRs: -mllvm -amdgpu-spill-vgpr-to-agpr=0), so two wavefronts share each SIMD
+// and each hides the other's memory latency; unbounded, the kernel takes 256 VGPRs and 58 AGPRs,
+// one wavefront per SIMD. MakeLibraryDevice (the copy built with ENG_PRIMARY_VARIANT) picks the
+// geometry per batch: as many matches per wavefront as fill every SIMD with two wavefronts, at most
+// 32, and the widest group those matches leave room for. Measured on gfx950, ms per step after 100
+// steps, one wavefront per SIMD against two: 4,096 environments of 11-a-side 118.5 at 16 lanes x 4
+// matches against 103.6 at 16 x 2; 8,192 of 11-a-side self-play 172.4 at 8 x 8 against 144.4 at
+// 16 x 4; 16,384 of 11-a-side 258.6 at 4 x 16 against 206.1 at 8 x 8 (205.6 at 8 x 6 with three
+// wavefronts per SIMD); 32,768 of the mixed batch 342.8 at 2 x 32 against 245.2 at 4 x 16. The
+// bound itself costs nothing: 257.7 at 4 x 16 with one wavefront per SIMD. 64 environments of
+// 5-a-side take 20.6 at 16 x 1 either way.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -49,7 +55,7 @@ __device__ int32_t gFaultEnvironment;
 constexpr int kWaveLanes = 64;
 // Wavefronts each SIMD must be able to hold, which bounds the registers of a lane.
 #ifndef ENG_WAVES_PER_SIMD
-#define ENG_WAVES_PER_SIMD 1
+#define ENG_WAVES_PER_SIMD 2
 #endif
 constexpr int kDeviceGroupLanes = ENG_GROUP_LANES;
 constexpr int kMaxMatches = kWaveLanes / kDeviceGroupLanes;
@@ -241,8 +247,8 @@ std::unique_ptr<Device> MakeLibraryDevice(int, int environments) {
     int device = 0, units = 0;
     Check(hipGetDevice(&device), "hipGetDevice");
     Check(hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
-    const int simds = std::max(1, 4 * units);
-    int matches = (std::max(1, environments) + simds - 1) / simds;
+    const int slots = std::max(1, 4 * units * ENG_WAVES_PER_SIMD);
+    int matches = (std::max(1, environments) + slots - 1) / slots;
     if (const char *v = getenv("CUJU_AMD_MATCHES")) matches = atoi(v);
     matches = std::max(1, std::min(32, matches));
     if (matches <= 4) return MakeHipDevice16(matches);

@@ -336,7 +336,7 @@ class BatchEnvironment:
     @property
     def geometry(self) -> tuple:
         """(environments per wavefront, lanes per environment) of the batch's kernels: the library
-        fills every SIMD with one wavefront where the batch allows, with wider groups for fewer
+        gives every SIMD two wavefronts where the batch allows, with wider groups for fewer
         environments per wavefront."""
         lanes = ctypes.c_int()
         matches = self._lib.cuju_environment_geometry(self._handle(), ctypes.byref(lanes))

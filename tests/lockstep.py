@@ -6,8 +6,8 @@ A run has `start()`, `launch()` (enqueue one step), `collect()` (wait for it and
 outputs) and `done`. `one_match_per_wavefront()` makes the batches created inside it put a single
 environment in each wavefront: a wavefront then follows one match's control flow, and a step of a
 small batch takes the least time. The environments of a wavefront are independent, so the
-geometry changes no result; the tests that run the default geometry (16 environments in a
-wavefront) cover the code where matches of a wavefront wait for each other.
+geometry changes no result; the tests that run the library's geometries (up to 32 environments in
+a wavefront) cover the code where matches of a wavefront wait for each other.
 """
 
 from __future__ import annotations

@@ -68,7 +68,7 @@ def test_gpu_matches_reference_on_headline_scenario(reference_library):
 def test_every_geometry_matches_the_reference(matches, lanes, reference_library, monkeypatch):
     """Each build of the kernels (2, 4, 8 and 16 lanes per environment) at the matches per wavefront
     it serves plays the headline scenario as the reference does: 48 environments, 40 steps, then
-    every state. 16 matches of 4 lanes is the geometry of the headline batch of 16,384."""
+    every state. 8 matches of 8 lanes is the geometry of the headline batch of 16,384."""
     monkeypatch.setenv('CUJU_AMD_MATCHES', str(matches))
     environments, steps = 48, 40
     mine = gpu_batch('11_vs_11_hard_stochastic_l11_r0', environment_count=environments, seed=2)
@@ -91,13 +91,12 @@ def test_every_geometry_matches_the_reference(matches, lanes, reference_library,
 
 
 def test_the_geometry_fills_the_simds():
-    """One wavefront for each SIMD where the batch allows: 32 environments of 2 lanes at 32,768, 16 of
-    4 lanes at 16,384,
-    8 of 8 lanes at 8,192, 4 of 16 lanes at 4,096, one of 16 lanes for a small batch
-    (memory_estimate sizes these without allocating)."""
+    """Two wavefronts for each SIMD where the batch allows: 32 environments of 2 lanes at 65,536,
+    16 of 4 lanes at 32,768, 8 of 8 lanes at 16,384, 4 of 16 lanes at 8,192, 2 of 16 lanes at
+    4,096 and one of 16 lanes for a small batch (memory_estimate sizes these without allocating)."""
     import cuju_amd
-    units = torch.cuda.get_device_properties(0).multi_processor_count
-    expected = {32 * 4 * units: (32, 2), 16 * 4 * units: (16, 4), 8 * 4 * units: (8, 8), 4 * 4 * units: (4, 16),
+    slots = 2 * 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    expected = {32 * slots: (32, 2), 16 * slots: (16, 4), 8 * slots: (8, 8), 4 * slots: (4, 16), 2 * slots: (2, 16),
                 64: (1, 16)}
     for environments, geometry in expected.items():
         batch = cuju_amd.BatchEnvironment('academy_empty_goal_close', library=PRODUCT, device='cuda:0',

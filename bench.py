@@ -36,7 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-WORLD_BYTES = 373_552
+WORLD_BYTES = 373_440  # sizeof(eng::World), checked by tests/test_workloads.py
 STEADY_WARMUP = 100
 
 # HBM bytes one step launch moves, read + written, from rocprofv3 FETCH_SIZE and WRITE_SIZE passes

@@ -1,6 +1,9 @@
 """The workloads' inputs: the counter hash gives the same draws as Python integers, numpy and torch
 (so the host, the oracle and the device consume identical inputs), a slice of a workload gets the
-inputs of the same environments in the full batch, and workload 5's drill family and assignment."""
+inputs of the same environments in the full batch, and workload 5's drill family and assignment;
+and the bench's algorithmic bytes use the engine's world size."""
+
+import ctypes
 
 import numpy as np
 import torch
@@ -47,3 +50,13 @@ def test_drill_family_and_the_mixed_assignment():
     assert (assignment == drills).mean() == 0.25 and (assignment == drills + 1).mean() == 0.25
     assert len(set(assignment[assignment < drills].tolist())) == drills
     assert np.array_equal(w.assignment(32760, 8), assignment[32760:])
+
+
+def test_the_bench_counts_the_engine_world(host_library):
+    import bench
+    lib = ctypes.CDLL(host_library)
+    sizes = (ctypes.c_ulonglong * 4)()
+    lib.cuju_debug_layout(sizes)
+    assert bench.WORLD_BYTES == sizes[0]
+    workload = workloads.WORKLOADS[3]
+    assert bench.algorithmic_bytes(workload, 11, 11) == 2 * sizes[0] + 11 * (4 + 460) + 4 * 11 + 5

@@ -36,7 +36,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-WORLD_BYTES = 373_440  # sizeof(eng::World), checked by tests/test_workloads.py
+# The reference world's size (sizeof(cuju::simulation::World), 11 players a side), read and written
+# once per environment step: the per-unit figure of the roofline, independent of this engine's own
+# layout (its World is 373,440 B).
+WORLD_BYTES = 373_552
 STEADY_WARMUP = 100
 
 # HBM bytes one step launch moves, read + written, from rocprofv3 FETCH_SIZE and WRITE_SIZE passes

@@ -1,9 +1,7 @@
 """The workloads' inputs: the counter hash gives the same draws as Python integers, numpy and torch
 (so the host, the oracle and the device consume identical inputs), a slice of a workload gets the
 inputs of the same environments in the full batch, and workload 5's drill family and assignment;
-and the bench's algorithmic bytes use the engine's world size."""
-
-import ctypes
+and the bench's algorithmic bytes of each workload."""
 
 import numpy as np
 import torch
@@ -52,11 +50,10 @@ def test_drill_family_and_the_mixed_assignment():
     assert np.array_equal(w.assignment(32760, 8), assignment[32760:])
 
 
-def test_the_bench_counts_the_engine_world(host_library):
+def test_the_bench_counts_the_algorithmic_bytes_of_each_workload():
+    """B_step = 2 x 373,552 (the reference world read and written) + the compulsory I/O of the
+    workload's agents: 748,981 B for workload 1, 747,577 for 2, 752,257 for 3, 818,125 for 4."""
     import bench
-    lib = ctypes.CDLL(host_library)
-    sizes = (ctypes.c_ulonglong * 4)()
-    lib.cuju_debug_layout(sizes)
-    assert bench.WORLD_BYTES == sizes[0]
-    workload = workloads.WORKLOADS[3]
-    assert bench.algorithmic_bytes(workload, 11, 11) == 2 * sizes[0] + 11 * (4 + 460) + 4 * 11 + 5
+    expected = {1: (4, 4, 748_981), 2: (1, 1, 747_577), 3: (11, 11, 752_257), 4: (22, 22, 818_125)}
+    for number, (present, axis, total) in expected.items():
+        assert bench.algorithmic_bytes(workloads.WORKLOADS[number], present, axis) == total, number

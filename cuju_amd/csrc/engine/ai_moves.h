@@ -501,7 +501,8 @@ struct AIBase {
         const int designated = Own().designatedTeamPossessionPlayer;
         Vec3 cur = Pos() + Mov() * 0.1f;
         Vec3 mainMan = Pos(designated) + Mov(designated) * 0.1f;
-        ForceField ff;
+        ForceField &ff = c.ws->forceField;
+        ff.clear();
         float mind = GetMindSet(DynamicRole());
         const bool forceNoOffside = true;
         const float baseW = 0.7f, overall = 1.0f;
@@ -789,7 +790,8 @@ struct AIBase {
         float offense = 0.7f + kDribbleOffensiveness * 0.05f + GetMindSet(DynamicRole()) * 0.05f;
         const float powerMul = 1.0f, futureS = 0.25f;
         PlayerList opps = GetClosestPlayers(w, c, oppID, mp, false, 5);
-        ForceField ff;
+        ForceField &ff = c.ws->forceField;
+        ff.clear();
         float nearBackline = NormalizedClamp(fabsf(mp.v[0]) / kPitchHalfLength, 0.0f, 1.0f);
         float centerInv = 1.0f - nearBackline * nearBackline;
         centerInv *= 0.5f;

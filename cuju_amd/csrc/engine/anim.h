@@ -150,65 +150,6 @@ HD void DeriveNodes(const Skeleton &sk, const NodeState *nodes, Derived *out) {
     }
 }
 
-struct Aabb {
-    Vec3 lo, hi;
-    // GRF: the maximum starts at FLT_MIN / 100, just above zero, which collisions depend on.
-    HD void Reset() {
-        const float smallest = 1.17549435e-38f / 100, largest = 3.40282347e+38f / 100;
-        lo = Vec3(largest, largest, largest);
-        hi = Vec3(smallest, smallest, smallest);
-    }
-    HDN Aabb Rotated(const Quat &r) const {
-        Vec3 corners[8] = {Vec3(lo.v[0], lo.v[1], lo.v[2]), Vec3(hi.v[0], lo.v[1], lo.v[2]),
-                           Vec3(lo.v[0], hi.v[1], lo.v[2]), Vec3(hi.v[0], hi.v[1], lo.v[2]),
-                           Vec3(lo.v[0], lo.v[1], hi.v[2]), Vec3(hi.v[0], lo.v[1], hi.v[2]),
-                           Vec3(lo.v[0], hi.v[1], hi.v[2]), Vec3(hi.v[0], hi.v[1], hi.v[2])};
-        Aabb b;
-        b.Reset();
-        for (Vec3 &cn : corners) {
-            cn = r * cn;
-            for (int k = 0; k < 3; k++) {
-                if (cn.v[k] < b.lo.v[k]) b.lo.v[k] = cn.v[k];
-                if (cn.v[k] > b.hi.v[k]) b.hi.v[k] = cn.v[k];
-            }
-        }
-        return b;
-    }
-    HD Aabb Translated(const Vec3 &o) const {
-        Aabb b = *this;
-        b.lo += o;
-        b.hi += o;
-        return b;
-    }
-    HDN bool Intersects(const Vec3 &center, float radius) const {
-        float d2 = 0;
-        for (int k = 0; k < 3; k++) {
-            if (center.v[k] < lo.v[k]) {
-                float d = center.v[k] - lo.v[k];
-                d2 += d * d;
-            } else if (center.v[k] > hi.v[k]) {
-                float d = center.v[k] - hi.v[k];
-                d2 += d * d;
-            }
-        }
-        return d2 <= radius * radius;
-    }
-    // Each coordinate divides by 2 in double and rounds to float.
-    HD Vec3 Center() const {
-        float x = (lo.v[0] + hi.v[0]) / 2.0, y = (lo.v[1] + hi.v[1]) / 2.0, z = (lo.v[2] + hi.v[2]) / 2.0;
-        return Vec3(x, y, z);
-    }
-    // Squares and roots in double (std::pow(float, int)), rounded to float twice.
-    HD float Radius() const {
-        float x = hi.v[0] - lo.v[0], y = hi.v[1] - lo.v[1], z = hi.v[2] - lo.v[2];
-        float l = (float)sqrt((double)x * x + (double)y * y);
-        return (float)(sqrt((double)l * l + (double)z * z) / 2.0);
-    }
-};
-struct WorldGeometry {
-    Aabb box;
-    Vec3 position;
-};
 // GRF: the mesh box rotated and moved by the world transform; the scale does not enter.
 HD WorldGeometry GeometryWorld(const SkelGeometry &g, const Derived &node) {
     Derived d = DeriveChild(&node, g.localMode, g.position, g.rotation, g.scale);

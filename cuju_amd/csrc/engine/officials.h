@@ -11,8 +11,6 @@
 
 namespace eng {
 
-constexpr int kMaxCommands = 16;
-using CommandQueue = Small<PlayerCommand, kMaxCommands>;
 constexpr int kModifierKnockOn = 1;
 
 HD PlayerCommand DefaultPlayerCommand() {
@@ -56,17 +54,6 @@ HD PlayerCommand GetBasicMovementCommand(const Humanoid &h, float velocity) {
 // ---- force fields -----------------------------------------------------------------------------------
 constexpr float kDistanceToVelocity = 2.6f;
 constexpr float kBallDistanceOptimizeThreshold = 10.0f;
-enum MagnetType { kAttract, kRepel };
-enum DecayType { kDecayConstant, kDecayVariable };
-struct ForceSpot {
-    Vec3 origin;
-    int32_t magnet = kAttract;
-    int32_t decay = kDecayConstant;
-    float exponent = 1.0f;
-    float power = 0.0f;
-    float scale = 0.0f;
-};
-using ForceField = Small<ForceSpot, 64>;
 
 HD ForceSpot MakeSpot(const Vec3 &origin, int magnet, int decay, float power, float scale = 0.0f,
                       float exponent = 1.0f) {
@@ -170,7 +157,7 @@ HDN Vec3 BallAveragePosition(const World &w, unsigned durationMs) {
 }
 
 // ---- officials ---------------------------------------------------------------------------------------
-HDN void RefereeRequestCommand(World &w, int official, CommandQueue &q) {
+HDN void RefereeRequestCommand(World &w, const Ctx &ctx, int official, CommandQueue &q) {
     const MatchState &m = w.match;
     const SpatialState &s = m.officials[official].humanoid.spatial;
     const Vec3 pos = s.position;
@@ -207,7 +194,8 @@ HDN void RefereeRequestCommand(World &w, int official, CommandQueue &q) {
             PlayerCommand c = DefaultPlayerCommand();
             c.useDesiredMovement = true;
             c.useDesiredLookAt = true;
-            ForceField field;
+            ForceField &field = ctx.ws->forceField;
+            field.clear();
             field.push_back(MakeSpot(BallAveragePosition(w, 2000).Get2D() * 0.6f, kAttract, kDecayConstant, 0.5f));
             field.push_back(MakeSpot(BallPredict(m.ball, 200).Get2D(), kRepel, kDecayVariable, 0.5f, 10.0f));
             const int first = w.FirstTeamID();
@@ -261,13 +249,14 @@ HDN bool OfficialHumanoidProcess(World &w, const Ctx &c, int official) {
     h.prevAnimFrameNum++;
     if (cur.frameNum == c.A(cur.anim).frameCount - 1 && h.interruptAnim == kIntNone) h.interruptAnim = kIntSwitch;
     if (h.interruptAnim != kIntNone) {
-        CommandQueue q;
+        CommandQueue &q = c.ws->commands;
+        q.clear();
         if (h.interruptAnim == kIntTrip && h.tripType != 0) {
             AddTripCommandToQueue(h, q, h.tripType);
             h.tripType = 0;
             q.push_back(GetBasicMovementCommand(h, h.spatial.floatVelocity));
         } else {
-            RefereeRequestCommand(w, official, q);
+            RefereeRequestCommand(w, c, official, q);
         }
         bool found = false;
         for (int i = 0; i < q.count; i++) {

@@ -369,7 +369,8 @@ HDN bool HumanoidProcessInterrupt(World &w, const Ctx &c, int p) {
     AnimationState &cur = h.anim;
     {
         ENG_SCOPE(30);
-        CommandQueue q;
+        CommandQueue &q = c.ws->commands;
+        q.clear();
         if (h.interruptAnim == kIntTrip && h.tripType != 0) {
             AddTripCommandToQueue(h, q, h.tripType);
             h.tripType = 0;

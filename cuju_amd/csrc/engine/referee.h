@@ -447,21 +447,11 @@ HDN void TripMe(World &w, const Ctx &c, int p, const Vec3 &tripVector, int tripT
     }
 }
 
-struct PlayerBounce {
-    int32_t opponent;
-    float force;
-};
-using PlayerBounceList = Small<PlayerBounce, kPlayers>;
 
 HD bool BoxesIntersect(const Aabb &a, const Aabb &o) {
     return (o.lo.v[0] < a.hi.v[0] && o.lo.v[1] < a.hi.v[1] && o.lo.v[2] < a.hi.v[2]) &&
            (o.hi.v[0] > a.lo.v[0] && o.hi.v[1] > a.lo.v[1] && o.hi.v[2] > a.lo.v[2]);
 }
-struct PlayerGeometry {
-    bool footOrLowerLeg;
-    WorldGeometry wg;
-};
-using PlayerGeometryList = Small<PlayerGeometry, kHumanoidNodes * 2>;
 HDN void PlayerGeometries(const World &w, const Ctx &c, int p, PlayerGeometryList &out) {
     const Skeleton &sk = c.skeletons[p];
     Derived der[kHumanoidNodes];
@@ -613,7 +603,7 @@ HDN void CheckHumanoidCollision(World &w, const Ctx &c, int p1, int p2, PlayerBo
     if ((fnOf(p2) == kFnSliding || fnOf(p2) == kFnInterfere) && frameOf(p2) > 5 && frameOf(p2) < 28) tackle += 2;
     if (dist < 2.0f && tackle > 0 && tackle < 3) {
         const int tackler = tackle == 1 ? p1 : p2, victim = tackle == 1 ? p2 : p1;
-        PlayerGeometryList tg, vg;
+        PlayerGeometryList &tg = c.ws->tackleGeometry[0], &vg = c.ws->tackleGeometry[1];
         PlayerGeometries(w, c, tackler, tg);
         PlayerGeometries(w, c, victim, vg);
         for (int i = 0; i < tg.count; i++) {
@@ -638,7 +628,8 @@ HDN void CheckHumanoidCollision(World &w, const Ctx &c, int p1, int p2, PlayerBo
 HDN bool CheckHumanoidCollisions(World &w, const Ctx &c) {
     ENG_SCOPE(17);
     PlayerList ps = PlayersInProcessingOrder(w);
-    PlayerBounceList bounces[kPlayers];
+    PlayerBounceList *const bounces = c.ws->bounces;
+    for (int i = 0; i < ps.count; i++) bounces[i].clear();
     // A pair farther apart than both contact radii changes nothing, so only near pairs make the
     // call; the test is the one the pair's own check starts with, on the same values.
     const float bounceRadius = 0.5f * 0.72f, similarRadius = 0.8f * 0.72f;

@@ -321,13 +321,128 @@ struct TimeWalk {
     float usual[kTimeWalkSteps], optimistic[kTimeWalkSteps];
     float usualSquared[kTimeWalkSteps], optimisticSquared[kTimeWalkSteps];
 };
+HD void Fatal(const char *reason);
+
+// A small inline list (GRF's std::vector uses), capacity fixed.
+template <class T, int N>
+struct Small {
+    int32_t count = 0;
+    T e[N];
+    HD int size() const { return count; }
+    HD bool empty() const { return count == 0; }
+    HD void clear() { count = 0; }
+    HD void push_back(const T &x) {
+        if (count >= N) Fatal("a fixed-capacity list outgrows its capacity");
+        else e[count++] = x;
+    }
+    HD T &operator[](int i) { return e[i]; }
+    HD const T &operator[](int i) const { return e[i]; }
+    HD T *begin() { return e; }
+    HD T *end() { return e + count; }
+    HD const T *begin() const { return e; }
+    HD const T *end() const { return e + count; }
+    HD T &back() { return e[count - 1]; }
+};
+struct Aabb {
+    Vec3 lo, hi;
+    // GRF: the maximum starts at FLT_MIN / 100, just above zero, which collisions depend on.
+    HD void Reset() {
+        const float smallest = 1.17549435e-38f / 100, largest = 3.40282347e+38f / 100;
+        lo = Vec3(largest, largest, largest);
+        hi = Vec3(smallest, smallest, smallest);
+    }
+    HDN Aabb Rotated(const Quat &r) const {
+        Vec3 corners[8] = {Vec3(lo.v[0], lo.v[1], lo.v[2]), Vec3(hi.v[0], lo.v[1], lo.v[2]),
+                           Vec3(lo.v[0], hi.v[1], lo.v[2]), Vec3(hi.v[0], hi.v[1], lo.v[2]),
+                           Vec3(lo.v[0], lo.v[1], hi.v[2]), Vec3(hi.v[0], lo.v[1], hi.v[2]),
+                           Vec3(lo.v[0], hi.v[1], hi.v[2]), Vec3(hi.v[0], hi.v[1], hi.v[2])};
+        Aabb b;
+        b.Reset();
+        for (Vec3 &cn : corners) {
+            cn = r * cn;
+            for (int k = 0; k < 3; k++) {
+                if (cn.v[k] < b.lo.v[k]) b.lo.v[k] = cn.v[k];
+                if (cn.v[k] > b.hi.v[k]) b.hi.v[k] = cn.v[k];
+            }
+        }
+        return b;
+    }
+    HD Aabb Translated(const Vec3 &o) const {
+        Aabb b = *this;
+        b.lo += o;
+        b.hi += o;
+        return b;
+    }
+    HDN bool Intersects(const Vec3 &center, float radius) const {
+        float d2 = 0;
+        for (int k = 0; k < 3; k++) {
+            if (center.v[k] < lo.v[k]) {
+                float d = center.v[k] - lo.v[k];
+                d2 += d * d;
+            } else if (center.v[k] > hi.v[k]) {
+                float d = center.v[k] - hi.v[k];
+                d2 += d * d;
+            }
+        }
+        return d2 <= radius * radius;
+    }
+    // Each coordinate divides by 2 in double and rounds to float.
+    HD Vec3 Center() const {
+        float x = (lo.v[0] + hi.v[0]) / 2.0, y = (lo.v[1] + hi.v[1]) / 2.0, z = (lo.v[2] + hi.v[2]) / 2.0;
+        return Vec3(x, y, z);
+    }
+    // Squares and roots in double (std::pow(float, int)), rounded to float twice.
+    HD float Radius() const {
+        float x = hi.v[0] - lo.v[0], y = hi.v[1] - lo.v[1], z = hi.v[2] - lo.v[2];
+        float l = (float)sqrt((double)x * x + (double)y * y);
+        return (float)(sqrt((double)l * l + (double)z * z) / 2.0);
+    }
+};
+struct WorldGeometry {
+    Aabb box;
+    Vec3 position;
+};
+struct PlayerGeometry {
+    bool footOrLowerLeg;
+    WorldGeometry wg;
+};
+using PlayerGeometryList = Small<PlayerGeometry, kHumanoidNodes * 2>;
+
+// Lists that the match's sequential code fills and reads within one call: an interruption's
+// command queue, one force field of the AI or the referee, the bounces of the collision pass and
+// the geometry of a tackler and its victim.
+constexpr int kMaxCommands = 16;
+using CommandQueue = Small<PlayerCommand, kMaxCommands>;
+enum MagnetType { kAttract, kRepel };
+enum DecayType { kDecayConstant, kDecayVariable };
+struct ForceSpot {
+    Vec3 origin;
+    int32_t magnet = kAttract;
+    int32_t decay = kDecayConstant;
+    float exponent = 1.0f;
+    float power = 0.0f;
+    float scale = 0.0f;
+};
+using ForceField = Small<ForceSpot, 64>;
+struct PlayerBounce {
+    int32_t opponent;
+    float force;
+};
+using PlayerBounceList = Small<PlayerBounce, kPlayers>;
+
 // Lanes of one match with a plan of their own in the candidate search.
 constexpr int kPlanLanes = 16;
 static_assert(kGroupLanes <= kPlanLanes, "every lane of a match needs a candidate plan");
-// Per-match working memory for the animation selection: candidate lists, planned positions, sort
-// keys and one candidate plan per lane of the match. One block per environment in HBM, which every
-// lane of the match addresses, in place of large per-lane stack arrays.
+// Per-match working memory: the animation selection's candidate lists, planned positions, sort keys
+// and one candidate plan per lane of the match, and the lists above. One block per environment in
+// HBM, which every lane of the match addresses, in place of large per-lane stack arrays: the lanes
+// run the code that fills the lists with the same data, so one copy serves the match. Each list is
+// cleared where its use begins; none is live across a call that uses the same list.
 struct Scratch {
+    CommandQueue commands;
+    ForceField forceField;
+    PlayerBounceList bounces[kPlayers];
+    PlayerGeometryList tackleGeometry[2];
     int16_t lists[3][kMaxAnimations];
     int32_t listCount[3];
     Vec3 plans[2][kAnimPositions];

@@ -44,26 +44,6 @@ HD bool Fail(const char *reason) {
     return false;
 }
 
-// A small inline list (GRF's std::vector uses), capacity fixed.
-template <class T, int N>
-struct Small {
-    int32_t count = 0;
-    T e[N];
-    HD int size() const { return count; }
-    HD bool empty() const { return count == 0; }
-    HD void clear() { count = 0; }
-    HD void push_back(const T &x) {
-        if (count >= N) Fatal("a fixed-capacity list outgrows its capacity");
-        else e[count++] = x;
-    }
-    HD T &operator[](int i) { return e[i]; }
-    HD const T &operator[](int i) const { return e[i]; }
-    HD T *begin() { return e; }
-    HD T *end() { return e + count; }
-    HD const T *begin() const { return e; }
-    HD const T *end() const { return e + count; }
-    HD T &back() { return e[count - 1]; }
-};
 using PlayerList = Small<int, kPlayers>;
 
 // ---- RNG: Boost.Random mt19937 and uniform_real<float> over the world's bytes ---------------------

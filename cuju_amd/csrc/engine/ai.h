@@ -89,13 +89,23 @@ HD bool AllowLastDitchOf(const World &w, int p, bool withPossessionAmount = true
     if (withPossessionAmount && TeamByID(w, w.playerTeamID[p]).teamPossessionAmount < 1.0f) return true;
     return (float)ps.timeToBallOptimisticMs * 1.7f + 800 < (float)ps.timeToBallMs;
 }
+// The mean of the newest min(count, ms / 10 + 1) possession sides, summed newest first. The
+// entries load in batches of 16 (indexes clamped into the history) so that a batch waits for
+// memory once; the additions keep their order.
 HD float AveragePossessionSide(const World &w, unsigned ms) {
     const auto &h = w.match.possessionSideHistory;
+    const unsigned cap = ms / 10 + 1;
+    const int k = (unsigned)h.count < cap ? h.count : (int)cap;
     float total = 0;
-    unsigned k = 0;
-    for (int i = h.count - 1; i >= 0 && k <= ms / 10; i--) {
-        total += h[i];
-        k++;
+    for (int first = 0; first < k; first += 16) {
+        float batch[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) batch[j] = h[h.count - 1 - (first + j < k ? first + j : k - 1)];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            if (first + j >= k) break;
+            total += batch[j];
+        }
     }
     if (k > 0) total /= (float)k;
     return total;
@@ -183,8 +193,13 @@ HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool 
     int role = dynamic ? m.players[p].dynamicFormationEntry.role : Formation(w, c, p).role;
     Vec3 focal = Sp(w, m.designatedPossessionPlayer).position;
     float urgency = 1.0f - NormalizedClamp((focal - Sp(w, p).position).Length(), 2.0f, 30.0f);
-    float ballX = BallAveragePosition(w, TruncToUint32(3500 * (1.0f - urgency * 0.7f))).v[0];
-    float ballY = BallAveragePosition(w, TruncToUint32(4000 * (1.0f - urgency * 0.5f))).v[1];
+    // The four averages of the ball's history this position reads, from one pass over it.
+    const unsigned durations[4] = {TruncToUint32(3500 * (1.0f - urgency * 0.7f)), TruncToUint32(4000 * (1.0f - urgency * 0.5f)),
+                                   3000, 2000};
+    Vec3 averages[4];
+    BallAveragePositions(w, durations, averages);
+    float ballX = averages[0].v[0];
+    float ballY = averages[1].v[1];
     auto T = [&](int id) { return Mixup(PropertiesGetReal(tac, id), id, role); };
     float offDepth = T(kOffenseDepth), defDepth = T(kDefenseDepth);
     float offWidth = T(kOffenseWidth), defWidth = T(kDefenseWidth);
@@ -205,8 +220,7 @@ HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool 
     bbb *= 0.6f;
     float pb = possAmount * (1.0f - bbb) + ballBias * bbb;
     pb = Clamp(pb + (ob - 0.5f) * 0.3f, 0.0f, 1.0f);
-    focal = (BallAveragePosition(w, 3000).Get2D() * 1.0f + focal * 0.0f) * pb +
-            (BallAveragePosition(w, 2000).Get2D() * 0.5f + focal * 0.5f) * (1.0f - pb);
+    focal = (averages[2].Get2D() * 1.0f + focal * 0.0f) * pb + (averages[3].Get2D() * 0.5f + focal * 0.5f) * (1.0f - pb);
     float depth = ai.depth * (offDepth * pb + defDepth * (1.0f - pb));
     float width = ai.width * (offWidth * pb + defWidth * (1.0f - pb));
     float offsetX = kPitchHalfLength * side * ((offOwnHalf * 2.0f - 1.0f) * pb + (defOwnHalf * 2.0f - 1.0f) * (1.0f - pb));

@@ -140,20 +140,61 @@ HDN float GetOffsideLine(const World &w, int k, int teamID, unsigned futureMs = 
     return OffsideLineFromImages(im, MentalBallPrediction(w, k, 0), TeamDynamicSide(w, teamID), futureMs);
 }
 // Mean of the last positions of the ball, newest first, about one entry per 10 ms.
-HDN Vec3 BallAveragePosition(const World &w, unsigned durationMs) {
+// The averages of the ball's last positions over several durations, from one pass: a duration of
+// d ms averages the newest min(count, d / 10 + 1) entries of the history, each mirrored when the
+// ball's frame is, summed newest first; an empty history gives the ball's position. Every average
+// is a prefix of the same running sum, so one pass records each at its length. The entries load
+// in batches of 8 (indexes clamped into the history), so a batch waits for memory once; the
+// additions keep their order.
+template <int N>
+HD void BallAveragePositions(const World &w, const unsigned (&durationsMs)[N], Vec3 (&out)[N]) {
     const Ball &b = w.match.ball;
-    unsigned total = 0;
-    Vec3 avg;
-    for (int i = b.positionHistory.count - 1; i >= 0; i--) {
-        Vec3 p = b.positionHistory[i];
-        if (b.lazyFlip) p.Mirror();
-        avg += p;
-        total++;
-        if (total * 10 > durationMs) break;
+    const int count = b.positionHistory.count;
+    const Vec3 *const history = b.positionHistory.e;
+    const bool flip = b.lazyFlip;
+    // Fully unrolled over the N averages, so the lengths and sums stay in registers.
+    int lengths[N];
+    int longest = 0;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const unsigned cap = durationsMs[i] / 10 + 1;
+        lengths[i] = (unsigned)count < cap ? count : (int)cap;
+        longest = lengths[i] > longest ? lengths[i] : longest;
     }
-    if (total > 0) avg /= Vec3((float)total);
-    else avg = BallPredict(b, 0);
-    return avg;
+    Vec3 sum, sums[N];
+    for (int first = 0; first < longest; first += 8) {
+        Vec3 batch[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = first + j < longest ? first + j : longest - 1;
+            batch[j] = history[count - 1 - k];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (first + j >= longest) break;
+            Vec3 p = batch[j];
+            if (flip) p.Mirror();
+            sum += p;
+#pragma unroll
+            for (int i = 0; i < N; i++)
+                if (lengths[i] == first + j + 1) sums[i] = sum;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        if (lengths[i] > 0) {
+            out[i] = sums[i];
+            out[i] /= Vec3((float)lengths[i]);
+        } else {
+            out[i] = BallPredict(b, 0);
+        }
+    }
+}
+HDN Vec3 BallAveragePosition(const World &w, unsigned durationMs) {
+    const unsigned durations[1] = {durationMs};
+    Vec3 avg[1];
+    BallAveragePositions(w, durations, avg);
+    return avg[0];
 }
 
 // ---- officials ---------------------------------------------------------------------------------------

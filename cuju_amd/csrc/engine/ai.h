@@ -184,7 +184,26 @@ HDN Vec3 GetAdaptedFormationPosition(const World &w, const Ctx &c, int p, float 
     return pos;
 }
 
-HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool dynamic) {
+// What a player's formation position reads of the match's history: four averages of the ball's
+// positions, over durations that shorten as the player nears the possession player, from one pass
+// over the history, and the average possession side over 6 s. A player's static and dynamic
+// formation positions read the same ones.
+struct FormationHistory {
+    Vec3 ball[4];
+    float possessionSide;
+};
+HDN FormationHistory FormationHistoryOf(const World &w, int p) {
+    const Vec3 focal = Sp(w, w.match.designatedPossessionPlayer).position;
+    const float urgency = 1.0f - NormalizedClamp((focal - Sp(w, p).position).Length(), 2.0f, 30.0f);
+    const unsigned durations[4] = {TruncToUint32(3500 * (1.0f - urgency * 0.7f)), TruncToUint32(4000 * (1.0f - urgency * 0.5f)),
+                                   3000, 2000};
+    FormationHistory h;
+    BallAveragePositions(w, durations, h.ball);
+    h.possessionSide = AveragePossessionSide(w, 6000);
+    return h;
+}
+
+HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool dynamic, const FormationHistory &history) {
     const int t = w.playerTeamID[p];
     const int side = TeamDynamicSide(w, t);
     const TeamAI &ai = TeamByID(w, t).ai;
@@ -192,12 +211,7 @@ HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool 
     const MatchState &m = w.match;
     int role = dynamic ? m.players[p].dynamicFormationEntry.role : Formation(w, c, p).role;
     Vec3 focal = Sp(w, m.designatedPossessionPlayer).position;
-    float urgency = 1.0f - NormalizedClamp((focal - Sp(w, p).position).Length(), 2.0f, 30.0f);
-    // The four averages of the ball's history this position reads, from one pass over it.
-    const unsigned durations[4] = {TruncToUint32(3500 * (1.0f - urgency * 0.7f)), TruncToUint32(4000 * (1.0f - urgency * 0.5f)),
-                                   3000, 2000};
-    Vec3 averages[4];
-    BallAveragePositions(w, durations, averages);
+    const Vec3 *const averages = history.ball;
     float ballX = averages[0].v[0];
     float ballY = averages[1].v[1];
     auto T = [&](int id) { return Mixup(PropertiesGetReal(tac, id), id, role); };
@@ -226,7 +240,7 @@ HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool 
     float offsetX = kPitchHalfLength * side * ((offOwnHalf * 2.0f - 1.0f) * pb + (defOwnHalf * 2.0f - 1.0f) * (1.0f - pb));
     float sideS = (offSideS * pb + defSideS * (1.0f - pb));
     float sideFocus = pb * 2.0f - 1.0f;
-    float sideX = 0.2f * sideFocus * -side * kPitchHalfLength + 0.8f * -AveragePossessionSide(w, 6000) * kPitchHalfLength;
+    float sideX = 0.2f * sideFocus * -side * kPitchHalfLength + 0.8f * -history.possessionSide * kPitchHalfLength;
     float centerX = Clamp((ballX * (1.0f - sideS) + sideX * sideS) + offsetX, -kPitchHalfLength, kPitchHalfLength);
     float centerY = Clamp(ballY, -kPitchHalfWidth, kPitchHalfWidth);
     const float fitDepth = 0.95f, fitWidth = 0.9f;
@@ -257,6 +271,9 @@ HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool 
     d.v[0] = Clamp(d.v[0], -kPitchHalfLength, kPitchHalfLength);
     d.v[1] = Clamp(d.v[1], -kPitchHalfWidth, kPitchHalfWidth);
     return d;
+}
+HD Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool dynamic) {
+    return TeamAdaptedFormationPosition(w, c, p, dynamic, FormationHistoryOf(w, p));
 }
 
 // Pulls a position in front of the trap line back into a 4 m band around it.

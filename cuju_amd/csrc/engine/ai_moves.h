@@ -581,8 +581,9 @@ struct AIBase {
         const float attackLow[3] = {0.2f, 0.1f, 0.1f}, attackHigh[3] = {0.9f, 0.7f, 0.6f};
         const float runThreshold[3] = {0.0f, 0.9f, 0.7f};
         const float defensiveBase[3] = {1.9f, 1.5f, 1.3f};
-        Vec3 st = TeamAdaptedFormationPosition(w, c, p, false);
-        Vec3 dy = TeamAdaptedFormationPosition(w, c, p, true);
+        const FormationHistory history = FormationHistoryOf(w, p);
+        Vec3 st = TeamAdaptedFormationPosition(w, c, p, false, history);
+        Vec3 dy = TeamAdaptedFormationPosition(w, c, p, true, history);
         float ad = NormalizedClamp(GetDistance(Pos(), Pos(m.designatedPossessionPlayer)), 15.0f, 20.0f);
         float sb = Curve(staticFactor[kind] * ad, 1.0f);
         Vec3 desired = st * sb + dy * (1.0f - sb);

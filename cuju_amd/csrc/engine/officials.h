@@ -169,6 +169,19 @@ HD void BallAveragePositions(const World &w, const unsigned (&durationsMs)[N], V
             const int k = first + j < longest ? first + j : longest - 1;
             batch[j] = history[count - 1 - k];
         }
+        // Only a batch that holds the end of an average records sums.
+        bool records = false;
+#pragma unroll
+        for (int i = 0; i < N; i++) records |= lengths[i] > first && lengths[i] <= first + 8;
+        if (!records) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                Vec3 p = batch[j];
+                if (flip) p.Mirror();
+                sum += p;
+            }
+            continue;
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             if (first + j >= longest) break;

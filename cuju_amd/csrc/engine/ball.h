@@ -638,20 +638,20 @@ HDN void TeamUpdatePossessionStatistics(World &w, const Ctx &c, int teamID) {
     ENG_SCOPE(16);
     // A player's statistics read only the ball, the opposing team and its own fields, so the lanes
     // of the match take the players in turn.
-    int players[kPlayers], n = 0;
-    for (int p = 0; p < w.match.playerCount; p++)
-        if (w.playerTeamID[p] == teamID && w.match.players[p].base.isActive) players[n++] = p;
-    for (int i = GroupRank(); i < n; i += kGroupLanes) PlayerUpdatePossessionStatistics(w, *c.sd, players[i]);
+    const PlayerList players = TeamActivePlayers(w, teamID);
+    for (int i = GroupRank(); i < players.count; i += kGroupLanes) PlayerUpdatePossessionStatistics(w, *c.sd, players[i]);
     GroupSync();
-    Team &t = TeamByID(w, teamID);
-    t.hasPossession = false;
-    t.timeToBallMs = 100000;
-    for (int p = 0; p < w.match.playerCount; p++) {
-        if (w.playerTeamID[p] != teamID || !w.match.players[p].base.isActive) continue;
-        const Player &ps = w.match.players[p];
-        if (ps.hasPossession) t.hasPossession = true;
-        if ((int)ps.timeToBallMs < t.timeToBallMs) t.timeToBallMs = (int)ps.timeToBallMs;
+    // The team's summary over its active players in state order, kept in registers and stored once.
+    bool hasPossession = false;
+    int timeToBall = 100000;
+    for (int i = 0; i < players.count; i++) {
+        const Player &ps = w.match.players[players[i]];
+        if (ps.hasPossession) hasPossession = true;
+        if ((int)ps.timeToBallMs < timeToBall) timeToBall = (int)ps.timeToBallMs;
     }
+    Team &t = TeamByID(w, teamID);
+    t.hasPossession = hasPossession;
+    t.timeToBallMs = timeToBall;
 }
 
 HDN void BallTouch(World &w, const Ctx &c, const Vec3 &target) {

@@ -156,11 +156,14 @@ HDN int GetClosestPlayer(const World &w, const Ctx &c, int teamID, const Vec3 &p
                          bool onlySelectable = false) {
     float best = 10000;
     int bp = -1;
-    for (int p = 0; p < w.match.playerCount; p++) {
-        if (w.playerTeamID[p] != teamID) continue;
-        if (!w.match.players[p].base.isActive || p == except) continue;
-        float d = (Sp(w, p).position - pos).Length();
-        if (d < best) {
+    const int players = w.match.playerCount;
+    // Every player's tests and position load together, without an early exit; the controller and
+    // formation tests run only for candidates.
+#pragma unroll
+    for (int p = 0; p < kPlayers; p++) {
+        const bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.match.players[p].base.isActive & (p != except);
+        const float d = (Sp(w, p).position - pos).Length();
+        if (in && d < best) {
             if ((!onlyAI || !ExternalControllerActive(w, p)) && (!onlySelectable || Formation(w, c, p).controllable)) {
                 best = d;
                 bp = p;

@@ -92,24 +92,49 @@ HD void PropertiesSet(Tactics &t, int id, float value) {
 }
 
 // The closest active players of a team to `pos`, nearest first, ties in state order.
+// The closest active players of a team to `pos`, nearest first, ties in state order: the first
+// `count` of a stable insertion sort by distance. Every player's tests and position load together
+// (the slots past the match's players are in the arrays; the controller and formation tests, which
+// index other tables, run only for the team's active players), and the sort runs in registers: an
+// insertion lands after the last kept entry it is not nearer than, where the shifting scan stops,
+// NaN distances included. A team holds at most kTeamPlayers players.
 HDN PlayerList GetClosestPlayers(const World &w, const Ctx &c, int teamID, const Vec3 &pos, bool onlyAI, unsigned count = 3,
                                  bool onlySelectable = false) {
-    float dist[kPlayers];
-    int who[kPlayers], n = 0;
-    for (int p = 0; p < w.match.playerCount; p++) {
-        if (w.playerTeamID[p] != teamID || !w.match.players[p].base.isActive) continue;
+    float dist[kTeamPlayers];
+    int who[kTeamPlayers], n = 0;
+    const int players = w.match.playerCount;
+#pragma unroll
+    for (int p = 0; p < kPlayers; p++) {
+        bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.match.players[p].base.isActive;
         const float d = (Sp(w, p).position - pos).Length();
-        if (!((!onlyAI || !ExternalControllerActive(w, p)) && (!onlySelectable || Formation(w, c, p).controllable))) continue;
-        int s = n++;
-        for (; s > 0 && d < dist[s - 1]; s--) {
-            dist[s] = dist[s - 1];
-            who[s] = who[s - 1];
+        if (in && !((!onlyAI || !ExternalControllerActive(w, p)) && (!onlySelectable || Formation(w, c, p).controllable))) in = false;
+        if (!in) continue;
+        if (n >= kTeamPlayers) {
+            Fatal("a team holds more players than a team has");
+            break;
         }
-        dist[s] = d;
-        who[s] = p;
+        int at = 0;
+#pragma unroll
+        for (int s = 0; s < kTeamPlayers; s++)
+            if (s < n && !(d < dist[s])) at = s + 1;
+#pragma unroll
+        for (int s = kTeamPlayers - 1; s > 0; s--)
+            if (s > at && s <= n) {
+                dist[s] = dist[s - 1];
+                who[s] = who[s - 1];
+            }
+#pragma unroll
+        for (int s = 0; s < kTeamPlayers; s++)
+            if (s == at) {
+                dist[s] = d;
+                who[s] = p;
+            }
+        n++;
     }
     PlayerList r;
-    for (unsigned i = 0; i < count && (int)i < n; i++) r.push_back(who[i]);
+#pragma unroll
+    for (int i = 0; i < kTeamPlayers; i++)
+        if ((unsigned)i < count && i < n) r.push_back(who[i]);
     return r;
 }
 HD int TeamGoalie(const World &w, const Ctx &c, int teamID) {
@@ -118,12 +143,15 @@ HD int TeamGoalie(const World &w, const Ctx &c, int teamID) {
     return -1;
 }
 // The active player of a team with the least time to the ball, the first in state order on ties.
+// Every player's tests and time load together, without an early exit.
 HDN int TeamBestPossessionPlayer(const World &w, int teamID) {
     int best = 10000000, bp = -1;
-    for (int p = 0; p < w.match.playerCount; p++) {
-        if (w.playerTeamID[p] != teamID || !w.match.players[p].base.isActive) continue;
-        int t = (int)w.match.players[p].timeToBallMs;
-        if (t < best) {
+    const int players = w.match.playerCount;
+#pragma unroll
+    for (int p = 0; p < kPlayers; p++) {
+        const bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.match.players[p].base.isActive;
+        const int t = (int)w.match.players[p].timeToBallMs;
+        if (in && t < best) {
             best = t;
             bp = p;
         }

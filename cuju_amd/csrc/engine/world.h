@@ -291,10 +291,19 @@ HD PlayerList TeamAllPlayers(const World &w, int teamID) {
         if (w.playerTeamID[p] == teamID) l.push_back(p);
     return l;
 }
+// The active players of a team in state order. Every player's two tests load and combine without
+// an early exit (the slots past the match's players are in the arrays), so the scan waits for
+// memory once rather than once a player; each player is written at the list's end, which moves
+// on when the player belongs.
 HD PlayerList TeamActivePlayers(const World &w, int teamID) {
     PlayerList l;
-    for (int p = 0; p < w.match.playerCount; p++)
-        if (w.playerTeamID[p] == teamID && w.match.players[p].base.isActive) l.push_back(p);
+    const int players = w.match.playerCount;
+#pragma unroll
+    for (int p = 0; p < kPlayers; p++) {
+        const bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.match.players[p].base.isActive;
+        l.e[l.count] = p;
+        l.count += in ? 1 : 0;
+    }
     return l;
 }
 HD int TeamDynamicSide(const World &w, int teamID) { return w.flags.teamSide[teamID]; }

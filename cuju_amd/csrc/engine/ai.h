@@ -53,12 +53,23 @@ HD bool NeedDefendingMovement(int side, const Vec3 &pos, const Vec3 &target) {
     return wide > deep * 0.8f;
 }
 // GRF: a player missing from the mental image gets the image's first entry.
+// The first entry of player `p` is found eight entries at a time: a batch's player numbers load
+// together, and the lowest matching index wins.
 HDN PlayerImage MentalPlayerImage(const World &w, int k, int p) {
     const MentalImage &mi = w.match.mentalImages[k];
     const int age = (int)(w.match.actualTimeMs - (uint64_t)mi.timeStampMs);
-    for (int i = 0; i < mi.players.count; i++) {
-        const PlayerImage &im = mi.players[i];
-        if (im.player != p) continue;
+    const int count = mi.players.count;
+    int found = -1;
+    for (int first = 0; first < count && found < 0; first += 8) {
+        int ids[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) ids[j] = mi.players[first + j < count ? first + j : count - 1].player;
+#pragma unroll
+        for (int j = 7; j >= 0; j--)
+            if (first + j < count && ids[j] == p) found = first + j;
+    }
+    if (found >= 0) {
+        const PlayerImage &im = mi.players[found];
         PlayerImage r = im;
         const SpatialState &s = Sp(w, im.player);
         r.position = im.position + im.movement * (float)age * 0.001f;

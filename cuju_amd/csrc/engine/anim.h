@@ -99,28 +99,25 @@ HD void InterpolatedZ(const Ctx &c, const Anim &a, const NodeAnim &n, int frame,
     ori.Angles(x, y, z);
 }
 
+// The node of a body part comes from the animation's map (each body part has at most one node, so
+// it is the node a scan of the node list finds first).
 HD void GetKeyFrameZ(const Ctx &c, const Anim &a, int bodyPart, int frame, Quat &ori, Vec3 &pos, float &z) {
-    for (int i = 0; i < a.nodeCount; i++) {
-        const NodeAnim &n = c.t->nodes[a.nodeFirst + i];
-        if (n.bodyPart == bodyPart) {
-            InterpolatedZ(c, a, n, frame, ori, pos, z);
-            return;
-        }
+    const int i = a.nodeOfBodyPart[bodyPart];
+    if (i >= 0) {
+        InterpolatedZ(c, a, c.t->nodes[a.nodeFirst + i], frame, ori, pos, z);
+        return;
     }
     float x, y;
     ori.Angles(x, y, z);
 }
 
 HD bool GetKeyFrame(const Ctx &c, const Anim &a, int bodyPart, int frame, Quat &ori, Vec3 &pos) {
-    for (int i = 0; i < a.nodeCount; i++) {
-        const NodeAnim &n = c.t->nodes[a.nodeFirst + i];
-        if (n.bodyPart == bodyPart) {
-            Interpolated(c, a, n, frame, ori, pos);
-            for (int k = 0; k < n.keyCount; k++)
-                if (c.t->keys[n.keyFirst + k].frame == frame) return true;
-            return false;
-        }
-    }
+    const int i = a.nodeOfBodyPart[bodyPart];
+    if (i < 0) return false;
+    const NodeAnim &n = c.t->nodes[a.nodeFirst + i];
+    Interpolated(c, a, n, frame, ori, pos);
+    for (int k = 0; k < n.keyCount; k++)
+        if (c.t->keys[n.keyFirst + k].frame == frame) return true;
     return false;
 }
 

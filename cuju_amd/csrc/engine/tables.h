@@ -212,6 +212,7 @@ struct Anim {
     bool lastDitch, baseAnimation;
     int32_t outgoingSpecialState, incomingRetainState, incomingSpecialState;
     int32_t nodeFirst, nodeCount;
+    int8_t nodeOfBodyPart[kBodyParts];  // the node that moves each body part, -1 for none
     bool hasFootball;
     int32_t footballFirst, footballCount;
     bool hasPositions;

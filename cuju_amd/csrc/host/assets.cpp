@@ -141,12 +141,14 @@ void ParseAnimations(const std::string &bytes, AnimationTables &t, Parsed &p) {
         const int32_t nodes = r.get<int32_t>();
         a.nodeFirst = (int32_t)t.nodes.size();
         a.nodeCount = nodes;
+        for (int b = 0; b < kBodyParts; b++) a.nodeOfBodyPart[b] = -1;
         for (int k = 0; k < nodes; k++) {
             NodeAnim na{};
             na.bodyPart = r.get<int32_t>();
             if (na.bodyPart < 0 || na.bodyPart >= kBodyParts) throw std::runtime_error("bad body part in the animation tables");
             for (int e = a.nodeFirst; e < (int)t.nodes.size(); e++)
                 if (t.nodes[e].bodyPart == na.bodyPart) throw std::runtime_error("an animation repeats a body part");
+            a.nodeOfBodyPart[na.bodyPart] = (int8_t)k;
             const int32_t keys = r.get<int32_t>();
             na.keyFirst = (int32_t)t.keys.size();
             na.keyCount = keys;

@@ -46,12 +46,12 @@ STEADY_WARMUP = 100
 # (each scaled by what the counter reads for a 1 GiB device copy), keyed by (workload,
 # environments, warm-up steps, timed steps): the window of launches the profile averaged.
 MEASURED_TRAFFIC = {
-    (1, 64, 100, 30): (33_352_036 + 40_307_723, 'profiles/step_kernel_5v5_64.md'),
-    (2, 4096, 100, 30): (34_936_595_755 + 24_824_990_430, 'profiles/step_kernel_11v11_4096.md'),
-    (3, 16384, 100, 30): (184_537_801_763 + 69_338_272_677, 'profiles/step_kernel_11v11_hard_16384.md'),
-    (3, 16384, 5, 20): (187_039_946_968 + 70_823_935_540, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
-    (4, 8192, 100, 30): (99_105_319_854 + 50_458_934_296, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
-    (5, 32768, 100, 30): (183_036_486_891 + 69_550_780_869, 'profiles/step_kernel_mixed_32768.md'),
+    (1, 64, 100, 30): (32_176_346 + 20_917_217, 'profiles/step_kernel_5v5_64.md'),
+    (2, 4096, 100, 30): (35_854_802_988 + 22_262_603_616, 'profiles/step_kernel_11v11_4096.md'),
+    (3, 16384, 100, 30): (192_960_602_215 + 65_532_858_741, 'profiles/step_kernel_11v11_hard_16384.md'),
+    (3, 16384, 5, 20): (190_233_894_462 + 66_079_099_342, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
+    (4, 8192, 100, 30): (97_178_541_564 + 47_806_937_893, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
+    (5, 32768, 100, 30): (200_386_916_603 + 65_144_207_928, 'profiles/step_kernel_mixed_32768.md'),
 }
 
 

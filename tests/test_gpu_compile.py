@@ -1,5 +1,6 @@
-"""`torch.compile` traces a step whole, through the `cuju_amd::step` and `cuju_amd::reset_done`
-operators, and gives the outputs of an eager step (tests/test_compile.py of the reference)."""
+"""`torch.compile` traces a step whole, through the `cuju_amd::advance` operator, and gives the
+outputs of an eager step (tests/test_compile.py of the reference); the async step, the torch
+allocator (and closing a batch whose step still runs on a side stream), and the memory estimate."""
 
 import pytest
 import torch
@@ -124,3 +125,32 @@ def test_memory_estimate_is_what_the_batch_reports():
         assert estimate.local_memory_bytes == 0
     finally:
         batch.close()
+
+
+def test_closing_waits_for_a_step_on_a_side_stream():
+    """A batch on the torch allocator hands its blocks back at close(): the steps launched on a side
+    stream have ended by then, so no block returns to the pool while a kernel still writes it."""
+    import cuju_amd
+    batch = cuju_amd.BatchEnvironment('11_vs_11_hard_stochastic_l11_r0', library=PRODUCT, device='cuda:0',
+                                      environment_count=64, allocator='torch', seed=0)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        batch.reset()
+        actions = torch.zeros((64, batch.agents), dtype=torch.int32, device='cuda:0')
+        for _ in range(3):
+            batch.step(actions)
+    batch.close()
+    assert side.query()
+
+
+def test_memory_estimate_of_a_batch_larger_than_the_device_allocates_nothing():
+    """The estimate sizes a batch without allocating it, so a batch that cannot fit still gets its
+    size."""
+    import cuju_amd
+    torch.cuda.synchronize()
+    free_before, total = torch.cuda.mem_get_info()
+    count = int(total // 480_000) + 1024
+    estimate = cuju_amd.memory_estimate('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=count)
+    free_after, _ = torch.cuda.mem_get_info()
+    assert estimate > total
+    assert free_after == free_before

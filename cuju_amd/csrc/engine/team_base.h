@@ -91,7 +91,6 @@ HD void PropertiesSet(Tactics &t, int id, float value) {
     t.value[id] = RoundTripSixDecimals(value);
 }
 
-// The closest active players of a team to `pos`, nearest first, ties in state order.
 // The closest active players of a team to `pos`, nearest first, ties in state order: the first
 // `count` of a stable insertion sort by distance. Every player's tests and position load together
 // (the slots past the match's players are in the arrays; the controller and formation tests, which

@@ -180,29 +180,37 @@ struct ApplyPlan {
     float beginBias;
 };
 
-// Each node takes the last history entry of its body part or appends one, in node order.
-HD void ApplyPrepare(const Ctx &c, const Anim &a, Humanoid &h, bool smooth, int frame, ApplyPlan &plan) {
+// Each node takes the last history entry of its body part or appends one, in node order. Only
+// with `append` are the new entries written; without it the plan is the same, for lanes that share
+// the humanoid with one that appends.
+HD void ApplyPrepare(const Ctx &c, const Anim &a, Humanoid &h, bool smooth, int frame, ApplyPlan &plan,
+                     bool append = true) {
     plan.beginBias = smooth ? SmoothBeginBias(frame) : 0.0f;
     if (a.nodeCount > kBodyParts) Fatal("an animation moves more body parts than a humanoid has");
     if (!smooth) return;
     auto &hist = h.movementHistory;
     int16_t last[kBodyParts];
     for (int b = 0; b < kBodyParts; b++) last[b] = -1;
-    for (int i = 0; i < hist.count; i++) {
+    const int entries = hist.count;
+    for (int i = 0; i < entries; i++) {
         int32_t b = hist[i].nodeName;
         if (b >= 0 && b < kBodyParts) last[b] = (int16_t)i;
     }
+    int count = entries;
     for (int n = 0; n < a.nodeCount; n++) {
         int bp = c.t->nodes[a.nodeFirst + n].bodyPart;
         int found = last[bp];
         plan.isNew[n] = found < 0;
         if (found < 0) {
-            MovementHistoryEntry e;
-            memset(&e, 0, sizeof(e));
-            e.nodeName = bp;
-            e.timeDifferenceMs = 10;
-            hist.push_back(e);
-            found = hist.count - 1;
+            if (append) {
+                MovementHistoryEntry e;
+                memset(&e, 0, sizeof(e));
+                e.nodeName = bp;
+                e.timeDifferenceMs = 10;
+                hist.push_back(e);
+            }
+            // A full history keeps its count (the append fails), and the node takes its last entry.
+            found = count < hist.kCapacity ? count++ : count - 1;
         }
         plan.entry[n] = (int16_t)found;
     }
@@ -333,14 +341,30 @@ HDN void ApplyNode(const Ctx &c, const Anim &a, const Skeleton &sk, Humanoid &h,
 // Applies every humanoid's buffered frame; humanoids are independent.
 HDN void FetchPutBuffers(const Ctx &c, const Skeleton *const *skels, Humanoid *const *hums, int count) {
     // A humanoid's pose reads and writes only its own state, so the lanes of the match take the
-    // humanoids in turn.
-    for (int k = GroupRank(); k < count; k += kGroupLanes) {
+    // humanoids in turn. A node reads and writes only its own body part's node, offset and history
+    // entry, so the humanoids left over after the whole rounds have their nodes split over the lanes
+    // instead, when that at least halves the rounds those humanoids take.
+    constexpr int kNodeRounds = (kBodyParts + kGroupLanes - 1) / kGroupLanes;
+    int whole = count;
+    if (2 * (count % kGroupLanes) * kNodeRounds <= kBodyParts) whole = count - count % kGroupLanes;
+    for (int k = GroupRank(); k < whole; k += kGroupLanes) {
         Humanoid &h = *hums[k];
         AnimApplyBuffer &buf = h.applyBuf;
         const Anim &a = c.A(buf.anim);
         ApplyPlan plan;
         ApplyPrepare(c, a, h, buf.smooth, buf.frameNum, plan);
         for (int n = 0; n < a.nodeCount; n++)
+            ApplyNode(c, a, *skels[k], h, n, buf.frameNum, buf.smooth, buf.smoothFactor, buf.position,
+                      buf.orientation.value(), buf.offsets, 10, buf.noPos, plan);
+    }
+    for (int k = whole; k < count; k++) {
+        Humanoid &h = *hums[k];
+        AnimApplyBuffer &buf = h.applyBuf;
+        const Anim &a = c.A(buf.anim);
+        ApplyPlan plan;
+        ApplyPrepare(c, a, h, buf.smooth, buf.frameNum, plan, GroupRank() == 0);
+        GroupSync();
+        for (int n = GroupRank(); n < a.nodeCount; n += kGroupLanes)
             ApplyNode(c, a, *skels[k], h, n, buf.frameNum, buf.smooth, buf.smoothFactor, buf.position,
                       buf.orientation.value(), buf.offsets, 10, buf.noPos, plan);
     }

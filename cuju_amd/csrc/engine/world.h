@@ -298,12 +298,14 @@ HD PlayerList TeamAllPlayers(const World &w, int teamID) {
 HD PlayerList TeamActivePlayers(const World &w, int teamID) {
     PlayerList l;
     const int players = w.match.playerCount;
+    int count = 0;
 #pragma unroll
     for (int p = 0; p < kPlayers; p++) {
         const bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.match.players[p].base.isActive;
-        l.e[l.count] = p;
-        l.count += in ? 1 : 0;
+        l.e[count] = p;
+        count += in ? 1 : 0;
     }
+    l.count = count;
     return l;
 }
 HD int TeamDynamicSide(const World &w, int teamID) { return w.flags.teamSide[teamID]; }

@@ -69,7 +69,7 @@ HDN PlayerImage MentalPlayerImage(const World &w, int k, int p) {
             if (first + j < count && ids[j] == p) found = first + j;
     }
     if (found >= 0) {
-        const PlayerImage &im = mi.players[found];
+        const PlayerImage im = MentalImageEntry(w, mi, found);
         PlayerImage r = im;
         const SpatialState &s = Sp(w, im.player);
         r.position = im.position + im.movement * (float)age * 0.001f;
@@ -77,7 +77,7 @@ HDN PlayerImage MentalPlayerImage(const World &w, int k, int p) {
         r.movement = r.movement.EnforceMaximumDeviation(s.movement, mi.maxMovementDeviation);
         return r;
     }
-    return mi.players[0];
+    return count > 0 ? MentalImageEntry(w, mi, 0) : mi.players[0];
 }
 HDN float PlayerAverageVelocity(const World &w, int p, float periodS) {
     const auto &hist = w.match.players[p].base.positionHistoryPerSecond;

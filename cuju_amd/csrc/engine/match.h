@@ -131,15 +131,16 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
     if (!TeamProcess(w, c, first)) return ok = false;
     MirrorMatch(w, true, true, true);
     if (!TeamProcess(w, c, second)) return ok = false;
-    MirrorMatch(w, first == 0, first == 1, first == 0);
-    MirrorMatch(w, rev, !rev, rev);
+    // Two frame changes in a row make one: each mirror is its own inverse on disjoint state, so a
+    // flag of the pair is the exclusive or of the two.
+    MirrorMatch(w, (first == 0) != rev, (first == 1) != !rev, (first == 0) != rev);
     if (!OfficialsProcess(w, c)) return ok = false;
-    MirrorMatch(w, rev, !rev, rev);
-    MirrorMatch(w, first == 1, first == 0, first == 1);
+    MirrorMatch(w, rev != (first == 1), !rev != (first == 0), rev != (first == 1));
     TeamUpdatePossessionStatistics(w, c, first);
     MirrorMatch(w, true, true, true);
     TeamUpdatePossessionStatistics(w, c, second);
-    MirrorMatch(w, first == 0, first == 1, first == 0);
+    // The possession choice reads times and IDs only, so the frame change back from the second
+    // team's frame joins the one before the humanoid collisions.
     CalculateBestPossessionTeamID(w);
     if (m.ballRetainer == -1) {
         if (m.bestPossessionTeam != -1) {
@@ -156,7 +157,7 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
     } else {
         m.designatedPossessionPlayer = m.ballRetainer;
     }
-    MirrorMatch(w, rev, !rev, rev);
+    MirrorMatch(w, (first == 0) != rev, (first == 1) != !rev, (first == 0) != rev);
     if (!CheckHumanoidCollisions(w, c)) return ok = false;
     BumpActualTime(w, c, 10);
     bool g1 = false, g2 = false;

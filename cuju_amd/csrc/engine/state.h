@@ -300,6 +300,8 @@ struct MentalImage {
     List<PlayerImage, kPlayers> players;
     List<Vec3, 320> ballPredictions;
     bool lazyFlip;  // not in the state: the predictions hold negated x and y
+    // Not in the state: the player images of team t hold negated x and y when lazyTeamFlip[t].
+    bool lazyTeamFlip[2];
 };
 
 struct Ball {

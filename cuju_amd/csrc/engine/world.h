@@ -144,13 +144,24 @@ HDN void MirrorHumanoid(Humanoid &h, bool &mirrored) {
     h.decayingPositionOffset.Mirror();
 }
 
-// Each humanoid mirrors on its own, so the lanes of the match take the players in turn; the caller
-// synchronizes the group before the mirrored state is read.
-HD void MirrorTeam(World &w, int teamID) {
-    w.flags.teamSide[teamID] *= -1;
-    w.flags.teamMirrored[teamID] = !w.flags.teamMirrored[teamID];
-    for (int p = GroupRank(); p < w.match.playerCount; p += kGroupLanes)
-        if (w.playerTeamID[p] == teamID) MirrorHumanoid(w.match.players[p].base.humanoid, w.flags.humanoidMirrored[p]);
+// The first-processed team's players come first in the player array, the other team's after them.
+HD int FirstTeamSize(const World &w) {
+    return w.FirstTeamID() == 0 ? w.scenario.leftTeamSize : w.scenario.rightTeamSize;
+}
+// Mirrors the humanoids of the flagged teams (by team ID). Their players form one range of the
+// player array, and each humanoid mirrors on its own, so the lanes of the match take the range's
+// players in turn; the caller synchronizes the group before the mirrored state is read.
+HD void MirrorTeams(World &w, bool t0, bool t1) {
+    for (int t = 0; t < 2; t++)
+        if (t == 0 ? t0 : t1) {
+            w.flags.teamSide[t] *= -1;
+            w.flags.teamMirrored[t] = !w.flags.teamMirrored[t];
+        }
+    const bool firstFlagged = w.FirstTeamID() == 0 ? t0 : t1, secondFlagged = w.FirstTeamID() == 0 ? t1 : t0;
+    const int split = FirstTeamSize(w);
+    const int lo = firstFlagged ? 0 : split, hi = secondFlagged ? w.match.playerCount : split;
+    for (int p = lo + GroupRank(); p < hi; p += kGroupLanes)
+        MirrorHumanoid(w.match.players[p].base.humanoid, w.flags.humanoidMirrored[p]);
 }
 
 // Prediction and history arrays mirror lazily: `lazyFlip` says they hold negated x and y.
@@ -181,23 +192,30 @@ HD void BallMaterialize(Ball &b) {
     GroupSync();
     b.lazyFlip = false;
 }
-HD void MentalMaterialize(MentalImage &m) {
-    if (!m.lazyFlip) return;
-    for (int i = 0; i < m.ballPredictions.count; i++) m.ballPredictions[i].Mirror();
+// Entry `i` (below the count) of a mental image's players, its team's lazy mirror applied.
+HD PlayerImage MentalImageEntry(const World &w, const MentalImage &m, int i) {
+    PlayerImage p = m.players[i];
+    if (m.lazyTeamFlip[w.playerTeamID[p.player]]) {
+        p.position.Mirror();
+        p.directionVector.Mirror();
+        p.movement.Mirror();
+    }
+    return p;
+}
+// Applies an image's lazy mirrors to its stored predictions and player images.
+HD void MentalMaterialize(const World &w, MentalImage &m) {
+    if (m.lazyFlip)
+        for (int i = 0; i < m.ballPredictions.count; i++) m.ballPredictions[i].Mirror();
     m.lazyFlip = false;
+    for (int i = 0; i < m.players.count; i++) m.players[i] = MentalImageEntry(w, m, i);
+    m.lazyTeamFlip[0] = m.lazyTeamFlip[1] = false;
 }
 
+// Player images mirror lazily per team, the ball's predictions lazily as a whole.
 HD void MirrorMentalImage(World &w, int k, bool t0, bool t1, bool ball) {
     MentalImage &m = w.match.mentalImages[k];
-    for (int i = GroupRank(); i < m.players.count; i += kGroupLanes) {
-        PlayerImage &p = m.players[i];
-        int team = w.playerTeamID[p.player];
-        if (team == 0 ? t0 : t1) {
-            p.position.Mirror();
-            p.directionVector.Mirror();
-            p.movement.Mirror();
-        }
-    }
+    m.lazyTeamFlip[0] ^= t0;
+    m.lazyTeamFlip[1] ^= t1;
     if (ball) {
         m.lazyFlip = !m.lazyFlip;
         w.flags.mentalBallMirrored[k] = !w.flags.mentalBallMirrored[k];
@@ -206,8 +224,11 @@ HD void MirrorMentalImage(World &w, int k, bool t0, bool t1, bool ball) {
 
 HDN void MirrorMatch(World &w, bool t0, bool t1, bool ball) {
     ENG_SCOPE(18);
-    if (t0) MirrorTeam(w, 0);
-    if (t1) MirrorTeam(w, 1);
+    if (!t0 && !t1 && !ball) {
+        GroupSync();
+        return;
+    }
+    MirrorTeams(w, t0, t1);
     if (ball) {
         w.flags.ballMirrored = !w.flags.ballMirrored;
         MirrorBall(w.match.ball);
@@ -279,8 +300,7 @@ HD int GlobalGamerIndex(const World &w, int teamID, int gamer) {
 }
 
 HD void InitializePlayerTeams(World &w) {
-    int first = w.FirstTeamID();
-    int firstSize = first == 0 ? w.scenario.leftTeamSize : w.scenario.rightTeamSize;
+    const int first = w.FirstTeamID(), firstSize = FirstTeamSize(w);
     for (int p = 0; p < w.match.playerCount; p++) w.playerTeamID[p] = p < firstSize ? first : 1 - first;
     for (int p = 0; p < kPlayers; p++) w.formationOverride[p] = 0;
 }

@@ -548,7 +548,7 @@ bool StateCodec::Load(const std::string &bytes, World &w) {
 }
 std::string StateCodec::Save(World &w, std::vector<codec::SchemaEntry> *schema) {
     BallMaterialize(w.match.ball);
-    for (int i = 0; i < w.match.mentalImages.count; i++) MentalMaterialize(w.match.mentalImages[i]);
+    for (int i = 0; i < w.match.mentalImages.count; i++) MentalMaterialize(w, w.match.mentalImages[i]);
     codec::Archive a(nullptr);
     a.schema = schema;
     codec::VWorld(a, w, freeControllerCount);

@@ -10,8 +10,11 @@
 
 namespace eng {
 
-// Slot 0 holds the newest of at most three mental images.
-HDN void PushMentalImage(World &w) {
+// Slot 0 holds the newest of at most three mental images. The images hold what a frame change
+// mirrors, so a team that the current frame holds mirrored from the rest frame (`mirrored`, by
+// team ID) stores its direction negated too: a frame change negates a humanoid's position and
+// movement but leaves its direction alone.
+HDN void PushMentalImage(World &w, const bool (&mirrored)[2]) {
     ENG_SCOPE(8);
     MatchState &m = w.match;
     const int n = m.mentalImages.count < 3 ? m.mentalImages.count + 1 : 3;
@@ -32,6 +35,7 @@ HDN void PushMentalImage(World &w) {
             im.player = ps[i];
             im.position = s.position;
             im.directionVector = s.directionVec;
+            if (mirrored[w.playerTeamID[ps[i]]]) im.directionVector.Mirror();
             im.velocity = s.velocityCat;
             im.movement = s.movement;
             im.role = m.players[ps[i]].dynamicFormationEntry.role;
@@ -116,18 +120,24 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
     if (m.inPlay && !CheckBallCollisions(w, c)) return ok = false;
     if (!RefereeProcess(w, c)) return ok = false;
     Vec3 prevBall = BallPredict(m.ball, 0);
-    MirrorMatch(w, rev, !rev, rev);
     if (!m.inPlay && m.referee.buffer.prepareTime + 10 < m.actualTimeMs) {
+        MirrorMatch(w, rev, !rev, rev);
         BumpActualTime(w, c, 10);
         return false;
     }
-    MirrorMatch(w, false, false, rev);
+    // GRF returns to the rest frame here, moves the ball alone for its flight, pushes the mental
+    // image and updates the switches. The collision frame already holds the ball where the flight
+    // expects it; the image takes the collision frame's players, their directions mirrored like
+    // their positions (PushMentalImage); and the switches read times, IDs and controllers only. So
+    // the three run in the collision frame, and one frame change leads to the first team's.
     BallProcess(m.ball, m.ballIsInGoal);
-    MirrorMatch(w, false, false, rev);
-    if (m.mentalImages.count == 0 || m.actualTimeMs % 100 == 0) PushMentalImage(w);
+    if (m.mentalImages.count == 0 || m.actualTimeMs % 100 == 0) {
+        const bool mirrored[2] = {rev, !rev};
+        PushMentalImage(w, mirrored);
+    }
     if (!TeamUpdateSwitch(w, c, first)) return ok = false;
     if (!TeamUpdateSwitch(w, c, second)) return ok = false;
-    MirrorMatch(w, first == 1, first == 0, first == 1);
+    MirrorMatch(w, rev != (first == 1), !rev != (first == 0), rev != (first == 1));
     if (!TeamProcess(w, c, first)) return ok = false;
     MirrorMatch(w, true, true, true);
     if (!TeamProcess(w, c, second)) return ok = false;
@@ -135,29 +145,42 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
     // flag of the pair is the exclusive or of the two.
     MirrorMatch(w, (first == 0) != rev, (first == 1) != !rev, (first == 0) != rev);
     if (!OfficialsProcess(w, c)) return ok = false;
-    MirrorMatch(w, rev != (first == 1), !rev != (first == 0), rev != (first == 1));
-    TeamUpdatePossessionStatistics(w, c, first);
-    MirrorMatch(w, true, true, true);
-    TeamUpdatePossessionStatistics(w, c, second);
-    // The possession choice reads times and IDs only, so the frame change back from the second
-    // team's frame joins the one before the humanoid collisions.
-    CalculateBestPossessionTeamID(w);
-    if (m.ballRetainer == -1) {
-        if (m.bestPossessionTeam != -1) {
-            const int bt = m.bestPossessionTeam == 0 ? first : second;
-            int cand = TeamByID(w, bt).designatedTeamPossessionPlayer;
-            if (cand != m.designatedPossessionPlayer) {
-                uint32_t dt = m.players[m.designatedPossessionPlayer].timeToBallMs;
-                uint32_t ct = m.players[cand].timeToBallMs;
-                if ((float)(ct + 10) / (float)(dt + 10) < 0.85f) m.designatedPossessionPlayer = cand;
+    // A team's possession statistics read its own players and the ball, and other teams' times
+    // only. Each runs with its team and the ball where GRF has them (the team in its own frame, the
+    // ball in that team's), leaving the other team where it is, which takes two team mirrors
+    // fewer than moving the whole match.
+    {
+        bool m0 = rev, m1 = !rev, mb = rev;  // the collision frame, relative to the rest frame
+        auto frame = [&](bool t0, bool t1, bool ball) {
+            MirrorMatch(w, m0 != t0, m1 != t1, mb != ball);
+            m0 = t0;
+            m1 = t1;
+            mb = ball;
+        };
+        frame(first == 0 ? false : m0, first == 1 ? false : m1, first == 1);
+        TeamUpdatePossessionStatistics(w, c, first);
+        frame(second == 0 ? false : m0, second == 1 ? false : m1, second == 1);
+        TeamUpdatePossessionStatistics(w, c, second);
+        // The possession choice reads times and IDs only, so the return to the collision frame
+        // waits for it.
+        CalculateBestPossessionTeamID(w);
+        if (m.ballRetainer == -1) {
+            if (m.bestPossessionTeam != -1) {
+                const int bt = m.bestPossessionTeam == 0 ? first : second;
+                int cand = TeamByID(w, bt).designatedTeamPossessionPlayer;
+                if (cand != m.designatedPossessionPlayer) {
+                    uint32_t dt = m.players[m.designatedPossessionPlayer].timeToBallMs;
+                    uint32_t ct = m.players[cand].timeToBallMs;
+                    if ((float)(ct + 10) / (float)(dt + 10) < 0.85f) m.designatedPossessionPlayer = cand;
+                }
+            } else {
+                m.designatedPossessionPlayer = TeamByID(w, w.playerTeamID[m.designatedPossessionPlayer]).designatedTeamPossessionPlayer;
             }
         } else {
-            m.designatedPossessionPlayer = TeamByID(w, w.playerTeamID[m.designatedPossessionPlayer]).designatedTeamPossessionPlayer;
+            m.designatedPossessionPlayer = m.ballRetainer;
         }
-    } else {
-        m.designatedPossessionPlayer = m.ballRetainer;
+        frame(rev, !rev, rev);
     }
-    MirrorMatch(w, (first == 0) != rev, (first == 1) != !rev, (first == 0) != rev);
     if (!CheckHumanoidCollisions(w, c)) return ok = false;
     BumpActualTime(w, c, 10);
     bool g1 = false, g2 = false;

@@ -46,12 +46,12 @@ STEADY_WARMUP = 100
 # (each scaled by what the counter reads for a 1 GiB device copy), keyed by (workload,
 # environments, warm-up steps, timed steps): the window of launches the profile averaged.
 MEASURED_TRAFFIC = {
-    (1, 64, 100, 30): (32_070_365 + 20_852_515, 'profiles/step_kernel_5v5_64.md'),
-    (2, 4096, 100, 30): (31_540_886_504 + 20_502_032_694, 'profiles/step_kernel_11v11_4096.md'),
-    (3, 16384, 100, 30): (172_485_211_010 + 59_862_352_334, 'profiles/step_kernel_11v11_hard_16384.md'),
-    (3, 16384, 5, 20): (169_134_578_136 + 60_421_896_914, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
-    (4, 8192, 100, 30): (86_691_737_027 + 45_138_324_785, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
-    (5, 32768, 100, 30): (180_713_776_746 + 59_573_900_107, 'profiles/step_kernel_mixed_32768.md'),
+    (1, 64, 100, 30): (32_089_784 + 21_041_280, 'profiles/step_kernel_5v5_64.md'),
+    (2, 4096, 100, 30): (30_384_280_765 + 19_816_283_962, 'profiles/step_kernel_11v11_4096.md'),
+    (3, 16384, 100, 30): (166_511_157_054 + 57_339_453_066, 'profiles/step_kernel_11v11_hard_16384.md'),
+    (3, 16384, 5, 20): (163_100_588_575 + 57_903_079_374, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
+    (4, 8192, 100, 30): (83_858_483_976 + 43_813_706_133, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
+    (5, 32768, 100, 30): (173_930_563_037 + 56_983_406_873, 'profiles/step_kernel_mixed_32768.md'),
 }
 
 

@@ -10,7 +10,9 @@ clones what it keeps.
 from __future__ import annotations
 
 import ctypes
+import importlib
 import io
+import logging
 import os
 import pickle
 import re
@@ -34,6 +36,20 @@ SMM_HEIGHT, SMM_WIDTH = 72, 96
 ACTION_SETS = {'default': 0, 'v2': 1, 'full': 2}
 ACTION_COUNTS = {'default': 19, 'v2': 20, 'full': 33}
 MAXIMUM_AGENTS = 22
+_LOGGER = logging.getLogger('cuju_amd')
+
+
+def _spaces():
+    """gymnasium's spaces, or gym's without it, and that package's `batch_space`
+    (python/cuju/_batch/environment.py:153-164)."""
+    try:
+        import gymnasium as gym
+    except ImportError:
+        try:
+            import gym
+        except ImportError:
+            raise ModuleNotFoundError('expected gymnasium or gym for the spaces of a batch') from None
+    return gym.spaces, importlib.import_module(gym.__name__ + '.vector.utils').batch_space
 
 
 def resolve_assets(name: str) -> tuple[str, tuple[int, int]]:
@@ -171,6 +187,9 @@ class BatchEnvironment:
         # threads, pin_threads, numa and pin_memory shape the reference's CPU batches; a device batch
         # takes them and has no use for them, as the reference's GPU batch does.
         del threads, pin_threads, numa, pin_memory
+        # Step observers (python/cuju/_batch/environment.py:722-815); a closing batch calls no more.
+        self._observers = ()
+        self._closing = False
         # GRF's `channel_dimensions`: the SMM's width and height.
         if (not isinstance(channel_dimensions, (tuple, list)) or len(channel_dimensions) != 2
                 or not all(isinstance(v, int) and v >= 1 for v in channel_dimensions)):
@@ -201,6 +220,7 @@ class BatchEnvironment:
         if lib.cuju_backend().decode() != 'cuda':
             raise ConfigurationError('expected the HIP library')
         names = [assets] if isinstance(assets, str) else list(assets)
+        self._requested = names
         resolved = [resolve_assets(n) for n in names]
         # A scenario file becomes an agentless bundle, built with this batch's animation tables;
         # the library reads bundles at creation only, so a temporary one goes with the batch.
@@ -347,6 +367,112 @@ class BatchEnvironment:
             raise ClosedError('the batch is closed')
         return self._native.handle
 
+    @property
+    def scenario_name(self) -> str:
+        """The scenarios the batch was created with, by name without folders or the `.cjb` and
+        `.py` suffixes, each once, joined by commas (python/cuju/_batch/environment.py:710-721)."""
+        names = []
+        for asset in self._requested:
+            name = os.path.basename(os.fspath(asset))
+            for suffix in ('.cjb', '.py'):
+                if name.endswith(suffix):
+                    name = name[:-len(suffix)]
+            if name not in names:
+                names.append(name)
+        return ', '.join(names)
+
+    # ---- step observers (python/cuju/_batch/environment.py:722-815) ----
+    @property
+    def observers(self) -> tuple:
+        """The step observers of the batch, in the order they are called."""
+        return self._observers
+
+    def add_observer(self, observer: Any) -> Any:
+        """Calls `observer(batch, done, information)` after every reset and step, and when the batch
+        closes. After `step` and `step_wait`, `done` is the step's done flags and `information` the
+        step's dictionary with its rewards under `reward`. After `reset` and `reset_done`, `done` is
+        None and `information['reset']` the environments that started an episode, or None for all
+        of them. At `close`, `information` is `{'close': True}`. An observer that raises an
+        `Exception` is removed with a warning on the `cuju_amd` logger. A step or reset captured in
+        a HIP graph or traced by `torch.compile` calls none. Returns the observer."""
+        self._handle()
+        if self._closing:
+            raise ClosedError('the batch is closing')
+        if not callable(observer):
+            raise ArgumentError(f'expected a callable observer, found {observer!r}')
+        if any(added is observer for added in self._observers):
+            raise ArgumentError(f'expected an observer that was not added yet, found {observer!r}')
+        self._observers = (*self._observers, observer)
+        return observer
+
+    def remove_observer(self, observer: Any) -> None:
+        """Stops calling an observer; once `close` begins there is none to remove."""
+        if not self._discard_observer(observer) and not self._closing:
+            raise ArgumentError(f'expected an observer of the batch, found {observer!r}')
+
+    def _discard_observer(self, observer) -> bool:
+        kept = tuple(added for added in self._observers if added is not observer)
+        found = len(kept) != len(self._observers)
+        self._observers = kept
+        return found
+
+    def _capturing(self) -> bool:
+        with torch.cuda.device(self._torch_device):
+            return torch.cuda.is_current_stream_capturing()
+
+    def _call_observers(self, done, information) -> None:
+        for observer in self._observers:
+            # An observer may remove another, which then misses the call.
+            if not any(added is observer for added in self._observers):
+                continue
+            try:
+                observer(self, done, information)
+            except Exception as error:
+                self._discard_observer(observer)
+                _LOGGER.warning('cuju_amd: removed the step observer %r, which raised %s: %s', observer,
+                                type(error).__name__, error)
+
+    def _notify(self, done, information) -> None:
+        if not self._observers or self._capturing():
+            return
+        self._call_observers(done, information)
+        # An observer that closed the batch freed the buffers the outputs view.
+        if self._closing:
+            raise ClosedError('an observer closed the batch during the call')
+
+    # ---- gym spaces (python/cuju/_batch/environment.py:1228-1266) ----
+    @property
+    def single_observation_space(self) -> Any:
+        """One environment's observation space, as GRF's for the same options; None for `raw`.
+        The spaces need gymnasium or gym."""
+        if self.representation == 'raw':
+            return None
+        spaces, _ = _spaces()
+        shape = tuple(self._view(self._observation).shape[1:])
+        if self.representation == 'extracted':
+            return spaces.Box(low=0, high=255, shape=shape, dtype=np.uint8)
+        return spaces.Box(low=-np.inf, high=np.inf, shape=shape, dtype=np.float32)
+
+    @property
+    def single_action_space(self) -> Any:
+        """One environment's action space: `Discrete` for a squeezed single agent, `MultiDiscrete`
+        over the agents otherwise."""
+        spaces, _ = _spaces()
+        if self.squeeze and self.agents == 1:
+            return spaces.Discrete(self.action_count)
+        return spaces.MultiDiscrete([self.action_count] * self.agents)
+
+    @property
+    def observation_space(self) -> Any:
+        """`single_observation_space` for each environment; None for `raw`."""
+        single = self.single_observation_space
+        return None if single is None else _spaces()[1](single, self.environment_count)
+
+    @property
+    def action_space(self) -> Any:
+        """`single_action_space` for each environment."""
+        return _spaces()[1](self.single_action_space, self.environment_count)
+
     def _check(self, status):
         if status == -2:
             raise ActionRangeError(self._lib.cuju_last_error().decode())
@@ -388,6 +514,13 @@ class BatchEnvironment:
             raise ConfigurationError('expected a batch with the raw representation or with_raw')
         return self._raw('raw')
 
+    def final_raw(self) -> dict:
+        """The raw observation of the step that ended each episode, as `raw` returns it
+        (python/cuju/_batch/environment.py:1278-1284)."""
+        if not self._raw_fields:
+            raise ConfigurationError('expected a batch with the raw representation or with_raw')
+        return self._raw('final_raw')
+
     def _stream(self):
         return torch.cuda.current_stream(self._torch_device).cuda_stream
 
@@ -415,10 +548,9 @@ class BatchEnvironment:
             if ((reverse_array != 0) & (reverse_array != 1)).any():
                 raise ArgumentError(f'expected reverse flags of 0 or 1, found {reverse_array.tolist()}')
             reverse_array = np.ascontiguousarray(reverse_array, dtype=np.int32)
+        device_mask = host_mask = None
         with torch.cuda.device(self._torch_device):
             if mask is not None or (seed_array is not None and (seed_array == -1).any()):
-                device_mask = None
-                host_mask = None
                 on_device = 0
                 if mask is not None:
                     if isinstance(mask, torch.Tensor) and mask.device == self._torch_device:
@@ -440,7 +572,13 @@ class BatchEnvironment:
                     self._handle(), None if seeds32 is None else seeds32.ctypes.data,
                     None if reverse_array is None else reverse_array.ctypes.data, self._stream()))
         self._wait_in_debug()
-        return self._outputs()[0]
+        observation = self._outputs()[0]
+        if self._observers:
+            # The environments that started an episode, or None for every one.
+            started = (device_mask.bool() if device_mask is not None
+                       else None if host_mask is None else torch.as_tensor(host_mask).bool())
+            self._notify(None, {'reset': started})
+        return observation
 
     def _integers(self, values, name):
         array = values.cpu().numpy() if isinstance(values, torch.Tensor) else np.asarray(values)
@@ -456,9 +594,13 @@ class BatchEnvironment:
         if torch.compiler.is_compiling():
             self._operator_call(True, torch.empty(0, dtype=torch.int32, device=self._torch_device))
             return
+        # The reset clears the done flags, so the observers receive a copy from before it.
+        ended = self._done.bool() if self._observers and not self._capturing() else None
         with torch.cuda.device(self._torch_device):
             self._check(self._lib.cuju_environment_reset_done(self._handle(), self._stream()))
         self._wait_in_debug()
+        if ended is not None:
+            self._notify(None, {'reset': ended})
 
     # ---- torch.compile: the operator of operators.py (python/cuju/_batch/environment.py:983-1056) ----
     def _operator_outputs(self):
@@ -492,6 +634,12 @@ class BatchEnvironment:
 
     def step(self, actions: Any):
         """Runs one step of every environment on the current stream, without waiting for it."""
+        outputs = self._step(actions)
+        if not torch.compiler.is_compiling() and self._observers:
+            self._notify(outputs[2], {**outputs[3], 'reward': outputs[1]})
+        return outputs
+
+    def _step(self, actions: Any):
         shape = (self.environment_count, self.agents)
         if not isinstance(actions, torch.Tensor):
             actions = torch.as_tensor(actions)
@@ -523,13 +671,17 @@ class BatchEnvironment:
     def step_async(self, actions: Any) -> None:
         """Starts a step of every environment on the current stream and returns at once; on the
         device this is `step` without reading its outputs (python/cuju/_batch/environment.py:1418)."""
-        self._pending = self.step(actions)
+        if self._pending is not None:
+            raise RuntimeError('a step is in flight; call step_wait before the next step_async')
+        self._pending = self._step(actions)
 
     def step_wait(self):
         """The outputs of the step `step_async` started (python/cuju/_batch/environment.py:1466)."""
         if self._pending is None:
             raise ArgumentError('expected a step_async before step_wait')
         outputs, self._pending = self._pending, None
+        if self._observers:
+            self._notify(outputs[2], {**outputs[3], 'reward': outputs[1]})
         return outputs
 
     def synchronize(self) -> None:
@@ -629,7 +781,16 @@ class BatchEnvironment:
         return int(self._lib.cuju_environment_memory_bytes(self._handle()))
 
     def close(self) -> None:
-        self._native.free()
+        """Frees the batch. The observers first receive their close call, in order; a `close` from
+        within one returns at once (python/cuju/_batch/environment.py:840-866)."""
+        if self._closing:
+            return
+        self._closing = True
+        try:
+            self._call_observers(None, {'close': True})
+        finally:
+            self._observers = ()
+            self._native.free()
 
     def __enter__(self):
         return self

@@ -141,7 +141,7 @@ def main():
     print(f'[bench] creating {environments} environments of workload {workload.number}', file=sys.stderr, flush=True)
     env = cuju_amd.BatchEnvironment(assets, device=device, seed=args.seed, **options)
     agents = env.agents
-    present = (env.left_agents + env.right_agents).astype(np.float64)
+    present = (env.left_agents + env.right_agents).numpy().astype(np.float64)
     bytes_per_step = float(np.mean([algorithmic_bytes(workload, a, agents) for a in present]))
     torch.cuda.synchronize()
     start = time.perf_counter()

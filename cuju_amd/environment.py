@@ -300,15 +300,17 @@ class BatchEnvironment:
             raise ConfigurationError(lib.cuju_last_error().decode())
         self._native.handle = handle
         self._lib = lib
-        left = np.zeros(environment_count, dtype=np.int32)
-        right = np.zeros(environment_count, dtype=np.int32)
-        self.agents = lib.cuju_environment_agents(handle, left.ctypes.data, right.ctypes.data)
-        self.left_agents, self.right_agents = left, right
-        pl = np.zeros(environment_count, dtype=np.int32)
-        pr = np.zeros(environment_count, dtype=np.int32)
-        self.players = lib.cuju_environment_players(handle, pl.ctypes.data, pr.ctypes.data)
-        self.agent_mask = torch.as_tensor(
-            np.arange(self.agents)[None, :] < (left + right)[:, None], device=self._torch_device)
+        # Per-environment agents and players of each side, [environment_count] int32 host tensors,
+        # and the agent axis (python/cuju/_batch/environment.py:616-629).
+        self.threads = lib.cuju_environment_threads(handle)
+        self.auto_reset = bool(auto_reset)
+        self.left_agents = torch.zeros(environment_count, dtype=torch.int32)
+        self.right_agents = torch.zeros(environment_count, dtype=torch.int32)
+        self.agents = lib.cuju_environment_agents(handle, self.left_agents.data_ptr(), self.right_agents.data_ptr())
+        self.left_players = torch.zeros(environment_count, dtype=torch.int32)
+        self.right_players = torch.zeros(environment_count, dtype=torch.int32)
+        self.players = lib.cuju_environment_players(handle, self.left_players.data_ptr(), self.right_players.data_ptr())
+        self.agent_mask = torch.arange(self.agents) < (self.left_agents + self.right_agents)[:, None]
         # One (left, right) pair per bundle, None keeping the scenario's; the library takes a
         # negative value for the scenario's (python/cuju/_batch/environment.py:496-507, 640-657).
         bundles = np.zeros(environment_count, dtype=np.int64) if self._assignment is None else self._assignment
@@ -777,7 +779,10 @@ class BatchEnvironment:
             with torch.cuda.device(self._torch_device):
                 self._check(self._lib.cuju_environment_set_stack(self._handle(), index, name, stack, len(stack)))
 
+    @property
     def memory_bytes(self) -> int:
+        """The device bytes the batch has requested, its tables included
+        (python/cuju/_batch/environment.py:884-895)."""
         return int(self._lib.cuju_environment_memory_bytes(self._handle()))
 
     def close(self) -> None:

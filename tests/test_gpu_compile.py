@@ -121,7 +121,7 @@ def test_memory_estimate_is_what_the_batch_reports():
     estimate = cuju_amd.memory_estimate('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=8)
     batch = cuju_amd.BatchEnvironment('5_vs_5_l4_r4', library=PRODUCT, device='cuda:0', environment_count=8)
     try:
-        assert estimate == batch.memory_bytes() > 8 * 373_552
+        assert estimate == batch.memory_bytes > 8 * 373_552
         assert estimate.local_memory_bytes == 0
     finally:
         batch.close()

@@ -5,11 +5,16 @@ CPU engine for the same seeds and actions. The native library is built in-tree b
 `python -m cuju_amd.build`.
 """
 
-from .environment import BatchEnvironment, episode_pickle, memory_estimate, resolve_assets
+from .environment import (BatchEnvironment, bundled_assets, bundled_scenarios, episode_pickle, memory_estimate,
+                          resolve_assets)
+from .library import library_path
 from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, ConfigurationError,
                      DeviceError, EnvironmentIndexError, Error, LibraryError, MissingFileError,
                      StateError, UndefinedPathError)
 
-__all__ = ['BatchEnvironment', 'episode_pickle', 'memory_estimate', 'resolve_assets', 'Error', 'ConfigurationError',
+__version__ = '0.2.0'
+
+__all__ = ['BatchEnvironment', 'bundled_assets', 'bundled_scenarios', 'episode_pickle', 'library_path',
+           'memory_estimate', 'resolve_assets', '__version__', 'Error', 'ConfigurationError',
            'ChoiceError', 'ArgumentError', 'ActionRangeError', 'EnvironmentIndexError', 'StateError',
            'ClosedError', 'DeviceError', 'UndefinedPathError', 'LibraryError', 'MissingFileError']

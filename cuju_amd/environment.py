@@ -52,6 +52,21 @@ def _spaces():
     return gym.spaces, importlib.import_module(gym.__name__ + '.vector.utils').batch_space
 
 
+def bundled_assets() -> list[str]:
+    """The names of the asset bundles the package ships, such as `5_vs_5_l4_r0`
+    (python/cuju/_batch/assets.py:16-25)."""
+    directory = os.path.join(_library.DATA, 'assets')
+    if not os.path.isdir(directory):
+        return []
+    return sorted(name[:-len('.cjb')] for name in os.listdir(directory) if name.endswith('.cjb'))
+
+
+def bundled_scenarios() -> list[str]:
+    """The scenarios of the shipped bundles, such as `5_vs_5` (python/cuju/_batch/assets.py:34-36)."""
+    matches = (re.fullmatch(r'(.+)_l(\d+)_r(\d+)', name) for name in bundled_assets())
+    return sorted({match.group(1) for match in matches if match})
+
+
 def resolve_assets(name: str) -> tuple[str, tuple[int, int]]:
     """`<scenario>_l<L>_r<R>` to a shipped bundle and the agents per side; a path stays a path,
     and a GRF scenario file (`.py`) gets one left agent, as GRF's `create_environment` gives it.

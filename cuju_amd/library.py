@@ -111,6 +111,17 @@ SIGNATURES = [
 _loaded = {}
 
 
+def library_path(device=None) -> str:
+    """The library `BatchEnvironment` loads by default for `device` (python/cuju/_batch/library.py:82-95).
+    This build has one, the HIP library, for `cuda`, `cuda:N`, a `torch.device` of type `cuda`, `auto`
+    or None; another device names no library here."""
+    name = 'cuda' if device is None else str(device)
+    if name != 'auto' and name.split(':')[0] != 'cuda':
+        from .errors import ChoiceError
+        raise ChoiceError(f'expected the device cuda, cuda:N or auto for the HIP library, found {device!r}')
+    return PRODUCT
+
+
 def load(path: str | None = None):
     """The library at `path`, by default the in-tree HIP build, with its signatures declared."""
     path = os.path.abspath(path or PRODUCT)

@@ -7,6 +7,7 @@ CPU engine for the same seeds and actions. The native library is built in-tree b
 
 from .environment import (BatchEnvironment, bundled_assets, bundled_scenarios, episode_pickle, memory_estimate,
                           resolve_assets)
+from .digests import Digest, digest
 from .library import library_path
 from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, ConfigurationError,
                      DeviceError, EnvironmentIndexError, Error, LibraryError, MissingFileError,
@@ -14,7 +15,7 @@ from .errors import (ActionRangeError, ArgumentError, ChoiceError, ClosedError, 
 
 __version__ = '0.2.0'
 
-__all__ = ['BatchEnvironment', 'bundled_assets', 'bundled_scenarios', 'episode_pickle', 'library_path',
+__all__ = ['BatchEnvironment', 'Digest', 'bundled_assets', 'bundled_scenarios', 'digest', 'episode_pickle', 'library_path',
            'memory_estimate', 'resolve_assets', '__version__', 'Error', 'ConfigurationError',
            'ChoiceError', 'ArgumentError', 'ActionRangeError', 'EnvironmentIndexError', 'StateError',
            'ClosedError', 'DeviceError', 'UndefinedPathError', 'LibraryError', 'MissingFileError']

@@ -6,7 +6,8 @@ python/cuju/_batch/environment.py:
   argument errors, and an observer that closes the batch during a step;
 * `scenario_name` (:710-721) and `final_raw` (:1278-1284);
 * the gym spaces (:1228-1266), which need gymnasium or gym: without either they raise
-  `ModuleNotFoundError`; with a stand-in module the shapes, bounds and sizes come through.
+  `ModuleNotFoundError`; with a stand-in module the shapes, bounds and sizes come through;
+* `digest` (python/cuju/action_log.py:104-145) against the shipped self-check digests.
 """
 
 import logging
@@ -209,3 +210,15 @@ def test_spaces(monkeypatch):
     finally:
         batch.close()
         smm.close()
+
+
+@pytest.mark.parametrize('name', ['5_vs_5/raw', '5_vs_5/stacked', '11_vs_11_stochastic/checkpoints',
+                                  'academy_corner/simple115v2'])
+def test_digest_reproduces_the_shipped_case(name, digests):
+    """`cuju_amd.digest` plays the reference self-check's run and gives its shipped SHA-256."""
+    import cuju_amd
+    from conftest import short_cases
+    case = dict(short_cases())[name]
+    got = cuju_amd.digest(case['assets'], device='cuda:0', steps=digests['steps'], seed=digests['seed'],
+                          environment_count=digests['environments'], library=PRODUCT, **dict(case['options']))
+    assert got == case['digest']

@@ -41,3 +41,29 @@ def test_library_path_names_the_hip_library():
     with pytest.raises(ChoiceError):
         cuju_amd.library_path('cpu')
     assert isinstance(cuju_amd.__version__, str) and cuju_amd.__version__
+
+
+def test_digest_hashes_tensors_dictionaries_sequences_and_bytes():
+    import hashlib
+
+    import numpy as np
+
+    from conftest import digest_actions
+    from cuju_amd.digests import digest_actions as package_actions
+
+    a = torch.arange(6, dtype=torch.int32).reshape(2, 3).t()
+    b = torch.tensor([1.5, -0.0], dtype=torch.float32)
+    value = cuju_amd.Digest()
+    value.update(a)
+    value.update({'z': b, 'a': a})
+    value.update([b'xy', (b, a)])
+    fork = value.copy()
+    fork.update(b'more')
+    expected = hashlib.sha256()
+    for part in (a, a, b, b'xy', b, a):
+        expected.update(part if isinstance(part, bytes) else part.contiguous().numpy().tobytes())
+    assert value.hexdigest() == expected.hexdigest() != fork.hexdigest()
+    with pytest.raises(TypeError):
+        value.update(3)
+    for step in (0, 1, 57):
+        assert np.array_equal(package_actions(step, 5, 3, 19).numpy(), digest_actions(step, 5, 3, 19))

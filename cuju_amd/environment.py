@@ -813,10 +813,16 @@ class BatchEnvironment:
             self._native.free()
 
     def __enter__(self):
+        self._handle()
         return self
 
     def __exit__(self, *exception):
         self.close()
+
+    def __reduce__(self):
+        # A batch owns device memory, which no pickle carries to another process
+        # (python/cuju/_batch/environment.py:873-876).
+        raise TypeError('a batch cannot be pickled; create it inside the worker process that uses it')
 
 
 class _Bytes(int):

@@ -67,3 +67,10 @@ def test_digest_hashes_tensors_dictionaries_sequences_and_bytes():
         value.update(3)
     for step in (0, 1, 57):
         assert np.array_equal(package_actions(step, 5, 3, 19).numpy(), digest_actions(step, 5, 3, 19))
+
+
+def test_a_batch_refuses_to_be_pickled():
+    import pickle
+    batch = object.__new__(cuju_amd.BatchEnvironment)
+    with pytest.raises(TypeError):
+        pickle.dumps(batch)

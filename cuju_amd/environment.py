@@ -190,15 +190,16 @@ class _Native:
 class BatchEnvironment:
     """A batch of GRF environments on one HIP device."""
 
+    # The arguments in the reference's order (python/cuju/_batch/environment.py:267-299), so that
+    # positional calls mean the same.
     def __init__(self, assets: str | list[str], animations: str | None = None, environment_count: int = 1024,
                  representation: str = 'simple115v2', rewards: str = 'scoring', action_set: str = 'default',
-                 seed: int = 0, numpy_legacy: bool = True, auto_reset: bool = True, assignment=None,
-                 difficulty=None, device: str | int | torch.device = 'cuda', physics_steps_per_frame: int = 10,
+                 seed: int = 0, numpy_legacy: bool = True, auto_reset: bool = True, library: str | None = None,
+                 assignment=None, with_raw: bool = False, difficulty=None, device: str | int | torch.device = 'cuda',
+                 threads: int = 0, physics_steps_per_frame: int = 10, channel_dimensions=(SMM_WIDTH, SMM_HEIGHT),
                  stacked: bool = False, game_engine_random_seed=None, squeeze: bool = False, agent_counts=None,
-                 episode_number: int = 0, first_index: int = 0, check_actions: bool = False,
-                 with_raw: bool = False, library: str | None = None, threads: int = 0, allocator: str = 'cuda',
-                 pin_threads: bool = False, numa: bool = False, pin_memory: bool = False, debug: bool = False,
-                 channel_dimensions=(SMM_WIDTH, SMM_HEIGHT)):
+                 episode_number: int = 0, first_index: int = 0, allocator: str = 'cuda', pin_threads: bool = False,
+                 numa: bool = False, pin_memory: bool = False, check_actions: bool = False, debug: bool = False):
         # threads, pin_threads, numa and pin_memory shape the reference's CPU batches; a device batch
         # takes them and has no use for them, as the reference's GPU batch does.
         del threads, pin_threads, numa, pin_memory
@@ -262,9 +263,14 @@ class BatchEnvironment:
             if any(v is not None and not 0 <= v <= 1 for p in pairs for v in p):
                 raise ConfigurationError(f"expected difficulties from 0 to 1, or None for the scenario's, found {difficulty!r}")
         if agent_counts is not None:
-            counts = [tuple(c) for c in agent_counts]
-            if len(counts) != len(names):
-                raise ConfigurationError('expected one agent count pair per bundle')
+            # One (left, right) pair per bundle; None keeps what the name or the bundle gives
+            # (python/cuju/_batch/environment.py:477-494).
+            if len(agent_counts) != len(names) or not all(isinstance(p, (tuple, list)) and len(p) == 2
+                                                          for p in agent_counts):
+                raise ConfigurationError(f'expected a (left, right) pair of agent counts for each of the {len(names)} '
+                                         f'bundles, such as [(4, 0)] for one, found {agent_counts!r}')
+            counts = [tuple(named if given is None else given for named, given in zip(pair, given_pair))
+                      for pair, given_pair in zip(counts, agent_counts)]
         self.checkpoints = 'checkpoints' in reward_parts
         self.stack = 4 if stacked else 1
         self.stacked = bool(stacked)
@@ -326,6 +332,9 @@ class BatchEnvironment:
         self.right_players = torch.zeros(environment_count, dtype=torch.int32)
         self.players = lib.cuju_environment_players(handle, self.left_players.data_ptr(), self.right_players.data_ptr())
         self.agent_mask = torch.arange(self.agents) < (self.left_agents + self.right_agents)[:, None]
+        if self.squeeze and not bool(((self.left_agents + self.right_agents) == 1).all()):
+            self.close()
+            raise ConfigurationError('expected one agent in every environment to squeeze the agent axis')
         # One (left, right) pair per bundle, None keeping the scenario's; the library takes a
         # negative value for the scenario's (python/cuju/_batch/environment.py:496-507, 640-657).
         bundles = np.zeros(environment_count, dtype=np.int64) if self._assignment is None else self._assignment

@@ -222,3 +222,18 @@ def test_digest_reproduces_the_shipped_case(name, digests):
     got = cuju_amd.digest(case['assets'], device='cuda:0', steps=digests['steps'], seed=digests['seed'],
                           environment_count=digests['environments'], library=PRODUCT, **dict(case['options']))
     assert got == case['digest']
+
+
+def test_agent_counts_keep_a_side_left_as_none_and_squeeze_needs_one_agent():
+    """python/cuju/_batch/environment.py:477-494 (a None count keeps what the name gives) and
+    :631-635 (squeezing needs one agent in every environment)."""
+    batch = gpu_batch('5_vs_5_l4_r4', environment_count=2, agent_counts=[(2, None)])
+    try:
+        assert batch.left_agents.tolist() == [2, 2] and batch.right_agents.tolist() == [4, 4]
+        assert batch.agent_mask.shape == (2, batch.agents) and batch.agent_mask.sum().item() == 12
+    finally:
+        batch.close()
+    with pytest.raises(ConfigurationError):
+        gpu_batch('5_vs_5_l4_r4', environment_count=2, agent_counts=[(2,)])
+    with pytest.raises(ConfigurationError):
+        gpu_batch('5_vs_5_l4_r4', environment_count=2, squeeze=True)

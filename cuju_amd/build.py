@@ -4,6 +4,10 @@
   ``include/cuju_amd.h``.
 * ``lib/libcuju_amd_host.so``: the same engine and C ABI on host threads, a debugging build that
   tests use to follow a match tick by tick. The package never loads it.
+* ``lib/libcuju_amd_host_sanitized.so``, on request only (``python -m cuju_amd.build --sanitize``):
+  the host build under AddressSanitizer and UndefinedBehaviorSanitizer. The host tests load it
+  in place of the host build when ``CUJU_AMD_HOST_LIBRARY`` names it, with the sanitizer runtimes
+  preloaded into Python (``LD_PRELOAD``).
 
 Every source compiles with IEEE semantics and no contraction of multiply-adds, which the engine's
 bit-exactness needs. ``python -m cuju_amd.build`` runs the same steps.
@@ -27,6 +31,9 @@ CXX = os.environ.get('CXX', 'g++')
 
 PRODUCT = os.path.join(OUT, 'libcuju_amd.so')
 HOST = os.path.join(OUT, 'libcuju_amd_host.so')
+HOST_SANITIZED = os.path.join(OUT, 'libcuju_amd_host_sanitized.so')
+# The sanitized host build: g++ only, so no GPU code is built with a sanitizer.
+SANITIZE = ['-O1', '-g', '-fno-omit-frame-pointer', '-fsanitize=address,undefined', '-fno-sanitize-recover=undefined']
 
 HOST_SOURCES = ['host/assets.cpp', 'host/runtime.cpp', 'host/api.cpp', 'host/scenario.cpp']
 COMMON = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math', '-fvisibility=hidden', '-w']
@@ -95,7 +102,22 @@ def build(host=True, product=True, jobs=8):
     return built
 
 
+def build_sanitized(jobs=8):
+    """Compiles the host build under the sanitizers and returns its path."""
+    os.makedirs(BUILD, exist_ok=True)
+    flags = [f for f in COMMON if f != '-O2'] + SANITIZE
+    sources = HOST_SOURCES + ['host/host_library.cpp']
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        for f in [pool.submit(_run, [CXX, *flags, '-c', os.path.join(SOURCE, s), '-o', _object(s, 's')])
+                  for s in sources]:
+            f.result()
+    _run([CXX, '-shared', '-fPIC', '-fsanitize=address,undefined', '-o', HOST_SANITIZED,
+          *[_object(s, 's') for s in sources], '-lpthread'])
+    shutil.rmtree(BUILD, ignore_errors=True)
+    return HOST_SANITIZED
+
+
 if __name__ == '__main__':
-    for path in build():
+    for path in (build_sanitized(),) if '--sanitize' in sys.argv[1:] else build():
         print(path)
     sys.exit(0)

@@ -15,7 +15,8 @@ sys.path.insert(0, ROOT)
 
 DATA = os.path.join(ROOT, 'cuju_amd', 'data')
 PRODUCT = os.path.join(ROOT, 'cuju_amd', 'lib', 'libcuju_amd.so')
-HOST = os.path.join(ROOT, 'cuju_amd', 'lib', 'libcuju_amd_host.so')
+# CUJU_AMD_HOST_LIBRARY names another host build, such as the sanitized one.
+HOST = os.environ.get('CUJU_AMD_HOST_LIBRARY') or os.path.join(ROOT, 'cuju_amd', 'lib', 'libcuju_amd_host.so')
 REFERENCE = os.path.join(ROOT, 'oracle', '_ref', 'libcuju_cpu.so')
 
 

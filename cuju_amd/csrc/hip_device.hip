@@ -223,12 +223,19 @@ namespace host {
 Scratch *StaticScratchOfCurrentDevice(int *environments) {
     *environments = 0;
     int device = 0;
-    if (hipGetDevice(&device) != hipSuccess) return nullptr;
+    if (hipGetDevice(&device) != hipSuccess) {
+        // Leave no error behind for the next launch check to report as its own.
+        (void)hipGetLastError();
+        return nullptr;
+    }
     std::lock_guard<std::mutex> lock(gScratchMutex);
     if ((int)gScratchAddress.size() <= device) gScratchAddress.resize(device + 1, nullptr);
     if (!gScratchAddress[device]) {
         void *p = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
         gScratchAddress[device] = p;
     }
     *environments = kStaticScratchEnvironments;
@@ -260,6 +267,7 @@ std::unique_ptr<Device> MakeLibraryDevice(int, int environments) {
 // torch names a HIP device "cuda" on ROCm; the reference binding compares this name with the
 // device type it was asked for (python/cuju/_batch/library.py:217-222).
 extern const char *const kBackendName = "cuda";
+extern const bool kLibraryHostMemory = false;
 
 }  // namespace host
 }  // namespace eng

@@ -16,6 +16,8 @@ namespace host {
 // Defined by each library: its device and backend name.
 std::unique_ptr<Device> MakeLibraryDevice(int threads, int environments);
 extern const char *const kBackendName;
+// Whether the library's device keeps the batch in host memory (the host debugging build).
+extern const bool kLibraryHostMemory;
 }  // namespace host
 }  // namespace eng
 
@@ -89,7 +91,7 @@ int cuju_memory_estimate(const struct cuju_configuration *settings, unsigned lon
         // The estimate takes nothing from the caller's allocator.
         c.allocate = nullptr;
         c.release = nullptr;
-        BatchRuntime sized(c, eng::host::MakeSizingDevice());
+        BatchRuntime sized(c, eng::host::MakeSizingDevice(eng::host::kLibraryHostMemory));
         *bytes = sized.MemoryBytes();
         return 0;
     } catch (const std::exception &e) {

@@ -83,6 +83,7 @@ private:
 
 std::unique_ptr<Device> MakeLibraryDevice(int threads, int) { return std::make_unique<HostDevice>(threads); }
 extern const char *const kBackendName = "host";
+extern const bool kLibraryHostMemory = true;
 }  // namespace host
 }  // namespace eng
 

@@ -200,8 +200,10 @@ void *BatchRuntime::AllocateBytes(size_t bytes) {
 namespace {
 class SizingDevice : public Device {
 public:
+    explicit SizingDevice(bool hostMemory) : hostMemory_(hostMemory) {}
     const char *Name() const override { return "sizing"; }
-    bool HostMemory() const override { return false; }
+    // As the library's own device: a device in host memory stages no actions.
+    bool HostMemory() const override { return hostMemory_; }
     // Every block is the same placeholder: nothing reads or writes it.
     void *Allocate(size_t) override { return &placeholder_; }
     void Release(void *) override {}
@@ -216,11 +218,12 @@ public:
     void CheckFault() override {}
 
 private:
+    bool hostMemory_;
     alignas(256) unsigned char placeholder_[256] = {};
 };
 }  // namespace
 
-std::unique_ptr<Device> MakeSizingDevice() { return std::make_unique<SizingDevice>(); }
+std::unique_ptr<Device> MakeSizingDevice(bool hostMemory) { return std::make_unique<SizingDevice>(hostMemory); }
 
 int BatchRuntime::LeftPlayers(int env) const { return VariantAt(slots_[env].bundle * 4).world->scenario.leftTeamSize; }
 int BatchRuntime::RightPlayers(int env) const { return VariantAt(slots_[env].bundle * 4).world->scenario.rightTeamSize; }

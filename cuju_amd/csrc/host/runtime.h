@@ -81,7 +81,8 @@ struct Configuration {
 // A device that holds no memory and runs nothing: a batch created on it checks its configuration,
 // loads its bundles and tables on the host and counts the bytes it would allocate on a HIP device
 // (src/environment_api.h:148-152, the reference's EstimateMemory).
-std::unique_ptr<Device> MakeSizingDevice();
+// A device that allocates placeholders only, to size a batch: `hostMemory` as the library's device.
+std::unique_ptr<Device> MakeSizingDevice(bool hostMemory);
 
 // The raw arrays of `outputs` agent views in one buffer, each at a multiple of 256 bytes.
 RawLayout MakeRawLayout(size_t outputs, int players, int sticky);

@@ -5,41 +5,48 @@ such digests, so a digest of this build equal to one there shows the same run bi
 
 from __future__ import annotations
 
-import ctypes
 import hashlib
-from typing import Any
+from typing import Any, Iterator
 
 import torch
 
 __all__ = ['Digest', 'digest']
 
 
+def _chunks(value: Any) -> Iterator[bytes]:
+    """The bytes a value contributes to a digest, in order: a tensor its elements' bytes in
+    row-major order (from any device), a dictionary its values by sorted key, a list or tuple its
+    items, bytes themselves."""
+    if isinstance(value, (bytes, bytearray)):
+        yield bytes(value)
+    elif isinstance(value, torch.Tensor):
+        flat = value.detach().to('cpu').contiguous().reshape(-1)
+        # Reinterpreting a one-dimensional tensor as bytes spreads each element over its width.
+        yield flat.view(torch.uint8).numpy().tobytes() if flat.numel() else b''
+    elif isinstance(value, dict):
+        for key in sorted(value):
+            yield from _chunks(value[key])
+    elif isinstance(value, (list, tuple)):
+        for item in value:
+            yield from _chunks(item)
+    else:
+        raise TypeError(f'expected tensors, dictionaries, sequences or bytes, found {value!r}')
+
+
 class Digest:
-    """The SHA-256 of a sequence of outputs: a tensor adds the bytes of its elements in order, on
-    any device; a dictionary adds its values by sorted key; a list or tuple adds its items in order;
-    bytes add as they are."""
+    """The SHA-256 of a sequence of outputs, each added as `_chunks` lays it out."""
 
     def __init__(self) -> None:
         self._hash = hashlib.sha256()
 
     def update(self, value: Any) -> None:
-        if isinstance(value, torch.Tensor):
-            tensor = value.detach().to('cpu').contiguous()
-            self._hash.update(ctypes.string_at(tensor.data_ptr(), tensor.numel() * tensor.element_size()))
-        elif isinstance(value, dict):
-            for key in sorted(value):
-                self.update(value[key])
-        elif isinstance(value, (list, tuple)):
-            for item in value:
-                self.update(item)
-        elif isinstance(value, (bytes, bytearray)):
-            self._hash.update(value)
-        else:
-            raise TypeError(f'expected tensors, dictionaries, sequences or bytes, found {value!r}')
+        # Every chunk is produced before any is hashed, so a value that raises adds nothing.
+        for chunk in list(_chunks(value)):
+            self._hash.update(chunk)
 
     def copy(self) -> Digest:
         """A digest of the same outputs that goes on apart."""
-        other = Digest()
+        other = Digest.__new__(Digest)
         other._hash = self._hash.copy()
         return other
 

@@ -165,15 +165,34 @@ DRILLS = tuple(Drill(a, d, m) for a in DRILL_ATTACKERS for d in DRILL_DEFENDERS 
 
 
 def drill_bundles(directory: str, library=None) -> list:
-    """Builds the bundle of every drill into `directory` (once) and returns their paths. `library`
-    is the path of a library with the builder's C ABI (by default this package's)."""
+    """Builds the bundle of every drill and returns their paths, `<drill>_l0_r0.cjb` in a
+    subdirectory of `directory` named by a digest of what the bytes depend on: the builder's
+    library (`library`, by default this package's), the animation tables and the drill
+    definitions of this module. A bundle is built once per digest and installed by rename, so a
+    reader never finds a partial file or one from another builder."""
+    import hashlib
+    import tempfile
+    from . import library as _library
     from . import scenarios
-    os.makedirs(directory, exist_ok=True)
+    key = hashlib.sha256(b'cuju_amd drill bundles 1')
+    for path in (os.path.abspath(library or _library.PRODUCT), os.path.join(_library.DATA, 'animations.bin'),
+                 os.path.abspath(__file__)):
+        with open(path, 'rb') as f:
+            key.update(hashlib.sha256(f.read()).digest())
+    folder = os.path.join(directory, key.hexdigest()[:24])
+    os.makedirs(folder, exist_ok=True)
     paths = []
     for drill in DRILLS:
-        out = os.path.join(directory, drill.name + '_l0_r0.cjb')
+        out = os.path.join(folder, drill.name + '_l0_r0.cjb')
         if not os.path.isfile(out):
-            scenarios.build_bundle(drill.build_scenario, out, name=drill.name, library=library)
+            handle, partial = tempfile.mkstemp(prefix=f'.{drill.name}-', suffix='.building', dir=folder)
+            os.close(handle)
+            try:
+                scenarios.build_bundle(drill.build_scenario, partial, name=drill.name, library=library)
+                os.replace(partial, out)
+            finally:
+                if os.path.exists(partial):
+                    os.remove(partial)
         paths.append(out)
     return paths
 

@@ -1,9 +1,13 @@
 """Per-environment digests of long episodes of the five benchmark workloads.
 
-A sample of each workload's environments is played for thousands of steps: two ranges of
-`RANGE` environments, one at the start of the workload's index range and one at its end, each a
-batch of its own whose `first_index` places it there. Inputs come from `cuju_amd.workloads`, so a
+A sample of each workload's environments is played for thousands of steps: two ranges, one at
+the start of the workload's index range and one at its end, each a batch of its own whose
+`first_index` places it there. Inputs come from `cuju_amd.workloads`, so a
 sampled environment plays exactly what it plays in the full batch.
+
+The start range plays one environment to a wavefront (a step then takes the least time), the end
+range at the geometry the full batch gets, several environments sharing each wavefront, as the
+benchmark runs them.
 
 The digest of one environment is SHA-256 over, in order:
 
@@ -28,12 +32,25 @@ import numpy as np
 from cuju_amd import workloads
 
 RANGE = 8
-CHECKPOINTS = (3000, 10000)
+CHECKPOINTS = (3000, 5000, 10000)
+
+# Environments per wavefront that the library gives each workload's full batch on an MI355X (256
+# compute units, two wavefronts per SIMD): 1 x 16 lanes for 64 environments, 2 x 16 for 4,096,
+# 8 x 8 for 16,384, 4 x 16 for 8,192 and 16 x 4 for 32,768.
+PRODUCTION_MATCHES = {1: 1, 2: 2, 3: 8, 4: 4, 5: 16}
+# Wavefronts of the end range, which plays at the full batch's geometry.
+END_WAVEFRONTS = 4
 
 
 def sample_ranges(workload):
+    """(first index, count, environments per wavefront) of the sampled ranges: `RANGE`
+    environments at the start of the index range, one to a wavefront, and the end of the index
+    range in `END_WAVEFRONTS` full wavefronts of the geometry the full batch gets (at most half of
+    the batch)."""
     n = workload.environments
-    return [(0, RANGE), (n - RANGE, RANGE)]
+    matches = PRODUCTION_MATCHES[workload.number]
+    end = max(RANGE, min(n // 2, matches * END_WAVEFRONTS))
+    return [(0, RANGE, 1), (n - end, end, matches)]
 
 
 def seed_of(workload):

@@ -27,6 +27,11 @@ sys.path.insert(0, os.path.dirname(HERE))
 OUT = os.path.join(HERE, 'episodes.json')
 
 
+# Environments of one job: a sampled range splits into jobs of at most this many, since each
+# environment's digest depends on its global index alone, not on the batch it plays in.
+JOB = 8
+
+
 def _play(number, first_index, count, drill_paths):
     from cuju_amd import workloads
     import episodes
@@ -49,17 +54,22 @@ def main():
     directory = tempfile.mkdtemp(prefix='drills_')
     drill_paths = workloads.drill_bundles(directory, library=ref.LIBRARY)
     bundles = {os.path.basename(p): hashlib.sha256(open(p, 'rb').read()).hexdigest() for p in drill_paths}
-    jobs = [(n, first, count) for n in sorted(workloads.WORKLOADS)
-            for first, count in episodes.sample_ranges(workloads.WORKLOADS[n])]
-    result = {'checkpoints': list(episodes.CHECKPOINTS), 'range': episodes.RANGE, 'drill_bundles': bundles,
-              'workloads': {}}
+    ranges = [(n, first, count) for n in sorted(workloads.WORKLOADS)
+              for first, count, _ in episodes.sample_ranges(workloads.WORKLOADS[n])]
+    jobs = [(n, first + k, min(JOB, count - k)) for n, first, count in ranges for k in range(0, count, JOB)]
+    result = {'checkpoints': list(episodes.CHECKPOINTS), 'drill_bundles': bundles, 'workloads': {}}
+    found = {}
     with concurrent.futures.ProcessPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as pool:
         futures = [pool.submit(_play, n, first, count, drill_paths) for n, first, count in jobs]
         for f in concurrent.futures.as_completed(futures):
             number, first, digests, seconds = f.result()
             print(f'workload {number} from {first}: {seconds:.0f} s', flush=True)
-            entry = result['workloads'].setdefault(str(number), {})
-            entry[str(first)] = {str(k): v for k, v in digests.items()}
+            found[number, first] = digests
+    # Each range's digests, its jobs' in index order.
+    for n, first, count in ranges:
+        entry = result['workloads'].setdefault(str(n), {})
+        parts = [found[n, first + k] for k in range(0, count, JOB)]
+        entry[str(first)] = {str(c): [d for part in parts for d in part[c]] for c in episodes.CHECKPOINTS}
     with open(OUT, 'w') as f:
         json.dump(result, f, indent=1, sort_keys=True)
         f.write('\n')

@@ -24,9 +24,10 @@ from conftest import PRODUCT, digest_actions
 
 
 @contextlib.contextmanager
-def one_match_per_wavefront():
+def matches_per_wavefront(matches):
+    """Batches created inside put `matches` environments in each wavefront."""
     before = os.environ.get('CUJU_AMD_MATCHES')
-    os.environ['CUJU_AMD_MATCHES'] = '1'
+    os.environ['CUJU_AMD_MATCHES'] = str(matches)
     try:
         yield
     finally:
@@ -34,6 +35,10 @@ def one_match_per_wavefront():
             os.environ.pop('CUJU_AMD_MATCHES', None)
         else:
             os.environ['CUJU_AMD_MATCHES'] = before
+
+
+def one_match_per_wavefront():
+    return matches_per_wavefront(1)
 
 
 def uncaptured(capsys):

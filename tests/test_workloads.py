@@ -57,3 +57,33 @@ def test_the_bench_counts_the_algorithmic_bytes_of_each_workload():
     expected = {1: (4, 4, 748_981), 2: (1, 1, 747_577), 3: (11, 11, 752_257), 4: (22, 22, 818_125)}
     for number, (present, axis, total) in expected.items():
         assert bench.algorithmic_bytes(workloads.WORKLOADS[number], present, axis) == total, number
+
+
+def test_the_bench_splits_its_timed_steps_into_rounds():
+    import bench
+    assert bench.round_sizes(20, 3) == [7, 7, 6]
+    assert bench.round_sizes(30, 3) == [10, 10, 10]
+    assert bench.round_sizes(2, 3) == [1, 1]
+    s = bench.summary(100, [1.0, 2.0, 0.5], [10, 10, 10])
+    assert s['env_steps_per_s'] == [1000.0, 500.0, 2000.0] and s['median'] == 1000.0 and s['spread'] == 1.5
+
+
+def test_the_bench_refuses_more_than_one_gpu():
+    import subprocess
+    import sys
+    import bench
+    done = subprocess.run([sys.executable, bench.__file__, '--gpus', '2'], capture_output=True, text=True)
+    assert done.returncode == 2 and 'one GPU' in done.stderr
+
+
+def test_the_cpu_baseline_times_the_device_window_in_interleaved_rounds(reference_library):
+    """The reference pool plays each workload's sample over the same warm-up and rounds."""
+    import argparse
+    import bench
+    args = argparse.Namespace(steps=3, rounds=2, warmup=2, seed=0, cpu_environments=4)
+    out = bench.cpu_baselines([1, 3], args, None, lambda text: None)
+    assert sorted(out) == [1, 3]
+    for n, line in out.items():
+        assert line['kind'] == 'reference' and line['cores'] >= 1 and line['value'] > 0
+        assert len(line['rounds']['env_steps_per_s']) == 2
+        assert 'environments 0-3' in line['sample'] and '3 timed steps in 2 interleaved rounds' in line['sample']

@@ -54,7 +54,7 @@ HIP_FLAGS = ['-std=c++17', '-O2', '-fPIC', '-ffp-contract=off', '-fno-fast-math'
 
 # The device code is built once per group width (lanes per environment); the first build also
 # holds the geometry choice, the static scratch and the math check kernel.
-GROUP_WIDTHS = (4, 2, 8, 16)
+GROUP_WIDTHS = (4, 2, 8, 16, 32, 64)
 
 
 def _variant_flags(lanes):

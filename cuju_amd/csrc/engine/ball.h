@@ -393,11 +393,11 @@ HDN TimeNeeded WalkTimeNeeded(const TimeWalk &wk, const Vec3 &pos, const Vec3 &m
             o = d2 < wk.optimisticSquared[k] || late;
             u = d2 < wk.usualSquared[k] || late;
         }
-        uint32_t um = cooperative ? GroupBallot(u) : (uint32_t)u;
-        uint32_t om = cooperative ? GroupBallot(o) : (uint32_t)o;
+        const LaneMask um = cooperative ? GroupBallot(u) : (LaneMask)u;
+        LaneMask om = cooperative ? GroupBallot(o) : (LaneMask)o;
         if (um) {
             reach = k0 + LowestBit(um);
-            om &= (2u << LowestBit(um)) - 1u;  // the optimistic test comes first within a step
+            om &= LanesThrough(LowestBit(um));  // the optimistic test comes first within a step
         }
         if (optimistic < 0 && om) optimistic = k0 + LowestBit(om);
     }
@@ -632,6 +632,7 @@ HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p)
     } else if (w.match.ballRetainer != -1) {
         ps.hasPossession = ps.hasBestPossession = ps.hasUniquePossession = false;
     }
+    w.roster.timeToBallMs[p] = ps.timeToBallMs;
 }
 
 HDN void TeamUpdatePossessionStatistics(World &w, const Ctx &c, int teamID) {
@@ -645,9 +646,9 @@ HDN void TeamUpdatePossessionStatistics(World &w, const Ctx &c, int teamID) {
     bool hasPossession = false;
     int timeToBall = 100000;
     for (int i = 0; i < players.count; i++) {
-        const Player &ps = w.match.players[players[i]];
-        if (ps.hasPossession) hasPossession = true;
-        if ((int)ps.timeToBallMs < timeToBall) timeToBall = (int)ps.timeToBallMs;
+        if (w.match.players[players[i]].hasPossession) hasPossession = true;
+        const int t = (int)w.roster.timeToBallMs[players[i]];
+        if (t < timeToBall) timeToBall = t;
     }
     Team &t = TeamByID(w, teamID);
     t.hasPossession = hasPossession;

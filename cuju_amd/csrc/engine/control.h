@@ -161,7 +161,7 @@ HDN int GetClosestPlayer(const World &w, const Ctx &c, int teamID, const Vec3 &p
     // formation tests run only for candidates.
 #pragma unroll
     for (int p = 0; p < kPlayers; p++) {
-        const bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.match.players[p].base.isActive & (p != except);
+        const bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.roster.active[p] & (p != except);
         const float d = (Sp(w, p).position - pos).Length();
         if (in && d < best) {
             if ((!onlyAI || !ExternalControllerActive(w, p)) && (!onlySelectable || Formation(w, c, p).controllable)) {
@@ -179,7 +179,7 @@ HD int HumanControlledToBallTime(const World &w, int teamID) {
     for (int g = 0; g < t.gamers.count; g++) {
         const HumanGamer &gm = t.gamers[g];
         if (gm.selectedPlayer >= 0 && !gm.controller.keyboard.disabled) {
-            int tt = (int)w.match.players[gm.selectedPlayer].timeToBallMs;
+            int tt = (int)w.roster.timeToBallMs[gm.selectedPlayer];
             best = (tt < best) ? tt : best;
         }
     }
@@ -199,7 +199,7 @@ HDN bool TeamUpdateSwitch(World &w, const Ctx &c, int teamID) {
     }
     if (m.inPlay && t.gamers.count > 0) {
         int d = t.designatedTeamPossessionPlayer;
-        if (!ExternalControllerActive(w, d) && 3 * (int)m.players[d].timeToBallMs < HumanControlledToBallTime(w, teamID) &&
+        if (!ExternalControllerActive(w, d) && 3 * (int)w.roster.timeToBallMs[d] < HumanControlledToBallTime(w, teamID) &&
             Formation(w, c, d).role != kRoleGoalkeeper) {
             if (!TeamSelectPlayer(w, c, teamID, d)) return false;
         }

@@ -90,13 +90,19 @@ HD bool AnyLane(bool x) {
 #endif
 #if ENG_DEVICE
 constexpr int kGroupLanes = ENG_GROUP_LANES;
-static_assert(kGroupLanes == 1 || kGroupLanes == 2 || kGroupLanes == 4 || kGroupLanes == 8 || kGroupLanes == 16,
+static_assert(kGroupLanes == 1 || kGroupLanes == 2 || kGroupLanes == 4 || kGroupLanes == 8 || kGroupLanes == 16 ||
+                  kGroupLanes == 32 || kGroupLanes == 64,
               "a group is a power of two of lanes within a wavefront");
 #else
 constexpr int kGroupLanes = 1;
 #endif
-// Groups never exceed this, which sizes per-lane working memory.
-constexpr int kMaxGroupLanes = 16;
+// Groups never exceed a wavefront.
+constexpr int kMaxGroupLanes = 64;
+// A set of the lanes of a match: bit r for the lane of rank r.
+using LaneMask = uint64_t;
+// The lanes of rank below r (r < 64), and of rank r and below.
+HD LaneMask LanesBelow(int r) { return ((LaneMask)1 << r) - 1u; }
+HD LaneMask LanesThrough(int r) { return r >= 63 ? ~(LaneMask)0 : ((LaneMask)1 << (r + 1)) - 1u; }
 
 HD int LaneId() {
 #if ENG_DEVICE
@@ -107,30 +113,36 @@ HD int LaneId() {
 }
 HD int GroupRank() { return LaneId() & (kGroupLanes - 1); }
 // Bit r: `x` in the group's lane of rank r. Every lane of the group must make the call.
-HD uint32_t GroupBallot(bool x) {
+HD LaneMask GroupBallot(bool x) {
 #if ENG_DEVICE
     const uint64_t all = __builtin_amdgcn_ballot_w64(x);
-    return (uint32_t)(all >> (LaneId() & ~(kGroupLanes - 1))) & ((1u << kGroupLanes) - 1u);
+    if constexpr (kGroupLanes == 64) return all;
+    else return (all >> (LaneId() & ~(kGroupLanes - 1))) & (((LaneMask)1 << kGroupLanes) - 1u);
 #else
     return x ? 1u : 0u;
 #endif
 }
-HD int PopCount(uint32_t x) {
+HD int PopCount(uint64_t x) {
 #if ENG_DEVICE
-    return __builtin_popcount(x);
+    return __builtin_popcountll(x);
 #else
     int n = 0;
     for (; x; x &= x - 1) n++;
     return n;
 #endif
 }
-HD int LowestBit(uint32_t x) {
+// The lowest set bit of a nonzero mask.
+HD int LowestBit(uint64_t x) {
+#if ENG_DEVICE
+    return __builtin_ctzll(x);
+#else
     int i = 0;
     while (!(x & 1u)) {
         x >>= 1;
         i++;
     }
     return i;
+#endif
 }
 // The value of the group's lane of rank `rank`. Every lane of the group must make the call.
 HD uint32_t GroupShuffle(uint32_t v, int rank) {

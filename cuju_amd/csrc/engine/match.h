@@ -169,8 +169,8 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
                 const int bt = m.bestPossessionTeam == 0 ? first : second;
                 int cand = TeamByID(w, bt).designatedTeamPossessionPlayer;
                 if (cand != m.designatedPossessionPlayer) {
-                    uint32_t dt = m.players[m.designatedPossessionPlayer].timeToBallMs;
-                    uint32_t ct = m.players[cand].timeToBallMs;
+                    uint32_t dt = w.roster.timeToBallMs[m.designatedPossessionPlayer];
+                    uint32_t ct = w.roster.timeToBallMs[cand];
                     if ((float)(ct + 10) / (float)(dt + 10) < 0.85f) m.designatedPossessionPlayer = cand;
                 }
             } else {
@@ -313,6 +313,13 @@ HDN bool GameTick(World &w, const Ctx &c) {
         MatchPreparePutBuffers(w);
         MatchFetchPutBuffers(w, c);
     }
+#if !ENG_DEVICE
+    // The host build checks the roster against the fields it copies after every tick.
+    if (!RosterMatches(w)) {
+        Unsupported("the roster differs from the players");
+        return false;
+    }
+#endif
     return true;
 }
 

@@ -108,7 +108,7 @@ HDN void MentalTeamPlayerImages(const World &w, int k, int teamID, ImageList &ou
     out.clear();
     for (int i = 0; i < mi.players.count; i++) {
         const PlayerImage im = MentalImageEntry(w, mi, i);
-        if (!w.match.players[im.player].base.isActive || w.playerTeamID[im.player] != teamID) continue;
+        if (!w.roster.active[im.player] || w.playerTeamID[im.player] != teamID) continue;
         const SpatialState &s = Sp(w, im.player);
         Vec3 pos = im.position + im.movement * (float)age * 0.001f;
         PlayerImagePos e;

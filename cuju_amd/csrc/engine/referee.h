@@ -12,8 +12,8 @@
 namespace eng {
 
 // Defined with the set pieces.
-HDN bool LeftTeamOwnsBall(const World &w);
-HDN bool RefereePrepareSetPiece(World &w, const Ctx &c, int setPiece);
+HDN bool LeftTeamStartsNearerBall(const World &w);
+HDN bool RefereeRestart(World &w, const Ctx &c, int setPiece);
 
 enum MatchPhase { kPreMatch, kFirstHalf, kSecondHalf };
 
@@ -158,7 +158,7 @@ HDN bool RefereeProcess(World &w, const Ctx &c) {
             b.restartPos = sc.ballPosition;
             b.active = true;
             b.endPhase = true;
-            b.teamID = LeftTeamOwnsBall(w) ? 1 : 0;
+            b.teamID = LeftTeamStartsNearerBall(w) ? 1 : 0;
             b.setPieceTeam = TeamSlot(w, b.teamID);
             b.taker = -1;
             ResetFoul(f);
@@ -218,7 +218,7 @@ HDN bool RefereeProcess(World &w, const Ctx &c) {
                 b.endPhase = false;
             }
             Rng{w.rng}.Seed(sc.gameEngineRandomSeed);
-            if (!RefereePrepareSetPiece(w, c, b.desiredSetPiece)) return false;
+            if (!RefereeRestart(w, c, b.desiredSetPiece)) return false;
         }
         if (b.startTime == m.actualTimeMs) {
             m.inPlay = true;
@@ -633,13 +633,18 @@ HDN bool CheckHumanoidCollisions(World &w, const Ctx &c) {
     // A pair farther apart than both contact radii changes nothing, so only near pairs make the
     // call; the test is the one the pair's own check starts with, on the same values.
     const float bounceRadius = 0.5f * 0.72f, similarRadius = 0.8f * 0.72f;
+    // The pairs read the positions from a copy gathered once, not from each player's spatial state
+    // (one cache line per player, read again for every pair); a call moves only its two players,
+    // whose copies it refreshes.
+    Vec3 at[kPlayers];
+    for (int i = 0; i < ps.count; i++) at[i] = Sp(w, ps[i]).position;
     for (int i = 0; i + 1 < ps.count; i++) {
-        Vec3 pi = Sp(w, ps[i]).position;
         for (int j = i + 1; j < ps.count; j++) {
-            const float dist = (pi - Sp(w, ps[j]).position).Length();
+            const float dist = (at[i] - at[j]).Length();
             if (dist < bounceRadius * 2.0f || dist < (bounceRadius + similarRadius) * 2.0f) {
                 CheckHumanoidCollision(w, c, ps[i], ps[j], bounces[i], bounces[j]);
-                pi = Sp(w, ps[i]).position;  // the call may push the player aside
+                at[i] = Sp(w, ps[i]).position;
+                at[j] = Sp(w, ps[j]).position;
             }
         }
     }

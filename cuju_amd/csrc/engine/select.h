@@ -550,8 +550,8 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &query, AList &out) {
         // The whole record at once, field by field into registers: the tests read its fields
         // one after another.
         const bool keep = k < n && accepts(records[k]);
-        const uint32_t passed = GroupBallot(keep);
-        if (keep) kept[count + PopCount(passed & ((1u << GroupRank()) - 1u))] = records[k].index;
+        const LaneMask passed = GroupBallot(keep);
+        if (keep) kept[count + PopCount(passed & LanesBelow(GroupRank()))] = records[k].index;
         count += PopCount(passed);
     }
     out.count = count;
@@ -625,7 +625,7 @@ HDN float ClosestOpponentDistance(const World &w, int p) {
     float best = 10000;
     int bi = -1;
     for (int o = 0; o < w.match.playerCount; o++) {
-        if (w.playerTeamID[o] != opp || !w.match.players[o].base.isActive) continue;
+        if (w.playerTeamID[o] != opp || !w.roster.active[o]) continue;
         float d = (Sp(w, o).position - pos).Length();
         if (d < best) {
             best = d;
@@ -808,9 +808,9 @@ struct Selector {
             const int k = k0 + GroupRank();
             const int16_t e = k < l.count ? l[k] : 0;
             const bool ok = k < l.count && keep((int)e);
-            const uint32_t mask = GroupBallot(ok);
+            const LaneMask mask = GroupBallot(ok);
             GroupSync();
-            if (ok) l.e[kept + PopCount(mask & ((1u << GroupRank()) - 1u))] = e;
+            if (ok) l.e[kept + PopCount(mask & LanesBelow(GroupRank()))] = e;
             kept += PopCount(mask);
             GroupSync();
         }
@@ -1497,8 +1497,8 @@ struct Selector {
         for (int k0 = 0; k0 < sorted.count; k0 += kGroupLanes) {
             const int k = k0 + GroupRank();
             const bool keep = k < sorted.count && mayPass(sorted[k]);
-            const uint32_t kept = GroupBallot(keep);
-            if (keep) candidates.e[candidates.count + PopCount(kept & ((1u << GroupRank()) - 1u))] = sorted[k];
+            const LaneMask kept = GroupBallot(keep);
+            if (keep) candidates.e[candidates.count + PopCount(kept & LanesBelow(GroupRank()))] = sorted[k];
             candidates.count += PopCount(kept);
         }
         GroupSync();
@@ -1512,7 +1512,7 @@ struct Selector {
             Vec3 ao, sm;
             int tf = 0;
             const bool ok = entry < candidates.count && evaluate(candidates[entry], mine, rot, pa, ao, sm, tf);
-            const uint32_t passed = GroupBallot(ok);
+            const LaneMask passed = GroupBallot(ok);
             if (!passed) continue;
             const int from = LowestBit(passed);
             tmpRotSmuggle = GroupShuffle(rot, from);

@@ -145,23 +145,25 @@ struct SpatialState {
     Vec3 relBodyDirectionVec, relBodyDirectionVecNonQuantized;
     int32_t foot;
 };
+// In the order of use: the spatial state and the small fields, the nodes, the apply buffer, the
+// animation (its planned positions last), the movement history.
 struct Humanoid {
-    NodeState nodes[kHumanoidNodes];
-    AnimApplyBuffer applyBuf;
-    BiasedOffset offsets[kBodyParts];
-    AnimationState anim;
+    SpatialState spatial;
     int32_t prevAnimFrameNum, prevAnimFunctionType;
     Vec3 startPos;
     Radian startAngle;
     Vec3 nextStartPos;
     Radian nextStartAngle;
-    SpatialState spatial;
     Vec3 prevPosition2D;
     int32_t interruptAnim, requeueDelayFrames, tripType;
     Vec3 tripDirection, decayingPositionOffset;
     float decayingDifficultyFactor;
-    List<MovementHistoryEntry, 32> movementHistory;
     int32_t mentalImageTime;
+    NodeState nodes[kHumanoidNodes];
+    AnimApplyBuffer applyBuf;
+    BiasedOffset offsets[kBodyParts];
+    AnimationState anim;
+    List<MovementHistoryEntry, 32> movementHistory;
 };
 
 // ---- controllers ----------------------------------------------------------------------------------
@@ -212,19 +214,18 @@ struct HumanGamer {
 // The part of a player an official shares.
 struct PersonBase {
     bool isActive;
-    Humanoid humanoid;
     int32_t externalController;
     uint64_t lastTouchTimeMs;
     int32_t lastTouchType;
     float fatigueFactorInverse;
+    Humanoid humanoid;
     List<Vec3, 512> positionHistoryPerSecond;
 };
 struct TacticalSituation {
     float forwardSpaceRating, toGoalSpaceRating, spaceRating, forwardRating;
 };
+// The player's own small fields first, then its controller and its person.
 struct Player {
-    PersonBase base;
-    AIControllerState controller;  // stored only while active
     int32_t manMarking;
     FormationEntry dynamicFormationEntry;
     bool hasPossession, hasBestPossession, hasUniquePossession;
@@ -236,6 +237,8 @@ struct Player {
     Vec3 bufferPlayerColor;
     int32_t desiredTimeToBallMs, cards;
     uint64_t cardEffectiveTimeMs;
+    AIControllerState controller;  // stored only while active
+    PersonBase base;
 };
 
 // ---- teams ----------------------------------------------------------------------------------------
@@ -288,10 +291,10 @@ struct Team {
     int32_t timeToBallMs;
     int32_t designatedTeamPossessionPlayer;
     float teamPossessionAmount, fadingTeamPossessionAmount;
-    TeamAI ai;
-    List<HumanGamer, kTeamPlayers> gamers;
-    List<int32_t, kTeamPlayers> switchPriority;
     int32_t lastTouchPlayer, mainSelectedPlayer;
+    TeamAI ai;
+    List<int32_t, kTeamPlayers> switchPriority;
+    List<HumanGamer, kTeamPlayers> gamers;
 };
 
 struct MentalImage {
@@ -304,13 +307,12 @@ struct MentalImage {
     bool lazyTeamFlip[2];
 };
 
+// The scalars first, then the prediction and history arrays.
 struct Ball {
     Vec3 momentum;
     Quat rotationPerMs;
-    Vec3 predictions[401];
     int32_t validPredictions;
     Quat orientationPrediction;
-    List<Vec3, 402> positionHistory;
     Vec3 positionBuffer;
     Quat orientationBuffer;
     bool touchesNet;
@@ -321,6 +323,8 @@ struct Ball {
     bool memoValid, memoInGoal, memoTouchesNet;
     Vec3 memoPosition, memoMomentum, memoOutMomentum;
     Quat memoOrientation, memoRotation, memoOutRotation;
+    Vec3 predictions[401];
+    List<Vec3, 402> positionHistory;
 };
 
 struct RefereeBuffer {
@@ -363,19 +367,12 @@ struct Scenario {
     FormationEntry leftTeam[kTeamPlayers], rightTeam[kTeamPlayers];
 };
 
+// The scalars first, then the teams, the ball and the referee, then the large arrays.
 struct MatchState {
     int32_t firstTeam, secondTeam;
-    List<MentalImage, 4> mentalImages;
-    Team teams[2];  // teams[0] is processed first
     int32_t playerCount;
-    Player players[kPlayers];
     int32_t goalCount[2];
     float possessionLastMinute;
-    PersonBase officials[3];  // referee, two linesmen
-    KeyboardState secondKeyboardCopies[kControllers];
-    int32_t freeControllerCount;
-    KeyboardState freeControllers[kControllers];
-    Ball ball;
     uint64_t matchTimeMs, actualTimeMs, goalScoredTimer;
     int32_t matchPhase;
     bool inPlay, inSetPiece, goalScored, ballIsInGoal;
@@ -387,14 +384,22 @@ struct MatchState {
     int32_t designatedPossessionPlayer;
     int32_t ballRetainer;
     uint32_t possessionSideHistoryMaxTimeMs;
-    List<float, 600> possessionSideHistory;
+    uint32_t lastBodyBallCollisionTimeMs;
+    int32_t freeControllerCount;
     bool autoUpdateInGameCamera;
+    float cameraFov, cameraNearCap, cameraFarCap;
     Quat cameraOrientation, cameraNodeOrientation;
     Vec3 cameraNodePosition;
-    float cameraFov, cameraNearCap, cameraFarCap;
-    List<Vec3, 160> cameraPosition;
-    uint32_t lastBodyBallCollisionTimeMs;
+    Team teams[2];  // teams[0] is processed first
+    Ball ball;
     Referee referee;
+    List<MentalImage, 4> mentalImages;
+    Player players[kPlayers];
+    PersonBase officials[3];  // referee, two linesmen
+    KeyboardState secondKeyboardCopies[kControllers];
+    KeyboardState freeControllers[kControllers];
+    List<float, 600> possessionSideHistory;
+    List<Vec3, 160> cameraPosition;
 };
 
 // Frames between ticks: each team in its own frame (side -1, unmirrored), the ball in team 0's.
@@ -406,18 +411,31 @@ struct FrameFlags {
     bool mentalBallMirrored[4];
 };
 
+// Copies of the per-player fields that scans over a team read for every player, side by side so
+// that a scan touches two cache lines instead of one line per player (a Player spans 13 KB). The
+// engine writes each copy where it writes the field (SetPlayerActive, SetPlayerTimeToBall); a load
+// of a state fills them (InitializePlayerTeams).
+struct Roster {
+    bool active[kPlayers];              // players[p].base.isActive
+    uint32_t timeToBallMs[kPlayers];    // players[p].timeToBallMs
+};
+
+// The members are in the order of their use, the small and often read first, so that a match's
+// hot scalars share a few cache lines; the state codec visits them in GRF's order by name.
 struct World {
     int32_t gameState;
     int32_t waitingForGameCount;
-    uint8_t rng[2512];
-    Scenario scenario;
     int32_t step;
-    MatchState match;
     // Not in a state.
     FrameFlags flags;
     int32_t playerTeamID[kPlayers];
     // 0: the player's own formation entry; else 1 + the player whose entry it uses.
     int8_t formationOverride[kPlayers];
+    Roster roster;
+    // The state.
+    Scenario scenario;
+    MatchState match;
+    uint8_t rng[2512];
     HD int FirstTeamID() const { return match.firstTeam ^ (scenario.reverseTeamProcessing ? 1 : 0); }
 };
 

@@ -432,7 +432,7 @@ struct PlayerBounce {
 using PlayerBounceList = Small<PlayerBounce, kPlayers>;
 
 // Lanes of one match with a plan of their own in the candidate search.
-constexpr int kPlanLanes = 16;
+constexpr int kPlanLanes = kMaxGroupLanes;
 static_assert(kGroupLanes <= kPlanLanes, "every lane of a match needs a candidate plan");
 // Per-match working memory: the animation selection's candidate lists, planned positions, sort keys
 // and one candidate plan per lane of the match, and the lists above. One block per environment in

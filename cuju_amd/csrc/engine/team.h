@@ -11,7 +11,7 @@
 namespace eng {
 
 // Defined with the set pieces.
-HDN bool PlayerSendOff(World &w, const Ctx &c, int p);
+HDN bool SendOff(World &w, const Ctx &c, int p);
 
 // Goals and the possession of the last minute are stored in processing order; these take IDs.
 HD int MatchGoalCount(const World &w, int teamID) { return w.match.goalCount[teamID == w.FirstTeamID() ? 0 : 1]; }
@@ -347,7 +347,7 @@ HDN bool TeamCalculateDynamicRoles(World &w, const Ctx &c, int teamID) {
             const int total = HungarianSolve(m, (int)n, colOfRow);
             ok = total != -1 && (total < 50000 || cutoff >= (unsigned)count - 5);
         }
-        const uint32_t solved = GroupBallot(ok);
+        const LaneMask solved = GroupBallot(ok);
         if (!solved) continue;
         const int from = LowestBit(solved);
         int chosen[kTeamPlayers];
@@ -460,7 +460,7 @@ HDN bool PlayerProcessEnd(World &w, const Ctx &c, int p, const Vec3 &before) {
         ps.base.fatigueFactorInverse = Clamp(ps.base.fatigueFactorInverse, 0.01f, 1.0f);
     }
     if (ps.cards > 1 && ps.cardEffectiveTimeMs <= m.actualTimeMs && TeamActivePlayers(w, w.playerTeamID[p]).size() > 1)
-        return PlayerSendOff(w, c, p);
+        return SendOff(w, c, p);
     return true;
 }
 
@@ -490,7 +490,7 @@ HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
     // stopped or finished, so that the interruptions run together; each match still processes
     // its players in order.
     auto next = [&](int from) {
-        while (from < m.playerCount && !(w.playerTeamID[from] == teamID && m.players[from].base.isActive)) from++;
+        while (from < m.playerCount && !(w.playerTeamID[from] == teamID && w.roster.active[from])) from++;
         return from;
     };
     int p = next(0);
@@ -546,12 +546,12 @@ HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
         t.mainSelectedPlayer = -1;
     }
     // The designated player changes to the best one when clearly quicker to the ball.
-    int dt = (int)m.players[t.designatedTeamPossessionPlayer].timeToBallMs;
+    int dt = (int)w.roster.timeToBallMs[t.designatedTeamPossessionPlayer];
     int best = TeamBestPossessionPlayer(w, teamID);
     int ot = opp.timeToBallMs;
     if (t.designatedTeamPossessionPlayer != best) {
         int d = t.designatedTeamPossessionPlayer;
-        float r = (float)((int)m.players[best].timeToBallMs + 500) / (float)(dt + 500);
+        float r = (float)((int)w.roster.timeToBallMs[best] + 500) / (float)(dt + 500);
         if (m.players[best].hasPossession) r *= 0.5f;
         if (m.players[d].hasPossession) r /= 0.5f;
         if (ExternalControllerActive(w, best)) r *= 0.8f;

@@ -104,7 +104,7 @@ HDN PlayerList GetClosestPlayers(const World &w, const Ctx &c, int teamID, const
     const int players = w.match.playerCount;
 #pragma unroll
     for (int p = 0; p < kPlayers; p++) {
-        bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.match.players[p].base.isActive;
+        bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.roster.active[p];
         const float d = (Sp(w, p).position - pos).Length();
         if (in && !((!onlyAI || !ExternalControllerActive(w, p)) && (!onlySelectable || Formation(w, c, p).controllable))) in = false;
         if (!in) continue;
@@ -138,7 +138,7 @@ HDN PlayerList GetClosestPlayers(const World &w, const Ctx &c, int teamID, const
 }
 HD int TeamGoalie(const World &w, const Ctx &c, int teamID) {
     for (int p = 0; p < w.match.playerCount; p++)
-        if (w.playerTeamID[p] == teamID && w.match.players[p].base.isActive && Formation(w, c, p).role == kRoleGoalkeeper) return p;
+        if (w.playerTeamID[p] == teamID && w.roster.active[p] && Formation(w, c, p).role == kRoleGoalkeeper) return p;
     return -1;
 }
 // The active player of a team with the least time to the ball, the first in state order on ties.
@@ -148,8 +148,8 @@ HDN int TeamBestPossessionPlayer(const World &w, int teamID) {
     const int players = w.match.playerCount;
 #pragma unroll
     for (int p = 0; p < kPlayers; p++) {
-        const bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.match.players[p].base.isActive;
-        const int t = (int)w.match.players[p].timeToBallMs;
+        const bool in = (p < players) & (w.playerTeamID[p] == teamID) & w.roster.active[p];
+        const int t = (int)w.roster.timeToBallMs[p];
         if (in && t < best) {
             best = t;
             bp = p;

@@ -70,8 +70,21 @@ __device__ void RecordFault(int env) {
 
 __device__ int MatchIndex() { return (int)(blockIdx.x * (blockDim.x / kDeviceGroupLanes) + threadIdx.x / kDeviceGroupLanes); }
 
-__global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) ResetKernel(eng::Batch b, const uint8_t *mask, const int64_t *seeds,
+// The batch description, the kernels' first argument, read where the launch placed it: at the
+// start of the kernel argument segment. A reference to the by-value parameter itself would make
+// every lane copy its 752 bytes onto its stack first.
+__device__ const eng::Batch &LaunchBatch() {
+#if defined(__HIP_DEVICE_COMPILE__)
+    // A constant-segment address is the same number as a generic one.
+    return *reinterpret_cast<const eng::Batch *>((uintptr_t)__builtin_amdgcn_kernarg_segment_ptr());
+#else
+    return *static_cast<const eng::Batch *>(nullptr);
+#endif
+}
+
+__global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) ResetKernel(eng::Batch, const uint8_t *mask, const int64_t *seeds,
                                                                       const int32_t *reverse) {
+    const eng::Batch &b = LaunchBatch();
     eng::libm::StageMathTables();
     const int env = MatchIndex();
     if (env >= b.count) return;
@@ -79,14 +92,16 @@ __global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) ResetKernel(en
     if (!eng::ResetAndWriteEnvironment(b, env, seeds, reverse)) RecordFault(env);
 }
 
-__global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) StepKernel(eng::Batch b, const int32_t *actions) {
+__global__ void __launch_bounds__(kWaveLanes, ENG_WAVES_PER_SIMD) StepKernel(eng::Batch, const int32_t *actions) {
+    const eng::Batch &b = LaunchBatch();
     eng::libm::StageMathTables();
     const int env = MatchIndex();
     if (env >= b.count) return;
     if (!eng::StepEnvironment(b, env, actions)) RecordFault(env);
 }
 
-__global__ void __launch_bounds__(kDeviceGroupLanes) OutputKernel(eng::Batch b, int env) {
+__global__ void __launch_bounds__(kDeviceGroupLanes) OutputKernel(eng::Batch, int env) {
+    const eng::Batch &b = LaunchBatch();
     eng::libm::StageMathTables();
     eng::WriteEnvironmentOutputs(b, env, false);
 }
@@ -246,6 +261,8 @@ std::unique_ptr<Device> MakeHipDevice2(int matches);
 std::unique_ptr<Device> MakeHipDevice4(int matches);
 std::unique_ptr<Device> MakeHipDevice8(int matches);
 std::unique_ptr<Device> MakeHipDevice16(int matches);
+std::unique_ptr<Device> MakeHipDevice32(int matches);
+std::unique_ptr<Device> MakeHipDevice64(int matches);
 
 // One wavefront for each SIMD where the batch allows it: the matches of a wavefront are the
 // environments over the SIMDs, 1 to 32, and the group is the widest of 16, 8, 4 or 2 lanes that
@@ -258,6 +275,18 @@ std::unique_ptr<Device> MakeLibraryDevice(int, int environments) {
     int matches = (std::max(1, environments) + slots - 1) / slots;
     if (const char *v = getenv("CUJU_AMD_MATCHES")) matches = atoi(v);
     matches = std::max(1, std::min(32, matches));
+    // CUJU_AMD_LANES sets the lanes of a match (2 to 64), and with it at most 64 / lanes matches.
+    if (const char *v = getenv("CUJU_AMD_LANES")) {
+        switch (atoi(v)) {
+        case 64: return MakeHipDevice64(1);
+        case 32: return MakeHipDevice32(std::min(matches, 2));
+        case 16: return MakeHipDevice16(std::min(matches, 4));
+        case 8: return MakeHipDevice8(std::min(matches, 8));
+        case 4: return MakeHipDevice4(std::min(matches, 16));
+        case 2: return MakeHipDevice2(matches);
+        default: throw std::invalid_argument("CUJU_AMD_LANES must be 2, 4, 8, 16, 32 or 64");
+        }
+    }
     if (matches <= 4) return MakeHipDevice16(matches);
     if (matches <= 8) return MakeHipDevice8(matches);
     if (matches <= 16) return MakeHipDevice4(matches);

@@ -64,12 +64,15 @@ def test_gpu_matches_reference_on_headline_scenario(reference_library):
         theirs.close()
 
 
-@pytest.mark.parametrize('matches,lanes', [(32, 2), (16, 4), (8, 8), (4, 16), (1, 16)])
+@pytest.mark.parametrize('matches,lanes', [(32, 2), (16, 4), (8, 8), (4, 16), (1, 16), (2, 32), (1, 64)])
 def test_every_geometry_matches_the_reference(matches, lanes, reference_library, monkeypatch):
-    """Each build of the kernels (2, 4, 8 and 16 lanes per environment) at the matches per wavefront
-    it serves plays the headline scenario as the reference does: 48 environments, 40 steps, then
-    every state. 8 matches of 8 lanes is the geometry of the headline batch of 16,384."""
+    """Each build of the kernels (2 to 64 lanes per environment) at the matches per wavefront it
+    serves plays the headline scenario as the reference does: 48 environments, 40 steps, then every
+    state. 8 matches of 8 lanes is the geometry of the headline batch of 16,384; the 32- and
+    64-lane builds take a whole half or whole wavefront per match (CUJU_AMD_LANES)."""
     monkeypatch.setenv('CUJU_AMD_MATCHES', str(matches))
+    if lanes > 16:
+        monkeypatch.setenv('CUJU_AMD_LANES', str(lanes))
     environments, steps = 48, 40
     mine = gpu_batch('11_vs_11_hard_stochastic_l11_r0', environment_count=environments, seed=2)
     theirs = ref.ReferenceBatch('11_vs_11_hard_stochastic_l11_r0', environment_count=environments, seed=2,

@@ -30,6 +30,170 @@ HD bool SameBits(const Quat &a, const Quat &b) {
            BitsOf(a.q[3]) == BitsOf(b.q[3]);
 }
 
+// A ball in flight stepped 10 ms at a time: the state that carries from one step to the next, and
+// the stages of a step in the order GRF applies them (the Land, RubGrass, HitFrame, PushNet, Roll
+// and Swerve of one step, then the position moves by the momentum). GRF's constants, SI units.
+struct BallFlight {
+    static constexpr float kDt = 0.01f, kRadius = 0.11f, kGrassHeight = 0.025f;
+    static constexpr float kGravity = -9.81f, kDrag = 0.015f, kBounce = 0.62f, kLinearBounce = 0.06f;
+    static constexpr float kFriction = 0.04f, kLinearFriction = 1.6f;
+    static constexpr float kPostRadius = 0.07f, kPostAbsorb = 0.8f;
+    static constexpr float kNetExponent = 2.6f, kNetPower = 1.8f, kNetAbsorb = 0.95f;
+
+    Vec3 pos, mom;
+    Quat rot;
+    // The Euler angles of `rot`, computed at their first use after `rot` changes.
+    Vec3 angles;
+    bool anglesKnown = false;
+
+    HD Vec3 Angles() {
+        if (!anglesKnown) {
+            rot.Angles(angles.v[0], angles.v[1], angles.v[2]);
+            anglesKnown = true;
+        }
+        return angles;
+    }
+    HD bool InGrass() const { return pos.v[2] < kRadius + kGrassHeight; }
+
+    // How deep the ball sits in the grass (0 to 1, before it lands on the ground) and how hard the
+    // landing was.
+    struct Contact {
+        float grass, impact;
+    };
+    // Gravity and air drag, then the ground: a falling ball bounces back up, losing speed, and the
+    // ball never sinks below its radius.
+    HD Contact Land() {
+        Contact c{0.0f, 0.0f};
+        mom.v[2] = mom.v[2] + kGravity * kDt;
+        const float speed = mom.Length();
+        const float dragged = speed - kDrag * (speed * speed) * kDt;
+        mom = mom.Normalized(0) * dragged;
+        const float depth = Clamp(1.0f - ((pos.v[2] - 0.11f) / kGrassHeight), 0.0f, 1.0f);
+        c.grass = libm::PowfPos(depth, 0.7f);
+        if (pos.v[2] < 0.11f) {
+            if (mom.v[2] < 0.0f) {
+                c.impact = NormalizedClamp(-mom.v[2] - 0.5f, 0.0f, 12.0f);
+                mom.v[2] = -mom.v[2] * kBounce;
+                const float up = mom.v[2] - kLinearBounce;
+                mom.v[2] = up > 0.0f ? up : 0.0f;
+            }
+            pos.v[2] = 0.11f;
+        }
+        return c;
+    }
+    // Rolling friction of the grass on the horizontal momentum.
+    HD void RubGrass(const Contact &c) {
+        const float rub = (kFriction * c.grass);
+        Vec3 flat = mom.Get2D();
+        const float speed = flat.Length();
+        float slowed = speed - rub * (speed * speed) * kDt;
+        slowed = Clamp(slowed - (kLinearFriction * c.grass * kDt), 0.0f, 100000.0f);
+        flat.Normalize(Vec3(0));
+        flat *= slowed;
+        mom.v[0] = flat.v[0];
+        mom.v[1] = flat.v[1];
+    }
+    // A ball touching a post bounces off it around the post, one touching the crossbar around the
+    // bar, each keeping 80% of the speed it had across it.
+    HD void HitFrame() {
+        const float reach = kRadius + kPostRadius;
+        if (pos.v[2] < kGoalHeight + kRadius + kPostRadius &&
+            (pos.Get2D().Absolute() - Vec3(kPitchHalfLength, kGoalHalfWidth, 0)).Length() < reach) {
+            const Vec3 post(pos.v[0] < 0 ? -kPitchHalfLength : kPitchHalfLength, pos.v[1] < 0 ? -kGoalHalfWidth : kGoalHalfWidth, 0);
+            const Vec3 away = (pos.Get2D() - post).Normalized(pos.v[0] < 0 ? Vec3(1, 0, 0) : Vec3(-1, 0, 0));
+            const float z = pos.v[2];
+            pos = post + away * (kPostRadius + kRadius);
+            pos.v[2] = z;
+            mom = (mom.Get2D().Normalized(away) + (away * 1.1f)).Normalized() * mom.Get2D().Length() * kPostAbsorb +
+                  (Vec3(0, 0, 1) * mom.v[2]);
+        }
+        const Vec3 side = pos * Vec3(1, 0, 1);
+        if ((side.Absolute() - Vec3(kPitchHalfLength, 0, kGoalHeight)).Length() < reach &&
+            fabsf(pos.v[1]) < kGoalHalfWidth + kRadius + kPostRadius) {
+            const Vec3 bar = pos.v[0] < 0 ? Vec3(-kPitchHalfLength, 0, kGoalHeight) : Vec3(kPitchHalfLength, 0, kGoalHeight);
+            const Vec3 away = (side - bar).Normalized(pos.v[0] < 0 ? Vec3(0, 0, 1) : Vec3(0, 0, -1));
+            const float y = pos.v[1];
+            pos = bar + away * (kPostRadius + kRadius);
+            pos.v[1] = y;
+            const Vec3 across = mom * Vec3(1, 0, 1);
+            mom = (across.Normalized(away) + (away * 1.1f)).Normalized() * across.Length() * kPostAbsorb + (Vec3(0, 1, 0) * mom.v[1]);
+        }
+    }
+    // Inside the goal, past the line, the side nettings, the back netting and the roof push the
+    // ball back in. Returns whether a netting touched it.
+    HD bool PushNet(bool inGoal) {
+        if (!inGoal) return false;
+        const float sign = 1;  // the nettings push a ball in the goal back toward the pitch
+        const bool behind = fabsf(pos.v[0]) > kPitchHalfLength + 0.11f;
+        if (!behind) return false;
+        const bool beforeBack = fabsf(pos.v[0]) < kPitchHalfLength + kGoalDepth - 0.11f;
+        const bool below = pos.v[2] < kGoalHeight + 0.11f;
+        const bool between = fabsf(pos.v[1]) < kGoalHalfWidth - 0.11f;
+        bool touched = false;
+        if (!between) {
+            const float reach = Clamp(fabsf(fabsf(pos.v[1]) - kGoalHalfWidth), 0, 1);
+            const float push = libm::powf(reach, kNetExponent) * -SignSide(pos.v[1]) * sign;
+            const float tension = Clamp((fabsf(mom.v[0]) - kPitchHalfLength) * 2.0f, 0.0f, 1.0f);
+            const float power = kNetPower + (1.0f - tension) * 3.0f;
+            mom.v[1] = mom.v[1] * kNetAbsorb + push * power * (100 * kDt);
+            touched = true;
+        }
+        if (!beforeBack) {
+            const float reach = Clamp(fabsf(fabsf(pos.v[0]) - (kPitchHalfLength + kGoalDepth)), 0, 1);
+            const float push = libm::powf(reach, kNetExponent) * -SignSide(pos.v[0]) * sign;
+            mom.v[0] = mom.v[0] * kNetAbsorb + push * kNetPower * (100 * kDt);
+            touched = true;
+        }
+        if (!below) {
+            const float reach = Clamp(fabsf(fabsf(pos.v[2]) - kGoalHeight), 0, 1);
+            const float push = libm::powf(reach, kNetExponent) * -sign;
+            const float tension = Clamp((fabsf(mom.v[0]) - kPitchHalfLength) * 2.0f, 0.0f, 1.0f);
+            const float power = kNetPower + (1.0f - tension) * 3.0f;
+            mom.v[2] = mom.v[2] * kNetAbsorb + push * power * (100 * kDt);
+            touched = true;
+        }
+        return touched;
+    }
+    // A ball on the grass turns toward rolling without slipping, the turn per ms bounded by the
+    // grass (more after a hard landing), and its momentum leans toward the rolling speed.
+    HD void Roll(const Contact &c) {
+        const float spinX = mom.v[1] / kRadius, spinY = mom.v[0] / kRadius;
+        Quat rx, ry;
+        rx.SetAngleAxis(Clamp(spinX * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(-1, 0, 0));
+        ry.SetAngleAxis(Clamp(spinY * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(0, 1, 0));
+        const Quat rolling = rx * ry;
+        Quat toRolling = rot.RotationTo(rolling).Normalized();
+        const float change = fabsf(toRolling.RotationAngle(Quat::Identity())) * 1000.0f;
+        float bound = 1.0f * PI * c.grass;
+        if (c.impact > 0.0f) bound += 4.0f * PI;
+        float share = 1.0f;
+        if (change > bound) share = bound / change;
+        if (share < 1.0f) toRolling = toRolling.RotationMultipliedBy(share);
+        const Quat turned = toRolling * rot;
+        const Vec3 a = Angles();
+        const float x = -a.v[0], y = a.v[1];
+        const float rollX = y * kRadius * 1000.0f, rollY = x * kRadius * 1000.0f;
+        float lean = 0.01f;
+        lean *= c.grass;
+        if (c.impact > 0.0f) lean += 0.5f * c.impact;
+        lean = Clamp(lean, 0.0f, 1.0f);
+        mom.v[0] = mom.v[0] * (1.0f - lean) + rollX * lean;
+        mom.v[1] = mom.v[1] * (1.0f - lean) + rollY * lean;
+        rot = turned;
+        anglesKnown = false;
+    }
+    // The Magnus force of the spin bends the momentum, strongest at middling speeds.
+    HD void Swerve() {
+        Vec3 spin = Angles();
+        spin *= 10.0f;
+        float strength = NormalizedClamp(mom.Length(), 0.0f, 70.0f);
+        strength = libm::PowfPos(libm::sinf(strength * PI * 0.94f), 2.6f);
+        const Vec3 along = mom.Normalized(0) * strength * 30.0f;
+        const Vec3 bend = along.Cross(-spin) * 1.0f;
+        mom += bend * kDt;
+    }
+};
+
 // The prediction is a function of the ball's position, orientation, momentum and rotation and of
 // whether it is in the goal. When those match the last full prediction bit for bit, its first step
 // lands on entry 1; unless the cached path applies, the full path would write exactly what the
@@ -49,177 +213,49 @@ HDN BallSpatial BallCalculatePrediction(Ball &ball, bool ballIsInGoal) {
     }
     const Vec3 inPosition = ball.positionBuffer, inMomentum = ball.momentum;
     const Quat inOrientation = ball.orientationBuffer, inRotation = ball.rotationPerMs;
-    const float bounce = 0.62f, linearBounce = 0.06f, drag = 0.015f, friction = 0.04f,
-                linearFriction = 1.6f, gravity = -9.81f, grassHeight = 0.025f, dt = 0.01f;
+    BallFlight f;
+    f.pos = ball.positionBuffer;
+    f.mom = ball.momentum;
+    f.rot = ball.rotationPerMs;
+    Quat orientation = ball.orientationBuffer;
     BallSpatial out;
-    Vec3 nextPos = ball.positionBuffer;
-    Quat nextOri = ball.orientationBuffer;
-    Vec3 mom = ball.momentum;
-    Quat rot = ball.rotationPerMs;
-    ball.predictions[0] = nextPos;
-    bool firstTime = true, useCache = false;
-    Vec3 angles;
-    bool anglesValid = false;
-    auto curAngles = [&]() {
-        if (!anglesValid) {
-            rot.Angles(angles.v[0], angles.v[1], angles.v[2]);
-            anglesValid = true;
-        }
-        return angles;
-    };
+    ball.predictions[0] = f.pos;
     ball.touchesNet = false;
+    bool useCache = false;
     for (uint32_t t = 10; t < kBallPredictionSpanMs + kCachedPredictions * 10; t += 10) {
         if (useCache) {
             // GRF: the last shift reads predictions[400], which no tick writes.
             ShiftPredictions(ball);
             break;
         }
-        float frictionFactor = 0.0f;
-        mom.v[2] = mom.v[2] + gravity * dt;
-        float vel = mom.Length();
-        float velDragged = vel - drag * (vel * vel) * dt;
-        mom = mom.Normalized(0) * velDragged;
-        float bottom = nextPos.v[2] - 0.11f;
-        float grass = Clamp(1.0f - (bottom / grassHeight), 0.0f, 1.0f);
-        grass = libm::PowfPos(grass, 0.7f);
-        if (nextPos.v[2] < 0.11f) {
-            if (mom.v[2] < 0.0f) {
-                frictionFactor = NormalizedClamp(-mom.v[2] - 0.5f, 0.0f, 12.0f);
-                mom.v[2] = -mom.v[2] * bounce;
-                float bv = mom.v[2] - linearBounce;
-                mom.v[2] = bv > 0.0f ? bv : 0.0f;
-            }
-            nextPos.v[2] = 0.11f;
+        const bool first = t == 10;
+        const BallFlight::Contact contact = f.Land();
+        if (f.InGrass()) f.RubGrass(contact);
+        // GRF: the posts, the crossbar and the netting act on the first step only.
+        if (first) {
+            f.HitFrame();
+            if (f.PushNet(ballIsInGoal)) ball.touchesNet = true;
         }
-        if (nextPos.v[2] < 0.11f + grassHeight) {
-            float af = (friction * grass);
-            Vec3 hm = mom.Get2D();
-            float hv = hm.Length();
-            float nv = hv - af * (hv * hv) * dt;
-            nv = Clamp(nv - (linearFriction * grass * dt), 0.0f, 100000.0f);
-            hm.Normalize(Vec3(0));
-            hm *= nv;
-            mom.v[0] = hm.v[0];
-            mom.v[1] = hm.v[1];
-        }
-        const float netExponent = 2.6f, powerFactor = 1.8f, postAbsorb = 0.8f, ballR = 0.11f,
-                    postR = 0.07f, netAbsorb = 0.95f;
-        // GRF: the posts and the crossbar act on the first step only.
-        if (firstTime) {
-            if (nextPos.v[2] < kGoalHeight + ballR + postR &&
-                (nextPos.Get2D().Absolute() - Vec3(kPitchHalfLength, kGoalHalfWidth, 0)).Length() < ballR + postR) {
-                float sx = nextPos.v[0] < 0 ? -kPitchHalfLength : kPitchHalfLength;
-                float sy = nextPos.v[1] < 0 ? -kGoalHalfWidth : kGoalHalfWidth;
-                Vec3 fallback = nextPos.v[0] < 0 ? Vec3(1, 0, 0) : Vec3(-1, 0, 0);
-                Vec3 post(sx, sy, 0);
-                Vec3 normal = (nextPos.Get2D() - post).Normalized(fallback);
-                float z = nextPos.v[2];
-                nextPos = post + normal * (postR + ballR);
-                nextPos.v[2] = z;
-                mom = (mom.Get2D().Normalized(normal) + (normal * 1.1f)).Normalized() * mom.Get2D().Length() * postAbsorb +
-                      (Vec3(0, 0, 1) * mom.v[2]);
-            }
-            Vec3 xz = nextPos * Vec3(1, 0, 1);
-            if ((xz.Absolute() - Vec3(kPitchHalfLength, 0, kGoalHeight)).Length() < ballR + postR &&
-                fabsf(nextPos.v[1]) < kGoalHalfWidth + ballR + postR) {
-                Vec3 bar = nextPos.v[0] < 0 ? Vec3(-kPitchHalfLength, 0, kGoalHeight) : Vec3(kPitchHalfLength, 0, kGoalHeight);
-                Vec3 fallback = nextPos.v[0] < 0 ? Vec3(0, 0, 1) : Vec3(0, 0, -1);
-                Vec3 normal = (xz - bar).Normalized(fallback);
-                float y = nextPos.v[1];
-                nextPos = bar + normal * (postR + ballR);
-                nextPos.v[1] = y;
-                Vec3 mxz = mom * Vec3(1, 0, 1);
-                mom = (mxz.Normalized(normal) + (normal * 1.1f)).Normalized() * mxz.Length() * postAbsorb +
-                      (Vec3(0, 1, 0) * mom.v[1]);
-            }
-        }
-        // GRF: the netting too acts on the first step only.
-        if (t <= 10) {
-            int inGoal = ballIsInGoal ? 1 : -1;
-            bool behind = fabsf(nextPos.v[0]) > kPitchHalfLength + 0.11f;
-            bool beforeBack = fabsf(nextPos.v[0]) < kPitchHalfLength + kGoalDepth - 0.11f;
-            bool below = nextPos.v[2] < kGoalHeight + 0.11f;
-            bool between = fabsf(nextPos.v[1]) < kGoalHalfWidth - 0.11f;
-            if (ballIsInGoal && !between && behind) {
-                float nd = Clamp(fabsf(fabsf(nextPos.v[1]) - kGoalHalfWidth), 0, 1);
-                float power = libm::powf(nd, netExponent) * -SignSide(nextPos.v[1]) * inGoal;
-                float tension = Clamp((fabsf(mom.v[0]) - kPitchHalfLength) * 2.0f, 0.0f, 1.0f);
-                float apf = powerFactor + (1.0f - tension) * 3.0f;
-                mom.v[1] = mom.v[1] * netAbsorb + power * apf * (100 * dt);
-                if (t == 10) ball.touchesNet = true;
-            }
-            if (ballIsInGoal && !beforeBack && behind) {
-                float nd = Clamp(fabsf(fabsf(nextPos.v[0]) - (kPitchHalfLength + kGoalDepth)), 0, 1);
-                float power = libm::powf(nd, netExponent) * -SignSide(nextPos.v[0]) * inGoal;
-                mom.v[0] = mom.v[0] * netAbsorb + power * powerFactor * (100 * dt);
-                if (t == 10) ball.touchesNet = true;
-            }
-            if (ballIsInGoal && !below && behind) {
-                float nd = Clamp(fabsf(fabsf(nextPos.v[2]) - kGoalHeight), 0, 1);
-                float power = libm::powf(nd, netExponent) * -inGoal;
-                float tension = Clamp((fabsf(mom.v[0]) - kPitchHalfLength) * 2.0f, 0.0f, 1.0f);
-                float apf = powerFactor + (1.0f - tension) * 3.0f;
-                mom.v[2] = mom.v[2] * netAbsorb + power * apf * (100 * dt);
-                if (t == 10) ball.touchesNet = true;
-            }
-        }
-        if (nextPos.v[2] < 0.11f + grassHeight) {
-            const float radius = 0.11f;
-            float avx = mom.v[1] / radius, avy = mom.v[0] / radius;
-            Quat rx, ry;
-            rx.SetAngleAxis(Clamp(avx * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(-1, 0, 0));
-            ry.SetAngleAxis(Clamp(avy * 0.001f, -PI * 0.49f, PI * 0.49f), Vec3(0, 1, 0));
-            Quat ground = rx * ry;
-            Quat o2n = rot.RotationTo(ground).Normalized();
-            float change = fabsf(o2n.RotationAngle(Quat::Identity())) * 1000.0f;
-            float maxChange = 1.0f * PI * grass;
-            if (frictionFactor > 0.0f) maxChange += 4.0f * PI;
-            float factor = 1.0f;
-            if (change > maxChange) factor = maxChange / change;
-            if (factor < 1.0f) o2n = o2n.RotationMultipliedBy(factor);
-            Quat newRot = o2n * rot;
-            const Vec3 a = curAngles();
-            float x = -a.v[0], y = a.v[1];
-            Vec3 rm;
-            rm.v[0] = y * radius * 1000.0f;
-            rm.v[1] = x * radius * 1000.0f;
-            float rb = 0.01f;
-            rb *= grass;
-            if (frictionFactor > 0.0f) rb += 0.5f * frictionFactor;
-            rb = Clamp(rb, 0.0f, 1.0f);
-            mom.v[0] = mom.v[0] * (1.0f - rb) + rm.v[0] * rb;
-            mom.v[1] = mom.v[1] * (1.0f - rb) + rm.v[1] * rb;
-            rot = newRot;
-            anglesValid = false;
-        }
-        {
-            Vec3 spin = curAngles();
-            spin *= 10.0f;
-            float swerve = NormalizedClamp(mom.Length(), 0.0f, 70.0f);
-            swerve = libm::PowfPos(libm::sinf(swerve * PI * 0.94f), 2.6f);
-            Vec3 adapted = mom.Normalized(0) * swerve * 30.0f;
-            Vec3 sw = adapted.Cross(-spin) * 1.0f;
-            mom += sw * dt;
-        }
-        nextPos += mom * dt;
-        if (t == 10) {
-            Vec3 rv = curAngles();
-            rv *= dt / 0.001f;
+        if (f.InGrass()) f.Roll(contact);
+        f.Swerve();
+        f.pos += f.mom * BallFlight::kDt;
+        if (first) {
+            Vec3 turn = f.Angles();
+            turn *= BallFlight::kDt / 0.001f;
             Quat step;
-            step.SetAngles(rv.v[0], rv.v[1], rv.v[2]);
-            nextOri = step * nextOri;
-            out.momentum = mom;
-            out.rotationPerMs = rot;
-            ball.orientationPrediction = nextOri;
-            if (ball.validPredictions > 0 && ball.predictions[2] == nextPos) {
+            step.SetAngles(turn.v[0], turn.v[1], turn.v[2]);
+            orientation = step * orientation;
+            out.momentum = f.mom;
+            out.rotationPerMs = f.rot;
+            ball.orientationPrediction = orientation;
+            if (ball.validPredictions > 0 && ball.predictions[2] == f.pos) {
                 ball.validPredictions--;
                 useCache = true;
             } else {
                 ball.validPredictions = kCachedPredictions;
             }
         }
-        ball.predictions[t / 10] = nextPos;
-        firstTime = false;
+        ball.predictions[t / 10] = f.pos;
     }
     ball.memoValid = !useCache;
     if (!useCache) {

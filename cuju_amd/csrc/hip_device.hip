@@ -264,9 +264,12 @@ std::unique_ptr<Device> MakeHipDevice16(int matches);
 std::unique_ptr<Device> MakeHipDevice32(int matches);
 std::unique_ptr<Device> MakeHipDevice64(int matches);
 
-// One wavefront for each SIMD where the batch allows it: the matches of a wavefront are the
-// environments over the SIMDs, 1 to 32, and the group is the widest of 16, 8, 4 or 2 lanes that
-// those matches leave room for in 64. CUJU_AMD_MATCHES sets the matches of a wavefront instead.
+// Two wavefronts for each SIMD where the batch allows it: the matches of a wavefront are the
+// environments over the wavefront slots, 1 to 32, and the group is the widest of 64, 32, 16, 8, 4
+// or 2 lanes that those matches leave room for in 64 (measured on an MI355X: one match of 64 lanes
+// steps 64 environments of 5-a-side in 17.7 ms at the median against 18.5 at 16 lanes; two of 32
+// step 4,096 of 11-a-side in 88.5 ms against 90.4 at 2 x 16). CUJU_AMD_MATCHES sets the matches of
+// a wavefront instead.
 std::unique_ptr<Device> MakeLibraryDevice(int, int environments) {
     int device = 0, units = 0;
     Check(hipGetDevice(&device), "hipGetDevice");
@@ -287,6 +290,8 @@ std::unique_ptr<Device> MakeLibraryDevice(int, int environments) {
         default: throw std::invalid_argument("CUJU_AMD_LANES must be 2, 4, 8, 16, 32 or 64");
         }
     }
+    if (matches == 1) return MakeHipDevice64(1);
+    if (matches == 2) return MakeHipDevice32(2);
     if (matches <= 4) return MakeHipDevice16(matches);
     if (matches <= 8) return MakeHipDevice8(matches);
     if (matches <= 16) return MakeHipDevice4(matches);

@@ -35,7 +35,7 @@ RANGE = 8
 CHECKPOINTS = (3000, 5000, 10000)
 
 # Environments per wavefront that the library gives each workload's full batch on an MI355X (256
-# compute units, two wavefronts per SIMD): 1 x 16 lanes for 64 environments, 2 x 16 for 4,096,
+# compute units, two wavefronts per SIMD): 1 x 64 lanes for 64 environments, 2 x 32 for 4,096,
 # 8 x 8 for 16,384, 4 x 16 for 8,192 and 16 x 4 for 32,768.
 PRODUCTION_MATCHES = {1: 1, 2: 2, 3: 8, 4: 4, 5: 16}
 # Wavefronts of the end range, which plays at the full batch's geometry.

@@ -24,21 +24,29 @@ from conftest import PRODUCT, digest_actions
 
 
 @contextlib.contextmanager
-def matches_per_wavefront(matches):
-    """Batches created inside put `matches` environments in each wavefront."""
-    before = os.environ.get('CUJU_AMD_MATCHES')
-    os.environ['CUJU_AMD_MATCHES'] = str(matches)
+def matches_per_wavefront(matches, lanes=None):
+    """Batches created inside put `matches` environments in each wavefront, of `lanes` lanes each
+    (by default the library's choice for that many)."""
+    settings = {'CUJU_AMD_MATCHES': str(matches), 'CUJU_AMD_LANES': None if lanes is None else str(lanes)}
+    before = {name: os.environ.get(name) for name in settings}
+    for name, value in settings.items():
+        if value is None:
+            os.environ.pop(name, None)
+        else:
+            os.environ[name] = value
     try:
         yield
     finally:
-        if before is None:
-            os.environ.pop('CUJU_AMD_MATCHES', None)
-        else:
-            os.environ['CUJU_AMD_MATCHES'] = before
+        for name, value in before.items():
+            if value is None:
+                os.environ.pop(name, None)
+            else:
+                os.environ[name] = value
 
 
 def one_match_per_wavefront():
-    return matches_per_wavefront(1)
+    """One environment of 16 lanes in each wavefront."""
+    return matches_per_wavefront(1, 16)
 
 
 def uncaptured(capsys):

@@ -9,7 +9,7 @@ its own:
   (`tests/golden/episodes.json`, written by `tests/golden/make_episodes.py`): the end of the
   workload's index range (`first_index`) in four full wavefronts, 8 environments of 8 lanes each
   for the 16,384-environment workload, 16 of 4 lanes for the 32,768-environment mixed batch, 4 of
-  16 for the 8,192 self-play batch, 2 of 16 for 4,096, and 1 of 16 for the 64 environments of
+  16 for the 8,192 self-play batch, 2 of 32 for 4,096, and 1 of 64 for the 64 environments of
   workload 1, whose start range (8 environments) plays too. `CUJU_AMD_LONG_RANGES=all` adds the
   start range of every workload, one environment to a wavefront.
 

@@ -71,8 +71,7 @@ def test_every_geometry_matches_the_reference(matches, lanes, reference_library,
     state. 8 matches of 8 lanes is the geometry of the headline batch of 16,384; the 32- and
     64-lane builds take a whole half or whole wavefront per match (CUJU_AMD_LANES)."""
     monkeypatch.setenv('CUJU_AMD_MATCHES', str(matches))
-    if lanes > 16:
-        monkeypatch.setenv('CUJU_AMD_LANES', str(lanes))
+    monkeypatch.setenv('CUJU_AMD_LANES', str(lanes))
     environments, steps = 48, 40
     mine = gpu_batch('11_vs_11_hard_stochastic_l11_r0', environment_count=environments, seed=2)
     theirs = ref.ReferenceBatch('11_vs_11_hard_stochastic_l11_r0', environment_count=environments, seed=2,
@@ -95,12 +94,12 @@ def test_every_geometry_matches_the_reference(matches, lanes, reference_library,
 
 def test_the_geometry_fills_the_simds():
     """Two wavefronts for each SIMD where the batch allows: 32 environments of 2 lanes at 65,536,
-    16 of 4 lanes at 32,768, 8 of 8 lanes at 16,384, 4 of 16 lanes at 8,192, 2 of 16 lanes at
-    4,096 and one of 16 lanes for a small batch (memory_estimate sizes these without allocating)."""
+    16 of 4 lanes at 32,768, 8 of 8 lanes at 16,384, 4 of 16 lanes at 8,192, 2 of 32 lanes at
+    4,096 and one of 64 lanes, a whole wavefront, for a small batch."""
     import cuju_amd
     slots = 2 * 4 * torch.cuda.get_device_properties(0).multi_processor_count
-    expected = {32 * slots: (32, 2), 16 * slots: (16, 4), 8 * slots: (8, 8), 4 * slots: (4, 16), 2 * slots: (2, 16),
-                64: (1, 16)}
+    expected = {32 * slots: (32, 2), 16 * slots: (16, 4), 8 * slots: (8, 8), 4 * slots: (4, 16), 2 * slots: (2, 32),
+                64: (1, 64)}
     for environments, geometry in expected.items():
         batch = cuju_amd.BatchEnvironment('academy_empty_goal_close', library=PRODUCT, device='cuda:0',
                                           environment_count=environments)

@@ -68,12 +68,12 @@ class DigestRun:
     SHA-256 over the reset observation, every step's observation, reward and done, then every
     environment's state."""
 
-    def __init__(self, name, case, environments, seed, steps):
+    def __init__(self, name, case, environments, seed, steps, stream=None):
         import cuju_amd
         self.name, self.case, self.environments, self.steps = name, case, environments, steps
         self.batch = cuju_amd.BatchEnvironment(case['assets'], library=PRODUCT, device='cuda:0',
                                                environment_count=environments, seed=seed, **dict(case['options']))
-        self.stream = torch.cuda.Stream()
+        self.stream = stream or torch.cuda.Stream()
         self.step = 0
 
     def start(self):
@@ -96,6 +96,9 @@ class DigestRun:
         if self.done and self.batch.stack == 1:
             for index in range(self.environments):
                 self.digest.update(self.batch.get_state(index))
+
+    def ready(self):
+        return self.stream.query()
 
     @property
     def done(self):
@@ -127,3 +130,66 @@ def play(runs, label='lockstep', every=250, report=print):
         step += 1
         if every and step % every == 0:
             report(f'{label}: step {step}, {len(live)} batches running, {time.time() - begin:.0f} s')
+
+
+def concurrent_streams(k, candidates=16, spin=4_000_000):
+    """Up to `k` streams whose kernels run side by side: HIP spreads streams over a few hardware
+    queues, and the kernels of streams that share one run one after another. Each candidate joins
+    the chosen ones if a spin kernel on it and on every chosen stream together takes about as long
+    as one alone."""
+    def together(streams):
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for st in streams:
+            with torch.cuda.stream(st):
+                torch.cuda._sleep(spin)
+        torch.cuda.synchronize()
+        return time.perf_counter() - start
+    pool = [torch.cuda.Stream() for _ in range(candidates)]
+    together(pool[:1])
+    alone = min(together(pool[:1]) for _ in range(3))
+    chosen = [pool[0]]
+    for st in pool[1:]:
+        if len(chosen) == k:
+            break
+        if together(chosen + [st]) < 1.5 * alone:
+            chosen.append(st)
+    return chosen
+
+
+def play_lanes(lanes, label='lanes', every_s=30.0, report=print):
+    """Plays lanes of runs: each lane is a list of runs that play one after another on the lane's
+    stream, every lane at its own pace (one step of each lane in flight; a lane whose step has
+    finished is collected and launched again at once). A run has start(), launch(), ready(),
+    collect(), done and step."""
+    cursors = [0] * len(lanes)
+    active = []
+    for i, lane in enumerate(lanes):
+        if lane:
+            lane[0].start()
+            active.append(i)
+    for i in active:
+        lanes[i][0].launch()
+    begin = last = time.time()
+    while active:
+        progressed = False
+        for i in list(active):
+            run = lanes[i][cursors[i]]
+            if not run.ready():
+                continue
+            run.collect()
+            progressed = True
+            if run.done:
+                cursors[i] += 1
+                if cursors[i] == len(lanes[i]):
+                    active.remove(i)
+                    continue
+                run = lanes[i][cursors[i]]
+                run.start()
+            run.launch()
+        if not progressed:
+            time.sleep(0.0005)
+        if every_s and time.time() - last >= every_s:
+            last = time.time()
+            state = '; '.join(f'lane {i}: {lanes[i][cursors[i]].name} step {lanes[i][cursors[i]].step}' for i in active)
+            report(f'{label}: {last - begin:.0f} s; {state}')

@@ -1,28 +1,20 @@
-"""Long horizons on the MI355X, in one loop so that every batch runs at once, each on a stream of
-its own:
+"""Long horizons on the MI355X, every batch on a stream of its own, each stream at its own pace:
 
 * the reference's five long digests (python/cuju/data/digests.json `long_cases`): full 3,010-step
-  matches and 1,500-2,000-step drill runs with raw, SMM and checkpoint outputs, 4 environments each
-  (the reference's tests/test_long.py:59-69);
-* long episodes of each of the five benchmark workloads at the geometry the workload's full batch
-  gets, as the benchmark runs it, against per-environment digests of the reference CPU library
-  (`tests/golden/episodes.json`, written by `tests/golden/make_episodes.py`): the end of the
-  workload's index range (`first_index`) in four full wavefronts, 8 environments of 8 lanes each
-  for the 16,384-environment workload, 16 of 4 lanes for the 32,768-environment mixed batch, 4 of
-  16 for the 8,192 self-play batch, 2 of 32 for 4,096, and 1 of 64 for the 64 environments of
-  workload 1, whose start range (8 environments) plays too. `CUJU_AMD_LONG_RANGES=all` adds the
-  start range of every workload, one environment to a wavefront.
+  matches and 1,500-2,000-step drill runs with raw, SMM and checkpoint outputs, 4 environments each,
+  one environment of 16 lanes to a wavefront (the reference's tests/test_long.py:59-69);
+* 10,000 steps of each of the five benchmark workloads at the geometry the workload's full batch
+  gets, as the benchmark runs it (8 environments of 8 lanes to a wavefront for the
+  16,384-environment headline, 16 of 4 for the 32,768-environment mixed batch, 4 of 16 for the
+  8,192 self-play batch, 2 of 32 for 4,096, 1 of 64 for 64): one batch of four blocks, one
+  wavefront each, that play global steps 0-3,000, 2,500-5,500, 5,000-8,000 and 7,000-10,000 of
+  the same environments (`segments.py`), against the reference CPU library playing the same
+  batch, and block 0 against the committed goldens at step 3,000 (`tests/golden/episodes.json`,
+  written by `tests/golden/make_episodes.py`).
 
-Horizons: 5,000 steps for the 16,384-environment workload (the headline), 3,000 for the others;
-`CUJU_AMD_EPISODE_STEPS` sets one horizon for all (10,000 is the last golden checkpoint).
-
-The long digests put one environment in a wavefront (`lockstep.one_match_per_wavefront`): a step
-of a small batch then takes the time of one match. HIP spreads the streams over the process's
-hardware queues (4 by default), and the batches that share a queue run one after another, so a
-lockstep step costs about a quarter of the sum of the batches' own step times; the batches are
-made in order of falling cost, so that the costly ones land on different queues.
-`CUJU_AMD_LONG_PARTS` (default `digests,1,2,3,4,5`) names the parts to play, so a 10,000-step run
-can be split over several processes.
+HIP spreads the streams over the process's hardware queues (4 by default); batches that share a
+queue run one after another. `CUJU_AMD_LONG_PARTS` (default `digests,1,2,3,4,5`) names the parts
+to play.
 """
 
 import hashlib
@@ -35,7 +27,7 @@ import torch
 
 import episodes
 import lockstep
-from conftest import PRODUCT, ROOT, load_digests
+from conftest import PRODUCT, REFERENCE, ROOT, load_digests
 from cuju_amd import workloads
 
 pytestmark = pytest.mark.gpu
@@ -47,66 +39,15 @@ def host(x):
     return x.detach().cpu().numpy()
 
 
-# Horizon of each workload's episodes unless CUJU_AMD_EPISODE_STEPS sets one for all.
-HORIZONS = {3: 5000}
-DEFAULT_HORIZON = 3000
-# A lockstep step's cost of a batch, by environments per wavefront (ms, measured alone on an MI355X):
-# the order in which batches take streams.
-COST = {1: 20, 2: 30, 4: 41, 8: 60, 16: 77}
-
-
-class DeviceSide:
-    """A `cuju_amd.BatchEnvironment` of one workload range on its own stream, `matches`
-    environments to a wavefront."""
-
-    def __init__(self, workload, first_index, count, drill_paths, matches):
-        import cuju_amd
-        options = workload.batch_options(first_index, count, drill_paths)
-        assets = options.pop('assets')
-        with lockstep.matches_per_wavefront(matches):
-            self.batch = cuju_amd.BatchEnvironment(assets, library=PRODUCT, device='cuda:0',
-                                                   seed=episodes.seed_of(workload), **options)
-        got, lanes = self.batch.geometry
-        assert got == matches, f'asked for {matches} environments per wavefront, the batch has {got}'
-        self.geometry = f'{got} x {lanes} lanes'
-        self.stream = torch.cuda.Stream()
-        self.stacked = workload.stacked
-
-    def reset(self):
-        with torch.cuda.stream(self.stream):
-            obs = self.batch.reset()
-        self.stream.synchronize()
-        return host(obs)
-
-    def reset_masked(self, mask, seeds):
-        with torch.cuda.stream(self.stream):
-            obs = self.batch.reset(seeds=seeds, mask=torch.as_tensor(mask.astype(bool)))
-        self.stream.synchronize()
-        return host(obs)
-
-    def launch(self, actions):
-        with torch.cuda.stream(self.stream):
-            self.out = self.batch.step(torch.as_tensor(actions, device='cuda:0'))
-
-    def collect(self):
-        self.stream.synchronize()
-        obs, reward, done, info = self.out
-        done = host(done).astype(np.uint8)
-        final = host(info['final_observation']) if done.any() else None
-        return host(obs), host(reward), done, final
-
-    def state(self, index):
-        state = self.batch.get_state(index, stacked=self.stacked)
-        return episodes.engine_bytes(state) if self.stacked else state
-
-    def close(self):
-        self.batch.close()
+# Seconds the four-block batch of each workload takes for its 3,000 steps alone on an MI355X.
+BLOCK_SECONDS = {1: 54, 2: 90, 3: 222, 4: 123, 5: 231}
 
 
 def test_long_horizons_match_the_reference(tmp_path, capsys):
+    import concurrent.futures
+    import segments
     with open(GOLDEN) as f:
         golden = json.load(f)
-    forced = os.environ.get('CUJU_AMD_EPISODE_STEPS')
     drill_paths = workloads.drill_bundles(str(tmp_path / 'drills'))
     built = {os.path.basename(p): hashlib.sha256(open(p, 'rb').read()).hexdigest() for p in drill_paths}
     assert built == golden['drill_bundles'], 'the drill bundles differ from the reference builder\'s'
@@ -115,41 +56,70 @@ def test_long_horizons_match_the_reference(tmp_path, capsys):
     parts = {p.strip() for p in parts.split(',') if p.strip()}
     unknown = parts - {'digests'} - {str(n) for n in workloads.WORKLOADS}
     assert not unknown, f'CUJU_AMD_LONG_PARTS names no part {sorted(unknown)}'
-    every_range = os.environ.get('CUJU_AMD_LONG_RANGES', 'production') == 'all'
     report = lockstep.uncaptured(capsys)
+    numbers = sorted(n for n in workloads.WORKLOADS if str(n) in parts)
+    # The reference plays block 0's environments to the blocks' starting steps, all workloads at once.
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, len(numbers))) as pool:
+        states = dict(zip(numbers, pool.map(
+            lambda n: segments.starting_states(workloads.WORKLOADS[n], drill_paths, REFERENCE), numbers)))
+    report(f'reference states at steps {list(segments.STARTS[1:])} for workloads {numbers}')
+    oracle_pool = concurrent.futures.ThreadPoolExecutor(max_workers=max(1, len(numbers)))
+    expected = {n: oracle_pool.submit(segments.play_oracle, segments.BlockRun(
+        workloads.WORKLOADS[n], segments.OracleBlocks(workloads.WORKLOADS[n], drill_paths, REFERENCE), states[n]))
+        for n in numbers}
+    # Streams on distinct hardware queues (HIP gives the process four; some may be taken), each a
+    # lane that plays its batches one after another; the batches go to the least loaded lane by
+    # their cost, the seconds their steps take alone on an MI355X.
+    streams = lockstep.concurrent_streams(4, candidates=24)
+    report(f'{len(streams)} streams run side by side')
+    items = []
+    for n in numbers:
+        w = workloads.WORKLOADS[n]
+        items.append((BLOCK_SECONDS[n], ('blocks', n)))
     digests = load_digests()
-    planned = []
-    for number in sorted(n for n in workloads.WORKLOADS if str(n) in parts):
-        w = workloads.WORKLOADS[number]
-        horizon = int(forced) if forced else HORIZONS.get(number, DEFAULT_HORIZON)
-        checkpoints = [c for c in golden['checkpoints'] if c <= horizon]
-        assert checkpoints, f'no golden checkpoint at or below {horizon} steps'
-        for first, count, matches in episodes.sample_ranges(w):
-            if every_range or matches == episodes.PRODUCTION_MATCHES[number]:
-                planned.append((COST[matches], w, first, count, matches, checkpoints))
+    if 'digests' in parts:
+        for name, case in sorted(digests['long_cases'].items()):
+            items.append((case['steps'] * 0.020, ('digest', name)))
+    lanes = [[] for _ in streams]
+    load = [0.0] * len(streams)
     runs = []
     try:
-        for _, w, first, count, matches, checkpoints in sorted(planned, key=lambda p: -p[0]):
-            side = DeviceSide(w, first, count, drill_paths, matches)
-            run = episodes.EpisodeRun(w, first, count, side, checkpoints=checkpoints)
-            report(f'{run.name}: {side.geometry}, to step {max(checkpoints)}')
+        for cost, (kind, key) in sorted(items, key=lambda item: -item[0]):
+            lane = min(range(len(streams)), key=lambda i: load[i])
+            load[lane] += cost
+            if kind == 'blocks':
+                w = workloads.WORKLOADS[key]
+                side = segments.DeviceBlocks(w, drill_paths, PRODUCT, episodes.PRODUCTION_MATCHES[key], streams[lane])
+                matches, lanes_per_match = side.geometry
+                assert matches == episodes.PRODUCTION_MATCHES[key], (key, side.geometry)
+                run = segments.BlockRun(w, side, states[key])
+                report(f'lane {lane}: {run.name}: {matches} x {lanes_per_match} lanes, {run.count} environments, '
+                       f'{segments.SEGMENT} steps')
+            else:
+                case = digests['long_cases'][key]
+                with lockstep.one_match_per_wavefront():
+                    run = lockstep.DigestRun(key, case, digests['environments'], digests['seed'], case['steps'], streams[lane])
+                report(f'lane {lane}: long digest {key}, {case["steps"]} steps')
+            lanes[lane].append(run)
             runs.append(run)
-        if 'digests' in parts:
-            with lockstep.one_match_per_wavefront():
-                for name, case in sorted(digests['long_cases'].items()):
-                    runs.append(lockstep.DigestRun(name, case, digests['environments'], digests['seed'],
-                                                   case['steps']))
-        lockstep.play(runs, label='long horizons', report=report)
+        lockstep.play_lanes(lanes, label='long horizons', report=report)
         failed = [r.name for r in runs if isinstance(r, lockstep.DigestRun) and r.hexdigest() != r.case['digest']]
         for r in runs:
-            if isinstance(r, episodes.EpisodeRun):
-                expected = golden['workloads'][str(r.workload.number)][str(r.first_index)]
-                for checkpoint in r.checkpoints:
-                    for i, (got, want) in enumerate(zip(r.digests[checkpoint], expected[str(checkpoint)], strict=True)):
-                        if got != want:
-                            failed.append(f'{r.name}: environment {r.first_index + i} at step {checkpoint}')
-                report(f'{r.name}: {r.count} environments checked at steps {list(r.checkpoints)}')
+            if not isinstance(r, segments.BlockRun):
+                continue
+            n = r.workload.number
+            want = expected[n].result()
+            for i, (got, ref_digest) in enumerate(zip(r.digests, want, strict=True)):
+                if got != ref_digest:
+                    failed.append(f'{r.name}: block {i // r.m} environment {i % r.m} against the reference')
+            first = segments.first_index(r.workload)
+            goldens = golden['workloads'][str(n)][str(first)]['3000'][:r.m]
+            for i in range(r.m):
+                if want[i] != goldens[i]:
+                    failed.append(f'{r.name}: the reference\'s block 0 environment {i} against the goldens')
+            report(f'{r.name}: {r.count} environments checked, global steps 0-10,000')
         assert not failed, f'digests that differ from the reference: {failed}'
     finally:
+        oracle_pool.shutdown(wait=True)
         for r in runs:
-            (r.side if isinstance(r, episodes.EpisodeRun) else r).close()
+            r.side.close() if isinstance(r, segments.BlockRun) else r.close()

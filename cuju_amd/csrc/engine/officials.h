@@ -211,89 +211,157 @@ HDN Vec3 BallAveragePosition(const World &w, unsigned durationMs) {
 }
 
 // ---- officials ---------------------------------------------------------------------------------------
+// The officials' decisions are GRF's (include/cuju/simulation/officials.h); their organisation here
+// (a command toward a target, one function per duty, the humanoid tick in stages) is this engine's.
+
+// A command to move toward `target` at `velocity`, looking at `lookAt`; the direction falls back to
+// the humanoid's own when the target is where it stands.
+HD PlayerCommand HeadFor(const SpatialState &s, const Vec3 &target, float velocity, const Vec3 &lookAt) {
+    PlayerCommand c = DefaultPlayerCommand();
+    c.useDesiredMovement = true;
+    c.useDesiredLookAt = true;
+    c.desiredDirection = (target - s.position).Normalized(s.directionVec);
+    c.desiredVelocityFloat = velocity;
+    c.desiredLookAt = lookAt;
+    return c;
+}
+
+// The referee books the player of a foul that earns a card: walks to two metres of the offender,
+// then shows the card (special animation 3) and stands facing the offender.
+HD void RefereeBooksOffender(const World &w, const SpatialState &s, CommandQueue &q) {
+    const Vec3 pos = s.position;
+    const Vec3 offender = Sp(w, w.match.referee.foul.foulPlayer).position;
+    const Vec3 spot = offender + (pos - offender).Normalized(0) * (float)2.0;
+    if ((double)(pos - spot).Length() > 2.0) {
+        q.push_back(HeadFor(s, spot, RangeVelocity((spot - pos).Length() * 1.0f), offender));
+        return;
+    }
+    PlayerCommand card = DefaultPlayerCommand();
+    card.desiredFunctionType = kFnSpecial;
+    card.useSpecialVar1 = true;
+    card.specialVar1 = 3;
+    q.push_back(card);
+    q.push_back(HeadFor(s, spot, kIdleVelocity, offender));
+}
+
+// Otherwise the referee keeps near the recent play: drawn toward 60% of the ball's mean position
+// over two seconds, pushed off where the ball will be in 200 ms and off every player's place in
+// 400 ms, looking where the ball will be in 60 ms.
+HD void RefereeFollowsPlay(const World &w, const Ctx &ctx, const SpatialState &s, CommandQueue &q) {
+    const MatchState &m = w.match;
+    const Vec3 pos = s.position;
+    ForceField &field = ctx.ws->forceField;
+    field.clear();
+    field.push_back(MakeSpot(BallAveragePosition(w, 2000).Get2D() * 0.6f, kAttract, kDecayConstant, 0.5f));
+    field.push_back(MakeSpot(BallPredict(m.ball, 200).Get2D(), kRepel, kDecayVariable, 0.5f, 10.0f));
+    const int first = w.FirstTeamID();
+    for (int k = 0; k < 2; k++) {
+        const PlayerList players = TeamActivePlayers(w, k == 0 ? first : 1 - first);
+        for (int i = 0; i < players.count; i++) {
+            const SpatialState &p = Sp(w, players[i]);
+            field.push_back(MakeSpot(p.position + p.movement * 0.4f, kRepel, kDecayVariable, 0.5f, 10.0f));
+        }
+    }
+    const Vec3 target = pos + GetForceFieldMovement(field, pos);
+    const float velocity = Clamp((target - pos).Length() * kDistanceToVelocity * 0.5f, kIdleVelocity, kSprintVelocity);
+    q.push_back(HeadFor(s, target, velocity, BallPredict(m.ball, 60).Get2D()));
+}
+
+// A linesman runs along his touchline level with the offside line of the team defending his half,
+// 0.8 m outside the pitch, looking across it.
+HD void LinesmanFollowsLine(const World &w, const SpatialState &s, CommandQueue &q) {
+    const Vec3 pos = s.position;
+    const int latest = MentalImageIndex(w, 0);
+    const bool lowerTouchline = pos.v[1] < 0;
+    const float line = GetOffsideLine(w, latest, lowerTouchline ? 1 : 0);
+    const Vec3 target(line, lowerTouchline ? -(kPitchHalfWidth + 0.8f) : kPitchHalfWidth + 0.8f, 0);
+    q.push_back(HeadFor(s, target, RangeVelocity((target - pos).Length() * kDistanceToVelocity), Vec3(target.v[0], 0, 0)));
+}
+
 HDN void RefereeRequestCommand(World &w, const Ctx &ctx, int official, CommandQueue &q) {
     const MatchState &m = w.match;
     const SpatialState &s = m.officials[official].humanoid.spatial;
-    const Vec3 pos = s.position;
-    if (official == 0) {
-        const Referee &ref = m.referee;
-        if (ref.buffer.active && (ref.foul.foulType == 2 || ref.foul.foulType == 3) &&
-            ref.buffer.prepareTime > m.actualTimeMs + 5000) {
-            // Walk to two meters of the offender, then show the card (special variable 3).
-            const Vec3 off = Sp(w, ref.foul.foulPlayer).position;
-            Vec3 target = off + (pos - off).Normalized(0) * (float)2.0;
-            if ((double)(pos - target).Length() > 2.0) {
-                PlayerCommand c = DefaultPlayerCommand();
-                c.useDesiredMovement = true;
-                c.useDesiredLookAt = true;
-                c.desiredDirection = (target - pos).Normalized(s.directionVec);
-                c.desiredVelocityFloat = RangeVelocity((target - pos).Length() * 1.0f);
-                c.desiredLookAt = off;
-                q.push_back(c);
-            } else {
-                PlayerCommand c = DefaultPlayerCommand();
-                c.desiredFunctionType = kFnSpecial;
-                c.useSpecialVar1 = true;
-                c.specialVar1 = 3;
-                q.push_back(c);
-                PlayerCommand f = DefaultPlayerCommand();
-                f.useDesiredMovement = true;
-                f.useDesiredLookAt = true;
-                f.desiredDirection = (target - pos).Normalized(s.directionVec);
-                f.desiredVelocityFloat = kIdleVelocity;
-                f.desiredLookAt = off;
-                q.push_back(f);
-            }
-        } else {
-            PlayerCommand c = DefaultPlayerCommand();
-            c.useDesiredMovement = true;
-            c.useDesiredLookAt = true;
-            ForceField &field = ctx.ws->forceField;
-            field.clear();
-            field.push_back(MakeSpot(BallAveragePosition(w, 2000).Get2D() * 0.6f, kAttract, kDecayConstant, 0.5f));
-            field.push_back(MakeSpot(BallPredict(m.ball, 200).Get2D(), kRepel, kDecayVariable, 0.5f, 10.0f));
-            const int first = w.FirstTeamID();
-            for (int t = 0; t < 2; t++) {
-                PlayerList ps = TeamActivePlayers(w, t == 0 ? first : 1 - first);
-                for (int i = 0; i < ps.count; i++) {
-                    const SpatialState &ps_s = Sp(w, ps[i]);
-                    field.push_back(MakeSpot(ps_s.position + ps_s.movement * 0.4f, kRepel, kDecayVariable, 0.5f, 10.0f));
-                }
-            }
-            Vec3 target = pos + GetForceFieldMovement(field, pos);
-            c.desiredDirection = (target - pos).Normalized(s.directionVec);
-            c.desiredVelocityFloat =
-                Clamp((target - pos).Length() * kDistanceToVelocity * 0.5f, kIdleVelocity, kSprintVelocity);
-            c.desiredLookAt = BallPredict(m.ball, 60).Get2D();
-            q.push_back(c);
-        }
-    } else {
-        // A linesman follows the offside line of the team whose half he runs along.
-        PlayerCommand c = DefaultPlayerCommand();
-        c.useDesiredMovement = true;
-        c.useDesiredLookAt = true;
-        const int latest = MentalImageIndex(w, 0);
-        float line;
-        Vec3 target;
-        if (pos.v[1] < 0) {
-            line = GetOffsideLine(w, latest, 1);
-            target = Vec3(line, -(kPitchHalfWidth + 0.8f), 0);
-        } else {
-            line = GetOffsideLine(w, latest, 0);
-            target = Vec3(line, kPitchHalfWidth + 0.8f, 0);
-        }
-        c.desiredDirection = (target - pos).Normalized(s.directionVec);
-        c.desiredVelocityFloat = RangeVelocity((target - pos).Length() * kDistanceToVelocity);
-        c.desiredLookAt = Vec3(target.v[0], 0, 0);
-        q.push_back(c);
+    if (official != 0) {
+        LinesmanFollowsLine(w, s, q);
+        return;
     }
+    const Referee &ref = m.referee;
+    const bool booking = ref.buffer.active && (ref.foul.foulType == 2 || ref.foul.foulType == 3) &&
+                         ref.buffer.prepareTime > m.actualTimeMs + 5000;
+    if (booking) RefereeBooksOffender(w, s, q);
+    else RefereeFollowsPlay(w, ctx, s, q);
 }
 
-// The tick of an official's humanoid: the player tick without touches, smuggles or requeues.
-HDN bool OfficialHumanoidProcess(World &w, const Ctx &c, int official) {
+// An interrupted official takes the first command whose animation it finds, and starts that
+// animation from where it stands, smoothed (less when it merely switches).
+HDN bool OfficialInterrupt(World &w, const Ctx &c, int official) {
     const int hi = w.match.playerCount + official;
     Humanoid &h = w.match.officials[official].humanoid;
+    CommandQueue &q = c.ws->commands;
+    q.clear();
+    if (h.interruptAnim == kIntTrip && h.tripType != 0) {
+        AddTripCommandToQueue(h, q, h.tripType);
+        h.tripType = 0;
+        q.push_back(GetBasicMovementCommand(h, h.spatial.floatVelocity));
+    } else {
+        RefereeRequestCommand(w, c, official, q);
+    }
+    bool found = false;
+    for (int i = 0; i < q.count && !found; i++) {
+        Selector sel(w, c, hi);
+        const SelectResult r = sel.BaseSelectAnimation(q[i], h.interruptAnim);
+        if (r == kSelectUnsupported) return false;
+        found = r == kSelectTrue;
+    }
+    if (!found) return true;
     AnimationState &cur = h.anim;
+    h.startPos = h.spatial.position;
+    h.startAngle = h.spatial.angle;
+    {
+        Selector sel(w, c, hi);
+        Vec3 nextPos;
+        float nextAngle;
+        sel.CalculatePredictedSituation(nextPos, nextAngle);
+        h.nextStartPos = nextPos;
+        h.nextStartAngle.set(nextAngle);
+    }
+    h.applyBuf.anim = cur.anim;
+    h.applyBuf.smooth = true;
+    h.applyBuf.smoothFactor = (h.interruptAnim == kIntSwitch) ? 0.6f : 1.0f;
+    const float difficulty = c.D(cur.anim).difficultyFactor;
+    if (difficulty > h.decayingDifficultyFactor) h.decayingDifficultyFactor = difficulty;
+    if (h.interruptAnim == kIntReQueue && h.prevAnimFunctionType == cur.functionType) h.requeueDelayFrames = 32;
+    return true;
+}
+
+// The apply buffer of an official's frame: its start plus the smuggled offsets, plus the frame's
+// planned position when the animation plans one (then the frame keeps the root in place).
+HD void OfficialFillApplyBuffer(const Ctx &c, Humanoid &h) {
+    AnimationState &cur = h.anim;
+    const Anim &a = c.A(cur.anim);
+    const float through = (cur.frameNum + 1) / (float)((a.frameCount - 1) + 1);
+    cur.rotationSmuggleOffset.set(cur.rotationSmuggleBegin.value() * (1.0f - through) + cur.rotationSmuggleEnd.value() * through);
+    AnimApplyBuffer &buf = h.applyBuf;
+    buf.frameNum = cur.frameNum;
+    // The start, then the smuggles, then the frame position, in that order of addition.
+    const Vec3 base = h.startPos + cur.actionSmuggleOffset + cur.actionSmuggleSustainOffset + cur.movementSmuggleOffset;
+    const bool planned = (uint32_t)cur.positions.count > (uint32_t)cur.frameNum;
+    if (planned) {
+        buf.position = base + cur.positions[cur.frameNum];
+        buf.orientation.set(h.startAngle.value() + cur.rotationSmuggleOffset.value());
+    } else {
+        buf.position = base;
+        buf.orientation = h.startAngle;
+    }
+    buf.noPos = planned;
+    for (int i = 0; i < kBodyParts; i++) buf.offsets[i] = h.offsets[i];
+}
+
+// The tick of an official's humanoid: the player's tick without touches, smuggles or requeues.
+HDN bool OfficialHumanoidProcess(World &w, const Ctx &c, int official) {
+    Humanoid &h = w.match.officials[official].humanoid;
+    AnimationState &cur = h.anim;
+    // The offset from the last collision and the difficulty of the last animation fade.
     h.decayingPositionOffset *= 0.95f;
     if ((double)h.decayingPositionOffset.Length() < 0.005) h.decayingPositionOffset = Vec3(0);
     h.decayingDifficultyFactor = Clamp(h.decayingDifficultyFactor - 0.002f, 0.0f, 1.0f);
@@ -301,62 +369,12 @@ HDN bool OfficialHumanoidProcess(World &w, const Ctx &c, int official) {
     h.spatial.positionOffsetMovement = Vec3(0);
     cur.frameNum++;
     h.prevAnimFrameNum++;
+    // The last frame of an animation interrupts it.
     if (cur.frameNum == c.A(cur.anim).frameCount - 1 && h.interruptAnim == kIntNone) h.interruptAnim = kIntSwitch;
-    if (h.interruptAnim != kIntNone) {
-        CommandQueue &q = c.ws->commands;
-        q.clear();
-        if (h.interruptAnim == kIntTrip && h.tripType != 0) {
-            AddTripCommandToQueue(h, q, h.tripType);
-            h.tripType = 0;
-            q.push_back(GetBasicMovementCommand(h, h.spatial.floatVelocity));
-        } else {
-            RefereeRequestCommand(w, c, official, q);
-        }
-        bool found = false;
-        for (int i = 0; i < q.count; i++) {
-            Selector sel(w, c, hi);
-            SelectResult r = sel.BaseSelectAnimation(q[i], h.interruptAnim);
-            if (r == kSelectUnsupported) return false;
-            found = r == kSelectTrue;
-            if (found) break;
-        }
-        if (found) {
-            h.startPos = h.spatial.position;
-            h.startAngle = h.spatial.angle;
-            {
-                Selector sel(w, c, hi);
-                Vec3 np;
-                float na;
-                sel.CalculatePredictedSituation(np, na);
-                h.nextStartPos = np;
-                h.nextStartAngle.set(na);
-            }
-            h.applyBuf.anim = cur.anim;
-            h.applyBuf.smooth = true;
-            h.applyBuf.smoothFactor = (h.interruptAnim == kIntSwitch) ? 0.6f : 1.0f;
-            float diff = c.D(cur.anim).difficultyFactor;
-            if (diff > h.decayingDifficultyFactor) h.decayingDifficultyFactor = diff;
-            if (h.interruptAnim == kIntReQueue && h.prevAnimFunctionType == cur.functionType) h.requeueDelayFrames = 32;
-        }
-    }
+    if (h.interruptAnim != kIntNone && !OfficialInterrupt(w, c, official)) return false;
     h.requeueDelayFrames = (int)Clamp((float)(h.requeueDelayFrames - 1), 0, 10000);
     h.interruptAnim = kIntNone;
-    const Anim &a = c.A(cur.anim);
-    float fb = (cur.frameNum + 1) / (float)((a.frameCount - 1) + 1);
-    cur.rotationSmuggleOffset.set(cur.rotationSmuggleBegin.value() * (1.0f - fb) + cur.rotationSmuggleEnd.value() * fb);
-    h.applyBuf.frameNum = cur.frameNum;
-    // Official: start + smuggles + frame position, in that order of addition.
-    Vec3 base = h.startPos + cur.actionSmuggleOffset + cur.actionSmuggleSustainOffset + cur.movementSmuggleOffset;
-    if ((uint32_t)cur.positions.count > (uint32_t)cur.frameNum) {
-        h.applyBuf.position = base + cur.positions[cur.frameNum];
-        h.applyBuf.orientation.set(h.startAngle.value() + cur.rotationSmuggleOffset.value());
-        h.applyBuf.noPos = true;
-    } else {
-        h.applyBuf.position = base;
-        h.applyBuf.orientation = h.startAngle;
-        h.applyBuf.noPos = false;
-    }
-    for (int i = 0; i < kBodyParts; i++) h.applyBuf.offsets[i] = h.offsets[i];
+    OfficialFillApplyBuffer(c, h);
     return true;
 }
 HDN bool OfficialsProcess(World &w, const Ctx &c) {

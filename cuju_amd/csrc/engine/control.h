@@ -38,37 +38,50 @@ HD float GetLastSwitchBias(World &w, PlayerControllerState &c) {
     return 0.0f;
 }
 
+// A stick held outward at a touchline or goal line is cut to zero in that axis (GRF clamps with
+// std::min(0, x) or std::max(0, x); the expression never gives -0).
+HD Vec3 StickInsidePitch(Vec3 stick, const Vec3 &pos) {
+    float &x = stick.v[0], &y = stick.v[1];
+    if (pos.v[0] > kPitchHalfLength) x = ((x < 0.0f) ? x : 0.0f) + 0.0f;
+    if (pos.v[0] < -kPitchHalfLength) x = (0.0f < x) ? x : 0.0f;
+    if (pos.v[1] > kPitchHalfWidth) y = ((y < 0.0f) ? y : 0.0f) + 0.0f;
+    if (pos.v[1] < -kPitchHalfWidth) y = (0.0f < y) ? y : 0.0f;
+    return stick;
+}
+// The velocity the held buttons ask for: sprint, then dribble, then standing to switch with the
+// ball, else walking.
+HD float ButtonVelocity(const World &w, const bool *buttons, int p) {
+    if (buttons[kBtnSprint]) return kSprintVelocity;
+    if (buttons[kBtnDribble]) return kDribbleVelocity;
+    if (buttons[kBtnSwitch] && w.match.designatedPossessionPlayer == p) return kIdleVelocity;
+    return kWalkVelocity;
+}
+// The player's own movement, fading out over the moments after a switch to it, blends into what the
+// gamer asks for.
+HD void BlendAfterSwitch(World &w, int p, PlayerControllerState &base, Vec3 &dir, float &vel) {
+    if (!(GetLastSwitchBias(w, base) > 0.0f)) return;
+    const float influence = 0.5f;
+    const float fading = libm::powf(GetLastSwitchBias(w, base), 0.7f);
+    const Vec3 own = Sp(w, p).directionVec * PlayerFloatVelocity(w, p);
+    const Vec3 asked = dir * vel;
+    const Vec3 blend = own * fading * influence + asked * (1.0f - fading * influence);
+    dir = blend.Normalized(dir);
+    vel = blend.Length();
+}
+// What a gamer's keyboard asks of player `p`: a direction and a velocity. A stick inside the dead
+// zone keeps the player's direction, idle.
 HDN void HumanGetKeyboardInput(World &w, int p, Vec3 &dir, float &vel) {
     HumanControllerState &hc = HumanGamerOf(w, p).controller;
     const SpatialState &s = Sp(w, p);
-    dir = KeyboardDirection(hc.keyboard);
-    const Vec3 pos = s.position;
-    float &dx = dir.v[0], &dy = dir.v[1];
-    // Each clamp is std::min(0, x) or std::max(0, x); the expression never gives -0.
-    if (pos.v[0] > kPitchHalfLength) dx = ((dx < 0.0f) ? dx : 0.0f) + 0.0f;
-    if (pos.v[0] < -kPitchHalfLength) dx = (0.0f < dx) ? dx : 0.0f;
-    if (pos.v[1] > kPitchHalfWidth) dy = ((dy < 0.0f) ? dy : 0.0f) + 0.0f;
-    if (pos.v[1] < -kPitchHalfWidth) dy = (0.0f < dy) ? dy : 0.0f;
+    dir = StickInsidePitch(KeyboardDirection(hc.keyboard), s.position);
     if (dir.Length() < kStickDeadzone) {
         dir = s.directionVec;
         vel = kIdleVelocity;
     } else {
-        const bool *b = hc.keyboard.buttons;
-        if (b[kBtnSprint]) vel = kSprintVelocity;
-        else if (b[kBtnDribble]) vel = kDribbleVelocity;
-        else if (b[kBtnSwitch] && w.match.designatedPossessionPlayer == p) vel = kIdleVelocity;
-        else vel = kWalkVelocity;
+        vel = ButtonVelocity(w, hc.keyboard.buttons, p);
         dir.Normalize();
     }
-    if (GetLastSwitchBias(w, hc.base) > 0.0f) {
-        float influence = 0.5f;
-        float sb = libm::powf(GetLastSwitchBias(w, hc.base), 0.7f);
-        Vec3 cur = s.directionVec * PlayerFloatVelocity(w, p);
-        Vec3 manual = dir * vel;
-        Vec3 res = cur * sb * influence + manual * (1.0f - sb * influence);
-        dir = res.Normalized(dir);
-        vel = res.Length();
-    }
+    BlendAfterSwitch(w, p, hc.base, dir, vel);
 }
 HD float HumanGetFloatVelocity(World &w, int p) {
     Vec3 d;
@@ -136,16 +149,22 @@ HDN void HumanGamerSetSelectedPlayer(World &w, int g, int p) {
         gm.selectedPlayer = -1;
     }
 }
+// The gamer first in the team's switch order goes to the back of it.
+HD void RotateSwitchOrder(Team &t) {
+    auto &order = t.switchPriority;
+    const int front = order[0];
+    for (int i = 0; i + 1 < order.count; i++) order[i] = order[i + 1];
+    order[order.count - 1] = front;
+}
+// A selectable player becomes the team's main selection and, when no gamer holds it, the player of
+// the gamer first in the switch order (who then goes to the back); it is the designated player.
 HDN bool TeamSelectPlayer(World &w, const Ctx &c, int teamID, int p) {
     Team &t = TeamByID(w, teamID);
     if (Formation(w, c, p).controllable) {
         t.mainSelectedPlayer = p;
         if (w.match.players[p].base.externalController < 0 && t.gamers.count > 0) {
-            auto &sp = t.switchPriority;
-            int g = sp[0];
-            HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), p);
-            for (int i = 0; i + 1 < sp.count; i++) sp[i] = sp[i + 1];
-            sp[sp.count - 1] = g;
+            HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, t.switchPriority[0]), p);
+            RotateSwitchOrder(t);
         }
     }
     t.designatedTeamPossessionPlayer = p;
@@ -185,32 +204,23 @@ HD int HumanControlledToBallTime(const World &w, int teamID) {
     }
     return best;
 }
+// GRF's automatic switching while in play: the gamer on the match's designated player yields the
+// front of the switch order; the team's designated outfield player goes to a gamer when it is
+// three times quicker to the ball than every controlled player, or when it alone has the ball (or
+// a set piece is on). Each test reads the designated player anew.
 HDN bool TeamUpdateSwitch(World &w, const Ctx &c, int teamID) {
     ENG_SCOPE(9);
     MatchState &m = w.match;
     Team &t = TeamByID(w, teamID);
-    if (m.inPlay && t.gamers.count > 1) {
-        auto &sp = t.switchPriority;
-        int mine = sp[0];
-        if (t.gamers[mine].selectedPlayer == m.designatedPossessionPlayer) {
-            for (int i = 0; i + 1 < sp.count; i++) sp[i] = sp[i + 1];
-            sp[sp.count - 1] = mine;
-        }
-    }
-    if (m.inPlay && t.gamers.count > 0) {
-        int d = t.designatedTeamPossessionPlayer;
-        if (!ExternalControllerActive(w, d) && 3 * (int)w.roster.timeToBallMs[d] < HumanControlledToBallTime(w, teamID) &&
-            Formation(w, c, d).role != kRoleGoalkeeper) {
-            if (!TeamSelectPlayer(w, c, teamID, d)) return false;
-        }
-    }
-    if (m.inPlay && t.gamers.count > 0) {
-        int d = t.designatedTeamPossessionPlayer;
-        if (!ExternalControllerActive(w, d) && (m.players[d].hasUniquePossession || m.inSetPiece)) {
-            if (Formation(w, c, d).role != kRoleGoalkeeper)
-                if (!TeamSelectPlayer(w, c, teamID, d)) return false;
-        }
-    }
+    if (!m.inPlay || t.gamers.count == 0) return true;
+    if (t.gamers.count > 1 && t.gamers[t.switchPriority[0]].selectedPlayer == m.designatedPossessionPlayer) RotateSwitchOrder(t);
+    auto freeOutfield = [&](int d) { return !ExternalControllerActive(w, d) && Formation(w, c, d).role != kRoleGoalkeeper; };
+    int d = t.designatedTeamPossessionPlayer;
+    if (!ExternalControllerActive(w, d) && 3 * (int)w.roster.timeToBallMs[d] < HumanControlledToBallTime(w, teamID) &&
+        Formation(w, c, d).role != kRoleGoalkeeper && !TeamSelectPlayer(w, c, teamID, d))
+        return false;
+    d = t.designatedTeamPossessionPlayer;
+    if (freeOutfield(d) && (m.players[d].hasUniquePossession || m.inSetPiece) && !TeamSelectPlayer(w, c, teamID, d)) return false;
     return true;
 }
 HDN void TeamHumanGamersSelectAnyone(World &w, const Ctx &c, int teamID) {

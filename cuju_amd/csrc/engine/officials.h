@@ -309,7 +309,7 @@ HDN bool OfficialInterrupt(World &w, const Ctx &c, int official) {
     bool found = false;
     for (int i = 0; i < q.count && !found; i++) {
         Selector sel(w, c, hi);
-        const SelectResult r = sel.BaseSelectAnimation(q[i], h.interruptAnim);
+        const SelectResult r = sel.SelectOfficialAnimation(q[i], h.interruptAnim);
         if (r == kSelectUnsupported) return false;
         found = r == kSelectTrue;
     }
@@ -321,7 +321,7 @@ HDN bool OfficialInterrupt(World &w, const Ctx &c, int official) {
         Selector sel(w, c, hi);
         Vec3 nextPos;
         float nextAngle;
-        sel.CalculatePredictedSituation(nextPos, nextAngle);
+        sel.PredictedPose(nextPos, nextAngle);
         h.nextStartPos = nextPos;
         h.nextStartAngle.set(nextAngle);
     }

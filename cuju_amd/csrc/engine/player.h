@@ -382,7 +382,7 @@ HDN bool HumanoidProcessInterrupt(World &w, const Ctx &c, int p) {
         for (int i = 0; i < q.count; i++) {
             if (IsPassOrShot(q[i].desiredFunctionType)) preferPassAndShot = true;
             Selector sel(w, c, p);
-            SelectResult r = sel.SelectAnimation(q[i], h.interruptAnim, preferPassAndShot);
+            SelectResult r = sel.SelectPlayerAnimation(q[i], h.interruptAnim, preferPassAndShot);
             if (r == kSelectUnsupported) return false;
             found = r == kSelectTrue;
             if (found) break;
@@ -398,7 +398,7 @@ HDN bool HumanoidProcessInterrupt(World &w, const Ctx &c, int p) {
                 Selector sel(w, c, p);
                 Vec3 np;
                 float na;
-                sel.CalculatePredictedSituation(np, na);
+                sel.PredictedPose(np, na);
                 h.nextStartPos = np;
                 h.nextStartAngle.set(na);
             }

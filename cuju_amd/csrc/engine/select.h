@@ -37,7 +37,7 @@ struct PList {
     HD const Vec3 &operator[](int i) const { return e[i]; }
 };
 
-HD int GetVelocityID(int v, bool dribbleAsWalk = false) {
+HD int VelocityRank(int v, bool dribbleAsWalk = false) {
     int id = 0;
     switch (v) {
         case kVelIdle:
@@ -112,7 +112,7 @@ HD float PreferredAngle(int i) {
     const double f[11] = {0, 0.111, -0.111, 0.25, -0.25, 0.5, -0.5, 0.75, -0.75, 0.999, -0.999};
     return (float)(f[i] * (double)PI);
 }
-HDN Vec3 ForceIntoPreferredDirectionVector(const Vec3 &src) {
+HDN Vec3 SnapToPreferredDirection(const Vec3 &src) {
     float best = -1.0f;
     Vec3 bv;
     for (int i = 0; i < 11; i++) {
@@ -125,7 +125,7 @@ HDN Vec3 ForceIntoPreferredDirectionVector(const Vec3 &src) {
     }
     return bv;
 }
-HDN float ForceIntoPreferredDirectionAngle(float a) {
+HDN float SnapToPreferredAngle(float a) {
     float bestDiff = 10000.0, bv = 0;
     for (int i = 0; i < 11; i++) {
         float d = fabsf(PreferredAngle(i) - a);
@@ -136,7 +136,7 @@ HDN float ForceIntoPreferredDirectionAngle(float a) {
     }
     return bv;
 }
-HDN float ForceIntoAllowedBodyDirectionAngle(float a) {
+HDN float SnapToBodyAngle(float a) {
     const double f[5] = {0, 0.25, -0.25, 0.75, -0.75};
     float bestDiff = 10000.0, bv = 0;
     for (int i = 0; i < 5; i++) {
@@ -150,21 +150,21 @@ HDN float ForceIntoAllowedBodyDirectionAngle(float a) {
     return bv;
 }
 
-HD float CalculateBiasForFastCornering(const Vec3 &cur, const Vec3 &desired, float velExp, float bias) {
+HD float CorneringBias(const Vec3 &cur, const Vec3 &desired, float velExp, float bias) {
     float angle = desired.Normalized(cur).Angle2D(cur);
     float cb = libm::sinf(fabsf(angle) - 0.5f * PI) * 0.5f + 0.5f;
     float vb = libm::powf(Clamp(cur.Length() / (kSprintVelocity - 0.5f), 0.0f, 1.0f), velExp);
     return vb * cb * bias;
 }
 
-HD float StretchSprintTo(float v, float inMax, float targetMax) {
+HD float StretchSprint(float v, float inMax, float targetMax) {
     if (v < kWalkSprintSwitch) return v;
     float part = v - kWalkSprintSwitch;
     float oldL = inMax - kWalkSprintSwitch, newL = targetMax - kWalkSprintSwitch;
     return kWalkSprintSwitch + part * (newL / oldL);
 }
 
-HD Vec3 GetFrontOfFootOffsetRelative(float velocity, float bodyAngleRel, float height) {
+HD Vec3 FootReachOffset(float velocity, float bodyAngleRel, float height) {
     float distance = 0.34f + velocity * kDefaultTouchOffsetMs * 0.001f * 1.0f;
     Vec3 fwd(0, -distance * 0.8f, 0);
     float ba = bodyAngleRel;
@@ -417,7 +417,7 @@ HD bool IncomingBodyPasses(const BodyRule &rule, int entry, const Vec3 &directio
 // body-prefiltered record lists (Tables::crudeBody).
 constexpr int kBodyEntries = 6;
 
-HDN void CrudeSelection(const Ctx &c, const CrudeQuery &query, AList &out) {
+HDN void FilterAnimations(const Ctx &c, const CrudeQuery &query, AList &out) {
     ENG_SCOPE(28);
     // The query, the tables' bounds and the list held in registers across the list's stores.
     const CrudeQuery q = query;
@@ -558,7 +558,7 @@ HDN void CrudeSelection(const Ctx &c, const CrudeQuery &query, AList &out) {
     GroupSync();
 }
 
-// The crude query of GetIdleMovementAnimationID: movement from idle to idle.
+// The crude query of IdleMovementAnimation: movement from idle to idle.
 HD CrudeQuery IdleMovementQuery() {
     CrudeQuery q;
     q.byFunctionType = true;
@@ -609,10 +609,10 @@ HD int KeyFoot(const Anim &a, const Predicates &p) {
     return r;
 }
 HD float KeyIncomingVelocity(const Anim &a, const Predicates &p) {
-    int cur = GetVelocityID(p.incomingVelocity);
-    int in = GetVelocityID(VelocityCat(a.incomingVelocity));
+    int cur = VelocityRank(p.incomingVelocity);
+    int in = VelocityRank(VelocityCat(a.incomingVelocity));
     float r = fabsf(Clamp((float)(in - cur), -3, 3));
-    int out = GetVelocityID(VelocityCat(a.outgoingVelocity));
+    int out = VelocityRank(VelocityCat(a.outgoingVelocity));
     if (in > (cur > out ? cur : out)) r += 0.5f;
     if (in < (cur < out ? cur : out)) r += 0.5f;
     return r;
@@ -689,6 +689,363 @@ HD Vec3 OutgoingMovementOf(const PList &p) {
     return (p[p.count - 1] - p[p.count - 2]) * 100.0f;
 }
 
+// ---- movement plans ------------------------------------------------------------------------------
+// A selected animation's positions, frame by frame (10 ms apart) from where the humanoid stands: the
+// animation's own movement, stretched to the player's top speed, turned toward the desired
+// direction and blended with it by the physics share, is what a carried velocity chases; the
+// velocity's turn, change and gain per frame are bounded. Every expression keeps GRF's operation
+// order (humanoid_base.cpp, CalculatePhysicsVector).
+
+// How much of the animation's outgoing movement replaces the desired one: all for touches,
+// deflections, specials and animations into or out of a special state, half for trips, none for
+// ball control, traps, interference, sliding and untouched movement.
+HD float OutgoingSwitch(int at, bool touch, bool special) {
+    if (special) return 1.0f;
+    switch (at) {
+        case kAtBallControl:
+        case kAtTrap:
+        case kAtInterfere:
+        case kAtSliding:
+            return 0.0f;
+        case kAtDeflect:
+        case kAtSpecial:
+            return 1.0f;
+        case kAtTrip:
+            return 0.5f;
+        default:
+            return touch ? 1.0f : 0.0f;
+    }
+}
+// How much of the plan follows physics rather than the animation's own movement: none for short
+// and high passes, shots, deflections, specials and animations from a special state; half for
+// interference and trips of type one (none for other trips); all otherwise.
+HD float PhysicsShare(int at, bool tripTypeIsOne, bool fromSpecial) {
+    if (fromSpecial) return 0.0f;
+    switch (at) {
+        case kAtShortPass:
+        case kAtHighPass:
+        case kAtShot:
+        case kAtDeflect:
+        case kAtSpecial:
+            return 0.0f;
+        case kAtInterfere:
+            return 0.5f;
+        case kAtTrip:
+            return tripTypeIsOne ? 0.5f : 0.0f;
+        default:
+            return 1.0f;
+    }
+}
+// The most the plan turns the animation toward the desired direction: when the animation already
+// turns that way (over), when it turns the other way (under), and when it runs straight.
+struct TurnCaps {
+    float under, over, straight;
+};
+HD TurnCaps PlanTurnCaps(bool touch, bool sliding, const Vec3 &carried, const Vec3 &outgoing, float ballControl) {
+    if (sliding) return {0.5f * PI, 0.5f * PI, 0.5f * PI};
+    if (!touch) return {0.125f * PI, 0.125f * PI, 0.125f * PI};
+    // A touch turns less the faster the humanoid moves through it and the worse its ball control.
+    float bonus = 1.0f - libm::PowfPos(NormalizedClamp((carried + outgoing).Length() * 0.5f, 0, kSprintVelocity), 0.8f) * 0.8f;
+    bonus *= 0.6f + 0.4f * ballControl;
+    return {0.2f * PI * bonus, 0.0f, 0.1f * PI * bonus};
+}
+// The turn the plan reaches by its last frame: from the animation's outgoing movement (its
+// outgoing direction when that is idle) to the desired movement (the desired body direction when
+// that is idle), within the caps; none when they lie more than a quarter turn apart, sliding aside.
+HD float PlanSteer(int at, const TurnCaps &caps, const Vec3 &outgoing, const Vec3 &outgoingFacing, const Vec3 &desired,
+                   const Vec3 &desiredBody, const Vec3 &facing) {
+    const Vec3 from = VelocityCat(outgoing.Length()) == kVelIdle ? outgoingFacing : outgoing.Normalized(0);
+    const Vec3 to = VelocityCat(desired.Length()) == kVelIdle ? desiredBody : desired.Normalized(0);
+    const float wanted = to.Angle2D(from);
+    if (!(fabsf(wanted) <= 0.5f * PI || at == kAtSliding)) return 0.0f;
+    const float animationTurn = from.Angle2D(facing);
+    float cap = caps.straight;
+    if (fabsf(animationTurn) > 0.06f * PI) cap = SignSide(wanted) == SignSide(animationTurn) ? caps.over : caps.under;
+    return Clamp(wanted, -cap, cap);
+}
+// The time warp of the animation: at progress p the plan reads animation frame effFrames * p^lag.
+// Movement and ball control under physics lag by the player's agility and the animation's
+// difficulty (at least 0.7 before a touch), blended toward no warp by the physics share.
+struct FrameLag {
+    float beforeTouch = 1.0f, afterTouch = 1.0f;
+};
+HD FrameLag PlanFrameLag(int at, float physicsBias, bool touch, float agility, float difficulty) {
+    FrameLag lag;
+    if (!(physicsBias > 0.0f && (at == kAtBallControl || at == kAtMovement))) return lag;
+    float e = 1.4f - 0.5f * 0.8f;
+    e *= 1.2f - agility * 0.4f;
+    if (touch) e += -0.1f + Clamp(difficulty * 0.4f, 0.0f, 0.5f);
+    else e += -0.2f + Clamp(difficulty * 0.2f, 0.0f, 0.2f);
+    e = Clamp(e, 0.25f, 4.0f);
+    lag.beforeTouch = (touch ? MaxF(e, 0.7f) : e) * physicsBias + 1.0f * (1.0f - physicsBias);
+    lag.afterTouch = e * physicsBias + 1.0f * (1.0f - physicsBias);
+    return lag;
+}
+constexpr float kFrameSeconds = 10 / 1000.0f;
+
+struct MovementPlanner {
+    // The plan's constants.
+    int at = 0, touchFrame = 0, effFrames = 0, settleFrom = 0, posCount = 0;
+    bool touch = false, outgoingIdle = false;
+    libm::SinCos turn{};
+    float agility = 0, accel = 0, physicsBias = 0, steer = 0, difficultyPenalty = 0, powerFactor = 0, maxVel = 0,
+          playerMaxVel = 0, desiredVel = 0;
+    FrameLag lag;
+    Vec3 desiredDir, outgoingTurned;
+    const Vec3 *smoothed = nullptr;  // the animation's smoothed movement, when tabulated
+    const Vec3 *positions = nullptr;
+    // What carries from frame to frame.
+    Vec3 velocity, position;
+
+    HD float Progress(int frame) const { return (frame * 10 + 10) / (float)((effFrames + 1) * 10); }
+    // The animation's movement at the warped frame, on the pitch.
+    HD Vec3 AnimationMovement(int frame, float progress) const {
+        const float e = touch && frame < touchFrame ? lag.beforeTouch : lag.afterTouch;
+        const float warped = e == 1.0f ? progress : libm::powf(progress, e);
+        const uint32_t animFrame = TruncToUint32(effFrames * warped);
+        return RotatedBy(smoothed && animFrame < (uint32_t)posCount ? smoothed[animFrame]
+                                                                      : MovementAtFrame(positions, posCount, animFrame, 1),
+                         turn);
+    }
+    // Movement, ball control and traps above the walk-sprint switch stretch to the player's top
+    // speed when it is higher.
+    HD void Stretch(Vec3 &movement, float &speed) const {
+        if (!(speed > kWalkSprintSwitch && (at == kAtMovement || at == kAtBallControl || at == kAtTrap))) return;
+        if (!(maxVel > speed)) return;
+        speed = StretchSprint(speed, kAnimSprintVelocity, maxVel);
+        movement = movement.Normalized(0) * speed;
+    }
+    // What the carried velocity chases this frame: the desired speed held near the stretched
+    // animation speed (down by 1.2 or 1.6 m/s; up by the carried excess, fading over the animation
+    // and with the angle to the desired direction), along the stretched movement turned by the
+    // frame's share of the steer, blended with the raw movement by the physics share.
+    HD Vec3 Target(const Vec3 &raw, const Vec3 &stretched, float stretchedSpeed, float progress, float carriedSpeed) const {
+        float faster = 0.0f;
+        if (carriedSpeed > stretchedSpeed) faster = MinF(1.0f - progress, MaxF(0.0f, carriedSpeed - stretchedSpeed));
+        if (faster > 0) faster *= MaxF(0.0f, NormalizedMaximum(stretched, 1.0f).Dot(desiredDir));
+        if (at == kAtSliding) faster = 100;
+        const float slower = touch ? 1.2f : 1.6f;
+        const float speed = Clamp(desiredVel, stretchedSpeed - slower, stretchedSpeed + faster);
+        const float rotation = steer * progress;
+        float rc = 1.0f, rs = rotation;
+        // Below 2^-12 the sine is the argument and the cosine 1, by the test of sinf/cosf.
+        if (!(libm::Top12f(rotation) < libm::Top12f(0x1p-12f))) {
+            const libm::SinCos t = libm::sincosf(rotation);
+            rc = t.c;
+            rs = t.s;
+        }
+        const Vec3 turned = RotatedCS(stretched.Normalized(0) * speed, rc, rs);
+        return turned * physicsBias + raw * (1.0f - physicsBias);
+    }
+    // A turn sharper than the agility allows per frame (less at speed, more without a touch) sheds
+    // carried speed in proportion to the excess.
+    HD void BoundTurn(Vec3 &change, float carriedSpeed) const {
+        const Vec3 next = velocity + change;
+        if (!(carriedSpeed > kIdleDribbleSwitch && next.Length() > kIdleDribbleSwitch)) return;
+        const Vec3 nextDir = next.Normalized(), carriedDir = velocity.Normalized();
+        float perFrame = 1.0f * kFrameSeconds;
+        perFrame *= (0.7f + 0.3f * agility);
+        if (!touch) perFrame *= 1.5f;
+        const float limit = perFrame * PI / (NormalizedClamp(carriedSpeed, 0, kSprintVelocity) + 0.01f);
+        const float corner = fabsf(nextDir.Angle2D(carriedDir));
+        if (corner > limit) change += -velocity * Clamp((corner - limit) / PI * 3.0f, 0.0f, 1.0f);
+    }
+    // The change per frame is capped by speed (movement less so), the frame's place on the
+    // acceleration curve and the humanoid's power.
+    HD void BoundChange(Vec3 &change, float carriedSpeed, int frame) const {
+        float cap = at == kAtSliding ? 0.1f : at == kAtTrip ? 0.03f * 0.7f : 0.03f;
+        const float fast = libm::PowfPos(NormalizedClamp(carriedSpeed, 0, kSprintVelocity), 1.5f);
+        const float curved = at == kAtMovement ? fast * 0.4f : fast;
+        cap *= (1.0f - curved) + curved * PhysicsCurvedTime(frame);
+        cap *= 1.2f - fast * 0.4f;
+        cap *= powerFactor;
+        NormalizeMaximum(change, MinF(change.Length(), cap * 10));
+    }
+    // Above the idle-dribble switch the speed gained per frame is capped by the player's
+    // acceleration, less in the air (near top speed) and for difficult animations.
+    HD void BoundGain(Vec3 &change, float carriedSpeed) const {
+        if (at == kAtSliding || at == kAtDeflect) return;
+        const Vec3 next = velocity + change;
+        const float nextSpeed = next.Length();
+        if (!(nextSpeed > kIdleDribbleSwitch)) return;
+        const float power = 11.0f * (1.0f - difficultyPenalty * 0.4f);
+        const float air = Clamp(
+            libm::PowfPos(Clamp((carriedSpeed - kIdleDribbleSwitch) / (playerMaxVel - kIdleDribbleSwitch), 0.0f, 1.0f), 1.8f), 0.0f,
+            1.0f);
+        Vec3 gain;
+        if (nextSpeed > carriedSpeed) gain = next.Normalized(0) * (nextSpeed - carriedSpeed);
+        const float gained = gain.Length();
+        const float most = power * (1.0f - air) * (accel * 0.3f + 0.7f) * kFrameSeconds;
+        if (gained > most) change = change - gain * (1.0f - most / gained);
+    }
+    // Over the last two frames the velocity settles into the animation's outgoing category: zero
+    // for an idle end, the outgoing direction at dribble speed for a moving end that came out idle.
+    HD Vec3 Settle(const Vec3 &v, int frame) const {
+        if (frame < settleFrom) return v;
+        const bool idle = VelocityCat(v.Length()) == kVelIdle;
+        if (outgoingIdle && !idle) return Vec3(0);
+        if (!outgoingIdle && idle) return NormalizedTo(outgoingTurned, kDribbleVelocity);
+        return v;
+    }
+    // One frame: the new position.
+    HD Vec3 Step(int frame) {
+        const float progress = Progress(frame);
+        const Vec3 raw = AnimationMovement(frame, progress);
+        Vec3 stretched = raw;
+        float stretchedSpeed = raw.Length();
+        Stretch(stretched, stretchedSpeed);
+        const float carriedSpeed = velocity.Length();
+        Vec3 change = Target(raw, stretched, stretchedSpeed, progress, carriedSpeed) - velocity;
+        BoundTurn(change, carriedSpeed);
+        BoundChange(change, carriedSpeed, frame);
+        BoundGain(change, carriedSpeed);
+        velocity = Settle(velocity + change, frame);
+        position += velocity * kFrameSeconds;
+        return position;
+    }
+};
+
+// ---- ball reach ----------------------------------------------------------------------------------
+// GRF's test of a touch at a ball key (humanoid_base.cpp, GetBestCheatableAnimationID and its
+// distance advantage): the ball must lie within a radius of a point a little behind the
+// animation's ball, measured in a frame that stretches the axis across the incoming movement.
+
+// The humanoid's movement through a candidate: incoming, at the touch and outgoing (relative to
+// its body), the outgoing angle and the animation's frame count.
+struct ReachMotion {
+    Vec3 in, touch, out;
+    float outAngle;
+    int frames;
+};
+// The factor on the bare radius: larger when the body (a foot's 10 cm ahead) is near the
+// animation's ball and near the ball, and when the humanoid moves slowly.
+HD float ReachGrowth(const ReachMotion &m, const Vec3 &body, const Vec3 &foot, const Vec3 &animBall, const Vec3 &ball) {
+    const float inSpeed = m.in.Length(), outSpeed = m.out.Length();
+    const float meanSpeed = (m.in + m.out).Length() * 0.5f;
+    const float gainPerSecond = (outSpeed - inSpeed) / (m.frames * 0.01f);
+    const Vec3 toe = body + foot.Normalized(0) * 0.1f;
+    const float nearAnimBall = 1.0f - Curve(NormalizedClamp((toe - animBall).Length(), 0.0f, 0.7f), 0.7f);
+    const float nearBall = 1.0f - Curve(NormalizedClamp((toe - ball).Length(), 0.0f, 0.7f), 0.4f);
+    const float slow = 1.0f - NormalizedClamp(meanSpeed, kIdleVelocity, kSprintVelocity);
+    const float steady = 1.0f - NormalizedClamp(gainPerSecond / 20.0f, -1.0f, 1.0f);
+    return 1.0f + 1.0f * nearAnimBall + 0.6f * nearBall + 0.8f * nearAnimBall * nearBall + 0.0f * steady + 1.0f * slow;
+}
+// The offset of the measuring point from the animation's ball: against the humanoid's weighted
+// movement (mostly outgoing), longer the faster it moves and the more its outgoing direction
+// points forward.
+HD Vec3 BehindBall(const ReachMotion &m, const Vec3 &outDir) {
+    const Vec3 back = -(m.in * 0.1f + m.touch * 0.2f + m.out * 0.7f);
+    Vec3 behind = back.Normalized(0) * libm::PowfPos(NormalizedClamp(back.Length(), 0, kSprintVelocity), 0.5f);
+    float forward = Vec3(0, -1, 0).Dot(outDir);
+    forward = 0.5f + Clamp(forward * 0.5f + 0.5f, 0.0f, 1.0f) * 0.5f;
+    behind *= forward;
+    return behind;
+}
+// Whether `ball` (2D, relative to the body's start) is within reach of `animBall` for a bare
+// radius and a cheat margin.
+HD bool BallWithinReach(const ReachMotion &m, const Vec3 &body, const Vec3 &foot, const Vec3 &animBall, const Vec3 &ball,
+                        float radiusFactor, float cheat) {
+    const float cheatFactor = 0.5f, cheatBonus = 0.02f;
+    float radius = radiusFactor;
+    radius *= ReachGrowth(m, body, foot, animBall, ball);
+    const Vec3 outDir = VelocityCat(m.out.Length()) == kVelIdle ? Vec3(0, -1, 0).Rotated2D(m.outAngle) : m.out.Normalized();
+    const Vec3 behind = BehindBall(m, outDir);
+    // Across the incoming movement the offset stretches by 1/0.6 standing to 1/0.3 at a sprint,
+    // and the radius by the root of that.
+    Vec3 offset = ball - animBall;
+    const float toStraight = Vec3(0, -1, 0).Angle2D(m.in.Normalized(outDir));
+    offset.Rotate2D(toStraight);
+    const float lateral = 0.6f - 0.3f * libm::PowfPos(NormalizedClamp(m.in.Length(), kIdleVelocity, kSprintVelocity), 0.7f);
+    offset.v[0] /= lateral;
+    radius *= libm::powf(1.0f / lateral, 0.5f);
+    offset.Rotate2D(-toStraight);
+    const Vec3 center = animBall + behind * (radius + (cheat * 0.6f)) * cheatFactor;
+    return !(GetDistance(animBall + offset, center) > (radius + cheat) * cheatFactor + cheatBonus);
+}
+// The bare radius and cheat margin at a key: 0.3 m less the key's distance from the animation's
+// own touch frame, wider for deflections, interference, passes and shots (which also cheat), much
+// narrower for sliding, and narrower for ball control and traps when a pass or shot is preferred.
+struct TouchReach {
+    float radius, cheat;
+};
+HD TouchReach KeyReach(int fn, float awkward, bool preferPassAndShot) {
+    TouchReach r{0.3f * (1.0f - awkward), 0.0f};
+    switch (fn) {
+        case kFnDeflect:
+            r.radius *= 1.8f;
+            r.cheat = 0.4f;
+            break;
+        case kFnSliding:
+            r.radius *= 0.2f;
+            break;
+        case kFnInterfere:
+            r.radius *= 1.4f;
+            r.cheat = 0.2f;
+            break;
+        case kFnShortPass:
+        case kFnLongPass:
+        case kFnHighPass:
+        case kFnShot:
+            r.radius *= 1.3f;
+            r.cheat = 0.15f;
+            break;
+        case kFnTrap:
+        case kFnBallControl:
+            if (preferPassAndShot) r.radius *= 0.3f;
+            break;
+        default:
+            break;
+    }
+    r.cheat *= 1.0f - awkward;
+    return r;
+}
+// What one touch search reads, fixed for its candidates.
+struct TouchSearch {
+    MentalBallView mental;
+    const Vec3 *predictions;
+    bool flip, retainerIsMe, preferPassAndShot, useDesiredMovement;
+    int fn;
+    libm::SinCos back;  // turns pitch directions into the body's frame
+    Vec3 inMov, position, desiredMovement, desiredBodyRel;
+    float height, ballControl;
+    uint64_t now;
+    HD TouchSearch(const World &w, int mentalImage, int humanoid, int function, const libm::SinCos &backTurn, const Vec3 &movement,
+                   const Vec3 &at, float bodyHeight, float control, bool prefer, bool useDesired, const Vec3 &desired,
+                   const Vec3 &desiredBody)
+        : mental(w, mentalImage),
+          predictions(w.match.ball.predictions),
+          flip(w.match.ball.lazyFlip),
+          retainerIsMe(w.match.ballRetainer == humanoid),
+          preferPassAndShot(prefer),
+          useDesiredMovement(useDesired),
+          fn(function),
+          back(backTurn),
+          inMov(RotatedBy(movement, backTurn)),
+          position(at),
+          desiredMovement(desired),
+          desiredBodyRel(desiredBody),
+          height(bodyHeight),
+          ballControl(control),
+          now(w.match.actualTimeMs) {}
+};
+// The height gap between the ball and the animation's ball at a key, eased for low balls and a
+// base animation's low ball, doubled and more for a ball far overhead; none for the retainer.
+HD float TouchHeightMiss(const TouchSearch &ts, bool baseAnimation, float animZ, float ballZ) {
+    float miss = fabsf(ballZ - animZ);
+    miss *= 1.0f - Clamp((float)(((double)animZ - 0.11) * (double)0.3f), 0.0f, 0.2f);
+    miss *= 1.0f - Clamp((float)(((double)ballZ - 0.11) * (double)0.4f), 0.0f, 0.3f);
+    if (ballZ > 1.8f && ballZ > animZ + 0.12f) miss *= 2.0f;
+    if (ballZ > 2.6f && ballZ > animZ + 0.08f) miss *= 20.0f;
+    if (ts.fn == kFnDeflect) miss *= 0.8f;
+    if (ts.retainerIsMe) miss = 0.0f;
+    if (ballZ < 0.5f && baseAnimation) miss = MaxF(miss - 0.15f, 0.0f);
+    return miss;
+}
+struct TouchProbe {
+    bool reaches = false;
+    Vec3 smuggle;  // from the animation's ball to the ball, 2D
+};
+
 struct Selector {
     World &w;
     const Ctx &c;
@@ -735,7 +1092,7 @@ struct Selector {
         return MovementSimilarityOf(r.preferredOutgoingDirection, r.preferredOutgoingMovement, pred.relDesiredDirection,
                                     pred.desiredVelocity, pred.corneringBias);
     }
-    HD int IncomingBodyDirectionQuery() { return ForceIntoAllowedBodyDirectionIndex(pred.relIncomingBodyDirection); }
+    HD int IncomingBodyDirectionQuery() { return BodyDirectionIndex(pred.relIncomingBodyDirection); }
     HD float IncomingBodyDirectionKey(int i, int q) {
         float r = AllowedBodyDirectionKey(c.t->selection[i].incomingBodyIndex, q);
         if (VelocityCat(A(i).incomingVelocity) == kVelIdle) r = 0;
@@ -753,7 +1110,7 @@ struct Selector {
     HD void SetMovementSimilarityPredicate(const Vec3 &relDesired, int desiredVel) {
         pred.relDesiredDirection = relDesired;
         pred.desiredVelocity = desiredVel;
-        pred.corneringBias = CalculateBiasForFastCornering(Vec3(0, -1.0f * S().floatVelocity, 0),
+        pred.corneringBias = CorneringBias(Vec3(0, -1.0f * S().floatVelocity, 0),
                                                            relDesired * VelocityFloat(desiredVel), 1.0f, 0.9f);
     }
 
@@ -881,7 +1238,7 @@ struct Selector {
         return false;
     }
 
-    HDN void KeepBestDirectionAnimations(AList &l, const PlayerCommand &cmd, bool strict, float allowedAngle = 0,
+    HDN void KeepNearestQuadrant(AList &l, const PlayerCommand &cmd, bool strict, float allowedAngle = 0,
                                          int allowedVelocitySteps = 0, int forcedQuadrant = -1) {
         ENG_SCOPE(32);
         if (l.empty()) return;
@@ -893,7 +1250,7 @@ struct Selector {
             const Quadrant &qd = c.t->quadrants[a.quadrantID];
             bool keep = true;
             if (!a.lastDitch) {
-                int dv = GetVelocityID(qd.velocity, true) - GetVelocityID(bq.velocity, true);
+                int dv = VelocityRank(qd.velocity, true) - VelocityRank(bq.velocity, true);
                 if ((dv < 0 ? -dv : dv) > allowedVelocitySteps) keep = false;
             }
             if (fabsf(qd.angle.value() - bq.angle.value()) > allowedAngle) keep = false;
@@ -918,12 +1275,12 @@ struct Selector {
         l.count = kept;
     }
 
-    HDN void KeepBestBodyDirectionAnimations(AList &l, const PlayerCommand &cmd, bool strict, float allowedAngle = 0) {
+    HDN void KeepNearestLook(AList &l, const PlayerCommand &cmd, bool strict, float allowedAngle = 0) {
         ENG_SCOPE(32);
         if (l.empty()) return;
         Vec3 relLookAt;
         if (l.count > 1) relLookAt = RelativeLookAt();
-        // As in KeepBestDirectionAnimations: the first element of GRF's sorted list passes its
+        // As in KeepNearestQuadrant: the first element of GRF's sorted list passes its
         // own test, so the kept elements are filtered first and sorted after.
         auto key = [&](int i) { return DirectionSimilarityRating(A(i), pred, relLookAt); };
         const bool byBase = strict && cmd.desiredFunctionType != kFnMovement;
@@ -934,7 +1291,7 @@ struct Selector {
         if (byBase) SortBaseAnimation(l);
     }
 
-    HDN int GetIdleMovementAnimationID() {
+    HDN int IdleMovementAnimation() {
         // The crude selection of IdleMovementQuery, made once from the tables; only read here.
         const AList l{const_cast<int16_t *>(c.t->idleMovement), c.t->idleMovementCount};
         pred.idle = 1;
@@ -957,236 +1314,70 @@ struct Selector {
         });
     }
 
-    HDN Vec3 CalculatePhysicsVector(int ai, bool useDesiredMovement, const Vec3 &desiredMovement, bool useDesiredBody,
-                                    const Vec3 &desiredBodyRel, PList &out, float &rotationOffset) {
+    // The movement plan of animation `ai` into `out` (see MovementPlanner); returns the velocity it
+    // ends with and sets `rotationOffset`, the turn the plan adds to the animation's outgoing angle.
+    HDN Vec3 PlanMovement(int ai, bool useDesiredMovement, const Vec3 &desiredMovement, const Vec3 &desiredBodyRel, PList &out,
+                          float &rotationOffset) {
         ENG_SCOPE(38);
-        (void)useDesiredBody;
         const Anim &a = A(ai);
         const AnimDerived &d = D(ai);
-        SpatialState &s = S();
+        const SpatialState &s = S();
         const float angle = s.angle.value();
-        const libm::SinCos turn = Turn(angle);
-        out.count = 0;
-        int touchFrame = d.touchFrame;
-        bool touch = (touchFrame > 0);
-        float agility = Statistic(kStatAgility), accel = Statistic(kStatAcceleration), dribble = Statistic(kStatDribble);
-        float inSwitch = 0.0f, outSwitch = 0.0f;
-        const int at = a.animationType;
-        if (at == kAtBallControl) outSwitch = 0.0f;
-        else if (at == kAtTrap) outSwitch = 0.0f;
-        else if (at == kAtInterfere) outSwitch = 0.0f;
-        else if (at == kAtDeflect) outSwitch = 1.0f;
-        else if (at == kAtSliding) outSwitch = 0.0f;
-        else if (at == kAtSpecial) outSwitch = 1.0f;
-        else if (at == kAtTrip) outSwitch = 0.5f;
-        else if (touch) outSwitch = 1.0f;
-        if (a.incomingSpecialState != kStrEmpty || a.outgoingSpecialState != kStrEmpty) outSwitch = 1.0f;
-        Vec3 animIn = RotatedBy(Vec3(0, -1, 0), turn) * RangeVelocity(a.incomingVelocity);
-        Vec3 adaptedCur = animIn * inSwitch + s.movement * (1.0f - inSwitch);
-        Vec3 predOut = RotatedBy(a.outgoingMovement, turn);
-        Vec3 velDesired = useDesiredMovement ? desiredMovement : predOut;
-        Vec3 adaptedDesired = predOut * outSwitch + velDesired * (1.0f - outSwitch);
-        const float playerMaxVel = GetMaximumVelocity(*c.sd, hi);
-        float maxVel = playerMaxVel;
-        if (touch) maxVel *= 0.92f;
-        const int stepMs = 10;
-        float difficulty = d.difficultyFactor;
-        float difficultyPenalty =
-            libm::PowfPos(Clamp((difficulty - 0.0f) * (1.0f - (agility * 0.2f + accel * 0.2f)) * 2.0f, 0.0f, 1.0f), 0.7f);
-        float powerFactor = 1.0f - Clamp(libm::PowfPos(BaseLastTouchBias(1000), 0.8f) * (0.8f - dribble * 0.3f), 0.0f, 0.4f);
-        powerFactor *= 1.0f - Clamp(H().decayingPositionOffset.Length() * (10.0f - Statistic(kStatBalance) * 5.0f) - 0.1f,
-                                    0.0f, 0.3f);
-        Vec3 temporal = adaptedCur;
-        Vec3 curPos;
-        float physicsBias = 1.0f;
-        float maxUnder = 0.125f * PI, maxOver = 0.125f * PI, maxStraight = 0.125f * PI;
-        if (touch) {
-            float bonus = 1.0f - libm::PowfPos(NormalizedClamp((adaptedCur + predOut).Length() * 0.5f, 0, kSprintVelocity), 0.8f) * 0.8f;
-            bonus *= 0.6f + 0.4f * Statistic(kStatBallControl);
-            maxUnder = 0.2f * PI * bonus;
-            maxOver = 0;
-            maxStraight = 0.1f * PI * bonus;
-        }
-        if (at == kAtSliding) maxUnder = maxOver = maxStraight = 0.5f * PI;
-        if (at == kAtMovement) physicsBias *= 1.0f;
-        if (at == kAtBallControl) physicsBias *= 1.0f;
-        if (at == kAtTrap) physicsBias *= 1.0f;
-        if (at == kAtShortPass) physicsBias *= 0.0f;
-        if (at == kAtHighPass) physicsBias *= 0.0f;
-        if (at == kAtShot) physicsBias *= 0.0f;
-        if (at == kAtInterfere) physicsBias *= 0.5f;
-        if (at == kAtDeflect) physicsBias *= 0.0f;
-        if (at == kAtSliding) physicsBias *= 1.0f;
-        if (at == kAtTrip) physicsBias *= d.tripTypeIsOne ? 0.5f : 0.0f;
-        if (at == kAtSpecial) physicsBias *= 0.0f;
-        if (a.incomingSpecialState != kStrEmpty) physicsBias *= 0.0f;
-        const float accelMul = 0.5f + 0.5f;
-        float capped = 0;
-        if (physicsBias > 0.0f) {
-            Vec3 animOut = predOut.Normalized(0);
-            if (VelocityCat(predOut.Length()) == kVelIdle) animOut = RotatedBy(a.outgoingDirection, turn);
-            Vec3 desiredVec = adaptedDesired.Normalized(0);
-            if (VelocityCat(adaptedDesired.Length()) == kVelIdle) desiredVec = RotatedBy(desiredBodyRel, turn);
-            float toDesired = desiredVec.Angle2D(animOut);
-            if (fabsf(toDesired) <= 0.5f * PI || at == kAtSliding) {
-                float change = animOut.Angle2D(s.directionVec);
-                if (fabsf(change) > 0.06f * PI) {
-                    int sign = SignSide(change);
-                    if (SignSide(toDesired) == sign) capped = Clamp(toDesired, -maxOver, maxOver);
-                    else capped = Clamp(toDesired, -maxUnder, maxUnder);
-                } else {
-                    capped = Clamp(toDesired, -maxStraight, maxStraight);
-                }
-            }
-        }
-        const int effFrames = a.frameCount - 1;
-        const float adaptedDesiredVel = adaptedDesired.Length();
-        const Vec3 adaptedDesiredDir = adaptedDesired.Normalized(0);
+        MovementPlanner plan;
+        plan.at = a.animationType;
+        plan.touchFrame = d.touchFrame;
+        plan.touch = d.touchFrame > 0;
+        plan.turn = Turn(angle);
+        plan.agility = Statistic(kStatAgility);
+        plan.accel = Statistic(kStatAcceleration);
+        const bool special = a.incomingSpecialState != kStrEmpty || a.outgoingSpecialState != kStrEmpty;
+        // The velocity carried into the animation: the humanoid's own (the animation's incoming
+        // velocity takes no part in it).
+        const float incomingSwitch = 0.0f;
+        const Vec3 animIn = RotatedBy(Vec3(0, -1, 0), plan.turn) * RangeVelocity(a.incomingVelocity);
+        plan.velocity = animIn * incomingSwitch + s.movement * (1.0f - incomingSwitch);
+        const Vec3 predOut = RotatedBy(a.outgoingMovement, plan.turn);
+        const float outgoingSwitch = OutgoingSwitch(plan.at, plan.touch, special);
+        const Vec3 asked = useDesiredMovement ? desiredMovement : predOut;
+        const Vec3 desired = predOut * outgoingSwitch + asked * (1.0f - outgoingSwitch);
+        plan.playerMaxVel = GetMaximumVelocity(*c.sd, hi);
+        plan.maxVel = plan.touch ? plan.playerMaxVel * 0.92f : plan.playerMaxVel;
+        const float difficulty = d.difficultyFactor;
+        plan.difficultyPenalty = libm::PowfPos(
+            Clamp((difficulty - 0.0f) * (1.0f - (plan.agility * 0.2f + plan.accel * 0.2f)) * 2.0f, 0.0f, 1.0f), 0.7f);
+        plan.powerFactor = 1.0f - Clamp(libm::PowfPos(BaseLastTouchBias(1000), 0.8f) * (0.8f - Statistic(kStatDribble) * 0.3f), 0.0f, 0.4f);
+        plan.powerFactor *= 1.0f - Clamp(H().decayingPositionOffset.Length() * (10.0f - Statistic(kStatBalance) * 5.0f) - 0.1f,
+                                         0.0f, 0.3f);
+        plan.physicsBias = PhysicsShare(plan.at, d.tripTypeIsOne, a.incomingSpecialState != kStrEmpty);
+        const TurnCaps caps = PlanTurnCaps(plan.touch, plan.at == kAtSliding, plan.velocity, predOut,
+                                           plan.touch ? Statistic(kStatBallControl) : 0.0f);
+        plan.steer = plan.physicsBias > 0.0f ? PlanSteer(plan.at, caps, predOut, RotatedBy(a.outgoingDirection, plan.turn), desired,
+                                                         RotatedBy(desiredBodyRel, plan.turn), s.directionVec)
+                                             : 0.0f;
+        plan.lag = PlanFrameLag(plan.at, plan.physicsBias, plan.touch, plan.agility, difficulty);
+        plan.desiredVel = desired.Length();
+        plan.desiredDir = desired.Normalized(0);
         if (a.frameCount > kAnimPositions) Fatal("a fixed-capacity list outgrows its capacity");
-        // The frames read only these values of the animation, held in registers across the
-        // plan's stores.
-        const int frameCount = a.frameCount, lastFramesMs = (a.frameCount - 2) * 10;
-        const bool outgoingIdle = VelocityCat(a.outgoingVelocity) == kVelIdle;
-        const Vec3 outgoingTurned = RotatedBy(a.outgoingMovement, turn);
+        plan.effFrames = a.frameCount - 1;
+        plan.settleFrom = a.frameCount - 2;
+        plan.outgoingIdle = VelocityCat(a.outgoingVelocity) == kVelIdle;
+        plan.outgoingTurned = RotatedBy(a.outgoingMovement, plan.turn);
         const int32_t smoothedFirst = c.t->selection[ai].smoothedFirst;
-        const Vec3 *const smoothed = c.t->smoothed + (smoothedFirst >= 0 ? smoothedFirst : 0);
-        const Vec3 *const animPositions = c.t->positions + a.posFirst;
-        const int posCount = a.posCount;
-        Vec3 *const plan = out.e;
-        for (int frame = 0; frame < frameCount; frame++) {
-            const int tms = frame * stepMs;
-            float frameBias = (tms + 10) / (float)((effFrames + 1) * 10);
-            // The frame's part independent of the carried movement.
-            float lagExp = 1.0f;
-            if (physicsBias > 0.0f && (at == kAtBallControl || at == kAtMovement)) {
-                lagExp = 1.4f - 0.5f * 0.8f;
-                lagExp *= 1.2f - agility * 0.4f;
-                if (touch) lagExp += -0.1f + Clamp(difficulty * 0.4f, 0.0f, 0.5f);
-                else lagExp += -0.2f + Clamp(difficulty * 0.2f, 0.0f, 0.2f);
-                lagExp = Clamp(lagExp, 0.25f, 4.0f);
-                if (touch && tms < touchFrame * 10) lagExp = MaxF(lagExp, 0.7f);
-                lagExp = lagExp * physicsBias + 1.0f * (1.0f - physicsBias);
-            }
-            float adaptedFrameBias = lagExp == 1.0f ? frameBias : libm::powf(frameBias, lagExp);
-            const uint32_t animFrame = TruncToUint32(effFrames * adaptedFrameBias);
-            Vec3 animMov = RotatedBy(smoothedFirst >= 0 && animFrame < (uint32_t)posCount
-                                         ? smoothed[animFrame]
-                                         : MovementAtFrame(animPositions, posCount, animFrame, 1),
-                                     turn);
-            float animVel = animMov.Length();
-            Vec3 adaptedAnimMov = animMov;
-            float adaptedAnimVel = animVel;
-            if (animVel > kWalkSprintSwitch && (at == kAtMovement || at == kAtBallControl || at == kAtTrap)) {
-                if (maxVel > animVel) {
-                    adaptedAnimVel = StretchSprintTo(animVel, kAnimSprintVelocity, maxVel);
-                    adaptedAnimMov = adaptedAnimMov.Normalized(0) * adaptedAnimVel;
-                }
-            }
-            const Vec3 normMax = NormalizedMaximum(adaptedAnimMov, 1.0f);
-            const Vec3 normAdapted = adaptedAnimMov.Normalized(0);
-            const float rotation = capped * frameBias;
-            float rc, rs;
-            // Below 2^-12 the sine is the argument and the cosine 1, by the test of sinf/cosf.
-            if (libm::Top12f(rotation) < libm::Top12f(0x1p-12f)) {
-                rc = 1.0f;
-                rs = rotation;
-            } else {
-                libm::SinCos ft = libm::sincosf(rotation);
-                rc = ft.c;
-                rs = ft.s;
-            }
-            const float curvedTime = PhysicsCurvedTime(frame);
-            // The part carried from frame to frame.
-            float maxSlower = touch ? 1.2f : 1.6f;
-            float maxFaster = 0.0f;
-            const float tLen = temporal.Length();
-            if (tLen > adaptedAnimVel) maxFaster = MinF(0.0f + 1.0f * (1.0f - frameBias), MaxF(maxFaster, tLen - adaptedAnimVel));
-            if (maxFaster > 0) maxFaster *= MaxF(0.0f, normMax.Dot(adaptedDesiredDir));
-            if (at == kAtSliding) maxFaster = 100;
-            adaptedAnimVel = Clamp(adaptedDesiredVel, adaptedAnimVel - maxSlower, adaptedAnimVel + maxFaster);
-            adaptedAnimMov = normAdapted * adaptedAnimVel;
-            Vec3 result = RotatedCS(adaptedAnimMov, rc, rs);
-            result = result * physicsBias + animMov * (1.0f - physicsBias);
-            Vec3 toDesired = (result - temporal);
-            float penaltyBreak = 0.0f;
-            {
-                Vec3 predicted = temporal + toDesired;
-                float startVel = kIdleDribbleSwitch;
-                if (tLen > startVel && predicted.Length() > startVel) {
-                    const Vec3 pd = predicted.Normalized(), td = temporal.Normalized();
-                    float maf = 1.0f * (stepMs / 1000.0f);
-                    maf *= (0.7f + 0.3f * agility);
-                    if (!touch) maf *= 1.5f;
-                    float maxAngle = maf * PI;
-                    float vf = NormalizedClamp(tLen, 0, kSprintVelocity);
-                    maxAngle = maxAngle / (vf + 0.01f);
-                    float corner = pd.Angle2D(td);
-                    if (fabsf(corner) > maxAngle) {
-                        float over = fabsf(corner) - maxAngle;
-                        toDesired += -temporal * Clamp(over / PI * 3.0f, 0.0f, 1.0f);
-                    }
-                }
-            }
-            {
-                float maxChange = 0.03f;
-                if (at == kAtTrip) maxChange *= 0.7f;
-                if (at == kAtSliding) maxChange = 0.1f;
-                float vf = libm::PowfPos(NormalizedClamp(tLen, 0, kSprintVelocity), 1.5f);
-                float fsf = vf;
-                if (at == kAtMovement) fsf *= 0.4f;
-                maxChange *= (1.0f - fsf) + fsf * curvedTime;
-                maxChange *= 1.2f - vf * 0.4f;
-                maxChange *= 0.75f + 0.5f * 0.5f;
-                maxChange *= powerFactor;
-                float dl = toDesired.Length();
-                float maxAdd = maxChange * stepMs;
-                NormalizeMaximum(toDesired, MinF(dl, maxAdd));
-            }
-            if (at != kAtSliding && at != kAtDeflect) {
-                float velExp = 1.8f;
-                float accPower = 11.0f * accelMul;
-                float falloff = kIdleDribbleSwitch;
-                const float nextLen = (temporal + toDesired).Length();
-                if (nextLen > falloff) {
-                    accPower *= 1.0f - difficultyPenalty * 0.4f;
-                    float air = Clamp(libm::PowfPos(Clamp((tLen - falloff) / (playerMaxVel - falloff), 0.0f, 1.0f), velExp), 0.0f, 1.0f);
-                    Vec3 fwdv;
-                    if (nextLen > tLen) {
-                        Vec3 dest = temporal + toDesired;
-                        float acc = nextLen - tLen;
-                        fwdv = dest.Normalized(0) * acc;
-                    }
-                    float add = fwdv.Length();
-                    float maxAccPerSec = accPower * (1.0f - air) * (accel * 0.3f + 0.7f);
-                    float maxAccAdd = maxAccPerSec * (stepMs / 1000.0f);
-                    if (add > maxAccAdd) {
-                        float remaining = maxAccAdd / add;
-                        toDesired = toDesired - fwdv * (1.0f - remaining);
-                    }
-                }
-            }
-            Vec3 tmp = temporal + toDesired;
-            if (tms >= lastFramesMs) {
-                if (outgoingIdle && VelocityCat(tmp.Length()) != kVelIdle)
-                    tmp = Vec3(0);
-                else if (!outgoingIdle && VelocityCat(tmp.Length()) == kVelIdle)
-                    tmp = NormalizedTo(outgoingTurned, kDribbleVelocity);
-            }
-            temporal = tmp;
-            if (tms >= lastFramesMs) penaltyBreak = 0.0f;
-            curPos += temporal * (1.0f - penaltyBreak) * (stepMs / 1000.0f);
-            plan[frame] = curPos;
-        }
-        out.count = a.frameCount > 0 ? a.frameCount : 0;
-        Vec3 resulting = temporal;
-        if (VelocityCat(a.outgoingVelocity) != kVelIdle && VelocityCat(resulting.Length()) != kVelIdle)
-            rotationOffset = RotatedBy(resulting, BackTurn(angle)).Angle2D(a.outgoingMovement);
+        plan.smoothed = smoothedFirst >= 0 ? c.t->smoothed + smoothedFirst : nullptr;
+        plan.positions = c.t->positions + a.posFirst;
+        plan.posCount = a.posCount;
+        Vec3 *const frames = out.e;
+        const int frameCount = a.frameCount;
+        for (int frame = 0; frame < frameCount; frame++) frames[frame] = plan.Step(frame);
+        out.count = frameCount > 0 ? frameCount : 0;
+        if (!plan.outgoingIdle && VelocityCat(plan.velocity.Length()) != kVelIdle)
+            rotationOffset = RotatedBy(plan.velocity, BackTurn(angle)).Angle2D(a.outgoingMovement);
         else
-            rotationOffset = capped * physicsBias;
-        return resulting;
+            rotationOffset = plan.steer * plan.physicsBias;
+        return plan.velocity;
     }
 
-    HDN bool NeedTouch(int ai, const PlayerCommand &cmd) {
+    HDN bool BallControlNeedsTouch(int ai, const PlayerCommand &cmd) {
         const Anim &a = A(ai);
         SpatialState &s = S();
         // GRF: never true, a bool as float is idle, kept as written.
@@ -1210,7 +1401,7 @@ struct Selector {
         return false;
     }
 
-    HDN void CalculatePredictedSituation(Vec3 &predPos, float &predAngle) {
+    HDN void PredictedPose(Vec3 &predPos, float &predAngle) {
         ENG_SCOPE(22);
         AnimationState &cur = H().anim;
         const Anim &a = A(cur.anim);
@@ -1228,7 +1419,7 @@ struct Selector {
         return TruncToInt32(Clamp((float)P().desiredTimeToBallMs, (float)(int)P().timeToBallMs, 1000000.0f));
     }
 
-    HDN Vec3 CalculateMovementSmuggle() {
+    HDN Vec3 MovementSmuggle() {
         AnimationState &cur = H().anim;
         const Anim &a = A(cur.anim);
         const MatchState &m = w.match;
@@ -1245,10 +1436,10 @@ struct Selector {
         Vec3 predOut = OutgoingMovementOf(PList{cur.positions.e, cur.positions.count});
         Vec3 predPos;
         float predAngle;
-        CalculatePredictedSituation(predPos, predAngle);
+        PredictedPose(predPos, predAngle);
         Vec3 ballPos = MentalBallAt((int)future);
         float bh = ballPos.v[2];
-        Vec3 foot = GetFrontOfFootOffsetRelative(predOut.Length(), a.outgoingBodyAngle.value(), bh).Rotated2D(predAngle);
+        Vec3 foot = FootReachOffset(predOut.Length(), a.outgoingBodyAngle.value(), bh).Rotated2D(predAngle);
         Vec3 desiredBall = predPos + foot;
         if (!P().hasPossession) {
             Vec3 bs = MentalBallAt(0).Get2D(), be = MentalBallAt((int)future).Get2D();
@@ -1285,209 +1476,124 @@ struct Selector {
         return 0.0f;
     }
 
-    HDN static float BodyBallDistanceAdvantage(const Anim &a, const Vec3 &touchMov, const Vec3 &inMov, const Vec3 &outMov,
-                                               float outAngle, const Vec3 &bodyPos, const Vec3 &footOff,
-                                               const Vec3 &animBall2D, const Vec3 &actualBall2D, float radiusFactor,
-                                               float radiusCheat) {
-        const float cheatFactor = 0.5f, cheatBonus = 0.02f;
-        float inV = inMov.Length(), outV = outMov.Length();
-        float avgV = (inMov + outMov).Length() * 0.5f;
-        float vChange = outV - inV;
-        float vChangePerSec = vChange / (a.frameCount * 0.01f);
-        float bodyAnimBall = 1.0f - Curve(NormalizedClamp(((bodyPos + footOff.Normalized(0) * 0.1f) - animBall2D).Length(), 0.0f, 0.7f), 0.7f);
-        float bodyActualBall =
-            1.0f - Curve(NormalizedClamp(((bodyPos + footOff.Normalized(0) * 0.1f) - actualBall2D).Length(), 0.0f, 0.7f), 0.4f);
-        float velBonus = 1.0f - NormalizedClamp(avgV, kIdleVelocity, kSprintVelocity);
-        float velChangeBonus = 1.0f - NormalizedClamp(vChangePerSec / 20.0f, -1.0f, 1.0f);
-        float radius = radiusFactor;
-        radius *= 1.0f + 1.0f * bodyAnimBall + 0.6f * bodyActualBall + 0.8f * bodyAnimBall * bodyActualBall +
-                  0.0f * velChangeBonus + 1.0f * velBonus;
-        float effCheat = radiusCheat;
-        Vec3 outDir;
-        if (VelocityCat(outMov.Length()) == kVelIdle) outDir = Vec3(0, -1, 0).Rotated2D(outAngle);
-        else outDir = outMov.Normalized();
-        Vec3 behindU = -(inMov * 0.1f + touchMov * 0.2f + outMov * 0.7f);
-        Vec3 behind = behindU.Normalized(0) * libm::PowfPos(NormalizedClamp(behindU.Length(), 0, kSprintVelocity), 0.5f);
-        float dot = Vec3(0, -1, 0).Dot(outDir);
-        dot = 0.5f + Clamp(dot * 0.5f + 0.5f, 0.0f, 1.0f) * 0.5f;
-        behind *= dot;
-        Vec3 a2b = actualBall2D - animBall2D;
-        {
-            Vec3 su = inMov;
-            Vec3 sv = su.Normalized(outDir);
-            float toStraight = Vec3(0, -1, 0).Angle2D(sv);
-            a2b.Rotate2D(toStraight);
-            float lateral = 0.6f - 0.3f * libm::PowfPos(NormalizedClamp(su.Length(), kIdleVelocity, kSprintVelocity), 0.7f);
-            a2b.v[0] /= lateral;
-            radius *= libm::powf(1.0f / lateral, 0.5f);
-            a2b.Rotate2D(-toStraight);
-        }
-        Vec3 adaptedActual = animBall2D + a2b;
-        Vec3 behindCenter = animBall2D + behind * (radius + (effCheat * 0.6f)) * cheatFactor;
-        float allowed = (radius + effCheat) * cheatFactor + cheatBonus;
-        return GetDistance(adaptedActual, behindCenter) > allowed ? 0.0f : 1.0f;
+    // Whether the ball, `frame` frames ahead on the match's own prediction, is on the pitch (with
+    // the line's width and the ball's radius).
+    HD static bool BallOnPitchAt(const Vec3 *predictions, bool flip, int frame) {
+        Vec3 at = BallPredictRaw(predictions, frame * 10);
+        if (flip) at.Mirror();
+        return !(fabsf(at.v[0]) > kPitchHalfLength + kLineHalfWidth + 0.11f || fabsf(at.v[1]) > kPitchHalfWidth + kLineHalfWidth + 0.11f);
     }
 
-    HDN int GetBestCheatableAnimationID(const AList &sorted, bool useDesiredMovement, const Vec3 &desiredDir, float desiredVel,
-                                        bool useDesiredBody, const Vec3 &desiredBodyRel, PList &positions, int &touchFrameOut,
-                                        Vec3 &touchPosOut, Vec3 &actionSmuggleOut, float &rotationSmuggleOut,
-                                        bool preferPassAndShot = false) {
+    // One candidate of the touch search: its movement plan into `plan`, then its ball keys from the
+    // middle one down, then up from the one after the middle; true with the first key whose ball
+    // the body reaches (TouchProbe).
+    HDN bool TryTouchAnimation(const TouchSearch &ts, int ai, PList &plan, float &rotSmuggle, float &predAngle, Vec3 &outMov,
+                               Vec3 &smuggle, int &touchFrame) {
+        const Anim &a = A(ai);
+        PlanMovement(ai, ts.useDesiredMovement, ts.desiredMovement, ts.desiredBodyRel, plan, rotSmuggle);
+        predAngle = ModulateIntoRange(-PI, PI, a.outgoingAngle.value() + rotSmuggle);
+        outMov = RotatedBy(OutgoingMovementOf(plan), ts.back);
+        const int total = a.footballCount, middle = total / 2;
+        for (int tn = 0; tn < total; tn++) {
+            const FootballKey &key = c.t->football[a.footballFirst + (tn <= middle ? middle - tn : tn)];
+            if (!ts.retainerIsMe && !BallOnPitchAt(ts.predictions, ts.flip, key.frame)) continue;
+            const TouchProbe probe = ProbeKey(ts, a, D(ai).touchFrame, key, plan, outMov, predAngle);
+            if (probe.reaches) {
+                smuggle = probe.smuggle;
+                touchFrame = key.frame;
+                return true;
+            }
+        }
+        return false;
+    }
+
+    // A ball key of a candidate against the ball: the body at the key's frame of the plan, the
+    // animation's ball there (scaled to the player's height), the mental ball moved along its path
+    // to the point nearest it. The key fails on the height gap (TouchHeightMiss); otherwise the ball
+    // must lie within the reach (TouchReach) of the animation's ball (BallWithinReach).
+    HD TouchProbe ProbeKey(const TouchSearch &ts, const Anim &a, int defaultTouchFrame, const FootballKey &key, const PList &plan,
+                           const Vec3 &outMov, float predAngle) {
+        const int tf = key.frame;
+        const Vec3 touchMov = RotatedBy(MovementAtFrame(plan.e, plan.count, tf, 0), ts.back);
+        const Vec3 ballNow = ts.mental.At(tf * 10);
+        const Vec3 ballMov = RotatedBy((ts.mental.At(tf * 10 + 10) - ballNow) * 100.0f, ts.back);
+        const Vec3 ballAt = RotatedBy(ballNow - ts.position, ts.back);
+        const Vec3 touchPos = RotatedBy(plan[tf], ts.back);
+        Quat bodyOrientation;
+        Vec3 bodyOrigin;
+        float bodyAngle;
+        GetKeyFrameZ(c, a, kBpPlayer, tf, bodyOrientation, bodyOrigin, bodyAngle);
+        Vec3 animBall = (key.position - bodyOrigin) + touchPos;
+        animBall.v[2] = key.position.v[2] * (ts.height / kDefaultPlayerHeight);
+        // The ball's path from 6 ms before the key to 3 ms after, at its point nearest the
+        // animation's ball.
+        const Vec3 before = ballAt - ballMov * 0.006f, after = ballAt + ballMov * 0.003f;
+        const Vec3 ball = before + (after - before) * Clamp(LineClosestToPoint(before, after, animBall), 0.0f, 1.0f);
+        TouchProbe probe;
+        probe.smuggle = (ball - animBall).Get2D();
+        if (!(TouchHeightMiss(ts, a.baseAnimation, animBall.v[2], ball.v[2]) < 0.22f)) return probe;
+        const int offTouch = defaultTouchFrame - tf;
+        float awkward = NormalizedClamp((float)(offTouch < 0 ? -offTouch : offTouch), 0.0f, 4.0f);
+        awkward = awkward * awkward * 0.5f;
+        float late = libm::powf(tf / 24.0f, 0.7f);
+        if (late > 1.0f) late = 1.0f + ((late - 1.0f) * 0.5f);
+        TouchReach reach = KeyReach(ts.fn, awkward, ts.preferPassAndShot);
+        const float touchSpeed = touchMov.Length();
+        Vec3 foot = FootReachOffset(touchSpeed, bodyAngle, ball.v[2]);
+        if (VelocityCat(touchSpeed) != kVelIdle) foot.Rotate2D(FixAngle(touchMov.Normalized(Vec3(0, -1, 0)).Angle2D()));
+        // Right after the player's last touch the reach shrinks (less with good ball control).
+        const float sinceTouch = Curve(LastTouchBiasAt(600, ts.now + (uint64_t)(int64_t)(tf * 10)), 1.0f);
+        if (sinceTouch > 0.0f) {
+            const float f = 1.0f - sinceTouch * 0.97f * (1.0f - ts.ballControl * 0.1f);
+            reach.radius *= f;
+            reach.cheat *= f;
+        }
+        Vec3 body = touchPos;
+        body.v[2] = 0;
+        const ReachMotion motion{ts.inMov, touchMov, outMov, predAngle, a.frameCount};
+        probe.reaches = BallWithinReach(motion, body, foot, animBall.Get2D(), ball.Get2D(), reach.radius * late, reach.cheat) ||
+                        ts.retainerIsMe;
+        return probe;
+    }
+
+    // GRF's touch search over `sorted` (humanoid_base.cpp, GetBestCheatableAnimationID): the first
+    // candidate, in list order, whose plan brings a ball key to the ball. Returns it (-1 for none)
+    // with its plan, touch frame and position, the smuggle that moves the body onto the ball and
+    // the plan's rotation offset.
+    HDN int FindTouchAnimation(const AList &sorted, bool useDesiredMovement, const Vec3 &desiredDir, float desiredVel,
+                               const Vec3 &desiredBodyRel, PList &positions, int &touchFrameOut, Vec3 &touchPosOut,
+                               Vec3 &actionSmuggleOut, float &rotationSmuggleOut, bool preferPassAndShot = false) {
         ENG_SCOPE(31);
         const MatchState &m = w.match;
-        SpatialState &s = S();
+        const SpatialState &s = S();
         const float angle = s.angle.value();
-        const bool retainerIsMe = m.ballRetainer == hi;
-        if (m.ballRetainer != -1 && !retainerIsMe) return -1;
-        const libm::SinCos bk = BackTurn(angle);
-        Vec3 inMov = RotatedBy(s.movement, bk);
-        int best = -1;
-        Vec3 bestSmuggle2D;
-        Vec3 desiredMovement = desiredDir * desiredVel;
-        float height = c.sd->data[hi].height;
-        const int fn = StringToFunctionType(A(sorted[0]).animationType);
-        float tmpRotSmuggle = 0, predAngle = 0;
-        Vec3 adaptedOut;
-        bool found = false;
+        if (m.ballRetainer != -1 && m.ballRetainer != hi) return -1;
         // What the keys read of the match, which the evaluations leave unchanged.
-        const MentalBallView mental(w, MentalImg());
-        const Vec3 position = s.position;
-        const Vec3 *const ballPredictions = m.ball.predictions;
-        const bool ballFlip = m.ball.lazyFlip;
-        const FootballKey *const footballKeys = c.t->football;
-        const float ballControl = Statistic(kStatBallControl);
-        const uint64_t now = m.actualTimeMs;
-        // One candidate: its physics plan into `plan`, then its ball keys from the middle one down,
-        // then up; true with the touch at the first key the body reaches.
-        auto evaluate = [&](int ai, PList &plan, float &rotSmuggle, float &predAngleOut, Vec3 &adaptedOutOut, Vec3 &smuggleOut,
-                            int &touchFrame) -> bool {
-            bool hit = false;
-            const Anim &a = A(ai);
-            bool isBase = a.baseAnimation;
-            CalculatePhysicsVector(ai, useDesiredMovement, desiredMovement, useDesiredBody, desiredBodyRel, plan, rotSmuggle);
-            predAngleOut = a.outgoingAngle.value() + rotSmuggle;
-            predAngleOut = ModulateIntoRange(-PI, PI, predAngleOut);
-            const float predAngle = predAngleOut;
-            PList &positions = plan;
-            Vec3 outMov = RotatedBy(OutgoingMovementOf(positions), bk);
-            adaptedOutOut = outMov;
-            const Vec3 adaptedOut = outMov;
-            const int total = a.footballCount;
-            int defaultTouchFrame = D(ai).touchFrame;
-            for (int tn = 0; tn < total && !hit; tn++) {
-                const int key = tn <= total / 2 ? total / 2 - tn : tn;
-                const FootballKey &fk = footballKeys[a.footballFirst + key];
-                Vec3 animBall = fk.position;
-                int tf = fk.frame;
-                if (!retainerIsMe) {
-                    Vec3 abs = BallPredictRaw(ballPredictions, tf * 10);
-                    if (ballFlip) abs.Mirror();
-                    if (fabsf(abs.v[0]) > kPitchHalfLength + kLineHalfWidth + 0.11f ||
-                        fabsf(abs.v[1]) > kPitchHalfWidth + kLineHalfWidth + 0.11f)
-                        continue;
-                }
-                Vec3 touchMov = RotatedBy(MovementAtFrame(positions.e, positions.count, tf, 0), bk);
-                Vec3 ballPos = mental.At(tf * 10);
-                Vec3 ballMov = (mental.At(tf * 10 + 10) - ballPos) * 100.0f;
-                ballPos = RotatedBy(ballPos - position, bk);
-                ballMov = RotatedBy(ballMov, bk);
-                const Vec3 touchPos = RotatedBy(positions[tf], bk);
-                Vec3 bodyPos = touchPos;
-                bodyPos.v[2] = 0;
-                Quat abr;
-                Vec3 abp;
-                float z;
-                GetKeyFrameZ(c, a, kBpPlayer, tf, abr, abp, z);
-                float abh = animBall.v[2];
-                animBall = (animBall - abp) + touchPos;
-                animBall.v[2] = abh * (height / kDefaultPlayerHeight);
-                {
-                    Vec3 before = ballPos - ballMov * 0.006f, after = ballPos + ballMov * 0.003f;
-                    float fr = Clamp(LineClosestToPoint(before, after, animBall), 0.0f, 1.0f);
-                    ballPos = before + (after - before) * fr;
-                }
-                Vec3 smuggle3D = ballPos - animBall;
-                Vec3 smuggle2D = smuggle3D.Get2D();
-                float dz = fabsf(smuggle3D.v[2]);
-                dz *= 1.0f - Clamp((float)(((double)animBall.v[2] - 0.11) * (double)0.3f), 0.0f, 0.2f);
-                dz *= 1.0f - Clamp((float)(((double)ballPos.v[2] - 0.11) * (double)0.4f), 0.0f, 0.3f);
-                if (ballPos.v[2] > 1.8f && ballPos.v[2] > animBall.v[2] + 0.12f) dz *= 2.0f;
-                if (ballPos.v[2] > 2.6f && ballPos.v[2] > animBall.v[2] + 0.08f) dz *= 20.0f;
-                if (fn == kFnDeflect) dz *= 0.8f;
-                if (retainerIsMe) dz = 0.0f;
-                if (ballPos.v[2] < 0.5f && isBase) dz = MaxF(dz - 0.15f, 0.0f);
-                if (dz < 0.22f) {
-                    int dtf = defaultTouchFrame - tf;
-                    float awk = NormalizedClamp((float)(dtf < 0 ? -dtf : dtf), 0.0f, 4.0f);
-                    awk = awk * awk * 0.5f;
-                    float tff = tf / 24.0f;
-                    tff = libm::powf(tff, 0.7f);
-                    if (tff > 1.0f) tff = 1.0f + ((tff - 1.0f) * 0.5f);
-                    float cheatOff = 0.0f;
-                    float rf = 0.3f * (1.0f - awk);
-                    if (fn == kFnDeflect) {
-                        rf *= 1.8f;
-                        cheatOff += 0.4f;
-                    }
-                    if (fn == kFnSliding) {
-                        rf *= 0.2f;
-                        cheatOff = 0.0f;
-                    }
-                    if (fn == kFnInterfere) {
-                        rf *= 1.4f;
-                        cheatOff += 0.2f;
-                    }
-                    if (fn == kFnShortPass || fn == kFnLongPass || fn == kFnHighPass || fn == kFnShot) {
-                        rf *= 1.3f;
-                        cheatOff += 0.15f;
-                    }
-                    if ((fn == kFnTrap || fn == kFnBallControl) && preferPassAndShot) rf *= 0.3f;
-                    cheatOff *= (1.0f - awk);
-                    float tv = touchMov.Length();
-                    Vec3 foot = GetFrontOfFootOffsetRelative(tv, z, ballPos.v[2]);
-                    if (VelocityCat(tv) != kVelIdle) foot.Rotate2D(FixAngle(touchMov.Normalized(Vec3(0, -1, 0)).Angle2D()));
-                    float ltb = Curve(LastTouchBiasAt(600, now + (uint64_t)(int64_t)(tf * 10)), 1.0f);
-                    if (ltb > 0.0f) {
-                        float f = 1.0f - ltb * 0.97f * (1.0f - ballControl * 0.1f);
-                        rf *= f;
-                        cheatOff *= f;
-                    }
-                    float adv = BodyBallDistanceAdvantage(a, touchMov, inMov, adaptedOut, predAngle, bodyPos, foot, animBall.Get2D(),
-                                                          ballPos.Get2D(), rf * tff, cheatOff);
-                    if (adv >= 1.0f || retainerIsMe) {
-                        hit = true;
-                        smuggleOut = smuggle2D;
-                        touchFrame = tf;
-                    }
-                }
-            }
-            return hit;
-        };
+        const TouchSearch ts(w, MentalImg(), hi, StringToFunctionType(A(sorted[0]).animationType), BackTurn(angle),
+                             s.movement, s.position, c.sd->data[hi].height, Statistic(kStatBallControl), preferPassAndShot,
+                             useDesiredMovement, desiredDir * desiredVel, desiredBodyRel);
         // A candidate passes only at a key where the ball is on the pitch and passes the height
-        // test (dz < 0.22). The plan moves the ball's height at a key only between its heights just
-        // before and just after the key, so a key whose ball height lies far enough from that span
-        // fails the test whatever the plan. The lanes keep, in list order, the candidates with a
-        // key that may pass; the others fail without a plan. The bound's factors are the smallest
-        // the test can apply, with margins over the rounding.
+        // test. The plan moves the ball's height at a key only between its heights just before
+        // and just after the key, so a key whose ball height lies far enough from that span fails
+        // the test whatever the plan. The lanes keep, in list order, the candidates with a key
+        // that may pass; the others fail without a plan. The bound's factors are the smallest the
+        // test can apply, with margins over the rounding.
         auto mayPass = [&](int ai) -> bool {
-            if (retainerIsMe) return true;
+            if (ts.retainerIsMe) return true;
             const Anim &a = A(ai);
             for (int key = 0; key < a.footballCount; key++) {
-                const FootballKey &fk = footballKeys[a.footballFirst + key];
+                const FootballKey &fk = c.t->football[a.footballFirst + key];
                 const int tf = fk.frame;
-                Vec3 abs = BallPredictRaw(ballPredictions, tf * 10);
-                if (ballFlip) abs.Mirror();
-                if (fabsf(abs.v[0]) > kPitchHalfLength + kLineHalfWidth + 0.11f ||
-                    fabsf(abs.v[1]) > kPitchHalfWidth + kLineHalfWidth + 0.11f)
-                    continue;
-                const float m0 = mental.At(tf * 10).v[2], m1 = mental.At(tf * 10 + 10).v[2];
-                const float z = m0 - position.v[2], dzdt = (m1 - m0) * 100.0f;
+                if (!BallOnPitchAt(ts.predictions, ts.flip, tf)) continue;
+                const float m0 = ts.mental.At(tf * 10).v[2], m1 = ts.mental.At(tf * 10 + 10).v[2];
+                const float z = m0 - ts.position.v[2], dzdt = (m1 - m0) * 100.0f;
                 const float zBefore = z - dzdt * 0.006f, zAfter = z + dzdt * 0.003f;
                 const float slack = (fabsf(zBefore) + fabsf(zAfter)) * 1e-5f + 1e-6f;
                 const float lo = MinF(zBefore, zAfter) - slack, hi = MaxF(zBefore, zAfter) + slack;
-                const float az = fk.position.v[2] * (height / kDefaultPlayerHeight);
+                const float az = fk.position.v[2] * (ts.height / kDefaultPlayerHeight);
                 const float gap = az < lo ? lo - az : az > hi ? az - hi : 0.0f;
                 float bound = gap * (1.0f - Clamp((float)(((double)az - 0.11) * (double)0.3f), 0.0f, 0.2f)) * 0.69f;
-                if (fn == kFnDeflect) bound *= 0.8f;
+                if (ts.fn == kFnDeflect) bound *= 0.8f;
                 if (a.baseAnimation && lo < 0.5f) bound -= 0.15f;
                 if (!(bound > 0.2201f)) return true;
             }
@@ -1504,24 +1610,26 @@ struct Selector {
         GroupSync();
         // The lanes of the match evaluate consecutive candidates; the earliest that passes wins.
         // Without one the caller reads neither the plan nor the rotation.
+        int best = -1;
+        float rotSmuggle = 0, predAngle = 0;
+        Vec3 outMov, smuggle;
         positions.count = 0;
-        for (int e0 = 0; e0 < candidates.count && !found; e0 += kGroupLanes) {
+        for (int e0 = 0; e0 < candidates.count && best < 0; e0 += kGroupLanes) {
             const int entry = e0 + GroupRank();
             PList mine{kGroupLanes == 1 ? positions.e : c.ws->lanePlans[GroupRank()], 0};
             float rot = 0, pa = 0;
             Vec3 ao, sm;
             int tf = 0;
-            const bool ok = entry < candidates.count && evaluate(candidates[entry], mine, rot, pa, ao, sm, tf);
+            const bool ok = entry < candidates.count && TryTouchAnimation(ts, candidates[entry], mine, rot, pa, ao, sm, tf);
             const LaneMask passed = GroupBallot(ok);
             if (!passed) continue;
             const int from = LowestBit(passed);
-            tmpRotSmuggle = GroupShuffle(rot, from);
+            rotSmuggle = GroupShuffle(rot, from);
             const int count = GroupShuffle((int32_t)mine.count, from);
-            found = true;
             best = candidates[e0 + from];
             predAngle = GroupShuffle(pa, from);
-            adaptedOut = GroupShuffle(ao, from);
-            bestSmuggle2D = GroupShuffle(sm, from);
+            outMov = GroupShuffle(ao, from);
+            smuggle = GroupShuffle(sm, from);
             touchFrameOut = GroupShuffle((int32_t)tf, from);
             if (kGroupLanes > 1) {
                 GroupSync();
@@ -1531,36 +1639,35 @@ struct Selector {
             }
             positions.count = count;
         }
-        if (found) {
+        if (best >= 0) {
             touchPosOut = MentalBallAt(touchFrameOut * 10);
-            actionSmuggleOut = RotatedBy(bestSmuggle2D, Turn(angle));
-            float sd = actionSmuggleOut.Length();
-            float discard = 0.4f;
-            if (fn != kFnBallControl) discard *= 0.8f;
-            if (touchPosOut.v[2] > 0.5f) discard *= 0.7f;
-            if (touchPosOut.v[2] > 1.0f) discard *= 0.7f;
-            float discardBonus = 0.0f;
-            if (fn == kFnInterfere) discardBonus += 0.1f;
-            sd = Clamp(sd - (0.02f + discardBonus), 0.0f, (float)100.0);
-            sd *= 1.0f - discard;
-            sd = MinF(sd, actionSmuggleOut.Length() - 0.2f);
-            if (retainerIsMe) sd = 0.0f;
-            actionSmuggleOut = actionSmuggleOut.Normalized(0) * sd;
-            {
-                float toStraight = angle + predAngle;
-                actionSmuggleOut.Rotate2D(-toStraight);
-                float shorten = 0.02f;
-                float allowFwd = 0.25f *
-                                 (1.0f - libm::powf(NormalizedClamp(adaptedOut.Length(), kIdleVelocity, kSprintVelocity - 2.0f), 0.6f)) *
-                                 (touchFrameOut * 0.1f);
-                if (fn != kFnBallControl && fn != kFnTrap) allowFwd += 0.1f;
-                if (actionSmuggleOut.v[1] < 0.0f) actionSmuggleOut.v[1] = Clamp(actionSmuggleOut.v[1] + shorten, -allowFwd, 0.0f);
-                actionSmuggleOut.Rotate2D(toStraight);
-            }
-            actionSmuggleOut *= 0.7f + 0.3f * NormalizedClamp(ClosestOpponentDistance(w, hi), 0.6f, 1.2f);
+            actionSmuggleOut = ShapeActionSmuggle(ts, RotatedBy(smuggle, Turn(angle)), touchPosOut.v[2], angle + predAngle,
+                                                  outMov.Length(), touchFrameOut);
         }
-        rotationSmuggleOut = tmpRotSmuggle;
+        rotationSmuggleOut = rotSmuggle;
         return best;
+    }
+
+    // The smuggle that moves the body onto the ball through the touch: the gap less a discard
+    // (more for ball control, less for a high ball) and 2 cm (more for interference), never more
+    // than the gap less 20 cm, none for the ball's retainer; along the outgoing direction it only
+    // shortens, by at most what a slow, late touch allows; less near an opponent.
+    HD Vec3 ShapeActionSmuggle(const TouchSearch &ts, const Vec3 &gap, float ballHeight, float outgoingAngle, float outSpeed,
+                               int touchFrame) {
+        float keep = 1.0f - 0.4f * (ts.fn != kFnBallControl ? 0.8f : 1.0f) * (ballHeight > 0.5f ? 0.7f : 1.0f) *
+                                (ballHeight > 1.0f ? 0.7f : 1.0f);
+        float length = Clamp(gap.Length() - (0.02f + (ts.fn == kFnInterfere ? 0.1f : 0.0f)), 0.0f, (float)100.0);
+        length *= keep;
+        length = MinF(length, gap.Length() - 0.2f);
+        if (ts.retainerIsMe) length = 0.0f;
+        Vec3 smuggle = gap.Normalized(0) * length;
+        smuggle.Rotate2D(-outgoingAngle);
+        float forward = 0.25f * (1.0f - libm::powf(NormalizedClamp(outSpeed, kIdleVelocity, kSprintVelocity - 2.0f), 0.6f)) *
+                        (touchFrame * 0.1f);
+        if (ts.fn != kFnBallControl && ts.fn != kFnTrap) forward += 0.1f;
+        if (smuggle.v[1] < 0.0f) smuggle.v[1] = Clamp(smuggle.v[1] + 0.02f, -forward, 0.0f);
+        smuggle.Rotate2D(outgoingAngle);
+        return smuggle * (0.7f + 0.3f * NormalizedClamp(ClosestOpponentDistance(w, hi), 0.6f, 1.2f));
     }
 
     HD void InstallAnimation(int sel, int fn, int interrupt, int touchFrame, const Vec3 &touchPos, float rotScale,
@@ -1613,46 +1720,45 @@ struct Selector {
         }
     }
 
-    HDN SelectResult BaseSelectAnimation(const PlayerCommand &cmd, int interrupt) {
-        AnimationState &cur = H().anim;
-        SpatialState &s = S();
-        const int fn = cmd.desiredFunctionType;
-        ApplyOutgoingState(interrupt);
-        const Anim &current = A(cur.anim);
-        const float angle = s.angle.value();
+    // The crude query of an official's command: strict incoming velocity and body direction.
+    HD CrudeQuery OfficialQuery(const PlayerCommand &cmd, int fn) {
+        const SpatialState &s = S();
         CrudeQuery q;
         q.byFunctionType = true;
         q.functionType = fn;
         q.byIncomingVelocity = true;
         q.incomingVelocity = s.velocityCat;
         q.incomingVelocityStrict = true;
-        q.byIncomingBodyDirection = true;
-        q.incomingBodyDirectionStrict = true;
-        q.incomingBodyDirection = s.relBodyDirectionVec;
         q.incomingVelocityForceLinearity = true;
+        q.byIncomingBodyDirection = true;
+        q.incomingBodyDirection = s.relBodyDirectionVec;
+        q.incomingBodyDirectionStrict = true;
         q.incomingBodyDirectionForceLinearity = true;
-        if (fn == kFnTrip) {
-            q.byTripType = true;
-            q.tripType = cmd.tripType;
-        }
-        q.incomingSpecialState = current.outgoingSpecialState;
-        if (w.match.ballRetainer == hi) q.incomingRetainState = D(cur.anim).outgoingRetainRawValue;
-        if (cmd.useSpecialVar1) q.specialVar1 = (float)cmd.specialVar1;
-        if (cmd.useSpecialVar2) q.specialVar2 = (float)cmd.specialVar2;
-        if (current.outgoingSpecialState != kStrEmpty) q.incomingVelocity = kVelIdle;
+        FinishQuery(q, cmd, fn, w.match.ballRetainer == hi);
+        return q;
+    }
+
+    // An official's animation for a command (GRF's HumanoidBase::SelectAnimation): for movement,
+    // trips and specials, the first candidate of the query by the ranking, with its movement plan;
+    // other function types select nothing.
+    HDN SelectResult SelectOfficialAnimation(const PlayerCommand &cmd, int interrupt) {
+        AnimationState &cur = H().anim;
+        const SpatialState &s = S();
+        const int fn = cmd.desiredFunctionType;
+        ApplyOutgoingState(interrupt);
+        const float angle = s.angle.value();
         AList l{c.ws->lists[0], 0};
-        CrudeSelection(c, q, l);
+        FilterAnimations(c, OfficialQuery(cmd, fn), l);
         if (l.empty()) {
-            if (fn == kFnMovement) l.push_back(GetIdleMovementAnimationID());
-            else return kSelectFalse;
+            if (fn != kFnMovement) return kSelectFalse;
+            l.push_back(IdleMovementAnimation());
         }
         if (cmd.useDesiredMovement) {
-            Vec3 rel = RotatedBy(cmd.desiredDirection, BackTurn(angle));
-            SetMovementSimilarityPredicate(rel, VelocityCat(cmd.desiredVelocityFloat));
+            SetMovementSimilarityPredicate(RotatedBy(cmd.desiredDirection, BackTurn(angle)), VelocityCat(cmd.desiredVelocityFloat));
             pred.lookAt = cmd.desiredLookAt;
             if (fn == kFnMovement) {
-                KeepBestDirectionAnimations(l, cmd, true);
-                if (cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, true);
+                KeepNearestQuadrant(l, cmd, true);
+                if (cmd.useDesiredLookAt) KeepNearestLook(l, cmd, true);
             } else {
                 Sort(l, [&](int i) { return MovementSimilarityKey(i); });
             }
@@ -1662,126 +1768,110 @@ struct Selector {
         pred.relIncomingBodyDirection = s.relBodyDirectionVec;
         pred.incomingVelocity = s.velocityCat;
         if (cmd.useDesiredTripDirection) pred.relDesiredTripDirection = RotatedBy(cmd.desiredTripDirection, BackTurn(angle));
-        int sel = -1;
+        if (l.empty() || !(fn == kFnMovement || fn == kFnTrip || fn == kFnSpecial)) return kSelectFalse;
+        const int sel = FirstOfChain(l, fn, cmd.useDesiredTripDirection, 4, false);
+        Vec3 lookRel = Vec3(0, -1, 0);
+        if (cmd.useDesiredLookAt)
+            lookRel = (RotatedBy((cmd.desiredLookAt - s.position).Get2D(), BackTurn(angle)) - A(sel).translation).Normalized(Vec3(0, -1, 0));
         PList plan{c.ws->plans[0], 0};
-        float rotSmuggle = 0;
-        if (l.empty()) return kSelectFalse;
-        const bool byTrip = cmd.useDesiredTripDirection, byBase = fn != kFnMovement;
-        const int qi = l.count > 1 ? IncomingBodyDirectionQuery() : 0;
-        const int first = FirstOfSortChain(l, 4 + byTrip + byBase, [&](int i, double *k) {
-            int n = 0;
-            if (byBase) k[n++] = A(i).baseAnimation ? 0 : 1;
-            if (byTrip) k[n++] = -D(i).bumpDirection.Dot(pred.relDesiredTripDirection);
-            k[n++] = KeyIncomingVelocity(A(i), pred);
-            k[n++] = IncomingBodyDirectionKey(i, qi);
-            k[n++] = KeyFoot(A(i), pred);
-            k[n++] = KeyIdle(A(i), pred);
-        });
-        if (fn == kFnMovement || fn == kFnTrip || fn == kFnSpecial) {
-            sel = first;
-            const Anim &na = A(sel);
-            Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
-            Vec3 dbr = Vec3(0, -1, 0);
-            if (cmd.useDesiredLookAt)
-                dbr = (RotatedBy((cmd.desiredLookAt - s.position).Get2D(), BackTurn(angle)) - na.translation).Normalized(Vec3(0, -1, 0));
-            CalculatePhysicsVector(sel, cmd.useDesiredMovement, dm, cmd.useDesiredLookAt, dbr, plan, rotSmuggle);
-        }
-        if (interrupt == kIntReQueue && sel != -1 && cur.positions.count > 1 && plan.count > 1) {
-            const Anim &sa = A(sel);
-            bool curIdle = VelocityCat(current.outgoingVelocity) == kVelIdle;
-            if (cur.functionType == fn && ((!curIdle && current.quadrantID == sa.quadrantID) ||
-                                           (curIdle && fabsf(PreferredOutgoingAngle(cur.anim) - PreferredOutgoingAngle(sel)) < 0.20f * PI)))
-                sel = -1;
-        }
-        if (sel == -1) return kSelectFalse;
-        InstallAnimation(sel, fn, interrupt, -1, Vec3(), 1.0f, rotSmuggle, Vec3(), plan, cmd);
+        float rotation = 0;
+        PlanMovement(sel, cmd.useDesiredMovement, cmd.desiredDirection * cmd.desiredVelocityFloat, lookRel, plan, rotation);
+        if (interrupt == kIntReQueue && cur.positions.count > 1 && plan.count > 1 && RestartsCurrent(sel, fn, 0.20f * PI, false))
+            return kSelectFalse;
+        InstallAnimation(sel, fn, interrupt, -1, Vec3(), 1.0f, rotation, Vec3(), plan, cmd);
         return kSelectTrue;
     }
 
-    HDN SelectResult SelectAnimation(const PlayerCommand &cmd, int interrupt, bool preferPassAndShot) {
-        ENG_SCOPE(14);
-        Player &player = P();
-        Humanoid &h = H();
-        AnimationState &cur = h.anim;
-        SpatialState &s = S();
+    // Whether the ball is out of a touch's range (function types other than movement, trips,
+    // specials and sliding): more than 10 m away in 200 ms; more than 2 m away at the touch and
+    // further from where the humanoid will be then than it is now; or, for the non-retainer and
+    // all but deflections, seen more than 2 m from where it will be a second ahead.
+    HD bool BallOutOfTouchRange(int fn, bool retainerIsMe) {
+        const SpatialState &s = S();
+        const bool needsBall = fn != kFnMovement && fn != kFnTrip && fn != kFnSpecial && fn != kFnSliding;
+        if (!needsBall) return false;
+        if ((MentalBallAt(200).Get2D() - s.position).Length() > 10.0f) return true;
+        const Vec3 atTouch = MentalBallAt(kDefaultTouchOffsetMs).Get2D();
+        const Vec3 humanoidThen = s.position + s.movement * (float)kDefaultTouchOffsetMs * (float)0.001;
+        if ((atTouch - s.position).Length() > 2.0f && (atTouch - humanoidThen).Length() > (MentalBallAt(0).Get2D() - s.position).Length())
+            return true;
+        return fn != kFnDeflect && !retainerIsMe && (MentalBallAt(1000) - BallPredict(w.match.ball, 1000)).Length() > 2.0f;
+    }
+
+    // GRF's rules for a command that arrives while an animation runs (a requeue): true when the
+    // running animation stays. Movement never replaces another function; a running movement stays
+    // for a player with the ball or far (12 m) from the designated player, in its last 6 frames or
+    // while requeues are delayed; ball control stays after frame 8 or while delayed, and against a
+    // trap; a trap stays within 6 frames of its touch or while delayed. Any of them stays for the
+    // command it came from (within 1.5 m/s) and, in a movement, ball control or trap, for a
+    // command close to what it already plans; movement stays against ball control just after a
+    // kick of the player's own ball, unless the velocity changes by 1 m/s or more.
+    HD bool RequeueKeepsCurrent(const PlayerCommand &cmd, int fn) {
+        const Player &player = P();
+        const Humanoid &h = H();
+        const AnimationState &cur = h.anim;
+        const SpatialState &s = S();
         const MatchState &m = w.match;
-        const int fn = cmd.desiredFunctionType;
-        const bool retainerIsMe = m.ballRetainer == hi;
-        if (fn != kFnMovement && fn != kFnTrip && fn != kFnSpecial && fn != kFnSliding) {
-            if ((MentalBallAt(200).Get2D() - s.position).Length() > 10.0f) return kSelectFalse;
-            if ((MentalBallAt(kDefaultTouchOffsetMs).Get2D() - s.position).Length() > 2.0f &&
-                (MentalBallAt(kDefaultTouchOffsetMs).Get2D() - (s.position + s.movement * (float)kDefaultTouchOffsetMs * (float)0.001)).Length() >
-                    (MentalBallAt(0).Get2D() - s.position).Length())
-                return kSelectFalse;
+        const int running = cur.functionType;
+        const bool delayed = h.requeueDelayFrames > 0;
+        const bool runningMovement = running == kFnMovement, runningControl = running == kFnBallControl, runningTrap = running == kFnTrap;
+        if (fn == kFnMovement) {
+            if (!runningMovement) return true;
+            const float focus = (Sp(w, m.designatedPossessionPlayer).position - s.position).Length();
+            if (player.hasPossession || focus > 12.0f || cur.frameNum + 6 > A(cur.anim).frameCount - 1 || delayed) return true;
         }
-        if (fn != kFnMovement && fn != kFnTrip && fn != kFnSpecial && fn != kFnSliding && fn != kFnDeflect && !retainerIsMe) {
-            if ((MentalBallAt(1000) - BallPredict(m.ball, 1000)).Length() > 2.0f) return kSelectFalse;
+        if (runningControl && fn == kFnBallControl && (cur.frameNum > 8 || delayed)) return true;
+        if (runningControl && fn == kFnTrap) return true;
+        if (runningTrap && (fn == kFnTrap || fn == kFnBallControl) && (cur.frameNum + 6 > cur.touchFrame || delayed)) return true;
+        const Vec3 asked = cmd.desiredDirection * cmd.desiredVelocityFloat;
+        const PlayerCommand &origin = cur.originatingCommand;
+        if (origin.desiredFunctionType == fn && ((origin.desiredDirection * origin.desiredVelocityFloat) - asked).Length() < 1.5f)
+            return true;
+        const bool continues = (runningMovement && fn == kFnMovement) || (runningControl && fn == kFnBallControl) ||
+                               (runningTrap && (fn == kFnBallControl || fn == kFnTrap));
+        if (continues) {
+            const Vec3 planned = cur.outgoingMovement - cur.incomingMovement;
+            const Vec3 wanted = asked - s.movement;
+            const float agreement = wanted.Dot(planned), gap = GetDistance(wanted, planned);
+            if ((agreement > 0.0f && gap < 4.0f) || agreement > 0.8f || gap < 2.0f) return true;
         }
-        if (interrupt == kIntReQueue) {
-            if (m.designatedPossessionPlayer < 0) return kSelectUnsupported;
-            float focus = (Sp(w, m.designatedPossessionPlayer).position - s.position).Length();
-            const int cf = cur.functionType;
-            const int eff = A(cur.anim).frameCount - 1;
-            if (cf != kFnMovement && fn == kFnMovement) return kSelectFalse;
-            if (cf == kFnMovement && fn == kFnMovement && (player.hasPossession || focus > 12.0f)) return kSelectFalse;
-            if (cf == kFnMovement && fn == kFnMovement && cur.frameNum + 6 > eff) return kSelectFalse;
-            if (cf == kFnMovement && fn == kFnMovement && h.requeueDelayFrames > 0) return kSelectFalse;
-            if (cf == kFnBallControl && fn == kFnBallControl && (cur.frameNum > 8 || h.requeueDelayFrames > 0)) return kSelectFalse;
-            if (cf == kFnBallControl && fn == kFnTrap) return kSelectFalse;
-            if (cf == kFnTrap && fn == kFnTrap && (cur.frameNum + 6 > cur.touchFrame || h.requeueDelayFrames > 0)) return kSelectFalse;
-            if (cf == kFnTrap && fn == kFnBallControl && (cur.frameNum + 6 > cur.touchFrame || h.requeueDelayFrames > 0))
-                return kSelectFalse;
-            const PlayerCommand &oc = cur.originatingCommand;
-            if (oc.desiredFunctionType == fn &&
-                ((oc.desiredDirection * oc.desiredVelocityFloat) - (cmd.desiredDirection * cmd.desiredVelocityFloat)).Length() < 1.5f)
-                return kSelectFalse;
-            if ((cf == kFnMovement && fn == kFnMovement) || (cf == kFnBallControl && fn == kFnBallControl) ||
-                (cf == kFnTrap && fn == kFnBallControl) || (cf == kFnTrap && fn == kFnTrap)) {
-                Vec3 planned = cur.outgoingMovement - cur.incomingMovement;
-                Vec3 desired = (cmd.desiredDirection * cmd.desiredVelocityFloat) - s.movement;
-                if ((desired.Dot(planned) > 0.0f && GetDistance(desired, planned) < 4.0f) || desired.Dot(planned) > 0.8f ||
-                    GetDistance(desired, planned) < 2.0f)
-                    return kSelectFalse;
-            }
-            if (cf == kFnMovement && fn == kFnBallControl &&
-                (m.actualTimeMs - player.base.lastTouchTimeMs < 600 && player.base.lastTouchType == kTouchKicked) && player.hasPossession) {
-                float change = (s.movement - (cmd.desiredDirection * cmd.desiredVelocityFloat)).Length();
-                if (change < 1.0f) return kSelectFalse;
-            }
-        }
-        ApplyOutgoingState(interrupt);
+        const bool justKicked = m.actualTimeMs - player.base.lastTouchTimeMs < 600 && player.base.lastTouchType == kTouchKicked;
+        return runningMovement && fn == kFnBallControl && justKicked && player.hasPossession && (s.movement - asked).Length() < 1.0f;
+    }
+
+    // The crude query of a player's command: the function type (long passes as short ones), the
+    // ball direction it asks for, the incoming velocity (dribble as walk beyond movement; idle out
+    // of a special state) and body direction under the function type's rules, the side the player
+    // looks to, pickup, the incoming ball direction of traps, interference and deflections, last
+    // ditch, trip type, and the special and retain states it comes from.
+    HD CrudeQuery CommandQuery(const PlayerCommand &cmd, int fn, bool retainerIsMe) {
+        const AnimationState &cur = H().anim;
+        const SpatialState &s = S();
         const Anim &current = A(cur.anim);
-        const float angle = s.angle.value();
+        const libm::SinCos back = BackTurn(s.angle.value());
         CrudeQuery q;
         q.byFunctionType = true;
-        q.functionType = fn;
-        if (q.functionType == kFnLongPass) q.functionType = kFnShortPass;
+        q.functionType = fn == kFnLongPass ? kFnShortPass : fn;
         if (cmd.touchInfo.desiredPower != 0.0f) {
             q.byOutgoingBallDirection = true;
-            q.outgoingBallDirection = RotatedBy(cmd.touchInfo.desiredDirection, BackTurn(angle));
+            q.outgoingBallDirection = RotatedBy(cmd.touchInfo.desiredDirection, back);
         }
+        const VelocityRule velocity = FunctionVelocityRule(q.functionType);
         q.byIncomingVelocity = true;
         q.incomingVelocity = s.velocityCat;
         if (q.functionType != kFnMovement && q.incomingVelocity == kVelDribble) q.incomingVelocity = kVelWalk;
-        {
-            const VelocityRule rule = FunctionVelocityRule(q.functionType);
-            q.incomingVelocityStrict = rule.strict;
-            q.incomingVelocityNoDribbleToIdle = rule.noDribbleToIdle;
-            q.incomingVelocityNoDribbleToSprint = rule.noDribbleToSprint;
-            q.incomingVelocityForceLinearity = rule.forceLinearity;
-        }
+        q.incomingVelocityStrict = velocity.strict;
+        q.incomingVelocityNoDribbleToIdle = velocity.noDribbleToIdle;
+        q.incomingVelocityNoDribbleToSprint = velocity.noDribbleToSprint;
+        q.incomingVelocityForceLinearity = velocity.forceLinearity;
+        const BodyRule body = FunctionBodyRule(q.functionType);
         q.byIncomingBodyDirection = true;
         q.incomingBodyDirection = s.relBodyDirectionVec;
-        {
-            const BodyRule rule = FunctionBodyRule(q.functionType);
-            q.incomingBodyDirectionStrict = rule.strict;
-            q.incomingBodyDirectionForceLinearity = rule.forceLinearity;
-        }
-        q.bySide = false;
-        if (cmd.useDesiredLookAt && (current.outgoingSpecialState == kStrEmpty) && !retainerIsMe) {
-            Vec3 look = (cmd.desiredLookAt - s.position).Normalized(s.directionVec);
-            q.lookAtVectorRelative = RotatedBy(look, BackTurn(angle));
+        q.incomingBodyDirectionStrict = body.strict;
+        q.incomingBodyDirectionForceLinearity = body.forceLinearity;
+        if (cmd.useDesiredLookAt && current.outgoingSpecialState == kStrEmpty && !retainerIsMe) {
             q.bySide = true;
+            q.lookAtVectorRelative = RotatedBy((cmd.desiredLookAt - s.position).Normalized(s.directionVec), back);
         }
         if (cmd.onlyDeflectAnimationsThatPickupBall) {
             q.byPickupBall = true;
@@ -1789,9 +1879,17 @@ struct Selector {
         }
         if (fn == kFnTrap || fn == kFnInterfere || fn == kFnDeflect) {
             q.byIncomingBallDirection = true;
-            q.incomingBallDirection = RotatedBy(MentalBallAt(180) - MentalBallAt(120), BackTurn(angle)).Normalized(Vec3(0));
+            q.incomingBallDirection = RotatedBy(MentalBallAt(180) - MentalBallAt(120), back).Normalized(Vec3(0));
         }
         q.allowLastDitch = AllowLastDitch();
+        FinishQuery(q, cmd, fn, retainerIsMe);
+        return q;
+    }
+    // What every query takes from the command and the running animation: trip type, the special
+    // and retain states it comes from, the special variables; idle velocity out of a special state.
+    HD void FinishQuery(CrudeQuery &q, const PlayerCommand &cmd, int fn, bool retainerIsMe) {
+        const AnimationState &cur = H().anim;
+        const Anim &current = A(cur.anim);
         if (fn == kFnTrip) {
             q.byTripType = true;
             q.tripType = cmd.tripType;
@@ -1801,141 +1899,179 @@ struct Selector {
         if (cmd.useSpecialVar1) q.specialVar1 = (float)cmd.specialVar1;
         if (cmd.useSpecialVar2) q.specialVar2 = (float)cmd.specialVar2;
         if (current.outgoingSpecialState != kStrEmpty) q.incomingVelocity = kVelIdle;
-        AList l{c.ws->lists[0], 0};
-        CrudeSelection(c, q, l);
-        if (l.empty()) {
-            if (fn == kFnMovement) l.push_back(GetIdleMovementAnimationID());
-            else return kSelectFalse;
+    }
+
+    // Narrows the candidates to the desired movement and look (the keep-best filters) for
+    // movement, ball control, traps and interference; false when a trap's best candidate leaves
+    // too far from the desired movement. Each filter is one call site, so matches of a wavefront
+    // that select for different function types run it together; per environment they run in
+    // GRF's order (body direction first for ball control only).
+    HD bool NarrowToDesired(AList &l, const PlayerCommand &cmd, int fn, bool allowLastDitch) {
+        const SpatialState &s = S();
+        SetMovementSimilarityPredicate(RotatedBy(cmd.desiredDirection, BackTurn(s.angle.value())), VelocityCat(cmd.desiredVelocityFloat));
+        pred.lookAt = cmd.desiredLookAt;
+        const bool keeps = fn == kFnMovement || fn == kFnBallControl || fn == kFnTrap || fn == kFnInterfere;
+        bool strict = true;
+        float allowed = 0.0f;
+        int velocitySteps = 0;
+        if (fn == kFnBallControl) {
+            strict = !AllowLastDitch();
+            allowed = 0.0f * PI;
+        } else if (fn == kFnTrap) {
+            strict = !(AllowLastDitch(false) || HighOrBouncyBall());
+            allowed = 0.3f * PI;
+            velocitySteps = 2;
+        } else if (fn == kFnInterfere) {
+            strict = cmd.strictMovement == kStrictTrue;
+            allowed = 0.3f * PI;
+            velocitySteps = 1;
         }
-        if (cmd.useDesiredMovement) {
-            Vec3 rel = RotatedBy(cmd.desiredDirection, BackTurn(angle));
-            SetMovementSimilarityPredicate(rel, VelocityCat(cmd.desiredVelocityFloat));
-            pred.lookAt = cmd.desiredLookAt;
-            // The keep-best filters of each function type, as one call site per filter: matches of
-            // a wavefront that select for different function types run each filter together. Per
-            // environment the filters run in GRF's order (body direction first for ball control
-            // only).
-            const bool keeps = fn == kFnMovement || fn == kFnBallControl || fn == kFnTrap || fn == kFnInterfere;
-            bool strict = true;
-            float allowed = 0.0f;
-            int velocitySteps = 0;
-            if (fn == kFnBallControl) {
-                strict = !AllowLastDitch();
-                allowed = 0.0f * PI;
-            } else if (fn == kFnTrap) {
-                strict = !(AllowLastDitch(false) || HighOrBouncyBall());
-                allowed = 0.3f * PI;
-                velocitySteps = 2;
-            } else if (fn == kFnInterfere) {
-                strict = cmd.strictMovement == kStrictTrue;
-                allowed = 0.3f * PI;
-                velocitySteps = 1;
-            }
-            if (fn == kFnBallControl && cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, strict, allowed);
-            if (keeps) KeepBestDirectionAnimations(l, cmd, strict, allowed, velocitySteps, -1);
-            if (keeps && fn != kFnBallControl && cmd.useDesiredLookAt) KeepBestBodyDirectionAnimations(l, cmd, strict, allowed);
-            if (fn == kFnTrap && !HighOrBouncyBall() && q.allowLastDitch == false) {
-                Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
-                const Anim &ba = A(l[0]);
-                Vec3 bestOut = RotatedBy(ba.outgoingMovement, Turn(angle));
-                float cdd = cmd.desiredDirection.Dot(s.directionVec);
-                bool allow = true;
-                float ad = fabsf(RotatedBy(ba.outgoingDirection, Turn(angle)).Angle2D(cmd.desiredDirection));
-                if (ad > 0.375f * PI) allow = false;
-                Vec3 diff = bestOut - dm;
-                if ((diff.Length() > kWalkVelocity + 0.5f && cdd > 0.0f) || (diff.Length() > kSprintVelocity + 0.5f && cdd <= 0.0f))
-                    allow = false;
-                if (!allow) return kSelectFalse;
-            }
-        }
-        // A movement, trip or special needs only the first of the sort chain.
-        const bool firstOnly = fn == kFnMovement || fn == kFnTrip || fn == kFnSpecial;
-        if (!firstOnly) Sort(l, [&](int i) { return D(i).priorityAbsolute; });
-        int idleLevel = 0;
-        if (!m.inPlay) idleLevel = 2;
-        if (m.inSetPiece) idleLevel = 1;
-        else if ((BallPredict(m.ball, 200) - s.position).Length() > 16.0f) idleLevel = 1;
-        pred.idle = (float)idleLevel;
-        if (!firstOnly) Sort(l, [&](int i) { return KeyIdle(A(i), pred); });
-        pred.desiredFoot = s.foot;
-        if (!firstOnly) Sort(l, [&](int i) { return KeyFoot(A(i), pred); });
+        if (fn == kFnBallControl && cmd.useDesiredLookAt) KeepNearestLook(l, cmd, strict, allowed);
+        if (keeps) KeepNearestQuadrant(l, cmd, strict, allowed, velocitySteps, -1);
+        if (keeps && fn != kFnBallControl && cmd.useDesiredLookAt) KeepNearestLook(l, cmd, strict, allowed);
+        if (fn == kFnTrap && !HighOrBouncyBall() && !allowLastDitch) return TrapLeavesTowardDesired(l[0], cmd);
+        return true;
+    }
+    // A trap's best candidate must leave within 0.375 pi of the desired direction and near the
+    // desired movement (within walking speed ahead, sprinting speed behind, plus 0.5 m/s).
+    HD bool TrapLeavesTowardDesired(int best, const PlayerCommand &cmd) {
+        const SpatialState &s = S();
+        const float angle = s.angle.value();
+        const Anim &a = A(best);
+        const Vec3 leaving = RotatedBy(a.outgoingMovement, Turn(angle));
+        const float ahead = cmd.desiredDirection.Dot(s.directionVec);
+        if (fabsf(RotatedBy(a.outgoingDirection, Turn(angle)).Angle2D(cmd.desiredDirection)) > 0.375f * PI) return false;
+        const float gap = (leaving - cmd.desiredDirection * cmd.desiredVelocityFloat).Length();
+        return !((gap > kWalkVelocity + 0.5f && ahead > 0.0f) || (gap > kSprintVelocity + 0.5f && ahead <= 0.0f));
+    }
+    // The idle level a player's candidates are ranked by: 1 at a set piece or with the ball more
+    // than 16 m away in 200 ms, else 2 out of play and 0 in play.
+    HD int IdleLevel() {
+        const MatchState &m = w.match;
+        if (m.inSetPiece) return 1;
+        if ((BallPredict(m.ball, 200) - S().position).Length() > 16.0f) return 1;
+        return m.inPlay ? 0 : 2;
+    }
+    // The sort keys of a candidate of a movement, trip or special, which take only the first of
+    // GRF's chain of stable sorts: base animation (all but movement), trip direction (with one),
+    // incoming velocity, body direction, foot, idle level and priority, most significant first.
+    HD int FirstOfChain(const AList &l, int fn, bool byTrip, int keyCount, bool withPriority) {
+        const bool byBase = fn != kFnMovement;
+        const int qi = l.count > 1 ? IncomingBodyDirectionQuery() : 0;
+        return FirstOfSortChain(l, keyCount + byTrip + byBase, [&](int i, double *k) {
+            int n = 0;
+            if (byBase) k[n++] = A(i).baseAnimation ? 0 : 1;
+            if (byTrip) k[n++] = -D(i).bumpDirection.Dot(pred.relDesiredTripDirection);
+            k[n++] = KeyIncomingVelocity(A(i), pred);
+            k[n++] = IncomingBodyDirectionKey(i, qi);
+            k[n++] = KeyFoot(A(i), pred);
+            k[n++] = KeyIdle(A(i), pred);
+            if (withPriority) k[n++] = D(i).priorityAbsolute;
+        });
+    }
+    // GRF's chain of stable sorts of a touch's candidates, least significant first: priority, idle
+    // level, foot, body direction (all but ball control), incoming velocity, trip direction, base
+    // animation; deflections that retain the ball to the front.
+    HD void OrderTouchCandidates(AList &l, const PlayerCommand &cmd, int fn) {
+        Sort(l, [&](int i) { return D(i).priorityAbsolute; });
+        Sort(l, [&](int i) { return KeyIdle(A(i), pred); });
+        Sort(l, [&](int i) { return KeyFoot(A(i), pred); });
         if (fn != kFnBallControl) {
-            pred.relIncomingBodyDirection = s.relBodyDirectionVec;
-            if (!firstOnly) {
-                const int qi = l.count > 1 ? IncomingBodyDirectionQuery() : 0;
-                Sort(l, [&](int i) { return IncomingBodyDirectionKey(i, qi); });
-            }
-        }
-        pred.incomingVelocity = s.velocityCat;
-        if (!firstOnly) Sort(l, [&](int i) { return KeyIncomingVelocity(A(i), pred); });
-        if (cmd.useDesiredTripDirection) {
-            pred.relDesiredTripDirection = RotatedBy(cmd.desiredTripDirection, BackTurn(angle));
-            if (!firstOnly) Sort(l, [&](int i) { return -D(i).bumpDirection.Dot(pred.relDesiredTripDirection); });
-        }
-        if (fn != kFnMovement && !firstOnly) SortBaseAnimation(l);
-        if (fn == kFnDeflect) Sort(l, [&](int i) { return D(i).outgoingRetainRaw ? 0 : 1; });
-        int sel = -1;
-        PList plan{c.ws->plans[0], 0};
-        int tmpTouchFrame = -1;
-        Vec3 tmpTouchPos, tmpSmuggle;
-        float tmpRot = 0;
-        if (l.empty() && fn == kFnMovement) l.push_back(GetIdleMovementAnimationID());
-        Vec3 dbr = Vec3(0, -1, 0);
-        if (cmd.useDesiredLookAt)
-            dbr = RotatedBy((cmd.desiredLookAt - (s.position + s.movement * 0.1f)).Normalized(Vec3(0, -1, 0)), BackTurn(angle));
-        // The candidate search of the touch function types and the physics plan of the others, as
-        // one call site each, so that matches selecting for different function types run them
-        // together.
-        bool cheat = false, prefer = false, physics = false;
-        if (firstOnly) {
-            const bool byTrip = cmd.useDesiredTripDirection, byBase = fn != kFnMovement;
             const int qi = l.count > 1 ? IncomingBodyDirectionQuery() : 0;
-            sel = FirstOfSortChain(l, 5 + byTrip + byBase, [&](int i, double *k) {
-                int n = 0;
-                if (byBase) k[n++] = A(i).baseAnimation ? 0 : 1;
-                if (byTrip) k[n++] = -D(i).bumpDirection.Dot(pred.relDesiredTripDirection);
-                k[n++] = KeyIncomingVelocity(A(i), pred);
-                k[n++] = IncomingBodyDirectionKey(i, qi);
-                k[n++] = KeyFoot(A(i), pred);
-                k[n++] = KeyIdle(A(i), pred);
-                k[n++] = D(i).priorityAbsolute;
-            });
+            Sort(l, [&](int i) { return IncomingBodyDirectionKey(i, qi); });
+        }
+        Sort(l, [&](int i) { return KeyIncomingVelocity(A(i), pred); });
+        if (cmd.useDesiredTripDirection) Sort(l, [&](int i) { return -D(i).bumpDirection.Dot(pred.relDesiredTripDirection); });
+        if (fn != kFnMovement) SortBaseAnimation(l);
+    }
+    // Whether a requeued selection would only restart what runs: the same function type with the
+    // same outgoing quadrant (a moving animation) or, both idle, preferred outgoing angles within
+    // `idleTolerance`.
+    HD bool RestartsCurrent(int sel, int fn, float idleTolerance, bool bothIdle) {
+        const AnimationState &cur = H().anim;
+        const Anim &current = A(cur.anim), &next = A(sel);
+        const bool currentIdle = VelocityCat(current.outgoingVelocity) == kVelIdle;
+        const bool idleAsWell = !bothIdle || VelocityCat(next.outgoingVelocity) == kVelIdle;
+        return cur.functionType == fn &&
+               ((!currentIdle && current.quadrantID == next.quadrantID) ||
+                ((currentIdle && idleAsWell) && fabsf(PreferredOutgoingAngle(cur.anim) - PreferredOutgoingAngle(sel)) < idleTolerance));
+    }
+
+    // A player's animation for a command (GRF's HumanoidBase::SelectAnimation for players): the
+    // candidates of the command's query, narrowed to the desired movement and ranked; a movement,
+    // trip or special takes the first by the ranking, a touch the first whose plan reaches the
+    // ball (sliding falls back to its first), then the plan is installed. kSelectFalse when none
+    // fits or a requeue keeps what runs.
+    HDN SelectResult SelectPlayerAnimation(const PlayerCommand &cmd, int interrupt, bool preferPassAndShot) {
+        ENG_SCOPE(14);
+        AnimationState &cur = H().anim;
+        const SpatialState &s = S();
+        const int fn = cmd.desiredFunctionType;
+        const bool retainerIsMe = w.match.ballRetainer == hi;
+        if (BallOutOfTouchRange(fn, retainerIsMe)) return kSelectFalse;
+        if (interrupt == kIntReQueue) {
+            if (w.match.designatedPossessionPlayer < 0) return kSelectUnsupported;
+            if (RequeueKeepsCurrent(cmd, fn)) return kSelectFalse;
+        }
+        ApplyOutgoingState(interrupt);
+        const float angle = s.angle.value();
+        const CrudeQuery q = CommandQuery(cmd, fn, retainerIsMe);
+        AList l{c.ws->lists[0], 0};
+        FilterAnimations(c, q, l);
+        if (l.empty()) {
+            if (fn != kFnMovement) return kSelectFalse;
+            l.push_back(IdleMovementAnimation());
+        }
+        if (cmd.useDesiredMovement && !NarrowToDesired(l, cmd, fn, q.allowLastDitch)) return kSelectFalse;
+        // The predicates of the ranking, set in GRF's order: idle level, foot, body direction
+        // (all but ball control), incoming velocity, trip direction.
+        pred.idle = (float)IdleLevel();
+        pred.desiredFoot = s.foot;
+        if (fn != kFnBallControl) pred.relIncomingBodyDirection = s.relBodyDirectionVec;
+        pred.incomingVelocity = s.velocityCat;
+        if (cmd.useDesiredTripDirection) pred.relDesiredTripDirection = RotatedBy(cmd.desiredTripDirection, BackTurn(angle));
+        const bool firstOnly = fn == kFnMovement || fn == kFnTrip || fn == kFnSpecial;
+        if (!firstOnly) OrderTouchCandidates(l, cmd, fn);
+        if (fn == kFnDeflect) Sort(l, [&](int i) { return D(i).outgoingRetainRaw ? 0 : 1; });
+        if (l.empty() && fn == kFnMovement) l.push_back(IdleMovementAnimation());
+        Vec3 lookRel = Vec3(0, -1, 0);
+        if (cmd.useDesiredLookAt)
+            lookRel = RotatedBy((cmd.desiredLookAt - (s.position + s.movement * 0.1f)).Normalized(Vec3(0, -1, 0)), BackTurn(angle));
+        // The touch search and the movement plan, one call site each, so that matches selecting
+        // for different function types run them together.
+        int sel = -1, touchFrame = -1;
+        PList plan{c.ws->plans[0], 0};
+        Vec3 touchPos, smuggle;
+        float rotation = 0;
+        bool search = false, prefer = false, physics = false;
+        if (firstOnly) {
+            sel = FirstOfChain(l, fn, cmd.useDesiredTripDirection, 5, true);
             physics = true;
         } else if (fn == kFnBallControl) {
-            cheat = NeedTouch(l[0], cmd);
+            search = BallControlNeedsTouch(l[0], cmd);
             prefer = preferPassAndShot;
         } else if (fn == kFnTrap || fn == kFnInterfere || fn == kFnDeflect) {
-            cheat = true;
+            search = true;
             prefer = preferPassAndShot;
         } else if (fn == kFnShortPass || fn == kFnLongPass || fn == kFnHighPass || fn == kFnShot || fn == kFnSliding) {
-            cheat = true;
+            search = true;
         }
-        if (cheat)
-            sel = GetBestCheatableAnimationID(l, cmd.useDesiredMovement, cmd.desiredDirection, cmd.desiredVelocityFloat,
-                                              cmd.useDesiredLookAt, dbr, plan, tmpTouchFrame, tmpTouchPos, tmpSmuggle, tmpRot,
-                                              prefer);
+        if (search)
+            sel = FindTouchAnimation(l, cmd.useDesiredMovement, cmd.desiredDirection, cmd.desiredVelocityFloat, lookRel, plan,
+                                     touchFrame, touchPos, smuggle, rotation, prefer);
         if (fn == kFnSliding && sel == -1 && !l.empty()) {
             sel = l[0];
             physics = true;
         }
         if (physics) {
             ENG_SCOPE(48);
-            Vec3 dm = cmd.desiredDirection * cmd.desiredVelocityFloat;
-            CalculatePhysicsVector(sel, cmd.useDesiredMovement, dm, cmd.useDesiredLookAt, dbr, plan, tmpRot);
+            PlanMovement(sel, cmd.useDesiredMovement, cmd.desiredDirection * cmd.desiredVelocityFloat, lookRel, plan, rotation);
         }
-        if (interrupt == kIntReQueue && sel != -1 && cur.positions.count > 1 && plan.count > 1) {
-            const Anim &sa = A(sel);
-            bool curIdle = VelocityCat(current.outgoingVelocity) == kVelIdle;
-            bool selIdle = VelocityCat(sa.outgoingVelocity) == kVelIdle;
-            if (cur.functionType == fn &&
-                ((!curIdle && current.quadrantID == sa.quadrantID) ||
-                 ((curIdle && selIdle) && fabsf(PreferredOutgoingAngle(cur.anim) - PreferredOutgoingAngle(sel)) < 0.06f * PI)))
-                sel = -1;
-        }
+        if (interrupt == kIntReQueue && sel != -1 && cur.positions.count > 1 && plan.count > 1 && RestartsCurrent(sel, fn, 0.06f * PI, true))
+            sel = -1;
         if (sel == -1) return kSelectFalse;
-        const float rotScale = fn == kFnMovement ? 1.0f : 0.5f;
-        InstallAnimation(sel, fn, interrupt, tmpTouchFrame, tmpTouchPos, rotScale, tmpRot, tmpSmuggle, plan, cmd);
-        cur.movementSmuggle = CalculateMovementSmuggle();
+        InstallAnimation(sel, fn, interrupt, touchFrame, touchPos, fn == kFnMovement ? 1.0f : 0.5f, rotation, smuggle, plan, cmd);
+        cur.movementSmuggle = MovementSmuggle();
         cur.movementSmuggleOffset = Vec3(0);
         return kSelectTrue;
     }

@@ -79,7 +79,7 @@ HDN bool PlaceHumanoid(World &w, const Ctx &c, int hi, const Vec3 &pos, const Ve
     StandStill(h.spatial, st);
 
     Selector sel(w, c, hi);
-    const int idle = sel.GetIdleMovementAnimationID();
+    const int idle = sel.IdleMovementAnimation();
     const Anim &ia = c.A(idle);
     AnimationState &a = h.anim;
     if (ia.posCount > a.positions.kCapacity) Unsupported("a state list outgrows its capacity");
@@ -126,7 +126,7 @@ HDN bool HoldBallForThrowIn(World &w, const Ctx &c, int hi) {
     hold.incomingVelocity = hold.outgoingVelocity = kVelIdle;
     hold.incomingRetainState = kStrRightElbow;
     AList found{c.ws->lists[0], 0};
-    CrudeSelection(c, hold, found);
+    FilterAnimations(c, hold, found);
     if (found.empty()) return Fail("no animation retains the ball for the restart");
     Selector sel(w, c, hi);
     sel.SetMovementSimilarityPredicate(Vec3(0, -1, 0), kVelIdle);

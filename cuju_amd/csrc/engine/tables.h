@@ -306,7 +306,7 @@ struct Tables {
     const CrudeRecord *crudeBody;
     const int32_t *crudeBodyOffset;
     const float *cameraWeights;
-    // The crude selection of idle movement in and out (GetIdleMovementAnimationID), which reads
+    // The crude selection of idle movement in and out (IdleMovementAnimation), which reads
     // only the tables: one list for every call.
     const int16_t *idleMovement;
     int32_t idleMovementCount;

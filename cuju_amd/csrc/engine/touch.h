@@ -76,12 +76,12 @@ HDN bool GetBallControlVector(World &w, const Ctx &c, int p, const Vec3 &nextSta
     float cv = ControllerFloatVelocity(w, p);
     Vec3 dm = oc.desiredDirection * (oc.desiredVelocityFloat * ob + cv * (1.0f - ob));
     if (dm.Length() > kWalkSprintSwitch)
-        dm = dm.Normalized(0) * StretchSprintTo(dm.Length(), kSprintVelocity, GetMaximumVelocity(*c.sd, p));
+        dm = dm.Normalized(0) * StretchSprint(dm.Length(), kSprintVelocity, GetMaximumVelocity(*c.sd, p));
     float vel = Clamp(dm.Length(), outMov.Length(), outMov.Length() + maxOverdrive);
     dm = dm.Normalized(Vec3(0, -1, 0).Rotated2D(nextStartAngle)) * vel;
     Vec3 pm = Vec3(0, -1, 0).Rotated2D(nextStartAngle) * vel;
     float dv = dm.Length(), pv = pm.Length();
-    Vec3 relFoot = GetFrontOfFootOffsetRelative(pv, nextBodyAngle - s.angle.value(), BallPredict(b, 0).v[2]);
+    Vec3 relFoot = FootReachOffset(pv, nextBodyAngle - s.angle.value(), BallPredict(b, 0).v[2]);
     float annoyVel = Curve(NormalizedClamp(a.outgoingVelocity, kIdleVelocity, kSprintVelocity), 0.7f);
     float annoy = (1.0f - NormalizedClamp(ClosestOpponentDistance(w, p), 0.5f, 1.5f)) *
                   (1.0f - (Stat(kStatCalmness) * 0.5f + Stat(kStatBalance) * 0.3f)) * annoyVel;

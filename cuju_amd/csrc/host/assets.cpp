@@ -286,11 +286,11 @@ void BuildSelection(AnimationTables &t) {
         s = SelectionRecord{};
         for (int k = 0; k < 6; k++) s.incomingBodyAngles[k] = a.incomingBodyDirection.Angle2D(AllowedBodyDir(k));
         s.bodyTurnAngle = a.incomingBodyDirection.Angle2D(d.crudeOutBodyDirection);
-        s.incomingBodyIndex = ForceIntoAllowedBodyDirectionIndex(a.incomingBodyDirection);
-        s.preferredOutgoingDirection = ForceIntoPreferredDirectionVector(a.outgoingDirection);
+        s.incomingBodyIndex = BodyDirectionIndex(a.incomingBodyDirection);
+        s.preferredOutgoingDirection = SnapToPreferredDirection(a.outgoingDirection);
         s.preferredOutgoingMovement = s.preferredOutgoingDirection * RangeVelocity(a.outgoingVelocity);
-        s.preferredOutgoingAngle = ForceIntoPreferredDirectionAngle(a.outgoingAngle.value());
-        s.lookAngle = ForceIntoAllowedBodyDirectionAngle(a.outgoingBodyAngle.value()) + s.preferredOutgoingAngle;
+        s.preferredOutgoingAngle = SnapToPreferredAngle(a.outgoingAngle.value());
+        s.lookAngle = SnapToBodyAngle(a.outgoingBodyAngle.value()) + s.preferredOutgoingAngle;
         s.smoothedFirst = a.posCount >= 2 ? a.posFirst : -1;
         const Vec3 &bd = d.crudeBallDirectionNormalized;
         s.ballDirectionFinite = std::isfinite(bd.v[0]) && std::isfinite(bd.v[1]) && std::isfinite(bd.v[2]);
@@ -362,7 +362,7 @@ void BuildSelection(AnimationTables &t) {
             t.crudeBodyOffset[slot * kBodyEntries + e] = (int32_t)t.crudeBody.size();
             for (int j = t.crudeVelocityOffset[slot]; j < t.crudeVelocityOffset[slot + 1]; j++) {
                 const CrudeRecord &r = t.crudeVelocity[j];
-                // An idle query velocity turns the body test off (CrudeSelection, byBody).
+                // An idle query velocity turns the body test off (FilterAnimations, byBody).
                 if (v == kVelIdle || IncomingBodyPasses(rule, e, AllowedBodyDir(e), AllowedBodyFixAbsolute(e),
                                                         AllowedBodyIdleAbsolute(e), r))
                     t.crudeBody.push_back(r);
@@ -508,7 +508,7 @@ std::unique_ptr<AnimationTables> LoadAnimationTables(const std::string &path) {
         c.t = &view;
         c.ws = scratch.get();
         AList idle{scratch->lists[1], 0};
-        CrudeSelection(c, IdleMovementQuery(), idle);
+        FilterAnimations(c, IdleMovementQuery(), idle);
         if (idle.count < 1) throw std::invalid_argument("expected animations of idle movement");
         t->idleMovement.assign(idle.e, idle.e + idle.count);
     }

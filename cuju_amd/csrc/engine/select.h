@@ -1377,96 +1377,93 @@ struct Selector {
         return plan.velocity;
     }
 
+    // Whether ball control needs a touch: when the command asks to move (above the idle-dribble
+    // switch), the ball moves faster than 2 m/s, the animation turns more than an eighth turn, or
+    // the humanoid's movement (its own blended with the animation's) and the ball's (as seen 240
+    // to 250 ms ahead) differ by 2 m/s or more, in speed beyond -1.4 to 0.7 m/s, or, for an
+    // animation that leaves moving, in direction.
     HDN bool BallControlNeedsTouch(int ai, const PlayerCommand &cmd) {
         const Anim &a = A(ai);
-        SpatialState &s = S();
-        // GRF: never true, a bool as float is idle, kept as written.
-        if (VelocityCat((float)(a.outgoingVelocity != (float)kVelIdle)) != kVelIdle) return true;
-        if (cmd.desiredVelocityFloat > kIdleDribbleSwitch) return true;
-        if (fabsf(w.match.ball.momentum.Length()) > 2.0f) return true;
-        Vec3 am = RotatedBy(a.outgoingMovement, Turn(s.angle.value())) * 0.3f + s.movement * 0.7f;
-        float av = am.Length();
-        am.Normalize(s.directionVec);
-        am *= s.movement.Length() * 0.8f + av * 0.2f;
-        Vec3 bm = (MentalBallAt(250).Get2D() - MentalBallAt(240).Get2D()) * 100;
+        const SpatialState &s = S();
+        if (cmd.desiredVelocityFloat > kIdleDribbleSwitch || fabsf(w.match.ball.momentum.Length()) > 2.0f) return true;
         if (fabsf(a.outgoingAngle.value()) > 0.125f * PI) return true;
-        float dd = (am - bm).Length();
-        if ((double)dd >= 2.0) return true;
-        float vd = am.Length() - bm.Length();
-        if ((double)vd < -1.4 || (double)vd >= 0.7) return true;
-        if (VelocityCat(a.outgoingVelocity) != kVelIdle) {
-            float ad = am.Normalized(s.directionVec).Dot(bm.Normalized(s.directionVec));
-            if ((double)ad < 0.975) return true;
-        }
-        return false;
+        Vec3 mine = RotatedBy(a.outgoingMovement, Turn(s.angle.value())) * 0.3f + s.movement * 0.7f;
+        const float blendedSpeed = mine.Length();
+        mine.Normalize(s.directionVec);
+        mine *= s.movement.Length() * 0.8f + blendedSpeed * 0.2f;
+        const Vec3 ball = (MentalBallAt(250).Get2D() - MentalBallAt(240).Get2D()) * 100;
+        if ((double)(mine - ball).Length() >= 2.0) return true;
+        const float speedGap = mine.Length() - ball.Length();
+        if ((double)speedGap < -1.4 || (double)speedGap >= 0.7) return true;
+        return VelocityCat(a.outgoingVelocity) != kVelIdle &&
+               (double)mine.Normalized(s.directionVec).Dot(ball.Normalized(s.directionVec)) < 0.975;
     }
 
-    HDN void PredictedPose(Vec3 &predPos, float &predAngle) {
+    // Where, and facing which way, the running animation ends: its last planned position (its
+    // own translation once the plan has run out) plus the smuggles; its outgoing angle plus the
+    // end rotation smuggle.
+    HDN void PredictedPose(Vec3 &position, float &angle) {
         ENG_SCOPE(22);
-        AnimationState &cur = H().anim;
+        const AnimationState &cur = H().anim;
         const Anim &a = A(cur.anim);
-        SpatialState &s = S();
-        if ((uint32_t)cur.positions.count > (uint32_t)cur.frameNum)
-            predPos = s.position + cur.positions[a.frameCount - 1] + cur.actionSmuggle + cur.actionSmuggleSustain + cur.movementSmuggle;
-        else
-            predPos = s.position + a.translation.Get2D().Rotated2D(s.angle.value()) + cur.actionSmuggle + cur.actionSmuggleSustain +
-                      cur.movementSmuggle;
-        predAngle = s.angle.value() + a.outgoingAngle.value() + cur.rotationSmuggleEnd.value();
-        predAngle = ModulateIntoRange(-PI, PI, predAngle);
+        const SpatialState &s = S();
+        const Vec3 travel = (uint32_t)cur.positions.count > (uint32_t)cur.frameNum ? cur.positions[a.frameCount - 1]
+                                                                                   : a.translation.Get2D().Rotated2D(s.angle.value());
+        position = s.position + travel + cur.actionSmuggle + cur.actionSmuggleSustain + cur.movementSmuggle;
+        angle = ModulateIntoRange(-PI, PI, s.angle.value() + a.outgoingAngle.value() + cur.rotationSmuggleEnd.value());
     }
 
     HD int DesiredTimeToBallMs() {
         return TruncToInt32(Clamp((float)P().desiredTimeToBallMs, (float)(int)P().timeToBallMs, 1000000.0f));
     }
 
-    HDN Vec3 MovementSmuggle() {
-        AnimationState &cur = H().anim;
+    // Whether the player steers its running animation toward the ball: the designated player of
+    // the match and of its team, in play, with no set piece, retainer, touch, special state or
+    // trip other than of type one.
+    HD bool SteersTowardBall() {
+        const AnimationState &cur = H().anim;
         const Anim &a = A(cur.anim);
         const MatchState &m = w.match;
-        if (TeamOfPlayer(w, hi).designatedTeamPossessionPlayer != hi || m.designatedPossessionPlayer != hi ||
-            cur.touchFrame != -1 || (cur.functionType == kFnTrip && !D(cur.anim).tripTypeIsOne) ||
-            a.incomingSpecialState != kStrEmpty || a.outgoingSpecialState != kStrEmpty || !m.inPlay || m.inSetPiece ||
-            m.ballRetainer != -1)
-            return Vec3(0);
-        Vec3 toDesired;
-        uint32_t ttb = (uint32_t)(int)P().timeToBallMs;
-        if (DesiredTimeToBallMs() > (int)ttb) ttb = (uint32_t)DesiredTimeToBallMs();
-        uint32_t animMs = (uint32_t)a.frameCount * 10;
-        uint32_t future = animMs + kDefaultTouchOffsetMs > ttb ? animMs + kDefaultTouchOffsetMs : ttb;
-        Vec3 predOut = OutgoingMovementOf(PList{cur.positions.e, cur.positions.count});
-        Vec3 predPos;
-        float predAngle;
-        PredictedPose(predPos, predAngle);
-        Vec3 ballPos = MentalBallAt((int)future);
-        float bh = ballPos.v[2];
-        Vec3 foot = FootReachOffset(predOut.Length(), a.outgoingBodyAngle.value(), bh).Rotated2D(predAngle);
-        Vec3 desiredBall = predPos + foot;
-        if (!P().hasPossession) {
-            Vec3 bs = MentalBallAt(0).Get2D(), be = MentalBallAt((int)future).Get2D();
-            if ((bs - be).Length() < 0.5f) return Vec3(0);
-            float fraction = 0.0f;
-            if (!(bs == be)) {
-                float ld = (be - bs).Length();
-                if (!(ld < 0.000001f))
-                    fraction = ((desiredBall.v[0] - bs.v[0]) * (be.v[0] - bs.v[0]) + (desiredBall.v[1] - bs.v[1]) * (be.v[1] - bs.v[1])) /
-                               (ld * ld);
-            }
-            Vec3 closest = bs + (be - bs) * fraction;
-            toDesired = closest - desiredBall;
+        if (m.designatedPossessionPlayer != hi || TeamOfPlayer(w, hi).designatedTeamPossessionPlayer != hi) return false;
+        if (!m.inPlay || m.inSetPiece || m.ballRetainer != -1 || cur.touchFrame != -1) return false;
+        if (a.incomingSpecialState != kStrEmpty || a.outgoingSpecialState != kStrEmpty) return false;
+        return !(cur.functionType == kFnTrip && !D(cur.anim).tripTypeIsOne);
+    }
+    // The movement smuggle: the shift that brings the foot of the animation's end pose onto the
+    // ball when it arrives (the later of the animation's touch time and the player's time to the
+    // ball), toward the ball's path when the player does not have it; none when the ball arrives
+    // too late (250 ms after the touch, 2 s for an animation that ends idle), barely moves or
+    // would speed the humanoid past the dribble-walk switch. At most 1.6 m/s over the animation,
+    // less 6 cm.
+    HDN Vec3 MovementSmuggle() {
+        if (!SteersTowardBall()) return Vec3(0);
+        AnimationState &cur = H().anim;
+        const Anim &a = A(cur.anim);
+        uint32_t ballDue = (uint32_t)(int)P().timeToBallMs;
+        if (DesiredTimeToBallMs() > (int)ballDue) ballDue = (uint32_t)DesiredTimeToBallMs();
+        const uint32_t animMs = (uint32_t)a.frameCount * 10, touchMs = animMs + kDefaultTouchOffsetMs;
+        const uint32_t arrival = touchMs > ballDue ? touchMs : ballDue;
+        const uint32_t latest = VelocityCat(a.outgoingVelocity) == kVelIdle ? 2000u : 250u + kDefaultTouchOffsetMs;
+        if (arrival - touchMs > latest) return Vec3(0);
+        const Vec3 outgoing = OutgoingMovementOf(PList{cur.positions.e, cur.positions.count});
+        Vec3 endPosition;
+        float endAngle;
+        PredictedPose(endPosition, endAngle);
+        const Vec3 ballThen = MentalBallAt((int)arrival);
+        const Vec3 foot =
+            endPosition + FootReachOffset(outgoing.Length(), a.outgoingBodyAngle.value(), ballThen.v[2]).Rotated2D(endAngle);
+        Vec3 gap;
+        if (P().hasPossession) {
+            gap = ballThen.Get2D() - foot;
         } else {
-            toDesired = ballPos.Get2D() - desiredBall;
+            const Vec3 from = MentalBallAt(0).Get2D(), to = ballThen.Get2D();
+            if ((from - to).Length() < 0.5f) return Vec3(0);
+            gap = (from + (to - from) * LineClosestToPoint(from, to, foot)) - foot;
         }
-        uint32_t maxEffectMs = 250 + kDefaultTouchOffsetMs;
-        if (VelocityCat(a.outgoingVelocity) == kVelIdle) maxEffectMs = 2000;
-        float maxEffectVel = kDribbleWalkSwitch, maxSmugglePerSec = 1.6f;
-        if (future - (animMs + kDefaultTouchOffsetMs) > maxEffectMs) return Vec3(0);
-        Vec3 toDesiredMov = toDesired / (animMs * 0.001f);
-        Vec3 resulting = predOut + toDesiredMov;
-        float pv = predOut.Length(), rv = resulting.Length();
-        if (rv > pv && rv > maxEffectVel) return Vec3(0);
-        NormalizeMaximum(toDesired, maxSmugglePerSec * ((a.frameCount - 1) * 0.01f));
-        toDesired = toDesired.Normalized(0) * MaxF(0.0f, toDesired.Length() - 0.06f);
-        return toDesired;
+        const Vec3 result = outgoing + gap / (animMs * 0.001f);
+        if (result.Length() > outgoing.Length() && result.Length() > kDribbleWalkSwitch) return Vec3(0);
+        NormalizeMaximum(gap, 1.6f * ((a.frameCount - 1) * 0.01f));
+        return gap.Normalized(0) * MaxF(0.0f, gap.Length() - 0.06f);
     }
 
     HD float LastTouchBiasAt(int decayMs, uint64_t t) {

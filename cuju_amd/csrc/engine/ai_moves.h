@@ -762,7 +762,7 @@ struct AIBase {
         t.inputPower = 0;
         t.autoDirectionBias = 1.0f;
         t.autoPowerBias = 1.0f;
-        GetPass(w, p, passType, t.inputDirection, t.inputPower, t.autoDirectionBias, t.autoPowerBias, t.desiredDirection,
+        AimPass(w, p, passType, t.inputDirection, t.inputPower, t.autoDirectionBias, t.autoPowerBias, t.desiredDirection,
                 t.desiredPower, t.targetPlayer, t.forcedTargetPlayer);
         q.push_back(cmd);
     }

@@ -239,7 +239,7 @@ struct AIController : AIBase {
             }
             if (doCommand) {
                 if (t.forcedTargetPlayer < 0) t.forcedTargetPlayer = GetClosestPlayer(w, c, teamID, target, false, p);
-                GetPass(w, p, action.desiredFunctionType, t.inputDirection, t.inputPower, t.autoDirectionBias, t.autoPowerBias,
+                AimPass(w, p, action.desiredFunctionType, t.inputDirection, t.inputPower, t.autoDirectionBias, t.autoPowerBias,
                         t.desiredDirection, t.desiredPower, t.targetPlayer, t.forcedTargetPlayer);
                 q.push_back(action);
             }
@@ -463,7 +463,7 @@ HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
                 ti.inputPower = Clamp(libm::powf(gauge, exponent), 0.01f, 1.0f);
                 ti.autoDirectionBias = autoDir;
                 ti.autoPowerBias = autoPower;
-                GetPass(w, p, type, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias, ti.desiredDirection,
+                AimPass(w, p, type, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias, ti.desiredDirection,
                         ti.desiredPower, ti.targetPlayer, -1);
                 q.push_back(cmd);
             };
@@ -477,7 +477,7 @@ HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
                 ti.inputDirection = ai.Dir();
                 ti.inputPower = 0.1f;
                 ti.forcedTargetPlayer = GetClosestPlayer(w, c, t, ai.Pos() + ai.Dir() * 1.0f, false, p);
-                GetPass(w, p, cmd.desiredFunctionType, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias,
+                AimPass(w, p, cmd.desiredFunctionType, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias,
                         ti.desiredDirection, ti.desiredPower, ti.targetPlayer, ti.forcedTargetPlayer);
                 q.push_back(cmd);
             } else if (hc.actionButton == kBtnShortPass || hc.actionButton == kBtnLongPass || hc.actionButton == kBtnHighPass) {
@@ -497,7 +497,7 @@ HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
                 cmd.touchInfo.inputDirection = ctl.inputDirection;
                 cmd.touchInfo.autoDirectionBias = 1.0f;
                 cmd.touchInfo.desiredDirection =
-                    GetShotDirection(w, p, cmd.touchInfo.inputDirection, cmd.touchInfo.autoDirectionBias);
+                    AimShot(w, p, cmd.touchInfo.inputDirection, cmd.touchInfo.autoDirectionBias);
                 cmd.touchInfo.desiredPower = Clamp(libm::powf(gauge, 0.6f), 0.01f, 1.0f);
                 q.push_back(cmd);
             }

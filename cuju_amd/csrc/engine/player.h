@@ -212,8 +212,8 @@ HDN bool PassTouch(World &w, const Ctx &c, int p, const AnimationState &cur, Vec
     Vec3 tDir = dir;
     float tPower = power;
     int tTarget = -1;
-    GetPass(w, p, cur.originatingCommand.desiredFunctionType, inDir, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias,
-            tDir, tPower, tTarget, ti.forcedTargetPlayer);
+    AimPass(w, p, cur.originatingCommand.desiredFunctionType, inDir, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias, tDir,
+            tPower, tTarget, ti.forcedTargetPlayer);
     const float maxDev = 0.15f * PI;
     float diff = tDir.Get2D().Angle2D(dir.Get2D());
     if (fabsf(diff) <= maxDev) {
@@ -233,13 +233,10 @@ HDN bool PassTouch(World &w, const Ctx &c, int p, const AnimationState &cur, Vec
     }
     if (target >= 0 && !TeamSelectPlayer(w, c, w.playerTeamID[p], target)) return false;
     touch = dir * 36 * (power + 0.3f);
-    touch = GetBestPossibleTouch(w, c, p, touch, cur.functionType);
-    float bodyTouch = h.spatial.bodyDirectionVec.Angle2D(touch) / PI;
-    if (fabsf(bodyTouch) > 0.5f) bodyTouch = (1.0f - fabsf(bodyTouch)) * SignSide(bodyTouch);
-    bodyTouch *= 2.0f;
-    float amount = bodyTouch * 0.25f;
+    touch = AttainableTouch(w, c, p, touch, cur.functionType);
+    float amount = CurlAmount(h.spatial.bodyDirectionVec, touch);
     if (cur.functionType == kFnHighPass) amount *= 0.2f;
-    touch.Rotate2D(amount * (0.4f + 0.6f * NormalizedClamp(touch.Length(), 0.0f, 70.0f)));
+    CurlKick(touch, amount);
     zRot = amount * -340;
     return true;
 }
@@ -265,24 +262,26 @@ HDN bool AnimationTouch(World &w, const Ctx &c, int p, const Anim &a, const Anim
     float rx = 0, ry = 0, rz = 0, bias = 1.0f;
     int touchType = d.touchType;
     if (fn == kFnTrap || (fn == kFnBallControl && !ps.hasPossession)) {
-        if (!GetTrapVector(w, c, p, h.nextStartPos, h.nextStartAngle.value(), nba, outMov, cur, cur.frameNum, h.spatial,
-                           h.decayingPositionOffset, rx, ry, tv))
-            return false;
+        const Kick k = TrapKick(w, c, p, h, nba, outMov);
+        tv = k.momentum;
+        rx = k.xRot;
+        ry = k.yRot;
         if (knockOn) tv *= 1.35f;
         tv = tv * (1.0f - bumpy) + bm * bumpy;
         bias = 0.5f * (1.0f - bumpy);
     } else if (fn == kFnBallControl) {
-        if (!GetBallControlVector(w, c, p, h.nextStartPos, h.nextStartAngle.value(), nba, outMov, cur, cur.frameNum, h.spatial, rx,
-                                  ry, tv))
-            return false;
+        const Kick k = BallControlKick(w, c, p, h, nba, outMov);
+        tv = k.momentum;
+        rx = k.xRot;
+        ry = k.yRot;
         if (knockOn) tv *= 1.35f;
         tv = tv * (1.0f - bumpy) + bm * bumpy;
         bias = 0.6f * (1.0f - bumpy);
     } else if (fn == kFnInterfere) {
-        if (!GetTrapVector(w, c, p, h.nextStartPos, h.nextStartAngle.value(), nba, outMov, cur, cur.frameNum, h.spatial,
-                           h.decayingPositionOffset, rx, ry, tv))
-            return false;
-        tv = tv * 0.5f + (BallPredict(w.match.ball, 0).Get2D() - h.spatial.position).Normalized() * 4.0f +
+        const Kick k = TrapKick(w, c, p, h, nba, outMov);
+        rx = k.xRot;
+        ry = k.yRot;
+        tv = k.momentum * 0.5f + (BallPredict(w.match.ball, 0).Get2D() - h.spatial.position).Normalized() * 4.0f +
              Vec3(0, 0, RandomInRange(w, 0.5f, 1.5f));
         tv = tv * (1.0f - bumpy) + bm * bumpy;
         // GRF passes the bias as the z rotation here, with the default bias of 1.
@@ -305,7 +304,7 @@ HDN bool AnimationTouch(World &w, const Ctx &c, int p, const Anim &a, const Anim
         bias = 0.9f * (1.0f - bumpy);
     } else if (fn == kFnShot) {
         // GRF computes a shot direction here and discards it; the call has no side effects.
-        tv = GetShotVector(w, c, p, cur, h.spatial, h.decayingPositionOffset, rx, ry, rz);
+        tv = ShotKick(w, c, p, cur, h.spatial, h.decayingPositionOffset, rx, ry, rz);
         tv = tv * (1.0f - bumpy) + bm * bumpy;
         bias = 0.7f * (1.0f - bumpy);
     } else if (fn == kFnDeflect) {
@@ -444,11 +443,9 @@ HDN bool HumanoidProcessEnd(World &w, const Ctx &c, int p) {
         Vec3 bm = w.match.ball.momentum;
         float nba = h.startAngle.value() + a.outgoingAngle.value() + a.outgoingBodyAngle.value() + cur.rotationSmuggleEnd.value();
         PList pl{cur.positions.e, cur.positions.count};
-        float xr = 0, yr = 0;
-        Vec3 tv;
-        if (!GetTrapVector(w, c, p, h.nextStartPos, h.nextStartAngle.value(), nba, OutgoingMovementOf(pl), cur, cur.frameNum,
-                           h.spatial, h.decayingPositionOffset, xr, yr, tv))
-            return false;
+        const Kick k = TrapKick(w, c, p, h, nba, OutgoingMovementOf(pl));
+        const float xr = k.xRot, yr = k.yRot;
+        Vec3 tv = k.momentum;
         if (cur.originatingCommand.modifier & kModifierKnockOn) tv *= 1.35f;
         const float bumpy = 0.0f;
         tv = tv * (1.0f - bumpy) + bm * bumpy;

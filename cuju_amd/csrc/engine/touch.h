@@ -1,9 +1,12 @@
 // SPDX-License-Identifier: Apache-2.0
 // Restates game logic of cuju (Copyright 2026 The cuju Authors), a reimplementation of Google
 // Research Football (Copyright 2019 Google LLC); see NOTICE.
-// Touch vectors (the ball momentum a touch gives) and pass/shot aiming.
-// Semantics: include/cuju/simulation/touch.h:15-400 (results depend on the number and order of the
-// RNG draws), include/cuju/simulation/ai_functions.h:27-190.
+// The ball momentum and spin of a touch, by kind (ball control, trap, shot, pass), and the aiming
+// of passes and shots. Semantics: include/cuju/simulation/touch.h:15-400 (results depend on the
+// number and order of the RNG draws), include/cuju/simulation/ai_functions.h:27-190. The float
+// operations and the draws are GRF's; the organisation (a difficulty record, a control intent, a
+// kick toward a planned point, shot power, ease and scatter, pass receivers and biases) is this
+// engine's own.
 #pragma once
 
 #include "control.h"
@@ -11,337 +14,430 @@
 
 namespace eng {
 
+// The velocity the player's controller asks for: the gamer's keyboard, or the AI's last command.
 HD float ControllerFloatVelocity(World &w, int p) {
     if (ExternalControllerActive(w, p)) return HumanGetFloatVelocity(w, p);
     return w.match.players[p].controller.lastDesiredVelocity;
 }
 
-HDN void GetDifficultyFactors(World &w, const Ctx &c, int p, const Vec3 &posOffset, float &distF, float &heightF,
-                              float &ballMovF) {
+// A touch's momentum and spin.
+struct Kick {
+    Vec3 momentum;
+    float xRot = 0, yRot = 0;
+};
+
+// How hard a touch is, from 0 to 1 in three respects: where the ball goes (distance), how high it
+// pops up (height) and how much of its incoming momentum it keeps (ball movement).
+struct TouchDifficulty {
+    float distance = 0, height = 0, ballMovement = 0;
+};
+// Player p's touch difficulty: an off-balance body (position offset up to 10 cm), a velocity gap
+// to the ball (10 to 50 m/s), a ball beyond the foot (0.7 to 1.3 m), an opponent's touch just
+// before (recovered from faster with reaction); scaled by ball control and one draw in 0.5..1.
+HDN TouchDifficulty TouchDifficultyOf(World &w, const Ctx &c, int p, const Vec3 &offset) {
     const Ball &b = w.match.ball;
     const SpatialState &s = Sp(w, p);
-    distF = heightF = ballMovF = 0.0f;
-    float posPenalty = NormalizedClamp(posOffset.Length(), 0.0f, 0.1f) * 2.0f;
-    float velPenalty = libm::powf(NormalizedClamp((s.movement - b.momentum).Length(), 10.0f, 50.0f), 1.5f) * 5.0f;
-    float nd = NormalizedClamp(((s.position + s.directionVec * 0.2f) - BallPredict(b, 0).Get2D()).Length(), 0.7f, 1.3f);
-    float farPenalty = nd * nd * 2.0f;
-    distF += posPenalty * 2.0f;
-    distF += velPenalty;
-    distF += farPenalty * 4.0f;
-    heightF += posPenalty * 0.5f;
-    heightF += velPenalty * 2.0f;
-    heightF += farPenalty;
+    const float offBalance = NormalizedClamp(offset.Length(), 0.0f, 0.1f) * 2.0f;
+    const float speedGap = libm::powf(NormalizedClamp((s.movement - b.momentum).Length(), 10.0f, 50.0f), 1.5f) * 5.0f;
+    const float reachGap = NormalizedClamp(((s.position + s.directionVec * 0.2f) - BallPredict(b, 0).Get2D()).Length(), 0.7f, 1.3f);
+    const float beyondFoot = reachGap * reachGap * 2.0f;
+    TouchDifficulty d;
+    d.distance = offBalance * 2.0f + speedGap + beyondFoot * 4.0f;
+    d.height = offBalance * 0.5f + speedGap * 2.0f + beyondFoot;
     const int teamID = w.playerTeamID[p];
     if (w.match.lastTouchTeamID != teamID) {
-        int lt = TeamByID(w, 1 - teamID).lastTouchPlayer;
-        if (lt >= 0) {
-            int decay = TruncToInt32(1000 - GetStatistic(w, c, p, kStatReaction) * 500);
-            float pen = libm::powf(GetLastTouchBias(w, lt, decay), 0.6f) * 5.0f;
-            distF += pen;
-            heightF += pen;
-            ballMovF += pen * 0.1f;
+        const int opponent = TeamByID(w, 1 - teamID).lastTouchPlayer;
+        if (opponent >= 0) {
+            const int recovery = TruncToInt32(1000 - GetStatistic(w, c, p, kStatReaction) * 500);
+            const float surprise = libm::powf(GetLastTouchBias(w, opponent, recovery), 0.6f) * 5.0f;
+            d.distance += surprise;
+            d.height += surprise;
+            d.ballMovement = surprise * 0.1f;
         }
     }
-    ballMovF = Clamp(ballMovF, 0.0f, 0.9f);
-    float skill = (1.0f - GetStatistic(w, c, p, kStatBallControl) * 0.5f) * RandomInRange(w, 0.5f, 1.0f);
-    distF *= skill;
-    heightF *= skill;
-    ballMovF *= skill;
-    distF = Clamp(distF, 0.0f, 1.0f);
-    heightF = Clamp(heightF, 0.0f, 1.0f);
-    ballMovF = Clamp(ballMovF, 0.0f, 1.0f);
+    d.ballMovement = Clamp(d.ballMovement, 0.0f, 0.9f);
+    const float skill = (1.0f - GetStatistic(w, c, p, kStatBallControl) * 0.5f) * RandomInRange(w, 0.5f, 1.0f);
+    d.distance = Clamp(d.distance * skill, 0.0f, 1.0f);
+    d.height = Clamp(d.height * skill, 0.0f, 1.0f);
+    d.ballMovement = Clamp(d.ballMovement * skill, 0.0f, 1.0f);
+    return d;
 }
 
-HDN bool GetBallControlVector(World &w, const Ctx &c, int p, const Vec3 &nextStartPos, float nextStartAngle,
-                              float nextBodyAngle, const Vec3 &outMov, const AnimationState &cur, int frameNum,
-                              const SpatialState &s, float &xRot, float &yRot, Vec3 &touch, float extraFoot = 0.0f) {
-    const Ball &b = w.match.ball;
-    const Player &ps = w.match.players[p];
+// ---- ball control and traps --------------------------------------------------------------------
+
+// How the humanoid moves through a controlled touch: the physics share (0.7 with the ball, 0.9
+// without, 1 for an animation that ends idle); its speed, the command's blended with the
+// controller's (stretched to the player's top speed above the walk-sprint switch), held between
+// the animation's outgoing speed and up to 0.6 m/s (walking) or 1.2 m/s (sprinting) above it as
+// far as the humanoid faces the command's direction; and two movements at that speed, along the
+// command's direction and straight ahead of the next start angle.
+struct ControlIntent {
+    float physicsBias = 0, speed = 0;
+    Vec3 desired, ahead;
+};
+HD ControlIntent BallControlIntent(World &w, const Ctx &c, int p, const Humanoid &h, const Anim &a, const Vec3 &outMov) {
+    const PlayerCommand &cmd = h.anim.originatingCommand;
+    const SpatialState &s = h.spatial;
+    const bool endsIdle = VelocityCat(a.outgoingVelocity) == kVelIdle;
+    ControlIntent in;
+    in.physicsBias = endsIdle ? 1.0f : w.match.players[p].hasPossession ? 0.7f : 0.9f;
+    const float explosiveness = 0.6f;
+    float overdrive = 1.0f * explosiveness;
+    if (cmd.desiredVelocityFloat < kDribbleWalkSwitch) overdrive = 0.0f;
+    if (cmd.desiredVelocityFloat > kWalkSprintSwitch) overdrive = 2.0f * explosiveness;
+    const Vec3 straight = Vec3(0, -1, 0).Rotated2D(h.nextStartAngle.value());
+    const float facing = s.directionVec.Dot(cmd.desiredDirection) * 0.5f + 0.5f;
+    const float facingNext = straight.Dot(cmd.desiredDirection) * 0.5f + 0.5f;
+    overdrive *= Clamp(MinF(facing, facingNext), 0.0f, 1.0f);
+    if (endsIdle) overdrive = 0.0f;
+    const float own = 0.7f;
+    Vec3 move = cmd.desiredDirection * (cmd.desiredVelocityFloat * own + ControllerFloatVelocity(w, p) * (1.0f - own));
+    if (move.Length() > kWalkSprintSwitch)
+        move = move.Normalized(0) * StretchSprint(move.Length(), kSprintVelocity, GetMaximumVelocity(*c.sd, p));
+    in.speed = Clamp(move.Length(), outMov.Length(), outMov.Length() + overdrive);
+    in.desired = move.Normalized(straight) * in.speed;
+    in.ahead = straight * in.speed;
+    return in;
+}
+
+// Where the foot meets the ball, relative to the body: the reach at the speed ahead, pushed out by
+// `extra` and by up to 3 m of annoyance (an opponent within 1.5 m of a fast animation, less with
+// calm and balance), along the next body direction; shifted toward the reach offset and the body
+// direction for a ball 0.5 to 1 m up.
+HD Vec3 ControlFoot(World &w, const Ctx &c, int p, const Humanoid &h, const Anim &a, float nextBodyAngle, float aheadSpeed,
+                    float extra) {
+    const SpatialState &s = h.spatial;
+    const float ballHeight = BallPredict(w.match.ball, 0).v[2];
+    const Vec3 reach = FootReachOffset(aheadSpeed, nextBodyAngle - s.angle.value(), ballHeight);
+    const float hurry = Curve(NormalizedClamp(a.outgoingVelocity, kIdleVelocity, kSprintVelocity), 0.7f);
+    const float annoy = (1.0f - NormalizedClamp(ClosestOpponentDistance(w, p), 0.5f, 1.5f)) *
+                        (1.0f - (GetStatistic(w, c, p, kStatCalmness) * 0.5f + GetStatistic(w, c, p, kStatBalance) * 0.3f)) * hurry;
+    Vec3 foot = Vec3(0, -1, 0).Rotated2D(nextBodyAngle) * (reach.Length() + extra + annoy * 3.0f);
+    const float lift = NormalizedClamp(ballHeight, 0.5f, 1.0f) * 0.5f;
+    foot += reach * lift * 0.5f + s.bodyDirectionVec * lift * 0.5f;
+    return foot;
+}
+
+// The spin of a controlled touch: about the axis between the foot and the touch's direction, a
+// roll of 2 pi per m/s less up to 30 of backspin.
+HD void SpinAgainstFoot(Kick &k, const Vec3 &foot) {
+    const float backspin = 30.0f;
+    const float speed = k.momentum.Length();
+    const float damping = libm::powf(NormalizedClamp(k.momentum.Length(), 0.0f, 10.0f), 0.7f);
+    const Vec3 axis = (foot.Normalized(0) * 0.6f + k.momentum.Normalized(0) * 0.4f).Normalized(0);
+    k.xRot = axis.v[1] * ((2 * PI * speed) - (backspin * damping));
+    k.yRot = axis.v[0] * ((2 * PI * speed) - (backspin * damping));
+}
+
+// A controlled touch of humanoid p: the ball goes toward a point ahead of the foot where the
+// humanoid will be after a speed-dependent delay (0.25 to 0.85 s) on each of its two movements,
+// blended by the physics share, in the time left in the animation plus that delay and the touch
+// offset. Power is the distance over a dribble-scaled time, to the 0.7; the height grows with it;
+// a fast player touches up to 20% harder, less with ball control.
+HDN Kick BallControlKick(World &w, const Ctx &c, int p, const Humanoid &h, float nextBodyAngle, const Vec3 &outMov,
+                         float extraFoot = 0.0f) {
+    const AnimationState &cur = h.anim;
     const Anim &a = c.A(cur.anim);
-    const PlayerCommand &oc = cur.originatingCommand;
-    auto Stat = [&](int st) { return GetStatistic(w, c, p, st); };
-    float physicsBias = 0.7f;
-    if (!ps.hasPossession) physicsBias = 0.9f;
-    if (VelocityCat(a.outgoingVelocity) == kVelIdle) physicsBias = 1.0f;
-    float explosiveness = 0.6f;
-    float maxOverdrive = 1.0f * explosiveness;
-    if (oc.desiredVelocityFloat < kDribbleWalkSwitch) maxOverdrive = 0.0f;
-    if (oc.desiredVelocityFloat > kWalkSprintSwitch) maxOverdrive = 2.0f * explosiveness;
-    float curDirF = s.directionVec.Dot(oc.desiredDirection) * 0.5f + 0.5f;
-    float nextDirF = Vec3(0, -1, 0).Rotated2D(nextStartAngle).Dot(oc.desiredDirection) * 0.5f + 0.5f;
-    float dotF = Clamp(MinF(curDirF, nextDirF), 0.0f, 1.0f);
-    maxOverdrive *= dotF;
-    if (VelocityCat(a.outgoingVelocity) == kVelIdle) maxOverdrive = 0.0f;
-    float ob = 0.7f;
-    float cv = ControllerFloatVelocity(w, p);
-    Vec3 dm = oc.desiredDirection * (oc.desiredVelocityFloat * ob + cv * (1.0f - ob));
-    if (dm.Length() > kWalkSprintSwitch)
-        dm = dm.Normalized(0) * StretchSprint(dm.Length(), kSprintVelocity, GetMaximumVelocity(*c.sd, p));
-    float vel = Clamp(dm.Length(), outMov.Length(), outMov.Length() + maxOverdrive);
-    dm = dm.Normalized(Vec3(0, -1, 0).Rotated2D(nextStartAngle)) * vel;
-    Vec3 pm = Vec3(0, -1, 0).Rotated2D(nextStartAngle) * vel;
-    float dv = dm.Length(), pv = pm.Length();
-    Vec3 relFoot = FootReachOffset(pv, nextBodyAngle - s.angle.value(), BallPredict(b, 0).v[2]);
-    float annoyVel = Curve(NormalizedClamp(a.outgoingVelocity, kIdleVelocity, kSprintVelocity), 0.7f);
-    float annoy = (1.0f - NormalizedClamp(ClosestOpponentDistance(w, p), 0.5f, 1.5f)) *
-                  (1.0f - (Stat(kStatCalmness) * 0.5f + Stat(kStatBalance) * 0.3f)) * annoyVel;
-    Vec3 foot = Vec3(0, -1, 0).Rotated2D(nextBodyAngle) * (relFoot.Length() + extraFoot + annoy * 3.0f);
-    float hf = NormalizedClamp(BallPredict(b, 0).v[2], 0.5f, 1.0f) * 0.5f;
-    foot += relFoot * hf * 0.5f + s.bodyDirectionVec * hf * 0.5f;
-    Vec3 dPlanned = nextStartPos, pPlanned = nextStartPos;
-    float dvf = NormalizedClamp(dv, 0.0f, kSprintVelocity);
-    float dDelay = dvf * dvf * 0.60f + 0.25f;
-    float pvf = NormalizedClamp(pv, 0.0f, kSprintVelocity);
-    float pDelay = pvf * pvf * 0.60f + 0.25f;
-    dPlanned += dm * dDelay + foot;
-    pPlanned += pm * pDelay + foot;
-    Vec3 planned = pPlanned * physicsBias + dPlanned * (1.0f - physicsBias);
-    Vec3 toPlanned = planned - BallPredict(b, 0).Get2D();
-    float timeToGo = (((a.frameCount - 1) - frameNum) * 10) * 0.001f;
-    timeToGo += pDelay * physicsBias + dDelay * (1.0f - physicsBias);
-    timeToGo += kDefaultTouchOffsetMs * 0.001f;
-    float divisor = timeToGo * (0.38f + 0.02f * Stat(kStatDribble));
+    const ControlIntent in = BallControlIntent(w, c, p, h, a, outMov);
+    const float desiredSpeed = in.desired.Length(), aheadSpeed = in.ahead.Length();
+    const Vec3 foot = ControlFoot(w, c, p, h, a, nextBodyAngle, aheadSpeed, extraFoot);
+    const float desiredFast = NormalizedClamp(desiredSpeed, 0.0f, kSprintVelocity);
+    const float desiredDelay = desiredFast * desiredFast * 0.60f + 0.25f;
+    const float aheadFast = NormalizedClamp(aheadSpeed, 0.0f, kSprintVelocity);
+    const float aheadDelay = aheadFast * aheadFast * 0.60f + 0.25f;
+    Vec3 viaDesired = h.nextStartPos, viaAhead = h.nextStartPos;
+    viaDesired += in.desired * desiredDelay + foot;
+    viaAhead += in.ahead * aheadDelay + foot;
+    const Vec3 point = viaAhead * in.physicsBias + viaDesired * (1.0f - in.physicsBias);
+    const Vec3 toPoint = point - BallPredict(w.match.ball, 0).Get2D();
+    float timeLeft = (((a.frameCount - 1) - cur.frameNum) * 10) * 0.001f;
+    timeLeft += aheadDelay * in.physicsBias + desiredDelay * (1.0f - in.physicsBias);
+    timeLeft += kDefaultTouchOffsetMs * 0.001f;
+    float divisor = timeLeft * (0.38f + 0.02f * GetStatistic(w, c, p, kStatDribble));
     divisor *= 1.1f;
-    float power = libm::powf((toPlanned.Length() / divisor), 0.7f);
-    Vec3 direction = toPlanned.Normalized(Vec3(0, -1, 0).Rotated2D(nextBodyAngle));
-    float height = Clamp(0.1f + 1.5f * libm::powf(power / 10.0f, 1.6f), 0.0f, 1.5f);
-    float pmul = 1.2f - (Stat(kStatBallControl) * 0.03f);
-    float vb = NormalizedClamp(vel, kWalkVelocity, kSprintVelocity - 0.8f);
-    pmul = 1.0f * (1.0f - vb) + pmul * vb;
-    touch = direction * power * pmul + Vec3(0, 0, height);
-    float backspin = 30.0f;
-    float tv = touch.Length();
-    float vf = libm::powf(NormalizedClamp(touch.Length(), 0.0f, 10.0f), 0.7f);
-    Vec3 spin = (foot.Normalized(0) * 0.6f + touch.Normalized(0) * 0.4f).Normalized(0);
-    xRot = spin.v[1] * ((2 * PI * tv) - (backspin * vf));
-    yRot = spin.v[0] * ((2 * PI * tv) - (backspin * vf));
-    return true;
+    const float power = libm::powf((toPoint.Length() / divisor), 0.7f);
+    const Vec3 direction = toPoint.Normalized(Vec3(0, -1, 0).Rotated2D(nextBodyAngle));
+    const float height = Clamp(0.1f + 1.5f * libm::powf(power / 10.0f, 1.6f), 0.0f, 1.5f);
+    const float fast = NormalizedClamp(in.speed, kWalkVelocity, kSprintVelocity - 0.8f);
+    const float harder = 1.0f * (1.0f - fast) + (1.2f - (GetStatistic(w, c, p, kStatBallControl) * 0.03f)) * fast;
+    Kick k;
+    k.momentum = direction * power * harder + Vec3(0, 0, height);
+    SpinAgainstFoot(k, foot);
+    return k;
 }
 
-HDN bool GetTrapVector(World &w, const Ctx &c, int p, const Vec3 &nsp, float nsa, float nba, const Vec3 &outMov,
-                       const AnimationState &cur, int frameNum, const SpatialState &s, const Vec3 &posOffset, float &xRot,
-                       float &yRot, Vec3 &result) {
-    float df, hf, bmf;
-    GetDifficultyFactors(w, c, p, posOffset, df, hf, bmf);
-    Vec3 bc;
-    if (!GetBallControlVector(w, c, p, nsp, nsa, nba, outMov, cur, frameNum, s, xRot, yRot, bc, df)) return false;
-    const Vec3 bm = w.match.ball.momentum;
-    bc.v[2] += bm.v[2] * hf * 1.0f + hf * 4.0f;
-    result = bc * (1.0f - bmf) + bm * bmf;
-    return true;
+// A trap: a controlled touch with the foot pushed out by the touch's distance difficulty, lifted
+// by its height difficulty (more for a falling ball) and keeping part of the ball's momentum.
+HDN Kick TrapKick(World &w, const Ctx &c, int p, const Humanoid &h, float nextBodyAngle, const Vec3 &outMov) {
+    const TouchDifficulty d = TouchDifficultyOf(w, c, p, h.decayingPositionOffset);
+    Kick k = BallControlKick(w, c, p, h, nextBodyAngle, outMov, d.distance);
+    const Vec3 incoming = w.match.ball.momentum;
+    k.momentum.v[2] += incoming.v[2] * d.height * 1.0f + d.height * 4.0f;
+    k.momentum = k.momentum * (1.0f - d.ballMovement) + incoming * d.ballMovement;
+    return k;
 }
 
-HDN Vec3 GetShotVector(World &w, const Ctx &c, int p, const AnimationState &cur, const SpatialState &s, const Vec3 &posOffset,
-                       float &xRot, float &yRot, float &zRot) {
+// ---- shots -----------------------------------------------------------------------------------------
+
+// The humanoid's movement at the touch frame, on the pitch, its direction (the facing when idle)
+// and speed.
+struct ShotTouch {
+    Vec3 movement, direction;
+    float speed = 0;
+};
+HD ShotTouch ShotTouchOf(const Ctx &c, const AnimationState &cur, const SpatialState &s) {
     const Anim &a = c.A(cur.anim);
-    const AnimDerived &d = c.D(cur.anim);
-    const PlayerCommand &oc = cur.originatingCommand;
-    const Vec3 bm = w.match.ball.momentum;
-    auto Stat = [&](int st) { return GetStatistic(w, c, p, st); };
-    Vec3 touchMov = MovementAtFrame(c.t->positions + a.posFirst, a.posCount, cur.frameNum, 0).Rotated2D(s.angle.value());
-    Vec3 touchDir = touchMov.Normalized(s.directionVec);
-    float touchVel = touchMov.Length();
-    if (VelocityCat(touchVel) == kVelIdle) touchDir = s.directionVec;
-    float ideal = 0.2f * PI;
-    float neg = fabsf(touchDir.Angle2D(oc.touchInfo.desiredDirection.Rotated2D(-ideal)));
-    float pos = fabsf(touchDir.Angle2D(oc.touchInfo.desiredDirection.Rotated2D(ideal)));
-    float angle = (pos < neg) ? pos : neg;
-    float dirF = Clamp(angle / PI, 0.0f, 1.0f);
-    dirF = Curve(1.0f - dirF, 0.8f);
-    float pdPower = libm::powf(dirF, 0.8f);
-    float pvPower = libm::powf(NormalizedClamp(touchVel, 0.0f, kSprintVelocity), 0.3f);
-    float poPower = 1.0f - NormalizedClamp(posOffset.Length(), 0.0f, 0.1f);
-    float powerF = 1.0f * (0.7f + pdPower * 0.3f) * (0.7f + pvPower * 0.3f) * (0.4f + poPower * 0.6f);
-    powerF = Clamp(powerF, 0.0f, 1.0f);
-    float adaptedDesired = 45.0f * (0.7f + libm::powf(oc.touchInfo.desiredPower, 0.5f) * 0.3f);
-    float animMaxPower = d.touchMaxPowerFactor;
-    if (animMaxPower == 0.0f) animMaxPower = 1.0f;
-    float power = Clamp(powerF * adaptedDesired, 0.0f, (32.0f + Stat(kStatShotPower) * 13.0f) * (0.2f + animMaxPower * 0.8f));
-    float pmbm = (touchMov - bm).Length();
-    pmbm = NormalizedClamp(pmbm, 0.0f, 10.0f);
-    power *= 1.0f + pmbm * 0.2f;
-    float pdEasy = libm::powf(dirF, 0.8f);
-    float pvEasy = 1.0f - NormalizedClamp(fabsf(touchVel - kDribbleVelocity), 0.0f, 4.0f);
-    float poEasy = 1.0f - NormalizedClamp(posOffset.Length(), 0.0f, 0.1f);
-    float pmbmEasy = 1.0f - pmbm * (0.5f - Stat(kStatVolley) * 0.3f);
-    float powerEasy = 1.0f - NormalizedClamp(power, 30.0f, 100.0f);
-    powerEasy = Curve(powerEasy, 1.0f);
-    float easy = 1.0f * (0.4f + pdEasy * 0.6f) * (0.7f + pvEasy * 0.3f) * (0.3f + poEasy * 0.7f) * (0.6f + pmbmEasy * 0.4f) *
-                 (0.6f + powerEasy * 0.4f);
-    float difficulty = Clamp(1.0f - easy, 0.0f, 1.0f);
-    Vec3 desiredShot = (oc.touchInfo.desiredDirection.Get2D() + Vec3(0, 0, 0.05f)).Normalized() * power;
-    Vec3 worst = oc.touchInfo.desiredDirection.Get2D();
-    float lag = difficulty * 0.8f;
-    worst = (touchDir * lag + worst * (1.0f - lag)).Normalized(0);
-    // GRF: the arguments evaluate right to left, so the components draw z, then y, then x.
-    float rz = RandomInRange(w, -1, 1);
-    float ry = RandomInRange(w, -1, 1);
-    float rx = RandomInRange(w, -1, 1);
+    ShotTouch t;
+    t.movement = MovementAtFrame(c.t->positions + a.posFirst, a.posCount, cur.frameNum, 0).Rotated2D(s.angle.value());
+    t.direction = t.movement.Normalized(s.directionVec);
+    t.speed = t.movement.Length();
+    if (VelocityCat(t.speed) == kVelIdle) t.direction = s.directionVec;
+    return t;
+}
+// How well the touch lines up with the shot: 1 when it runs 0.2 pi off the desired direction on
+// either side, curving down to 0 a half turn from there.
+HD float ShotAlignment(const ShotTouch &t, const Vec3 &desired) {
+    const float ideal = 0.2f * PI;
+    const float left = fabsf(t.direction.Angle2D(desired.Rotated2D(-ideal)));
+    const float right = fabsf(t.direction.Angle2D(desired.Rotated2D(ideal)));
+    const float off = (right < left) ? right : left;
+    return Curve(1.0f - Clamp(off / PI, 0.0f, 1.0f), 0.8f);
+}
+// The shot's strength: the desired power (45 m/s at full, to the 0.5) cut by a misaligned touch, a
+// slow approach and an off-balance body; capped by shot power and the animation's touch power;
+// raised by up to 20% by the gap to the ball's momentum (`ballGap`, 0 to 1 over 10 m/s).
+HD float ShotPower(World &w, const Ctx &c, int p, const ShotTouch &t, float fromLine, float fromBalance, const AnimDerived &d,
+                   float desiredPower, const Vec3 &ballMomentum, float &ballGap) {
+    const float fromSpeed = libm::powf(NormalizedClamp(t.speed, 0.0f, kSprintVelocity), 0.3f);
+    const float share =
+        Clamp(1.0f * (0.7f + fromLine * 0.3f) * (0.7f + fromSpeed * 0.3f) * (0.4f + fromBalance * 0.6f), 0.0f, 1.0f);
+    const float asked = 45.0f * (0.7f + libm::powf(desiredPower, 0.5f) * 0.3f);
+    float animationMax = d.touchMaxPowerFactor;
+    if (animationMax == 0.0f) animationMax = 1.0f;
+    float power = Clamp(share * asked, 0.0f, (32.0f + GetStatistic(w, c, p, kStatShotPower) * 13.0f) * (0.2f + animationMax * 0.8f));
+    ballGap = NormalizedClamp((t.movement - ballMomentum).Length(), 0.0f, 10.0f);
+    power *= 1.0f + ballGap * 0.2f;
+    return power;
+}
+// The shot's difficulty, 1 less its ease: a product of the alignment, a touch near dribble speed,
+// the body's balance, a small gap to the ball's momentum (volleys are easier with the volley
+// statistic) and a moderate power (30 to 100 m/s).
+HD float ShotDifficulty(World &w, const Ctx &c, int p, const ShotTouch &t, float fromLine, float fromBalance, float ballGap,
+                        float power) {
+    const float nearDribble = 1.0f - NormalizedClamp(fabsf(t.speed - kDribbleVelocity), 0.0f, 4.0f);
+    const float steadyBall = 1.0f - ballGap * (0.5f - GetStatistic(w, c, p, kStatVolley) * 0.3f);
+    const float moderate = Curve(1.0f - NormalizedClamp(power, 30.0f, 100.0f), 1.0f);
+    const float ease = 1.0f * (0.4f + fromLine * 0.6f) * (0.7f + nearDribble * 0.3f) * (0.3f + fromBalance * 0.7f) *
+                       (0.6f + steadyBall * 0.4f) * (0.6f + moderate * 0.4f);
+    return Clamp(1.0f - ease, 0.0f, 1.0f);
+}
+// The shot between the desired one (lifted 0.05) and a worst one: the touch's direction mixed in
+// by the difficulty, scattered by three draws (z, y, x: GRF evaluates the arguments right to
+// left), lifted and weakened with the difficulty. One more draw, to the power of 0.7 times the
+// shot statistic, is how far toward the worst the shot goes (`worstShare`).
+HD Vec3 ScatterShot(World &w, const Ctx &c, int p, const ShotTouch &t, const Vec3 &desired, float power, float difficulty,
+                    float &worstShare) {
+    const Vec3 desiredShot = (desired.Get2D() + Vec3(0, 0, 0.05f)).Normalized() * power;
+    const float lag = difficulty * 0.8f;
+    Vec3 worst = (t.direction * lag + desired.Get2D() * (1.0f - lag)).Normalized(0);
+    const float rz = RandomInRange(w, -1, 1);
+    const float ry = RandomInRange(w, -1, 1);
+    const float rx = RandomInRange(w, -1, 1);
     worst = worst + (Vec3(rx, ry, rz) * 0.5f * difficulty);
     worst.Normalize();
-    float worstH = Curve(libm::powf(difficulty, 0.7f), 0.7f) * 0.7f;
-    float worstP = power * (1.0f - libm::powf(difficulty, 0.7f) * 0.5f);
-    Vec3 worstShot = (worst + Vec3(0, 0, worstH)).Normalized() * worstP;
-    float wf = RandomInRange(w, 0.0f, 1.0f);
-    wf = libm::powf(wf, Stat(kStatShot) * 0.7f);
-    Vec3 shot = desiredShot * (1.0f - wf) + worstShot * wf;
-    float rcf = 0.3f + wf * 0.7f;
-    float pcf = 0.7f;
-    xRot = -oc.touchInfo.desiredDirection.v[1] * 20.0f + (RandomInRange(w, -20, 20) * rcf);
-    yRot = -oc.touchInfo.desiredDirection.v[0] * 20.0f + (RandomInRange(w, -20, 20) * rcf);
-    float bta = s.bodyDirectionVec.Angle2D(shot) / PI;
-    if (fabsf(bta) > 0.5f) bta = (1.0f - fabsf(bta)) * SignSide(bta);
-    bta *= 2.0f;
-    float amount = bta * 0.25f;
-    shot.Rotate2D(amount * (0.4f + 0.6f * NormalizedClamp(shot.Length(), 0.0f, 70.0f)));
-    zRot = amount * -420 + (RandomInRange(w, -20, 20) * pcf);
+    const float worstLift = Curve(libm::powf(difficulty, 0.7f), 0.7f) * 0.7f;
+    const float worstPower = power * (1.0f - libm::powf(difficulty, 0.7f) * 0.5f);
+    const Vec3 worstShot = (worst + Vec3(0, 0, worstLift)).Normalized() * worstPower;
+    worstShare = libm::powf(RandomInRange(w, 0.0f, 1.0f), GetStatistic(w, c, p, kStatShot) * 0.7f);
+    return desiredShot * (1.0f - worstShare) + worstShot * worstShare;
+}
+// How far a kick curls away from the body direction: the angle between them in half turns,
+// folded so that a kick behind the body counts from the back, doubled, a quarter of that.
+HD float CurlAmount(const Vec3 &body, const Vec3 &kick) {
+    float across = body.Angle2D(kick) / PI;
+    if (fabsf(across) > 0.5f) across = (1.0f - fabsf(across)) * SignSide(across);
+    across *= 2.0f;
+    return across * 0.25f;
+}
+// Turns a kick by its curl, more for a harder kick (to 70 m/s).
+HD void CurlKick(Vec3 &kick, float amount) { kick.Rotate2D(amount * (0.4f + 0.6f * NormalizedClamp(kick.Length(), 0.0f, 70.0f))); }
+
+// A shot's momentum and spin (x and y against the desired direction, z with the curl), with a
+// draw each, the x and y draws scaled up the nearer the shot comes to the worst one.
+HDN Vec3 ShotKick(World &w, const Ctx &c, int p, const AnimationState &cur, const SpatialState &s, const Vec3 &offset,
+                  float &xRot, float &yRot, float &zRot) {
+    const PlayerCommand &cmd = cur.originatingCommand;
+    const Vec3 desired = cmd.touchInfo.desiredDirection;
+    const ShotTouch t = ShotTouchOf(c, cur, s);
+    const float fromLine = libm::powf(ShotAlignment(t, desired), 0.8f);
+    const float fromBalance = 1.0f - NormalizedClamp(offset.Length(), 0.0f, 0.1f);
+    float ballGap = 0;
+    const float power = ShotPower(w, c, p, t, fromLine, fromBalance, c.D(cur.anim), cmd.touchInfo.desiredPower,
+                                  w.match.ball.momentum, ballGap);
+    const float difficulty = ShotDifficulty(w, c, p, t, fromLine, fromBalance, ballGap, power);
+    float worstShare = 0;
+    Vec3 shot = ScatterShot(w, c, p, t, desired, power, difficulty, worstShare);
+    const float spinScatter = 0.3f + worstShare * 0.7f, curlScatter = 0.7f;
+    xRot = -desired.v[1] * 20.0f + (RandomInRange(w, -20, 20) * spinScatter);
+    yRot = -desired.v[0] * 20.0f + (RandomInRange(w, -20, 20) * spinScatter);
+    const float amount = CurlAmount(s.bodyDirectionVec, shot);
+    CurlKick(shot, amount);
+    zRot = amount * -420 + (RandomInRange(w, -20, 20) * curlScatter);
     return shot;
 }
 
-HDN Vec3 GetBestPossibleTouch(World &w, const Ctx &c, int p, const Vec3 &desired, int fn) {
+// ---- passes ------------------------------------------------------------------------------------
+
+// A desired pass momentum within the animation's power: 30 m/s (42 for high passes) scaled by the
+// animation's touch power and cut by up to a quarter for an off-balance body, plus half the
+// ball's speed; the excess (up to 10 m/s) lifts the ball by a quarter of it.
+HD Vec3 CapTouchPower(Vec3 r, int fn, const AnimDerived &d, const Vec3 &offset, const Vec3 &incoming) {
+    float animation = d.touchMaxPowerFactor;
+    if (animation == 0.0f) animation = 1.0f;
+    animation = animation * 0.7f + 0.3f;
+    float most = (fn == kFnHighPass ? 42.0f : 30.0f) * animation * (1.0f - Clamp(offset.Length() * 2.5f, 0.0f, 0.25f));
+    most += incoming.Length() * 0.5f;
+    if (r.Length() > most) {
+        const float excess = r.Length() - most;
+        r = r.Normalized(0) * most;
+        r.v[2] += Clamp(excess, 0.0f, 10.0f) * 0.25f;
+    }
+    return r;
+}
+// The touch a player manages for a desired pass momentum: within the animation's power, turned
+// toward the animation's own ball direction by the touch's difficulty (without one, by a draw of
+// up to a quarter turn either way), weakened and lifted by it, keeping some of the ball's
+// momentum, and lifted by one more draw scaled by the pass's own difficulty (less with the pass
+// statistics).
+HDN Vec3 AttainableTouch(World &w, const Ctx &c, int p, const Vec3 &desired, int fn) {
     Humanoid &h = Hum(w, p);
     const AnimationState &cur = h.anim;
     const AnimDerived &d = c.D(cur.anim);
-    const Vec3 bm = w.match.ball.momentum;
-    float maxBase = 30.0f;
-    if (fn == kFnHighPass) maxBase = 42.0f;
-    Vec3 r = desired;
-    float mpf = d.touchMaxPowerFactor;
-    if (mpf == 0.0f) mpf = 1.0f;
-    mpf = mpf * 0.7f + 0.3f;
-    float maxPower = maxBase * mpf * (1.0f - Clamp(h.decayingPositionOffset.Length() * 2.5f, 0.0f, 0.25f));
-    maxPower += bm.Length() * 0.5f;
-    if (r.Length() > maxPower) {
-        float missing = r.Length() - maxPower;
-        r = r.Normalized(0) * maxPower;
-        r.v[2] += Clamp(missing, 0.0f, 10.0f) * 0.25f;
-    }
-    float diff = d.touchDifficultyFactor;
-    if (fn == kFnShortPass || fn == kFnLongPass) diff *= (1.0f - GetStatistic(w, c, p, kStatShortPass) * 0.5f);
-    if (fn == kFnHighPass) diff *= (1.0f - GetStatistic(w, c, p, kStatHighPass) * 0.5f);
-    float df, hf, bmf;
-    GetDifficultyFactors(w, c, p, h.decayingPositionOffset, df, hf, bmf);
-    float randomRot = df * 0.15f + hf * 0.15f + bmf * 0.3f + diff * 0.5f;
-    Vec3 abd = d.ballDirection.Rotated2D(h.startAngle.value() + cur.rotationSmuggleOffset.value());
-    if (abd.Length() > 0.01f) {
-        float bias = Clamp(randomRot * 1.5f, 0.0f, 1.0f);
-        Vec3 native = abd.Normalized(r).Get2D() * r.Length() + r * Vec3(0, 0, 1);
+    const Vec3 incoming = w.match.ball.momentum;
+    Vec3 r = CapTouchPower(desired, fn, d, h.decayingPositionOffset, incoming);
+    float passDifficulty = d.touchDifficultyFactor;
+    if (fn == kFnShortPass || fn == kFnLongPass) passDifficulty *= (1.0f - GetStatistic(w, c, p, kStatShortPass) * 0.5f);
+    if (fn == kFnHighPass) passDifficulty *= (1.0f - GetStatistic(w, c, p, kStatHighPass) * 0.5f);
+    const TouchDifficulty td = TouchDifficultyOf(w, c, p, h.decayingPositionOffset);
+    const float wobble = td.distance * 0.15f + td.height * 0.15f + td.ballMovement * 0.3f + passDifficulty * 0.5f;
+    const Vec3 own = d.ballDirection.Rotated2D(h.startAngle.value() + cur.rotationSmuggleOffset.value());
+    if (own.Length() > 0.01f) {
+        const float bias = Clamp(wobble * 1.5f, 0.0f, 1.0f);
+        const Vec3 native = own.Normalized(r).Get2D() * r.Length() + r * Vec3(0, 0, 1);
         r = r * (1.0f - bias) + native * bias;
     } else {
-        float capped = (0.5f < randomRot) ? 0.5f : randomRot;
-        float rot = RandomInRange(w, -0.5f * PI, 0.5f * PI) * capped;
-        r.Rotate2D(rot);
+        r.Rotate2D(RandomInRange(w, -0.5f * PI, 0.5f * PI) * MinF(wobble, 0.5f));
     }
-    r *= 1.0f - df * 0.3f;
-    r.v[2] += df * 1.5f;
-    r.v[2] += bm.v[2] * hf * 0.5f + hf * 1.0f;
-    r = r * (1.0f - bmf) + bm * bmf;
-    r.v[2] += diff * 5.0f * RandomInRange(w, 0.2f, 1.0f);
+    r *= 1.0f - td.distance * 0.3f;
+    r.v[2] += td.distance * 1.5f;
+    r.v[2] += incoming.v[2] * td.height * 0.5f + td.height * 1.0f;
+    r = r * (1.0f - td.ballMovement) + incoming * td.ballMovement;
+    r.v[2] += passDifficulty * 5.0f * RandomInRange(w, 0.2f, 1.0f);
     return r;
 }
 
-// ---- pass and shot aiming ----------------------------------------------------------------------
-HDN void GetAutoPass(int passType, const Vec3 &v, Vec3 &dir, float &power) {
-    float heightOffset = 0.11f, powerFactor = 1.8f, distExp = 1.4f;
-    if (passType == kFnHighPass) {
-        heightOffset = 0.45f - NormalizedClamp(v.Length(), 0.0f, 60.0f) * 0.15f;
-        powerFactor = 1.15f;
-        distExp = 1.4f;
-    }
-    dir = (v.Normalized(0) + Vec3(0, 0, heightOffset)).Normalized(0);
-    power = libm::powf(NormalizedClamp(v.Length(), 0.0f, 60.0f), distExp) * powerFactor;
+// The direction and power of a pass along `v`: lifted 0.11 (a high pass 0.45, less up to 0.15 with
+// distance); power the distance over 60 m to the 1.4, times 1.8 (1.15 for a high pass).
+HDN void PassForVector(int passType, const Vec3 &v, Vec3 &dir, float &power) {
+    const bool high = passType == kFnHighPass;
+    const float lift = high ? 0.45f - NormalizedClamp(v.Length(), 0.0f, 60.0f) * 0.15f : 0.11f;
+    dir = (v.Normalized(0) + Vec3(0, 0, lift)).Normalized(0);
+    power = libm::powf(NormalizedClamp(v.Length(), 0.0f, 60.0f), 1.4f) * (high ? 1.15f : 1.8f);
 }
 
-HDN void GetPass(const World &w, int p, int passType, const Vec3 &inDir, float inPower, float autoDirBias, float autoPowerBias,
-                 Vec3 &outDir, float &outPower, int &target, int forcedTarget = -1) {
+// Where a pass leaves from: the touch position during a touch, else 20 cm ahead along the movement.
+HD Vec3 PassOrigin(const World &w, int p) {
     const SpatialState &s = Sp(w, p);
     const AnimationState &cur = Hum(w, p).anim;
-    const int teamID = w.playerTeamID[p];
-    bool fullAutoDir = false, fullAutoPower = false;
-    if (ExternalControllerActive(w, p)) fullAutoDir = fullAutoPower = true;
-    float adb = autoDirBias, apb = autoPowerBias;
-    Vec3 ppos = s.position + s.movement.Normalized(0) * 0.2f;
-    if (cur.touchFrame != -1) ppos = cur.touchPos.Get2D();
-    Vec3 manual = ppos + inDir * Clamp(inPower * 60.0f, 1.0f, 100.0f);
-    PlayerList players = TeamActivePlayers(w, teamID);
-    if (players.size() < 2) {
-        outDir = s.directionVec;
-        outPower = 1.0f;
-        target = p;
-        fullAutoDir = fullAutoPower = false;
-        adb = apb = 0.0f;
-    }
+    if (cur.touchFrame != -1) return cur.touchPos.Get2D();
+    return s.position + s.movement.Normalized(0) * 0.2f;
+}
+// Where a teammate will be when a pass from `origin` arrives: ahead along its movement by 0.3 s
+// plus 0.05 s per metre (at most 1 s), to the 0.7, times 0.7.
+HD Vec3 LeadPoint(const SpatialState &mate, const Vec3 &origin) {
+    float lead = 0.3f + (mate.position - origin).Length() * 0.05f;
+    lead = libm::powf(Clamp(lead, 0.0f, 1.0f), 0.7f) * 0.7f;
+    return mate.position + mate.movement * lead;
+}
+// The teammate a pass toward `manual` (input direction `inDir`) goes to, and where: the lowest
+// rating of distance from the manual target (over 70 m, to the 0.8, times 0.8) plus angle off the
+// input direction (in half turns); the passer, at the origin, without teammates.
+HD int PassReceiver(const World &w, int p, const PlayerList &players, const Vec3 &origin, const Vec3 &manual, const Vec3 &inDir,
+                    Vec3 &aim) {
     int best = p;
-    Vec3 autoT = manual;
-    if (forcedTarget >= 0) {
-        best = forcedTarget;
-        const SpatialState &fs = Sp(w, forcedTarget);
-        float dur = 0.3f + (fs.position - ppos).Length() * 0.05f;
-        dur = libm::powf(Clamp(dur, 0.0f, 1.0f), 0.7f) * 0.7f;
-        autoT = fs.position + fs.movement * dur;
-    } else {
-        float bestRating = 10000;
-        autoT = ppos;
-        for (int tm : players) {
-            if (tm == p) continue;
-            const SpatialState &ts = Sp(w, tm);
-            float dur = 0.3f + (ts.position - ppos).Length() * 0.05f;
-            dur = libm::powf(Clamp(dur, 0.0f, 1.0f), 0.7f) * 0.7f;
-            Vec3 tp = ts.position + ts.movement * dur;
-            float dr = libm::powf(NormalizedClamp((tp - manual).Length(), 0.0f, 70.0f), 0.8f) * 0.8f;
-            float ar = fabsf((tp - ppos).Normalized(0).Angle2D(inDir) / (1.0f * PI)) * 1.0f;
-            if (dr + ar < bestRating) {
-                bestRating = dr + ar;
-                best = tm;
-                autoT = tp;
-            }
+    float bestRating = 10000;
+    aim = origin;
+    for (int mate : players) {
+        if (mate == p) continue;
+        const Vec3 lead = LeadPoint(Sp(w, mate), origin);
+        const float fromManual = libm::powf(NormalizedClamp((lead - manual).Length(), 0.0f, 70.0f), 0.8f) * 0.8f;
+        const float offInput = fabsf((lead - origin).Normalized(0).Angle2D(inDir) / (1.0f * PI)) * 1.0f;
+        if (fromManual + offInput < bestRating) {
+            bestRating = fromManual + offInput;
+            best = mate;
+            aim = lead;
         }
     }
-    target = best;
-    Vec3 autoRel = autoT - ppos, manualRel = manual - ppos;
-    if (forcedTarget >= 0 || (fullAutoDir && fullAutoPower)) {
-        adb = 1.0;
-        apb = 1.0;
+    return best;
+}
+// A pass's direction, power and receiver. The receiver is the forced one or the best-rated
+// teammate; the pass blends the manual target (the input direction, 60 m per unit of input power,
+// 1 to 100 m) with the receiver's lead point, by direction and by distance, with the auto biases
+// cut as the two targets part (to 50 m) and, for direction, raised toward 1 near the receiver
+// (within 12 m). A forced receiver or a gamer-controlled passer passes fully automatically; a
+// player without teammates fully manually. Long passes aim 20% of their length further upfield.
+HDN void AimPass(const World &w, int p, int passType, const Vec3 &inDir, float inPower, float autoDirBias, float autoPowerBias,
+                 Vec3 &outDir, float &outPower, int &target, int forcedTarget = -1) {
+    const int teamID = w.playerTeamID[p];
+    const Vec3 origin = PassOrigin(w, p);
+    const Vec3 manual = origin + inDir * Clamp(inPower * 60.0f, 1.0f, 100.0f);
+    const PlayerList players = TeamActivePlayers(w, teamID);
+    const bool alone = players.size() < 2;
+    const bool automatic = ExternalControllerActive(w, p) && !alone;
+    float dirBias = alone ? 0.0f : autoDirBias, powerBias = alone ? 0.0f : autoPowerBias;
+    Vec3 aim;
+    if (forcedTarget >= 0) {
+        target = forcedTarget;
+        aim = LeadPoint(Sp(w, forcedTarget), origin);
     } else {
-        float maxDist = 50.0f;
+        target = PassReceiver(w, p, players, origin, manual, inDir, aim);
+    }
+    Vec3 autoRel = aim - origin, manualRel = manual - origin;
+    if (forcedTarget >= 0 || automatic) {
+        dirBias = 1.0f;
+        powerBias = 1.0f;
+    } else {
         // The subtraction from 1 runs in double and rounds once.
-        float distF = (float)(1.0 - (double)libm::powf(Clamp((autoRel - manualRel).Length() / maxDist, 0.0f, 1.0f), 1.5f));
-        float prox = libm::powf(1.0f - NormalizedClamp((ppos - autoT).Length(), 0.0f, 12.0f), 0.5f);
-        if (fullAutoDir) {
-            adb = 1.0f;
-        } else {
-            adb *= distF;
-            adb = libm::powf(adb, 1.0f - prox * 0.9f);
-        }
-        if (fullAutoPower) {
-            apb = 1.0f;
-        } else {
-            apb *= distF;
-            apb = Clamp((float)((double)apb * (1.0 + (double)prox)), 0.0f, 1.0f);
-        }
+        const float agreement = (float)(1.0 - (double)libm::powf(Clamp((autoRel - manualRel).Length() / 50.0f, 0.0f, 1.0f), 1.5f));
+        const float near = libm::powf(1.0f - NormalizedClamp((origin - aim).Length(), 0.0f, 12.0f), 0.5f);
+        dirBias *= agreement;
+        dirBias = libm::powf(dirBias, 1.0f - near * 0.9f);
+        powerBias *= agreement;
+        powerBias = Clamp((float)((double)powerBias * (1.0 + (double)near)), 0.0f, 1.0f);
     }
     if (passType == kFnLongPass) {
-        float td = autoRel.Length() * adb + manualRel.Length() * (1.0f - adb);
-        Vec3 off = Vec3(-TeamDynamicSide(w, teamID) * td * 0.2f, 0, 0);
-        autoRel += off;
-        manualRel += off;
+        const float length = autoRel.Length() * dirBias + manualRel.Length() * (1.0f - dirBias);
+        const Vec3 upfield = Vec3(-TeamDynamicSide(w, teamID) * length * 0.2f, 0, 0);
+        autoRel += upfield;
+        manualRel += upfield;
     }
-    Vec3 res = (autoRel.Normalized(0) * adb + manualRel.Normalized(0) * (1.0f - adb)).Normalized(manual);
-    res *= float(autoRel.Length() * apb + manualRel.Length() * (1.0f - apb));
-    GetAutoPass(passType, res, outDir, outPower);
+    Vec3 pass = (autoRel.Normalized(0) * dirBias + manualRel.Normalized(0) * (1.0f - dirBias)).Normalized(manual);
+    pass *= float(autoRel.Length() * powerBias + manualRel.Length() * (1.0f - powerBias));
+    PassForVector(passType, pass, outDir, outPower);
 }
 
-HDN Vec3 GetShotDirection(const World &w, int p, const Vec3 &inDir, float autoDirBias) {
+// A shot's direction: the input direction blended by the auto bias with a direction at the goal,
+// aimed across its mouth (up to 90% of its half width) as far as the input points away from the
+// goal's centre (a quarter turn reaches the post; the offset to the 0.7).
+HDN Vec3 AimShot(const World &w, int p, const Vec3 &inDir, float autoDirBias) {
     const SpatialState &s = Sp(w, p);
     const int side = TeamDynamicSide(w, w.playerTeamID[p]);
+    const Vec3 from = s.position + s.movement * 0.12f;
     Vec3 goal = Vec3(side * -kPitchHalfLength, 0, 0);
-    Vec3 toGoal = (goal - (s.position + s.movement * 0.12f)).Normalized(0);
-    float rel = toGoal.Angle2D(inDir);
-    float sf = Clamp((rel / PI) / 0.5f, -1.0f, 1.0f);
-    sf = libm::powf(fabsf(sf), 0.7f) * SignSide(sf);
-    goal.v[1] = sf * kGoalHalfWidth * 0.9f * side;
-    Vec3 autoDir = (goal - (s.position + s.movement * 0.12f)).Normalized(0);
-    return (inDir * (1.0f - autoDirBias) + autoDir * autoDirBias).Normalized(inDir);
+    float across = Clamp(((goal - from).Normalized(0).Angle2D(inDir) / PI) / 0.5f, -1.0f, 1.0f);
+    across = libm::powf(fabsf(across), 0.7f) * SignSide(across);
+    goal.v[1] = across * kGoalHalfWidth * 0.9f * side;
+    return (inDir * (1.0f - autoDirBias) + (goal - from).Normalized(0) * autoDirBias).Normalized(inDir);
 }
 
 }  // namespace eng

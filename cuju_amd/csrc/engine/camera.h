@@ -157,6 +157,39 @@ HD void CameraIntro(MatchState &m) {
     m.cameraNearCap = m.cameraNearCap * (1.0f - ease) + 2.0f * ease;
 }
 
+// While the referee shows a card (from a second after play stopped until the restart is prepared)
+// the camera leaves play and frames the referee from 10 m away (zoom 1.5) and 3 m up; after that
+// it follows play again. A change of mode clears the aim history. GRF also holds the restart back
+// while the referee's card animation runs: prepared a second later, started two seconds after
+// that. `mirrored`: the match is in a frame that mirrors the referee's position.
+HD void CameraOnCard(World &w, bool mirrored) {
+    MatchState &m = w.match;
+    Referee &ref = m.referee;
+    const bool card = ref.foul.foulType == 2 || ref.foul.foulType == 3;
+    if (!(ref.buffer.active && card && ref.buffer.stopTime < m.actualTimeMs - 1000)) return;
+    const bool follow = !(ref.buffer.prepareTime > m.actualTimeMs);
+    if (follow != m.autoUpdateInGameCamera) {
+        m.cameraPosition.count = 0;
+        m.autoUpdateInGameCamera = follow;
+    }
+    if (follow) return;
+    Humanoid &referee = m.officials[0].humanoid;
+    Vec3 at = referee.spatial.position;
+    if (mirrored) at.Mirror();
+    const Vec3 target = at + Vec3(0, 0, 0.8f);
+    const float zoom = 1.5f;
+    m.cameraOrientation.SetAngleAxis(0.4f * PI, Vec3(1, 0, 0));
+    m.cameraNodeOrientation.SetAngleAxis((float)((double)target.Angle2D() + 1.5 * (double)PI), Vec3(0, 0, 1));
+    m.cameraNodePosition = target - target.Get2D().Normalized(Vec3(0, -1, 0)) * 10 * (1.0f / zoom) + Vec3(0, 0, 3);
+    m.cameraFov = 60.0f;
+    m.cameraNearCap = 1;
+    m.cameraFarCap = 220;
+    if (referee.anim.functionType == kFnSpecial && ref.buffer.active) {
+        ref.buffer.prepareTime = m.actualTimeMs + 1000;
+        ref.buffer.startTime = ref.buffer.prepareTime + 2000;
+    }
+}
+
 // The camera's tick, on the unmirrored pitch (team 1 read mirrored in place).
 HDN void UpdateCamera(World &w, const Ctx &c) {
     ENG_SCOPE(19);

@@ -61,40 +61,101 @@ HDN void CalculateBestPossessionTeamID(World &w) {
     m.bestPossessionTeam = a < b ? TeamSlot(w, first) : a > b ? TeamSlot(w, 1 - first) : -1;
 }
 
-// Parameter bounds compare in double.
-HDN bool TriangleIntersectsLine(const Vec3 *v, const Vec3 &normal, const Vec3 &start, const Vec3 &end) {
-    Vec3 e1 = v[1] - v[0], e2 = v[2] - v[0];
-    Vec3 dir = end - start;
-    Vec3 so = start - v[0];
-    float num = -normal.Dot(so);
-    float den = normal.Dot(dir);
-    if (fabsf(den) < 0.000001f) return false;
-    float r = num / den;
+// ---- goals ---------------------------------------------------------------------------------------
+// GRF counts a goal when the ball's path over the tick crosses the goal plane (the goal line moved
+// out by the line's half width and the ball's radius) inside the mouth, which it splits into two
+// triangles. The crossing point's parameters along the path and within a triangle compare in
+// double.
+
+// Where the segment from `from` to `to` crosses the plane through `on` with normal `normal`, as a
+// fraction of the segment strictly between 0 and 1; false when it runs parallel or misses.
+HD bool SegmentCrossesPlane(const Vec3 &on, const Vec3 &normal, const Vec3 &from, const Vec3 &to, Vec3 &at) {
+    const Vec3 path = to - from;
+    const float along = normal.Dot(path);
+    if (fabsf(along) < 0.000001f) return false;
+    const float r = -normal.Dot(from - on) / along;
     if ((double)r <= 0.0 || (double)r >= 1.0) return false;
-    Vec3 iv = start + dir * r;
-    float uu = e1.Dot(e1), uv = e1.Dot(e2), vv = e2.Dot(e2);
-    Vec3 wv = iv - v[0];
-    float wu = wv.Dot(e1), wv2 = wv.Dot(e2);
-    float d = uv * uv - uu * vv;
-    float s = (uv * wv2 - vv * wu) / d;
-    if ((double)s < 0.0 || (double)s > 1.0) return false;
-    float t = (uv * wu - uu * wv2) / d;
-    if ((double)t < 0.0 || (double)(s + t) > 1.0) return false;
+    at = from + path * r;
     return true;
 }
-// Whether the ball crossed the goal mouth on `side` this tick.
-HDN bool CheckForGoal(const World &w, int side, const Vec3 &prev) {
+// Whether a point of a triangle's plane lies inside it: its barycentric coordinates along the
+// edges from corner 0, each at least 0 and summing to at most 1.
+HD bool InsideTriangle(const Vec3 (&corner)[3], const Vec3 &point) {
+    const Vec3 e1 = corner[1] - corner[0], e2 = corner[2] - corner[0], rel = point - corner[0];
+    const float uu = e1.Dot(e1), uv = e1.Dot(e2), vv = e2.Dot(e2);
+    const float wu = rel.Dot(e1), wv = rel.Dot(e2);
+    const float d = uv * uv - uu * vv;
+    const float s = (uv * wv - vv * wu) / d;
+    if ((double)s < 0.0 || (double)s > 1.0) return false;
+    const float t = (uv * wu - uu * wv) / d;
+    return !((double)t < 0.0 || (double)(s + t) > 1.0);
+}
+HD bool PathThroughTriangle(const Vec3 (&corner)[3], const Vec3 &normal, const Vec3 &from, const Vec3 &to) {
+    Vec3 at;
+    return SegmentCrossesPlane(corner[0], normal, from, to, at) && InsideTriangle(corner, at);
+}
+// Whether the ball went into the goal at `side` this tick, from `before`: it must end near the
+// goal line, and a ball that started wide of the posts beyond the line does not count.
+HDN bool BallEnteredGoal(const World &w, int side, const Vec3 &before) {
     const Ball &b = w.match.ball;
     if ((double)fabsf(BallPredict(b, 10).v[0]) < (double)kPitchHalfLength - 1.0) return false;
-    const Vec3 end = BallPredict(b, 0);
+    const Vec3 after = BallPredict(b, 0);
     const float x = (kPitchHalfLength + kLineHalfWidth + 0.11f) * side;
     const Vec3 normal(-side, 0, 0);
     const Vec3 lower[3] = {Vec3(x, 3.7f, 0), Vec3(x, -3.7f, 0), Vec3(x, 3.7f, 2.5f)};
     const Vec3 upper[3] = {Vec3(x, -3.7f, 0), Vec3(x, -3.7f, 2.5f), Vec3(x, 3.7f, 2.5f)};
-    bool lo = TriangleIntersectsLine(lower, normal, prev, end);
-    bool hi = TriangleIntersectsLine(upper, normal, prev, end);
-    if ((double)fabsf(prev.v[1]) > 3.7 && (double)fabsf(prev.v[0]) > (double)(kPitchHalfLength - kLineHalfWidth) - 0.11) return false;
-    return lo || hi;
+    const bool crossed = PathThroughTriangle(lower, normal, before, after) || PathThroughTriangle(upper, normal, before, after);
+    if ((double)fabsf(before.v[1]) > 3.7 && (double)fabsf(before.v[0]) > (double)(kPitchHalfLength - kLineHalfWidth) - 0.11)
+        return false;
+    return crossed;
+}
+// A goal for team `scorer`: it changes its tactics, and the scorer is the last toucher of the
+// scoring team, or of the other team for an own goal (one whose last touches of both kinds were
+// not the scoring team's).
+HD void RecordGoal(World &w, int first, int scorer) {
+    MatchState &m = w.match;
+    m.goalCount[scorer == first ? 0 : 1] += 1;
+    m.goalScored = true;
+    m.lastGoalTeam = TeamSlot(w, scorer);
+    TeamUpdateTactics(w, scorer);
+    const int team = m.lastGoalTeam == 0 ? first : 1 - first;
+    const bool own = !(m.lastTouchTeamIDs[kTouchKicked] == team || m.lastTouchTeamIDs[kTouchNonKicked] == team);
+    m.lastGoalScorer = TeamByID(w, own ? 1 - team : team).lastTouchPlayer;
+}
+
+// The designated possession player after the possession choice: the retainer; else, when one team
+// is quicker to the ball, its designated player once it is at least 15% quicker (10 ms added to
+// both times) than the current one; else the designated player of the current one's team.
+HD void HandOverDesignation(World &w, int first) {
+    MatchState &m = w.match;
+    if (m.ballRetainer != -1) {
+        m.designatedPossessionPlayer = m.ballRetainer;
+        return;
+    }
+    if (m.bestPossessionTeam == -1) {
+        m.designatedPossessionPlayer = TeamByID(w, w.playerTeamID[m.designatedPossessionPlayer]).designatedTeamPossessionPlayer;
+        return;
+    }
+    const int candidate = TeamByID(w, m.bestPossessionTeam == 0 ? first : 1 - first).designatedTeamPossessionPlayer;
+    if (candidate == m.designatedPossessionPlayer) return;
+    const uint32_t current = w.roster.timeToBallMs[m.designatedPossessionPlayer], quicker = w.roster.timeToBallMs[candidate];
+    if ((float)(quicker + 10) / (float)(current + 10) < 0.85f) m.designatedPossessionPlayer = candidate;
+}
+
+// The last six seconds of which side holds the ball (each team's fading possession less a half,
+// signed by its side), one entry a tick while a team is best placed.
+HD void RecordPossessionSide(World &w) {
+    MatchState &m = w.match;
+    float side = 0;
+    side += (TeamByID(w, 0).fadingTeamPossessionAmount - 0.5f) * TeamDynamicSide(w, 0);
+    side += (TeamByID(w, 1).fadingTeamPossessionAmount - 0.5f) * TeamDynamicSide(w, 1);
+    auto &history = m.possessionSideHistory;
+    if (history.count < 600) {
+        history.push_back(side);
+        return;
+    }
+    GroupShiftDown<8>(history.e, history.count - 1);
+    history[history.count - 1] = side;
 }
 
 // False when the tick ends early: while play waits for a restart (the clock still advances), or
@@ -164,87 +225,19 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
         // The possession choice reads times and IDs only, so the return to the collision frame
         // waits for it.
         CalculateBestPossessionTeamID(w);
-        if (m.ballRetainer == -1) {
-            if (m.bestPossessionTeam != -1) {
-                const int bt = m.bestPossessionTeam == 0 ? first : second;
-                int cand = TeamByID(w, bt).designatedTeamPossessionPlayer;
-                if (cand != m.designatedPossessionPlayer) {
-                    uint32_t dt = w.roster.timeToBallMs[m.designatedPossessionPlayer];
-                    uint32_t ct = w.roster.timeToBallMs[cand];
-                    if ((float)(ct + 10) / (float)(dt + 10) < 0.85f) m.designatedPossessionPlayer = cand;
-                }
-            } else {
-                m.designatedPossessionPlayer = TeamByID(w, w.playerTeamID[m.designatedPossessionPlayer]).designatedTeamPossessionPlayer;
-            }
-        } else {
-            m.designatedPossessionPlayer = m.ballRetainer;
-        }
+        HandOverDesignation(w, first);
         frame(rev, !rev, rev);
     }
     if (!CheckHumanoidCollisions(w, c)) return ok = false;
     BumpActualTime(w, c, 10);
-    bool g1 = false, g2 = false;
-    if (m.inPlay) {
-        g1 = CheckForGoal(w, TeamDynamicSide(w, first), prevBall);
-        g2 = CheckForGoal(w, TeamDynamicSide(w, second), prevBall);
-    }
-    bool goal = g1 | g2;
-    m.ballIsInGoal |= goal;
+    // A goal counts into the goal of the team whose side it is: the other team scores.
+    const bool intoFirst = m.inPlay && BallEnteredGoal(w, TeamDynamicSide(w, first), prevBall);
+    const bool intoSecond = m.inPlay && BallEnteredGoal(w, TeamDynamicSide(w, second), prevBall);
+    m.ballIsInGoal |= intoFirst || intoSecond;
     MirrorMatch(w, rev, !rev, rev);
-    if (m.inPlay) {
-        if (goal) {
-            // The ball entered one team's goal, so the other team scores.
-            const int scorer = g1 ? second : first;
-            m.goalCount[scorer == first ? 0 : 1] += 1;
-            m.goalScored = true;
-            m.lastGoalTeam = TeamSlot(w, scorer);
-            TeamUpdateTactics(w, scorer);
-            const int gt = m.lastGoalTeam == 0 ? first : second;
-            bool own = !(m.lastTouchTeamIDs[kTouchKicked] == gt || m.lastTouchTeamIDs[kTouchNonKicked] == gt);
-            m.lastGoalScorer = TeamByID(w, own ? 1 - gt : gt).lastTouchPlayer;
-        }
-    }
-    if (m.inPlay && m.bestPossessionTeam != -1) {
-        float sv = 0;
-        sv += (TeamByID(w, 0).fadingTeamPossessionAmount - 0.5f) * TeamDynamicSide(w, 0);
-        sv += (TeamByID(w, 1).fadingTeamPossessionAmount - 0.5f) * TeamDynamicSide(w, 1);
-        auto &h = m.possessionSideHistory;
-        if (h.count == 600) {
-            GroupShiftDown<8>(h.e, h.count - 1);
-            h[h.count - 1] = sv;
-        } else {
-            h.push_back(sv);
-        }
-    }
-    Referee &ref = m.referee;
-    if (ref.buffer.active && (ref.foul.foulType == 2 || ref.foul.foulType == 3) && ref.buffer.stopTime < m.actualTimeMs - 1000) {
-        // The camera frames the referee showing the card.
-        auto setAuto = [&](bool a) {
-            if (a != m.autoUpdateInGameCamera) {
-                m.cameraPosition.count = 0;
-                m.autoUpdateInGameCamera = a;
-            }
-        };
-        if (ref.buffer.prepareTime > m.actualTimeMs) {
-            setAuto(false);
-            Vec3 rp = m.officials[0].humanoid.spatial.position;
-            if (rev) rp.Mirror();
-            const Vec3 target = rp + Vec3(0, 0, 0.8f);
-            const float zoom = 1.5f;
-            m.cameraOrientation.SetAngleAxis(0.4f * PI, Vec3(1, 0, 0));
-            m.cameraNodeOrientation.SetAngleAxis((float)((double)target.Angle2D() + 1.5 * (double)PI), Vec3(0, 0, 1));
-            m.cameraNodePosition = target - target.Get2D().Normalized(Vec3(0, -1, 0)) * 10 * (1.0f / zoom) + Vec3(0, 0, 3);
-            m.cameraFov = 60.0f;
-            m.cameraNearCap = 1;
-            m.cameraFarCap = 220;
-            if (m.officials[0].humanoid.anim.functionType == kFnSpecial && ref.buffer.active) {
-                ref.buffer.prepareTime = m.actualTimeMs + 1000;
-                ref.buffer.startTime = ref.buffer.prepareTime + 2000;
-            }
-        } else {
-            setAuto(true);
-        }
-    }
+    if (m.inPlay && (intoFirst || intoSecond)) RecordGoal(w, first, intoFirst ? second : first);
+    if (m.inPlay && m.bestPossessionTeam != -1) RecordPossessionSide(w);
+    CameraOnCard(w, rev);
     return true;
 }
 

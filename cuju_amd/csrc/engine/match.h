@@ -242,7 +242,7 @@ HDN bool MatchProcess(World &w, const Ctx &c, bool &ok) {
 }
 
 HDN void PlayerPreparePutBuffers(World &w, int p) {
-    CalculateGeometryOffsets(w, p);
+    PoseOffsets(w, p);
     Player &ps = w.match.players[p];
     const Team &t = TeamByID(w, w.playerTeamID[p]);
     const bool ext = ExternalControllerActive(w, p);

@@ -529,7 +529,7 @@ HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
                 } else if (m.players[best].base.externalController < 0 && bestTeam) {
                     target = best;
                 } else {
-                    target = GetBestSwitchTargetPlayer(w, c, teamID);
+                    target = SwitchTargetPlayer(w, c, teamID);
                     if (target >= 0 && m.players[target].base.externalController >= 0) target = -1;
                 }
                 if (target == TeamGoalie(w, c, teamID)) target = -1;

@@ -165,44 +165,51 @@ HD bool DynamicPlayerSelection(const World &w) {
     for (int i = 0; i < s.rightTeamSize; i++) r += s.rightTeam[i].controllable ? 1 : 0;
     return !((l == s.leftAgents || s.leftAgents == 0) && (r == s.rightAgents || s.rightAgents == 0));
 }
-HDN int GetBestSwitchTargetPlayer(const World &w, const Ctx &c, int teamID) {
+// Where a gamer's switch looks for a player: the middle of the designated player and the ball in
+// 100 ms, its width squeezed to 80%; from there 4 m back toward the team's goal (and a fifth of
+// the way to the team's designated player) when defending, 8 m upfield when attacking, blended by
+// how much the team holds the ball.
+HD Vec3 SwitchFocus(const World &w, int teamID) {
     const MatchState &m = w.match;
     const Team &t = TeamByID(w, teamID);
     const int side = TeamDynamicSide(w, teamID);
-    Vec3 action = Sp(w, m.designatedPossessionPlayer).position * 0.5f + BallPredict(m.ball, 100).Get2D() * 0.5f;
-    Vec3 def = (action * Vec3(1.0f, 0.8f, 0.0f)) + Vec3(side * 4.0f, 0.0f, 0.0f);
-    Vec3 off = (action * Vec3(1.0f, 0.8f, 0.0f)) + Vec3(-side * 8.0f, 0.0f, 0.0f);
-    def = def * 0.8f + Sp(w, t.designatedTeamPossessionPlayer).position * 0.2f;
-    float ob = t.fadingTeamPossessionAmount - 0.5f;
-    ob = ob * 0.2f + Clamp(t.teamPossessionAmount - 0.5f, 0.0f, 1.0f) * 0.8f;
-    ob = Clamp((float)((double)(ob - 0.5f) * 2.0 + 0.5), 0.0f, 1.0f);
-    ob = Clamp(libm::powf(ob, 1.5f), 0.0f, 1.0f);
-    Vec3 res = def * (1.0f - ob) + off * ob;
-    PlayerList cand = GetClosestPlayers(w, c, teamID, res, true, 8);
-    PlayerList kept;
-    for (int i = 0; i < cand.count; i++)
-        if (Formation(w, c, cand[i]).role != kRoleGoalkeeper) kept.push_back(cand[i]);
-    if (kept.empty()) return -1;
-    int best = 0;
+    const Vec3 action = Sp(w, m.designatedPossessionPlayer).position * 0.5f + BallPredict(m.ball, 100).Get2D() * 0.5f;
+    const Vec3 squeezed = action * Vec3(1.0f, 0.8f, 0.0f);
+    const Vec3 defending = (squeezed + Vec3(side * 4.0f, 0.0f, 0.0f)) * 0.8f + Sp(w, t.designatedTeamPossessionPlayer).position * 0.2f;
+    const Vec3 attacking = squeezed + Vec3(-side * 8.0f, 0.0f, 0.0f);
+    float attack = t.fadingTeamPossessionAmount - 0.5f;
+    attack = attack * 0.2f + Clamp(t.teamPossessionAmount - 0.5f, 0.0f, 1.0f) * 0.8f;
+    attack = Clamp((float)((double)(attack - 0.5f) * 2.0 + 0.5), 0.0f, 1.0f);
+    attack = Clamp(libm::powf(attack, 1.5f), 0.0f, 1.0f);
+    return defending * (1.0f - attack) + attacking * attack;
+}
+// How far a humanoid will be from `goal` half a second ahead.
+HD float GoalDistanceAhead(const SpatialState &s, const Vec3 &goal) { return (goal - (s.position + s.movement * 0.5f)).Length(); }
+// The player a gamer's switch goes to (-1 for none): of the 8 AI-controlled players nearest the
+// switch focus, goalkeepers aside, the nearest; while an opponent is the designated player, the
+// first of them that will be at most a metre (plus a tenth of the opponent's distance, up to 3 m)
+// further from the team's goal than the opponent.
+HDN int SwitchTargetPlayer(const World &w, const Ctx &c, int teamID) {
+    const int designated = w.match.designatedPossessionPlayer;
+    const PlayerList nearest = GetClosestPlayers(w, c, teamID, SwitchFocus(w, teamID), true, 8);
+    PlayerList field;
+    for (int i = 0; i < nearest.count; i++)
+        if (Formation(w, c, nearest[i]).role != kRoleGoalkeeper) field.push_back(nearest[i]);
+    if (field.empty()) return -1;
+    if (w.playerTeamID[designated] == teamID) return field[0];
+    const Vec3 goal = Vec3(TeamDynamicSide(w, teamID) * kPitchHalfLength, 0.0f, 0.0f);
+    const float opponent = GoalDistanceAhead(Sp(w, designated), goal);
     const float tooLate = 1.0f;
-    const int d = m.designatedPossessionPlayer;
-    if (w.playerTeamID[d] != teamID) {
-        const SpatialState &os = Sp(w, d);
-        Vec3 goal = Vec3(side * kPitchHalfLength, 0.0f, 0.0f);
-        float og = (goal - (os.position + os.movement * 0.5f)).Length();
-        for (int i = 0; i < kept.count; i++) {
-            const SpatialState &ms = Sp(w, kept[i]);
-            float mg = (goal - (ms.position + ms.movement * 0.5f)).Length();
-            if (mg < og + tooLate + Clamp(og * 0.1f, 0.0f, 3.0f)) {
-                best = i;
-                break;
-            }
-        }
-    }
-    return kept[best];
+    for (int i = 0; i < field.count; i++)
+        if (GoalDistanceAhead(Sp(w, field[i]), goal) < opponent + tooLate + Clamp(opponent * 0.1f, 0.0f, 3.0f)) return field[i];
+    return field[0];
 }
 
 // ---- pose offsets ------------------------------------------------------------------------------------
+// A humanoid's pose offsets bend body parts from the animation's pose (a bias toward an
+// orientation per part). In play, off the ball and moving, the legs bend, the upper body turns to
+// the ball and an arm fends off a close opponent alongside. The offsets are GRF's
+// (geometry_offsets.h); the orientations are built the same way.
 HD void SetOffset(Humanoid &h, int bp, float bias, const Quat &q) {
     h.offsets[bp].bias = bias;
     h.offsets[bp].orientation = q;
@@ -212,55 +219,49 @@ HD Quat AngleAxis(float angle, const Vec3 &axis) {
     q.SetAngleAxis(angle, axis);
     return q;
 }
-// Legs bend to the true velocity, the upper body turns to the ball, the arms fend off a close
-// opponent alongside.
-HDN void CalculateGeometryOffsets(World &w, int p) {
-    Humanoid &h = Hum(w, p);
+// The legs bend as far as the humanoid moves slower than its animation (to a tenth of it; above
+// 7 m/s it may run 10% faster), by up to `influence`.
+HD void BendLegs(Humanoid &h, float influence) {
     const SpatialState &s = h.spatial;
-    const Quat identity(0, 0, 0, 1);
-    for (int bp = kBpMiddle; bp <= kBpBody; bp++) SetOffset(h, bp, 0.0, identity);
-    const float legsInfluence = 0.7f, bodyInfluence = 0.5f, armsInfluence = 0.9f;
-    if (!(w.match.inPlay && w.match.ballRetainer != p)) return;
-    if (h.anim.functionType != kFnMovement) return;
-    {
-        float actual = s.actualMovement.Length();
-        float anim = s.animationMovement.Length();
-        float vf = (actual + 0.2f) / (anim + 0.2f);
-        float allowFaster = 0.0f;
-        if (s.actualMovement.Length() > 7.0f) allowFaster = (float)((double)allowFaster + 0.1);
-        vf = Clamp(vf, 0.1f, 1.0f + allowFaster);
-        const float bend = 0.8f;
-        Quat leftHip = AngleAxis(-0.15f * PI * bend, Vec3(1, 0.06, -0.12).Normalized());
-        Quat rightHip = AngleAxis(-0.15f * PI * bend, Vec3(1, -0.06, 0.12).Normalized());
-        Quat knee = AngleAxis(0.3f * PI * bend, Vec3(1, 0, 0));
-        Quat ankle = AngleAxis(-0.1f * PI * bend, Vec3(1, 0, 0));
-        float legBias = (1.0f - vf) * legsInfluence;
-        SetOffset(h, kBpLeftThigh, legBias, leftHip);
-        SetOffset(h, kBpRightThigh, legBias, rightHip);
-        SetOffset(h, kBpLeftKnee, legBias, knee);
-        SetOffset(h, kBpRightKnee, legBias, knee);
-        SetOffset(h, kBpLeftAnkle, legBias, ankle);
-        SetOffset(h, kBpRightAnkle, legBias, ankle);
-    }
-    if (!w.match.players[p].hasPossession) {
-        Vec3 toBall = (MentalBallPrediction(w, MentalImageIndex(w, h.mentalImageTime), 10).Get2D() - s.position)
-                          .Normalized(s.directionVec);
-        float a = toBall.Angle2D(s.relBodyDirectionVecNonQuantized.Rotated2D(s.angle.value()));
-        a = Clamp(fabsf(a) - 0.05f * PI, 0.0f, PI) * SignSide(a);
-        float lb = libm::powf(1.0f - fabsf(a / PI), 0.3f);
-        lb = Clamp(lb * bodyInfluence, 0.0f, 1.0f);
-        float bd = GetDistance(BallPredict(w.match.ball, 100).Get2D(), s.position);
-        const float falloff = 1.6f;
-        if (bd < falloff) lb *= NormalizedClamp(bd, falloff * 0.4f, falloff);
-        float vfr = NormalizedClamp(s.floatVelocity, kIdleVelocity, kSprintVelocity - 0.5f);
-        lb *= 1.0f - vfr * vfr * 0.3f;
-        Quat middle = AngleAxis(a, Vec3(0, 0, 1));
-        middle.Normalize();
-        SetOffset(h, kBpMiddle, lb * 0.3f, middle);
-        Quat head = AngleAxis(a, Vec3(0, 0, 1));
-        head.Normalize();
-        SetOffset(h, kBpNeck, lb * 0.7f, head);
-    }
+    const float actual = s.actualMovement.Length();
+    const float slower = Clamp((actual + 0.2f) / (s.animationMovement.Length() + 0.2f), 0.1f, 1.0f + (actual > 7.0f ? (float)0.1 : 0.0f));
+    const float bend = 0.8f;
+    const float bias = (1.0f - slower) * influence;
+    const Quat knee = AngleAxis(0.3f * PI * bend, Vec3(1, 0, 0)), ankle = AngleAxis(-0.1f * PI * bend, Vec3(1, 0, 0));
+    SetOffset(h, kBpLeftThigh, bias, AngleAxis(-0.15f * PI * bend, Vec3(1, 0.06, -0.12).Normalized()));
+    SetOffset(h, kBpRightThigh, bias, AngleAxis(-0.15f * PI * bend, Vec3(1, -0.06, 0.12).Normalized()));
+    SetOffset(h, kBpLeftKnee, bias, knee);
+    SetOffset(h, kBpRightKnee, bias, knee);
+    SetOffset(h, kBpLeftAnkle, bias, ankle);
+    SetOffset(h, kBpRightAnkle, bias, ankle);
+}
+// The upper body (30%) and the head (70%) turn toward the ball as the humanoid sees it, beyond a
+// 0.05 pi dead zone, by up to `influence`: less the further it has to turn, for a ball within
+// 1.6 m and at speed.
+HD void TurnTowardBall(World &w, Humanoid &h, float influence) {
+    const SpatialState &s = h.spatial;
+    const Vec3 toBall = (MentalBallPrediction(w, MentalImageIndex(w, h.mentalImageTime), 10).Get2D() - s.position).Normalized(s.directionVec);
+    float turn = toBall.Angle2D(s.relBodyDirectionVecNonQuantized.Rotated2D(s.angle.value()));
+    turn = Clamp(fabsf(turn) - 0.05f * PI, 0.0f, PI) * SignSide(turn);
+    float bias = Clamp(libm::powf(1.0f - fabsf(turn / PI), 0.3f) * influence, 0.0f, 1.0f);
+    const float ballDistance = GetDistance(BallPredict(w.match.ball, 100).Get2D(), s.position);
+    const float falloff = 1.6f;
+    if (ballDistance < falloff) bias *= NormalizedClamp(ballDistance, falloff * 0.4f, falloff);
+    const float fast = NormalizedClamp(s.floatVelocity, kIdleVelocity, kSprintVelocity - 0.5f);
+    bias *= 1.0f - fast * fast * 0.3f;
+    Quat middle = AngleAxis(turn, Vec3(0, 0, 1));
+    middle.Normalize();
+    SetOffset(h, kBpMiddle, bias * 0.3f, middle);
+    Quat head = AngleAxis(turn, Vec3(0, 0, 1));
+    head.Normalize();
+    SetOffset(h, kBpNeck, bias * 0.7f, head);
+}
+// The opponent quickest to the ball, within 1.4 m and running the same way, is fended off with the
+// arm on its side: raised and bent out when it is behind (0.6 to 0.85 pi off the body), raised
+// and bent forward when alongside (0.2 to 0.6 pi), held low ahead (within 0.2 rad: GRF's bound is
+// in radians there). Angle bounds compare in double.
+HD void FendOff(World &w, Humanoid &h, int p, float influence) {
+    const SpatialState &s = h.spatial;
     const int o = TeamBestPossessionPlayer(w, 1 - w.playerTeamID[p]);
     if (o < 0) {
         Fatal("a player has no active opponent");
@@ -268,30 +269,36 @@ HDN void CalculateGeometryOffsets(World &w, int p) {
     }
     const SpatialState &os = Sp(w, o);
     if (!((double)(os.position - s.position).Length() < 1.4 && (double)os.directionVec.Dot(s.directionVec) > 0.0)) return;
-    Vec3 base = Vec3(0, -1, 0).Rotated2D(s.angle.value()).Rotated2D(s.relBodyAngle.value());
-    Vec3 ov = os.position - s.position;
-    float a = base.Angle2D(ov.Normalized(base));
-    // The angle bounds compare in double.
-    const double aa = fabsf(a);
-    const double dpi = (double)PI;
-    const bool right = a > 0;
-    const int shoulderPart = right ? kBpRightShoulder : kBpLeftShoulder;
-    const int elbowPart = right ? kBpRightElbow : kBpLeftElbow;
-    const float shoulderAngle = (float)((right ? 0.4 : -0.4) * dpi);
-    if (aa > 0.6 * dpi && aa < 0.85 * dpi) {
-        SetOffset(h, shoulderPart, 0.8f * armsInfluence, AngleAxis(shoulderAngle, Vec3(0, 1, 0)).Normalized());
-        SetOffset(h, elbowPart, 0.7f * armsInfluence, AngleAxis(0, Vec3(0, 1, 0)).Normalized());
-        SetOffset(h, kBpMiddle, 0.3f * armsInfluence, AngleAxis(0.2f * PI, Vec3(1, 0, 0)).Normalized());
+    const Vec3 body = Vec3(0, -1, 0).Rotated2D(s.angle.value()).Rotated2D(s.relBodyAngle.value());
+    const float toOpponent = body.Angle2D((os.position - s.position).Normalized(body));
+    const double off = fabsf(toOpponent), dpi = (double)PI;
+    const bool right = toOpponent > 0;
+    const int shoulder = right ? kBpRightShoulder : kBpLeftShoulder, elbow = right ? kBpRightElbow : kBpLeftElbow;
+    const float raise = (float)((right ? 0.4 : -0.4) * dpi);
+    if (off > 0.6 * dpi && off < 0.85 * dpi) {
+        SetOffset(h, shoulder, 0.8f * influence, AngleAxis(raise, Vec3(0, 1, 0)).Normalized());
+        SetOffset(h, elbow, 0.7f * influence, AngleAxis(0, Vec3(0, 1, 0)).Normalized());
+        SetOffset(h, kBpMiddle, 0.3f * influence, AngleAxis(0.2f * PI, Vec3(1, 0, 0)).Normalized());
     }
-    if (aa > 0.2 * dpi && aa <= 0.6 * dpi) {
-        SetOffset(h, shoulderPart, 0.7f * armsInfluence, AngleAxis(shoulderAngle, Vec3(0, 1, 0)).Normalized());
-        SetOffset(h, elbowPart, 0.8f * armsInfluence, AngleAxis((float)(-0.5 * dpi), Vec3(1, 0, 0)).Normalized());
+    if (off > 0.2 * dpi && off <= 0.6 * dpi) {
+        SetOffset(h, shoulder, 0.7f * influence, AngleAxis(raise, Vec3(0, 1, 0)).Normalized());
+        SetOffset(h, elbow, 0.8f * influence, AngleAxis((float)(-0.5 * dpi), Vec3(1, 0, 0)).Normalized());
     }
-    // GRF: this bound is 0.2 radians, not 0.2 pi.
-    if (aa < 0.2) {
-        SetOffset(h, shoulderPart, 0.6f * armsInfluence, AngleAxis((float)(-0.4 * dpi), Vec3(1, 0, 0)).Normalized());
-        SetOffset(h, elbowPart, 0.8f * armsInfluence, AngleAxis((float)(-0.2 * dpi), Vec3(1, 0, 0)).Normalized());
+    if (off < 0.2) {
+        SetOffset(h, shoulder, 0.6f * influence, AngleAxis((float)(-0.4 * dpi), Vec3(1, 0, 0)).Normalized());
+        SetOffset(h, elbow, 0.8f * influence, AngleAxis((float)(-0.2 * dpi), Vec3(1, 0, 0)).Normalized());
     }
+}
+// Player p's pose offsets for the tick: cleared, then, in play without holding the ball and
+// moving, the legs, the upper body (off the ball) and the arms.
+HDN void PoseOffsets(World &w, int p) {
+    Humanoid &h = Hum(w, p);
+    const Quat identity(0, 0, 0, 1);
+    for (int bp = kBpMiddle; bp <= kBpBody; bp++) SetOffset(h, bp, 0.0, identity);
+    if (!(w.match.inPlay && w.match.ballRetainer != p) || h.anim.functionType != kFnMovement) return;
+    BendLegs(h, 0.7f);
+    if (!w.match.players[p].hasPossession) TurnTowardBall(w, h, 0.5f);
+    FendOff(w, h, p, 0.9f);
 }
 
 }  // namespace eng

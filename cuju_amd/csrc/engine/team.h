@@ -74,16 +74,12 @@ HDN void TeamApplyAttackingRun(World &w, const Ctx &c, int teamID, int manualPla
     ai.attackingRunPlayer = manualPlayer >= 0 ? manualPlayer : SelectAttackingRunPlayer(w, c, teamID);
 }
 
-HDN bool TeamAIProcess(World &w, const Ctx &c, int teamID) {
-    ENG_SCOPE(10);
-    MatchState &m = w.match;
-    Team &team = TeamByID(w, teamID);
-    const Team &opp = TeamByID(w, 1 - teamID);
-    TeamAI &ai = team.ai;
-    const int side = TeamDynamicSide(w, teamID);
-    auto pos = [&](int p) { return Sp(w, p).position; };
-    auto mov = [&](int p) { return Sp(w, p).movement; };
-    if (m.actualTimeMs % 1000 == 0) TeamUpdateTactics(w, teamID);
+// What the team AI copies of the match each tick: who has the ball, the possession amounts and
+// both teams' times to the ball.
+HD void RefreshTeamView(World &w, int teamID) {
+    const MatchState &m = w.match;
+    const Team &team = TeamByID(w, teamID), &opp = TeamByID(w, 1 - teamID);
+    TeamAI &ai = TeamByID(w, teamID).ai;
     ai.teamHasPossession = team.hasPossession;
     ai.teamHasUniquePossession = TeamHasUniquePossession(w, teamID);
     ai.oppTeamHasPossession = opp.hasPossession;
@@ -93,73 +89,101 @@ HDN bool TeamAIProcess(World &w, const Ctx &c, int teamID) {
     ai.fadingTeamPossessionAmount = team.fadingTeamPossessionAmount;
     ai.timeNeededToGetToBall = team.timeToBallMs;
     ai.oppTimeNeededToGetToBall = opp.timeToBallMs;
-    // The offside trap line: the deepest of the danger, the ball, the opponent on the ball and
-    // the slackened offside line.
-    const float ob = ai.offensivenessBias;
-    float startDistance = 30.0f + 20.0f * ob;
-    const float forceDistance = 6.0f;
+}
+// The x of the team's offside trap: the deepest (toward the team's own goal) of a line 30 to 50 m
+// out from goal (nearer the more offensive the team), the ball pushed 20 to 30 m back when far
+// out, the ball in 700 ms, the opponents' designated player 4 m goalside (tested 0.15 s ahead,
+// placed 0.1 s ahead) and the offside line less 4 m of slack. False without an opponent
+// designated player.
+HD bool OffsideTrapLine(World &w, int teamID, float &x) {
+    const MatchState &m = w.match;
+    const TeamAI &ai = TeamByID(w, teamID).ai;
+    const int side = TeamDynamicSide(w, teamID);
+    const float offensive = ai.offensivenessBias;
+    const float startDistance = 30.0f + 20.0f * offensive, forceDistance = 6.0f;
     float deepest = (kPitchHalfLength - startDistance) * side;
-    float bx = BallPredict(m.ball, 0).v[0];
-    bx *= side;
-    float offsetX = 20.0f + 10.0f * (1.0f - ob);
-    float stf = NormalizedClamp(bx, kPitchHalfLength - startDistance - offsetX, kPitchHalfLength - forceDistance);
-    bx += offsetX * (1.0f - stf);
-    bx *= side;
-    if (bx * side > deepest * side) deepest = bx;
+    const float push = 20.0f + 10.0f * (1.0f - offensive);
+    float ball = BallPredict(m.ball, 0).v[0] * side;
+    ball += push * (1.0f - NormalizedClamp(ball, kPitchHalfLength - startDistance - push, kPitchHalfLength - forceDistance));
+    ball *= side;
+    if (ball * side > deepest * side) deepest = ball;
     if (BallPredict(m.ball, 700).v[0] * side > deepest * side) deepest = BallPredict(m.ball, 700).v[0];
-    const int opp_p = opp.designatedTeamPossessionPlayer;
-    if (opp_p < 0) return Fail("the team AI finds no opponent possession player");
-    float caution = 4.0f * side;
-    // GRF: the comparison predicts 0.15 s ahead, the stored danger 0.1 s.
-    if ((pos(opp_p).v[0] + mov(opp_p).v[0] * 0.15f + caution) * side > deepest * side)
-        deepest = pos(opp_p).v[0] + mov(opp_p).v[0] * 0.1f + caution;
-    float lineX = GetOffsideLine(w, MentalImageIndex(w, 0), teamID);
+    const int carrier = TeamByID(w, 1 - teamID).designatedTeamPossessionPlayer;
+    if (carrier < 0) return false;
+    const SpatialState &cs = Sp(w, carrier);
+    const float caution = 4.0f * side;
+    if ((cs.position.v[0] + cs.movement.v[0] * 0.15f + caution) * side > deepest * side)
+        deepest = cs.position.v[0] + cs.movement.v[0] * 0.1f + caution;
+    const float offside = GetOffsideLine(w, MentalImageIndex(w, 0), teamID);
     const float slack = 4.0f;
-    if (lineX * side - slack > deepest * side) deepest = lineX - slack * side;
-    ai.offsideTrapX = deepest;
-    // Opponents ranked by danger, a stable insertion sort (GRF's std::sort below 17 elements).
-    PlayerList opps = TeamActivePlayers(w, 1 - teamID);
-    Vec3 dangerous = Vec3((float)(((double)kPitchHalfLength - 2.0) * side), 0, 0);
-    dangerous = dangerous * 0.8f + BallPredict(m.ball, 100).Get2D() * 0.2f;
-    Small<TacticalOpponent, kTeamPlayers> info;
-    for (int i = 0; i < opps.count; i++) {
-        TacticalOpponent e;
-        e.player = opps[i];
-        e.dangerFactor = (1.0f - NormalizedClamp((pos(opps[i]) - dangerous).Length(), 0, kPitchHalfLength * 2));
-        e.dangerFactor *= 0.95f;
-        if (opps[i] == opp.designatedTeamPossessionPlayer) e.dangerFactor += 0.05f;
-        info.push_back(e);
-    }
-    for (int n = 1; n < info.count; n++) {
-        TacticalOpponent mv = info[n];
-        int s = n;
-        while (s > 0 && mv.dangerFactor > info[s - 1].dangerFactor) {
-            info[s] = info[s - 1];
-            s--;
-        }
-        info[s] = mv;
-    }
+    if (offside * side - slack > deepest * side) deepest = offside - slack * side;
+    x = deepest;
+    return true;
+}
+// The opponents by danger, most dangerous first (ties in state order, GRF's insertion sort below
+// 17 elements): nearness to a point 2 m out from the team's goal line, a fifth of the way to the
+// ball in 100 ms, scaled to 95%, and 5% more for their designated player.
+HD void RankOpponentsByDanger(World &w, int teamID) {
+    const MatchState &m = w.match;
+    const Team &opp = TeamByID(w, 1 - teamID);
+    TeamAI &ai = TeamByID(w, teamID).ai;
+    const int side = TeamDynamicSide(w, teamID);
+    const PlayerList opponents = TeamActivePlayers(w, 1 - teamID);
+    Vec3 danger = Vec3((float)(((double)kPitchHalfLength - 2.0) * side), 0, 0);
+    danger = danger * 0.8f + BallPredict(m.ball, 100).Get2D() * 0.2f;
     ai.tacticalOpponents.count = 0;
-    for (int i = 0; i < info.count; i++) ai.tacticalOpponents.push_back(info[i]);
-    if (m.actualTimeMs % 500 == 0 && ai.endApplyAttackingRunMs <= m.actualTimeMs && HumanGamerCount(team) < 2 &&
-        m.bestPossessionTeam == TeamSlot(w, teamID)) {
-        int runner = SelectAttackingRunPlayer(w, c, teamID);
-        if (runner >= 0) {
-            float d = (pos(runner) - pos(team.designatedTeamPossessionPlayer)).Length();
-            float dr = libm::powf(1.0f - NormalizedClamp(d, 0, 40), 0.5f);
-            Vec3 spot = pos(runner) * Vec3(1.0f, 0.8f, 0.0f) + Vec3(side * 10.0f, 0, 0);
-            PlayerList near = GetClosestPlayers(w, c, 1 - teamID, spot, false, 4);
-            float density = 1.0f;
-            for (int i = 0; i < near.count; i++) {
-                float od = (pos(near[i]) - spot).Length();
-                density -= libm::powf(Curve(1.0f - NormalizedClamp(od, 0, 15), 1.0f), 0.5f) * 0.3f;
-            }
-            if (dr * density >= 0.5f) TeamApplyAttackingRun(w, c, teamID, -1);
-        }
+    for (int i = 0; i < opponents.count; i++) {
+        TacticalOpponent e;
+        e.player = opponents[i];
+        e.dangerFactor = (1.0f - NormalizedClamp((Sp(w, opponents[i]).position - danger).Length(), 0, kPitchHalfLength * 2));
+        e.dangerFactor *= 0.95f;
+        if (opponents[i] == opp.designatedTeamPossessionPlayer) e.dangerFactor += 0.05f;
+        int at = ai.tacticalOpponents.count;
+        ai.tacticalOpponents.push_back(e);
+        for (; at > 0 && e.dangerFactor > ai.tacticalOpponents[at - 1].dangerFactor; at--)
+            ai.tacticalOpponents[at] = ai.tacticalOpponents[at - 1];
+        ai.tacticalOpponents[at] = e;
     }
+}
+// Every half second, with the team best placed for the ball, at most one gamer and no run on, an
+// attacking run starts when the runner is near the designated player (within 40 m, to the 0.5)
+// and finds space 10 m ahead of it (the 4 nearest opponents within 15 m crowd it).
+HD void ConsiderAttackingRun(World &w, const Ctx &c, int teamID) {
+    const MatchState &m = w.match;
+    const Team &team = TeamByID(w, teamID);
+    if (!(m.actualTimeMs % 500 == 0 && team.ai.endApplyAttackingRunMs <= m.actualTimeMs && HumanGamerCount(team) < 2 &&
+          m.bestPossessionTeam == TeamSlot(w, teamID)))
+        return;
+    const int runner = SelectAttackingRunPlayer(w, c, teamID);
+    if (runner < 0) return;
+    const Vec3 at = Sp(w, runner).position;
+    const float near = libm::powf(1.0f - NormalizedClamp((at - Sp(w, team.designatedTeamPossessionPlayer).position).Length(), 0, 40), 0.5f);
+    const Vec3 spot = at * Vec3(1.0f, 0.8f, 0.0f) + Vec3(TeamDynamicSide(w, teamID) * 10.0f, 0, 0);
+    const PlayerList crowd = GetClosestPlayers(w, c, 1 - teamID, spot, false, 4);
+    float space = 1.0f;
+    for (int i = 0; i < crowd.count; i++)
+        space -= libm::powf(Curve(1.0f - NormalizedClamp((Sp(w, crowd[i]).position - spot).Length(), 0, 15), 1.0f), 0.5f) * 0.3f;
+    if (near * space >= 0.5f) TeamApplyAttackingRun(w, c, teamID, -1);
+}
+
+// The team AI's tick: tactics each second, the view of the match, the offside trap, the danger
+// ranking, attacking runs and, every 1.5 s, the forward support player (the nearest to a point
+// 1.5 m upfield of the designated player).
+HDN bool TeamAIProcess(World &w, const Ctx &c, int teamID) {
+    ENG_SCOPE(10);
+    const MatchState &m = w.match;
+    TeamAI &ai = TeamByID(w, teamID).ai;
+    if (m.actualTimeMs % 1000 == 0) TeamUpdateTactics(w, teamID);
+    RefreshTeamView(w, teamID);
+    float trap = 0;
+    if (!OffsideTrapLine(w, teamID, trap)) return Fail("the team AI finds no opponent possession player");
+    ai.offsideTrapX = trap;
+    RankOpponentsByDanger(w, teamID);
+    ConsiderAttackingRun(w, c, teamID);
     if (m.actualTimeMs % 1500 == 0) {
-        const int d = team.designatedTeamPossessionPlayer;
-        ai.forwardSupportPlayer = GetClosestPlayer(w, c, teamID, pos(d) * Vec3(1.0f, 1.0f, 0.0f) + Vec3(-side * 1.5f, 0, 0), false, d);
+        const int d = TeamByID(w, teamID).designatedTeamPossessionPlayer;
+        const Vec3 ahead = Sp(w, d).position * Vec3(1.0f, 1.0f, 0.0f) + Vec3(-TeamDynamicSide(w, teamID) * 1.5f, 0, 0);
+        ai.forwardSupportPlayer = GetClosestPlayer(w, c, teamID, ahead, false, d);
     }
     return true;
 }
@@ -368,34 +392,35 @@ HDN bool TeamCalculateDynamicRoles(World &w, const Ctx &c, int teamID) {
     return true;
 }
 
-// How well `p` stands between `o` and the own goal: a line across the goal direction in front of
-// `p`, with the opponent's side, distance from it and position along it.
-HDN float TeamCalculateMarkingQuality(const World &w, int teamID, int p, int o) {
+// How well player `p` marks opponent `o` (both 0.1 s ahead): the marker stands on a line across
+// its way to the team's goal (half a metre behind it, 4 to 14 m each way); the opponent should be
+// on the far side of that line, 2 m from it, and across from its middle. The quality loses up to
+// half for distance from the line (to 60 m, to the 0.5) and half for distance from the middle
+// (to the 0.5); an opponent on the near side counts 60%; a fifth is nearness (to the pitch's
+// length).
+HDN float MarkingQuality(const World &w, int teamID, int p, int o) {
     const int side = TeamDynamicSide(w, teamID);
-    const SpatialState &s = Sp(w, p), &os = Sp(w, o);
-    Vec3 op = os.position + os.movement * 0.1f;
-    Vec3 pp = s.position + s.movement * 0.1f;
-    Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
-    Vec3 toGoal = goal - pp;
-    float ll = Clamp((toGoal).Length(), 4.0f, 14.0f);
-    Vec3 tgd = toGoal.Normalized(Vec3(side, 0, 0));
-    Vec3 safety = -tgd * 0.5f;
-    Line line(pp + safety + tgd.Rotated2D((float)(-0.5 * (double)PI)) * ll, pp + safety + tgd.Rotated2D((float)(0.5 * (double)PI)) * ll);
-    bool rightSide = ((line.pts[1].v[0] - line.pts[0].v[0]) * (op.v[1] - line.pts[0].v[1]) -
-                      (line.pts[1].v[1] - line.pts[0].v[1]) * (op.v[0] - line.pts[0].v[0])) > 0;
-    float f = 0.0f;
-    float fromLine = line.DistanceToPoint(op, f);
-    float adapted = fromLine;
-    if (rightSide) adapted = fabsf(fromLine - 2.0f);
-    float fromFactor = libm::powf(NormalizedClamp(adapted, 0.0f, 60.0f), 0.5f);
-    float onFactor = libm::powf(Clamp(fabsf(f * 2.0f - 1.0f), 0.0f, 1.0f), 0.5f);
-    float r = 1.0f;
-    r -= fromFactor * 0.5f;
-    r -= onFactor * 0.5f;
-    r = Clamp(r, 0.0f, 1.0f);
-    if (!rightSide) r *= 0.6f;
-    float od = (1.0f - NormalizedClamp((pp - op).Length(), 0.0f, kPitchHalfLength * 2.0f));
-    return r * 0.8f + od * 0.2f;
+    const SpatialState &ms = Sp(w, p), &os = Sp(w, o);
+    const Vec3 opponent = os.position + os.movement * 0.1f, marker = ms.position + ms.movement * 0.1f;
+    const Vec3 toGoal = Vec3(kPitchHalfLength * side, 0, 0) - marker;
+    const float reach = Clamp((toGoal).Length(), 4.0f, 14.0f);
+    const Vec3 home = toGoal.Normalized(Vec3(side, 0, 0));
+    const Vec3 behind = -home * 0.5f;
+    const Line across(marker + behind + home.Rotated2D((float)(-0.5 * (double)PI)) * reach,
+                      marker + behind + home.Rotated2D((float)(0.5 * (double)PI)) * reach);
+    const Vec3 &a = across.pts[0], &b = across.pts[1];
+    const bool farSide = ((b.v[0] - a.v[0]) * (opponent.v[1] - a.v[1]) - (b.v[1] - a.v[1]) * (opponent.v[0] - a.v[0])) > 0;
+    float along = 0.0f;
+    const float fromLine = across.DistanceToPoint(opponent, along);
+    const float offLine = libm::powf(NormalizedClamp(farSide ? fabsf(fromLine - 2.0f) : fromLine, 0.0f, 60.0f), 0.5f);
+    const float offMiddle = libm::powf(Clamp(fabsf(along * 2.0f - 1.0f), 0.0f, 1.0f), 0.5f);
+    float quality = 1.0f;
+    quality -= offLine * 0.5f;
+    quality -= offMiddle * 0.5f;
+    quality = Clamp(quality, 0.0f, 1.0f);
+    if (!farSide) quality *= 0.6f;
+    const float nearness = (1.0f - NormalizedClamp((marker - opponent).Length(), 0.0f, kPitchHalfLength * 2.0f));
+    return quality * 0.8f + nearness * 0.2f;
 }
 // The three most dangerous opponents get the best-placed outfield marker each, in danger order.
 HDN bool TeamCalculateManMarking(World &w, const Ctx &c, int teamID) {
@@ -411,7 +436,7 @@ HDN bool TeamCalculateManMarking(World &w, const Ctx &c, int teamID) {
         const int o = ai.tacticalOpponents[rank].player;
         for (int i = 0; i < ps.count; i++) {
             if (Formation(w, c, ps[i]).role == kRoleGoalkeeper) continue;
-            float qv = TeamCalculateMarkingQuality(w, teamID, ps[i], o);
+            float qv = MarkingQuality(w, teamID, ps[i], o);
             if (qv > bestQ) {
                 best = ps[i];
                 bestQ = qv;
@@ -464,20 +489,94 @@ HDN bool PlayerProcessEnd(World &w, const Ctx &c, int p, const Vec3 &before) {
     return true;
 }
 
-HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
-    ENG_SCOPE(25);
-    MatchState &m = w.match;
+// The team's possession amount: the opponents' time to the ball over its own (1.5 s added to
+// each), and a fading amount that follows it (clamped to 0.5..1.5) at most 0.005 a tick. Out of
+// play, at a set piece or with a retainer both are 1.5 for the team with (or best placed for) the
+// ball and 0.5 for the other.
+HD void UpdatePossessionAmounts(World &w, int teamID) {
+    const MatchState &m = w.match;
     Team &t = TeamByID(w, teamID);
     const Team &opp = TeamByID(w, 1 - teamID);
     t.teamPossessionAmount = (float)(opp.timeToBallMs + 1500) / (float)(t.timeToBallMs + 1500);
-    float fading = t.fadingTeamPossessionAmount * 0.995f + Clamp(t.teamPossessionAmount, 0.5f, 1.5f) * 0.005f;
+    const float fading = t.fadingTeamPossessionAmount * 0.995f + Clamp(t.teamPossessionAmount, 0.5f, 1.5f) * 0.005f;
     t.fadingTeamPossessionAmount += Clamp(fading - t.fadingTeamPossessionAmount, -0.005f, 0.005f);
-    if (!m.inPlay || m.inSetPiece || m.ballRetainer != -1) {
-        float amount;
-        if (m.ballRetainer != -1) amount = (w.playerTeamID[m.ballRetainer] == teamID) ? 1.5f : 0.5f;
-        else amount = (m.bestPossessionTeam == TeamSlot(w, teamID)) ? 1.5f : 0.5f;
-        t.fadingTeamPossessionAmount = t.teamPossessionAmount = amount;
+    if (m.inPlay && !m.inSetPiece && m.ballRetainer == -1) return;
+    const bool ours = m.ballRetainer != -1 ? w.playerTeamID[m.ballRetainer] == teamID : m.bestPossessionTeam == TeamSlot(w, teamID);
+    t.fadingTeamPossessionAmount = t.teamPossessionAmount = ours ? 1.5f : 0.5f;
+}
+
+// In play, a gamer's held switch button (GRF reads a held switch as a fresh press every tick)
+// moves it off a player that does not alone hold the ball, unless it is already on the team's
+// best and designated player with the team holding the ball: to the designated player, else the
+// best one, when the team is best placed and no gamer holds them; else to the switch target. Never
+// to the goalkeeper or an uncontrollable player. Out of play, from the third second, gamers with
+// dynamic selection let go of their players. False on a switch with no selected player.
+HD bool HonourSwitchButtons(World &w, const Ctx &c, int teamID) {
+    MatchState &m = w.match;
+    Team &t = TeamByID(w, teamID);
+    if (!m.inPlay) {
+        if (m.actualTimeMs < 2000) return true;
+        if (DynamicPlayerSelection(w))
+            for (int g = 0; g < t.gamers.count; g++)
+                if (t.gamers[g].selectedPlayer >= 0) HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), -1);
+        t.mainSelectedPlayer = -1;
+        return true;
     }
+    for (int g = 0; g < t.gamers.count; g++) {
+        const int selected = t.gamers[g].selectedPlayer, best = TeamBestPossessionPlayer(w, teamID);
+        const bool settled = selected == best && selected == t.designatedTeamPossessionPlayer && !(t.teamPossessionAmount < 1.0f);
+        if (!t.gamers[g].controller.keyboard.buttons[kBtnSwitch] || settled) continue;
+        if (selected < 0) return Fail("the switch of a gamer that controls no player");
+        if (m.players[selected].hasUniquePossession) continue;
+        const bool bestPlaced = m.bestPossessionTeam == TeamSlot(w, teamID);
+        int target;
+        if (m.players[t.designatedTeamPossessionPlayer].base.externalController < 0 && bestPlaced) {
+            target = t.designatedTeamPossessionPlayer;
+        } else if (m.players[best].base.externalController < 0 && bestPlaced) {
+            target = best;
+        } else {
+            target = SwitchTargetPlayer(w, c, teamID);
+            if (target >= 0 && m.players[target].base.externalController >= 0) target = -1;
+        }
+        if (target == TeamGoalie(w, c, teamID)) target = -1;
+        if (target >= 0 && Formation(w, c, target).controllable) {
+            t.mainSelectedPlayer = target;
+            HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), target);
+        }
+    }
+    return true;
+}
+
+// The team's designated player becomes its best one (the quickest to the ball) when that is
+// clearly quicker: the ratio of their times (500 ms added to each) below 0.8, halved for a best
+// player on the ball and doubled for a designated one, 20% easier for a gamer's best player and
+// harder for a gamer's designated one, and harder for an AI best player while the designated one
+// beats the opponents by more than 100 ms.
+HD void ReconsiderDesignatedPlayer(World &w, int teamID) {
+    const MatchState &m = w.match;
+    Team &t = TeamByID(w, teamID);
+    const int designated = t.designatedTeamPossessionPlayer, best = TeamBestPossessionPlayer(w, teamID);
+    if (designated == best) return;
+    const int current = (int)w.roster.timeToBallMs[designated];
+    float ratio = (float)((int)w.roster.timeToBallMs[best] + 500) / (float)(current + 500);
+    if (m.players[best].hasPossession) ratio *= 0.5f;
+    if (m.players[designated].hasPossession) ratio /= 0.5f;
+    if (ExternalControllerActive(w, best)) ratio *= 0.8f;
+    if (ExternalControllerActive(w, designated)) ratio /= 0.8f;
+    if (!ExternalControllerActive(w, best) && current < TeamByID(w, 1 - teamID).timeToBallMs - 100) {
+        ratio += 0.2f;
+        ratio *= 1.2f;
+    }
+    if (ratio < 0.8f) t.designatedTeamPossessionPlayer = best;
+}
+
+// A team's tick: possession amounts, gamers' automatic selection, the team AI with dynamic roles
+// and man marking (staggered between the teams), its players, gamer switches and the designated
+// player.
+HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
+    ENG_SCOPE(25);
+    MatchState &m = w.match;
+    UpdatePossessionAmounts(w, teamID);
     TeamHumanGamersSelectAnyone(w, c, teamID);
     if (m.inPlay && !m.inSetPiece) {
         if (!TeamAIProcess(w, c, teamID)) return false;
@@ -511,57 +610,8 @@ HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
             p = next(p + 1);
         }
     }
-    if (m.inPlay) {
-        for (int g = 0; g < t.gamers.count; g++) {
-            HumanGamer &gm = t.gamers[g];
-            int sel = gm.selectedPlayer;
-            int best = TeamBestPossessionPlayer(w, teamID);
-            const bool *b = gm.controller.keyboard.buttons;
-            // GRF: a held switch reads as a fresh press every tick.
-            const bool sw = b[kBtnSwitch] &&
-                            (!(sel == best && sel == t.designatedTeamPossessionPlayer) || t.teamPossessionAmount < 1.0f);
-            if (sw && sel < 0) return Fail("the switch of a gamer that controls no player");
-            if (sw && !m.players[sel].hasUniquePossession) {
-                int target = -1;
-                const bool bestTeam = m.bestPossessionTeam == TeamSlot(w, teamID);
-                if (m.players[t.designatedTeamPossessionPlayer].base.externalController < 0 && bestTeam) {
-                    target = t.designatedTeamPossessionPlayer;
-                } else if (m.players[best].base.externalController < 0 && bestTeam) {
-                    target = best;
-                } else {
-                    target = SwitchTargetPlayer(w, c, teamID);
-                    if (target >= 0 && m.players[target].base.externalController >= 0) target = -1;
-                }
-                if (target == TeamGoalie(w, c, teamID)) target = -1;
-                if (target >= 0 && Formation(w, c, target).controllable) {
-                    t.mainSelectedPlayer = target;
-                    HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), target);
-                }
-            }
-        }
-    } else if (m.actualTimeMs >= 2000) {
-        if (DynamicPlayerSelection(w))
-            for (int g = 0; g < t.gamers.count; g++)
-                if (t.gamers[g].selectedPlayer >= 0) HumanGamerSetSelectedPlayer(w, GlobalGamerIndex(w, teamID, g), -1);
-        t.mainSelectedPlayer = -1;
-    }
-    // The designated player changes to the best one when clearly quicker to the ball.
-    int dt = (int)w.roster.timeToBallMs[t.designatedTeamPossessionPlayer];
-    int best = TeamBestPossessionPlayer(w, teamID);
-    int ot = opp.timeToBallMs;
-    if (t.designatedTeamPossessionPlayer != best) {
-        int d = t.designatedTeamPossessionPlayer;
-        float r = (float)((int)w.roster.timeToBallMs[best] + 500) / (float)(dt + 500);
-        if (m.players[best].hasPossession) r *= 0.5f;
-        if (m.players[d].hasPossession) r /= 0.5f;
-        if (ExternalControllerActive(w, best)) r *= 0.8f;
-        if (ExternalControllerActive(w, d)) r /= 0.8f;
-        if (!ExternalControllerActive(w, best) && dt < ot - 100) {
-            r += 0.2f;
-            r *= 1.2f;
-        }
-        if (r < 0.8f) t.designatedTeamPossessionPlayer = best;
-    }
+    if (!HonourSwitchButtons(w, c, teamID)) return false;
+    ReconsiderDesignatedPlayer(w, teamID);
     return true;
 }
 

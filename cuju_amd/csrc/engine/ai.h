@@ -143,55 +143,73 @@ HDN float Mixup(float base, int id, int role) {
     return base;
 }
 
-// The formation position (normalized to [-1, 1]) mapped into the team's current block and pulled
-// towards the focus points.
-HDN Vec3 GetAdaptedFormationPosition(const World &w, const Ctx &c, int p, float backX, float frontX, float lowY, float highY,
-                                     float xFocus, float xFocusStrength, float yFocus, float yFocusStrength,
-                                     const Vec3 &microFocus, float microFocusStrength, float midFocus,
-                                     float midFocusStrength, bool dynamic) {
-    int side = TeamDynamicSide(w, w.playerTeamID[p]);
+// ---- formation positions -------------------------------------------------------------------------
+// A player's place comes from its formation position (x and y in [-1, 1]) mapped into a block of
+// the pitch (`back` to `front` along x, `low` to `high` across) and pulled toward focus points.
+// The restarts set the block and foci by rule; in play the team's tactics and the ball set them.
+struct Placement {
+    float back, front, low, high;
+    float xFocus, xFocusStrength, yFocus, yFocusStrength;
+    Vec3 microFocus;
+    float microFocusStrength;
+    float midFocus, midFocusStrength;
+};
+// Formation x squeezed toward a midfield line (`focus` in 0..1 across the formation's length),
+// most for the middle of the formation (none beyond 1/1.2 of its half length).
+HD float StretchTowardMidfield(float x, float focus, float strength) {
+    const float line = focus * 2.0f - 1.0f;
+    float stretch = Clamp(1.0f - fabsf(x * 1.2f), 0.0f, 1.0f);
+    stretch = Curve(stretch, 1.0f);
+    stretch *= strength;
+    return x * (1.0f - stretch) + line * stretch;
+}
+// The pull toward the x focus: up to `strength`, easing (a cosine, to the 0.8 in double) with
+// nearness over the block's length.
+HD float PullTowardX(float x, const Placement &r) {
+    float bias = 1.0f - Clamp(fabsf(r.xFocus - x) / fabsf(r.back - r.front), 0.0f, 1.0f);
+    bias = -libm::cosf(bias * PI) * 0.5f + 0.5f;
+    bias = (float)libm::pow((double)bias, 0.8);
+    bias *= r.xFocusStrength;
+    return x * (1.0f - bias) + r.xFocus * bias;
+}
+// The pull toward the y focus: up to `strength`, by nearness over the block's width, more for a
+// focus far from the centre line.
+HD float PullTowardY(float y, const Placement &r) {
+    float bias = 1.0f - Clamp(fabsf(r.yFocus - y) / fabsf(r.high - r.low), 0.0f, 1.0f);
+    bias *= 0.2f + 0.8f * fabsf(r.yFocus) / kPitchHalfWidth;
+    bias *= r.yFocusStrength;
+    return y * (1.0f - bias) + r.yFocus * bias;
+}
+// The pull toward the micro focus of the block position `unpulled`, within 50 m (across distance
+// counted at 80%): falling with distance (curved), with a bump of 0.1 around 15% of the range; the
+// focus keeps 60% of its y and takes 40% of the player's.
+HD Vec3 PullTowardMicro(const Vec3 &pos, const Vec3 &unpulled, const Placement &r) {
+    const float yInfluence = 0.2f, yPosition = 0.4f;
+    const float reach = ((r.microFocus - unpulled) * Vec3(1, 1.0f - yInfluence, 0)).Length() / 50.0f;
+    if (!(reach < 1.0f)) return pos;
+    float bias = 1.0f;
+    bias *= 1.0f - reach;
+    bias = Curve(bias, 0.3f);
+    const float peakAt = 0.15f, peakWidth = 0.25f, peakHeight = 0.1f;
+    bias += (1.0f - NormalizedClamp(fabsf(reach - peakAt), 0.0f, peakWidth)) * peakHeight;
+    bias = Clamp(bias, 0.0f, 1.0f);
+    bias *= r.microFocusStrength;
+    const Vec3 focus = r.microFocus * Vec3(1, 1.0f - yPosition, 1) + pos * Vec3(0, yPosition, 0);
+    return pos * (1.0f - bias) + focus * (bias);
+}
+// Player p's place by a placement: its static (or dynamic) formation position squeezed toward
+// the midfield line, mapped into the block (y mirrored for the side), then pulled toward the x, y
+// and micro foci.
+HDN Vec3 PlaceInFormation(const World &w, const Ctx &c, int p, const Placement &r, bool dynamic) {
+    const int side = TeamDynamicSide(w, w.playerTeamID[p]);
     Vec3 pos = dynamic ? w.match.players[p].dynamicFormationEntry.position : Formation(w, c, p).position;
-    if (midFocusStrength > 0.0f) {
-        float factor = midFocus * 2.0f - 1.0f;
-        float stretch = Clamp(1.0f - fabsf(pos.v[0] * 1.2f), 0.0f, 1.0f);
-        stretch = Curve(stretch, 1.0f);
-        stretch *= midFocusStrength;
-        pos.v[0] = pos.v[0] * (1.0f - stretch) + factor * stretch;
-    }
-    float xl = frontX - backX;
-    pos.v[0] = backX + (pos.v[0] * 0.5f + 0.5f) * xl;
-    float yl = highY - lowY;
-    pos.v[1] = lowY + (pos.v[1] * -side * 0.5f + 0.5f) * yl;
-    Vec3 pure = pos;
-    if (xFocusStrength > 0.0f) {
-        float bias = 1.0f - Clamp(fabsf(xFocus - pos.v[0]) / fabsf(backX - frontX), 0.0f, 1.0f);
-        bias = -libm::cosf(bias * PI) * 0.5f + 0.5f;
-        bias = (float)libm::pow((double)bias, 0.8);
-        bias *= xFocusStrength;
-        pos.v[0] = pos.v[0] * (1.0f - bias) + xFocus * bias;
-    }
-    if (yFocusStrength > 0.0f) {
-        float d = Clamp(fabsf(yFocus - pos.v[1]) / fabsf(highY - lowY), 0.0f, 1.0f);
-        float bias = 1.0f - d;
-        bias *= 0.2f + 0.8f * fabsf(yFocus) / kPitchHalfWidth;
-        bias *= yFocusStrength;
-        pos.v[1] = pos.v[1] * (1.0f - bias) + yFocus * bias;
-    }
-    if (microFocusStrength > 0.0f) {
-        const float yInfluence = 0.2f, yPosition = 0.4f;
-        float fd = ((microFocus - pure) * Vec3(1, 1.0f - yInfluence, 0)).Length() / 50.0f;
-        if (fd < 1.0f) {
-            float mb = 1.0f;
-            mb *= 1.0f - fd;
-            mb = Curve(mb, 0.3f);
-            const float peakAt = 0.15f, peakWidth = 0.25f, peakHeight = 0.1f;
-            mb += (1.0f - NormalizedClamp(fabsf(fd - peakAt), 0.0f, peakWidth)) * peakHeight;
-            mb = Clamp(mb, 0.0f, 1.0f);
-            mb *= microFocusStrength;
-            Vec3 mfp = microFocus * Vec3(1, 1.0f - yPosition, 1) + pos * Vec3(0, yPosition, 0);
-            pos = pos * (1.0f - mb) + mfp * (mb);
-        }
-    }
+    if (r.midFocusStrength > 0.0f) pos.v[0] = StretchTowardMidfield(pos.v[0], r.midFocus, r.midFocusStrength);
+    pos.v[0] = r.back + (pos.v[0] * 0.5f + 0.5f) * (r.front - r.back);
+    pos.v[1] = r.low + (pos.v[1] * -side * 0.5f + 0.5f) * (r.high - r.low);
+    const Vec3 unpulled = pos;
+    if (r.xFocusStrength > 0.0f) pos.v[0] = PullTowardX(pos.v[0], r);
+    if (r.yFocusStrength > 0.0f) pos.v[1] = PullTowardY(pos.v[1], r);
+    if (r.microFocusStrength > 0.0f) pos = PullTowardMicro(pos, unpulled, r);
     return pos;
 }
 
@@ -214,74 +232,116 @@ HDN FormationHistory FormationHistoryOf(const World &w, int p) {
     return h;
 }
 
-HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool dynamic, const FormationHistory &history) {
-    const int t = w.playerTeamID[p];
-    const int side = TeamDynamicSide(w, t);
-    const TeamAI &ai = TeamByID(w, t).ai;
-    const Tactics &tac = ai.liveTactics;
-    const MatchState &m = w.match;
-    int role = dynamic ? m.players[p].dynamicFormationEntry.role : Formation(w, c, p).role;
-    Vec3 focal = Sp(w, m.designatedPossessionPlayer).position;
-    const Vec3 *const averages = history.ball;
-    float ballX = averages[0].v[0];
-    float ballY = averages[1].v[1];
-    auto T = [&](int id) { return Mixup(PropertiesGetReal(tac, id), id, role); };
-    float offDepth = T(kOffenseDepth), defDepth = T(kDefenseDepth);
-    float offWidth = T(kOffenseWidth), defWidth = T(kDefenseWidth);
-    float offOwnHalf = T(kOffenseOwnHalf), defOwnHalf = T(kDefenseOwnHalf);
-    float offMid = T(kOffenseMidfieldFocus), defMid = T(kDefenseMidfieldFocus);
-    float offMidS = T(kOffenseMidfieldFocusStrength), defMidS = T(kDefenseMidfieldFocusStrength);
-    float offSideS = T(kOffenseSideFocusStrength), defSideS = T(kDefenseSideFocusStrength);
-    float offMicroS = T(kOffenseMicroFocusStrength), defMicroS = T(kDefenseMicroFocusStrength);
+// The tactic values a role plays to (GRF's live tactics with the role's mixups): depth, width,
+// own-half offset, midfield focus and strengths, offensive and defensive. The side focus strengths
+// lean by the role's mindset and the team's offensiveness.
+struct RoleTactics {
+    float offDepth, defDepth, offWidth, defWidth, offOwnHalf, defOwnHalf, offMid, defMid, offMidS, defMidS, offSideS, defSideS,
+        offMicroS, defMicroS;
+};
+HD RoleTactics RoleTacticsOf(const TeamAI &ai, int role) {
+    auto T = [&](int id) { return Mixup(PropertiesGetReal(ai.liveTactics, id), id, role); };
+    RoleTactics t;
+    t.offDepth = T(kOffenseDepth);
+    t.defDepth = T(kDefenseDepth);
+    t.offWidth = T(kOffenseWidth);
+    t.defWidth = T(kDefenseWidth);
+    t.offOwnHalf = T(kOffenseOwnHalf);
+    t.defOwnHalf = T(kDefenseOwnHalf);
+    t.offMid = T(kOffenseMidfieldFocus);
+    t.defMid = T(kDefenseMidfieldFocus);
+    t.offMidS = T(kOffenseMidfieldFocusStrength);
+    t.defMidS = T(kDefenseMidfieldFocusStrength);
+    t.offSideS = T(kOffenseSideFocusStrength);
+    t.defSideS = T(kDefenseSideFocusStrength);
+    t.offMicroS = T(kOffenseMicroFocusStrength);
+    t.defMicroS = T(kDefenseMicroFocusStrength);
     const double mind = GetMindSet(role);
-    offSideS = (float)((double)offSideS + (-0.5 + mind) * (double)0.2f);
-    defSideS = (float)((double)defSideS + (0.5 - mind) * (double)0.2f);
+    t.offSideS = (float)((double)t.offSideS + (-0.5 + mind) * (double)0.2f);
+    t.defSideS = (float)((double)t.defSideS + (0.5 - mind) * (double)0.2f);
     const float ob = ai.offensivenessBias;
-    offSideS = Clamp(offSideS + -0.3f + (ob) * 0.3f, 0.0f, 1.0f);
-    defSideS = Clamp(defSideS + -0.3f + (1.0f - ob) * 0.3f, 0.0f, 1.0f);
-    float possAmount = NormalizedClamp(ai.fadingTeamPossessionAmount - 0.5f, 0.3f, 0.7f);
-    float ballBias = NormalizedClamp(((ballX / kPitchHalfLength) * -side), -0.7f, 0.7f);
-    float bbb = 1.0f - fabsf(possAmount * 2.0f - 1.0f);
-    bbb *= 0.6f;
-    float pb = possAmount * (1.0f - bbb) + ballBias * bbb;
-    pb = Clamp(pb + (ob - 0.5f) * 0.3f, 0.0f, 1.0f);
-    focal = (averages[2].Get2D() * 1.0f + focal * 0.0f) * pb + (averages[3].Get2D() * 0.5f + focal * 0.5f) * (1.0f - pb);
-    float depth = ai.depth * (offDepth * pb + defDepth * (1.0f - pb));
-    float width = ai.width * (offWidth * pb + defWidth * (1.0f - pb));
-    float offsetX = kPitchHalfLength * side * ((offOwnHalf * 2.0f - 1.0f) * pb + (defOwnHalf * 2.0f - 1.0f) * (1.0f - pb));
-    float sideS = (offSideS * pb + defSideS * (1.0f - pb));
-    float sideFocus = pb * 2.0f - 1.0f;
-    float sideX = 0.2f * sideFocus * -side * kPitchHalfLength + 0.8f * -history.possessionSide * kPitchHalfLength;
-    float centerX = Clamp((ballX * (1.0f - sideS) + sideX * sideS) + offsetX, -kPitchHalfLength, kPitchHalfLength);
+    t.offSideS = Clamp(t.offSideS + -0.3f + (ob) * 0.3f, 0.0f, 1.0f);
+    t.defSideS = Clamp(t.defSideS + -0.3f + (1.0f - ob) * 0.3f, 0.0f, 1.0f);
+    return t;
+}
+// How offensively the team sets up, 0 to 1: its fading possession (0.8 to 1.2 maps to 0 to 1),
+// blended (up to 60%, at even possession) with how far upfield the ball has been (within 70% of
+// the half length), shifted by the team's offensiveness.
+HD float AttackShare(const TeamAI &ai, float ballX, int side) {
+    const float possession = NormalizedClamp(ai.fadingTeamPossessionAmount - 0.5f, 0.3f, 0.7f);
+    const float upfield = NormalizedClamp(((ballX / kPitchHalfLength) * -side), -0.7f, 0.7f);
+    float blend = 1.0f - fabsf(possession * 2.0f - 1.0f);
+    blend *= 0.6f;
+    const float share = possession * (1.0f - blend) + upfield * blend;
+    return Clamp(share + (ai.offensivenessBias - 0.5f) * 0.3f, 0.0f, 1.0f);
+}
+// The block a team plays in: centred on the ball's averages (x shifted toward the possession side
+// and by the own-half offset; y), squeezed toward the centre by the depth and width it spans
+// (95% and 90% fit), never behind the offside trap.
+HD void TeamBlock(const TeamAI &ai, const RoleTactics &t, float share, int side, float ballX, float ballY, float possessionSide,
+                  Placement &r) {
+    const float depth = ai.depth * (t.offDepth * share + t.defDepth * (1.0f - share));
+    const float width = ai.width * (t.offWidth * share + t.defWidth * (1.0f - share));
+    const float offsetX =
+        kPitchHalfLength * side * ((t.offOwnHalf * 2.0f - 1.0f) * share + (t.defOwnHalf * 2.0f - 1.0f) * (1.0f - share));
+    const float sideStrength = (t.offSideS * share + t.defSideS * (1.0f - share));
+    const float sideX = 0.2f * (share * 2.0f - 1.0f) * -side * kPitchHalfLength + 0.8f * -possessionSide * kPitchHalfLength;
+    float centerX = Clamp((ballX * (1.0f - sideStrength) + sideX * sideStrength) + offsetX, -kPitchHalfLength, kPitchHalfLength);
     float centerY = Clamp(ballY, -kPitchHalfWidth, kPitchHalfWidth);
     const float fitDepth = 0.95f, fitWidth = 0.9f;
     centerX *= ((1.0f - depth) / 1.0f) * fitDepth + (1.0f - fitDepth);
     centerY *= ((1.0f - width) / 1.0f) * fitWidth + (1.0f - fitWidth);
-    float backX = centerX - depth * kPitchHalfLength * -side;
-    float frontX = centerX + depth * kPitchHalfLength * -side;
-    float lowY = centerY - width * kPitchHalfWidth;
-    float highY = centerY + width * kPitchHalfWidth;
-    if (backX * side > ai.offsideTrapX * side) backX = Clamp(ai.offsideTrapX, -kPitchHalfLength, kPitchHalfLength);
-    float yFocus = ballY * 1.0f;
-    float yFocusS = 0.5f * pb + 0.2f * (1.0f - pb);
-    Vec3 micro = focal;
-    Vec3 defensive = Vec3(Clamp(micro.v[0] + side * 2.0f, -kPitchHalfLength, backX * side), micro.v[1] * 0.9f, 0);
-    micro = (Vec3(Clamp(micro.v[0] - side * 1.0f, -kPitchHalfLength, kPitchHalfLength), micro.v[1] * 0.9f, 0)) * pb +
-            (defensive) * (1.0f - pb);
-    float microS = (offMicroS * pb + defMicroS * (1.0f - pb));
-    float msb = NormalizedClamp((ballX / kPitchHalfLength) * -side, -0.7f, 0.7f);
-    msb = msb * 0.7f + 0.3f;
-    float autoMicro = (libm::powf(msb, 0.8f) * pb + (libm::powf(1.0f - msb, 0.6f)) * (1.0f - pb));
-    microS = microS * (0.2f + 0.8f * autoMicro);
-    float manualMid = (offMid * pb + defMid * (1.0f - pb));
-    float autoMid = NormalizedClamp((ballX / kPitchHalfLength) * -side, -0.8f, 0.8f);
-    float midFocus = manualMid * 0.7f + autoMid * 0.3f;
-    float midS = (offMidS * pb + defMidS * (1.0f - pb));
-    Vec3 d = GetAdaptedFormationPosition(w, c, p, backX, frontX, lowY, highY, 0.0f, 0.0f, yFocus, yFocusS, micro, microS,
-                                         midFocus, midS, dynamic);
-    d.v[0] = Clamp(d.v[0], -kPitchHalfLength, kPitchHalfLength);
-    d.v[1] = Clamp(d.v[1], -kPitchHalfWidth, kPitchHalfWidth);
-    return d;
+    r.back = centerX - depth * kPitchHalfLength * -side;
+    r.front = centerX + depth * kPitchHalfLength * -side;
+    r.low = centerY - width * kPitchHalfWidth;
+    r.high = centerY + width * kPitchHalfWidth;
+    if (r.back * side > ai.offsideTrapX * side) r.back = Clamp(ai.offsideTrapX, -kPitchHalfLength, kPitchHalfLength);
+}
+// The micro focus around the play (`focal`): a metre upfield when attacking, 2 m goalside (no
+// deeper than the block's back) when defending, its y at 90%; its strength scaled by how far
+// upfield (attacking) or back (defending) the ball has been.
+HD void TeamMicroFocus(const RoleTactics &t, float share, int side, float ballX, const Vec3 &focal, Placement &r) {
+    const Vec3 defensive = Vec3(Clamp(focal.v[0] + side * 2.0f, -kPitchHalfLength, r.back * side), focal.v[1] * 0.9f, 0);
+    r.microFocus = (Vec3(Clamp(focal.v[0] - side * 1.0f, -kPitchHalfLength, kPitchHalfLength), focal.v[1] * 0.9f, 0)) * share +
+                   (defensive) * (1.0f - share);
+    const float strength = (t.offMicroS * share + t.defMicroS * (1.0f - share));
+    float upfield = NormalizedClamp((ballX / kPitchHalfLength) * -side, -0.7f, 0.7f);
+    upfield = upfield * 0.7f + 0.3f;
+    const float automatic = (libm::powf(upfield, 0.8f) * share + (libm::powf(1.0f - upfield, 0.6f)) * (1.0f - share));
+    r.microFocusStrength = strength * (0.2f + 0.8f * automatic);
+}
+
+// Player p's place in open play (GRF's adapted formation position): the role's tactics and the
+// team's attack share set the block around the ball's recent averages, a y focus on the ball
+// (stronger attacking), the micro focus around the play (the 3 s ball average attacking; the 2 s
+// average halfway to the designated player defending), and a midfield focus from the tactics
+// (70%) and the ball (30%). Clamped to the pitch.
+HDN Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool dynamic, const FormationHistory &history) {
+    const int side = TeamDynamicSide(w, w.playerTeamID[p]);
+    const TeamAI &ai = TeamByID(w, w.playerTeamID[p]).ai;
+    const MatchState &m = w.match;
+    const int role = dynamic ? m.players[p].dynamicFormationEntry.role : Formation(w, c, p).role;
+    const float ballX = history.ball[0].v[0], ballY = history.ball[1].v[1];
+    const RoleTactics t = RoleTacticsOf(ai, role);
+    const float share = AttackShare(ai, ballX, side);
+    const Vec3 designated = Sp(w, m.designatedPossessionPlayer).position;
+    const Vec3 focal =
+        (history.ball[2].Get2D() * 1.0f + designated * 0.0f) * share + (history.ball[3].Get2D() * 0.5f + designated * 0.5f) * (1.0f - share);
+    Placement r{};
+    TeamBlock(ai, t, share, side, ballX, ballY, history.possessionSide, r);
+    r.xFocus = 0.0f;
+    r.xFocusStrength = 0.0f;
+    r.yFocus = ballY * 1.0f;
+    r.yFocusStrength = 0.5f * share + 0.2f * (1.0f - share);
+    TeamMicroFocus(t, share, side, ballX, focal, r);
+    const float manualMid = (t.offMid * share + t.defMid * (1.0f - share));
+    const float autoMid = NormalizedClamp((ballX / kPitchHalfLength) * -side, -0.8f, 0.8f);
+    r.midFocus = manualMid * 0.7f + autoMid * 0.3f;
+    r.midFocusStrength = (t.offMidS * share + t.defMidS * (1.0f - share));
+    Vec3 place = PlaceInFormation(w, c, p, r, dynamic);
+    place.v[0] = Clamp(place.v[0], -kPitchHalfLength, kPitchHalfLength);
+    place.v[1] = Clamp(place.v[1], -kPitchHalfWidth, kPitchHalfWidth);
+    return place;
 }
 HD Vec3 TeamAdaptedFormationPosition(const World &w, const Ctx &c, int p, bool dynamic) {
     return TeamAdaptedFormationPosition(w, c, p, dynamic, FormationHistoryOf(w, p));

@@ -253,16 +253,8 @@ HDN bool RestartMatch(World &w, const Ctx &c, const Vec3 &focus) {
 HD float ToFloat(double v) { return (float)v; }
 
 // Where the outfield players of a team go for a goal kick, corner, throw-in, free kick or penalty:
-// the arguments of their adapted formation positions (GetAdaptedFormationPosition), for the team
-// that takes the restart or the one that defends it. `side` is the team's side of the pitch and
-// `ball` the ball on the ground.
-struct Placement {
-    float back, front, low, high;
-    float xFocus, xFocusStrength, yFocus, yFocusStrength;
-    Vec3 microFocus;
-    float microFocusStrength;
-    float midFocus, midFocusStrength;
-};
+// the placement of their formation positions, for the team that takes the restart or the one that
+// defends it. `side` is the team's side of the pitch and `ball` the ball on the ground.
 HD Placement PlacementRule(int setPiece, bool taking, int side, const Vec3 &ball) {
     const double hw = kPitchHalfWidth;
     const float L = kPitchHalfLength, own = side * kPitchHalfLength, theirs = -side * kPitchHalfLength;
@@ -389,9 +381,7 @@ HDN bool PlaceByRule(World &w, const Ctx &c, int teamID, int setPiece, bool taki
     const double hl = kPitchHalfLength;
     const int penaltyEnd = (ball.v[0] < 0) ? -1 : 1;
     for (int i = 0; i < outfield.count; i++) {
-        Vec3 bp = GetAdaptedFormationPosition(w, c, outfield[i], r.back, r.front, r.low, r.high, r.xFocus, r.xFocusStrength, r.yFocus,
-                                              r.yFocusStrength, r.microFocus, r.microFocusStrength, r.midFocus, r.midFocusStrength,
-                                              false);
+        Vec3 bp = PlaceInFormation(w, c, outfield[i], r, false);
         if (setPiece == kModeFreeKick && !taking && (double)(bp - ball).Length() < 9.15) bp = KeepOff(bp, ball, 9.15f);
         if (setPiece == kModePenalty) {
             if ((double)(bp.v[0] * penaltyEnd) > hl - 16.5 - 0.5) bp.v[0] = ToFloat((hl - 16.5 - 0.5) * penaltyEnd);

@@ -256,49 +256,84 @@ struct AIBase {
         return ps.timeToBallMs;
     }
 
-    // Picks the interception time on the ball's path that best fits the desired movement (or the
-    // earliest reachable one, with haste).
+    // The desired direction snapped to the nearest of 16 directions in the frame of the ball's
+    // path (the path from now to a second ahead as the x axis).
+    HD Vec3 SnapInBallFrame(const Vec3 &desiredDir) const {
+        const Vec3 along = (MentalBall(0).Get2D() - MentalBall(1000).Get2D()).Normalized(desiredDir);
+        const float frame = along.Angle2D();
+        Vec3 inFrame = desiredDir.Rotated2D(-frame);
+        const int directions = 16;
+        float a = inFrame.Angle2D();
+        a /= PI * 2.0f;
+        a = roundf(a * directions);
+        a /= directions;
+        a *= PI * 2.0f;
+        const float bias = 1.0f;
+        inFrame = (inFrame * (1.0f - bias) + (Vec3(1, 0, 0).Rotated2D(a) * bias)).Normalized(inFrame);
+        return inFrame.Rotated2D(frame);
+    }
+    // How an interception point suits the chase: the movement toward it against the desired
+    // movement (40%) and direction (60%), its time (within 5 s), its distance from the point of the
+    // ball's path nearest the player (within two sprint seconds) and the last desired time to the
+    // ball, by the weights.
+    struct InterceptWeights {
+        float movement, time, perpendicular, previous;
+    };
+    HD float InterceptRating(const InterceptWeights &wt, const Vec3 &target, unsigned t, const Vec3 &desiredDir, const Vec3 &desiredMov,
+                             const Vec3 &nearestOnPath, int previousDesired, int timeToBall) const {
+        const Vec3 pp = Pos();
+        const float speed = Clamp((target - pp).Length() * kDistanceToVelocity, kIdleVelocity, kSprintVelocity);
+        const Vec3 toward = (target - pp).Normalized(0) * speed;
+        float movement = 1.0f - NormalizedClamp((desiredMov - toward).Length(), 0.0f, kSprintVelocity);
+        const float direction = 1.0f - NormalizedClamp(fabsf(desiredDir.Angle2D(toward.Normalized(desiredDir))), 0.0f, 0.5f * PI);
+        movement = movement * 0.4f + direction * 0.6f;
+        const float time = 1.0f - NormalizedClamp((float)t, 0, 5000);
+        const float perpendicular = 1.0f - NormalizedClamp((nearestOnPath - target).Length(), 0, 2.0f * kSprintVelocity);
+        float previous = 0.0f;
+        if (previousDesired >= timeToBall) {
+            const int diff = previousDesired - timeToBall;
+            previous = 1.0f - (diff < 0 ? -diff : diff) / 500.0f;
+        }
+        return movement * wt.movement + time * wt.time + perpendicular * wt.perpendicular + previous * wt.previous;
+    }
+    // Where to look while chasing: along the desired direction when the interception is within
+    // 100 ms or the chase is idle, else the desired direction held within the sector between the
+    // ball and the chase direction; at most a quarter turn off the ball, 10 m out.
+    HD Vec3 ChaseLookAt(int bestTime, float bestVel, const Vec3 &desiredDir, const Vec3 &chaseDir) const {
+        const Vec3 pp = Pos();
+        const Vec3 ball = (MentalBall(20).Get2D() - pp).Normalized(desiredDir);
+        Vec3 look = desiredDir;
+        if (!(bestTime < 100) && VelocityCat(bestVel) != kVelIdle) look = GetClamped2D(desiredDir, ball, chaseDir);
+        return pp + ball.Rotated2D(Clamp(look.Angle2D(ball) * 1.0f, -0.25f * PI, 0.25f * PI)) * 10.0f;
+    }
+
+    // GRF's chase of a loose ball: from the player's time to the ball on, the points of the
+    // mental ball's path below 1 m (stepping by a twentieth of the slack, 10 to 100 ms) that the
+    // player reaches in time, rated by how they suit the desired movement (or, with haste, by
+    // time); a point off the pitch, or one reached while the ball comes toward the player or far
+    // earlier than its time to the ball, ends the scan. Returns the chosen time (the span's end
+    // without one), with the direction, speed and look-at of the chase.
     HDN unsigned ToBallMovement(const Vec3 &desiredDir, float desiredVel, Vec3 &bestDir, float &bestVel, Vec3 &bestLookAt,
                                 float haste) const {
         ENG_SCOPE(39);
         const Vec3 pp = Pos();
         const float maxVel = GetMaximumVelocity(*c.sd, p);
-        float movementW = 1.0f, timeW = 0.0f, perpW = 0.1f, prevW = 0.0f;
-        Vec3 adDir = desiredDir;
-        Line ballLine(MentalBall(0).Get2D(), MentalBall(1000).Get2D());
-        float frac = 0;
-        ballLine.DistanceToPoint(pp, frac);
-        Vec3 shortest = ballLine.pts[0] + (ballLine.pts[1] - ballLine.pts[0]) * frac;
-        Vec3 ballSpace = (MentalBall(0).Get2D() - MentalBall(1000).Get2D()).Normalized(adDir);
-        float bsAngle = ballSpace.Angle2D();
-        Vec3 adBs = adDir.Rotated2D(-bsAngle);
-        {
-            const int directions = 16;
-            float a = adBs.Angle2D();
-            a /= PI * 2.0f;
-            a = roundf(a * directions);
-            a /= directions;
-            a *= PI * 2.0f;
-            const float bias = 1.0f;
-            adBs = (adBs * (1.0f - bias) + (Vec3(1, 0, 0).Rotated2D(a) * bias)).Normalized(adBs);
-        }
-        adDir = adBs.Rotated2D(bsAngle);
-        Vec3 desiredMov = adDir * desiredVel;
-        if (haste > 0.0f) {
-            movementW = 0.0f;
-            timeW = 1.0f;
-            perpW = 0.0f;
-        }
+        InterceptWeights weights{1.0f, 0.0f, 0.1f, 0.0f};
+        if (haste > 0.0f) weights = {0.0f, 1.0f, 0.0f, 0.0f};
+        const Line path(MentalBall(0).Get2D(), MentalBall(1000).Get2D());
+        float along = 0;
+        path.DistanceToPoint(pp, along);
+        const Vec3 nearestOnPath = path.pts[0] + (path.pts[1] - path.pts[0]) * along;
+        const Vec3 snapped = SnapInBallFrame(desiredDir);
+        const Vec3 desiredMov = snapped * desiredVel;
         float bestRating = -10000.0f;
         int bestNeeded = -10, bestTime = -10;
         const uint32_t ttb = ps.timeToBallMs;
         unsigned start = TruncToUint32(Clamp((float)ttb, 40, (float)(kBallPredictionSpanMs - 10)));
-        Vec3 bpStart = MentalBall((int)start);
-        if (fabsf(bpStart.v[0]) > kPitchHalfLength - 0.2f || fabsf(bpStart.v[1]) > kPitchHalfWidth - 0.2f) start = 80;
-        const int prevDesired = ps.desiredTimeToBallMs;
-        const int ttbInt = (int)ttb;
-        Vec3 ballMovRough = (MentalBall((int)(ttb + 10)) - MentalBall((int)ttb)).Get2D() * 100.0f;
-        Vec3 ballDirRough = ballMovRough.Normalized(adDir);
+        const Vec3 first = MentalBall((int)start);
+        if (fabsf(first.v[0]) > kPitchHalfLength - 0.2f || fabsf(first.v[1]) > kPitchHalfWidth - 0.2f) start = 80;
+        const int previousDesired = ps.desiredTimeToBallMs;
+        const Vec3 ballHeading = ((MentalBall((int)(ttb + 10)) - MentalBall((int)ttb)).Get2D() * 100.0f).Normalized(snapped);
         unsigned step = 1;
         const Vec3 mov = Mov();
         const bool walks = TimeWalkApplies(mov);
@@ -307,10 +342,9 @@ struct AIBase {
         const MentalBallView mental(w, k);
         TimeNeededScan scan(pp, mov, maxVel);
         for (unsigned t = start; t < (unsigned)kBallPredictionSpanMs; t += 10 * step) {
-            bool forced = false;
             Vec3 target = mental.At((int)t);
-            if (fabsf(target.v[0]) > kPitchHalfLength - 0.2f || fabsf(target.v[1]) > kPitchHalfWidth - 0.2f) forced = true;
-            if (!forced && target.v[2] >= 1.0f) continue;
+            bool last = fabsf(target.v[0]) > kPitchHalfLength - 0.2f || fabsf(target.v[1]) > kPitchHalfWidth - 0.2f;
+            if (!last && target.v[2] >= 1.0f) continue;
             target = target.Get2D();
             TimeNeeded tn;
             if (!scan.Unreachable(target, true, t, tn)) {
@@ -321,55 +355,31 @@ struct AIBase {
                 }
                 tn = walks ? WalkTimeNeeded(walk, pp, mov, target, maxVel, true, t, true) : GetTimeNeededMs(pp, mov, target, maxVel, true, t);
             }
-            unsigned needed = tn.usual;
+            const unsigned needed = tn.usual;
             int next = TruncToInt32(roundf((float)(int)(needed - t) * 0.05f)) - 5;
             next = next < 1 ? 1 : next;
             next = 10 < next ? 10 : next;
             step = (unsigned)next;
             if (needed <= t) {
-                float dot = (target - pp).Normalized(0).Dot(ballDirRough);
-                float jit = Clamp((float)ttb / (float)t, 0.0f, 1.0f);
-                if (jit < 0.35f) forced = true;
-                if (dot > 0.0f) forced = true;
-                float td = (target - pp).Length();
-                float tv = Clamp(td * kDistanceToVelocity, kIdleVelocity, kSprintVelocity);
-                Vec3 tm = (target - pp).Normalized(0) * tv;
-                float movementRating = 1.0f - NormalizedClamp((desiredMov - tm).Length(), 0.0f, kSprintVelocity);
-                float directionRating = 1.0f - NormalizedClamp(fabsf(adDir.Angle2D(tm.Normalized(adDir))), 0.0f, 0.5f * PI);
-                movementRating = movementRating * 0.4f + directionRating * 0.6f;
-                float timeRating = 1.0f - NormalizedClamp((float)t, 0, 5000);
-                float perpRating = 1.0f - NormalizedClamp((shortest - target).Length(), 0, 2.0f * kSprintVelocity);
-                float prevRating = 0.0f;
-                if (prevDesired >= ttbInt) {
-                    int diff = prevDesired - ttbInt;
-                    prevRating = 1.0f - (diff < 0 ? -diff : diff) / 500.0f;
-                }
-                float rating = movementRating * movementW + timeRating * timeW + perpRating * perpW + prevRating * prevW;
-                if (rating > bestRating || (forced && bestTime == -10)) {
+                if (Clamp((float)ttb / (float)t, 0.0f, 1.0f) < 0.35f) last = true;
+                if ((target - pp).Normalized(0).Dot(ballHeading) > 0.0f) last = true;
+                const float rating = InterceptRating(weights, target, t, snapped, desiredMov, nearestOnPath, previousDesired, (int)ttb);
+                if (rating > bestRating || (last && bestTime == -10)) {
                     bestRating = rating;
                     bestTime = (int)t;
                     bestNeeded = (int)needed;
                 }
             }
-            if (forced) {
-                if (bestTime == -10) {
-                    bestTime = (int)t;
-                    bestNeeded = (int)t;
-                }
+            if (last) {
+                if (bestTime == -10) bestTime = bestNeeded = (int)t;
                 break;
             }
         }
         if (bestTime == -10) bestTime = bestNeeded = kBallPredictionSpanMs - 10;
-        Vec3 target = MentalBall(bestTime).Get2D();
-        bestDir = (target - pp).Normalized(Dir());
+        bestDir = (MentalBall(bestTime).Get2D() - pp).Normalized(Dir());
         bestVel = Clamp(((float)bestNeeded / (float)bestTime) * maxVel, kIdleVelocity, kSprintVelocity);
         if (bestTime > 250) bestVel = bestVel * 0.97f + FloatVelocity() * 0.03f;
-        Vec3 lookBall = (MentalBall(20).Get2D() - pp).Normalized(adDir);
-        Vec3 lookDesired;
-        if (bestTime < 100) lookDesired = adDir;
-        else if (VelocityCat(bestVel) != kVelIdle) lookDesired = GetClamped2D(adDir, lookBall, bestDir);
-        else lookDesired = adDir;
-        bestLookAt = pp + lookBall.Rotated2D(Clamp(lookDesired.Angle2D(lookBall) * 1.0f, -0.25f * PI, 0.25f * PI)) * 10.0f;
+        bestLookAt = ChaseLookAt(bestTime, bestVel, snapped, bestDir);
         return (unsigned)bestTime;
     }
 
@@ -626,92 +636,93 @@ struct AIBase {
         float d = (goal - from).Length();
         return Clamp(d - threshold * NormalizedClamp(d, 0.0f, threshold * 2.0f), 0.0f, kPitchHalfLength);
     }
+    // How far the keeper comes off its line, 0 to 1: 30% with the ball well held (fading
+    // possession 1 to 1.5); without it, all the way when the opponent on the ball will reach its
+    // shooting point (20 m out, less near goal) before any teammate reaches it, unless a second
+    // attacker's shooting point (24 m) is as badly covered. `path` starts where the attack comes
+    // from (the opponent 0.32 s ahead, blended with the ball).
+    HD float KeeperRush(const Vec3 &ball, const Vec3 &goal, Line &path) const {
+        float rush = 0.3f;
+        rush *= NormalizedClamp(ctl.fadingTeamPossessionAmount, 1.0f, 1.5f);
+        if (!(ctl.fadingTeamPossessionAmount < 1.0f)) return rush;
+        const int o = Opp().designatedTeamPossessionPlayer;
+        const Vec3 op = Pos(o) + Mov(o) * 0.32f;
+        if (m.players[o].hasPossession == false) path.pts[0] = op * 0.6f + ball * 0.4f;
+        else path.pts[0] = op * 0.4f + ball * 0.6f;
+        const float oppThreshold = ToThreshold(goal, op, 20.0f);
+        const Vec3 shootingPoint = op + (goal - op).Normalized(0) * oppThreshold;
+        const int mate = GetClosestPlayer(w, c, teamID, shootingPoint, false, p);
+        float mateThreshold = 99999;
+        if (mate >= 0) mateThreshold = (shootingPoint - (Pos(mate) + Mov(mate) * 0.24f)).Length();
+        if (!(mateThreshold > oppThreshold + 1.0f)) return rush;
+        const int helper = GetClosestPlayer(w, c, oppID, goal, false, o);
+        if (helper < 0) return 1.0f;
+        const Vec3 hp = Pos(helper) + Mov(helper) * 0.32f;
+        const float helperThreshold = ToThreshold(goal, hp, 24.0f);
+        const Vec3 helperPoint = hp + (goal - hp).Normalized(0) * helperThreshold;
+        const int mateHelper = GetClosestPlayer(w, c, teamID, helperPoint, false, p);
+        float mateHelperThreshold = 99999;
+        if (mateHelper >= 0) mateHelperThreshold = (helperPoint - (Pos(mateHelper) + Mov(mateHelper) * 0.24f)).Length();
+        float second = 0.0f;
+        if (mateHelperThreshold > helperThreshold) second = NormalizedClamp(mateHelperThreshold - helperThreshold, 0.0f, 2.0f);
+        float ratio = 1.0f - NormalizedClamp(helperThreshold / (oppThreshold + 0.0001f), 1.0f, 1.5f);
+        ratio *= 0.7f;
+        return Clamp(1.0f - (second * ratio), 0.0f, 1.0f);
+    }
+    // The keeper covering its goal from a ball in its half: on the bisector of the angle the posts
+    // make from the ball (met 0.7 m inside the goal line, within the posts), out from there by
+    // the rush (at least 0.7 m) toward where the attack comes from; walking once in front of its
+    // target near that line.
+    HD Vec3 KeeperCover(const Vec3 &ball, const Vec3 &goal, float &maxVel) const {
+        const Vec3 post1 = Vec3(kPitchHalfLength * side, 3.7f, 0) - ball;
+        const Vec3 post2 = Vec3(kPitchHalfLength * side, -3.7f, 0) - ball;
+        const Vec3 middle = post1.Rotated2D(post2.Angle2D(post1) * 0.5f).Normalized(Vec3(side, 0, 0));
+        Line path(ball, ball + middle);
+        const Line inside(Vec3((kPitchHalfLength - 0.7f) * side, -kPitchHalfWidth, 0), Vec3((kPitchHalfLength - 0.7f) * side, kPitchHalfWidth, 0));
+        Vec3 onLine = path.IntersectionPoint(inside).Get2D();
+        onLine.v[1] = Clamp(onLine.v[1], -3.7f, 3.7f);
+        path.pts[1] = onLine;
+        float rush = KeeperRush(ball, goal, path);
+        if (AI().endApplyKeeperRushMs > m.actualTimeMs) rush = 1.0f;
+        const float out = Clamp(MaxF(path.Length() - 0.5f, 0.0f) * rush, 0.7f, kPitchHalfLength);
+        Vec3 target = path.pts[1] + (path.pts[0] - path.pts[1]).Normalized(0) * out;
+        float along = 0.0f;
+        const float fromPath = path.DistanceToPoint(Pos(), along);
+        if ((target - goal).Length() < (Pos() - goal).Length() && fromPath < 1.0f && along > 0.0f) maxVel = kWalkVelocity;
+        target.v[0] = Clamp(target.v[0], -kPitchHalfLength + 0.2f, kPitchHalfLength - 0.2f);
+        return target;
+    }
+    // The keeper against a ball bound for goal: onto the ball's line to where it crosses the goal
+    // line (0.4 m short), at the point nearest the keeper; at the crossing itself when the ball
+    // will pass the keeper above 2.5 m.
+    HD Vec3 KeeperSave() const {
+        Line path;
+        path.pts[0] = MentalBall(10).Get2D();
+        Vec3 crossing = Vec3(kPitchHalfLength * side, eliza->ballBoundForGoalY, 0);
+        crossing += (path.pts[0] - crossing).Normalized(0) * 0.4f;
+        path.pts[1] = crossing;
+        float keeperAt = 0.0f;
+        path.DistanceToPoint(Pos() + Mov() * 0.05f, keeperAt);
+        float secondAt = 0.0f;
+        path.DistanceToPoint(MentalBall(1010).Get2D(), secondAt);
+        if ((double)secondAt > 1e-4 && (double)MentalBall(TruncToInt32(10 + 1000 * (keeperAt / secondAt))).v[2] > 2.5) return crossing;
+        keeperAt = Clamp(keeperAt, 0.0f, 1.0f);
+        Vec3 target = path.pts[0] + (path.pts[1] - path.pts[0]) * keeperAt;
+        target.v[2] = 0.0f;
+        target.v[0] = Clamp(target.v[0], -kPitchHalfLength + 0.2f, kPitchHalfLength - 0.2f);
+        return target;
+    }
+    // The goalkeeper's movement: 10 m off its goal line by default; with the ball (600 ms plus a
+    // fifth of its time to it ahead) in its half, covering the goal or saving a ball bound for it.
     HDN void GoalieRequestInput(Vec3 &dir, float &vel) {
         ENG_SCOPE(46);
-        const float lineDistance = 10.0f;
-        Vec3 bp = MentalBall(TruncToInt32(600 + (float)ps.timeToBallMs * 0.2f)).Get2D();
-        Vec3 target = Vec3((kPitchHalfLength - lineDistance) * side, 0, 0);
-        Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
+        const Vec3 ball = MentalBall(TruncToInt32(600 + (float)ps.timeToBallMs * 0.2f)).Get2D();
+        const Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
+        Vec3 target = Vec3((kPitchHalfLength - 10.0f) * side, 0, 0);
         float maxVel = kSprintVelocity;
-        if (bp.v[0] * side > 0) {
+        if (ball.v[0] * side > 0) {
             CalculateIfBallIsBoundForGoal();
-            if (!eliza->ballBoundForGoal) {
-                maxVel = kSprintVelocity;
-                Vec3 post1 = Vec3(kPitchHalfLength * side, 3.7f, 0) - bp;
-                Vec3 post2 = Vec3(kPitchHalfLength * side, -3.7f, 0) - bp;
-                float a = post2.Angle2D(post1);
-                Vec3 middle = post1.Rotated2D(a * 0.5f).Normalized(Vec3(side, 0, 0));
-                Line toGoal(bp, bp + middle);
-                Line back(Vec3((kPitchHalfLength - 0.7f) * side, -kPitchHalfWidth, 0), Vec3((kPitchHalfLength - 0.7f) * side, kPitchHalfWidth, 0));
-                Vec3 is = toGoal.IntersectionPoint(back).Get2D();
-                is.v[1] = Clamp(is.v[1], -3.7f, 3.7f);
-                toGoal.pts[1] = is;
-                float awayOffset = 0.7f;
-                float awayBias = 0.3f;
-                awayBias *= NormalizedClamp(ctl.fadingTeamPossessionAmount, 1.0f, 1.5f);
-                if (ctl.fadingTeamPossessionAmount < 1.0f) {
-                    const int o = Opp().designatedTeamPossessionPlayer;
-                    Vec3 op = Pos(o) + Mov(o) * 0.32f;
-                    if (m.players[o].hasPossession == false) toGoal.pts[0] = op * 0.6f + bp * 0.4f;
-                    else toGoal.pts[0] = op * 0.4f + bp * 0.6f;
-                    float oppTh = ToThreshold(goal, op, 20.0f);
-                    Vec3 shootingPoint = op + (goal - op).Normalized(0) * oppTh;
-                    int mate = GetClosestPlayer(w, c, teamID, shootingPoint, false, p);
-                    float mateTh = 99999;
-                    if (mate >= 0) mateTh = (shootingPoint - (Pos(mate) + Mov(mate) * 0.24f)).Length();
-                    if (mateTh > oppTh + 1.0f) {
-                        awayBias = 1.0f;
-                        int helper = GetClosestPlayer(w, c, oppID, goal, false, o);
-                        if (helper >= 0) {
-                            Vec3 hp = Pos(helper) + Mov(helper) * 0.32f;
-                            float helperTh = ToThreshold(goal, hp, 24.0f);
-                            Vec3 hsp = hp + (goal - hp).Normalized(0) * helperTh;
-                            int mateHelper = GetClosestPlayer(w, c, teamID, hsp, false, p);
-                            float mateHelperTh = 99999;
-                            if (mateHelper >= 0) mateHelperTh = (hsp - (Pos(mateHelper) + Mov(mateHelper) * 0.24f)).Length();
-                            float second = 0.0f;
-                            if (mateHelperTh > helperTh) second = NormalizedClamp(mateHelperTh - helperTh, 0.0f, 2.0f);
-                            float ratio = 1.0f - NormalizedClamp(helperTh / (oppTh + 0.0001f), 1.0f, 1.5f);
-                            ratio *= 0.7f;
-                            awayBias = Clamp(1.0f - (second * ratio), 0.0f, 1.0f);
-                        }
-                    }
-                }
-                if (AI().endApplyKeeperRushMs > m.actualTimeMs) awayBias = 1.0f;
-                float d = MaxF(toGoal.Length() - 0.5f, 0.0f);
-                awayOffset = Clamp(d * awayBias, awayOffset, kPitchHalfLength);
-                target = toGoal.pts[1] + (toGoal.pts[0] - toGoal.pts[1]).Normalized(0) * awayOffset;
-                float f = 0.0f;
-                float dl = toGoal.DistanceToPoint(Pos(), f);
-                if ((target - goal).Length() < (Pos() - goal).Length() && dl < 1.0f && f > 0.0f) maxVel = kWalkVelocity;
-                target.v[0] = Clamp(target.v[0], -kPitchHalfLength + 0.2f, kPitchHalfLength - 0.2f);
-            } else {
-                maxVel = kSprintVelocity;
-                Line toGoal;
-                toGoal.pts[0] = MentalBall(10).Get2D();
-                const float minGoalLine = 0.4f;
-                Vec3 over = Vec3(kPitchHalfLength * side, eliza->ballBoundForGoalY, 0);
-                over += (toGoal.pts[0] - over).Normalized(0) * minGoalLine;
-                toGoal.pts[1] = over;
-                float f = 0.0f;
-                toGoal.DistanceToPoint(Pos() + Mov() * 0.05f, f);
-                float f1 = 0.0f;
-                toGoal.DistanceToPoint(MentalBall(1010).Get2D(), f1);
-                bool runsToGoal = false;
-                if ((double)f1 > 1e-4) {
-                    float tr = f / f1;
-                    Vec3 atKeeper = MentalBall(TruncToInt32(10 + 1000 * tr));
-                    if ((double)atKeeper.v[2] > 2.5) runsToGoal = true;
-                }
-                f = Clamp(f, 0.0f, 1.0f);
-                if (runsToGoal) {
-                    target = over;
-                } else {
-                    target = toGoal.pts[0] + (toGoal.pts[1] - toGoal.pts[0]) * f;
-                    target.v[2] = 0.0f;
-                    target.v[0] = Clamp(target.v[0], -kPitchHalfLength + 0.2f, kPitchHalfLength - 0.2f);
-                }
-            }
+            target = eliza->ballBoundForGoal ? KeeperSave() : KeeperCover(ball, goal, maxVel);
         }
         dir = target - Pos();
         vel = Clamp(dir.Length() * kDistanceToVelocity, kIdleVelocity, maxVel);

@@ -383,99 +383,112 @@ struct AIBase {
         return (unsigned)bestTime;
     }
 
+    // Where a player moving by its input looks: turned from its direction toward the ball in
+    // 40 ms (half a metre ahead of it), fully when slow, 30% less (to the 0.5, then the 0.7) at a
+    // sprint.
+    HD Vec3 InputLook(const Vec3 &manualDir) const {
+        const float slow =
+            1.0f - libm::powf(NormalizedClamp(MinF(ctl.inputVelocityFloat, FloatVelocity()), kIdleDribbleSwitch, kSprintVelocity), 0.5f) *
+                       0.3f;
+        Vec3 focus = MentalBall(40).Get2D();
+        focus += Dir() * 0.5f;
+        const float toFocus = (focus - Pos()).Normalized(manualDir).Angle2D(manualDir);
+        return manualDir.Rotated2D(toFocus * libm::powf(slow, 0.7f));
+    }
+    // Whether the player goes for the ball: forced; the match's designated player; or the team's
+    // designated player with its team holding the ball (possession over 0.5 after a recent touch
+    // of its own or with the opponents off it, over 0.99, or its own best possession).
+    HD bool GoesForBall(bool forceMagnet) const {
+        const int teamDesignated = Own().designatedTeamPossessionPlayer;
+        const float poss = ctl.possessionAmount;
+        return forceMagnet || m.designatedPossessionPlayer == p ||
+               ((GetLastTouchBias(w, p, 2000) > 0.01f && poss > 0.5f) && teamDesignated == p) ||
+               ((!ctl.oppTeamHasPossession && poss > 0.5f) && teamDesignated == p) || (poss > 0.99f && teamDesignated == p) ||
+               (ctl.hasBestPossession && teamDesignated == p);
+    }
+    // How much a chase that is not the match's designated player's overrides the input: by a
+    // recent own touch (within 1.7 s of the ball, to the 0.4) and the chase's agreement with the
+    // input (to the 0.5); for a gamer's player with the opponents off the ball, at least the
+    // magnet of agreement or a recent switch, by possession and less toward the own half; all of
+    // it when forced.
+    HD float ChaseOverride(const Vec3 &chaseDir, const Vec3 &manualDir, float ownHalf, bool forceMagnet) const {
+        float agree = 1.0f - Clamp(fabsf(chaseDir.Angle2D(manualDir)) / PI, 0.0f, 1.0f);
+        agree = agree * 0.5f + 0.5f;
+        float bias = 0.0f;
+        if (GetLastTouchBias(w, p, 2000) > 0.01f && ps.timeToBallMs < 1700)
+            bias = libm::powf(GetLastTouchBias(w, p, 2000), 0.4f) * libm::powf(agree, 0.5f);
+        if (!ctl.oppTeamHasPossession && ps.base.externalController >= 0) {
+            float magnet = MaxF(Curve(agree, 0.8f), libm::powf(GetLastSwitchBias(w, ctl), 0.5f));
+            magnet *= 1.0f - ownHalf;
+            bias = Clamp(libm::powf((MaxF(ctl.possessionAmount, 0.5f) - 0.5f) * 2.0f, 0.5f) * magnet, bias, 1.0f);
+        }
+        if (forceMagnet) bias = 1.0f;
+        return bias;
+    }
+    // The team's designated player against an opponent on the ball: a gamer's player is pulled
+    // (30% of a recent switch, less toward the own half) toward shadowing the opponent (near it:
+    // its movement) or hunting it (further: a point 30% of the way from it to the goal).
+    HD float ShadowOpponent(float ownHalf, Vec3 &autoDir, float &autoVel, Vec3 &autoLook) const {
+        const int lookMs = 40;
+        const PlayerImage oi = MentalPlayerImage(w, k, ctl.opponentPlayer);
+        const Vec3 op = oi.position + oi.movement * 0.14f + oi.directionVector * 0.6f;
+        const Vec3 oppToGoal = (Vec3(kPitchHalfLength * side, 0, 0) - op).Normalized(0);
+        const float radius = 5.0f;
+        const Vec3 front = op + (oppToGoal * radius * 0.7f);
+        const float actionBias = 1.0f - Curve(NormalizedClamp((Pos() - front).Length(), 0.0f, radius), 0.7f);
+        float bias;
+        if (ExternalControllerActive(w, p)) bias = actionBias * 0.0f + GetLastSwitchBias(w, ctl) * 0.3f;
+        else bias = actionBias * 0.0f;
+        bias *= 1.0f - ownHalf;
+        if (!(bias > 0.0f)) return bias;
+        const float apart = (op - Pos()).Length();
+        const float shadow = libm::powf(1.0f - Curve(NormalizedClamp(apart, 0.0f, 7.0f), 0.7f), 1.2f);
+        const Vec3 shadowDir = oi.movement.Normalized(ctl.inputDirection);
+        const float shadowVel = VelocityFloat(oi.velocity);
+        const Vec3 shadowLook = (MentalBall(lookMs).Get2D() - Pos()).Normalized(0);
+        const Vec3 huntMov = (op + oppToGoal * apart * 0.3f) - Pos();
+        const Vec3 huntDir = huntMov.Normalized(ctl.inputDirection);
+        const float huntVel = Clamp(huntMov.Length() * kDistanceToVelocity, kIdleVelocity, kSprintVelocity);
+        const Vec3 huntLook = (MentalBall(lookMs).Get2D() - Pos()).Normalized(0);
+        autoDir = (shadowDir * shadow + huntDir * (1.0f - shadow)).Normalized(ctl.inputDirection);
+        autoVel = Clamp(shadowVel * shadow + huntVel * (1.0f - shadow), kIdleVelocity, kSprintVelocity);
+        autoLook = ((shadowLook * shadow + huntLook * (1.0f - shadow))).Normalized(0);
+        return bias;
+    }
+    // A movement command: the input (direction snapped to 8 directions with no bias, its speed)
+    // blended with an automatic movement by its override: the ball control or chase of a player
+    // going for the ball (a retainer keeps its input), or the shadowing of the opponent on the
+    // ball. Below the idle-dribble switch the player faces where it looks.
     HDN void MovementCommand(bool forceMagnet, bool extraHaste) {
         ENG_SCOPE(40);
-        const int lookMs = 40;
-        Vec3 qin = ctl.inputDirection;
-        QuantizeDirection(qin, kQuantizedDirectionBias);
+        Vec3 manualDir = ctl.inputDirection;
+        QuantizeDirection(manualDir, kQuantizedDirectionBias);
+        const float manualVel = ctl.inputVelocityFloat;
+        Vec3 autoDir = manualDir, autoLook = InputLook(manualDir);
+        float autoVel = manualVel, autoBias = 0.0f;
+        ps.desiredTimeToBallMs = 0;
+        const float ownHalf = NormalizedClamp(ctl.inputDirection.Dot(Vec3(side, 0, 0)), -1.0f, 1.0f);
+        if (m.ballRetainer == p) {
+            autoBias = 0.0f;
+        } else if (GoesForBall(forceMagnet)) {
+            Vec3 lookAt;
+            if (ctl.hasBestPossession) {
+                ps.desiredTimeToBallMs = (int)BallControlMovement(ctl.inputVelocityFloat, autoDir, autoVel, lookAt);
+            } else {
+                const float haste = (extraHaste || forceMagnet || ctl.possessionAmount < 1.1f) ? 1.0f : 0.0f;
+                ps.desiredTimeToBallMs = (int)ToBallMovement(manualDir, ctl.inputVelocityFloat, autoDir, autoVel, lookAt, haste);
+            }
+            autoLook = (lookAt - Pos()).Normalized(0);
+            autoBias = 1.0f;
+            if (!ctl.hasBestPossession && m.designatedPossessionPlayer != p) autoBias = ChaseOverride(autoDir, manualDir, ownHalf, forceMagnet);
+        } else if (w.playerTeamID[m.designatedPossessionPlayer] != teamID && Own().designatedTeamPossessionPlayer == p) {
+            autoBias = ShadowOpponent(ownHalf, autoDir, autoVel, autoLook);
+        }
+        const Vec3 res = (manualDir * manualVel) * (1.0f - autoBias) + (autoDir * autoVel) * autoBias;
         PlayerCommand cmd = DefaultPlayerCommand();
         cmd.useDesiredMovement = true;
         cmd.useDesiredLookAt = true;
-        Vec3 manualDir = qin;
-        float manualVel = ctl.inputVelocityFloat;
-        float dvf = 1.0f - libm::powf(NormalizedClamp(MinF(ctl.inputVelocityFloat, FloatVelocity()), kIdleDribbleSwitch,
-                                                      kSprintVelocity),
-                                      0.5f) *
-                               0.3f;
-        Vec3 focus = MentalBall(lookMs).Get2D();
-        focus += Dir() * 0.5f;
-        float toFocus = (focus - Pos()).Normalized(manualDir).Angle2D(manualDir);
-        Vec3 defaultLook = manualDir.Rotated2D(toFocus * libm::powf(dvf, 0.7f));
-        cmd.desiredDirection = manualDir;
-        cmd.desiredVelocityFloat = manualVel;
-        Vec3 autoDir = cmd.desiredDirection;
-        float autoVel = cmd.desiredVelocityFloat;
-        Vec3 autoLook = defaultLook;
-        const float adaptedPossession = ctl.possessionAmount;
-        ps.desiredTimeToBallMs = 0;
-        float autoBias = 0.0f;
-        float ownHalfFactor = NormalizedClamp(ctl.inputDirection.Dot(Vec3(side, 0, 0)), -1.0f, 1.0f);
-        const int teamDesignated = Own().designatedTeamPossessionPlayer;
-        const float poss = ctl.possessionAmount;
-        if (m.ballRetainer == p) {
-            autoBias = 0.0f;
-        } else if (forceMagnet || m.designatedPossessionPlayer == p ||
-                   ((GetLastTouchBias(w, p, 2000) > 0.01f && poss > 0.5f) && teamDesignated == p) ||
-                   ((!ctl.oppTeamHasPossession && poss > 0.5f) && teamDesignated == p) || (poss > 0.99f && teamDesignated == p) ||
-                   (ctl.hasBestPossession && teamDesignated == p)) {
-            if (ctl.hasBestPossession) {
-                Vec3 la;
-                ps.desiredTimeToBallMs = (int)BallControlMovement(ctl.inputVelocityFloat, autoDir, autoVel, la);
-                autoLook = (la - Pos()).Normalized(0);
-                autoBias = 1.0f;
-            } else {
-                float haste = 0.0f;
-                if (extraHaste || forceMagnet) haste = 1.0f;
-                else if (adaptedPossession < 1.1f) haste = 1.0f;
-                Vec3 la;
-                ps.desiredTimeToBallMs = (int)ToBallMovement(qin, ctl.inputVelocityFloat, autoDir, autoVel, la, haste);
-                autoLook = (la - Pos()).Normalized(0);
-                autoBias = 1.0f;
-                if (m.designatedPossessionPlayer != p) {
-                    float same = 1.0f - Clamp(fabsf(autoDir.Angle2D(manualDir)) / PI, 0.0f, 1.0f);
-                    same = same * 0.5f + 0.5f;
-                    autoBias = 0.0f;
-                    if (GetLastTouchBias(w, p, 2000) > 0.01f && ps.timeToBallMs < 1700)
-                        autoBias = libm::powf(GetLastTouchBias(w, p, 2000), 0.4f) * libm::powf(same, 0.5f);
-                    if (!ctl.oppTeamHasPossession && ps.base.externalController >= 0) {
-                        float sb = GetLastSwitchBias(w, ctl);
-                        float magnet = MaxF(Curve(same, 0.8f), libm::powf(sb, 0.5f));
-                        magnet *= 1.0f - ownHalfFactor;
-                        autoBias = Clamp(libm::powf((MaxF(poss, 0.5f) - 0.5f) * 2.0f, 0.5f) * magnet, autoBias, 1.0f);
-                    }
-                    if (forceMagnet) autoBias = 1.0f;
-                }
-            }
-        } else if (w.playerTeamID[m.designatedPossessionPlayer] != teamID && teamDesignated == p) {
-            PlayerImage oi = MentalPlayerImage(w, k, ctl.opponentPlayer);
-            Vec3 op = oi.position + oi.movement * 0.14f + oi.directionVector * 0.6f;
-            Vec3 oppToGoal = (Vec3(kPitchHalfLength * side, 0, 0) - op).Normalized(0);
-            const float radius = 5.0f;
-            Vec3 fp = op + (oppToGoal * radius * 0.7f);
-            float actionBias = 1.0f - Curve(NormalizedClamp((Pos() - fp).Length(), 0.0f, radius), 0.7f);
-            if (ExternalControllerActive(w, p)) autoBias = actionBias * 0.0f + GetLastSwitchBias(w, ctl) * 0.3f;
-            else autoBias = actionBias * 0.0f;
-            autoBias *= 1.0f - ownHalfFactor;
-            if (autoBias > 0.0f) {
-                float pod = (op - Pos()).Length();
-                float mmBias = libm::powf(1.0f - Curve(NormalizedClamp(pod, 0.0f, 7.0f), 0.7f), 1.2f);
-                Vec3 mmDir = oi.movement.Normalized(ctl.inputDirection);
-                float mmVel = VelocityFloat(oi.velocity);
-                Vec3 mmLook = (MentalBall(lookMs).Get2D() - Pos()).Normalized(0);
-                Vec3 hunt = op + oppToGoal * pod * 0.3f;
-                Vec3 huntMov = hunt - Pos();
-                Vec3 huntDir = huntMov.Normalized(ctl.inputDirection);
-                float huntVel = Clamp(huntMov.Length() * kDistanceToVelocity, kIdleVelocity, kSprintVelocity);
-                Vec3 huntLook = (MentalBall(lookMs).Get2D() - Pos()).Normalized(0);
-                autoDir = (mmDir * mmBias + huntDir * (1.0f - mmBias)).Normalized(ctl.inputDirection);
-                autoVel = Clamp(mmVel * mmBias + huntVel * (1.0f - mmBias), kIdleVelocity, kSprintVelocity);
-                autoLook = ((mmLook * mmBias + huntLook * (1.0f - mmBias))).Normalized(0);
-            }
-        }
-        Vec3 autoMov = autoDir * autoVel;
-        Vec3 manualMov = manualDir * manualVel;
-        Vec3 res = manualMov * (1.0f - autoBias) + autoMov * autoBias;
-        cmd.desiredDirection = res.Normalized(qin);
+        cmd.desiredDirection = res.Normalized(manualDir);
         cmd.desiredVelocityFloat = Clamp(res.Length(), kIdleVelocity, kSprintVelocity);
         if (cmd.desiredVelocityFloat < kIdleDribbleSwitch) cmd.desiredDirection = autoLook;
         cmd.desiredLookAt = Pos() + autoLook * 10.0f;

@@ -20,105 +20,128 @@ struct AIController : AIBase {
         return (t.forwardSpaceRating * fsw + t.spaceRating * sw + t.forwardRating * fw) / total;
     }
 
-    // Pass to the best-placed team mate, a panic clearance near the own goal, a shot when placed
-    // for one, and a dribble direction from a force field.
-    HDN void GetOnTheBallCommands(Vec3 &rawDir, float &rawVel) {
-        ENG_SCOPE(44);
-        float movDiff = NormalizedClamp((m.ball.momentum - Mov()).Length(), 0.0f, 10.0f);
-        float oneTouchIsHard = movDiff - Stat(kStatShortPass) * movDiff * 0.8f;
-        ImageList opps;
-        MentalTeamPlayerImages(w, k, oppID, opps);
-        float ptf = NormalizedClamp((float)ps.possessionDurationMs, 0, 5000);
-        float longPossession = ptf * ptf;
-        const float mind = GetMindSet(DynamicRole());
-        const float fsw = 0.4f, sw = 0.3f;
-        float fw = 2.0f + mind * 6.0f;
-        float totalTactical = fsw + sw + fw;
-        float improvement = 0.06f * (1.0f - mind);
-        float diffW = 1.0f + (mind * mind) * 10.0f;
-        const float passW = 1.0f;
-        float passMinimum = 0.2f * (1.0f - mind) - longPossession * 0.1f;
-        float totalPassW = diffW + passW;
-        float passThreshold = 0.1f - longPossession * 0.05f;
-        float rating = TacticalRating(ps, fsw, sw, fw, totalTactical);
-        PlayerList mates = TeamActivePlayers(w, teamID);
-        float bestTotal = 0.0f, bestPassRating = 0.0f;
-        int bestPlayer = -1, bestPassType = kFnShortPass;
+    // The weights of the tactical rating a player on the ball compares with its teammates':
+    // forward space 0.4, space 0.3 and forwardness 2 to 8 by the role's mindset.
+    struct PassWeights {
+        float forwardSpace, space, forward, total;
+    };
+    HD PassWeights PassWeightsOf(float mind) const {
+        PassWeights pw;
+        pw.forwardSpace = 0.4f;
+        pw.space = 0.3f;
+        pw.forward = 2.0f + mind * 6.0f;
+        pw.total = pw.forwardSpace + pw.space + pw.forward;
+        return pw;
+    }
+    // The teammate best worth a pass and the pass's type: one rated better than the passer (by 6%
+    // less the mindset's share; a goalkeeper at 70%), by the rating gain (weighted 1 to 11 by the
+    // mindset) and the best odds of a short, long or high pass, less how hard a one-touch pass is;
+    // above a threshold and minimum odds that fall as possession lasts. -1 for none.
+    HD int BestPassTarget(float mind, const ImageList &opps, float oneTouchIsHard, float longPossession, int &passType,
+                          float &passOdds) const {
+        const PassWeights pw = PassWeightsOf(mind);
+        const float improvement = 0.06f * (1.0f - mind);
+        const float gainWeight = 1.0f + (mind * mind) * 10.0f, oddsWeight = 1.0f;
+        const float minimum = 0.2f * (1.0f - mind) - longPossession * 0.1f;
+        const float threshold = 0.1f - longPossession * 0.05f;
+        const float own = TacticalRating(ps, pw.forwardSpace, pw.space, pw.forward, pw.total);
+        const PlayerList mates = TeamActivePlayers(w, teamID);
+        float bestTotal = 0.0f;
+        int best = -1;
+        passType = kFnShortPass;
+        passOdds = 0.0f;
         for (int i = 0; i < mates.count; i++) {
             const int mate = mates[i];
             if (mate == p) continue;
-            float mr = TacticalRating(m.players[mate], fsw, sw, fw, totalTactical);
-            if (StaticRole(mate) == kRoleGoalkeeper) mr *= 0.7f;
-            if (!(mr > rating + improvement)) continue;
-            float diff = mr - rating;
-            float oShort = PassingOddsTo(mate, kFnShortPass, opps);
-            float oLong = PassingOddsTo(mate, kFnLongPass, opps);
-            float oHigh = PassingOddsTo(mate, kFnHighPass, opps);
-            float pr;
-            int pt;
-            if (oShort >= oLong && oShort >= oHigh) {
-                pr = oShort;
-                pt = kFnShortPass;
-            } else if (oLong >= oHigh) {
-                pr = oLong;
-                pt = kFnLongPass;
-            } else {
-                pr = oHigh;
-                pt = kFnHighPass;
+            float rating = TacticalRating(m.players[mate], pw.forwardSpace, pw.space, pw.forward, pw.total);
+            if (StaticRole(mate) == kRoleGoalkeeper) rating *= 0.7f;
+            if (!(rating > own + improvement)) continue;
+            const float shortOdds = PassingOddsTo(mate, kFnShortPass, opps);
+            const float longOdds = PassingOddsTo(mate, kFnLongPass, opps);
+            const float highOdds = PassingOddsTo(mate, kFnHighPass, opps);
+            float odds = highOdds;
+            int type = kFnHighPass;
+            if (shortOdds >= longOdds && shortOdds >= highOdds) {
+                odds = shortOdds;
+                type = kFnShortPass;
+            } else if (longOdds >= highOdds) {
+                odds = longOdds;
+                type = kFnLongPass;
             }
-            float total = diff * diffW + pr * passW - oneTouchIsHard;
-            total /= totalPassW;
-            if (total > bestTotal && total > passThreshold && pr > passMinimum) {
+            float total = (rating - own) * gainWeight + odds * oddsWeight - oneTouchIsHard;
+            total /= gainWeight + oddsWeight;
+            if (total > bestTotal && total > threshold && odds > minimum) {
                 bestTotal = total;
-                bestPlayer = mate;
-                bestPassRating = pr;
-                bestPassType = pt;
+                best = mate;
+                passOdds = odds;
+                passType = type;
             }
         }
-        if (mind < 0.25f) {
-            float panic = 1.0f - mind * 2.0f;
-            float goalCloseness = 1.0f - NormalizedClamp((Pos() - Vec3(kPitchHalfLength * side, 0, 0)).Length(), 2.0f, 16.0f);
-            if (DynamicRole() != kRoleGoalkeeper) {
-                if ((bestPlayer < 0 || bestPassRating < panic * goalCloseness) &&
-                    ctl.possessionAmount < 0.9f + panic * goalCloseness * 0.8f)
-                    AddPanicPass();
-            } else if (ctl.possessionAmount < 3.0f) {
-                AddPanicPass();
-            }
+        return best;
+    }
+    // A defensive player (mindset below 0.25) near its own goal (2 to 16 m) clears in a panic when
+    // no pass is good enough for the danger and its possession is shaky; a goalkeeper clears when
+    // its possession is below 3.
+    HD void ConsiderClearance(float mind, int bestPlayer, float bestOdds) {
+        if (!(mind < 0.25f)) return;
+        const float panic = 1.0f - mind * 2.0f;
+        const float nearGoal = 1.0f - NormalizedClamp((Pos() - Vec3(kPitchHalfLength * side, 0, 0)).Length(), 2.0f, 16.0f);
+        if (DynamicRole() != kRoleGoalkeeper) {
+            if ((bestPlayer < 0 || bestOdds < panic * nearGoal) && ctl.possessionAmount < 0.9f + panic * nearGoal * 0.8f) AddPanicPass();
+        } else if (ctl.possessionAmount < 3.0f) {
+            AddPanicPass();
         }
-        if (bestPlayer >= 0) AddPass(bestPlayer, bestPassType);
-        float goalDistance = NormalizedClamp((Vec3(kPitchHalfLength * -side, 0, 0) - Pos()).Length(), 0.0f, 32.0f);
-        float ideal = 1.0f - NormalizedClamp((Vec3((kPitchHalfLength - 7.0f) * -side, 0, 0) - Pos()).Length(), 0.0f, 16.0f);
-        ideal = Curve(ideal, 1.0f);
-        if (ideal > 0.1f) {
-            const float gx = (kPitchHalfLength + 1.0f) * -side;
-            float low = PassingOdds(Vec3(gx, -3.6f, 0), kFnShot, opps, 3.0f);
-            float center = PassingOdds(Vec3(gx, 0.0f, 0), kFnShot, opps, 3.0f);
-            float high = PassingOdds(Vec3(gx, 3.6f, 0), kFnShot, opps, 3.0f);
-            float odds = center, y = 0.0f;
-            if (low > odds) {
-                odds = low;
-                y = -3.5f;
-            }
-            if (high > odds) {
-                odds = high;
-                y = 3.5f;
-            }
-            odds = libm::powf(odds, 0.5f);
-            if (odds + Random(0.0f, 0.5f) > 0.5f) {
-                PlayerCommand cmd = DefaultPlayerCommand();
-                cmd.desiredFunctionType = kFnShot;
-                cmd.desiredVelocityFloat = rawVel;
-                const float shot = Stat(kStatShot);
-                float ry = y + Random(-1.0f + shot, 1.0f - shot);
-                TouchInformation &t = cmd.touchInfo;
-                t.desiredDirection = (Vec3(gx, ry, 0) - (Pos() + Mov() * 0.2f)).Normalized(Vec3(-side, 0, 0));
-                t.desiredDirection = (t.desiredDirection * 0.7f + -Dir() * (FloatVelocity() / kSprintVelocity) * 0.3f).Normalized();
-                t.autoDirectionBias = 1.0f;
-                t.desiredPower = Random(0.7f * (0.6f + goalDistance * 0.4f), 1.0f * (0.6f + goalDistance * 0.4f));
-                q.push_back(cmd);
-            }
+    }
+    // Near the ideal shooting spot (7 m out, within 16 m) the player shoots at the best of the
+    // goal's centre and the posts' insides (odds to the 0.5) when they and a draw of up to 0.5
+    // pass 0.5: at that point, scattered by a draw (less with the shot statistic), leaning 30%
+    // against its running direction by speed, with a drawn power (stronger further out).
+    HD void ConsiderShot(const ImageList &opps, float rawVel) {
+        const float goalDistance = NormalizedClamp((Vec3(kPitchHalfLength * -side, 0, 0) - Pos()).Length(), 0.0f, 32.0f);
+        const float ideal = Curve(1.0f - NormalizedClamp((Vec3((kPitchHalfLength - 7.0f) * -side, 0, 0) - Pos()).Length(), 0.0f, 16.0f), 1.0f);
+        if (!(ideal > 0.1f)) return;
+        const float gx = (kPitchHalfLength + 1.0f) * -side;
+        const float low = PassingOdds(Vec3(gx, -3.6f, 0), kFnShot, opps, 3.0f);
+        const float center = PassingOdds(Vec3(gx, 0.0f, 0), kFnShot, opps, 3.0f);
+        const float high = PassingOdds(Vec3(gx, 3.6f, 0), kFnShot, opps, 3.0f);
+        float odds = center, y = 0.0f;
+        if (low > odds) {
+            odds = low;
+            y = -3.5f;
         }
+        if (high > odds) {
+            odds = high;
+            y = 3.5f;
+        }
+        if (!(libm::powf(odds, 0.5f) + Random(0.0f, 0.5f) > 0.5f)) return;
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnShot;
+        cmd.desiredVelocityFloat = rawVel;
+        const float shot = Stat(kStatShot);
+        const float aimY = y + Random(-1.0f + shot, 1.0f - shot);
+        TouchInformation &t = cmd.touchInfo;
+        t.desiredDirection = (Vec3(gx, aimY, 0) - (Pos() + Mov() * 0.2f)).Normalized(Vec3(-side, 0, 0));
+        t.desiredDirection = (t.desiredDirection * 0.7f + -Dir() * (FloatVelocity() / kSprintVelocity) * 0.3f).Normalized();
+        t.autoDirectionBias = 1.0f;
+        t.desiredPower = Random(0.7f * (0.6f + goalDistance * 0.4f), 1.0f * (0.6f + goalDistance * 0.4f));
+        q.push_back(cmd);
+    }
+    // The commands of a player on the ball: a panic clearance, a pass to the best-placed teammate,
+    // a shot, and a dribble direction from a force field.
+    HDN void GetOnTheBallCommands(Vec3 &rawDir, float &rawVel) {
+        ENG_SCOPE(44);
+        const float ballGap = NormalizedClamp((m.ball.momentum - Mov()).Length(), 0.0f, 10.0f);
+        const float oneTouchIsHard = ballGap - Stat(kStatShortPass) * ballGap * 0.8f;
+        ImageList opps;
+        MentalTeamPlayerImages(w, k, oppID, opps);
+        const float held = NormalizedClamp((float)ps.possessionDurationMs, 0, 5000);
+        const float mind = GetMindSet(DynamicRole());
+        int passType = kFnShortPass;
+        float passOdds = 0.0f;
+        const int target = BestPassTarget(mind, opps, oneTouchIsHard, held * held, passType, passOdds);
+        ConsiderClearance(mind, target, passOdds);
+        if (target >= 0) AddPass(target, passType);
+        ConsiderShot(opps, rawVel);
         BestDribbleMovement(rawDir, rawVel);
     }
 
@@ -258,6 +281,70 @@ struct AIController : AIBase {
         q.push_back(cmd);
     }
 
+    // The command out of open play, when there is one: celebrating after a goal, watching the
+    // referee show a card (from a second after play stopped until the restart is prepared), and,
+    // out of play or for a lazy player, drifting toward the centre (60% its own direction) at
+    // 95% of its speed less a draw of up to 3.2 m/s, looking at the ball. True when one was given.
+    HD bool StoppageCommand(bool lazy) {
+        const RefereeBuffer &rb = m.referee.buffer;
+        if (!m.inPlay && m.goalScored) {
+            AddCelebration();
+            return true;
+        }
+        const bool card = m.referee.foul.foulType == 2 || m.referee.foul.foulType == 3;
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.useDesiredMovement = true;
+        cmd.useDesiredLookAt = true;
+        if (!m.inPlay && rb.active && card && rb.stopTime < m.actualTimeMs - 1000 && rb.prepareTime > m.actualTimeMs) {
+            cmd.desiredDirection = Dir();
+            cmd.desiredVelocityFloat = kIdleVelocity;
+            cmd.desiredLookAt = m.officials[0].humanoid.spatial.position;
+            q.push_back(cmd);
+            return true;
+        }
+        if (m.inPlay && !lazy) return false;
+        cmd.desiredDirection = (Dir() * 0.6f + (Vec3(0) - Pos()).Normalized(Dir()) * 0.4f).Normalized(Dir());
+        cmd.desiredVelocityFloat = ClampVelocity(FloatVelocity() * 0.95f - Random(0.0f, 3.2f));
+        cmd.desiredLookAt = Pos() + (BallAt(0).Get2D() - Pos()).Normalized(cmd.desiredDirection) * 10.0f;
+        q.push_back(cmd);
+        return true;
+    }
+    // How a player off the ball presses the opponents' designated player: under team pressure, it
+    // faces its own goal and stands; else, with the opponents best placed, no man to mark and the
+    // opponent within the hunting distance (10 to 20 m by mindset, shorter when tired or for an
+    // easy team), the team's designated player (with possession over 0.8) goes for the ball in
+    // haste, and one of the two nearest to the opponent moves to its defending position when it
+    // is out of line.
+    HD void PressOpponent(bool &forceMagnet, bool &extraHaste) {
+        const int o = Opp().designatedTeamPossessionPlayer;
+        const float mind = GetMindSet(DynamicRole());
+        float hunt = 10.0f + (1.0f - mind) * 10.0f;
+        hunt *= 0.5f * ps.base.fatigueFactorInverse +
+                0.5f * (1.0f - NormalizedClamp(PlayerAverageVelocity(w, p, 10), kIdleVelocity, kSprintVelocity));
+        hunt *= 0.3f + TeamDifficulty(w, teamID) * 0.7f;
+        if (forceMagnet) {
+            ctl.inputDirection = Vec3(side * kPitchHalfLength, 0, 0) - Pos();
+            ctl.inputVelocityFloat = kIdleVelocity;
+            ctl.inputDirection.Normalize(Dir());
+            return;
+        }
+        if (!(!ctl.teamHasBestPossession && ps.manMarking < 0 && ((Pos(o) + Mov(o) * 0.12f) - (Pos() + Mov() * 0.04f)).Length() < hunt))
+            return;
+        if (p == Own().designatedTeamPossessionPlayer && ctl.possessionAmount > 0.8f) {
+            forceMagnet = true;
+            extraHaste = true;
+        }
+        const PlayerList nearest = GetClosestPlayers(w, c, teamID, Pos(o) + Mov(o) * 0.1f, false, 2);
+        bool near = false;
+        for (int i = 0; i < nearest.count && !near; i++) near = nearest[i] == p;
+        if (!near) return;
+        const Vec3 defend = GetDefendPosition(o);
+        if (!NeedDefendingMovement(side, Pos(), defend)) return;
+        ctl.inputDirection = (defend - Pos()).Normalized(ctl.inputDirection);
+        ctl.inputVelocityFloat = Clamp((defend - Pos()).Length() * kDistanceToVelocity, 0.0f, kSprintVelocity);
+        forceMagnet = true;
+    }
+
     HDN bool RequestCommand() {
         if (m.designatedPossessionPlayer < 0) return Fail("the AI controller finds no designated possession player");
         if (Own().designatedTeamPossessionPlayer < 0 || Opp().designatedTeamPossessionPlayer < 0)
@@ -277,33 +364,7 @@ struct AIController : AIBase {
         // GRF: laziness is fixed at creation from the player's own static entry.
         const bool lazy = c.sd->formation[p].lazy;
         const int role = StaticRole(p);
-        const RefereeBuffer &rb = m.referee.buffer;
-        if (!m.inPlay && m.goalScored) {
-            AddCelebration();
-            return true;
-        }
-        if (!m.inPlay && rb.active && (m.referee.foul.foulType == 2 || m.referee.foul.foulType == 3) &&
-            rb.stopTime < m.actualTimeMs - 1000 && rb.prepareTime > m.actualTimeMs) {
-            // Everyone watches the referee show the card.
-            PlayerCommand cmd = DefaultPlayerCommand();
-            cmd.useDesiredMovement = true;
-            cmd.useDesiredLookAt = true;
-            cmd.desiredDirection = Dir();
-            cmd.desiredVelocityFloat = kIdleVelocity;
-            cmd.desiredLookAt = m.officials[0].humanoid.spatial.position;
-            q.push_back(cmd);
-            return true;
-        }
-        if (!m.inPlay || lazy) {
-            PlayerCommand cmd = DefaultPlayerCommand();
-            cmd.useDesiredMovement = true;
-            cmd.desiredDirection = (Dir() * 0.6f + (Vec3(0) - Pos()).Normalized(Dir()) * 0.4f).Normalized(Dir());
-            cmd.desiredVelocityFloat = ClampVelocity(FloatVelocity() * 0.95f - Random(0.0f, 3.2f));
-            cmd.useDesiredLookAt = true;
-            cmd.desiredLookAt = Pos() + (BallAt(0).Get2D() - Pos()).Normalized(cmd.desiredDirection) * 10.0f;
-            q.push_back(cmd);
-            return true;
-        }
+        if (StoppageCommand(lazy)) return true;
         if ((m.inSetPiece && AI().taker == p) || m.ballRetainer == p) {
             SetPieceCommands();
             return true;
@@ -351,40 +412,7 @@ struct AIController : AIBase {
             SlidingCommand();
         }
         if (!manual && m.inPlay && !m.inSetPiece) {
-            const int o = Opp().designatedTeamPossessionPlayer;
-            if (p != m.designatedPossessionPlayer) {
-                float mind = GetMindSet(DynamicRole());
-                float hunt = 10.0f + (1.0f - mind) * 10.0f;
-                hunt *= 0.5f * ps.base.fatigueFactorInverse +
-                        0.5f * (1.0f - NormalizedClamp(PlayerAverageVelocity(w, p, 10), kIdleVelocity, kSprintVelocity));
-                hunt *= 0.3f + TeamDifficulty(w, teamID) * 0.7f;
-                if (forceMagnet) {
-                    ctl.inputDirection = Vec3(side * kPitchHalfLength, 0, 0) - Pos();
-                    ctl.inputVelocityFloat = kIdleVelocity;
-                    ctl.inputDirection.Normalize(Dir());
-                } else if (!ctl.teamHasBestPossession && ps.manMarking < 0 &&
-                           ((Pos(o) + Mov(o) * 0.12f) - (Pos() + Mov() * 0.04f)).Length() < hunt) {
-                    if (p == Own().designatedTeamPossessionPlayer && ctl.possessionAmount > 0.8f) {
-                        forceMagnet = true;
-                        extraHaste = true;
-                    }
-                    PlayerList closest = GetClosestPlayers(w, c, teamID, Pos(o) + Mov(o) * 0.1f, false, 2);
-                    bool close = false;
-                    for (int i = 0; i < closest.count; i++)
-                        if (closest[i] == p) {
-                            close = true;
-                            break;
-                        }
-                    if (close) {
-                        Vec3 dp = GetDefendPosition(o);
-                        if (NeedDefendingMovement(side, Pos(), dp)) {
-                            ctl.inputDirection = (dp - Pos()).Normalized(ctl.inputDirection);
-                            ctl.inputVelocityFloat = Clamp((dp - Pos()).Length() * kDistanceToVelocity, 0.0f, kSprintVelocity);
-                            forceMagnet = true;
-                        }
-                    }
-                }
-            }
+            if (p != m.designatedPossessionPlayer) PressOpponent(forceMagnet, extraHaste);
             ctl.inputVelocityFloat = RangeVelocity(ctl.inputVelocityFloat);
             MovementCommand(forceMagnet, extraHaste);
         } else {

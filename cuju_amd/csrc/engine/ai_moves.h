@@ -519,54 +519,68 @@ struct AIBase {
         return MinF(r, kSprintVelocity * breath);
     }
 
-    HDN Vec3 GetSupportPositionForceField(const Vec3 &base, bool makeRun) const {
-        ENG_SCOPE(41);
-        const int designated = Own().designatedTeamPossessionPlayer;
-        Vec3 cur = Pos() + Mov() * 0.1f;
-        Vec3 mainMan = Pos(designated) + Mov(designated) * 0.1f;
-        ForceField &ff = c.ws->forceField;
-        ff.clear();
-        float mind = GetMindSet(DynamicRole());
-        const bool forceNoOffside = true;
-        const float baseW = 0.7f, overall = 1.0f;
-        float oppRepelW = 0.3f * overall;
-        const float mateRepelW = 0.4f * overall, ballRepelW = 1.0f * overall, runW = 1.0f * overall,
-                    flockW = 0.45f * overall, webScale = 0.75f;
+    // ---- support positions: a force field around the formation place ----
+    // How strongly opponents push a supporting player away: 0.3, times 2.2 for full and centre
+    // backs, 2 for defensive midfielders, 1.6 for midfielders, 1.2 for attacking midfielders.
+    HD float OpponentRepelWeight() const {
+        float weight = 0.3f * 1.0f;
         switch (DynamicRole()) {
             case kRoleCentreBack:
             case kRoleLeftBack:
-            case kRoleRightBack: oppRepelW *= 2.2f; break;
-            case kRoleDefensiveMid: oppRepelW *= 2.0f; break;
+            case kRoleRightBack: weight *= 2.2f; break;
+            case kRoleDefensiveMid: weight *= 2.0f; break;
             case kRoleCentralMid:
             case kRoleLeftMid:
-            case kRoleRightMid: oppRepelW *= 1.6f; break;
-            case kRoleAttackingMid: oppRepelW *= 1.2f; break;
-            case kRoleCentreForward: oppRepelW *= 1.0f; break;
+            case kRoleRightMid: weight *= 1.6f; break;
+            case kRoleAttackingMid: weight *= 1.2f; break;
+            case kRoleCentreForward: weight *= 1.0f; break;
             default: break;
         }
-        float offsideX = GetOffsideLine(w, k, oppID, 240);
-        {
-            ForceSpot s;
-            s.origin = base;
-            if (p == AI().forwardSupportPlayer) {
-                s.origin.v[0] += -side * (0.3f + 0.7f * mind) * 12.0f;
-            } else {
-                float amount = 22.0f;
-                float laneY = -SignSide(mainMan.v[1]) * 8.0f;
-                amount *= Curve(1.0f - NormalizedClamp(fabsf(laneY - cur.v[1]), 0.0f, 30.0f), 1.0f);
-                s.origin.v[0] += -side * libm::powf(mind, 1.5f) * amount;
-            }
-            s.power = 1.0f * baseW;
-            s.power *= 0.3f + 0.7f * NormalizedClamp((s.origin - cur).Length(), 0.0f, 20.0f);
-            ff.push_back(s);
+        return weight;
+    }
+    // The anchor: the formation place moved upfield, 3.6 to 12 m by mindset for the forward
+    // support player, else up to 22 m (to the 1.5 of the mindset) the nearer the player is to
+    // the lane 8 m across from the carrier; pulling harder the further the player is from it.
+    HD ForceSpot SupportAnchor(const Vec3 &base, float mind, const Vec3 &cur, const Vec3 &carrier) const {
+        ForceSpot s;
+        s.origin = base;
+        if (p == AI().forwardSupportPlayer) {
+            s.origin.v[0] += -side * (0.3f + 0.7f * mind) * 12.0f;
+        } else {
+            float amount = 22.0f;
+            const float laneY = -SignSide(carrier.v[1]) * 8.0f;
+            amount *= Curve(1.0f - NormalizedClamp(fabsf(laneY - cur.v[1]), 0.0f, 30.0f), 1.0f);
+            s.origin.v[0] += -side * libm::powf(mind, 1.5f) * amount;
         }
-        if (makeRun) ff.push_back(MakeSpot(Vec3(-side * kPitchHalfLength, cur.v[1] * 0.5f, 0.0f), kAttract, kDecayConstant, 2.0f * runW));
+        s.power = 1.0f * 0.7f;
+        s.power *= 0.3f + 0.7f * NormalizedClamp((s.origin - cur).Length(), 0.0f, 20.0f);
+        return s;
+    }
+    // GRF's support position (the forces in GRF's order): the anchor; a run toward the opponents'
+    // goal line; the 3 opponents nearest a point near the carrier pushing away (from 2 m beyond
+    // them, away from the carrier; softer and wider on a run); with the ball well held, the 6
+    // nearest teammates; with it held better still, the ball's path 200 to 650 ms ahead; and for
+    // players other than the carrier, a flock ring around it (attract to 21 m, repel within 12 m).
+    // The result stays onside (8 cm) and on the pitch.
+    HDN Vec3 GetSupportPositionForceField(const Vec3 &base, bool makeRun) const {
+        ENG_SCOPE(41);
+        const int designated = Own().designatedTeamPossessionPlayer;
+        const Vec3 cur = Pos() + Mov() * 0.1f;
+        const Vec3 carrier = Pos(designated) + Mov(designated) * 0.1f;
+        const float mind = GetMindSet(DynamicRole());
+        const float opponentWeight = OpponentRepelWeight(), mateWeight = 0.4f * 1.0f, ballWeight = 1.0f * 1.0f,
+                    runWeight = 1.0f * 1.0f, flockWeight = 0.45f * 1.0f, webScale = 0.75f;
+        const float offsideX = GetOffsideLine(w, k, oppID, 240);
+        ForceField &ff = c.ws->forceField;
+        ff.clear();
+        ff.push_back(SupportAnchor(base, mind, cur, carrier));
+        if (makeRun) ff.push_back(MakeSpot(Vec3(-side * kPitchHalfLength, cur.v[1] * 0.5f, 0.0f), kAttract, kDecayConstant, 2.0f * runWeight));
         // GRF adds 0.7 to every coordinate of the focus here.
-        PlayerList opps = GetClosestPlayers(w, c, oppID, mainMan * 0.3f + cur + 0.7f, false, 3);
-        for (int i = 0; i < opps.count; i++) {
-            PlayerImage oi = MentalPlayerImage(w, k, opps[i]);
-            Vec3 op = oi.position + oi.movement * 0.1f;
-            ForceSpot s = MakeSpot(op + (op - mainMan).Normalized(0) * 2.0f, kRepel, kDecayVariable, 1.0f * oppRepelW, 5.0f, 0.7f);
+        const PlayerList opponents = GetClosestPlayers(w, c, oppID, carrier * 0.3f + cur + 0.7f, false, 3);
+        for (int i = 0; i < opponents.count; i++) {
+            const PlayerImage oi = MentalPlayerImage(w, k, opponents[i]);
+            const Vec3 at = oi.position + oi.movement * 0.1f;
+            ForceSpot s = MakeSpot(at + (at - carrier).Normalized(0) * 2.0f, kRepel, kDecayVariable, 1.0f * opponentWeight, 5.0f, 0.7f);
             if (makeRun) {
                 s.scale = 2.0f;
                 s.power *= 0.5f;
@@ -574,25 +588,25 @@ struct AIBase {
             ff.push_back(s);
         }
         if (Own().fadingTeamPossessionAmount >= 1.02f) {
-            PlayerList mates = GetClosestPlayers(w, c, teamID, cur, false, 6);
+            const PlayerList mates = GetClosestPlayers(w, c, teamID, cur, false, 6);
             for (int i = 0; i < mates.count; i++) {
                 if (mates[i] == p) continue;
-                PlayerImage mi = MentalPlayerImage(w, k, mates[i]);
-                ff.push_back(MakeSpot(mi.position + mi.movement * 0.1f, kRepel, kDecayVariable, 1.0f * mateRepelW, 14.0f * webScale, 1.0f));
+                const PlayerImage mi = MentalPlayerImage(w, k, mates[i]);
+                ff.push_back(MakeSpot(mi.position + mi.movement * 0.1f, kRepel, kDecayVariable, 1.0f * mateWeight, 14.0f * webScale, 1.0f));
             }
         }
         if (p != designated && Own().fadingTeamPossessionAmount >= 1.06f) {
             const int times[4] = {200, 350, 500, 650};
             for (int i = 0; i < 4; i++)
-                ff.push_back(MakeSpot(MentalBall(times[i]).Get2D(), kRepel, kDecayVariable, 1.0f * ballRepelW, 2.0f, 0.5f));
+                ff.push_back(MakeSpot(MentalBall(times[i]).Get2D(), kRepel, kDecayVariable, 1.0f * ballWeight, 2.0f, 0.5f));
         }
         if (p != designated) {
-            ff.push_back(MakeSpot(mainMan, kAttract, kDecayVariable, 1.0f * flockW, 28.0f * webScale, 1.0f));
-            ff.push_back(MakeSpot(mainMan, kRepel, kDecayVariable, 1.0f * flockW, 16.0f * webScale, 1.0f));
+            ff.push_back(MakeSpot(carrier, kAttract, kDecayVariable, 1.0f * flockWeight, 28.0f * webScale, 1.0f));
+            ff.push_back(MakeSpot(carrier, kRepel, kDecayVariable, 1.0f * flockWeight, 16.0f * webScale, 1.0f));
         }
         Vec3 r = cur + GetForceFieldMovement(ff, cur, 7);
         const float margin = 0.08f;
-        if (forceNoOffside && r.v[0] * -side > (offsideX * -side) - margin) r.v[0] = offsideX - (margin * -side);
+        if (r.v[0] * -side > (offsideX * -side) - margin) r.v[0] = offsideX - (margin * -side);
         r.v[0] = Clamp(r.v[0], -kPitchHalfLength, kPitchHalfLength);
         r.v[1] = Clamp(r.v[1], -kPitchHalfWidth, kPitchHalfWidth);
         return r;

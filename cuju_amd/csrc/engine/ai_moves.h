@@ -495,25 +495,29 @@ struct AIBase {
         q.push_back(cmd);
     }
 
-    // Slows players far from the action, by role, possession and recent running.
+    // How lazy a player is, 0 to 1: by its distance from the opponents' designated player (lazy
+    // from 20 m, fully at 65 m, both nearer when tired), half of it always and half by role (the
+    // mindset, inverted as the team holds the ball).
+    HD float Laziness() const {
+        const float fresh = ps.base.fatigueFactorInverse;
+        const float from = 20.0f * (fresh * 0.8f + 0.2f), to = 65.0f * (fresh * 0.5f + 0.5f);
+        const float away = (Pos() - Pos(Opp().designatedTeamPossessionPlayer)).Length();
+        const float holding = Clamp(ctl.fadingTeamPossessionAmount - 0.5f, 0.0f, 1.0f);
+        const float mind = GetMindSet(DynamicRole());
+        const float byRole = mind + holding * (1.0f - mind * 2.0f);
+        return NormalizedClamp(away, from, to) * (0.5f + byRole * 0.5f);
+    }
+    // GRF's lazy velocity: a desired speed beyond a sprint counts a tenth of the excess; a lazy
+    // player slows (not below dribbling when it asked for that) and, after running a lot in the
+    // last 10 s (less with work rate), stays below a share of a sprint.
     HDN float GetLazyVelocity(float desiredVel) const {
         float v = desiredVel;
         if (v > kSprintVelocity) v = kSprintVelocity + (v - kSprintVelocity) * 0.1f;
-        const float fi = ps.base.fatigueFactorInverse;
-        float startLazy = 20.0f * (fi * 0.8f + 0.2f);
-        float endLazy = 65.0f * (fi * 0.5f + 0.5f);
-        Vec3 op = Pos(Opp().designatedTeamPossessionPlayer);
-        float actionDistance = (Pos() - op).Length();
-        float teamPoss = Clamp(ctl.fadingTeamPossessionAmount - 0.5f, 0.0f, 1.0f);
-        float mind = GetMindSet(DynamicRole());
-        float byRole = mind + teamPoss * (1.0f - mind * 2.0f);
-        float byPosition = NormalizedClamp(actionDistance, startLazy, endLazy);
-        float lazy = byPosition * (0.5f + byRole * 0.5f);
+        const float lazy = Laziness();
         float r = v * (1.0f - lazy);
         if (desiredVel >= kDribbleVelocity && r < kDribbleVelocity) r = kDribbleVelocity;
         float breath = 1.0f - NormalizedClamp(PlayerAverageVelocity(w, p, 10), kIdleVelocity, kSprintVelocity);
-        float workRate = Stat(kStatWorkRate);
-        breath = libm::powf(breath, 0.8f - workRate * 0.2f);
+        breath = libm::powf(breath, 0.8f - Stat(kStatWorkRate) * 0.2f);
         breath = Clamp(breath * 1.2f, 0.0f, 1.0f);
         breath = breath * lazy + 1.0f * (1.0f - lazy);
         return MinF(r, kSprintVelocity * breath);

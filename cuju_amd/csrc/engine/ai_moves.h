@@ -616,35 +616,43 @@ struct AIBase {
         return r;
     }
 
+    // The field strategy of each line (defence, midfield, attack): how much of the static
+    // formation place a player far from the ball keeps, the range of fading possession over
+    // which it moves to support, above which share of support it may make a run, and the base of
+    // its defensive pull.
     enum StrategyKind { kDefense, kMidfield, kOffense };
+    struct LineStrategy {
+        float staticShare, attackLow, attackHigh, runThreshold, defensiveBase;
+    };
+    HD static LineStrategy LineStrategyOf(int kind) {
+        switch (kind) {
+            case kDefense: return {1.0f, 0.2f, 0.9f, 0.0f, 1.9f};
+            case kMidfield: return {0.9f, 0.1f, 0.7f, 0.9f, 1.5f};
+            default: return {0.8f, 0.1f, 0.6f, 0.7f, 1.3f};
+        }
+    }
+    // Where a player of a line goes: its static formation place blended into its dynamic one as
+    // the match's designated player comes within 15 to 20 m; moved toward its support position as
+    // the team holds the ball (a run when it is the team's runner); pulled to defend its man by
+    // the line's base less its mindset and the possession; inside the offside trap except for
+    // attackers. Its speed is the distance at the AI's distance-to-velocity rate, made lazy.
     HDN void FieldStrategyRequestInput(int kind, Vec3 &dir, float &vel) const {
-        const float staticFactor[3] = {1.0f, 0.9f, 0.8f};
-        const float attackLow[3] = {0.2f, 0.1f, 0.1f}, attackHigh[3] = {0.9f, 0.7f, 0.6f};
-        const float runThreshold[3] = {0.0f, 0.9f, 0.7f};
-        const float defensiveBase[3] = {1.9f, 1.5f, 1.3f};
+        const LineStrategy line = LineStrategyOf(kind);
         const FormationHistory history = FormationHistoryOf(w, p);
-        Vec3 st = TeamAdaptedFormationPosition(w, c, p, false, history);
-        Vec3 dy = TeamAdaptedFormationPosition(w, c, p, true, history);
-        float ad = NormalizedClamp(GetDistance(Pos(), Pos(m.designatedPossessionPlayer)), 15.0f, 20.0f);
-        float sb = Curve(staticFactor[kind] * ad, 1.0f);
-        Vec3 desired = st * sb + dy * (1.0f - sb);
-        {
-            float attackBias = NormalizedClamp((ctl.fadingTeamPossessionAmount - 0.5f) * 1.0f, attackLow[kind], attackHigh[kind]);
-            bool makeRun = kind != kDefense && attackBias > runThreshold[kind] &&
-                           AI().endApplyAttackingRunMs > m.actualTimeMs && AI().attackingRunPlayer == p;
-            Vec3 support = GetSupportPositionForceField(desired, makeRun);
-            desired = desired * (1.0f - attackBias) + support * attackBias;
-        }
-        {
-            float mind = GetMindSet(DynamicRole());
-            AddDefensiveComponent(desired,
-                                  libm::powf(Clamp(defensiveBase[kind] - mind - ctl.fadingTeamPossessionAmount, 0.0f, 1.0f), 0.7f));
-            if (kind != kOffense) TeamApplyOffsideTrap(w, teamID, desired);
-        }
+        const Vec3 fixed = TeamAdaptedFormationPosition(w, c, p, false, history);
+        const Vec3 dynamic = TeamAdaptedFormationPosition(w, c, p, true, history);
+        const float far = NormalizedClamp(GetDistance(Pos(), Pos(m.designatedPossessionPlayer)), 15.0f, 20.0f);
+        const float keep = Curve(line.staticShare * far, 1.0f);
+        Vec3 desired = fixed * keep + dynamic * (1.0f - keep);
+        const float attack = NormalizedClamp((ctl.fadingTeamPossessionAmount - 0.5f) * 1.0f, line.attackLow, line.attackHigh);
+        const bool run = kind != kDefense && attack > line.runThreshold && AI().endApplyAttackingRunMs > m.actualTimeMs &&
+                         AI().attackingRunPlayer == p;
+        desired = desired * (1.0f - attack) + GetSupportPositionForceField(desired, run) * attack;
+        const float mind = GetMindSet(DynamicRole());
+        AddDefensiveComponent(desired, libm::powf(Clamp(line.defensiveBase - mind - ctl.fadingTeamPossessionAmount, 0.0f, 1.0f), 0.7f));
+        if (kind != kOffense) TeamApplyOffsideTrap(w, teamID, desired);
         dir = (desired - Pos()).Normalized(Dir());
-        float v = (desired - Pos()).Length() * kDistanceToVelocity;
-        v = GetLazyVelocity(v);
-        vel = Clamp(v, 0, kSprintVelocity);
+        vel = Clamp(GetLazyVelocity((desired - Pos()).Length() * kDistanceToVelocity), 0, kSprintVelocity);
     }
 
     HDN void CalculateIfBallIsBoundForGoal() {

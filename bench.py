@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 # The reference world's size (sizeof(cuju::simulation::World), 11 players a side), read and written
 # once per environment step: the per-unit figure of the roofline, independent of this engine's own
-# layout (its World is 373,440 B).
+# layout (its World is 373,536 B).
 WORLD_BYTES = 373_552
 STEADY_WARMUP = 100
 HEADLINE = 3
@@ -61,6 +61,11 @@ MEASURED_TRAFFIC = {
     (3, 16384, 5, 20, 3): (182050013204, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
     (4, 8192, 5, 20, 3): (105271636700, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
     (5, 32768, 5, 20, 3): (176145907215, 'profiles/step_kernel_mixed_32768_driver_window.md'),
+    (1, 64, 100, 30, 3): (73175198, 'profiles/step_kernel_5v5_64.md'),
+    (2, 4096, 100, 30, 3): (62038437940, 'profiles/step_kernel_11v11_4096.md'),
+    (3, 16384, 100, 30, 3): (183560102391, 'profiles/step_kernel_11v11_hard_16384.md'),
+    (4, 8192, 100, 30, 3): (106199422724, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
+    (5, 32768, 100, 30, 3): (183738509781, 'profiles/step_kernel_mixed_32768.md'),
 }
 
 

@@ -131,37 +131,49 @@ struct AIBase {
         cmd.desiredLookAt = m.ballRetainer == p ? Pos() + ctl.inputDirection * 10.0f : BallAt(0).Get2D();
         q.push_back(cmd);
     }
+    // ---- touch commands: each a guard, then a command from the input ----
+    // The ball free and near (within the optimization threshold of where it will be in 200 ms).
+    HD bool BallFreeAndNear() const { return !(GetDistance(BallAt(200), Pos()) > kBallDistanceOptimizeThreshold) && m.ballRetainer < 0; }
+    // A command of `fn` along the input (snapped to 8 directions with no bias when `snap`), at the
+    // input's speed; an idle input turns to the opponents' goal on request.
+    HD PlayerCommand InputCommand(int fn, bool snap, bool idleTurnToGoal) const {
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = fn;
+        cmd.useDesiredMovement = true;
+        cmd.desiredDirection = ctl.inputDirection;
+        if (snap) QuantizeDirection(cmd.desiredDirection, kQuantizedDirectionBias);
+        cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
+        if (VelocityCat(cmd.desiredVelocityFloat) == kVelIdle && idleTurnToGoal) cmd.desiredDirection = Vec3(-side, 0, 0);
+        return cmd;
+    }
+    // Ball control: for the match's designated player, or the team's one likely enough (25%) to win
+    // the duel; off the ball and not in last ditch, only for a ball neither rising nor falling and
+    // not running faster than 15 m/s relative to the player. A sprinting dribbler's sticky run
+    // turns at most an eighth turn; a walking or dribbling player asked to dribble can keep its
+    // body direction, walking.
     HDN void BallControlCommand(bool idleTurnToGoal = false, bool knockOn = false, bool stickyRun = false,
                                 bool keepBodyDirection = false) {
-        if (GetDistance(BallAt(200), Pos()) > kBallDistanceOptimizeThreshold) return;
-        if (m.ballRetainer >= 0) return;
+        if (!BallFreeAndNear()) return;
         if (!ps.hasPossession && !AllowLastDitchOf(w, p)) {
             const float strictnessInverse = 3.0f;
             if (fabsf(m.ball.momentum.v[2]) > 5.0f * strictnessInverse) return;
             if ((m.ball.momentum.Get2D() - Mov()).Length() > 5.0f * strictnessInverse) return;
         }
-        if (!(m.designatedPossessionPlayer == p ||
-              (Own().designatedTeamPossessionPlayer == p && CouldWinABallDuelLikeliness() >= 0.25f)))
+        if (!(m.designatedPossessionPlayer == p || (Own().designatedTeamPossessionPlayer == p && CouldWinABallDuelLikeliness() >= 0.25f)))
             return;
-        PlayerCommand cmd = DefaultPlayerCommand();
-        cmd.desiredFunctionType = kFnBallControl;
-        cmd.useDesiredMovement = true;
-        cmd.desiredDirection = ctl.inputDirection;
-        QuantizeDirection(cmd.desiredDirection, kQuantizedDirectionBias);
-        cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
-        if (VelocityCat(cmd.desiredVelocityFloat) == kVelIdle && idleTurnToGoal) cmd.desiredDirection = Vec3(-side, 0, 0);
+        PlayerCommand cmd = InputCommand(kFnBallControl, true, idleTurnToGoal);
         if (knockOn) cmd.modifier |= kModifierKnockOn;
-        if (ctl.hasPossession && ctl.hasBestPossession && cmd.desiredVelocityFloat > kWalkSprintSwitch &&
-            FloatVelocity() > kDribbleWalkSwitch && stickyRun) {
-            float a = cmd.desiredDirection.Angle2D(Dir());
-            if (fabsf(a) > 0.125f * PI && fabsf(a) < 0.7f * PI) {
-                if (a > 0) cmd.desiredDirection = Dir().Rotated2D(0.125f * PI);
-                if (a < 0) cmd.desiredDirection = Dir().Rotated2D(0.125f * -PI);
+        if (stickyRun && ctl.hasPossession && ctl.hasBestPossession && cmd.desiredVelocityFloat > kWalkSprintSwitch &&
+            FloatVelocity() > kDribbleWalkSwitch) {
+            const float turn = cmd.desiredDirection.Angle2D(Dir());
+            if (fabsf(turn) > 0.125f * PI && fabsf(turn) < 0.7f * PI) {
+                if (turn > 0) cmd.desiredDirection = Dir().Rotated2D(0.125f * PI);
+                if (turn < 0) cmd.desiredDirection = Dir().Rotated2D(0.125f * -PI);
             }
         }
         cmd.useDesiredLookAt = true;
-        const int vc = Sp(w, p).velocityCat;
-        if (keepBodyDirection && (vc == kVelWalk || vc == kVelDribble) && VelocityCat(cmd.desiredVelocityFloat) == kVelDribble) {
+        const int moving = Sp(w, p).velocityCat;
+        if (keepBodyDirection && (moving == kVelWalk || moving == kVelDribble) && VelocityCat(cmd.desiredVelocityFloat) == kVelDribble) {
             cmd.desiredVelocityFloat = kWalkVelocity;
             cmd.desiredLookAt = Pos() + Dir() * 10.0f;
         } else {
@@ -169,21 +181,17 @@ struct AIBase {
         }
         q.push_back(cmd);
     }
+    // A trap of a ball moving at least 2 m/s that the player does not hold: for the match's
+    // designated player, or the team's one that reaches the ball within a second while the
+    // opponents need 400 ms more, do not hold it and are half likely to lose the duel. An AI
+    // goalkeeper traps facing upfield, standing.
     HDN void TrapCommand(bool idleTurnToGoal = false, bool knockOn = false) {
-        if (m.ball.momentum.Get2D().Length() < 2.0f) return;
-        if (GetDistance(BallAt(200), Pos()) > kBallDistanceOptimizeThreshold) return;
-        if (m.ballRetainer >= 0) return;
-        if (ctl.hasPossession) return;
+        if (m.ball.momentum.Get2D().Length() < 2.0f || !BallFreeAndNear() || ctl.hasPossession) return;
         if (!(m.designatedPossessionPlayer == p ||
-              (Own().designatedTeamPossessionPlayer == p && ps.timeToBallOptimisticMs < 1000 &&
-               ctl.oppTimeNeededToGetToBall > 400 && !ctl.oppTeamHasPossession && CouldWinABallDuelLikeliness() >= 0.5f)))
+              (Own().designatedTeamPossessionPlayer == p && ps.timeToBallOptimisticMs < 1000 && ctl.oppTimeNeededToGetToBall > 400 &&
+               !ctl.oppTeamHasPossession && CouldWinABallDuelLikeliness() >= 0.5f)))
             return;
-        PlayerCommand cmd = DefaultPlayerCommand();
-        cmd.desiredFunctionType = kFnTrap;
-        cmd.useDesiredMovement = true;
-        cmd.desiredDirection = ctl.inputDirection;
-        QuantizeDirection(cmd.desiredDirection, kQuantizedDirectionBias);
-        cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
+        PlayerCommand cmd = InputCommand(kFnTrap, true, false);
         if (StaticRole(p) == kRoleGoalkeeper && !ExternalControllerActive(w, p)) {
             cmd.desiredDirection = Vec3(-side, 0, 0);
             cmd.desiredVelocityFloat = kIdleVelocity;
@@ -194,42 +202,40 @@ struct AIBase {
         cmd.desiredLookAt = Pos() + Mov() * 0.3f + cmd.desiredDirection * 10.0f;
         q.push_back(cmd);
     }
+    // Interference when the team is not best placed: by any means (loosely), or strictly when at
+    // least 20% likely to win the duel.
     HDN void InterfereCommand(bool byAnyMeans) {
-        if (GetDistance(BallAt(200), Pos()) > kBallDistanceOptimizeThreshold) return;
-        if (m.ballRetainer >= 0) return;
-        if (ctl.teamHasBestPossession) return;
+        if (!BallFreeAndNear() || ctl.teamHasBestPossession) return;
         if (!byAnyMeans && CouldWinABallDuelLikeliness() < 0.2f) return;
-        PlayerCommand cmd = DefaultPlayerCommand();
-        cmd.desiredFunctionType = kFnInterfere;
-        cmd.useDesiredMovement = true;
+        PlayerCommand cmd = InputCommand(kFnInterfere, false, false);
         cmd.strictMovement = byAnyMeans ? kStrictFalse : kStrictTrue;
-        cmd.desiredDirection = ctl.inputDirection;
-        cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
         q.push_back(cmd);
     }
+    // A sliding tackle, only without gamers in the team: the opponents hold the ball, the team is
+    // badly placed (possession under 0.6) and the player, not the designated one, 70% likely to
+    // win the duel, with the ball 0.7 to 1.6 m from where it will be in 200 ms (the opponents
+    // needing more than 260 ms to it), or 0.6 to 1.8 m from it while their player winds up a shot.
+    // It sprints at the ball, led by the opponent's movement.
     HDN void SlidingCommand() {
-        if (HumanGamerCount(Own()) != 0) return;
-        if (m.ballRetainer >= 0) return;
-        if (CouldWinABallDuelLikeliness() < 0.7f) return;
-        if (!(!ctl.teamHasBestPossession && ctl.possessionAmount < 0.6f && m.designatedPossessionPlayer != p &&
-              ctl.oppTeamHasPossession))
+        if (HumanGamerCount(Own()) != 0 || m.ballRetainer >= 0 || CouldWinABallDuelLikeliness() < 0.7f) return;
+        if (!(!ctl.teamHasBestPossession && ctl.possessionAmount < 0.6f && m.designatedPossessionPlayer != p && ctl.oppTeamHasPossession))
             return;
         const int o = ctl.opponentPlayer;
-        Vec3 bp = MentalBallPrediction(w, MentalImageIndex(w, 20), 200);
-        Vec3 pp = Pos() + Mov() * (float)0.2;
-        float bd = (pp - bp).Length();
+        const Vec3 ball = MentalBallPrediction(w, MentalImageIndex(w, 20), 200);
+        const Vec3 ahead = Pos() + Mov() * (float)0.2;
+        const float gap = (ahead - ball).Length();
         const AnimationState &oa = Hum(w, o).anim;
-        if ((bd > 0.7f && bd < 1.6f && ctl.oppTimeNeededToGetToBall > 260) ||
-            (bd > 0.6f && bd < 1.8f && oa.functionType == kFnShot && oa.frameNum < oa.touchFrame)) {
-            PlayerCommand cmd = DefaultPlayerCommand();
-            cmd.desiredFunctionType = kFnSliding;
-            cmd.useDesiredMovement = true;
-            cmd.desiredDirection = ((bp.Get2D() + Mov(o) * 0.2f) - pp).Normalized(Vec3(-side, 0, 0));
-            cmd.desiredVelocityFloat = kSprintVelocity;
-            cmd.useDesiredLookAt = true;
-            cmd.desiredLookAt = Pos() + Mov() * 0.1f + cmd.desiredDirection * 10.0f;
-            q.push_back(cmd);
-        }
+        const bool loose = gap > 0.7f && gap < 1.6f && ctl.oppTimeNeededToGetToBall > 260;
+        const bool shooting = gap > 0.6f && gap < 1.8f && oa.functionType == kFnShot && oa.frameNum < oa.touchFrame;
+        if (!(loose || shooting)) return;
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnSliding;
+        cmd.useDesiredMovement = true;
+        cmd.desiredDirection = ((ball.Get2D() + Mov(o) * 0.2f) - ahead).Normalized(Vec3(-side, 0, 0));
+        cmd.desiredVelocityFloat = kSprintVelocity;
+        cmd.useDesiredLookAt = true;
+        cmd.desiredLookAt = Pos() + Mov() * 0.1f + cmd.desiredDirection * 10.0f;
+        q.push_back(cmd);
     }
 
     // ---- movement towards the ball ----

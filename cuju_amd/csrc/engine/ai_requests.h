@@ -145,66 +145,145 @@ struct AIController : AIBase {
         BestDribbleMovement(rawDir, rawVel);
     }
 
-    HDN void AddCelebration() {
-        int xSide = (BallAt(0).Get2D().v[0] > 0) ? 1 : -1;
-        int ySide = side;
-        const int ltp = Own().lastTouchPlayer;
-        if (ltp >= 0) ySide = (Pos(ltp).v[1] > 0) ? 1 : -1;
-        Vec3 cp = Vec3(kPitchHalfLength * xSide, kPitchHalfWidth * ySide, 0);
-        Vec3 dd = (cp - Pos()).Normalized();
-        float dv = ClampVelocity((cp - Pos()).Length() / 4.0f);
-        Vec3 look = Pos() + Dir() * 1000;
-        int type = 1;
+    // ---- celebrations ----
+    // After a goal the scoring team runs to the corner on the ball's end and the scorer's flank
+    // (a quarter of the distance per second), the scorer sprinting, teammates within 20 m
+    // joining the scorer (half the distance per second) and looking its way; the conceding team
+    // stands (type 2). Two to four seconds after play stopped each plays its celebration.
+    struct Celebration {
+        Vec3 dir, look;
+        float vel;
+        int type, scorer;  // type 1 scored, 2 conceded; scorer 2 for the scorer itself
+    };
+    HD Celebration CelebrationOf() const {
+        const int xSide = (BallAt(0).Get2D().v[0] > 0) ? 1 : -1;
+        const int last = Own().lastTouchPlayer;
+        const int ySide = last >= 0 ? ((Pos(last).v[1] > 0) ? 1 : -1) : side;
+        const Vec3 corner = Vec3(kPitchHalfLength * xSide, kPitchHalfWidth * ySide, 0);
+        Celebration c{(corner - Pos()).Normalized(), Pos() + Dir() * 1000, ClampVelocity((corner - Pos()).Length() / 4.0f), 1, 1};
         if (m.lastGoalTeam != TeamSlot(w, teamID)) {
-            type = 2;
-            dv = kIdleVelocity;
+            c.type = 2;
+            c.vel = kIdleVelocity;
+            return c;
         }
-        int madeGoal = 1;
-        if (type == 1) {
-            if (ltp == p) {
-                madeGoal = 2;
-                dv = kSprintVelocity;
-            } else if (ltp >= 0) {
-                if ((Pos(ltp) - Pos()).Length() < 20) {
-                    cp = Pos(ltp);
-                    dd = ((Pos(ltp) * 0.5f + cp * 0.5f) - Pos()).Normalized();
-                    dv = ClampVelocity((float)((double)(Pos(ltp) - Pos()).Length() / 2.0));
-                } else {
-                    dv = kIdleVelocity;
-                }
-                look = Pos() + Dir(ltp) * 100;
+        if (last == p) {
+            c.scorer = 2;
+            c.vel = kSprintVelocity;
+        } else if (last >= 0) {
+            const Vec3 at = Pos(last);
+            if ((at - Pos()).Length() < 20) {
+                c.dir = ((at * 0.5f + at * 0.5f) - Pos()).Normalized();
+                c.vel = ClampVelocity((float)((double)(at - Pos()).Length() / 2.0));
+            } else {
+                c.vel = kIdleVelocity;
             }
+            c.look = Pos() + Dir(last) * 100;
         }
+        return c;
+    }
+    HDN void AddCelebration() {
+        const Celebration c = CelebrationOf();
         const uint64_t stop = m.referee.buffer.stopTime;
         if (m.actualTimeMs - stop > 2000 && m.actualTimeMs - stop < 4000) {
             PlayerCommand cmd = DefaultPlayerCommand();
             cmd.desiredFunctionType = kFnSpecial;
             cmd.useSpecialVar1 = true;
-            cmd.specialVar1 = type;
+            cmd.specialVar1 = c.type;
             cmd.useSpecialVar2 = true;
-            cmd.specialVar2 = madeGoal;
+            cmd.specialVar2 = c.scorer;
             q.push_back(cmd);
         }
         PlayerCommand cmd = DefaultPlayerCommand();
         cmd.useDesiredMovement = true;
-        cmd.desiredDirection = dd;
-        cmd.desiredVelocityFloat = dv;
+        cmd.desiredDirection = c.dir;
+        cmd.desiredVelocityFloat = c.vel;
         cmd.useDesiredLookAt = true;
-        cmd.desiredLookAt = look;
+        cmd.desiredLookAt = c.look;
         q.push_back(cmd);
     }
 
+    // ---- restarts ----
+    // The penalty taker shoots at a drawn point up to 5 m from the goal's centre with a drawn
+    // power. Returns the shot's direction.
+    HD Vec3 PenaltyShot() {
+        PlayerCommand action = DefaultPlayerCommand();
+        action.desiredFunctionType = kFnShot;
+        TouchInformation &t = action.touchInfo;
+        const float y = Random(-5, 5);
+        t.desiredDirection = (Vec3(-side * kPitchHalfLength, y, 0) - Pos()).Normalized(Vec3(-side, 0, 0));
+        t.desiredPower = Random(0.4f, 1.0f);
+        q.push_back(action);
+        return t.desiredDirection;
+    }
+    // Where a restart's pass goes, by draws: a goal kick, 60% of the time without gamers, lofted
+    // 20% upfield across the pitch, else short to the taker's x; a kick-off a metre ahead; a free
+    // kick, half the time, lofted into the box, else 10 m upfield; a corner, 70% of the time,
+    // lofted to the far post area (1% to 13% out, GRF's draws y first), else to 80% upfield; a
+    // throw-in at the taker; a goalkeeper holding the ball lofts it upfield to a teammate who has
+    // 10 m of space (or after 4 s), or waits. Returns false when the keeper waits.
+    HD bool RestartPassTarget(int type, PlayerCommand &action, Vec3 &target) {
+        TouchInformation &t = action.touchInfo;
+        switch (type) {
+            case kModeGoalKick:
+                if (Random(0.0f, 1.0f) > 0.4f && HumanGamerCount(Own()) == 0) {
+                    action.desiredFunctionType = kFnHighPass;
+                    target = Vec3((kPitchHalfLength * -side) * 0.2f, Random(-kPitchHalfWidth, kPitchHalfWidth), 0.0f);
+                } else {
+                    target = Vec3(Pos().v[0] * 0.9f, Random(-kPitchHalfWidth, kPitchHalfWidth), 0.0f);
+                }
+                return true;
+            case kModeKickOff:
+                target = Pos() + Dir() * 1.0f;
+                return true;
+            case kModeFreeKick:
+                if (Random(0.0f, 1.0f) > 0.5f) {
+                    action.desiredFunctionType = kFnHighPass;
+                    target = Vec3(kPitchHalfLength * -side, Random(-10.0f, 10.0f), 0.0f);
+                } else {
+                    const float y = Random(-10.0f, 10.0f);
+                    target = Pos() + Vec3(-side * 10.0f, y, 0.0f);
+                }
+                return true;
+            case kModeCorner:
+                if (Random(0.0f, 1.0f) > 0.3f) {
+                    action.desiredFunctionType = kFnHighPass;
+                    const float y = Random(-10.0f, 10.0f);
+                    const float x = Random(0.0f, 0.12f);
+                    target = Vec3((kPitchHalfLength * -side) * (0.99f - x), y, 0.0f);
+                } else {
+                    target = Vec3((kPitchHalfLength * -side) * 0.8f, Pos().v[1] * 0.8f, 0.0f);
+                }
+                return true;
+            case kModeThrowIn:
+                target = Pos();
+                return true;
+            default:
+                break;
+        }
+        if (m.ballRetainer != p) return true;
+        action.desiredFunctionType = kFnHighPass;
+        target = Vec3(kPitchHalfLength * side, Random(-kPitchHalfWidth, kPitchHalfWidth), 0.0f);
+        const int mate = GetClosestPlayer(w, c, teamID, target, false, p);
+        if (mate < 0) return true;
+        const int marker = GetClosestPlayer(w, c, oppID, Pos(mate), false, -1);
+        if (marker < 0) return true;
+        if (((Pos(marker) + Mov(marker) * 0.1f) - Pos(mate)).Length() > 10.0f || ps.possessionDurationMs > 4000) {
+            t.forcedTargetPlayer = mate;
+            return true;
+        }
+        return false;
+    }
+    // The commands of a set piece's taker (or the ball's retainer): the restart's shot or pass to
+    // the teammate nearest its target, then a movement: toward the ball at walking pace, or, for
+    // the retainer, facing its pass (or the centre) standing.
     HDN void SetPieceCommands() {
         const int type = AI().setPieceType;
-        PlayerCommand action = DefaultPlayerCommand();
-        TouchInformation &t = action.touchInfo;
+        Vec3 passDir;
         if (type == kModePenalty) {
-            action.desiredFunctionType = kFnShot;
-            float ry = Random(-5, 5);
-            t.desiredDirection = (Vec3(-side * kPitchHalfLength, ry, 0) - Pos()).Normalized(Vec3(-side, 0, 0));
-            t.desiredPower = Random(0.4f, 1.0f);
-            q.push_back(action);
+            passDir = PenaltyShot();
         } else {
+            PlayerCommand action = DefaultPlayerCommand();
+            TouchInformation &t = action.touchInfo;
             action.desiredFunctionType = kFnShortPass;
             t.inputDirection = Dir();
             t.inputPower = 0.5f;
@@ -212,60 +291,13 @@ struct AIController : AIBase {
             t.autoPowerBias = 1.0f;
             t.forcedTargetPlayer = -1;
             Vec3 target;
-            bool doCommand = true;
-            if (type == kModeGoalKick) {
-                if (Random(0.0f, 1.0f) > 0.4f && HumanGamerCount(Own()) == 0) {
-                    action.desiredFunctionType = kFnHighPass;
-                    float ry = Random(-kPitchHalfWidth, kPitchHalfWidth);
-                    target = Vec3((kPitchHalfLength * -side) * 0.2f, ry, 0.0f);
-                } else {
-                    float ry = Random(-kPitchHalfWidth, kPitchHalfWidth);
-                    target = Vec3(Pos().v[0] * 0.9f, ry, 0.0f);
-                }
-            } else if (type == kModeKickOff) {
-                target = Pos() + Dir() * 1.0f;
-            } else if (type == kModeFreeKick) {
-                if (Random(0.0f, 1.0f) > 0.5f) {
-                    action.desiredFunctionType = kFnHighPass;
-                    float ry = Random(-10.0f, 10.0f);
-                    target = Vec3(kPitchHalfLength * -side, ry, 0.0f);
-                } else {
-                    float ry = Random(-10.0f, 10.0f);
-                    target = Pos() + Vec3(-side * 10.0f, ry, 0.0f);
-                }
-            } else if (type == kModeCorner) {
-                if (Random(0.0f, 1.0f) > 0.3f) {
-                    action.desiredFunctionType = kFnHighPass;
-                    // GRF: arguments evaluate right to left, so y draws first.
-                    float ry = Random(-10.0f, 10.0f);
-                    float rx = Random(0.0f, 0.12f);
-                    target = Vec3((kPitchHalfLength * -side) * (0.99f - rx), ry, 0.0f);
-                } else {
-                    target = Vec3((kPitchHalfLength * -side) * 0.8f, Pos().v[1] * 0.8f, 0.0f);
-                }
-            } else if (type == kModeThrowIn) {
-                target = Pos();
-            } else if (m.ballRetainer == p) {
-                action.desiredFunctionType = kFnHighPass;
-                float ry = Random(-kPitchHalfWidth, kPitchHalfWidth);
-                target = Vec3(kPitchHalfLength * side, ry, 0.0f);
-                int tp = GetClosestPlayer(w, c, teamID, target, false, p);
-                if (tp >= 0) {
-                    int co = GetClosestPlayer(w, c, oppID, Pos(tp), false, -1);
-                    if (co >= 0) {
-                        if (((Pos(co) + Mov(co) * 0.1f) - Pos(tp)).Length() > 10.0f || ps.possessionDurationMs > 4000)
-                            t.forcedTargetPlayer = tp;
-                        else
-                            doCommand = false;
-                    }
-                }
-            }
-            if (doCommand) {
+            if (RestartPassTarget(type, action, target)) {
                 if (t.forcedTargetPlayer < 0) t.forcedTargetPlayer = GetClosestPlayer(w, c, teamID, target, false, p);
                 AimPass(w, p, action.desiredFunctionType, t.inputDirection, t.inputPower, t.autoDirectionBias, t.autoPowerBias,
                         t.desiredDirection, t.desiredPower, t.targetPlayer, t.forcedTargetPlayer);
                 q.push_back(action);
             }
+            passDir = t.desiredDirection;
         }
         PlayerCommand cmd = DefaultPlayerCommand();
         cmd.useDesiredMovement = true;
@@ -273,8 +305,7 @@ struct AIController : AIBase {
         if (m.ballRetainer != p) {
             BallControlMovement(kWalkVelocity, cmd.desiredDirection, cmd.desiredVelocityFloat, cmd.desiredLookAt);
         } else {
-            cmd.desiredDirection = (t.desiredDirection.Length() > 0.0f) ? t.desiredDirection.Get2D().Normalized(Dir())
-                                                                       : (Vec3(0) - Pos()).Normalized(Dir());
+            cmd.desiredDirection = (passDir.Length() > 0.0f) ? passDir.Get2D().Normalized(Dir()) : (Vec3(0) - Pos()).Normalized(Dir());
             cmd.desiredVelocityFloat = kIdleVelocity;
             cmd.desiredLookAt = Pos() + cmd.desiredDirection * 10.0f;
         }

@@ -471,8 +471,141 @@ HDN void TeamApplyTeamPressure(World &w, const Ctx &c, int teamID) {
 }
 HD void TeamApplyKeeperRush(World &w, int teamID) { TeamByID(w, teamID).ai.endApplyKeeperRushMs = w.match.actualTimeMs + 300; }
 
-// The commands of a gamer's player: the armed action, then ball control, trap, interference and a
-// movement that follows the stick (steady direction) with the default gameplay settings.
+// ---- a gamer's player ------------------------------------------------------------------------------
+// A gamer's armed action expires: a pass or shot once its touch has happened, when the shot or
+// high-pass gauge is overridden by the short-pass button outside set pieces, after 2 s without
+// release, when the player's time to the ball grows by 700 ms, or in an interference; a defensive
+// action once its tackle has happened or after a second.
+HD void ExpireGamerAction(const MatchState &m, const Player &ps, const AnimationState &cur, HumanControllerState &hc) {
+    const bool *b = hc.keyboard.buttons;
+    const int fn = cur.functionType;
+    const bool touched = !(cur.frameNum < cur.touchFrame);
+    bool expired = false;
+    if (hc.actionMode == 2) {
+        expired = (IsPassOrShot(fn) && touched) ||
+                  (!m.inSetPiece && b[kBtnShortPass] && (hc.actionButton == kBtnShot || hc.actionButton == kBtnHighPass)) ||
+                  (!m.inSetPiece && (hc.actionBufferTimeMs > 2000 || ps.timeToBallMs > ps.timeToBallPreviousMs + 700 || fn == kFnInterfere));
+    } else if (hc.actionMode == 1) {
+        expired = ((fn == kFnSliding || fn == kFnInterfere) && touched) || hc.actionBufferTimeMs > 1000;
+    }
+    if (!expired) return;
+    hc.actionMode = 0;
+    hc.gaugeMs = 0;
+    hc.actionBufferTimeMs = 0;
+}
+// A pass of a gamer's: the stick's direction at a power from the gauge (to the pass type's
+// exponent) with the default gameplay settings' auto biases.
+HD void GamerPass(World &w, int p, const PlayerControllerState &ctl, int type, float gauge, CommandQueue &q) {
+    const float exponent = type == kFnShortPass ? 0.7f : type == kFnLongPass ? 0.65f : 0.55f;
+    PlayerCommand cmd = DefaultPlayerCommand();
+    cmd.desiredFunctionType = type;
+    TouchInformation &ti = cmd.touchInfo;
+    ti.inputDirection = ctl.inputDirection;
+    ti.inputPower = Clamp(libm::powf(gauge, exponent), 0.01f, 1.0f);
+    ti.autoDirectionBias = type == kFnShortPass ? 0.4f : 0.2f;
+    ti.autoPowerBias = type == kFnHighPass ? 0.5f : 0.7f;
+    AimPass(w, p, type, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias, ti.desiredDirection, ti.desiredPower,
+            ti.targetPlayer, -1);
+    q.push_back(cmd);
+}
+// A pass or shot armed by a gamer goes out when its button is released, held past half a second,
+// or (off the ball, outside set pieces) once it has been released before; its gauge runs from
+// 60 ms to a second. A kick-off taker passes short to the nearest teammate ahead whatever the
+// button; passes share one call site, so that matches of a wavefront passing in different ways
+// run the pass search together.
+HD void ReleaseGamerAction(World &w, const Ctx &c, int p, AIController &ai, HumanControllerState &hc, CommandQueue &q) {
+    const MatchState &m = w.match;
+    const bool *b = hc.keyboard.buttons;
+    const int t = w.playerTeamID[p];
+    const TeamAI &tai = TeamByID(w, t).ai;
+    const PlayerControllerState &ctl = hc.base;
+    if (!(!b[hc.actionButton] || (b[hc.actionButton] && hc.gaugeMs > 500) ||
+          (!m.players[p].hasPossession && !m.inSetPiece && hc.actionBufferTimeMs > 0)))
+        return;
+    const int baseMs = 60;
+    float gauge = (float)(hc.gaugeMs - baseMs) * (1.0f / float(1000 - baseMs));
+    gauge = Clamp(gauge, 0.0f, 1.0f);
+    if (m.inSetPiece && tai.taker == p && tai.setPieceType == kModeKickOff) {
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnShortPass;
+        TouchInformation &ti = cmd.touchInfo;
+        ti.autoDirectionBias = 1.0f;
+        ti.autoPowerBias = 1.0f;
+        ti.inputDirection = ai.Dir();
+        ti.inputPower = 0.1f;
+        ti.forcedTargetPlayer = GetClosestPlayer(w, c, t, ai.Pos() + ai.Dir() * 1.0f, false, p);
+        AimPass(w, p, cmd.desiredFunctionType, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias,
+                ti.desiredDirection, ti.desiredPower, ti.targetPlayer, ti.forcedTargetPlayer);
+        q.push_back(cmd);
+    } else if (hc.actionButton == kBtnShortPass || hc.actionButton == kBtnLongPass || hc.actionButton == kBtnHighPass) {
+        const int type = hc.actionButton == kBtnShortPass ? kFnShortPass : hc.actionButton == kBtnLongPass ? kFnLongPass : kFnHighPass;
+        GamerPass(w, p, ctl, type, gauge, q);
+    } else if (hc.actionButton == kBtnShot) {
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnShot;
+        cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
+        cmd.touchInfo.inputDirection = ctl.inputDirection;
+        cmd.touchInfo.autoDirectionBias = 1.0f;
+        cmd.touchInfo.desiredDirection = AimShot(w, p, cmd.touchInfo.inputDirection, cmd.touchInfo.autoDirectionBias);
+        cmd.touchInfo.desiredPower = Clamp(libm::powf(gauge, 0.6f), 0.01f, 1.0f);
+        q.push_back(cmd);
+    }
+}
+// A defensive action lasts while its button is held: a sliding tackle along the stick, team
+// pressure, or the keeper's rush; released, it ends.
+HD void HoldDefensiveAction(World &w, const Ctx &c, int p, AIController &ai, HumanControllerState &hc, CommandQueue &q) {
+    const int t = w.playerTeamID[p];
+    if (!hc.keyboard.buttons[hc.actionButton]) {
+        hc.actionMode = 0;
+        return;
+    }
+    if (hc.actionButton == kBtnSliding) {
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.desiredFunctionType = kFnSliding;
+        cmd.useDesiredMovement = true;
+        cmd.desiredDirection = hc.base.inputDirection;
+        cmd.desiredVelocityFloat = hc.base.inputVelocityFloat;
+        cmd.useDesiredLookAt = true;
+        cmd.desiredLookAt = ai.Pos() + ai.Mov() * 0.1f + cmd.desiredDirection * 10.0f;
+        q.push_back(cmd);
+    }
+    if (hc.actionButton == kBtnTeamPressure) TeamApplyTeamPressure(w, c, t);
+    if (hc.actionButton == kBtnKeeperRush) TeamApplyKeeperRush(w, t);
+}
+// In open play a gamer's player controls and traps along the stick's steady direction (dribble
+// turns an idle touch to goal, dribble with sprint knocks on); with a pass or shot armed it
+// does so along its own direction at a speed that falls the more the stick points away, then
+// interferes when pressure is held.
+HD void GamerTouchCommands(World &w, int p, AIController &ai, HumanControllerState &hc) {
+    const bool *b = hc.keyboard.buttons;
+    PlayerControllerState &ctl = hc.base;
+    const bool idleTurn = b[kBtnDribble];
+    const bool knockOn = b[kBtnDribble] && b[kBtnSprint];
+    const Vec3 savedDir = ctl.inputDirection;
+    const float savedVel = ctl.inputVelocityFloat;
+    if (hc.actionMode == 2) {
+        float along = ai.Dir().Dot(ctl.inputDirection) * 0.5f + 0.5f;
+        if (along < 0) along = 0;
+        if (Sp(w, p).velocityCat != kVelIdle)
+            ctl.inputDirection = (ai.Dir() * 1.0f + ctl.inputDirection * 0.0f).Normalized(ctl.inputDirection);
+        along = libm::powf(along, 1.5f);
+        along = along * 0.8f + 0.2f;
+        along *= 0.9f;
+        ctl.inputVelocityFloat = ai.FloatVelocity() * along;
+    }
+    ai.BallControlCommand(idleTurn, knockOn, true, false);
+    ai.TrapCommand(idleTurn, knockOn);
+    if (hc.actionMode == 2) {
+        ctl.inputDirection = savedDir;
+        ctl.inputVelocityFloat = savedVel;
+    }
+    ai.InterfereCommand(b[kBtnPressure]);
+}
+// The commands of a gamer's player (GRF's human controller with the default gameplay settings):
+// the armed action expires, goes out or holds; at a set piece the taker (until its pass goes)
+// and the others wait in position; otherwise the touch commands and a movement, forced toward
+// the ball by pressure or an armed pass or shot. Without the magnet the movement follows the
+// stick, facing the ball half a second ahead; dribble with sprint off the ball follows it too.
 HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
     ENG_SCOPE(45);
     HumanControllerState &hc = HumanGamerOf(w, p).controller;
@@ -483,11 +616,6 @@ HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
     const int t = w.playerTeamID[p];
     const TeamAI &tai = TeamByID(w, t).ai;
     const bool *b = hc.keyboard.buttons;
-    auto resetAction = [&]() {
-        hc.actionMode = 0;
-        hc.gaugeMs = 0;
-        hc.actionBufferTimeMs = 0;
-    };
     ai.k = MentalImageIndex(w, ctl.mentalImageTime);
     ps.desiredTimeToBallMs = 0;
     ctl.opponentPlayer = TeamBestPossessionPlayer(w, 1 - t);
@@ -497,128 +625,25 @@ HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
     HumanGetKeyboardInput(w, p, rawDir, rawVel);
     ctl.inputDirection = rawDir;
     ctl.inputVelocityFloat = rawVel;
-    const AnimationState &cur = Hum(w, p).anim;
-    const int fn = cur.functionType;
-    const bool touchPending = cur.frameNum < cur.touchFrame;
-    if (hc.actionMode == 2 && IsPassOrShot(fn) && !touchPending) resetAction();
-    if (hc.actionMode == 1 && (fn == kFnSliding || fn == kFnInterfere) && !touchPending) resetAction();
-    if (hc.actionMode == 2 && hc.actionButton == kBtnShot && b[kBtnShortPass] && !m.inSetPiece) resetAction();
-    if (hc.actionMode == 2 && hc.actionButton == kBtnHighPass && b[kBtnShortPass] && !m.inSetPiece) resetAction();
-    if (hc.actionMode == 2 && !m.inSetPiece &&
-        (hc.actionBufferTimeMs > 2000 || ps.timeToBallMs > ps.timeToBallPreviousMs + 700 || fn == kFnInterfere))
-        resetAction();
-    if (hc.actionMode == 1 && hc.actionBufferTimeMs > 1000) resetAction();
-    if (hc.actionMode == 2) {
-        if (!b[hc.actionButton] || (b[hc.actionButton] && hc.gaugeMs > 500) ||
-            (!ps.hasPossession && !m.inSetPiece && hc.actionBufferTimeMs > 0)) {
-            const int baseMs = 60;
-            float gauge = (float)(hc.gaugeMs - baseMs) * (1.0f / float(1000 - baseMs));
-            gauge = Clamp(gauge, 0.0f, 1.0f);
-            auto pass = [&](int type, float exponent, float autoDir, float autoPower) {
-                PlayerCommand cmd = DefaultPlayerCommand();
-                cmd.desiredFunctionType = type;
-                TouchInformation &ti = cmd.touchInfo;
-                ti.inputDirection = ctl.inputDirection;
-                ti.inputPower = Clamp(libm::powf(gauge, exponent), 0.01f, 1.0f);
-                ti.autoDirectionBias = autoDir;
-                ti.autoPowerBias = autoPower;
-                AimPass(w, p, type, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias, ti.desiredDirection,
-                        ti.desiredPower, ti.targetPlayer, -1);
-                q.push_back(cmd);
-            };
-            // GRF: the exponents and biases are the default gameplay settings.
-            if (m.inSetPiece && tai.taker == p && tai.setPieceType == kModeKickOff) {
-                PlayerCommand cmd = DefaultPlayerCommand();
-                cmd.desiredFunctionType = kFnShortPass;
-                TouchInformation &ti = cmd.touchInfo;
-                ti.autoDirectionBias = 1.0f;
-                ti.autoPowerBias = 1.0f;
-                ti.inputDirection = ai.Dir();
-                ti.inputPower = 0.1f;
-                ti.forcedTargetPlayer = GetClosestPlayer(w, c, t, ai.Pos() + ai.Dir() * 1.0f, false, p);
-                AimPass(w, p, cmd.desiredFunctionType, ti.inputDirection, ti.inputPower, ti.autoDirectionBias, ti.autoPowerBias,
-                        ti.desiredDirection, ti.desiredPower, ti.targetPlayer, ti.forcedTargetPlayer);
-                q.push_back(cmd);
-            } else if (hc.actionButton == kBtnShortPass || hc.actionButton == kBtnLongPass || hc.actionButton == kBtnHighPass) {
-                // One call site for the three passes, so that matches of a wavefront passing in
-                // different ways run the pass search together.
-                const int type = hc.actionButton == kBtnShortPass ? kFnShortPass
-                                 : hc.actionButton == kBtnLongPass ? kFnLongPass
-                                                                   : kFnHighPass;
-                const float exponent = type == kFnShortPass ? 0.7f : type == kFnLongPass ? 0.65f : 0.55f;
-                const float autoDir = type == kFnShortPass ? 0.4f : 0.2f;
-                const float autoPower = type == kFnHighPass ? 0.5f : 0.7f;
-                pass(type, exponent, autoDir, autoPower);
-            } else if (hc.actionButton == kBtnShot) {
-                PlayerCommand cmd = DefaultPlayerCommand();
-                cmd.desiredFunctionType = kFnShot;
-                cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
-                cmd.touchInfo.inputDirection = ctl.inputDirection;
-                cmd.touchInfo.autoDirectionBias = 1.0f;
-                cmd.touchInfo.desiredDirection =
-                    AimShot(w, p, cmd.touchInfo.inputDirection, cmd.touchInfo.autoDirectionBias);
-                cmd.touchInfo.desiredPower = Clamp(libm::powf(gauge, 0.6f), 0.01f, 1.0f);
-                q.push_back(cmd);
-            }
-        }
-    } else if (hc.actionMode == 1) {
-        if (b[hc.actionButton]) {
-            if (hc.actionButton == kBtnSliding) {
-                PlayerCommand cmd = DefaultPlayerCommand();
-                cmd.desiredFunctionType = kFnSliding;
-                cmd.useDesiredMovement = true;
-                cmd.desiredDirection = ctl.inputDirection;
-                cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
-                cmd.useDesiredLookAt = true;
-                cmd.desiredLookAt = ai.Pos() + ai.Mov() * 0.1f + cmd.desiredDirection * 10.0f;
-                q.push_back(cmd);
-            }
-            if (hc.actionButton == kBtnTeamPressure) TeamApplyTeamPressure(w, c, t);
-            if (hc.actionButton == kBtnKeeperRush) TeamApplyKeeperRush(w, t);
-        } else {
-            hc.actionMode = 0;
-        }
-    }
-    if ((m.inSetPiece && tai.taker == p && (hc.actionMode != 2 || (hc.actionMode == 2 && b[hc.actionButton]) || m.ballRetainer == p)) ||
-        (m.inSetPiece && tai.taker != p && m.ballRetainer < 0)) {
+    ExpireGamerAction(m, ps, Hum(w, p).anim, hc);
+    if (hc.actionMode == 2) ReleaseGamerAction(w, c, p, ai, hc, q);
+    else if (hc.actionMode == 1) HoldDefensiveAction(w, c, p, ai, hc, q);
+    const bool takerWaits = tai.taker == p && (hc.actionMode != 2 || (hc.actionMode == 2 && b[hc.actionButton]) || m.ballRetainer == p);
+    if (m.inSetPiece && (takerWaits || (tai.taker != p && m.ballRetainer < 0))) {
         ai.SetPieceCommand();
         return true;
     }
-    Vec3 savedNonsteady = ctl.inputDirection;
+    const Vec3 unsteady = ctl.inputDirection;
     ctl.inputDirection = hc.steadyDirection;
-    if (m.inPlay && !m.inSetPiece) {
-        bool idleTurn = b[kBtnDribble];
-        bool knockOn = b[kBtnDribble] && b[kBtnSprint];
-        Vec3 savedDir = ctl.inputDirection;
-        float savedVel = ctl.inputVelocityFloat;
-        if (hc.actionMode == 2) {
-            float dot = ai.Dir().Dot(ctl.inputDirection) * 0.5f + 0.5f;
-            if (dot < 0) dot = 0;
-            if (Sp(w, p).velocityCat != kVelIdle)
-                ctl.inputDirection = (ai.Dir() * 1.0f + ctl.inputDirection * 0.0f).Normalized(ctl.inputDirection);
-            dot = libm::powf(dot, 1.5f);
-            dot = dot * 0.8f + 0.2f;
-            dot *= 0.9f;
-            ctl.inputVelocityFloat = ai.FloatVelocity() * dot;
-        }
-        ai.BallControlCommand(idleTurn, knockOn, true, false);
-        ai.TrapCommand(idleTurn, knockOn);
-        if (hc.actionMode == 2) {
-            ctl.inputDirection = savedDir;
-            ctl.inputVelocityFloat = savedVel;
-        }
-        ai.InterfereCommand(b[kBtnPressure]);
-    }
-    bool forceMagnet = false, extraHaste = false;
-    if ((hc.actionMode != 2 && b[kBtnPressure]) || hc.actionMode == 2) forceMagnet = extraHaste = true;
-    ai.MovementCommand(forceMagnet, extraHaste);
+    if (m.inPlay && !m.inSetPiece) GamerTouchCommands(w, p, ai, hc);
+    const bool urge = (hc.actionMode != 2 && b[kBtnPressure]) || hc.actionMode == 2;
+    ai.MovementCommand(urge, urge);
     if (!q.empty()) {
         PlayerCommand &cmd = q.back();
         if (!w.scenario.useMagnet) {
             cmd.desiredDirection = ctl.inputDirection;
             cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
-            if (cmd.desiredVelocityFloat < kIdleDribbleSwitch)
-                cmd.desiredDirection = (ai.MentalBall(500).Get2D() - ai.Pos()).Normalized(ctl.inputDirection);
+            if (cmd.desiredVelocityFloat < kIdleDribbleSwitch) cmd.desiredDirection = (ai.MentalBall(500).Get2D() - ai.Pos()).Normalized(ctl.inputDirection);
             cmd.desiredLookAt = ai.MentalBall(500).Get2D();
         }
         if (m.inPlay && !m.inSetPiece && b[kBtnDribble] && b[kBtnSprint] && !ctl.hasBestPossession) {
@@ -626,7 +651,7 @@ HDN bool HumanRequestCommand(World &w, const Ctx &c, int p, CommandQueue &q) {
             cmd.desiredVelocityFloat = ctl.inputVelocityFloat;
         }
     }
-    ctl.inputDirection = savedNonsteady;
+    ctl.inputDirection = unsteady;
     return true;
 }
 

@@ -52,61 +52,75 @@ struct AIBase {
     HD Vec3 MentalBall(int ms) const { return MentalBallPrediction(w, k, ms); }
     HD Vec3 BallAt(int ms) const { return BallPredict(m.ball, ms); }
 
+    // How likely the player is to win a duel for the ball with the opponents' designated player
+    // (both 0.1 s ahead): 1 when the opponent stands between it and the ball seen 100 ms ahead
+    // facing away, 0 when the player is between.
     HD float CouldWinABallDuelLikeliness() const {
-        int o = Opp().designatedTeamPossessionPlayer;
-        Vec3 op = Pos(o) + Mov(o) * 0.1f;
-        Vec3 meToOpp = op - (Pos() + Mov() * 0.1f);
-        Vec3 oppToBall = MentalBall(100).Get2D() - (Pos(o) + Mov(o) * 0.1f);
-        float dot = meToOpp.Normalized(0).Dot(oppToBall.Normalized(0));
-        dot = dot * 0.5f + 0.5f;
-        return (1.0f - dot);
+        const int o = Opp().designatedTeamPossessionPlayer;
+        const Vec3 opponent = Pos(o) + Mov(o) * 0.1f;
+        const Vec3 toOpponent = opponent - (Pos() + Mov() * 0.1f);
+        const Vec3 opponentToBall = MentalBall(100).Get2D() - (Pos(o) + Mov(o) * 0.1f);
+        const float behind = toOpponent.Normalized(0).Dot(opponentToBall.Normalized(0)) * 0.5f + 0.5f;
+        return (1.0f - behind);
     }
 
-    // Moves `desired` towards the spot that keeps the marked opponent from a shooting point.
+    // The shooting point of an opponent (as the player saw it a reaction time ago, 0.5 s ahead):
+    // on its way to the team's goal, 24 m out for the designated player and 8 m for others (at
+    // least 0.4 m from where it is), held to the offside trap. Returns its distance from the
+    // opponent in `reach`.
+    HD Vec3 ShootingPoint(int o, const Vec3 &goal, float &reach) const {
+        const PlayerImage oi = MentalPlayerImage(w, MentalImageIndex(w, PlayerControllerReactionTime(w, c, p)), o);
+        const Vec3 op = oi.position + oi.movement * 0.5f;
+        const float range = o == m.designatedPossessionPlayer ? 24.0f : 8.0f;
+        reach = Clamp((goal - op).Length() - range, 0.4f, kPitchHalfLength);
+        Vec3 point = op + (goal - op).Normalized(0) * reach;
+        const float trapX = AI().offsideTrapX;
+        if (point.v[0] * side > trapX * side) {
+            const Line toGoal(op, goal);
+            const Line trap(Vec3(trapX, -kPitchHalfWidth, 0), Vec3(trapX, kPitchHalfWidth, 0));
+            point = toGoal.IntersectionPoint(trap);
+            reach = (point - op).Length();
+        }
+        return point;
+    }
+    // Moves `desired` toward defending the marked (or forced) opponent, by `bias`, in open play
+    // for outfield players: to within the opponent's reach of its shooting point less a 4 m
+    // buffer, then goalside by 70% of however far the player (0.14 s ahead) is beyond that reach.
     HDN void AddDefensiveComponent(Vec3 &desired, float bias, int forcedOpp = -1) const {
-        int o = forcedOpp < 0 ? ps.manMarking : forcedOpp;
+        const int o = forcedOpp < 0 ? ps.manMarking : forcedOpp;
         if (!(m.inPlay && !m.inSetPiece && StaticRole(p) != kRoleGoalkeeper)) return;
         if (o < 0) return;
+        const float buffer = 4.0f;
+        const Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
+        float reach = 0;
+        const Vec3 point = ShootingPoint(o, goal, reach);
         Vec3 defend = desired;
-        const float possShoot = 24.0f, genericShoot = 8.0f, minDistance = 0.4f, buffer = 4.0f;
-        PlayerImage oi = MentalPlayerImage(w, MentalImageIndex(w, PlayerControllerReactionTime(w, c, p)), o);
-        Vec3 op = oi.position + oi.movement * 0.5f;
-        float shoot = o == m.designatedPossessionPlayer ? possShoot : genericShoot;
-        Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
-        float oppToGoal = (goal - op).Length();
-        float oppToThreshold = Clamp(oppToGoal - shoot, minDistance, kPitchHalfLength);
-        Vec3 shootingPoint = op + (goal - op).Normalized(0) * oppToThreshold;
-        const float trapX = AI().offsideTrapX;
-        if (shootingPoint.v[0] * side > trapX * side) {
-            Line l1(op, goal);
-            Line l2(Vec3(trapX, -kPitchHalfWidth, 0), Vec3(trapX, kPitchHalfWidth, 0));
-            shootingPoint = l1.IntersectionPoint(l2);
-            oppToThreshold = (shootingPoint - op).Length();
-        }
-        Vec3 meToThreshold = shootingPoint - desired;
-        float meDist = meToThreshold.Length();
-        float slack = meDist - (oppToThreshold - buffer);
-        if (slack > 0.0f) defend = desired + meToThreshold.Normalized(0) * Clamp(slack, 0.0f, meDist);
-        Vec3 actual = Pos() + Mov() * 0.14f;
-        float actualSlack = (shootingPoint - actual).Length() - oppToThreshold;
-        if (actualSlack > 0.0f) defend += (goal - defend).Normalized(0) * actualSlack * 0.7f;
+        const Vec3 toPoint = point - desired;
+        const float toPointLength = toPoint.Length();
+        const float slack = toPointLength - (reach - buffer);
+        if (slack > 0.0f) defend = desired + toPoint.Normalized(0) * Clamp(slack, 0.0f, toPointLength);
+        const float late = (point - (Pos() + Mov() * 0.14f)).Length() - reach;
+        if (late > 0.0f) defend += (goal - defend).Normalized(0) * late * 0.7f;
         desired = desired * (1.0f - bias) + defend * bias;
     }
+    // Where to stand against opponent `o` (as the player sees it): on its line to the team's goal
+    // where the perpendicular bisector of the player and the opponent crosses it (within the
+    // line), plus a tenth of a sprint second and `distance` toward goal and its movement 0.14 s on.
     HDN Vec3 GetDefendPosition(int o, float distance = 0.0f) const {
-        PlayerImage oi = MentalPlayerImage(w, k, o);
-        Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
-        Vec3 op = oi.position;
-        Vec3 oppToGoal = goal - op;
-        Line toGoal(op, goal);
-        Line meToOpp(Pos(), op);
-        Vec3 mid = meToOpp.pts[0] * 0.5f + meToOpp.pts[1] * 0.5f;
-        Line perp(mid, mid + (meToOpp.pts[0] - mid).Rotated2D((float)(0.5 * (double)PI)));
-        float f = 0.0f;
-        toGoal.IntersectionPoint(perp, f);
-        f = Clamp(f, 0.0f, 1.0f);
-        Vec3 t = toGoal.pts[0] + (toGoal.pts[1] - toGoal.pts[0]) * f;
-        t += (oppToGoal.Normalized(0) * kSprintVelocity * 0.1f) + (oi.movement * 0.14f) + (oppToGoal.Normalized(0) * distance);
-        return t;
+        const PlayerImage oi = MentalPlayerImage(w, k, o);
+        const Vec3 goal = Vec3(kPitchHalfLength * side, 0, 0);
+        const Vec3 op = oi.position;
+        const Vec3 home = goal - op;
+        const Line toGoal(op, goal);
+        const Line between(Pos(), op);
+        const Vec3 mid = between.pts[0] * 0.5f + between.pts[1] * 0.5f;
+        const Line bisector(mid, mid + (between.pts[0] - mid).Rotated2D((float)(0.5 * (double)PI)));
+        float along = 0.0f;
+        toGoal.IntersectionPoint(bisector, along);
+        along = Clamp(along, 0.0f, 1.0f);
+        Vec3 stand = toGoal.pts[0] + (toGoal.pts[1] - toGoal.pts[0]) * along;
+        stand += (home.Normalized(0) * kSprintVelocity * 0.1f) + (oi.movement * 0.14f) + (home.Normalized(0) * distance);
+        return stand;
     }
 
     // ---- commands ----

@@ -789,38 +789,49 @@ struct AIBase {
     }
 
     // ---- passes ----
+    // How much an opponent (0.2 s ahead) threatens a ball on its way from `origin` to `target`,
+    // 0 to 1: the seconds the ball needs to reach the opponent's point of the line (0.7 s plus
+    // 0.03 times the distance to that point times its fraction of the way, 2.5 s more past the
+    // middle of a high pass; divided by the ball-speed factor) against the seconds the opponent
+    // needs to reach the line at a sprint, with half a second of slack. Opponents behind the passer or 20% past the target do not count, nor
+    // those under a high pass's flight (20% to 65% of the way).
+    HD float InterceptThreat(const Vec3 &origin, const Vec3 &target, const Line &line, int passType, const PlayerImagePos &opp,
+                             float ballVelMul) const {
+        const float secondScale = 1.0f;
+        const Vec3 at = opp.position + opp.movement * 0.2f;
+        float along = 0.0f;
+        const float away = line.DistanceToPoint(at, along);
+        if (!(along >= 0.0f && along <= 1.0f + 0.2f)) return 0.0f;
+        if (passType == kFnHighPass && !(along < 0.2f || along > 0.65f)) return 0.0f;
+        const float onLine = Clamp(along, 0.0f, 1.0f);
+        const Vec3 meet = origin * (1.0f - onLine) + target * onLine;
+        const float opponentSeconds = (away + 1.0f) / kSprintVelocity;
+        const float lofted = (passType == kFnHighPass && along > 0.5f) ? 2.5f : 0.0f;
+        float ballSeconds = 0.7f + (meet - origin).Length() * along * 0.03f + lofted;
+        ballSeconds *= 1.0f / ballVelMul;
+        return Clamp(ballSeconds - opponentSeconds + (secondScale * 0.5f), 0.0f, secondScale);
+    }
+    // The odds of a pass (or, with a ball-speed factor, a shot) to `target` from 0.12 s ahead:
+    // 1 less the summed threats (a high pass starts at 0.4), clamped.
     HDN float PassingOdds(const Vec3 &target, int passType, const ImageList &opps, float ballVelMul = 1.0f) const {
         ENG_SCOPE(42);
         const float secondScale = 1.0f;
-        Vec3 origin = Pos() + Mov() * 0.12f;
-        Line line(origin, target);
+        const Vec3 origin = Pos() + Mov() * 0.12f;
+        const Line line(origin, target);
         float danger = 0.0f;
-        for (int i = 0; i < opps.count; i++) {
-            Vec3 op = opps[i].position + opps[i].movement * 0.2f;
-            float f = 0.0f;
-            float od = line.DistanceToPoint(op, f);
-            if (!(f >= 0.0f && f <= 1.0f + 0.2f)) continue;
-            if (passType == kFnHighPass && !(f < 0.2f || f > 0.65f)) continue;
-            float cf = Clamp(f, 0.0f, 1.0f);
-            Vec3 is = origin * (1.0f - cf) + target * cf;
-            float oppSeconds = (od + 1.0f) / kSprintVelocity;
-            Vec3 originToBall = (is - origin);
-            float penalty = (passType == kFnHighPass && f > 0.5f) ? 2.5f : 0.0f;
-            float ballSeconds = 0.7f + originToBall.Length() * f * 0.03f + penalty;
-            ballSeconds *= 1.0f / ballVelMul;
-            danger += Clamp(ballSeconds - oppSeconds + (secondScale * 0.5f), 0.0f, secondScale);
-        }
+        for (int i = 0; i < opps.count; i++) danger += InterceptThreat(origin, target, line, passType, opps[i], ballVelMul);
         if (passType == kFnHighPass) danger += 0.4f;
         danger = NormalizedClamp(danger, 0.0f, secondScale);
         return 1.0f - danger;
     }
+    // The odds of a pass to teammate `target` where it will be (0.7 s plus 3% a metre ahead, at
+    // most half a second; a long pass 20% further upfield); no high pass under 10 m.
     HDN float PassingOddsTo(int target, int passType, const ImageList &opps) const {
-        float d = (Pos(target) - Pos()).Length();
+        const float d = (Pos(target) - Pos()).Length();
         if (passType == kFnHighPass && d < 10.0f) return 0.0f;
-        float est = 0.7f + d * 0.03f;
-        Vec3 tp = Pos(target) + Mov(target) * Clamp(est, 0.0f, 0.5f);
-        if (passType == kFnLongPass) tp += Vec3(-side * d * 0.2f, 0, 0);
-        return PassingOdds(tp, passType, opps);
+        Vec3 at = Pos(target) + Mov(target) * Clamp(0.7f + d * 0.03f, 0.0f, 0.5f);
+        if (passType == kFnLongPass) at += Vec3(-side * d * 0.2f, 0, 0);
+        return PassingOdds(at, passType, opps);
     }
     HDN void AddPass(int target, int passType) {
         PlayerCommand cmd = DefaultPlayerCommand();

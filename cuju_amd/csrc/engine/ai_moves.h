@@ -124,18 +124,26 @@ struct AIBase {
     }
 
     // ---- commands ----
+    // The ball in the goalkeeper's reach for a save: within 10 m beyond the optimization
+    // threshold in 400 ms, free, in its penalty box in 160 ms (compared in double), and not a
+    // teammate's kick (a back pass).
+    HD bool BallSaveable() const {
+        if (GetDistance(BallAt(400), Pos()) > kBallDistanceOptimizeThreshold + 10.0f) return false;
+        if (m.lastTouchTeamID == teamID && MatchLastTouchPlayer(w) != p && m.lastTouchTeamIDs[kTouchKicked] == teamID) return false;
+        if (m.ballRetainer >= 0) return false;
+        const Vec3 ball = BallAt(160);
+        return !(fabsf(ball.v[1]) > 20.05f) && !((double)(ball.v[0] * -side) > -(double)kPitchHalfLength + 16.4);
+    }
+    // A goalkeeper's deflection (only those that pick the ball up, on request) of a saveable ball.
     HDN void KeeperDeflectCommand(bool onlyPickup) {
-        if (StaticRole(p) != kRoleGoalkeeper) return;
-        if (GetDistance(BallAt(400), Pos()) > kBallDistanceOptimizeThreshold + 10.0f) return;
-        if (m.lastTouchTeamID == teamID && MatchLastTouchPlayer(w) != p && m.lastTouchTeamIDs[kTouchKicked] == teamID) return;
-        if (m.ballRetainer >= 0) return;
-        if (fabsf(BallAt(160).v[1]) > 20.05f) return;
-        if ((double)(BallAt(160).v[0] * -side) > -(double)kPitchHalfLength + 16.4) return;
+        if (StaticRole(p) != kRoleGoalkeeper || !BallSaveable()) return;
         PlayerCommand cmd = DefaultPlayerCommand();
         cmd.desiredFunctionType = kFnDeflect;
         if (onlyPickup) cmd.onlyDeflectAnimationsThatPickupBall = true;
         q.push_back(cmd);
     }
+    // Waiting at a set piece: standing, facing on; looking at the ball, or, for the retainer,
+    // along its input.
     HDN void SetPieceCommand() {
         PlayerCommand cmd = DefaultPlayerCommand();
         cmd.useDesiredMovement = true;
@@ -253,18 +261,18 @@ struct AIBase {
     }
 
     // ---- movement towards the ball ----
+    // Staying on a held ball: toward where it will be at the touch (250 ms plus the touch offset
+    // ahead), blending back to the player's own direction within 0.4 m (to the 0.5), looking that
+    // way; the speed the distance at the AI's rate, or, from dribbling speed on, the desired speed
+    // held up to 8 m/s above it and eased 10% toward (90% up to) the nearest velocity category.
+    // Returns the player's time to the ball.
     HDN unsigned BallControlMovement(float desiredVel, Vec3 &bestDir, float &bestVel, Vec3 &bestLookAt) const {
         ENG_SCOPE(47);
-        const unsigned desiredMs = 250 + kDefaultTouchOffsetMs;
-        Vec3 toBall = MentalBall((int)desiredMs).Get2D() - Pos();
-        float dist = toBall.Length();
-        float autoBias = 1.0f;
-        if (dist < 0.4f) autoBias = libm::powf(NormalizedClamp(dist, 0.2f, 0.4f), 0.5f);
-        Vec3 autoDir = toBall.Normalized(Dir());
-        Vec3 manualDir = Dir();
-        bestDir = autoDir * autoBias + manualDir * (1.0f - autoBias);
+        const Vec3 toBall = MentalBall((int)(250 + kDefaultTouchOffsetMs)).Get2D() - Pos();
+        const float dist = toBall.Length();
+        const float toward = dist < 0.4f ? libm::powf(NormalizedClamp(dist, 0.2f, 0.4f), 0.5f) : 1.0f;
+        bestDir = toBall.Normalized(Dir()) * toward + Dir() * (1.0f - toward);
         bestDir.Normalize(Dir());
-        Vec3 look = bestDir;
         bestVel = dist * kDistanceToVelocity;
         // GRF: a velocity not below the dribble velocity, NaN included, takes the clamp.
         if (!(bestVel < kDribbleVelocity)) {
@@ -272,7 +280,7 @@ struct AIBase {
             if (RangeVelocity(bestVel) < bestVel) bestVel = bestVel * 0.9f + RangeVelocity(bestVel) * 0.1f;
             if (RangeVelocity(bestVel) > bestVel) bestVel = bestVel * 0.1f + RangeVelocity(bestVel) * 0.9f;
         }
-        bestLookAt = Pos() + look * 10.0f;
+        bestLookAt = Pos() + bestDir * 10.0f;
         return ps.timeToBallMs;
     }
 

@@ -841,6 +841,7 @@ struct AIBase {
         if (passType == kFnLongPass) at += Vec3(-side * d * 0.2f, 0, 0);
         return PassingOdds(at, passType, opps);
     }
+    // A fully automatic pass of `passType` to teammate `target`.
     HDN void AddPass(int target, int passType) {
         PlayerCommand cmd = DefaultPlayerCommand();
         cmd.desiredFunctionType = passType;
@@ -855,48 +856,57 @@ struct AIBase {
                 t.desiredPower, t.targetPlayer, t.forcedTargetPlayer);
         q.push_back(cmd);
     }
+    // A panic clearance away from the own goal: the facing direction (its x squeezed to 80%)
+    // turned upfield and toward the touchline it faces, lifted 0.3; offered as a high pass (power
+    // 0.7), a shot (0.6) and a long pass (0.8), fully manual.
     HDN void AddPanicPass() {
-        int ySide = SignSide(Dir().v[1]);
-        Vec3 away = ((Dir() * Vec3(0.8f, 1.0f, 0.0f)).Normalized() + Vec3(-side * 0.7f, ySide * 0.5f, 0)).Normalized(0) +
-                    Vec3(0, 0, 0.3f);
+        const int flank = SignSide(Dir().v[1]);
+        Vec3 away = ((Dir() * Vec3(0.8f, 1.0f, 0.0f)).Normalized() + Vec3(-side * 0.7f, flank * 0.5f, 0)).Normalized(0) + Vec3(0, 0, 0.3f);
         away.Normalize(Dir());
         PlayerCommand cmd = DefaultPlayerCommand();
         cmd.touchInfo.inputDirection = away;
         cmd.touchInfo.desiredDirection = away;
         cmd.touchInfo.autoDirectionBias = 0.0f;
         cmd.touchInfo.autoPowerBias = 0.0f;
-        const int types[3] = {kFnHighPass, kFnShot, kFnLongPass};
-        const float powers[3] = {0.7f, 0.6f, 0.8f};
-        for (int i = 0; i < 3; i++) {
-            cmd.desiredFunctionType = types[i];
-            cmd.touchInfo.inputPower = powers[i];
-            cmd.touchInfo.desiredPower = powers[i];
+        const struct {
+            int type;
+            float power;
+        } clearances[3] = {{kFnHighPass, 0.7f}, {kFnShot, 0.6f}, {kFnLongPass, 0.8f}};
+        for (const auto &option : clearances) {
+            cmd.desiredFunctionType = option.type;
+            cmd.touchInfo.inputPower = option.power;
+            cmd.touchInfo.desiredPower = option.power;
             q.push_back(cmd);
         }
     }
+    // The dribble: a force field around where the player will be in 0.25 s, pushed by the 5
+    // nearest opponents (0.25 s ahead, within 10 m), the near touchline and goal line (5 m beyond
+    // them, within 20 m), and pulled to the opponents' goal (its y following the player's, less
+    // near the goal line and by the center magnet) by the offensiveness (0.7 plus small shares of
+    // the dribble setting and the mindset). The speed is the pull at the AI's rate, snapped to a
+    // velocity category.
     HDN void BestDribbleMovement(Vec3 &desiredDir, float &desiredVel) const {
         ENG_SCOPE(43);
-        Vec3 mp = Pos(), mm = Mov();
-        float offense = 0.7f + kDribbleOffensiveness * 0.05f + GetMindSet(DynamicRole()) * 0.05f;
+        const Vec3 at = Pos(), mov = Mov();
+        const float offense = 0.7f + kDribbleOffensiveness * 0.05f + GetMindSet(DynamicRole()) * 0.05f;
         const float powerMul = 1.0f, futureS = 0.25f;
-        PlayerList opps = GetClosestPlayers(w, c, oppID, mp, false, 5);
+        const PlayerList opponents = GetClosestPlayers(w, c, oppID, at, false, 5);
         ForceField &ff = c.ws->forceField;
         ff.clear();
-        float nearBackline = NormalizedClamp(fabsf(mp.v[0]) / kPitchHalfLength, 0.0f, 1.0f);
-        float centerInv = 1.0f - nearBackline * nearBackline;
-        centerInv *= 0.5f;
-        Vec3 oppGoal = Vec3(-side * kPitchHalfLength, mp.v[1] * (1.0f - kDribbleCenterMagnet) * centerInv, 0);
-        for (int i = 0; i < opps.count; i++) {
-            PlayerImage oi = MentalPlayerImage(w, k, opps[i]);
+        const float nearGoalLine = NormalizedClamp(fabsf(at.v[0]) / kPitchHalfLength, 0.0f, 1.0f);
+        float central = 1.0f - nearGoalLine * nearGoalLine;
+        central *= 0.5f;
+        const Vec3 goal = Vec3(-side * kPitchHalfLength, at.v[1] * (1.0f - kDribbleCenterMagnet) * central, 0);
+        for (int i = 0; i < opponents.count; i++) {
+            const PlayerImage oi = MentalPlayerImage(w, k, opponents[i]);
             ff.push_back(MakeSpot(oi.position + oi.movement * futureS, kRepel, kDecayVariable, 2.0f * powerMul, 10.0f, 1.0f));
         }
-        ff.push_back(MakeSpot(Vec3(mp.v[0], (kPitchHalfWidth + 5.0f) * SignSide(mp.v[1]), 0), kRepel, kDecayVariable, 4.0f * powerMul, 20.0f, 0.7f));
-        ff.push_back(MakeSpot(Vec3((kPitchHalfLength + 5.0f) * SignSide(mp.v[0]), mp.v[1], 0), kRepel, kDecayVariable, 4.0f * powerMul, 20.0f, 0.7f));
-        ff.push_back(MakeSpot(oppGoal, kAttract, kDecayConstant, offense * powerMul));
-        Vec3 mv = GetForceFieldMovement(ff, mp + mm * futureS, 1.0f);
-        desiredDir = mv.Normalized(Dir());
-        desiredVel = Clamp(mv.Length() * kDistanceToVelocity, kIdleVelocity, kSprintVelocity);
-        desiredVel = RangeVelocity(desiredVel);
+        ff.push_back(MakeSpot(Vec3(at.v[0], (kPitchHalfWidth + 5.0f) * SignSide(at.v[1]), 0), kRepel, kDecayVariable, 4.0f * powerMul, 20.0f, 0.7f));
+        ff.push_back(MakeSpot(Vec3((kPitchHalfLength + 5.0f) * SignSide(at.v[0]), at.v[1], 0), kRepel, kDecayVariable, 4.0f * powerMul, 20.0f, 0.7f));
+        ff.push_back(MakeSpot(goal, kAttract, kDecayConstant, offense * powerMul));
+        const Vec3 pull = GetForceFieldMovement(ff, at + mov * futureS, 1.0f);
+        desiredDir = pull.Normalized(Dir());
+        desiredVel = RangeVelocity(Clamp(pull.Length() * kDistanceToVelocity, kIdleVelocity, kSprintVelocity));
     }
 };
 

@@ -683,19 +683,25 @@ struct AIBase {
         vel = Clamp(GetLazyVelocity((desired - Pos()).Length() * kDistanceToVelocity), 0, kSprintVelocity);
     }
 
-    HDN void CalculateIfBallIsBoundForGoal() {
-        eliza->ballBoundForGoal = false;
-        eliza->ballBoundForGoalY = 0;
-        float panic = 1.02f + (1.0f - (Stat(kStatDefensivePositioning) * 0.6f + Stat(kStatVision) * 0.4f)) * 0.5f;
+    // Whether the ball is bound for the keeper's goal, kept in the controller with where it will
+    // cross the goal line: the ball 4 s ahead is beyond the goal line, the keeper is within 32 m
+    // of the ball 250 ms ahead, and the ball's path (now to 800 ms ahead) crosses the goal line
+    // within 3.7 m of the centre, widened by the keeper's panic (1.02, up to 1.52 as its
+    // defensive positioning and vision fall).
+    HDN bool BallBoundForGoal() {
+        const float panic = 1.02f + (1.0f - (Stat(kStatDefensivePositioning) * 0.6f + Stat(kStatVision) * 0.4f)) * 0.5f;
+        bool bound = false;
+        float crossY = 0;
         if (MentalBall(4000).v[0] * side > kPitchHalfLength && (Pos() - MentalBall(250)).Length() < 32.0f) {
-            Line toGoal(MentalBall(0).Get2D(), MentalBall(800).Get2D());
-            Line goalLine(Vec3(kPitchHalfLength * side, -kPitchHalfWidth, 0), Vec3(kPitchHalfLength * side, kPitchHalfWidth, 0));
-            Vec3 ip = toGoal.IntersectionPoint(goalLine).Get2D();
-            if (!((double)fabsf(ip.v[1]) > 3.7 * (double)panic)) {
-                eliza->ballBoundForGoalY = ip.v[1];
-                eliza->ballBoundForGoal = true;
-            }
+            const Line path(MentalBall(0).Get2D(), MentalBall(800).Get2D());
+            const Line goalLine(Vec3(kPitchHalfLength * side, -kPitchHalfWidth, 0), Vec3(kPitchHalfLength * side, kPitchHalfWidth, 0));
+            const float y = path.IntersectionPoint(goalLine).Get2D().v[1];
+            bound = !((double)fabsf(y) > 3.7 * (double)panic);
+            if (bound) crossY = y;
         }
+        eliza->ballBoundForGoal = bound;
+        eliza->ballBoundForGoalY = crossY;
+        return bound;
     }
 
     // How far an opponent is from a shot, scaled down close to goal.
@@ -788,8 +794,7 @@ struct AIBase {
         Vec3 target = Vec3((kPitchHalfLength - 10.0f) * side, 0, 0);
         float maxVel = kSprintVelocity;
         if (ball.v[0] * side > 0) {
-            CalculateIfBallIsBoundForGoal();
-            target = eliza->ballBoundForGoal ? KeeperSave() : KeeperCover(ball, goal, maxVel);
+            target = BallBoundForGoal() ? KeeperSave() : KeeperCover(ball, goal, maxVel);
         }
         dir = target - Pos();
         vel = Clamp(dir.Length() * kDistanceToVelocity, kIdleVelocity, maxVel);
@@ -801,8 +806,9 @@ struct AIBase {
     // 0 to 1: the seconds the ball needs to reach the opponent's point of the line (0.7 s plus
     // 0.03 times the distance to that point times its fraction of the way, 2.5 s more past the
     // middle of a high pass; divided by the ball-speed factor) against the seconds the opponent
-    // needs to reach the line at a sprint, with half a second of slack. Opponents behind the passer or 20% past the target do not count, nor
-    // those under a high pass's flight (20% to 65% of the way).
+    // needs to reach the line at a sprint, with half a second of slack. Opponents behind the
+    // passer or 20% past the target do not count, nor those under a high pass's flight (20% to
+    // 65% of the way).
     HD float InterceptThreat(const Vec3 &origin, const Vec3 &target, const Line &line, int passType, const PlayerImagePos &opp,
                              float ballVelMul) const {
         const float secondScale = 1.0f;

@@ -376,6 +376,62 @@ struct AIController : AIBase {
         forceMagnet = true;
     }
 
+    // The part a player without a gamer plays in open play: the keeper keeps goal; an outfield
+    // player off the ball keeps its line's place; the designated player plays the ball when its
+    // team has no gamer, or it has a gamer's controller that is not active. (A ball retainer was
+    // handled as a restart before.)
+    enum OpenPlayPart { kNoPart, kLinePart, kBallPart, kKeeperPart };
+    HD int OpenPlayPartOf(int role) const {
+        if (!m.inPlay || m.inSetPiece) return kNoPart;
+        if (role == kRoleGoalkeeper) return kKeeperPart;
+        if (m.designatedPossessionPlayer != p) return kLinePart;
+        const bool unattended = HumanGamerCount(Own()) == 0 || (!ExternalControllerActive(w, p) && ps.base.externalController >= 0);
+        return unattended ? kBallPart : kNoPart;
+    }
+    // The line an outfield role keeps: backs defend, the five midfield roles hold the middle, the
+    // centre-forward attacks.
+    HD static int LineOfRole(int role) {
+        switch (role) {
+            case kRoleLeftBack:
+            case kRoleCentreBack:
+            case kRoleRightBack: return kDefense;
+            case kRoleCentreForward: return kOffense;
+            default: return kMidfield;
+        }
+    }
+    // The keeper's part: its own movement, which replaces the movement command when the ball is
+    // bound for goal or another player is designated (the return value), and a deflection unless
+    // it holds the ball uniquely with possession 3.4 or more (pickups only when nothing is bound
+    // for goal and the possession passes 1.3).
+    HD bool KeeperPart(Vec3 &dir, float &vel) {
+        const bool bound = BallBoundForGoal();
+        GoalieRequestInput(dir, vel);
+        if (!ctl.hasUniquePossession || ctl.possessionAmount < 3.4f) KeeperDeflectCommand(!bound && ctl.possessionAmount > 1.3f);
+        return bound || p != m.designatedPossessionPlayer;
+    }
+    // The team's pressure order names this player, still running, while the opponents hold the
+    // ball better; never the designated player or the keeper.
+    HD bool PressureOrdered(int role) const {
+        return m.inPlay && !m.inSetPiece && (AI().endApplyTeamPressureMs > m.actualTimeMs && AI().teamPressurePlayer == p) &&
+               !ctl.teamHasBestPossession && m.designatedPossessionPlayer != p && role != kRoleGoalkeeper;
+    }
+    // Moving by the player's own choice: along `dir` at `vel`, looking 10 m toward the ball 40 ms
+    // ahead.
+    HD void OwnMovement(const Vec3 &dir, float vel) {
+        PlayerCommand cmd = DefaultPlayerCommand();
+        cmd.useDesiredMovement = true;
+        cmd.desiredDirection = dir;
+        cmd.desiredVelocityFloat = vel;
+        cmd.useDesiredLookAt = true;
+        cmd.desiredLookAt = Pos() + (MentalBall(40).Get2D() - Pos()).Normalized(0) * 10.0f;
+        q.push_back(cmd);
+    }
+
+    // The request of a player without a gamer: the situation and the opponent on the ball, then
+    // a stoppage command or the restart when there is one; in open play its part's input (one
+    // call site per part, so that the matches of a wavefront whose players differ in role run it
+    // together), the touch commands, and the movement command (pressing first), or the keeper's
+    // own movement.
     HDN bool RequestCommand() {
         if (m.designatedPossessionPlayer < 0) return Fail("the AI controller finds no designated possession player");
         if (Own().designatedTeamPossessionPlayer < 0 || Opp().designatedTeamPossessionPlayer < 0)
@@ -387,74 +443,43 @@ struct AIController : AIBase {
         ControllerCalculateSituation(w, p, ctl);
         ctl.opponentPlayer = TeamBestPossessionPlayer(w, oppID);
         ctl.timeNeededMs = (float)ps.timeToBallMs;
-        Vec3 rawDir = Dir();
-        float rawVel = kIdleVelocity;
-        Vec3 manualDir = Dir();
-        float manualVel = kIdleVelocity;
-        bool manual = false, extraHaste = false;
         // GRF: laziness is fixed at creation from the player's own static entry.
-        const bool lazy = c.sd->formation[p].lazy;
-        const int role = StaticRole(p);
-        if (StoppageCommand(lazy)) return true;
+        if (StoppageCommand(c.sd->formation[p].lazy)) return true;
         if ((m.inSetPiece && AI().taker == p) || m.ballRetainer == p) {
             SetPieceCommands();
             return true;
         }
-        // The field strategy of each line and the on-the-ball commands each have one call site, so
-        // that matches of a wavefront whose players differ in role or situation run them together;
-        // per environment the calls and their order are GRF's.
-        int strategy = -1;
-        bool onTheBall = false;
-        if (m.inPlay && !m.inSetPiece && m.ballRetainer != p && m.designatedPossessionPlayer != p && role != kRoleGoalkeeper) {
-            if (role == kRoleLeftBack || role == kRoleCentreBack || role == kRoleRightBack)
-                strategy = kDefense;
-            else if (role == kRoleDefensiveMid || role == kRoleLeftMid || role == kRoleCentralMid || role == kRoleRightMid ||
-                     role == kRoleAttackingMid)
-                strategy = kMidfield;
-            else if (role == kRoleCentreForward)
-                strategy = kOffense;
-        } else if (m.inPlay && !m.inSetPiece && m.designatedPossessionPlayer == p &&
-                   (HumanGamerCount(Own()) == 0 || (!ExternalControllerActive(w, p) && ps.base.externalController >= 0)) &&
-                   role != kRoleGoalkeeper) {
-            onTheBall = ps.timeToBallMs < 1000;
-            extraHaste = false;
-        } else if (m.inPlay && !m.inSetPiece && role == kRoleGoalkeeper) {
-            CalculateIfBallIsBoundForGoal();
-            const bool bound = eliza->ballBoundForGoal;
-            if (bound) manual = true;
-            if (p != m.designatedPossessionPlayer) manual = true;
-            GoalieRequestInput(manualDir, manualVel);
-            if (!ctl.hasUniquePossession || ctl.possessionAmount < 3.4f)
-                KeeperDeflectCommand(!bound && ctl.possessionAmount > 1.3f);
+        const int role = StaticRole(p);
+        const int part = OpenPlayPartOf(role);
+        Vec3 input = Dir(), own = Dir();
+        float inputVel = kIdleVelocity, ownVel = kIdleVelocity;
+        bool ownMovement = false;
+        bool onTheBall = part == kBallPart && ps.timeToBallMs < 1000;
+        if (part == kKeeperPart) {
+            ownMovement = KeeperPart(own, ownVel);
             onTheBall = ps.timeToBallMs < 1000 && m.designatedPossessionPlayer == p;
         }
-        if (strategy >= 0) FieldStrategyRequestInput(strategy, rawDir, rawVel);
-        if (onTheBall) GetOnTheBallCommands(rawDir, rawVel);
-        bool forceMagnet = m.inPlay && !m.inSetPiece && (AI().endApplyTeamPressureMs > m.actualTimeMs && AI().teamPressurePlayer == p) &&
-                           !ctl.teamHasBestPossession && m.designatedPossessionPlayer != p && role != kRoleGoalkeeper;
-        ctl.inputDirection = rawDir;
-        ctl.inputVelocityFloat = rawVel;
-        eliza->lastDesiredDirection = rawDir.Length() != 0 ? rawDir : Dir();
-        eliza->lastDesiredVelocity = rawVel;
-        if (m.inPlay && !m.inSetPiece) {
+        if (part == kLinePart) FieldStrategyRequestInput(LineOfRole(role), input, inputVel);
+        if (onTheBall) GetOnTheBallCommands(input, inputVel);
+        bool forceMagnet = PressureOrdered(role), extraHaste = false;
+        ctl.inputDirection = input;
+        ctl.inputVelocityFloat = inputVel;
+        eliza->lastDesiredDirection = input.Length() != 0 ? input : Dir();
+        eliza->lastDesiredVelocity = inputVel;
+        const bool openPlay = m.inPlay && !m.inSetPiece;
+        if (openPlay) {
             BallControlCommand();
             TrapCommand();
             InterfereCommand(false);
             SlidingCommand();
         }
-        if (!manual && m.inPlay && !m.inSetPiece) {
-            if (p != m.designatedPossessionPlayer) PressOpponent(forceMagnet, extraHaste);
-            ctl.inputVelocityFloat = RangeVelocity(ctl.inputVelocityFloat);
-            MovementCommand(forceMagnet, extraHaste);
-        } else {
-            PlayerCommand cmd = DefaultPlayerCommand();
-            cmd.useDesiredMovement = true;
-            cmd.desiredDirection = manualDir;
-            cmd.desiredVelocityFloat = manualVel;
-            cmd.useDesiredLookAt = true;
-            cmd.desiredLookAt = Pos() + (MentalBall(40).Get2D() - Pos()).Normalized(0) * 10.0f;
-            q.push_back(cmd);
+        if (ownMovement || !openPlay) {
+            OwnMovement(own, ownVel);
+            return true;
         }
+        if (p != m.designatedPossessionPlayer) PressOpponent(forceMagnet, extraHaste);
+        ctl.inputVelocityFloat = RangeVelocity(ctl.inputVelocityFloat);
+        MovementCommand(forceMagnet, extraHaste);
         return true;
     }
 };

@@ -149,8 +149,6 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_time_needed(co
     }
 }
 
-// The engine's math routines for tests, by the codes of eng::libm::EvaluateFloat and
-// EvaluateDouble: on arrays, and on the consecutive float bit patterns from `first`.
 // The bytes of one environment's blocks in device memory: World, EnvCore, EnvSlot and Scratch. The
 // engine's structs have the same layout on the host and the device.
 extern "C" __attribute__((visibility("default"))) void cuju_debug_layout(unsigned long long *out) {
@@ -159,6 +157,8 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_layout(unsigne
     out[2] = sizeof(eng::EnvSlot);
     out[3] = sizeof(eng::Scratch);
 }
+// The engine's math routines for tests, by the codes of eng::libm::EvaluateFloat and
+// EvaluateDouble: on arrays, and on the consecutive float bit patterns from `first`.
 extern "C" __attribute__((visibility("default"))) void cuju_debug_libm(int which, const float *x, const float *y, float *out,
                                                                          long long count) {
     for (long long i = 0; i < count; i++) out[i] = eng::libm::EvaluateFloat(which, x[i], y[i]);

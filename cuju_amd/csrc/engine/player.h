@@ -503,9 +503,9 @@ HD bool CarryRetainedBall(World &w, const Ctx &c, int p, const Anim &a, const An
         return false;
     }
     const Skeleton &sk = c.skeletons[p];
-    Derived der[kHumanoidNodes];
-    DeriveNodes(sk, h.nodes, der);
-    const Derived &node = der[sk.nodeMap[part]];
+    Transform der[kHumanoidNodes];
+    WorldTransforms(sk, h.nodes, der);
+    const Transform &node = der[sk.nodeMap[part]];
     BallTouch(w, c, Vec3(0));
     // BallSetPosition predicts again from its own position before anything reads the
     // predictions, so this rotation's prediction is left out.

@@ -433,11 +433,11 @@ HDN bool CheckBallCollisions(World &w, const Ctx &c) {
         const float reach = BodyReach(pl);
         if (!(((h.spatial.position + Vec3(0, 0, 0.8f)) - BallPredict(m.ball, 0)).Length() < 2.5f)) continue;
         const Skeleton &sk = c.skeletons[p];
-        Derived der[kHumanoidNodes];
-        DeriveNodes(sk, h.nodes, der);
+        Transform der[kHumanoidNodes];
+        WorldTransforms(sk, h.nodes, der);
         for (int n = 0; n < sk.nodeCount; n++) {
             for (int g = 0; g < sk.nodes[n].geometryCount; g++) {
-                const WorldGeometry part = GeometryWorld(sk.nodes[n].geometries[g], der[n]);
+                const WorldGeometry part = PlacedGeometry(sk.nodes[n].geometries[g], der[n]);
                 const float radius = 0.11f + reach;
                 const Vec3 ball = BallPredict(m.ball, 0);
                 if (!part.box.Intersects(ball, radius)) continue;
@@ -529,13 +529,13 @@ HD bool BoxesIntersect(const Aabb &a, const Aabb &o) {
 }
 HDN void PlayerGeometries(const World &w, const Ctx &c, int p, PlayerGeometryList &out) {
     const Skeleton &sk = c.skeletons[p];
-    Derived der[kHumanoidNodes];
-    DeriveNodes(sk, Hum(w, p).nodes, der);
+    Transform der[kHumanoidNodes];
+    WorldTransforms(sk, Hum(w, p).nodes, der);
     out.clear();
     for (int n = 0; n < sk.nodeCount; n++)
         for (int g = 0; g < sk.nodes[n].geometryCount; g++) {
             const SkelGeometry &sg = sk.nodes[n].geometries[g];
-            out.push_back(PlayerGeometry{sg.footOrLowerLeg, GeometryWorld(sg, der[n])});
+            out.push_back(PlayerGeometry{sg.footOrLowerLeg, PlacedGeometry(sg, der[n])});
         }
 }
 

@@ -352,20 +352,19 @@ struct Aabb {
         lo = Vec3(largest, largest, largest);
         hi = Vec3(smallest, smallest, smallest);
     }
+    // Grows the box to hold `p`, axis by axis (a zero bound keeps the sign it was first set with).
+    HD void Hold(const Vec3 &p) {
+        for (int k = 0; k < 3; k++) {
+            if (p.v[k] < lo.v[k]) lo.v[k] = p.v[k];
+            if (p.v[k] > hi.v[k]) hi.v[k] = p.v[k];
+        }
+    }
+    // The box that holds this one turned by `r`: its eight corners turned, taken x fastest, then y,
+    // then z.
     HDN Aabb Rotated(const Quat &r) const {
-        Vec3 corners[8] = {Vec3(lo.v[0], lo.v[1], lo.v[2]), Vec3(hi.v[0], lo.v[1], lo.v[2]),
-                           Vec3(lo.v[0], hi.v[1], lo.v[2]), Vec3(hi.v[0], hi.v[1], lo.v[2]),
-                           Vec3(lo.v[0], lo.v[1], hi.v[2]), Vec3(hi.v[0], lo.v[1], hi.v[2]),
-                           Vec3(lo.v[0], hi.v[1], hi.v[2]), Vec3(hi.v[0], hi.v[1], hi.v[2])};
         Aabb b;
         b.Reset();
-        for (Vec3 &cn : corners) {
-            cn = r * cn;
-            for (int k = 0; k < 3; k++) {
-                if (cn.v[k] < b.lo.v[k]) b.lo.v[k] = cn.v[k];
-                if (cn.v[k] > b.hi.v[k]) b.hi.v[k] = cn.v[k];
-            }
-        }
+        for (int i = 0; i < 8; i++) b.Hold(r * Vec3((i & 1 ? hi : lo).v[0], (i & 2 ? hi : lo).v[1], (i & 4 ? hi : lo).v[2]));
         return b;
     }
     HD Aabb Translated(const Vec3 &o) const {

@@ -119,6 +119,20 @@ extern "C" __attribute__((visibility("default"))) void cuju_debug_episode_seeds(
     for (int i = 0; i < count; i++) out[i] = eng::DrawEpisodeSeed(*g);
 }
 
+// The world generator seeded with `seed`: `count` raw words, then `count` uniform floats in
+// [low, high) from a second generator of the same seed.
+extern "C" __attribute__((visibility("default"))) void cuju_debug_world_rng(unsigned int seed, int count, float low, float high,
+                                                                              unsigned int *words, float *uniforms) {
+    uint8_t bytes[sizeof(eng::World::rng)];
+    eng::Rng g{bytes};
+    g.Seed(seed);
+    for (int i = 0; i < count; i++) words[i] = g.Next();
+    g.Seed(seed);
+    g.Store(eng::Rng::kLowAt, low);
+    g.Store(eng::Rng::kHighAt, high);
+    for (int i = 0; i < count; i++) uniforms[i] = g.Uniform();
+}
+
 // GRF's time-to-target estimate for `count` cases: directly, along the shared walk, and by the
 // possession scan's shortcut (usual and optimistic times of each, direct first); tests compare them.
 extern "C" __attribute__((visibility("default"))) void cuju_debug_time_needed(const float *cases, int count, unsigned int *out) {

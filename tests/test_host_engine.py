@@ -82,6 +82,36 @@ def test_episode_seeds_follow_cpython_random(host_library):
         assert out.tolist() == [rng.randint(0, 2000000000) for _ in range(8)]
 
 
+def test_world_generator_is_mt19937(host_library):
+    """The world's generator against numpy's MT19937 under Knuth's seeding (std::mt19937's and
+    Boost's seed; Boost's extra normalization touches only bits no draw reads), over 2,000 words
+    (three state renewals), and its uniform floats against that word stream: each is the word
+    over 2**32 in float, scaled to [low, high), drawn again when it rounds up to `high`."""
+    lib = ctypes.CDLL(host_library)
+    lib.cuju_debug_world_rng.argtypes = [ctypes.c_uint, ctypes.c_int, ctypes.c_float, ctypes.c_float,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    last, unused = np.zeros(10000, dtype=np.uint32), np.zeros(10000, dtype=np.float32)
+    lib.cuju_debug_world_rng(5489, 10000, 0.0, 1.0, last.ctypes.data, unused.ctypes.data)
+    assert int(last[-1]) == 4123659995  # the C++ standard's check of std::mt19937 (seed 5489)
+    count = 2000
+    for seed, low, high in [(5489, 0.0, 1.0), (0, -3.0, 5.5), (2**32 - 1, 1.0, 4.0), (1, 0.0, 1e-30)]:
+        words = np.zeros(count, dtype=np.uint32)
+        uniforms = np.zeros(count, dtype=np.float32)
+        lib.cuju_debug_world_rng(seed, count, low, high, words.ctypes.data, uniforms.ctypes.data)
+        bits = np.random.MT19937()
+        bits._legacy_seeding(seed)
+        stream = bits.random_raw(3 * count).astype(np.uint32)
+        assert words.tolist() == stream[:count].tolist()
+        lo, hi = np.float32(low), np.float32(high)
+        expected, k = [], 0
+        while len(expected) < count:
+            r = np.float32(np.float32(stream[k]) / np.float32(2.0**32)) * np.float32(hi - lo) + lo
+            k += 1
+            if r < hi:
+                expected.append(np.float32(r))
+        assert uniforms.tobytes() == np.array(expected, dtype=np.float32).tobytes()
+
+
 @pytest.mark.parametrize('assets', ['11_vs_11_hard_stochastic_l11_r0', 'academy_corner_l1_r0'])
 def test_set_state_continues_as_the_reference(assets, reference_library, host_library):
     """States of a played batch load into another batch (environments shuffled) in the reference

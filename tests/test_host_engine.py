@@ -349,6 +349,33 @@ def test_host_engine_smm_and_raw_match_reference(representation, stacked, with_r
         theirs.close()
 
 
+def test_every_action_of_the_full_set_plays_as_the_reference(reference_library, host_library):
+    """Random actions over all 33 of the `full` set (presses, releases, the built-in AI, keeper
+    rush, pressure and switch) on agents of both teams, several per team, with the raw arrays
+    (which hold each agent's sticky actions) and the states at the end, against the reference
+    library (environment.h:14-330)."""
+    options = dict(environment_count=4, seed=11, threads=2, action_set='full', with_raw=True,
+                   assignment=[0, 1, 0, 1])
+    assets = ['11_vs_11_kaggle_l3_r2', '5_vs_5_l2_r3']
+    mine = ref.ReferenceBatch(assets, library_path=host_library, **options)
+    theirs = ref.ReferenceBatch(assets, library_path=reference_library, **options)
+    rng = np.random.default_rng(33)
+    try:
+        assert mine.action_count == 33
+        assert _same(mine.reset(), theirs.reset())
+        for step in range(160):
+            actions = rng.integers(0, 33, size=(4, mine.agents)).astype(np.int32)
+            a, b = mine.step(actions), theirs.step(actions)
+            for x, y, what in zip(a, b, ('observation', 'reward', 'done')):
+                assert _same(x, y), f'{what} at step {step}'
+            assert _same(mine.raw(), theirs.raw()), f'raw at step {step}'
+        for e in range(4):
+            assert mine.get_state(e) == theirs.get_state(e), f'state of environment {e}'
+    finally:
+        mine.close()
+        theirs.close()
+
+
 def test_difficulty_override_plays_as_the_reference(reference_library, host_library):
     """Per-environment difficulties (negative keeps the scenario's) change the AI identically."""
     difficulty = np.array([[-1.0, 0.25], [0.75, -1.0], [0.1, 0.9]], dtype=np.float32)

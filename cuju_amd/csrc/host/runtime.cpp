@@ -458,7 +458,7 @@ void BatchRuntime::SetState(int env, const std::string &bytes, int prevScoreDiff
     core->prevScoreDiff = prevScoreDiff;
     core->prevGameMode = prevGameMode;
     core->prevBallOwnedTeam = prevBallOwnedTeam;
-    EnvironmentGetState(*w, c, core->obs);
+    Observe(*w, c, core->obs);
     auto slot = std::make_unique<EnvSlot>();
     dev_->ToHost(slot.get(), b_.slots + env, sizeof(EnvSlot));
     slot->variant = variant;

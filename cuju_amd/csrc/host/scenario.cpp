@@ -438,7 +438,7 @@ BuiltVariant BuildVariant(const ScenarioDescription &d, bool reverse, const Anim
 
     // GRF: creating the match draws the idle frames, the officials' skin and the lighting.
     InitializePlayerTeams(w);
-    if (!EnvironmentResetFromTemplate(w, c, seed)) throw std::runtime_error("the simulation does not support the creation of this scenario");
+    if (!ResetFromTemplate(w, c, seed)) throw std::runtime_error("the simulation does not support the creation of this scenario");
     // GRF: `Team::AddHumanGamers` takes each team's player closest to the ball at the origin.
     for (int teamID = 0; teamID < 2; teamID++)
         TeamByID(w, teamID).designatedTeamPossessionPlayer = GetClosestPlayer(w, c, teamID, BallPredict(m.ball, 0).Get2D(), false);
@@ -451,7 +451,7 @@ BuiltVariant BuildVariant(const ScenarioDescription &d, bool reverse, const Anim
     auto played = std::make_unique<World>(w);
     auto core = std::make_unique<EnvCore>();
     memset(core.get(), 0, sizeof(EnvCore));
-    if (!EnvironmentCoreAfterReset(*played, c, *core))
+    if (!SettleAfterReset(*played, c, *core))
         throw std::runtime_error("the simulation does not support the ticks that bring this scenario into play");
     std::vector<const NodeState *> nodes;
     for (int p = 0; p < m.playerCount; p++) nodes.push_back(played->match.players[p].base.humanoid.nodes);

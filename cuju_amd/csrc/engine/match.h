@@ -298,6 +298,9 @@ HDN void MatchFetchPutBuffers(World &w, const Ctx &c) {
 }
 // One 10 ms tick of the game.
 HDN bool GameTick(World &w, const Ctx &c) {
+#if !ENG_DEVICE
+    HostTicks()++;
+#endif
     bool ok;
     bool process = MatchProcess(w, c, ok);
     if (!ok) return false;

@@ -43,8 +43,16 @@ public:
         });
     }
     void Step(const Batch &b, const int32_t *actions, void *) override {
-        ForEach(b.count, [&](int e) { return StepEnvironment(b, e, actions); });
+        stepTicks_.assign(b.count, 0);
+        ForEach(b.count, [&](int e) {
+            const long long before = HostTicks();
+            const bool ok = StepEnvironment(b, e, actions);
+            stepTicks_[e] = HostTicks() - before;
+            return ok;
+        });
     }
+    // The ticks each environment ran in the last step, its auto-reset's included.
+    const std::vector<long long> &StepTicks() const { return stepTicks_; }
     void Outputs(const Batch &b, int env, void *) override { WriteEnvironmentOutputs(b, env, false); }
 
 private:
@@ -78,8 +86,19 @@ private:
     }
     int threads_;
     std::string fault_;
+    std::vector<long long> stepTicks_;
 };
 }  // namespace
+
+// The ticks each environment ran in the batch's last step: GRF's step ticks until play, so a
+// stoppage makes one environment step run many more than the ticks per step.
+extern "C" __attribute__((visibility("default"))) int cuju_debug_step_ticks(void *environment, long long *out) {
+    auto *device = dynamic_cast<HostDevice *>(&static_cast<BatchRuntime *>(environment)->Dev());
+    if (!device) return -1;
+    const std::vector<long long> &ticks = device->StepTicks();
+    std::copy(ticks.begin(), ticks.end(), out);
+    return (int)ticks.size();
+}
 
 std::unique_ptr<Device> MakeLibraryDevice(int threads, int) { return std::make_unique<HostDevice>(threads); }
 extern const char *const kBackendName = "host";

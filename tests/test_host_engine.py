@@ -376,6 +376,30 @@ def test_every_action_of_the_full_set_plays_as_the_reference(reference_library, 
         theirs.close()
 
 
+@pytest.mark.parametrize('ticks_per_step', [10, 5])
+def test_a_step_ticks_until_play(ticks_per_step, host_library):
+    """GRF's environment step runs whole steps of ticks until play is on (environment.h:539-556):
+    every environment step runs a positive multiple of the ticks per step, and a stoppage makes
+    some run many more. The host build counts the ticks of each environment step."""
+    batch = ref.ReferenceBatch('11_vs_11_hard_stochastic_l11_r0', environment_count=96, seed=0, threads=4,
+                               library_path=host_library, physics_steps_per_frame=ticks_per_step)
+    lib = ref.library(host_library)
+    lib.cuju_debug_step_ticks.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    ticks = np.zeros(96, dtype=np.int64)
+    seen = []
+    try:
+        batch.reset()
+        for step in range(40):
+            batch.step(digest_actions(step, 96, batch.agents, batch.action_count))
+            assert lib.cuju_debug_step_ticks(batch._handle, ticks.ctypes.data) == 96
+            seen.append(ticks.copy())
+    finally:
+        batch.close()
+    seen = np.array(seen)
+    assert (seen >= ticks_per_step).all() and (seen % ticks_per_step == 0).all()
+    assert (seen > ticks_per_step).any()
+
+
 def test_difficulty_override_plays_as_the_reference(reference_library, host_library):
     """Per-environment difficulties (negative keeps the scenario's) change the AI identically."""
     difficulty = np.array([[-1.0, 0.25], [0.75, -1.0], [0.1, 0.9]], dtype=np.float32)

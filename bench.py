@@ -61,11 +61,11 @@ MEASURED_TRAFFIC = {
     (3, 16384, 5, 20, 3): (180356929366, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
     (4, 8192, 5, 20, 3): (103799821236, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
     (5, 32768, 5, 20, 3): (174769688406, 'profiles/step_kernel_mixed_32768_driver_window.md'),
-    (1, 64, 100, 30, 3): (73175198, 'profiles/step_kernel_5v5_64.md'),
-    (2, 4096, 100, 30, 3): (62038437940, 'profiles/step_kernel_11v11_4096.md'),
-    (3, 16384, 100, 30, 3): (183560102391, 'profiles/step_kernel_11v11_hard_16384.md'),
-    (4, 8192, 100, 30, 3): (106199422724, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
-    (5, 32768, 100, 30, 3): (183738509781, 'profiles/step_kernel_mixed_32768.md'),
+    (1, 64, 100, 30, 3): (72495638, 'profiles/step_kernel_5v5_64.md'),
+    (2, 4096, 100, 30, 3): (61081372503, 'profiles/step_kernel_11v11_4096.md'),
+    (3, 16384, 100, 30, 3): (182212291889, 'profiles/step_kernel_11v11_hard_16384.md'),
+    (4, 8192, 100, 30, 3): (104878188369, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
+    (5, 32768, 100, 30, 3): (182231472159, 'profiles/step_kernel_mixed_32768.md'),
 }
 
 

@@ -365,7 +365,8 @@ HDN bool OfficialHumanoidProcess(World &w, const Ctx &c, int official) {
     h.decayingPositionOffset *= 0.95f;
     if ((double)h.decayingPositionOffset.Length() < 0.005) h.decayingPositionOffset = Vec3(0);
     h.decayingDifficultyFactor = Clamp(h.decayingDifficultyFactor - 0.002f, 0.0f, 1.0f);
-    CalculateSpatialState(c, h);
+    h.spatial = c.ws->spatialAhead[kPlayers + official];
+    h.prevPosition2D = h.spatial.position;
     h.spatial.positionOffsetMovement = Vec3(0);
     cur.frameNum++;
     h.prevAnimFrameNum++;
@@ -379,6 +380,11 @@ HDN bool OfficialHumanoidProcess(World &w, const Ctx &c, int official) {
 }
 HDN bool OfficialsProcess(World &w, const Ctx &c) {
     ENG_SCOPE(15);
+    // The three spatial states for the tick at once, as a team's players' are: each reads its own
+    // official's animation and last position, which the others' ticks leave alone.
+    for (int o = GroupRank(); o < 3; o += kGroupLanes)
+        c.ws->spatialAhead[kPlayers + o] = NextSpatialState(c, w.match.officials[o].humanoid);
+    GroupSync();
     for (int o = 0; o < 3; o++)
         if (!OfficialHumanoidProcess(w, c, o)) return false;
     return true;

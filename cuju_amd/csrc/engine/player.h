@@ -367,7 +367,8 @@ HDN void HumanoidProcessBegin(World &w, const Ctx &c, int p) {
     if ((double)h.decayingPositionOffset.Length() < 0.005) h.decayingPositionOffset = Vec3(0);
     h.decayingDifficultyFactor = Clamp(h.decayingDifficultyFactor - 0.002f, 0.0f, 1.0f);
     h.mentalImageTime = w.match.lastTouchTeamID == t ? 0 : GetReactionTimeMs(w, c, p);
-    CalculateSpatialState(c, h);
+    h.spatial = c.ws->spatialAhead[p];
+    h.prevPosition2D = h.spatial.position;
     h.spatial.positionOffsetMovement = Vec3(0);
     cur.frameNum++;
     h.prevAnimFrameNum++;

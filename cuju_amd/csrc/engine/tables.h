@@ -450,6 +450,7 @@ struct Scratch {
     TimeWalk walk;  // the match's sequential code
     double keys[kMaxAnimations];
     int16_t order[2][kMaxAnimations];
+    SpatialState spatialAhead[kPlayers + 3];  // spatial states computed ahead: the players', then the officials'
 };
 
 // Everything a match reads besides its world: the shared tables, its variant's static data and

@@ -573,6 +573,15 @@ HD void ReconsiderDesignatedPlayer(World &w, int teamID) {
 // A team's tick: possession amounts, gamers' automatic selection, the team AI with dynamic roles
 // and man marking (staggered between the teams), its players, gamer switches and the designated
 // player.
+// Each active player's spatial state for the tick, on the group's lanes at once: it reads the
+// player's own animation and last position only, which no other player's tick changes, so each
+// player's turn takes it from the match's scratch block instead of computing it in order.
+HDN void SpatialStatesAhead(World &w, const Ctx &c, int teamID) {
+    const PlayerList ahead = TeamActivePlayers(w, teamID);
+    for (int i = GroupRank(); i < ahead.count; i += kGroupLanes)
+        c.ws->spatialAhead[ahead[i]] = NextSpatialState(c, Hum(w, ahead[i]));
+    GroupSync();
+}
 HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
     ENG_SCOPE(25);
     MatchState &m = w.match;
@@ -584,6 +593,7 @@ HDN bool TeamProcess(World &w, const Ctx &c, int teamID) {
         if ((m.actualTimeMs + off) % 400 == 0 && !TeamCalculateDynamicRoles(w, c, teamID)) return false;
         if ((m.actualTimeMs + off + 100) % 400 == 0 && !TeamCalculateManMarking(w, c, teamID)) return false;
     }
+    SpatialStatesAhead(w, c, teamID);
     // The active players of the team in state order, each checked when its turn comes. A match
     // whose next humanoid needs a new animation stops there until every match of the wavefront has
     // stopped or finished, so that the interruptions run together; each match still processes

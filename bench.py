@@ -56,11 +56,11 @@ CPU_SAMPLE = 2048
 # (each scaled by what the counter reads for a 1 GiB device copy), keyed by (workload,
 # environments, warm-up steps, timed steps, rounds): the window of launches the profile averaged.
 MEASURED_TRAFFIC = {
-    (1, 64, 5, 20, 3): (70078927, 'profiles/step_kernel_5v5_64_driver_window.md'),
-    (2, 4096, 5, 20, 3): (61112313590, 'profiles/step_kernel_11v11_4096_driver_window.md'),
-    (3, 16384, 5, 20, 3): (180356929366, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
-    (4, 8192, 5, 20, 3): (103799821236, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
-    (5, 32768, 5, 20, 3): (174769688406, 'profiles/step_kernel_mixed_32768_driver_window.md'),
+    (1, 64, 5, 20, 3): (73289833, 'profiles/step_kernel_5v5_64_driver_window.md'),
+    (2, 4096, 5, 20, 3): (63427466912, 'profiles/step_kernel_11v11_4096_driver_window.md'),
+    (3, 16384, 5, 20, 3): (188039431955, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
+    (4, 8192, 5, 20, 3): (108637917918, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
+    (5, 32768, 5, 20, 3): (183701236223, 'profiles/step_kernel_mixed_32768_driver_window.md'),
     (1, 64, 100, 30, 3): (72495638, 'profiles/step_kernel_5v5_64.md'),
     (2, 4096, 100, 30, 3): (61081372503, 'profiles/step_kernel_11v11_4096.md'),
     (3, 16384, 100, 30, 3): (182212291889, 'profiles/step_kernel_11v11_hard_16384.md'),

@@ -568,6 +568,97 @@ HD Vec3 PredFlip(const Vec3 *pred, bool flip, int ms) {
     return v;
 }
 
+// GRF's earliest time to the ball over the 3 s of predictions. It visits points of the prediction
+// from `start` at a stride of the ball's distance (10 to 500 ms) until the walk reaches one in its
+// usual time, then goes back to the point before and steps 10 ms at a time to the first that is
+// reached; the optimistic time is the first visited point reached optimistically. Points above
+// 1.5 m count as unreached.
+//
+// Here `lanes` lanes of the match share one scan (this one is `lane`): the points before the
+// refinement follow from the prediction alone, so every lane walks them and each evaluates the
+// walk at its own point of a round of `lanes`; the lowest reached point of a round ends the coarse
+// part, and the refinement's 10 ms points are shared the same way. What the scan visits, and so
+// its result, is the same for any number of lanes.
+HDN ScanResult SharedPossessionScan(const Vec3 *pred, bool flip, const Vec3 &pos, const Vec3 &mov, float maxVel,
+                                    bool precise, uint32_t start, int lane, int lanes) {
+    ENG_SCOPE(35);
+    ScanResult s;
+    {
+        uint32_t latest = kBallPredictionSpanMs;
+        uint32_t direct = TruncToUint32(roundf(
+            (PredFlip(pred, flip, kBallPredictionSpanMs - 10).Get2D() - (pos + mov * 0.2f)).Length() /
+            (maxVel * 0.75f) * 1000));
+        s.timeToBall = latest > direct ? latest : direct;
+    }
+    s.timeToBallOptimistic = s.timeToBall;
+    TimeNeededScan times(pos, mov, maxVel);
+    const int base = GroupRank() - lane;
+    const LaneMask mine = lanes >= 64 ? ~(LaneMask)0 : (((LaneMask)1 << lanes) - 1u);
+    // This lane's point: whether the walk reaches it usually and optimistically (never above 1.5 m).
+    auto evaluate = [&](uint32_t ms, bool &usual, bool &optimistic) {
+        usual = optimistic = false;
+        const Vec3 at = PredFlip(pred, flip, (int)ms);
+        if (!(at.v[2] < 1.5f)) return;
+        const TimeNeeded r = times.Get(at.Get2D(), precise, ms);
+        usual = r.usual <= ms;
+        optimistic = r.optimistic <= ms;
+    };
+    // The round's lowest usual hit, or -1; the optimistic time takes the lowest optimistic hit up
+    // to it (the points of a round rise with the lane).
+    auto settle = [&](bool usual, bool optimistic, uint32_t ms) {
+        const LaneMask hits = (GroupBallot(usual) >> base) & mine;
+        LaneMask opts = (GroupBallot(optimistic) >> base) & mine;
+        if (hits) opts &= LanesThrough(LowestBit(hits));
+        if (opts) {
+            const uint32_t o = GroupShuffle(ms, base + LowestBit(opts));
+            if (o < s.timeToBallOptimistic) s.timeToBallOptimistic = o;
+        }
+        return hits ? LowestBit(hits) : -1;
+    };
+    uint32_t ms = start, prev = 0, from = 0, to = 0;
+    bool reached = false;
+    while (!reached && ms < kBallPredictionSpanMs) {
+        uint32_t myMs = 0, myPrev = 0;
+        bool here = false;
+        for (int t = 0; t < lanes && ms < kBallPredictionSpanMs; t++) {
+            if (t == lane) {
+                myMs = ms;
+                myPrev = prev;
+                here = true;
+            }
+            const float dist = (pos - PredFlip(pred, flip, (int)ms).Get2D()).Length() + 0.2f;
+            const uint32_t toGo = (uint32_t)TruncToInt32(roundf((dist / 50.0f) * 1000.0f));
+            uint32_t stepMs = TruncToUint32(Clamp((float)toGo, 10, 500));
+            stepMs = (stepMs / 10) * 10;
+            prev = ms;
+            ms += stepMs;
+        }
+        bool usual = false, optimistic = false;
+        if (here) evaluate(myMs, usual, optimistic);
+        const int hit = settle(usual, optimistic, myMs);
+        if (hit >= 0) {
+            from = GroupShuffle(myPrev, base + hit);
+            to = GroupShuffle(myMs, base + hit);
+            reached = true;
+        }
+    }
+    if (!reached) return s;
+    // The refinement reaches `to` at the latest, where the coarse part already did.
+    for (uint32_t r0 = from + 10; r0 <= to; r0 += 10 * (uint32_t)lanes) {
+        const uint32_t myMs = r0 + 10 * (uint32_t)lane;
+        bool usual = false, optimistic = false;
+        if (myMs <= to) evaluate(myMs, usual, optimistic);
+        const int hit = settle(usual, optimistic, myMs);
+        if (hit >= 0) {
+            s.timeToBall = r0 + 10 * (uint32_t)hit;
+            return s;
+        }
+    }
+    s.timeToBall = to;
+    return s;
+}
+
+// The same scan on one lane, point after point.
 HDN ScanResult PossessionScan(const Vec3 *pred, bool flip, const Vec3 &pos, const Vec3 &mov, float maxVel,
                               bool precise, uint32_t start) {
     ENG_SCOPE(35);
@@ -628,7 +719,7 @@ HDN bool HasPossession(const World &w, int p) {
 
 HD bool IsPassOrShot(int f) { return f == kFnShortPass || f == kFnLongPass || f == kFnHighPass || f == kFnShot; }
 
-HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p) {
+HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p, int lane = 0, int lanes = 1) {
     Player &ps = w.match.players[p];
     const Humanoid &h = ps.base.humanoid;
     const Ball &b = w.match.ball;
@@ -641,7 +732,10 @@ HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p)
     const bool touchPending = h.anim.frameNum < h.anim.touchFrame;
     if (IsPassOrShot(h.anim.functionType) && !touchPending) start = 500;
     bool precise = team.designatedTeamPossessionPlayer == p;
-    ScanResult s = PossessionScan(b.predictions, b.lazyFlip, pos, mov, maxVel, precise, start);
+    // The host build runs the shared scan with one lane, so its tests check that scan's order.
+    const ScanResult s = lanes > 1 || !ENG_DEVICE
+                             ? SharedPossessionScan(b.predictions, b.lazyFlip, pos, mov, maxVel, precise, start, lane, lanes)
+                             : PossessionScan(b.predictions, b.lazyFlip, pos, mov, maxVel, precise, start);
     ps.timeToBallMs = s.timeToBall;
     ps.timeToBallOptimisticMs = s.timeToBallOptimistic;
     if (h.anim.touchFrame != -1 && touchPending) {
@@ -674,9 +768,15 @@ HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p)
 HDN void TeamUpdatePossessionStatistics(World &w, const Ctx &c, int teamID) {
     ENG_SCOPE(16);
     // A player's statistics read only the ball, the opposing team and its own fields, so the lanes
-    // of the match take the players in turn.
+    // of the match take the players in turn; a group with lanes to spare gives each player as many
+    // lanes as it can, which share its scan (they write the same results).
     const PlayerList players = TeamActivePlayers(w, teamID);
-    for (int i = GroupRank(); i < players.count; i += kGroupLanes) PlayerUpdatePossessionStatistics(w, *c.sd, players[i]);
+    const int share = players.count > 0 && kGroupLanes >= 2 * players.count ? kGroupLanes / players.count : 1;
+    if (share == 1) {
+        for (int i = GroupRank(); i < players.count; i += kGroupLanes) PlayerUpdatePossessionStatistics(w, *c.sd, players[i]);
+    } else if (GroupRank() < share * players.count) {
+        PlayerUpdatePossessionStatistics(w, *c.sd, players[GroupRank() / share], GroupRank() % share, share);
+    }
     GroupSync();
     // The team's summary over its active players in state order, kept in registers and stored once.
     bool hasPossession = false;

@@ -56,11 +56,11 @@ CPU_SAMPLE = 2048
 # (each scaled by what the counter reads for a 1 GiB device copy), keyed by (workload,
 # environments, warm-up steps, timed steps, rounds): the window of launches the profile averaged.
 MEASURED_TRAFFIC = {
-    (1, 64, 5, 20, 3): (73289833, 'profiles/step_kernel_5v5_64_driver_window.md'),
-    (2, 4096, 5, 20, 3): (63427466912, 'profiles/step_kernel_11v11_4096_driver_window.md'),
-    (3, 16384, 5, 20, 3): (188039431955, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
-    (4, 8192, 5, 20, 3): (108637917918, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
-    (5, 32768, 5, 20, 3): (183701236223, 'profiles/step_kernel_mixed_32768_driver_window.md'),
+    (1, 64, 5, 20, 3): (74510143, 'profiles/step_kernel_5v5_64_driver_window.md'),
+    (2, 4096, 5, 20, 3): (64544411205, 'profiles/step_kernel_11v11_4096_driver_window.md'),
+    (3, 16384, 5, 20, 3): (187948348015, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
+    (4, 8192, 5, 20, 3): (108514748425, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
+    (5, 32768, 5, 20, 3): (183745304461, 'profiles/step_kernel_mixed_32768_driver_window.md'),
     (1, 64, 100, 30, 3): (75342188, 'profiles/step_kernel_5v5_64.md'),
     (2, 4096, 100, 30, 3): (63368742327, 'profiles/step_kernel_11v11_4096.md'),
     (3, 16384, 100, 30, 3): (190382653272, 'profiles/step_kernel_11v11_hard_16384.md'),

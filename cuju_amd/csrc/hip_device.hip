@@ -6,7 +6,7 @@
 // matches' divergent control flow runs one path after another (16 identical matches step in a
 // quarter of the time of 16 ordinary ones), and a match's own sequential chain of dependent loads
 // sets a floor that wider groups lower, since the loops of independent iterations split over the
-// group. This file is compiled once per group width (2, 4, 8 and 16 lanes), each copy with its own
+// group. This file is compiled once per group width (2, 4, 8, 16, 32 and 64 lanes), each copy with its own
 // kernels, fault words and device class.
 //
 // Occupancy. The step kernel is bounded to the registers of two wavefronts per SIMD (256 VGPRs,

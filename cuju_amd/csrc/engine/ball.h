@@ -768,15 +768,17 @@ HDN void PlayerUpdatePossessionStatistics(World &w, const StaticData &sd, int p,
 HDN void TeamUpdatePossessionStatistics(World &w, const Ctx &c, int teamID) {
     ENG_SCOPE(16);
     // A player's statistics read only the ball, the opposing team and its own fields, so the lanes
-    // of the match take the players in turn; a group with lanes to spare gives each player as many
-    // lanes as it can, which share its scan (they write the same results).
+    // of the match take the players in turn, one a lane in whole rounds. The players left after
+    // the whole rounds, when the group has at least two lanes for each, get as many lanes each as
+    // the group holds, which share the player's scan (they write the same results).
     const PlayerList players = TeamActivePlayers(w, teamID);
-    const int share = players.count > 0 && kGroupLanes >= 2 * players.count ? kGroupLanes / players.count : 1;
-    if (share == 1) {
-        for (int i = GroupRank(); i < players.count; i += kGroupLanes) PlayerUpdatePossessionStatistics(w, *c.sd, players[i]);
-    } else if (GroupRank() < share * players.count) {
-        PlayerUpdatePossessionStatistics(w, *c.sd, players[GroupRank() / share], GroupRank() % share, share);
-    }
+    const int whole = players.count - players.count % kGroupLanes;
+    const int rest = players.count - whole;
+    const int share = rest > 0 && kGroupLanes >= 2 * rest ? kGroupLanes / rest : 1;
+    const int single = share == 1 ? players.count : whole;
+    for (int i = GroupRank(); i < single; i += kGroupLanes) PlayerUpdatePossessionStatistics(w, *c.sd, players[i]);
+    if (share > 1 && GroupRank() < share * rest)
+        PlayerUpdatePossessionStatistics(w, *c.sd, players[whole + GroupRank() / share], GroupRank() % share, share);
     GroupSync();
     // The team's summary over its active players in state order, kept in registers and stored once.
     bool hasPossession = false;

@@ -61,11 +61,11 @@ MEASURED_TRAFFIC = {
     (3, 16384, 5, 20, 3): (189491064338, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
     (4, 8192, 5, 20, 3): (108512362680, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
     (5, 32768, 5, 20, 3): (183526186828, 'profiles/step_kernel_mixed_32768_driver_window.md'),
-    (1, 64, 100, 30, 3): (76477365, 'profiles/step_kernel_5v5_64.md'),
-    (2, 4096, 100, 30, 3): (64349349101, 'profiles/step_kernel_11v11_4096.md'),
-    (3, 16384, 100, 30, 3): (190108244493, 'profiles/step_kernel_11v11_hard_16384.md'),
-    (4, 8192, 100, 30, 3): (109445629387, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
-    (5, 32768, 100, 30, 3): (191104010544, 'profiles/step_kernel_mixed_32768.md'),
+    (1, 64, 100, 30, 3): (76344677, 'profiles/step_kernel_5v5_64.md'),
+    (2, 4096, 100, 30, 3): (64353806618, 'profiles/step_kernel_11v11_4096.md'),
+    (3, 16384, 100, 30, 3): (191785421254, 'profiles/step_kernel_11v11_hard_16384.md'),
+    (4, 8192, 100, 30, 3): (109437097192, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
+    (5, 32768, 100, 30, 3): (190759609408, 'profiles/step_kernel_mixed_32768.md'),
 }
 
 

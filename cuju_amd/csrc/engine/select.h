@@ -815,27 +815,42 @@ struct MovementPlanner {
         speed = StretchSprint(speed, kAnimSprintVelocity, maxVel);
         movement = movement.Normalized(0) * speed;
     }
+    // The terms of a frame that the carried velocity leaves alone: the animation's movement on the
+    // pitch, stretched to the top speed, its direction and lean toward the desired direction, and
+    // the sine and cosine of the frame's share of the steer.
+    HD PlanFrame Ahead(int frame) const {
+        PlanFrame a;
+        const float progress = Progress(frame);
+        a.raw = AnimationMovement(frame, progress);
+        Vec3 stretched = a.raw;
+        a.stretchedSpeed = a.raw.Length();
+        Stretch(stretched, a.stretchedSpeed);
+        a.lean = MaxF(0.0f, NormalizedMaximum(stretched, 1.0f).Dot(desiredDir));
+        a.unit = stretched.Normalized(0);
+        const float rotation = steer * progress;
+        a.rc = 1.0f;
+        a.rs = rotation;
+        // Below 2^-12 the sine is the argument and the cosine 1, by the test of sinf/cosf.
+        if (!(libm::Top12f(rotation) < libm::Top12f(0x1p-12f))) {
+            const libm::SinCos t = libm::sincosf(rotation);
+            a.rc = t.c;
+            a.rs = t.s;
+        }
+        return a;
+    }
     // What the carried velocity chases this frame: the desired speed held near the stretched
     // animation speed (down by 1.2 or 1.6 m/s; up by the carried excess, fading over the animation
     // and with the angle to the desired direction), along the stretched movement turned by the
     // frame's share of the steer, blended with the raw movement by the physics share.
-    HD Vec3 Target(const Vec3 &raw, const Vec3 &stretched, float stretchedSpeed, float progress, float carriedSpeed) const {
+    HD Vec3 Target(const PlanFrame &a, float progress, float carriedSpeed) const {
         float faster = 0.0f;
-        if (carriedSpeed > stretchedSpeed) faster = MinF(1.0f - progress, MaxF(0.0f, carriedSpeed - stretchedSpeed));
-        if (faster > 0) faster *= MaxF(0.0f, NormalizedMaximum(stretched, 1.0f).Dot(desiredDir));
+        if (carriedSpeed > a.stretchedSpeed) faster = MinF(1.0f - progress, MaxF(0.0f, carriedSpeed - a.stretchedSpeed));
+        if (faster > 0) faster *= a.lean;
         if (at == kAtSliding) faster = 100;
         const float slower = touch ? 1.2f : 1.6f;
-        const float speed = Clamp(desiredVel, stretchedSpeed - slower, stretchedSpeed + faster);
-        const float rotation = steer * progress;
-        float rc = 1.0f, rs = rotation;
-        // Below 2^-12 the sine is the argument and the cosine 1, by the test of sinf/cosf.
-        if (!(libm::Top12f(rotation) < libm::Top12f(0x1p-12f))) {
-            const libm::SinCos t = libm::sincosf(rotation);
-            rc = t.c;
-            rs = t.s;
-        }
-        const Vec3 turned = RotatedCS(stretched.Normalized(0) * speed, rc, rs);
-        return turned * physicsBias + raw * (1.0f - physicsBias);
+        const float speed = Clamp(desiredVel, a.stretchedSpeed - slower, a.stretchedSpeed + faster);
+        const Vec3 turned = RotatedCS(a.unit * speed, a.rc, a.rs);
+        return turned * physicsBias + a.raw * (1.0f - physicsBias);
     }
     // A turn sharper than the agility allows per frame (less at speed, more without a touch) sheds
     // carried speed in proportion to the excess.
@@ -887,15 +902,11 @@ struct MovementPlanner {
         if (!outgoingIdle && idle) return NormalizedTo(outgoingTurned, kDribbleVelocity);
         return v;
     }
-    // One frame: the new position.
-    HD Vec3 Step(int frame) {
+    // One frame, from its terms computed ahead: the new position.
+    HD Vec3 Step(int frame, const PlanFrame &a) {
         const float progress = Progress(frame);
-        const Vec3 raw = AnimationMovement(frame, progress);
-        Vec3 stretched = raw;
-        float stretchedSpeed = raw.Length();
-        Stretch(stretched, stretchedSpeed);
         const float carriedSpeed = velocity.Length();
-        Vec3 change = Target(raw, stretched, stretchedSpeed, progress, carriedSpeed) - velocity;
+        Vec3 change = Target(a, progress, carriedSpeed) - velocity;
         BoundTurn(change, carriedSpeed);
         BoundChange(change, carriedSpeed, frame);
         BoundGain(change, carriedSpeed);
@@ -1316,8 +1327,10 @@ struct Selector {
 
     // The movement plan of animation `ai` into `out` (see MovementPlanner); returns the velocity it
     // ends with and sets `rotationOffset`, the turn the plan adds to the animation's outgoing angle.
+    // `together`: every lane of the match makes this call with the same arguments, and they share
+    // the frames' terms; otherwise a lane plans alone.
     HDN Vec3 PlanMovement(int ai, bool useDesiredMovement, const Vec3 &desiredMovement, const Vec3 &desiredBodyRel, PList &out,
-                          float &rotationOffset) {
+                          float &rotationOffset, bool together) {
         ENG_SCOPE(38);
         const Anim &a = A(ai);
         const AnimDerived &d = D(ai);
@@ -1368,7 +1381,16 @@ struct Selector {
         plan.posCount = a.posCount;
         Vec3 *const frames = out.e;
         const int frameCount = a.frameCount;
-        for (int frame = 0; frame < frameCount; frame++) frames[frame] = plan.Step(frame);
+        if (together) {
+            // The lanes of the match compute the frames' terms ahead; the carried velocity then
+            // runs through them in order.
+            PlanFrame *const ahead = c.ws->planFrames;
+            for (int frame = GroupRank(); frame < frameCount; frame += kGroupLanes) ahead[frame] = plan.Ahead(frame);
+            GroupSync();
+            for (int frame = 0; frame < frameCount; frame++) frames[frame] = plan.Step(frame, ahead[frame]);
+        } else {
+            for (int frame = 0; frame < frameCount; frame++) frames[frame] = plan.Step(frame, plan.Ahead(frame));
+        }
         out.count = frameCount > 0 ? frameCount : 0;
         if (!plan.outgoingIdle && VelocityCat(plan.velocity.Length()) != kVelIdle)
             rotationOffset = RotatedBy(plan.velocity, BackTurn(angle)).Angle2D(a.outgoingMovement);
@@ -1487,7 +1509,7 @@ struct Selector {
     HDN bool TryTouchAnimation(const TouchSearch &ts, int ai, PList &plan, float &rotSmuggle, float &predAngle, Vec3 &outMov,
                                Vec3 &smuggle, int &touchFrame) {
         const Anim &a = A(ai);
-        PlanMovement(ai, ts.useDesiredMovement, ts.desiredMovement, ts.desiredBodyRel, plan, rotSmuggle);
+        PlanMovement(ai, ts.useDesiredMovement, ts.desiredMovement, ts.desiredBodyRel, plan, rotSmuggle, false);
         predAngle = ModulateIntoRange(-PI, PI, a.outgoingAngle.value() + rotSmuggle);
         outMov = RotatedBy(OutgoingMovementOf(plan), ts.back);
         const int total = a.footballCount, middle = total / 2;
@@ -1772,7 +1794,7 @@ struct Selector {
             lookRel = (RotatedBy((cmd.desiredLookAt - s.position).Get2D(), BackTurn(angle)) - A(sel).translation).Normalized(Vec3(0, -1, 0));
         PList plan{c.ws->plans[0], 0};
         float rotation = 0;
-        PlanMovement(sel, cmd.useDesiredMovement, cmd.desiredDirection * cmd.desiredVelocityFloat, lookRel, plan, rotation);
+        PlanMovement(sel, cmd.useDesiredMovement, cmd.desiredDirection * cmd.desiredVelocityFloat, lookRel, plan, rotation, true);
         if (interrupt == kIntReQueue && cur.positions.count > 1 && plan.count > 1 && RestartsCurrent(sel, fn, 0.20f * PI, false))
             return kSelectFalse;
         InstallAnimation(sel, fn, interrupt, -1, Vec3(), 1.0f, rotation, Vec3(), plan, cmd);
@@ -2062,7 +2084,7 @@ struct Selector {
         }
         if (physics) {
             ENG_SCOPE(48);
-            PlanMovement(sel, cmd.useDesiredMovement, cmd.desiredDirection * cmd.desiredVelocityFloat, lookRel, plan, rotation);
+            PlanMovement(sel, cmd.useDesiredMovement, cmd.desiredDirection * cmd.desiredVelocityFloat, lookRel, plan, rotation, true);
         }
         if (interrupt == kIntReQueue && sel != -1 && cur.positions.count > 1 && plan.count > 1 && RestartsCurrent(sel, fn, 0.06f * PI, true))
             sel = -1;

@@ -433,6 +433,13 @@ using PlayerBounceList = Small<PlayerBounce, kPlayers>;
 // Lanes of one match with a plan of their own in the candidate search.
 constexpr int kPlanLanes = kMaxGroupLanes;
 static_assert(kGroupLanes <= kPlanLanes, "every lane of a match needs a candidate plan");
+
+// A frame's terms of a movement plan that do not depend on the velocity it carries.
+struct PlanFrame {
+    Vec3 raw, unit;
+    float stretchedSpeed, lean, rc, rs;
+};
+
 // Per-match working memory: the animation selection's candidate lists, planned positions, sort keys
 // and one candidate plan per lane of the match, and the lists above. One block per environment in
 // HBM, which every lane of the match addresses, in place of large per-lane stack arrays: the lanes
@@ -451,6 +458,7 @@ struct Scratch {
     double keys[kMaxAnimations];
     int16_t order[2][kMaxAnimations];
     SpatialState spatialAhead[kPlayers + 3];  // spatial states computed ahead: the players', then the officials'
+    PlanFrame planFrames[kAnimPositions];     // a movement plan's frame terms, computed ahead
 };
 
 // Everything a match reads besides its world: the shared tables, its variant's static data and

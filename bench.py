@@ -56,11 +56,11 @@ CPU_SAMPLE = 2048
 # (each scaled by what the counter reads for a 1 GiB device copy), keyed by (workload,
 # environments, warm-up steps, timed steps, rounds): the window of launches the profile averaged.
 MEASURED_TRAFFIC = {
-    (1, 64, 5, 20, 3): (74513612, 'profiles/step_kernel_5v5_64_driver_window.md'),
-    (2, 4096, 5, 20, 3): (64536282450, 'profiles/step_kernel_11v11_4096_driver_window.md'),
-    (3, 16384, 5, 20, 3): (189491064338, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
-    (4, 8192, 5, 20, 3): (108512362680, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
-    (5, 32768, 5, 20, 3): (183526186828, 'profiles/step_kernel_mixed_32768_driver_window.md'),
+    (1, 64, 5, 20, 3): (75848861, 'profiles/step_kernel_5v5_64_driver_window.md'),
+    (2, 4096, 5, 20, 3): (65277143487, 'profiles/step_kernel_11v11_4096_driver_window.md'),
+    (3, 16384, 5, 20, 3): (191055945597, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
+    (4, 8192, 5, 20, 3): (109599148534, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
+    (5, 32768, 5, 20, 3): (185300503006, 'profiles/step_kernel_mixed_32768_driver_window.md'),
     (1, 64, 100, 30, 3): (76344677, 'profiles/step_kernel_5v5_64.md'),
     (2, 4096, 100, 30, 3): (64353806618, 'profiles/step_kernel_11v11_4096.md'),
     (3, 16384, 100, 30, 3): (191785421254, 'profiles/step_kernel_11v11_hard_16384.md'),

@@ -61,11 +61,11 @@ MEASURED_TRAFFIC = {
     (3, 16384, 5, 20, 3): (191055945597, 'profiles/step_kernel_11v11_hard_16384_driver_window.md'),
     (4, 8192, 5, 20, 3): (109599148534, 'profiles/step_kernel_11v11_selfplay_stacked_8192_driver_window.md'),
     (5, 32768, 5, 20, 3): (185300503006, 'profiles/step_kernel_mixed_32768_driver_window.md'),
-    (1, 64, 100, 30, 3): (76344677, 'profiles/step_kernel_5v5_64.md'),
-    (2, 4096, 100, 30, 3): (64353806618, 'profiles/step_kernel_11v11_4096.md'),
-    (3, 16384, 100, 30, 3): (191785421254, 'profiles/step_kernel_11v11_hard_16384.md'),
-    (4, 8192, 100, 30, 3): (109437097192, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
-    (5, 32768, 100, 30, 3): (190759609408, 'profiles/step_kernel_mixed_32768.md'),
+    (1, 64, 100, 30, 3): (77848709, 'profiles/step_kernel_5v5_64.md'),
+    (2, 4096, 100, 30, 3): (65060719838, 'profiles/step_kernel_11v11_4096.md'),
+    (3, 16384, 100, 30, 3): (193424500413, 'profiles/step_kernel_11v11_hard_16384.md'),
+    (4, 8192, 100, 30, 3): (110546197410, 'profiles/step_kernel_11v11_selfplay_stacked_8192.md'),
+    (5, 32768, 100, 30, 3): (192416493757, 'profiles/step_kernel_mixed_32768.md'),
 }
 
 
